@@ -1,0 +1,146 @@
+"""ctypes wrapper around the C oracle (``oracle/ggml_oracle.c``).
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of ``bench.py`` may import this module; the product
+package never does.  Arrays are numpy; block buffers are GGML bytes (uint8).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "libggml_oracle.so")
+
+F32, F16, Q8_0, Q4K, Q6K, Q8K = 0, 1, 8, 12, 14, 15
+_ELEMS = {Q8_0: 32, Q4K: 256, Q6K: 256, Q8K: 256}
+_BYTES = {Q8_0: 34, Q4K: 144, Q6K: 210, Q8K: 292}
+VEC_DOT_TYPE = {Q8_0: Q8_0, Q4K: Q8K, Q6K: Q8K}
+
+_lib = None
+
+
+def build() -> None:
+    """Compile the oracle with its Makefile (gcc, no reference sources)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.orc_f32_to_f16.argtypes = [ctypes.c_float]
+        L.orc_f32_to_f16.restype = ctypes.c_uint16
+        L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.orc_f16_to_f32.restype = ctypes.c_float
+        L.orc_quantize.argtypes = [i32, vp, i64, vp]
+        L.orc_dequantize.argtypes = [i32, vp, i64, vp]
+        L.orc_vec_dot.argtypes = [i32, i64, vp, vp]
+        L.orc_vec_dot.restype = ctypes.c_float
+        L.orc_block_dots.argtypes = [i32, i64, vp, vp, vp]
+        L.orc_matmul.argtypes = [i32, i64, i64, i64, vp, vp, vp, i32]
+        L.orc_matmul_prequant.argtypes = [i32, i64, i64, i64, vp, vp, vp, i32]
+        for f in ("orc_block_elems", "orc_block_bytes", "orc_vec_dot_type"):
+            getattr(L, f).argtypes = [i32]
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def block_elems(dt: int) -> int:
+    return _ELEMS[dt]
+
+
+def block_bytes(dt: int) -> int:
+    return _BYTES[dt]
+
+
+def row_bytes(dt: int, k: int) -> int:
+    return k // _ELEMS[dt] * _BYTES[dt]
+
+
+def f32_to_f16_bits(x: float) -> int:
+    return lib().orc_f32_to_f16(float(x))
+
+
+def f16_bits_to_f32(h: int) -> float:
+    return lib().orc_f16_to_f32(int(h))
+
+
+def quantize(dt: int, x: np.ndarray) -> np.ndarray:
+    """from_float of a row-major f32 array; returns GGML bytes, shape [rows, row_bytes]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    k = x.shape[-1]
+    rows = x.size // k
+    out = np.zeros((rows, row_bytes(dt, k)), dtype=np.uint8)
+    rc = lib().orc_quantize(dt, _ptr(x), x.size, _ptr(out))
+    if rc != 0:
+        raise ValueError(f"oracle quantize failed for dtype {dt}, shape {x.shape}")
+    return out
+
+
+def dequantize(dt: int, blocks: np.ndarray, n_elems: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.zeros(n_elems, dtype=np.float32)
+    rc = lib().orc_dequantize(dt, _ptr(blocks), n_elems, _ptr(out))
+    if rc != 0:
+        raise ValueError("oracle dequantize failed")
+    return out
+
+
+def vec_dot(dt: int, k: int, w_row: np.ndarray, x_row: np.ndarray) -> float:
+    return lib().orc_vec_dot(dt, k, _ptr(np.ascontiguousarray(w_row)), _ptr(np.ascontiguousarray(x_row)))
+
+
+def block_dots(dt: int, w: np.ndarray, xq: np.ndarray, k: int) -> np.ndarray:
+    """Integer block dots for every (token m, weight row n).
+
+    Returns int32 [m, n, nb] (Q8_0, Q6_K) or [m, n, nb, 2] (Q4_K: isum_d, isum_m)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1, row_bytes(dt, k))
+    vt = VEC_DOT_TYPE[dt]
+    xq = np.ascontiguousarray(xq, dtype=np.uint8).reshape(-1, row_bytes(vt, k))
+    nb = k // _ELEMS[dt]
+    per = 2 if dt == Q4K else 1
+    out = np.zeros((xq.shape[0], w.shape[0], nb * per), dtype=np.int32)
+    L = lib()
+    for m in range(xq.shape[0]):
+        for n in range(w.shape[0]):
+            row = out[m, n]
+            rc = L.orc_block_dots(dt, k, _ptr(w[n]), _ptr(xq[m]), row.ctypes.data)
+            if rc != 0:
+                raise ValueError("oracle block_dots failed")
+    if dt == Q4K:
+        return out.reshape(xq.shape[0], w.shape[0], nb, 2)
+    return out
+
+
+def matmul(dt: int, x: np.ndarray, w: np.ndarray, k: int, nthreads: int = 0) -> np.ndarray:
+    """Candle k_quants::matmul: y[m, n] = vec_dot(W[n], quant(x[m]))."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, k)
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1, row_bytes(dt, k))
+    y = np.zeros((x.shape[0], w.shape[0]), dtype=np.float32)
+    rc = lib().orc_matmul(dt, x.shape[0], k, w.shape[0], _ptr(x), _ptr(w), _ptr(y), nthreads)
+    if rc != 0:
+        raise ValueError("oracle matmul failed")
+    return y
+
+
+def matmul_prequant(dt: int, xq: np.ndarray, w: np.ndarray, k: int, nthreads: int = 0) -> np.ndarray:
+    vt = VEC_DOT_TYPE[dt]
+    xq = np.ascontiguousarray(xq, dtype=np.uint8).reshape(-1, row_bytes(vt, k))
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1, row_bytes(dt, k))
+    y = np.zeros((xq.shape[0], w.shape[0]), dtype=np.float32)
+    rc = lib().orc_matmul_prequant(dt, xq.shape[0], k, w.shape[0], _ptr(xq), _ptr(w), _ptr(y), nthreads)
+    if rc != 0:
+        raise ValueError("oracle matmul failed")
+    return y
