@@ -1,0 +1,256 @@
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+Default workload: the Q4_K decode GEMV set at
+Llama-3-8B layer shapes, batch M = 1 -- q_proj 4096x4096, k_proj / v_proj
+1024x4096, gate / up 14336x4096, down 4096x14336. One step is one pass over
+the set as a decoder layer runs it: quantize the 4096-wide activation to Q8_K
+on the device, q/k/v/gate/up GEMVs, quantize the 14336-wide activation, down
+GEMV. Weights are N(0, 0.02^2) seed 2, activations N(0, 1) seed 3
+(SplitMix64 + Box-Muller), quantized on the GPU (bit-identical to the CPU
+quantizer). Several weight copies (> 2x the 256 MB Infinity Cache) are
+rotated so every step streams its weights from HBM.
+
+Steps are captured into HIP graphs (torch.cuda.graph) and replayed; the timed
+region is bracketed by torch.cuda.synchronize(). `value` is algorithmic bytes
+(weights + f32 activations + f32 outputs) per second over the timed steps.
+The roofline object times the dominant kernel (the gate/up GEMV) alone with
+HIP events on the stream it runs on. The CPU baseline is the oracle's C
+restatement of Candle's CPU quantized matmul (k_quants::matmul with the
+generic vec_dot), run on this host's cores over a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Q4_K GEMV GB/s (% of HBM peak) + decode tok/s, Llama-3-8B-shape Q4_K_M"
+
+# (name, out, in) of the config-2 set
+GEMV_SET = [("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 4096),
+            ("gate_proj", 14336, 4096), ("up_proj", 14336, 4096), ("down_proj", 4096, 14336)]
+
+
+def gemv_bytes(dt, n, k):
+    from inference_amd import GgmlDType
+    dt = GgmlDType(dt)
+    w = n * (k // dt.block_size()) * dt.type_size()
+    return w + 4 * k + 4 * n  # weights + f32 activation + f32 output
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_set(torch, dev, dt, copies):
+    """`copies` independent weight sets of GEMV_SET, quantized on the GPU."""
+    from inference_amd import QTensor
+    from inference_amd.synth import normal
+    sets = []
+    for c in range(copies):
+        layer = {}
+        for i, (name, n, k) in enumerate(GEMV_SET):
+            w = normal(2 + 1000 * c + 17 * i, (n, k), 0.02) if c == 0 else None
+            if w is None:
+                # further copies: same distribution, distinct bytes, generated on device
+                g = torch.Generator(device=dev)
+                g.manual_seed(1000 * c + i)
+                wt = torch.randn((n, k), generator=g, device=dev) * 0.02
+            else:
+                wt = torch.from_numpy(w).to(dev)
+            layer[name] = QTensor.quantize(wt, dt)
+            del wt
+        sets.append(layer)
+    return sets
+
+
+def run_gemv_set(torch, dev, args):
+    from inference_amd import GgmlDType, qmm
+    from inference_amd.synth import normal
+
+    dt = GgmlDType.Q4K
+    vt = dt.vec_dot_type()
+    set_weight_bytes = sum(n * (k // 256) * 144 for _, n, k in GEMV_SET)
+    copies = max(2, -(-args.rotate_mb * 2 ** 20 // set_weight_bytes))
+    log(f"[bench] building {copies} weight copies of the Q4_K GEMV set ({copies * set_weight_bytes / 2**20:.0f} MiB)")
+    sets = build_set(torch, dev, dt, copies)
+
+    x4096 = torch.from_numpy(normal(3, (1, 4096))).to(dev)
+    x14336 = torch.from_numpy(normal(3, (1, 14336))).to(dev)
+    xq4096 = torch.empty((1, 16 * 292), dtype=torch.uint8, device=dev)
+    xq14336 = torch.empty((1, 56 * 292), dtype=torch.uint8, device=dev)
+    outs = {name: torch.empty((1, n), dtype=torch.float32, device=dev) for name, n, _ in GEMV_SET}
+    L = qmm.lib()
+
+    def step(layer):
+        s = qmm._stream(dev)
+        qmm._check(L.qmm_quantize_rows(int(vt), x4096.data_ptr(), 1, 4096, 4096, xq4096.data_ptr(), s))
+        for name, n, k in GEMV_SET[:5]:
+            qmm._check(L.qmm_matmul_q(layer[name].handle, xq4096.data_ptr(), 1, outs[name].data_ptr(), n, s))
+        qmm._check(L.qmm_quantize_rows(int(vt), x14336.data_ptr(), 1, 14336, 14336, xq14336.data_ptr(), s))
+        qmm._check(L.qmm_matmul_q(layer["down_proj"].handle, xq14336.data_ptr(), 1, outs["down_proj"].data_ptr(),
+                                  4096, s))
+
+    def gate_only(layer):
+        s = qmm._stream(dev)
+        qmm._check(L.qmm_matmul_q(layer["gate_proj"].handle, xq4096.data_ptr(), 1, outs["gate_proj"].data_ptr(),
+                                  14336, s))
+
+    # warm up eagerly (module load, kernel lookup), then capture graphs
+    for c in range(copies):
+        step(sets[c])
+    torch.cuda.synchronize()
+
+    def capture(fn, reps):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for r in range(reps):
+                fn(sets[r % copies])
+        return g
+
+    per_graph = copies * max(1, 24 // copies)
+    g_step = capture(step, per_graph)
+    reps = max(1, -(-args.steps // per_graph))
+    steps = reps * per_graph
+    for _ in range(max(1, args.warmup // per_graph)):
+        g_step.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g_step.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    step_bytes = sum(gemv_bytes(dt, n, k) for _, n, k in GEMV_SET)
+    value = step_bytes * steps / elapsed / 1e9
+
+    # dominant kernel alone: gate/up GEMV, HIP events on the capture/replay stream
+    g_gate = capture(gate_only, per_graph)
+    g_gate.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gate_reps = max(4, args.steps // per_graph)
+    e0.record(stream)
+    for _ in range(gate_reps):
+        g_gate.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    gate_us = e0.elapsed_time(e1) * 1e3 / (gate_reps * per_graph)
+    gate_bytes = gemv_bytes(dt, 14336, 4096)
+    achieved = gate_bytes / (gate_us * 1e-6) / 1e9
+
+    # per-shape figures (same method)
+    per_shape = {}
+    for name, n, k in GEMV_SET:
+        xq = xq4096 if k == 4096 else xq14336
+        y = outs[name]
+
+        def one(layer, name=name, n=n, xq=xq, y=y):
+            qmm._check(L.qmm_matmul_q(layer[name].handle, xq.data_ptr(), 1, y.data_ptr(), n, qmm._stream(dev)))
+        g = capture(one, per_graph)
+        g.replay()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(gate_reps):
+            g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (gate_reps * per_graph)
+        b = gemv_bytes(dt, n, k)
+        per_shape[name] = {"shape": [n, k], "us": round(us, 3), "GB/s": round(b / us / 1e3, 1),
+                           "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+    result = {
+        "value": value,
+        "ms_per_step": elapsed / steps * 1e3,
+        "steps": steps,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "qmm_gemv_q4k_m1 (gate_proj 14336x4096)", "avg_us": round(gate_us, 3),
+                     "algorithmic_bytes": gate_bytes},
+        "per_shape": per_shape,
+        "weight_copies": copies,
+    }
+    return result, sets
+
+
+def cpu_baseline(sets, budget_s):
+    """Oracle restatement of Candle's CPU quantized matmul over the same GEMV set."""
+    from oracle import oracle as orc
+    from inference_amd.synth import normal
+    threads = min(16, os.cpu_count() or 1)
+    layer = sets[0]
+    w = {name: layer[name].to_ggml() for name, _, _ in GEMV_SET}
+    x4096 = normal(3, (1, 4096))
+    x14336 = normal(3, (1, 14336))
+    total_bytes = sum(gemv_bytes(12, n, k) for _, n, k in GEMV_SET)
+    orc.lib()
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        for name, n, k in GEMV_SET:
+            orc.matmul(orc.Q4K, x4096 if k == 4096 else x14336, w[name], k, nthreads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 1000:
+            break
+    return {"value": round(total_bytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} passes of the Q4_K GEMV set (M=1, 6 projections) with the oracle's generic "
+                      f"vec_dot, {threads} OpenMP threads, {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--warmup", type=int, default=24)
+    ap.add_argument("--rotate-mb", type=int, default=640, help="distinct weight bytes rotated (MiB)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
+              f"(the path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    res, sets = run_gemv_set(torch, dev, args)
+    cpu = cpu_baseline(sets, args.cpu_seconds) if args.cpu_seconds > 0 else None
+    line = {
+        "metric": METRIC,
+        "value": round(res["value"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": res["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "q4k_decode_gemv_set_llama3_8b_m1", "shapes_out_in": [[n, k] for _, n, k in GEMV_SET],
+                   "batch_m": 1, "weights": "Q4_K, N(0,0.02^2) seed 2", "activations": "Q8_K on device, seed 3",
+                   "weight_copies_rotated": res["weight_copies"]},
+        "hbm_frac": round(res["value"] / HBM_PEAK_GBS, 4),
+        "roofline": res["roofline"],
+        "per_shape": res["per_shape"],
+        "decode_tok_s": None,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,136 @@
+/*
+ * qmm.h -- C ABI of the MI355X (gfx950) quantized-matmul backend.
+ *
+ * This is the drop-in boundary for Candle's quantized matmul path as the
+ * reference LLM engine uses it:
+ *   QuantizedLinear::{quantize, forward}  crates/llm/candle-llm/src/primitives/quant.rs:26-43
+ *   QTensor::quantize / QMatMul::from_qtensor / QMatMul::forward (candle-core @1e6aa85e,
+ *     called at quant.rs:27, :29, :38)
+ *   QTensor::new(QStorage::from_data(..)) crates/media/candle-gen/candle-gen/src/quant/repack.rs:202-203
+ *   QTensor::dequantize                   crates/llm/candle-llm/src/gguf.rs:104
+ * and for the kernel-level launchers those calls reach on a GPU:
+ *   launch_mmvq_gguf_quantize_q8_1_f32    crates/media/candle-gen/vendor/candle-kernels/src/ffi.rs:412-419
+ *   launch_mmvq_gguf_{q8_0,q4_k,q6_k}_f32_plain  ffi.rs:217-227, 250-260, 272-282
+ *   launch_mmq_gguf_{q4_k,q6_k}           ffi.rs:583-598, 615-630
+ *   moe_gemm_gguf                         ffi.rs:25-39
+ *
+ * Conventions (deliberately stricter than the reference's void launchers):
+ *   - every entry point returns an int status (QMM_OK == 0); qmm_last_error()
+ *     gives a message for the calling thread;
+ *   - all tensors are device pointers owned by the caller unless a function
+ *     says otherwise; `stream` is a hipStream_t (NULL = the default stream);
+ *   - weights live in opaque qmm_qtensor handles created from GGML block bytes
+ *     or by quantizing f32 on the device; the handle owns its device memory;
+ *   - a kernel image that cannot be loaded for the current device is an error
+ *     (QMM_ERR_NO_KERNEL), never a silent no-op.
+ * Kernels are launched only with hipModuleLaunchKernel from a gfx950 code
+ * object embedded in the library.
+ */
+#ifndef QMM_H
+#define QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+enum {
+    QMM_OK = 0,
+    QMM_ERR_INVALID = 1,     /* bad argument: shape, dtype, null pointer, size   */
+    QMM_ERR_HIP = 2,         /* a HIP runtime call failed                         */
+    QMM_ERR_NO_KERNEL = 3,   /* code object or kernel missing for this device     */
+    QMM_ERR_UNSUPPORTED = 4, /* valid request this build does not implement       */
+    QMM_ERR_OOM = 5          /* device allocation failed                          */
+};
+
+/* GGML dtype tags (GGUF numbering, crates/llm/mlx-llm/src/gguf/dequant.rs:87-113). */
+enum {
+    QMM_F32 = 0,
+    QMM_Q8_0 = 8,  /* 34 B / 32:   f16 d, i8 qs[32]                          */
+    QMM_Q4K = 12,  /* 144 B / 256: f16 d, f16 dmin, u8 scales[12], u8 qs[128] */
+    QMM_Q6K = 14,  /* 210 B / 256: u8 ql[128], u8 qh[64], i8 scales[16], f16 d */
+    QMM_Q8K = 15   /* 292 B / 256: f32 d, i8 qs[256], i16 bsums[16] (activations only) */
+};
+
+typedef struct qmm_qtensor qmm_qtensor;
+
+/* Last error message of the calling thread ("" if none). */
+const char *qmm_last_error(void);
+
+/* Load the kernel code object on `device` (optional: every entry point loads it
+ * lazily for the current device). */
+int qmm_init(int device);
+
+/* GGML geometry: elements per block, bytes per block, and the activation type a
+ * weight type multiplies against (Q8_0 -> Q8_0, Q4K/Q6K -> Q8K). -1 if unknown.
+ * (GgmlDType::block_size / type_size / vec_dot_type.) */
+int qmm_block_size(int dtype);
+int qmm_type_size(int dtype);
+int qmm_vec_dot_type(int dtype);
+
+/* QTensor::new(QStorage::from_data(bytes, device, dtype), (n, k)).
+ * `bytes` holds n*k/block_size GGML blocks, row-major over n then k, on the
+ * host (bytes_on_device = 0) or on the current device (= 1). The bytes are
+ * copied into the handle's own device layout; the caller keeps `bytes`. */
+int qmm_qtensor_from_ggml(int dtype, int64_t n, int64_t k, const void *bytes, int bytes_on_device,
+                          void *stream, qmm_qtensor **out);
+
+/* QTensor::quantize(&Tensor f32 [n, k], dtype) computed on the device:
+ * `w` is a device pointer to n*k f32 (row-major). The result's GGML bytes
+ * equal those of candle's CPU from_float for the same input. */
+int qmm_qtensor_quantize(int dtype, int64_t n, int64_t k, const float *w, void *stream,
+                         qmm_qtensor **out);
+
+/* QTensor::dequantize: n*k f32 into the device buffer `dst`. */
+int qmm_qtensor_dequantize(const qmm_qtensor *t, float *dst, void *stream);
+
+/* Export the tensor as GGML block bytes (qmm_qtensor_ggml_bytes() of them) into
+ * `dst` on the host (dst_on_device = 0, synchronous) or the device (= 1). */
+int qmm_qtensor_to_ggml(const qmm_qtensor *t, void *dst, int dst_on_device, void *stream);
+
+/* Shape and dtype; size of the GGML byte image. */
+int qmm_qtensor_info(const qmm_qtensor *t, int *dtype, int64_t *n, int64_t *k);
+size_t qmm_qtensor_ggml_bytes(const qmm_qtensor *t);
+
+/* Free a handle and its device memory (NULL is ignored). */
+void qmm_qtensor_free(qmm_qtensor *t);
+
+/* VecDotType::from_float on the device (replaces launch_mmvq_gguf_quantize_q8_1_f32,
+ * ffi.rs:412-419): x is f32 [m, k] with row stride ldx (elements); xq receives
+ * m rows of k/block_size blocks of `vdtype` (QMM_Q8_0 or QMM_Q8K), GGML bytes,
+ * contiguous. Bytes equal the CPU quantizer's for the same input. */
+int qmm_quantize_rows(int vdtype, const float *x, int64_t m, int64_t k, int64_t ldx, void *xq,
+                      void *stream);
+
+/* Bytes of workspace qmm_matmul needs for m activation rows. */
+size_t qmm_matmul_workspace_size(const qmm_qtensor *w, int64_t m);
+
+/* QMatMul::forward: y[i, j] = sum_k x[i, k] * W[j, k] for i < m, j < n, with x
+ * quantized to W's vec-dot type first (as Candle's CPU path does).
+ * x: f32 [m, k] (row stride ldx); y: f32 [m, n] (row stride ldy); ws: device
+ * scratch of qmm_matmul_workspace_size(w, m) bytes. m = 1..8 runs the decode
+ * GEMV (replaces launch_mmvq_gguf_*_f32_plain); larger m runs the GEMM path
+ * (replaces launch_mmq_gguf_*). */
+int qmm_matmul(const qmm_qtensor *w, const float *x, int64_t m, int64_t ldx, float *y, int64_t ldy,
+               void *ws, size_t ws_bytes, void *stream);
+
+/* The same with activations already quantized (xq: m rows of vec-dot blocks,
+ * as produced by qmm_quantize_rows). */
+int qmm_matmul_q(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy, void *stream);
+
+/* Debug entry: exact int32 block dots of every (activation row, weight row,
+ * super-block), computed by the same GEMV kernel that qmm_matmul_q runs.
+ * dots: device int32 [m, n, k/block_size, per] with per = 2 for Q4K
+ * (isum_d = sum_j sc_j*sum q4*q8, isum_m = sum_j m_j*(bsum_2j + bsum_2j+1))
+ * and per = 1 for Q6K (sum_j sc_j*sum (q6-32)*q8) and Q8_0 (sum qw*qx).
+ * y receives the f32 outputs as qmm_matmul_q would. m = 1..8. */
+int qmm_block_dots(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy,
+                   int32_t *dots, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QMM_H */

@@ -1,0 +1,509 @@
+// Host side of the C ABI declared in include/qmm.h.
+//
+// Plain C++ over the HIP runtime: device memory with hipMalloc/hipMemcpyAsync,
+// kernels from the embedded gfx950 code object through hipModuleLoadData /
+// hipModuleGetFunction / hipModuleLaunchKernel. No torch types cross this
+// boundary; callers pass raw device pointers and a hipStream_t.
+#include "qmm.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+extern "C" const unsigned char qmm_code_object_start[];
+extern "C" const unsigned char qmm_code_object_end[];
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define QMM_HIP(expr)                                                                 \
+  do {                                                                                \
+    hipError_t e_ = (expr);                                                           \
+    if (e_ != hipSuccess) return fail(QMM_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+#define QMM_TRY(expr)          \
+  do {                         \
+    int rc_ = (expr);          \
+    if (rc_ != QMM_OK) return rc_; \
+  } while (0)
+
+enum { kFmtQ80 = 0, kFmtQ4K = 1, kFmtQ6K = 2 };
+
+int fmt_of(int dtype) {
+  switch (dtype) {
+    case QMM_Q8_0: return kFmtQ80;
+    case QMM_Q4K: return kFmtQ4K;
+    case QMM_Q6K: return kFmtQ6K;
+    default: return -1;
+  }
+}
+
+const char* fmt_name(int fmt) { return fmt == kFmtQ80 ? "q8_0" : fmt == kFmtQ4K ? "q4k" : "q6k"; }
+
+struct Device {
+  hipModule_t module = nullptr;
+  std::unordered_map<std::string, hipFunction_t> fns;
+  int max_lds = 0;
+  int num_cu = 0;
+};
+
+std::mutex g_mu;
+Device* g_dev[64] = {};
+
+// Launch-shape overrides for tuning sweeps, read at every launch:
+// QMM_GEMV_RU="R,U" (rows per wave, loads per row in flight), QMM_GEMV_MAXWG=<workgroups>.
+struct Tuning {
+  int r = 0, u = 0, max_wg = 0;
+};
+Tuning tuning() {
+  Tuning t;
+  if (const char* s = getenv("QMM_GEMV_RU")) {
+    if (sscanf(s, "%d,%d", &t.r, &t.u) != 2) t.r = t.u = 0;
+  }
+  if (const char* s = getenv("QMM_GEMV_MAXWG")) t.max_wg = atoi(s);
+  return t;
+}
+
+int current_device(Device** out) {
+  int dev = 0;
+  QMM_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return fail(QMM_ERR_INVALID, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!g_dev[dev]) {
+    Device* d = new Device();
+    hipError_t e = hipModuleLoadData(&d->module, qmm_code_object_start);
+    if (e != hipSuccess) {
+      delete d;
+      return fail(QMM_ERR_NO_KERNEL, "hipModuleLoadData(gfx950 code object) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    }
+    e = hipDeviceGetAttribute(&d->max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&d->num_cu, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) {
+      (void)hipModuleUnload(d->module);
+      delete d;
+      return fail(QMM_ERR_HIP, "hipDeviceGetAttribute: %s", hipGetErrorString(e));
+    }
+    g_dev[dev] = d;
+  }
+  *out = g_dev[dev];
+  return QMM_OK;
+}
+
+int kernel(Device* d, const std::string& name, hipFunction_t* f) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = d->fns.find(name);
+  if (it != d->fns.end()) {
+    *f = it->second;
+    return QMM_OK;
+  }
+  hipFunction_t fn = nullptr;
+  hipError_t e = hipModuleGetFunction(&fn, d->module, name.c_str());
+  if (e != hipSuccess || !fn)
+    return fail(QMM_ERR_NO_KERNEL, "kernel %s missing from the code object: %s", name.c_str(),
+                hipGetErrorString(e));
+  d->fns.emplace(name, fn);
+  *f = fn;
+  return QMM_OK;
+}
+
+int launch(Device* d, const std::string& name, unsigned grid, unsigned block, unsigned lds,
+           hipStream_t s, void** args) {
+  hipFunction_t f;
+  QMM_TRY(kernel(d, name, &f));
+  if (grid == 0) return QMM_OK;
+  QMM_HIP(hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, lds, s, args, nullptr));
+  return QMM_OK;
+}
+
+unsigned ceil_div(long long a, long long b) { return (unsigned)((a + b - 1) / b); }
+
+}  // namespace
+
+struct qmm_qtensor {
+  int dtype;
+  int64_t n, k;
+  int device;
+  void* data;    // device layout (see qmm_common.h)
+  size_t bytes;  // == GGML bytes of the tensor
+};
+
+extern "C" {
+
+const char* qmm_last_error(void) { return g_err.c_str(); }
+
+int qmm_init(int device) {
+  int prev = 0;
+  QMM_HIP(hipGetDevice(&prev));
+  QMM_HIP(hipSetDevice(device));
+  Device* d;
+  int rc = current_device(&d);
+  (void)hipSetDevice(prev);
+  return rc;
+}
+
+int qmm_block_size(int dtype) {
+  switch (dtype) {
+    case QMM_Q8_0: return 32;
+    case QMM_Q4K: case QMM_Q6K: case QMM_Q8K: return 256;
+    default: return -1;
+  }
+}
+
+int qmm_type_size(int dtype) {
+  switch (dtype) {
+    case QMM_Q8_0: return 34;
+    case QMM_Q4K: return 144;
+    case QMM_Q6K: return 210;
+    case QMM_Q8K: return 292;
+    default: return -1;
+  }
+}
+
+int qmm_vec_dot_type(int dtype) {
+  switch (dtype) {
+    case QMM_Q8_0: return QMM_Q8_0;
+    case QMM_Q4K: case QMM_Q6K: return QMM_Q8K;
+    default: return -1;
+  }
+}
+
+static int check_shape(int dtype, int64_t n, int64_t k) {
+  if (fmt_of(dtype) < 0) return fail(QMM_ERR_INVALID, "unsupported weight dtype %d", dtype);
+  const int bs = qmm_block_size(dtype);
+  if (n <= 0 || k <= 0) return fail(QMM_ERR_INVALID, "empty shape (%lld, %lld)", (long long)n, (long long)k);
+  if (k % bs) return fail(QMM_ERR_INVALID, "k = %lld is not a multiple of the block size %d", (long long)k, bs);
+  if (n > (1LL << 31) - 1 || k > (1LL << 31) - 1) return fail(QMM_ERR_INVALID, "shape too large");
+  return QMM_OK;
+}
+
+static int alloc_tensor(int dtype, int64_t n, int64_t k, qmm_qtensor** out) {
+  qmm_qtensor* t = new qmm_qtensor();
+  t->dtype = dtype;
+  t->n = n;
+  t->k = k;
+  QMM_HIP(hipGetDevice(&t->device));
+  t->bytes = (size_t)(n * (k / qmm_block_size(dtype))) * qmm_type_size(dtype);
+  hipError_t e = hipMalloc(&t->data, t->bytes);
+  if (e != hipSuccess) {
+    delete t;
+    return fail(QMM_ERR_OOM, "hipMalloc(%zu): %s", t->bytes, hipGetErrorString(e));
+  }
+  *out = t;
+  return QMM_OK;
+}
+
+// Device GGML bytes -> the tensor's device layout.
+static int ggml_to_dev(Device* d, qmm_qtensor* t, const void* src, hipStream_t s) {
+  const int fmt = fmt_of(t->dtype);
+  if (fmt == kFmtQ4K) {
+    QMM_HIP(hipMemcpyAsync(t->data, src, t->bytes, hipMemcpyDeviceToDevice, s));
+    return QMM_OK;
+  }
+  long long nblocks = t->n * (t->k / qmm_block_size(t->dtype));
+  const void* a0 = src;
+  void* a1 = t->data;
+  int f = fmt;
+  void* args[] = {&a0, &a1, &nblocks, &f};
+  return launch(d, "qmm_ggml_to_dev", ceil_div(nblocks, 256), 256, 0, s, args);
+}
+
+int qmm_qtensor_from_ggml(int dtype, int64_t n, int64_t k, const void* bytes, int bytes_on_device,
+                          void* stream, qmm_qtensor** out) {
+  if (!out || !bytes) return fail(QMM_ERR_INVALID, "null pointer");
+  *out = nullptr;
+  QMM_TRY(check_shape(dtype, n, k));
+  Device* d;
+  QMM_TRY(current_device(&d));
+  hipStream_t s = (hipStream_t)stream;
+  qmm_qtensor* t;
+  QMM_TRY(alloc_tensor(dtype, n, k, &t));
+  const void* src = bytes;
+  void* staging = nullptr;
+  int rc = QMM_OK;
+  if (!bytes_on_device) {
+    if (fmt_of(dtype) == kFmtQ4K) {
+      hipError_t e = hipMemcpyAsync(t->data, bytes, t->bytes, hipMemcpyHostToDevice, s);
+      if (e == hipSuccess) e = hipStreamSynchronize(s);
+      if (e != hipSuccess) rc = fail(QMM_ERR_HIP, "upload: %s", hipGetErrorString(e));
+      if (rc != QMM_OK) {
+        qmm_qtensor_free(t);
+        return rc;
+      }
+      *out = t;
+      return QMM_OK;
+    }
+    hipError_t e = hipMalloc(&staging, t->bytes);
+    if (e != hipSuccess) {
+      qmm_qtensor_free(t);
+      return fail(QMM_ERR_OOM, "hipMalloc(staging %zu): %s", t->bytes, hipGetErrorString(e));
+    }
+    e = hipMemcpyAsync(staging, bytes, t->bytes, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) rc = fail(QMM_ERR_HIP, "upload: %s", hipGetErrorString(e));
+    src = staging;
+  }
+  if (rc == QMM_OK) rc = ggml_to_dev(d, t, src, s);
+  if (staging) {
+    hipError_t e = hipStreamSynchronize(s);
+    if (rc == QMM_OK && e != hipSuccess) rc = fail(QMM_ERR_HIP, "sync: %s", hipGetErrorString(e));
+    (void)hipFree(staging);
+  }
+  if (rc != QMM_OK) {
+    qmm_qtensor_free(t);
+    return rc;
+  }
+  *out = t;
+  return QMM_OK;
+}
+
+int qmm_qtensor_quantize(int dtype, int64_t n, int64_t k, const float* w, void* stream, qmm_qtensor** out) {
+  if (!out || !w) return fail(QMM_ERR_INVALID, "null pointer");
+  *out = nullptr;
+  QMM_TRY(check_shape(dtype, n, k));
+  Device* d;
+  QMM_TRY(current_device(&d));
+  hipStream_t s = (hipStream_t)stream;
+  qmm_qtensor* t;
+  QMM_TRY(alloc_tensor(dtype, n, k, &t));
+  const int fmt = fmt_of(dtype);
+  long long nblocks = n * (k / qmm_block_size(dtype));
+  void* ggml = t->data;
+  int rc = QMM_OK;
+  if (fmt != kFmtQ4K) {
+    hipError_t e = hipMalloc(&ggml, t->bytes);
+    if (e != hipSuccess) {
+      qmm_qtensor_free(t);
+      return fail(QMM_ERR_OOM, "hipMalloc(staging %zu): %s", t->bytes, hipGetErrorString(e));
+    }
+  }
+  if (fmt == kFmtQ80) {
+    // Q8_0 weights use the same from_float as Q8_0 activations: treat the
+    // matrix as one row of n*k values.
+    long long ld = 0;
+    int kk = (int)(n * k), one = 1;
+    if ((long long)kk != n * k) rc = fail(QMM_ERR_INVALID, "Q8_0 tensor too large");
+    const float* x = w;
+    void* args[] = {&x, &ld, &ggml, &kk, &one};
+    if (rc == QMM_OK) rc = launch(d, "qmm_quantize_q8_0", ceil_div(nblocks * 8, 256), 256, 0, s, args);
+  } else {
+    const float* x = w;
+    void* args[] = {&x, &ggml, &nblocks};
+    rc = launch(d, fmt == kFmtQ4K ? "qmm_quantize_q4k_w" : "qmm_quantize_q6k_w", ceil_div(nblocks, 64), 64,
+                0, s, args);
+  }
+  if (rc == QMM_OK && fmt != kFmtQ4K) rc = ggml_to_dev(d, t, ggml, s);
+  if (fmt != kFmtQ4K) {
+    hipError_t e = hipStreamSynchronize(s);
+    if (rc == QMM_OK && e != hipSuccess) rc = fail(QMM_ERR_HIP, "sync: %s", hipGetErrorString(e));
+    (void)hipFree(ggml);
+  }
+  if (rc != QMM_OK) {
+    qmm_qtensor_free(t);
+    return rc;
+  }
+  *out = t;
+  return QMM_OK;
+}
+
+int qmm_qtensor_dequantize(const qmm_qtensor* t, float* dst, void* stream) {
+  if (!t || !dst) return fail(QMM_ERR_INVALID, "null pointer");
+  Device* d;
+  QMM_TRY(current_device(&d));
+  const int fmt = fmt_of(t->dtype);
+  long long nblocks = t->n * (t->k / qmm_block_size(t->dtype));
+  const void* a0 = t->data;
+  float* a1 = dst;
+  int f = fmt;
+  void* args[] = {&a0, &a1, &nblocks, &f};
+  const long long threads = fmt == kFmtQ80 ? nblocks : nblocks * 8;
+  return launch(d, "qmm_dequantize", ceil_div(threads, 256), 256, 0, (hipStream_t)stream, args);
+}
+
+int qmm_qtensor_to_ggml(const qmm_qtensor* t, void* dst, int dst_on_device, void* stream) {
+  if (!t || !dst) return fail(QMM_ERR_INVALID, "null pointer");
+  Device* d;
+  QMM_TRY(current_device(&d));
+  hipStream_t s = (hipStream_t)stream;
+  const int fmt = fmt_of(t->dtype);
+  if (fmt == kFmtQ4K) {
+    QMM_HIP(hipMemcpyAsync(dst, t->data, t->bytes, dst_on_device ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, s));
+    if (!dst_on_device) QMM_HIP(hipStreamSynchronize(s));
+    return QMM_OK;
+  }
+  void* out = dst;
+  if (!dst_on_device) {
+    hipError_t e = hipMalloc(&out, t->bytes);
+    if (e != hipSuccess) return fail(QMM_ERR_OOM, "hipMalloc(staging %zu): %s", t->bytes, hipGetErrorString(e));
+  }
+  long long nblocks = t->n * (t->k / qmm_block_size(t->dtype));
+  const void* a0 = t->data;
+  void* a1 = out;
+  int f = fmt;
+  void* args[] = {&a0, &a1, &nblocks, &f};
+  int rc = launch(d, "qmm_dev_to_ggml", ceil_div(nblocks, 256), 256, 0, s, args);
+  if (!dst_on_device) {
+    if (rc == QMM_OK) {
+      hipError_t e = hipMemcpyAsync(dst, out, t->bytes, hipMemcpyDeviceToHost, s);
+      if (e == hipSuccess) e = hipStreamSynchronize(s);
+      if (e != hipSuccess) rc = fail(QMM_ERR_HIP, "download: %s", hipGetErrorString(e));
+    } else {
+      (void)hipStreamSynchronize(s);
+    }
+    (void)hipFree(out);
+  }
+  return rc;
+}
+
+int qmm_qtensor_info(const qmm_qtensor* t, int* dtype, int64_t* n, int64_t* k) {
+  if (!t) return fail(QMM_ERR_INVALID, "null tensor");
+  if (dtype) *dtype = t->dtype;
+  if (n) *n = t->n;
+  if (k) *k = t->k;
+  return QMM_OK;
+}
+
+size_t qmm_qtensor_ggml_bytes(const qmm_qtensor* t) { return t ? t->bytes : 0; }
+
+void qmm_qtensor_free(qmm_qtensor* t) {
+  if (!t) return;
+  if (t->data) {
+    int prev = 0;
+    (void)hipGetDevice(&prev);
+    if (prev != t->device) (void)hipSetDevice(t->device);
+    (void)hipFree(t->data);
+    if (prev != t->device) (void)hipSetDevice(prev);
+  }
+  delete t;
+}
+
+int qmm_quantize_rows(int vdtype, const float* x, int64_t m, int64_t k, int64_t ldx, void* xq, void* stream) {
+  if (!x || !xq) return fail(QMM_ERR_INVALID, "null pointer");
+  if (vdtype != QMM_Q8K && vdtype != QMM_Q8_0) return fail(QMM_ERR_INVALID, "vec-dot dtype %d is not Q8_0/Q8K", vdtype);
+  const int bs = qmm_block_size(vdtype);
+  if (m <= 0 || k <= 0 || k % bs) return fail(QMM_ERR_INVALID, "bad activation shape (%lld, %lld) for block size %d", (long long)m, (long long)k, bs);
+  if (ldx < k) return fail(QMM_ERR_INVALID, "row stride %lld < k %lld", (long long)ldx, (long long)k);
+  if (k > (1LL << 30) || m > (1LL << 30)) return fail(QMM_ERR_INVALID, "activation too large");
+  Device* d;
+  QMM_TRY(current_device(&d));
+  long long ld = ldx;
+  int kk = (int)k, mm = (int)m;
+  void* args[] = {&x, &ld, &xq, &kk, &mm};
+  const long long nblocks = m * (k / bs);
+  if (vdtype == QMM_Q8K) return launch(d, "qmm_quantize_q8k", ceil_div(nblocks, 4), 256, 0, (hipStream_t)stream, args);
+  return launch(d, "qmm_quantize_q8_0", ceil_div(nblocks * 8, 256), 256, 0, (hipStream_t)stream, args);
+}
+
+size_t qmm_matmul_workspace_size(const qmm_qtensor* w, int64_t m) {
+  if (!w || m <= 0) return 0;
+  const int vt = qmm_vec_dot_type(w->dtype);
+  return (size_t)m * (size_t)(w->k / qmm_block_size(vt)) * qmm_type_size(vt);
+}
+
+// GEMV launch for m <= 8 activation rows.
+static int gemv(Device* d, const qmm_qtensor* w, const void* xq, int m, float* y, int64_t ldy, int* dump,
+                hipStream_t s) {
+  const int fmt = fmt_of(w->dtype);
+  const int nb = (int)(w->k / qmm_block_size(w->dtype));
+  const int lpb = fmt == kFmtQ80 ? 2 : 8;
+  const int bpi = 64 / lpb;
+  const int niter = (nb + bpi - 1) / bpi;
+  const int xbb = fmt == kFmtQ80 ? 36 : 292;  // LDS bytes per staged activation block
+  const unsigned lds = (unsigned)(m * nb * xbb);
+  if ((int)lds > d->max_lds)
+    return fail(QMM_ERR_UNSUPPORTED, "activation of %d rows x %lld needs %u B of LDS (> %d)", m, (long long)w->k, lds,
+                d->max_lds);
+  int r, u;
+  if (fmt == kFmtQ80) {
+    if (niter <= 2) { r = 4; u = 2; }
+    else if (niter <= 4) { r = 1; u = 4; }
+    else { r = 1; u = 8; }
+  } else if (fmt == kFmtQ4K) {
+    if (niter <= 2) { r = 4; u = 2; }
+    else if (niter <= 4) { r = 1; u = 4; }
+    else { r = 1; u = 8; }
+  } else {
+    if (niter <= 2) { r = 2; u = 2; }
+    else { r = 1; u = 4; }
+  }
+  if (m > 4 && r == 4) r = 2;
+  const Tuning tu = tuning();
+  if (tu.r > 0 && tu.u > 0) { r = tu.r; u = tu.u; }
+  char name[64];
+  snprintf(name, sizeof(name), "qmm_gemv_%s_m%d_r%d_u%d", fmt_name(fmt), m, r, u);
+  const int waves = 4;
+  long long wgs = ((long long)w->n + waves * r - 1) / (waves * r);
+  if (tu.max_wg > 0 && wgs > tu.max_wg) wgs = tu.max_wg;
+  const void* wq = w->data;
+  float* yy = y;
+  int N = (int)w->n, K = (int)w->k, ld = (int)ldy;
+  int* dp = dump;
+  void* args[] = {&wq, &xq, &yy, &N, &K, &ld, &dp};
+  return launch(d, name, (unsigned)wgs, 64 * waves, lds, s, args);
+}
+
+static int check_matmul(const qmm_qtensor* w, int64_t m, const float* y, int64_t ldy) {
+  if (!w || !y) return fail(QMM_ERR_INVALID, "null pointer");
+  if (m <= 0) return fail(QMM_ERR_INVALID, "m = %lld must be positive", (long long)m);
+  if (ldy < w->n) return fail(QMM_ERR_INVALID, "output row stride %lld < n %lld", (long long)ldy, (long long)w->n);
+  if (ldy > (1LL << 31) - 1) return fail(QMM_ERR_INVALID, "output row stride too large");
+  int dev = 0;
+  QMM_HIP(hipGetDevice(&dev));
+  if (dev != w->device) return fail(QMM_ERR_INVALID, "tensor lives on device %d, current device is %d", w->device, dev);
+  return QMM_OK;
+}
+
+int qmm_matmul_q(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int64_t ldy, void* stream) {
+  QMM_TRY(check_matmul(w, m, y, ldy));
+  if (!xq) return fail(QMM_ERR_INVALID, "null activation");
+  Device* d;
+  QMM_TRY(current_device(&d));
+  const int vt = qmm_vec_dot_type(w->dtype);
+  const size_t xrow = (size_t)(w->k / qmm_block_size(vt)) * qmm_type_size(vt);
+  // Rows are processed in groups of up to 8 by the GEMV (the GEMM path for
+  // large m is selected in qmm_matmul_q once available).
+  for (int64_t m0 = 0; m0 < m; m0 += 8) {
+    const int mm = (int)(m - m0 < 8 ? m - m0 : 8);
+    QMM_TRY(gemv(d, w, (const uint8_t*)xq + m0 * xrow, mm, y + m0 * ldy, ldy, nullptr, (hipStream_t)stream));
+  }
+  return QMM_OK;
+}
+
+int qmm_matmul(const qmm_qtensor* w, const float* x, int64_t m, int64_t ldx, float* y, int64_t ldy, void* ws,
+               size_t ws_bytes, void* stream) {
+  QMM_TRY(check_matmul(w, m, y, ldy));
+  if (!x || !ws) return fail(QMM_ERR_INVALID, "null pointer");
+  const size_t need = qmm_matmul_workspace_size(w, m);
+  if (ws_bytes < need) return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed", ws_bytes, need);
+  QMM_TRY(qmm_quantize_rows(qmm_vec_dot_type(w->dtype), x, m, w->k, ldx, ws, stream));
+  return qmm_matmul_q(w, ws, m, y, ldy, stream);
+}
+
+int qmm_block_dots(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int64_t ldy, int32_t* dots,
+                   void* stream) {
+  QMM_TRY(check_matmul(w, m, y, ldy));
+  if (!xq || !dots) return fail(QMM_ERR_INVALID, "null pointer");
+  if (m > 8) return fail(QMM_ERR_INVALID, "block dots are produced by the GEMV: m = %lld > 8", (long long)m);
+  Device* d;
+  QMM_TRY(current_device(&d));
+  return gemv(d, w, xq, (int)m, y, ldy, dots, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,393 @@
+"""Candle-shaped host API over the libqmm C ABI (include/qmm.h).
+
+Mirrors the surface the reference engine uses for its quantized projections:
+
+* ``GgmlDType``             -- candle ``quantized::GgmlDType`` (Q8_0, Q4K, Q6K; Q8K as vec-dot type)
+* ``QTensor``               -- ``QTensor::{quantize, new(QStorage::from_data), dequantize, dtype}``
+* ``QMatMul``               -- ``QMatMul::{from_qtensor, forward}``
+* ``QuantSpec``             -- crates/llm/candle-llm/src/primitives/projection.rs:16-52
+* ``QuantizedLinear``       -- crates/llm/candle-llm/src/primitives/quant.rs:17-43
+* ``Projection``            -- crates/llm/candle-llm/src/primitives/projection.rs:56-95
+
+Tensors are torch tensors on the GPU; torch only provides device memory and the
+current stream. Every computation runs in the HIP kernels of ``libqmm.so``; if
+that library is missing this module raises instead of falling back.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+import threading
+from typing import Optional, Sequence, Tuple
+
+import numpy as np
+import torch
+
+LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
+LIB_PATH = os.path.join(LIB_DIR, "libqmm.so")
+
+
+class QmmError(RuntimeError):
+    """An error reported by the C ABI (status code + message)."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"qmm error {status}: {message}")
+        self.status = status
+
+
+_lib = None
+_lib_lock = threading.Lock()
+
+EXPORTS = (
+    "qmm_last_error", "qmm_init", "qmm_block_size", "qmm_type_size", "qmm_vec_dot_type",
+    "qmm_qtensor_from_ggml", "qmm_qtensor_quantize", "qmm_qtensor_dequantize",
+    "qmm_qtensor_to_ggml", "qmm_qtensor_info", "qmm_qtensor_ggml_bytes", "qmm_qtensor_free",
+    "qmm_quantize_rows", "qmm_matmul_workspace_size", "qmm_matmul", "qmm_matmul_q",
+    "qmm_block_dots",
+)
+
+
+def lib() -> ctypes.CDLL:
+    """Load libqmm.so (built in-tree by ``__graft_entry__.build()``)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lib_lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i64, i32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
+        pp = ctypes.POINTER(ctypes.c_void_p)
+        sig = {
+            "qmm_last_error": ([], ctypes.c_char_p),
+            "qmm_init": ([i32], i32),
+            "qmm_block_size": ([i32], i32),
+            "qmm_type_size": ([i32], i32),
+            "qmm_vec_dot_type": ([i32], i32),
+            "qmm_qtensor_from_ggml": ([i32, i64, i64, vp, i32, vp, pp], i32),
+            "qmm_qtensor_quantize": ([i32, i64, i64, vp, vp, pp], i32),
+            "qmm_qtensor_dequantize": ([vp, vp, vp], i32),
+            "qmm_qtensor_to_ggml": ([vp, vp, i32, vp], i32),
+            "qmm_qtensor_info": ([vp, ctypes.POINTER(i32), ctypes.POINTER(i64), ctypes.POINTER(i64)], i32),
+            "qmm_qtensor_ggml_bytes": ([vp], sz),
+            "qmm_qtensor_free": ([vp], None),
+            "qmm_quantize_rows": ([i32, vp, i64, i64, i64, vp, vp], i32),
+            "qmm_matmul_workspace_size": ([vp, i64], sz),
+            "qmm_matmul": ([vp, vp, i64, i64, vp, i64, vp, sz, vp], i32),
+            "qmm_matmul_q": ([vp, vp, i64, vp, i64, vp], i32),
+            "qmm_block_dots": ([vp, vp, i64, vp, i64, vp, vp], i32),
+        }
+        for name, (args, res) in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        msg = lib().qmm_last_error().decode(errors="replace")
+        raise QmmError(status, msg)
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+class GgmlDType(enum.IntEnum):
+    """GGML block types of the quantized path (GGUF numbering)."""
+
+    Q8_0 = 8
+    Q4K = 12
+    Q6K = 14
+    Q8K = 15
+
+    def block_size(self) -> int:
+        return lib().qmm_block_size(int(self))
+
+    def type_size(self) -> int:
+        return lib().qmm_type_size(int(self))
+
+    def vec_dot_type(self) -> "GgmlDType":
+        v = lib().qmm_vec_dot_type(int(self))
+        if v < 0:
+            raise QmmError(1, f"{self.name} has no vec-dot type")
+        return GgmlDType(v)
+
+
+def _device_of(t: torch.Tensor) -> torch.device:
+    if t.device.type != "cuda":
+        raise QmmError(1, f"tensor must be on a GPU, got {t.device}")
+    return t.device
+
+
+def quantize_rows(vdtype: GgmlDType, x: torch.Tensor) -> torch.Tensor:
+    """VecDotType::from_float on the GPU: f32 [m, k] -> uint8 [m, row_bytes] GGML blocks."""
+    dev = _device_of(x)
+    if x.dtype != torch.float32 or x.dim() != 2:
+        raise QmmError(1, "quantize_rows expects a 2-D float32 tensor")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    vdtype = GgmlDType(vdtype)
+    m, k = x.shape
+    if k % vdtype.block_size():
+        raise QmmError(1, f"k = {k} is not a multiple of {vdtype.name}'s block size {vdtype.block_size()}")
+    out = torch.empty((m, k // vdtype.block_size() * vdtype.type_size()), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib().qmm_quantize_rows(int(vdtype), x.data_ptr(), m, k, x.stride(0), out.data_ptr(),
+                                       _stream(dev)))
+    return out
+
+
+class QTensor:
+    """A GGML block-quantized [n, k] weight resident on one GPU."""
+
+    def __init__(self, handle: ctypes.c_void_p, device: torch.device):
+        self._h = handle
+        self.device = device
+        dt, n, k = ctypes.c_int(), ctypes.c_int64(), ctypes.c_int64()
+        _check(lib().qmm_qtensor_info(handle, ctypes.byref(dt), ctypes.byref(n), ctypes.byref(k)))
+        self._dtype = GgmlDType(dt.value)
+        self.shape: Tuple[int, int] = (n.value, k.value)
+
+    # -- constructors ---------------------------------------------------
+    @classmethod
+    def quantize(cls, tensor: torch.Tensor, dtype: GgmlDType) -> "QTensor":
+        """QTensor::quantize of a dense [n, k] weight, computed on the tensor's GPU."""
+        dtype = GgmlDType(dtype)
+        if dtype == GgmlDType.Q8K:
+            raise QmmError(1, "Q8K is an activation-only type")
+        dev = _device_of(tensor)
+        if tensor.dim() != 2:
+            raise QmmError(1, f"QTensor::quantize expects a 2-D weight, got shape {tuple(tensor.shape)}")
+        n, k = tensor.shape
+        if k % dtype.block_size():
+            raise QmmError(1, f"quantize: the last dim {k} is not a multiple of {dtype.name}'s block size "
+                              f"{dtype.block_size()}")
+        w = tensor.to(torch.float32).contiguous()
+        h = ctypes.c_void_p()
+        with torch.cuda.device(dev):
+            _check(lib().qmm_qtensor_quantize(int(dtype), n, k, w.data_ptr(), _stream(dev), ctypes.byref(h)))
+        return cls(h, dev)
+
+    @classmethod
+    def from_ggml(cls, data, dtype: GgmlDType, shape: Sequence[int],
+                  device: Optional[torch.device] = None) -> "QTensor":
+        """QTensor::new(QStorage::from_data(GGML bytes), shape).
+
+        ``data`` is bytes / a uint8 numpy array (host) or a uint8 torch tensor (host or GPU)."""
+        dtype = GgmlDType(dtype)
+        n, k = int(shape[0]), int(shape[1])
+        on_dev = 0
+        keep = None
+        if isinstance(data, torch.Tensor):
+            t = data.contiguous().view(torch.uint8)
+            if t.device.type == "cuda":
+                device = t.device
+                on_dev = 1
+            keep = t
+            ptr = t.data_ptr()
+            nbytes = t.numel()
+        else:
+            arr = np.ascontiguousarray(np.frombuffer(data, dtype=np.uint8) if isinstance(data, (bytes, bytearray))
+                                       else data, dtype=np.uint8)
+            keep = arr
+            ptr = arr.ctypes.data
+            nbytes = arr.size
+        if dtype == GgmlDType.Q8K:
+            raise QmmError(1, "Q8K is an activation-only type")
+        if k % dtype.block_size():
+            raise QmmError(1, f"k = {k} is not a multiple of {dtype.name}'s block size {dtype.block_size()}")
+        expect = n * (k // dtype.block_size()) * dtype.type_size()
+        if nbytes != expect:
+            raise QmmError(1, f"{dtype.name} [{n}, {k}] needs {expect} bytes, got {nbytes}")
+        if device is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        h = ctypes.c_void_p()
+        with torch.cuda.device(device):
+            _check(lib().qmm_qtensor_from_ggml(int(dtype), n, k, ptr, on_dev, _stream(device), ctypes.byref(h)))
+        del keep
+        return cls(h, device)
+
+    # -- accessors ------------------------------------------------------
+    def dtype(self) -> GgmlDType:
+        return self._dtype
+
+    def storage_size_in_bytes(self) -> int:
+        return int(lib().qmm_qtensor_ggml_bytes(self._h))
+
+    def dequantize(self) -> torch.Tensor:
+        """QTensor::dequantize -> f32 [n, k] on the tensor's GPU."""
+        out = torch.empty(self.shape, dtype=torch.float32, device=self.device)
+        with torch.cuda.device(self.device):
+            _check(lib().qmm_qtensor_dequantize(self._h, out.data_ptr(), _stream(self.device)))
+        return out
+
+    def to_ggml(self) -> np.ndarray:
+        """GGML block bytes of the tensor (host, uint8)."""
+        out = np.empty(self.storage_size_in_bytes(), dtype=np.uint8)
+        with torch.cuda.device(self.device):
+            _check(lib().qmm_qtensor_to_ggml(self._h, out.ctypes.data, 0, _stream(self.device)))
+        return out
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and _lib is not None:
+            _lib.qmm_qtensor_free(h)
+            self._h = None
+
+
+class QMatMul:
+    """QMatMul over a QTensor: ``forward(x) = x @ dequant(W)^T`` with x quantized to the vec-dot type."""
+
+    def __init__(self, qtensor: QTensor):
+        self.qtensor = qtensor
+
+    @classmethod
+    def from_qtensor(cls, qtensor: QTensor) -> "QMatMul":
+        return cls(qtensor)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        n, k = self.qtensor.shape
+        if x.dtype != torch.float32:
+            raise QmmError(1, f"QMatMul::forward expects float32 input, got {x.dtype}")
+        if x.shape[-1] != k:
+            raise QmmError(1, f"shape mismatch: input last dim {x.shape[-1]} vs weight in-dim {k}")
+        if x.device != self.qtensor.device:
+            raise QmmError(1, f"input on {x.device}, weight on {self.qtensor.device}")
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, k)
+        if x2.stride(-1) != 1:
+            x2 = x2.contiguous()
+        m = x2.shape[0]
+        y = torch.empty((m, n), dtype=torch.float32, device=x.device)
+        if m == 0:
+            return y.reshape(*lead, n)
+        L = lib()
+        ws_bytes = int(L.qmm_matmul_workspace_size(self.qtensor.handle, m))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+        with torch.cuda.device(x.device):
+            _check(L.qmm_matmul(self.qtensor.handle, x2.data_ptr(), m, x2.stride(0), y.data_ptr(), n,
+                                ws.data_ptr(), ws_bytes, _stream(x.device)))
+        return y.reshape(*lead, n)
+
+    __call__ = forward
+
+
+def matmul_q(qt: QTensor, xq: torch.Tensor, m: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y[m, n] from pre-quantized activations (uint8 GGML vec-dot blocks on the GPU)."""
+    n = qt.shape[0]
+    y = out if out is not None else torch.empty((m, n), dtype=torch.float32, device=qt.device)
+    with torch.cuda.device(qt.device):
+        _check(lib().qmm_matmul_q(qt.handle, xq.data_ptr(), m, y.data_ptr(), y.stride(0), _stream(qt.device)))
+    return y
+
+
+def block_dots(qt: QTensor, xq: torch.Tensor, m: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Exact int32 block dots [m, n, nb(, 2)] and the f32 outputs of the same GEMV launch."""
+    n, k = qt.shape
+    nb = k // qt.dtype().block_size()
+    per = 2 if qt.dtype() == GgmlDType.Q4K else 1
+    dots = torch.zeros((m, n, nb, per), dtype=torch.int32, device=qt.device)
+    y = torch.empty((m, n), dtype=torch.float32, device=qt.device)
+    with torch.cuda.device(qt.device):
+        _check(lib().qmm_block_dots(qt.handle, xq.data_ptr(), m, y.data_ptr(), n, dots.data_ptr(),
+                                    _stream(qt.device)))
+    return (dots if per == 2 else dots[..., 0]), y
+
+
+# ---------------------------------------------------------------------------
+# engine-level wrappers (crates/llm/candle-llm/src/primitives/{projection,quant}.rs)
+# ---------------------------------------------------------------------------
+
+class QuantSpec:
+    """Group-wise quantization spec: 4 bits -> Q4_K, 8 bits -> Q8_0 (projection.rs:16-52)."""
+
+    def __init__(self, dtype: GgmlDType):
+        self.dtype = GgmlDType(dtype)
+
+    @classmethod
+    def q4(cls) -> "QuantSpec":
+        return cls(GgmlDType.Q4K)
+
+    @classmethod
+    def q8(cls) -> "QuantSpec":
+        return cls(GgmlDType.Q8_0)
+
+    @classmethod
+    def from_bits(cls, bits: int) -> Optional["QuantSpec"]:
+        if bits == 4:
+            return cls.q4()
+        if bits == 8:
+            return cls.q8()
+        return None
+
+    def bits(self) -> int:
+        return 8 if self.dtype == GgmlDType.Q8_0 else 4
+
+    def __eq__(self, other) -> bool:
+        return isinstance(other, QuantSpec) and other.dtype == self.dtype
+
+    def __repr__(self) -> str:
+        return f"QuantSpec({self.dtype.name})"
+
+
+class QuantizedLinear:
+    """A linear projection with a GGML block-quantized weight (quant.rs:17-43)."""
+
+    def __init__(self, inner: QMatMul, bias: Optional[torch.Tensor]):
+        self.inner = inner
+        self.bias = bias
+
+    @classmethod
+    def quantize(cls, weight: torch.Tensor, dtype: GgmlDType, bias: Optional[torch.Tensor] = None) -> "QuantizedLinear":
+        qt = QTensor.quantize(weight.to(torch.float32), dtype)
+        return cls(QMatMul.from_qtensor(qt), bias)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        y = self.inner.forward(x.to(torch.float32)).to(x.dtype)
+        if self.bias is not None:
+            y = y + self.bias
+        return y
+
+    __call__ = forward
+
+
+class Projection:
+    """A projection weight that is dense or quantized (projection.rs:56-95)."""
+
+    def __init__(self, dense_weight: Optional[torch.Tensor] = None, dense_bias: Optional[torch.Tensor] = None,
+                 quantized: Optional[QuantizedLinear] = None):
+        self._w = dense_weight
+        self._b = dense_bias
+        self._q = quantized
+
+    @classmethod
+    def load(cls, weight: torch.Tensor, quant: Optional[QuantSpec]) -> "Projection":
+        return cls.load_with_bias(weight, None, quant)
+
+    @classmethod
+    def load_with_bias(cls, weight: torch.Tensor, bias: Optional[torch.Tensor],
+                       quant: Optional[QuantSpec]) -> "Projection":
+        if quant is None:
+            return cls(dense_weight=weight, dense_bias=bias)
+        return cls(quantized=QuantizedLinear.quantize(weight, quant.dtype, bias))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self._q is not None:
+            return self._q.forward(x)
+        return torch.nn.functional.linear(x, self._w, self._b)
+
+    __call__ = forward
+
+    def is_quantized(self) -> bool:
+        return self._q is not None

@@ -1,0 +1,274 @@
+"""GPU parity of the HIP path against the CPU oracle (run on an MI355X).
+
+Bars (from the task's parity contract):
+  * byte / integer work bit-exact: activation quantizers (Q8_K, Q8_0), weight
+    quantizers (Q4_K, Q6_K, Q8_0), GGML import/export, dequantization, and
+    every per-(row, super-block) integer block dot;
+  * f32 outputs: max|y_gpu - y_cpu| / rms(y_cpu) <= 1e-3 (TOL below).
+Sizes: small shapes where the oracle's per-block dump is cheap, and the
+BASELINE configuration shapes for the f32 outputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from inference_amd import GgmlDType, QMatMul, QTensor, QuantizedLinear, QmmError, block_dots, quantize_rows
+from inference_amd import matmul_q
+from inference_amd.synth import normal
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # max|dy| / rms(y_ref), the north-star tolerance for f32 outputs
+DEV = torch.device("cuda", 0)
+ORC = {GgmlDType.Q8_0: orc.Q8_0, GgmlDType.Q4K: orc.Q4K, GgmlDType.Q6K: orc.Q6K, GgmlDType.Q8K: orc.Q8K}
+WEIGHT_TYPES = [GgmlDType.Q4K, GgmlDType.Q6K, GgmlDType.Q8_0]
+
+
+def rel_err(y, y_ref):
+    y_ref = np.asarray(y_ref, dtype=np.float64)
+    rms = np.sqrt(np.mean(y_ref ** 2))
+    return float(np.abs(np.asarray(y, dtype=np.float64) - y_ref).max() / rms)
+
+
+def special_activation_rows(k):
+    """Rows exercising the Q8_K / Q8_0 edge cases: zero blocks, ties, sign of the max, clamping."""
+    rows = []
+    z = np.zeros(k, np.float32)
+    rows.append(z.copy())  # all-zero -> d = 0, q = 0, bsums = 0
+    t = np.zeros(k, np.float32)
+    t[0] = -128.0  # Q8_K: iscale = 1 exactly -> x.5 values are exact ties (round away from zero)
+    t[1:16] = np.array([2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 3.5, -3.5, 126.5, -126.5, 7.5, 11.5, -0.5, 0.5, 64.5],
+                       np.float32)
+    rows.append(t)
+    c = np.zeros(k, np.float32)
+    c[::2] = -1.0
+    c[1::2] = 1.0  # first max is -1 -> iscale = +128, +1 clamps to +127
+    rows.append(c)
+    c2 = -c  # first max is +1 -> iscale = -128
+    rows.append(c2)
+    s = np.zeros(k, np.float32)
+    s[k // 2 + 3] = 3.0  # single non-zero in a later block
+    rows.append(s)
+    q = np.zeros(k, np.float32)
+    q[:32] = np.arange(-16, 16, dtype=np.float32) * (127.0 / 16.0)  # Q8_0 ties around d
+    if k >= 64:
+        q[32:64] = 127.0 * np.linspace(-1, 1, 32, dtype=np.float32)
+    rows.append(q)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("m,k", [(1, 256), (1, 4096), (3, 4096), (8, 14336), (2, 512)])
+def test_q8k_activation_quantizer_bit_exact(m, k):
+    x = np.concatenate([normal(10 + m, (m, k)), special_activation_rows(k)])
+    xq = quantize_rows(GgmlDType.Q8K, torch.from_numpy(x).to(DEV)).cpu().numpy()
+    ref = orc.quantize(orc.Q8K, x)
+    assert xq.shape == ref.shape
+    assert np.array_equal(xq, ref)
+
+
+@pytest.mark.parametrize("m,k", [(1, 32), (1, 4096), (5, 4096), (2, 14336)])
+def test_q8_0_activation_quantizer_bit_exact(m, k):
+    x = np.concatenate([normal(20 + m, (m, k)), special_activation_rows(k)])
+    xq = quantize_rows(GgmlDType.Q8_0, torch.from_numpy(x).to(DEV)).cpu().numpy()
+    ref = orc.quantize(orc.Q8_0, x)
+    assert np.array_equal(xq, ref)
+
+
+def test_activation_quantizer_honours_row_stride():
+    x = normal(30, (4, 8192))
+    xt = torch.from_numpy(x).to(DEV)[:, 1024:1024 + 4096]  # row stride 8192, offset view
+    xq = quantize_rows(GgmlDType.Q8K, xt).cpu().numpy()
+    assert np.array_equal(xq, orc.quantize(orc.Q8K, np.ascontiguousarray(x[:, 1024:1024 + 4096])))
+
+
+def special_weight_rows(k):
+    rows = [np.zeros(k, np.float32), np.full(k, 0.5, np.float32), np.full(k, -0.25, np.float32)]
+    one_hot = np.zeros(k, np.float32)
+    one_hot[5] = 1.0
+    rows.append(one_hot)
+    rows.append(normal(41, (k,), 1e-6))  # f16 scales in the subnormal range
+    rows.append(normal(42, (k,), 100.0))
+    rows.append(np.abs(normal(43, (k,), 0.02)))  # non-negative rows: min clamps to 0
+    rows.append(-np.abs(normal(44, (k,), 0.02)))
+    ramp = np.linspace(-1, 1, k, dtype=np.float32)
+    rows.append(ramp)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("dt", WEIGHT_TYPES)
+def test_weight_quantizer_bit_exact(dt):
+    k = 4096
+    w = np.concatenate([normal(40, (48, k), 0.02), special_weight_rows(k)])
+    qt = QTensor.quantize(torch.from_numpy(w).to(DEV), dt)
+    assert qt.shape == w.shape and qt.dtype() == dt
+    got = qt.to_ggml()
+    ref = orc.quantize(ORC[dt], w).reshape(-1)
+    assert got.size == ref.size == qt.storage_size_in_bytes()
+    mism = np.flatnonzero(got != ref)
+    assert mism.size == 0, f"{mism.size} bytes differ, first at {mism[:8]}"
+
+
+@pytest.mark.parametrize("dt", WEIGHT_TYPES)
+def test_ggml_import_export_and_dequantize_bit_exact(dt):
+    n, k = 40, 1024
+    w = np.concatenate([normal(50, (n, k), 0.02), special_weight_rows(k)])
+    ref_bytes = orc.quantize(ORC[dt], w)
+    for src in (ref_bytes, torch.from_numpy(ref_bytes).to(DEV)):  # host and device GGML bytes
+        qt = QTensor.from_ggml(src, dt, w.shape, device=DEV)
+        assert np.array_equal(qt.to_ggml(), ref_bytes.reshape(-1))
+        deq = qt.dequantize().cpu().numpy()
+        ref = orc.dequantize(ORC[dt], ref_bytes, w.size).reshape(w.shape)
+        assert np.array_equal(deq.view(np.uint32), ref.view(np.uint32))
+
+
+BLOCK_DOT_CASES = [
+    (GgmlDType.Q4K, 64, 256), (GgmlDType.Q4K, 37, 2048), (GgmlDType.Q4K, 96, 4096), (GgmlDType.Q4K, 24, 14336),
+    (GgmlDType.Q6K, 64, 256), (GgmlDType.Q6K, 37, 2048), (GgmlDType.Q6K, 96, 4096), (GgmlDType.Q6K, 24, 14336),
+    (GgmlDType.Q8_0, 64, 32), (GgmlDType.Q8_0, 37, 2048), (GgmlDType.Q8_0, 96, 4096), (GgmlDType.Q8_0, 8, 14336),
+]
+
+
+@pytest.mark.parametrize("dt,n,k", BLOCK_DOT_CASES)
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_block_dots_bit_exact_and_outputs(dt, n, k, m):
+    w = np.concatenate([normal(60, (n, k), 0.02), special_weight_rows(k)[:3]])
+    wq = orc.quantize(ORC[dt], w)
+    x = normal(61 + m, (m, k))
+    x[0, :k // 2] *= 50.0  # uneven activation scales across blocks
+    qt = QTensor.from_ggml(wq, dt, w.shape, device=DEV)
+    vt = dt.vec_dot_type()
+    xq = quantize_rows(vt, torch.from_numpy(x).to(DEV))
+    dots, y = block_dots(qt, xq, m)
+    ref = orc.block_dots(ORC[dt], wq, xq.cpu().numpy(), k)
+    assert np.array_equal(dots.cpu().numpy(), ref)
+    y_ref = orc.matmul_prequant(ORC[dt], xq.cpu().numpy(), wq, k)
+    assert rel_err(y.cpu().numpy(), y_ref) <= TOL
+    # the plain GEMV launch (no dump) gives the same outputs
+    y2 = matmul_q(qt, xq, m).cpu().numpy()
+    assert rel_err(y2, y_ref) <= TOL
+
+
+@pytest.mark.parametrize("ru", ["4,2", "2,2", "1,4", "1,8"])
+@pytest.mark.parametrize("dt", WEIGHT_TYPES)
+def test_every_launch_shape_is_correct(dt, ru, monkeypatch):
+    """All compiled (rows/wave, loads/row) variants, on ragged row counts."""
+    monkeypatch.setenv("QMM_GEMV_RU", ru)
+    for n, k in ((1, 256), (13, 2048), (70, 4096)):
+        w = normal(70 + n, (n, k), 0.02)
+        wq = orc.quantize(ORC[dt], w)
+        qt = QTensor.from_ggml(wq, dt, w.shape, device=DEV)
+        for m in (1, 2, 8):
+            x = normal(71, (m, k))
+            xq = quantize_rows(dt.vec_dot_type(), torch.from_numpy(x).to(DEV))
+            dots, y = block_dots(qt, xq, m)
+            assert np.array_equal(dots.cpu().numpy(), orc.block_dots(ORC[dt], wq, xq.cpu().numpy(), k))
+            assert rel_err(y.cpu().numpy(), orc.matmul_prequant(ORC[dt], xq.cpu().numpy(), wq, k)) <= TOL
+
+
+def test_grid_cap_keeps_results(monkeypatch):
+    """A capped grid makes every wave loop over several row groups."""
+    monkeypatch.setenv("QMM_GEMV_MAXWG", "3")
+    n, k = 300, 4096
+    w = normal(80, (n, k), 0.02)
+    wq = orc.quantize(orc.Q4K, w)
+    qt = QTensor.from_ggml(wq, GgmlDType.Q4K, w.shape, device=DEV)
+    x = normal(81, (2, k))
+    y = QMatMul.from_qtensor(qt).forward(torch.from_numpy(x).to(DEV)).cpu().numpy()
+    assert rel_err(y, orc.matmul(orc.Q4K, x, wq, k)) <= TOL
+
+
+CONFIG_SHAPES = [
+    (GgmlDType.Q8_0, 4096, 4096, 0, 1),      # config 1 (seeds 0 / 1)
+    (GgmlDType.Q4K, 4096, 4096, 2, 3),       # config 2: q_proj
+    (GgmlDType.Q4K, 1024, 4096, 2, 3),       # k/v_proj
+    (GgmlDType.Q4K, 14336, 4096, 2, 3),      # gate/up
+    (GgmlDType.Q4K, 4096, 14336, 2, 3),      # down
+    (GgmlDType.Q6K, 1024, 4096, 4, 3),       # config 3: attn_v
+    (GgmlDType.Q6K, 4096, 14336, 4, 3),      # ffn_down
+]
+
+
+@pytest.mark.parametrize("dt,n,k,wseed,xseed", CONFIG_SHAPES)
+def test_config_shapes_match_cpu_path(dt, n, k, wseed, xseed):
+    w = normal(wseed, (n, k), 0.02)
+    wq = orc.quantize(ORC[dt], w)
+    qt = QTensor.from_ggml(wq, dt, (n, k), device=DEV)
+    x = normal(xseed, (1, k))
+    y = QMatMul.from_qtensor(qt).forward(torch.from_numpy(x).to(DEV)).cpu().numpy()
+    y_ref = orc.matmul(ORC[dt], x, wq, k)
+    assert rel_err(y, y_ref) <= TOL
+    # sampled exact block dots at full size (rows spread over the matrix)
+    rows = np.linspace(0, n - 1, 8).astype(int)
+    xq = quantize_rows(dt.vec_dot_type(), torch.from_numpy(x).to(DEV))
+    dots, _ = block_dots(qt, xq, 1)
+    ref = orc.block_dots(ORC[dt], wq[rows], xq.cpu().numpy(), k)
+    assert np.array_equal(dots.cpu().numpy()[:, rows], ref)
+
+
+def test_batched_rows_beyond_eight_are_chunked():
+    n, k = 200, 2048
+    w = normal(90, (n, k), 0.02)
+    wq = orc.quantize(orc.Q6K, w)
+    qt = QTensor.from_ggml(wq, GgmlDType.Q6K, w.shape, device=DEV)
+    x = normal(91, (2, 13, k))  # [b, s, k] -> 26 rows
+    y = QMatMul.from_qtensor(qt).forward(torch.from_numpy(x).to(DEV))
+    assert tuple(y.shape) == (2, 13, n)
+    assert rel_err(y.cpu().numpy().reshape(26, n), orc.matmul(orc.Q6K, x.reshape(26, k), wq, k)) <= TOL
+
+
+def test_reference_quantized_linear_q8_approximates_dense():
+    """crates/llm/candle-llm/src/primitives/quant.rs:52-80 on the GPU path."""
+    out, inn = 4, 256
+    i = np.arange(out * inn)
+    w = ((i * 7 % 13).astype(np.float32) / 13.0 - 0.5).reshape(out, inn)
+    x = (np.arange(inn, dtype=np.float32) / inn - 0.5).reshape(1, inn)
+    dense = x @ w.T
+    q = QuantizedLinear.quantize(torch.from_numpy(w).to(DEV), GgmlDType.Q8_0, None)
+    got = q.forward(torch.from_numpy(x).to(DEV)).cpu().numpy()
+    assert np.all(np.abs(dense - got) < 0.05)
+
+
+def test_reference_q4k_cosine_vs_dense():
+    """candle-gen/src/quant/mod.rs:1141-1172: Q4_K 64x256, x 4x256, cos > 0.99 vs dense."""
+    w = normal(100, (64, 256), 0.1)
+    x = normal(101, (4, 256))
+    q = QuantizedLinear.quantize(torch.from_numpy(w).to(DEV), GgmlDType.Q4K, None)
+    got = q.forward(torch.from_numpy(x).to(DEV)).cpu().numpy().ravel()
+    dense = (x @ w.T).ravel()
+    cos = float(np.dot(got, dense) / np.linalg.norm(got) / np.linalg.norm(dense))
+    assert cos > 0.99
+
+
+def test_bias_and_dtype_cast_in_quantized_linear():
+    w = normal(110, (32, 512), 0.05)
+    b = normal(111, (32,))
+    x = normal(112, (3, 512))
+    q = QuantizedLinear.quantize(torch.from_numpy(w).to(DEV), GgmlDType.Q4K, torch.from_numpy(b).to(DEV))
+    y16 = q.forward(torch.from_numpy(x).to(DEV).to(torch.bfloat16))
+    assert y16.dtype == torch.bfloat16
+    y = q.forward(torch.from_numpy(x).to(DEV)).cpu().numpy()
+    wq = orc.quantize(orc.Q4K, w)
+    assert rel_err(y - b, orc.matmul(orc.Q4K, x, wq, 512)) <= TOL
+
+
+def test_errors_are_raised_not_swallowed():
+    qt = QTensor.quantize(torch.from_numpy(normal(120, (8, 512), 0.02)).to(DEV), GgmlDType.Q4K)
+    mm = QMatMul.from_qtensor(qt)
+    with pytest.raises(QmmError):
+        mm.forward(torch.zeros(1, 512, device=DEV, dtype=torch.float16))  # f32 required
+    with pytest.raises(QmmError):
+        mm.forward(torch.zeros(1, 256, device=DEV))  # K mismatch
+    with pytest.raises(QmmError):
+        QTensor.quantize(torch.zeros(4, 200, device=DEV), GgmlDType.Q4K)  # not a block multiple
+    with pytest.raises(QmmError):
+        QTensor.from_ggml(np.zeros(100, np.uint8), GgmlDType.Q4K, (1, 256), device=DEV)  # wrong byte count
+
+
+def test_repeated_calls_are_deterministic():
+    qt = QTensor.quantize(torch.from_numpy(normal(130, (4096, 4096), 0.02)).to(DEV), GgmlDType.Q4K)
+    x = torch.from_numpy(normal(131, (1, 4096))).to(DEV)
+    mm = QMatMul.from_qtensor(qt)
+    y0 = mm.forward(x)
+    for _ in range(5):
+        assert torch.equal(mm.forward(x), y0)
