@@ -84,6 +84,7 @@ def run_gemv_set(torch, dev, args):
     log(f"[bench] building {copies} weight copies of the Q4_K GEMV set ({copies * set_weight_bytes / 2**20:.0f} MiB)")
     sets = build_set(torch, dev, dt, copies)
 
+    shapes = {name: (n, k) for name, n, k in GEMV_SET}
     x4096 = torch.from_numpy(normal(3, (1, 4096))).to(dev)
     x14336 = torch.from_numpy(normal(3, (1, 14336))).to(dev)
     xq4096 = torch.empty((1, 16 * 292), dtype=torch.uint8, device=dev)
@@ -91,14 +92,41 @@ def run_gemv_set(torch, dev, args):
     outs = {name: torch.empty((1, n), dtype=torch.float32, device=dev) for name, n, _ in GEMV_SET}
     L = qmm.lib()
 
-    def step(layer):
-        s = qmm._stream(dev)
-        qmm._check(L.qmm_quantize_rows(int(vt), x4096.data_ptr(), 1, 4096, 4096, xq4096.data_ptr(), s))
-        for name, n, k in GEMV_SET[:5]:
-            qmm._check(L.qmm_matmul_q(layer[name].handle, xq4096.data_ptr(), 1, outs[name].data_ptr(), n, s))
-        qmm._check(L.qmm_quantize_rows(int(vt), x14336.data_ptr(), 1, 14336, 14336, xq14336.data_ptr(), s))
-        qmm._check(L.qmm_matmul_q(layer["down_proj"].handle, xq14336.data_ptr(), 1, outs["down_proj"].data_ptr(),
-                                  4096, s))
+    def q8k(x, xq, k):
+        qmm._check(L.qmm_quantize_rows(int(vt), x.data_ptr(), 1, k, k, xq.data_ptr(), qmm._stream(dev)))
+
+    def gemv(layer, name):
+        n, k = shapes[name]
+        xq = xq4096 if k == 4096 else xq14336
+        qmm._check(L.qmm_matmul_q(layer[name].handle, xq.data_ptr(), 1, outs[name].data_ptr(), n, qmm._stream(dev)))
+
+    def step_serial(layer):
+        q8k(x4096, xq4096, 4096)
+        for name in ("q_proj", "k_proj", "v_proj", "gate_proj", "up_proj"):
+            gemv(layer, name)
+        q8k(x14336, xq14336, 14336)
+        gemv(layer, "down_proj")
+
+    # The six GEMVs of the set are independent given their activations, so a
+    # step can also run them on four streams (fork/join inside the graph), the
+    # way a decode layer overlaps q/k/v and gate/up.
+    side = [torch.cuda.Stream(device=dev) for _ in range(3)]
+    branches = [("q_proj", "k_proj"), ("v_proj", "gate_proj"), ("up_proj",), ("down_proj",)]
+
+    def step_concurrent(layer):
+        main = torch.cuda.current_stream(dev)
+        q8k(x4096, xq4096, 4096)
+        q8k(x14336, xq14336, 14336)
+        for sb in side:
+            sb.wait_stream(main)
+        for br, st in zip(branches, [main] + side):
+            with torch.cuda.stream(st):
+                for name in br:
+                    gemv(layer, name)
+        for sb in side:
+            main.wait_stream(sb)
+
+    step = step_concurrent if args.schedule == "concurrent" else step_serial
 
     def gate_only(layer):
         s = qmm._stream(dev)
@@ -202,7 +230,7 @@ def cpu_baseline(sets, budget_s):
             orc.matmul(orc.Q4K, x4096 if k == 4096 else x14336, w[name], k, nthreads=threads)
         reps += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 1000:
+        if el >= budget_s or reps >= 100000:
             break
     return {"value": round(total_bytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{reps} passes of the Q4_K GEMV set (M=1, 6 projections) with the oracle's generic "
@@ -215,7 +243,9 @@ def main():
     ap.add_argument("--steps", type=int, default=240)
     ap.add_argument("--warmup", type=int, default=24)
     ap.add_argument("--rotate-mb", type=int, default=640, help="distinct weight bytes rotated (MiB)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 = skip)")
+    ap.add_argument("--schedule", choices=("concurrent", "serial"), default="concurrent",
+                    help="run the set's independent GEMVs on 4 streams or one after another")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -242,7 +272,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": "q4k_decode_gemv_set_llama3_8b_m1", "shapes_out_in": [[n, k] for _, n, k in GEMV_SET],
                    "batch_m": 1, "weights": "Q4_K, N(0,0.02^2) seed 2", "activations": "Q8_K on device, seed 3",
-                   "weight_copies_rotated": res["weight_copies"]},
+                   "weight_copies_rotated": res["weight_copies"], "schedule": args.schedule},
         "hbm_frac": round(res["value"] / HBM_PEAK_GBS, 4),
         "roofline": res["roofline"],
         "per_shape": res["per_shape"],

@@ -111,11 +111,20 @@ size_t qmm_matmul_workspace_size(const qmm_qtensor *w, int64_t m);
 /* QMatMul::forward: y[i, j] = sum_k x[i, k] * W[j, k] for i < m, j < n, with x
  * quantized to W's vec-dot type first (as Candle's CPU path does).
  * x: f32 [m, k] (row stride ldx); y: f32 [m, n] (row stride ldy); ws: device
- * scratch of qmm_matmul_workspace_size(w, m) bytes. m = 1..8 runs the decode
- * GEMV (replaces launch_mmvq_gguf_*_f32_plain); larger m runs the GEMM path
- * (replaces launch_mmq_gguf_*). */
+ * scratch of qmm_matmul_workspace_size(w, m) bytes (may be NULL for m <= 2,
+ * where one kernel quantizes x in its prologue). m = 1..8 runs the decode
+ * GEMV (replaces launch_mmvq_gguf_quantize_q8_1_f32 + launch_mmvq_gguf_*_f32_plain);
+ * larger m runs the GEMM path (replaces launch_mmq_gguf_*). */
 int qmm_matmul(const qmm_qtensor *w, const float *x, int64_t m, int64_t ldx, float *y, int64_t ldy,
                void *ws, size_t ws_bytes, void *stream);
+
+/* `count` (1..4) QMatMul::forward calls on one input in a single launch:
+ * y[j] = x . W[j]^T for weights of one dtype and k (e.g. a layer's q/k or
+ * gate/up projections, which the reference engine runs as separate
+ * QuantizedLinear::forward calls on the same activation, llama.rs:1066-1092,
+ * 1386-1391). ldy[j] is the row stride of y[j]; ws as for qmm_matmul. */
+int qmm_matmul_multi(const qmm_qtensor *const *w, int count, const float *x, int64_t m, int64_t ldx,
+                     float *const *y, const int64_t *ldy, void *ws, size_t ws_bytes, void *stream);
 
 /* The same with activations already quantized (xq: m rows of vec-dot blocks,
  * as produced by qmm_quantize_rows). */

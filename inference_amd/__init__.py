@@ -13,6 +13,7 @@ from .qmm import (  # noqa: F401
     QuantizedLinear,
     QuantSpec,
     block_dots,
+    matmul_multi,
     matmul_q,
     quantize_rows,
 )

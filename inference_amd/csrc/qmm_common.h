@@ -55,4 +55,40 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Max over the 64 lanes of a wave (every lane receives it): DPP inside rows
+// of 16 lanes, then the four row results are read with v_readlane.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f<0xb1>(v));
+  v = fmaxf(v, dpp_f<0x4e>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+
+// Min over the 64 lanes of a wave (every lane receives it).
+__device__ __forceinline__ int wave_min(int v) {
+  v = min(v, dpp_i<0xb1>(v));
+  v = min(v, dpp_i<0x4e>(v));
+  v = min(v, dpp_i<0x141>(v));
+  v = min(v, dpp_i<0x140>(v));
+  const int a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+  const int c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+  return min(min(a, b), min(c, d));
+}
+
+// Sum over aligned groups of 4 lanes (every lane of the group receives it).
+__device__ __forceinline__ int quad_sum(int v) {
+  v += dpp_i<0xb1>(v);
+  return v + dpp_i<0x4e>(v);
+}
+
 }  // namespace qmm

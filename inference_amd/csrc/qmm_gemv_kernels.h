@@ -1,15 +1,20 @@
 // Decode GEMV (M = 1..8 activation rows) over Q8_0 / Q4_K / Q6_K weights.
 //
 // Work split (wave64, CDNA4):
-//   * a k-quant super-block is decoded by 8 lanes, each owning one 16-byte
-//     slice of its quants (one dwordx4 load); a wave-wide load therefore
-//     covers 8 consecutive super-blocks of a row, i.e. ~1.1 KB (Q4_K) or
-//     ~1.7 KB (Q6_K) of contiguous HBM. Q8_0 uses 2 lanes per 32-block.
+//   * a k-quant super-block is decoded by 4 lanes, each owning 32 bytes of
+//     its quants (two dwordx4 loads) plus the block header, so one wave-wide
+//     iteration covers 16 consecutive super-blocks of a row: 2304 B (Q4_K) or
+//     3360 B (Q6_K) of contiguous HBM. A Q8_0 block (32 quants) is one lane's,
+//     64 blocks per iteration.
 //   * the activation rows (already quantized to Q8_K / Q8_0) are staged once
-//     per workgroup in LDS, permuted so that each lane reads its two 16-byte
-//     operand slices and its pair of 16-element sums with single LDS reads;
+//     per workgroup in LDS, in the order each lane consumes them, with the
+//     16-byte chunks XOR-swizzled so that a wave's ds_read_b128 hits distinct
+//     banks; each lane also gets its 32-element (Q4_K) or 16-element (Q6_K)
+//     activation sums precombined.
+//   * the first batch of weight loads is issued before the activation is
+//     staged, so the HBM latency overlaps the LDS fill and the barrier.
 //   * each wave owns R weight rows and issues U iterations of loads for all of
-//     them before using any, so every lane has R*U 16-byte loads in flight;
+//     them before using any, so every lane has R*U*32 bytes in flight;
 //   * integer block dots use v_dot4_i32_i8; the f32 row sums are reduced
 //     across the wave with DPP row operations and two cross-row exchanges.
 // Integer decomposition per super-block (the algebraic image of the GGML
@@ -21,6 +26,7 @@
 #pragma once
 
 #include "qmm_common.h"
+#include "qmm_quant_kernels.h"
 
 namespace qmm {
 
@@ -28,48 +34,48 @@ template <int FMT>
 struct FmtInfo;
 template <>
 struct FmtInfo<kFmtQ80> {
-  static constexpr int kLanesPerBlock = 2;
+  static constexpr int kLanesPerBlock = 1;
   static constexpr int kBlockElems = 32;
   static constexpr int kBodyBytes = kQ80Body;
+  static constexpr int kLdsBlock = 32 + 4;  // q8[32] | d (f32)
 };
 template <>
 struct FmtInfo<kFmtQ4K> {
-  static constexpr int kLanesPerBlock = 8;
+  static constexpr int kLanesPerBlock = 4;
   static constexpr int kBlockElems = 256;
   static constexpr int kBodyBytes = kQ4KBytes;
+  static constexpr int kLdsBlock = 256 + 32 + 4;  // q8[256] | sums u32[8] | d (f32)
 };
 template <>
 struct FmtInfo<kFmtQ6K> {
-  static constexpr int kLanesPerBlock = 8;
+  static constexpr int kLanesPerBlock = 4;
   static constexpr int kBlockElems = 256;
   static constexpr int kBodyBytes = kQ6KBody;
+  static constexpr int kLdsBlock = 256 + 32 + 4;
 };
 
-// LDS bytes per staged activation block.
+// First activation element of chunk k (16 elements, k = 0..3) of lane l of a
+// k-quant super-block.
+//   Q4_K lane l holds qs[32l, 32l+32): low nibbles are elements 64l + [0,32)
+//        (chunks 0,1), high nibbles 64l + 32 + [0,32) (chunks 2,3).
+//   Q6_K lane l holds ql[64h + 32p, +32) (h = l/2, p = l%2): low nibbles are
+//        elements 128h + 32p + [0,32) (chunks 0,1), high nibbles 64 further (2,3).
 template <int FMT>
-constexpr int lds_block_bytes() {
-  return FMT == kFmtQ80 ? 32 + 4 : 256 + 32 + 4;
+__device__ __forceinline__ int act_chunk(int l, int k) {
+  return FMT == kFmtQ4K ? 64 * l + 16 * k : 128 * (l >> 1) + 32 * (l & 1) + 64 * (k >> 1) + 16 * (k & 1);
 }
 
-// Start of the two 16-element activation slices lane l (0..7) of a k-quant
-// super-block multiplies.
-//   Q4_K lane l: quants qs[16l, 16l+16): low nibbles are elements
-//                64(l/2) + 16(l%2) + i, high nibbles 32 further.
-//   Q6_K lane l: ql[16l, 16l+16) low nibbles are elements 128(l/4) + 16(l%4) + i,
-//                high nibbles 64 further.
-template <int FMT>
-__device__ __forceinline__ int act_slice0(int l) {
-  return FMT == kFmtQ4K ? 64 * (l >> 1) + 16 * (l & 1) : 128 * (l >> 2) + 16 * (l & 3);
+// LDS position (16-byte slot) of chunk k of lane l in block b.
+__device__ __forceinline__ int kq_slot(int b, int l, int k) {
+  return 4 * l + (k ^ ((l >> 1) | ((b & 1) << 1)));
 }
-template <int FMT>
-constexpr int act_slice_gap() {
-  return FMT == kFmtQ4K ? 32 : 64;
-}
+__device__ __forceinline__ int q80_slot(int b, int k) { return k ^ ((b >> 2) & 1); }
 
-// Stage m_rows activation rows of nb blocks each into LDS.
-//   k-quants: q8[blk][256] = [slice0 of lanes 0..7][slice1 of lanes 0..7],
-//             bsum pairs u32[blk][8], d f32[blk]
-//   Q8_0:     q8[blk][32], d f32[blk]
+// Stage nblk activation blocks (M rows of nb blocks, contiguous) into LDS.
+//   k-quants: q8 [blk][256] (swizzled chunks), sums u32 [blk][8], d f32 [blk]
+//     Q4_K sums: lane l -> (bsum_4l + bsum_4l+1) | (bsum_4l+2 + bsum_4l+3) << 16
+//     Q6_K sums: lane l -> two u32: bsums of its chunks (0,1) and (2,3)
+//   Q8_0: q8 [blk][32] (swizzled halves), d f32 [blk]
 template <int FMT>
 __device__ __forceinline__ void stage_act(const uint8_t* __restrict__ xq, int nblk, uint8_t* lds) {
   if constexpr (FMT == kFmtQ80) {
@@ -83,61 +89,95 @@ __device__ __forceinline__ void stage_act(const uint8_t* __restrict__ xq, int nb
       v.y = q[2] | ((uint32_t)q[3] << 16);
       v.z = q[4] | ((uint32_t)q[5] << 16);
       v.w = q[6] | ((uint32_t)q[7] << 16);
-      *reinterpret_cast<uint4*>(lds + 32 * blk + 16 * half) = v;
+      *reinterpret_cast<uint4*>(lds + 32 * blk + 16 * q80_slot(blk, half)) = v;
       if (half == 0) ld[blk] = h2f(s[0]);
     }
   } else {
-    uint32_t* lb = reinterpret_cast<uint32_t*>(lds + 256 * nblk);
-    float* ld = reinterpret_cast<float*>(lb + 8 * nblk);
-    for (int t = threadIdx.x; t < 8 * nblk; t += blockDim.x) {
-      const int blk = t >> 3, l = t & 7;
+    uint32_t* lsum = reinterpret_cast<uint32_t*>(lds + 256 * nblk);
+    float* ld = reinterpret_cast<float*>(lsum + 8 * nblk);
+    for (int t = threadIdx.x; t < 16 * nblk; t += blockDim.x) {
+      const int blk = t >> 4, l = (t >> 2) & 3, k = t & 3;
       const uint8_t* s = xq + (size_t)kQ8KBytes * blk;
-      const uint32_t* q = reinterpret_cast<const uint32_t*>(s + 4);
-      const int s0 = act_slice0<FMT>(l), s1 = s0 + act_slice_gap<FMT>();
-      uint4 a, b;
-      a.x = q[s0 / 4 + 0];
-      a.y = q[s0 / 4 + 1];
-      a.z = q[s0 / 4 + 2];
-      a.w = q[s0 / 4 + 3];
-      b.x = q[s1 / 4 + 0];
-      b.y = q[s1 / 4 + 1];
-      b.z = q[s1 / 4 + 2];
-      b.w = q[s1 / 4 + 3];
-      *reinterpret_cast<uint4*>(lds + 256 * blk + 16 * l) = a;
-      *reinterpret_cast<uint4*>(lds + 256 * blk + 128 + 16 * l) = b;
-      const uint16_t* bs = reinterpret_cast<const uint16_t*>(s + 4 + 256);
-      lb[8 * blk + l] = (uint32_t)bs[s0 / 16] | ((uint32_t)bs[s1 / 16] << 16);
-      if (l == 0) ld[blk] = *reinterpret_cast<const float*>(s);
+      const uint32_t* q = reinterpret_cast<const uint32_t*>(s + 4 + act_chunk<FMT>(l, k));
+      uint4 v;
+      v.x = q[0];
+      v.y = q[1];
+      v.z = q[2];
+      v.w = q[3];
+      *reinterpret_cast<uint4*>(lds + 256 * blk + 16 * kq_slot(blk, l, k)) = v;
+      const int16_t* bs = reinterpret_cast<const int16_t*>(s + 4 + 256);
+      if (k < 2) {
+        const int e0 = act_chunk<FMT>(l, 2 * k) / 16;  // chunks 2k and 2k+1
+        const int e1 = act_chunk<FMT>(l, 2 * k + 1) / 16;
+        if (FMT == kFmtQ4K) {
+          if (k == 0) {
+            const int a = bs[e0] + bs[e1];
+            const int b2 = bs[act_chunk<FMT>(l, 2) / 16] + bs[act_chunk<FMT>(l, 3) / 16];
+            lsum[8 * blk + l] = ((uint32_t)a & 0xffffu) | ((uint32_t)b2 << 16);
+          }
+        } else {
+          lsum[8 * blk + 2 * l + k] = ((uint32_t)(uint16_t)bs[e0]) | ((uint32_t)(uint16_t)bs[e1] << 16);
+        }
+      }
+      if (l == 0 && k == 0) ld[blk] = *reinterpret_cast<const float*>(s);
     }
   }
 }
 
-// One lane's share of one weight super-block.
+// One lane's share of one weight block.
 struct WSlice {
-  uint4 a;     // Q4_K: header (d, dmin, scales[12]); Q6_K: ql slice; Q8_0: qs slice
-  uint4 b;     // Q4_K: qs slice; Q6_K: qh slice
-  uint4 c;     // Q6_K: scales[16]
+  uint4 a;     // Q4_K: header (d, dmin, scales[12]); Q6_K: ql[0:16); Q8_0: qs[0:16)
+  uint4 b;     // Q4_K: qs[0:16);  Q6_K: ql[16:32); Q8_0: qs[16:32)
+  uint4 c;     // Q4_K: qs[16:32); Q6_K: qh[0:16)
+  uint4 e;     // Q6_K: qh[16:32)
+  uint4 f;     // Q6_K: scales[16]
   uint32_t d;  // Q6_K / Q8_0: f16 scale
 };
 
-// Weight row pointers: `wq` = block bodies, `wd` = separated f16 scales.
+// `wq` = block bodies (N rows x nb blocks), `wd` = separated f16 scales.
 template <int FMT>
 __device__ __forceinline__ void load_slice(WSlice& s, const uint8_t* __restrict__ wq,
                                            const uint16_t* __restrict__ wd, size_t blk, int l) {
   if constexpr (FMT == kFmtQ4K) {
     const uint8_t* p = wq + blk * kQ4KBytes;
     s.a = *reinterpret_cast<const uint4*>(p);
-    s.b = *reinterpret_cast<const uint4*>(p + 16 + 16 * l);
+    s.b = *reinterpret_cast<const uint4*>(p + 16 + 32 * l);
+    s.c = *reinterpret_cast<const uint4*>(p + 32 + 32 * l);
   } else if constexpr (FMT == kFmtQ6K) {
     const uint8_t* p = wq + blk * kQ6KBody;
-    s.a = *reinterpret_cast<const uint4*>(p + 16 * l);
-    s.b = *reinterpret_cast<const uint4*>(p + 128 + 32 * (l >> 2) + 16 * (l & 1));
-    s.c = *reinterpret_cast<const uint4*>(p + 192);
+    s.a = *reinterpret_cast<const uint4*>(p + 32 * l);
+    s.b = *reinterpret_cast<const uint4*>(p + 32 * l + 16);
+    s.c = *reinterpret_cast<const uint4*>(p + 128 + 32 * (l >> 1));
+    s.e = *reinterpret_cast<const uint4*>(p + 128 + 32 * (l >> 1) + 16);
+    s.f = *reinterpret_cast<const uint4*>(p + 192);
     s.d = wd[blk];
   } else {
-    s.a = *reinterpret_cast<const uint4*>(wq + blk * kQ80Body + 16 * l);
+    const uint8_t* p = wq + blk * kQ80Body;
+    s.a = *reinterpret_cast<const uint4*>(p);
+    s.b = *reinterpret_cast<const uint4*>(p + 16);
     s.d = wd[blk];
   }
+}
+
+__device__ __forceinline__ int dot16(uint4 w, uint4 x, int acc) {
+  acc = dot4(w.x, x.x, acc);
+  acc = dot4(w.y, x.y, acc);
+  acc = dot4(w.z, x.z, acc);
+  return dot4(w.w, x.w, acc);
+}
+
+__device__ __forceinline__ uint4 lo_nib(uint4 v) {
+  return make_uint4(v.x & 0x0f0f0f0fu, v.y & 0x0f0f0f0fu, v.z & 0x0f0f0f0fu, v.w & 0x0f0f0f0fu);
+}
+__device__ __forceinline__ uint4 hi_nib(uint4 v) {
+  return make_uint4((v.x >> 4) & 0x0f0f0f0fu, (v.y >> 4) & 0x0f0f0f0fu, (v.z >> 4) & 0x0f0f0f0fu,
+                    (v.w >> 4) & 0x0f0f0f0fu);
+}
+// 6-bit Q6_K quants (0..63) of 16 elements: 4 low bits from `ql` (already
+// shifted to the low nibble), 2 high bits at bit `sh` of `qh`.
+__device__ __forceinline__ uint4 q6_bytes(uint4 ql, uint4 qh, int sh) {
+  auto one = [sh](uint32_t l, uint32_t h) { return (l & 0x0f0f0f0fu) | (((h >> sh) & 0x03030303u) << 4); };
+  return make_uint4(one(ql.x, qh.x), one(ql.y, qh.y), one(ql.z, qh.z), one(ql.w, qh.w));
 }
 
 // Multiply one lane's slice with the staged activation block `xb` of each of
@@ -148,37 +188,30 @@ __device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t*
                                           int nblk, int xb, int nbx, bool ok, float (&acc)[M],
                                           int (&ia)[M], int (&ib)[M]) {
   if constexpr (FMT == kFmtQ4K) {
-    const uint32_t* lb = reinterpret_cast<const uint32_t*>(lds + 256 * nblk);
-    const float* ld = reinterpret_cast<const float*>(lb + 8 * nblk);
+    const uint32_t* lsum = reinterpret_cast<const uint32_t*>(lds + 256 * nblk);
+    const float* ld = reinterpret_cast<const float*>(lsum + 8 * nblk);
     const float dw = h2f(s.a.x), dm = h2f(s.a.x >> 16);
-    // 6-bit scale/min pairs of sub-blocks 2c and 2c+1, c = l/2 (get_scale_min_k4).
-    const int c = l >> 1;
-    const int sh = (c & 1) * 16;
+    // 6-bit scale/min of sub-blocks 2l and 2l+1 (get_scale_min_k4).
+    const int sh = (l & 1) * 16;
     const uint32_t A = s.a.y >> sh, B = s.a.z >> sh, C = s.a.w >> sh;
-    const bool upper = c >= 2;
+    const bool upper = l >= 2;
     const uint32_t scp = upper ? ((C & 0x0f0fu) | ((A >> 2) & 0x3030u)) : (A & 0x3f3fu);
     const uint32_t mnp = upper ? (((C >> 4) & 0x0f0fu) | ((B >> 2) & 0x3030u)) : (B & 0x3f3fu);
     const int sc0 = scp & 0xff, sc1 = (scp >> 8) & 0xff;
     const int m0 = mnp & 0xff, m1 = (mnp >> 8) & 0xff;
-    const uint32_t lo0 = s.b.x & 0x0f0f0f0fu, hi0 = (s.b.x >> 4) & 0x0f0f0f0fu;
-    const uint32_t lo1 = s.b.y & 0x0f0f0f0fu, hi1 = (s.b.y >> 4) & 0x0f0f0f0fu;
-    const uint32_t lo2 = s.b.z & 0x0f0f0f0fu, hi2 = (s.b.z >> 4) & 0x0f0f0f0fu;
-    const uint32_t lo3 = s.b.w & 0x0f0f0f0fu, hi3 = (s.b.w >> 4) & 0x0f0f0f0fu;
+    const uint4 w0 = lo_nib(s.b), w1 = lo_nib(s.c), w2 = hi_nib(s.b), w3 = hi_nib(s.c);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       const int bx = xb + m * nbx;
-      const uint8_t* e = lds + 256 * bx + 16 * l;
-      const uint4 x0 = *reinterpret_cast<const uint4*>(e);
-      const uint4 x1 = *reinterpret_cast<const uint4*>(e + 128);
-      int s0 = dot4(lo0, x0.x, 0);
-      s0 = dot4(lo1, x0.y, s0);
-      s0 = dot4(lo2, x0.z, s0);
-      s0 = dot4(lo3, x0.w, s0);
-      int s1 = dot4(hi0, x1.x, 0);
-      s1 = dot4(hi1, x1.y, s1);
-      s1 = dot4(hi2, x1.z, s1);
-      s1 = dot4(hi3, x1.w, s1);
-      const uint32_t bp = lb[8 * bx + l];
+      const uint8_t* e = lds + 256 * bx;
+      const int sw = (l >> 1) | ((bx & 1) << 1);
+      const uint4 x0 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (0 ^ sw)));
+      const uint4 x1 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (1 ^ sw)));
+      const uint4 x2 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (2 ^ sw)));
+      const uint4 x3 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (3 ^ sw)));
+      const int s0 = dot16(w1, x1, dot16(w0, x0, 0));
+      const int s1 = dot16(w3, x3, dot16(w2, x2, 0));
+      const uint32_t bp = lsum[8 * bx + l];
       const int bs0 = (int)(int16_t)(bp & 0xffffu), bs1 = (int)bp >> 16;
       const int isd = sc0 * s0 + sc1 * s1;
       const int ism = m0 * bs0 + m1 * bs1;
@@ -188,38 +221,35 @@ __device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t*
       ib[m] = ism;
     }
   } else if constexpr (FMT == kFmtQ6K) {
-    const uint32_t* lb = reinterpret_cast<const uint32_t*>(lds + 256 * nblk);
-    const float* ld = reinterpret_cast<const float*>(lb + 8 * nblk);
+    const uint32_t* lsum = reinterpret_cast<const uint32_t*>(lds + 256 * nblk);
+    const float* ld = reinterpret_cast<const float*>(lsum + 8 * nblk);
     const float dw = h2f(s.d);
-    const int h = l >> 2, j = l & 3;
-    const int sh0 = (j >> 1) * 2, sh1 = sh0 + 4;
-    const uint32_t w0 = h ? s.c.z : s.c.x, w1 = h ? s.c.w : s.c.y;
-    const int sc0 = (int)(int8_t)(w0 >> (8 * j)), sc1 = (int)(int8_t)(w1 >> (8 * j));
-    uint32_t q0[4], q1[4];
-    const uint32_t ql[4] = {s.a.x, s.a.y, s.a.z, s.a.w};
-    const uint32_t qh[4] = {s.b.x, s.b.y, s.b.z, s.b.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      q0[k] = (ql[k] & 0x0f0f0f0fu) | (((qh[k] >> sh0) & 0x03030303u) << 4);
-      q1[k] = ((ql[k] >> 4) & 0x0f0f0f0fu) | (((qh[k] >> sh1) & 0x03030303u) << 4);
-    }
+    const int h = l >> 1, p = l & 1;
+    // scales of the lane's four 16-element groups: 8h + 2p + {0, 1} and +4.
+    const uint32_t wlo = h ? s.f.z : s.f.x, whi = h ? s.f.w : s.f.y;
+    const uint32_t sl = wlo >> (16 * p), shh = whi >> (16 * p);
+    const int sc0 = (int)(int8_t)(sl & 0xff), sc1 = (int)(int8_t)((sl >> 8) & 0xff);
+    const int sc2 = (int)(int8_t)(shh & 0xff), sc3 = (int)(int8_t)((shh >> 8) & 0xff);
+    const int sh0 = 2 * p, sh1 = 2 * p + 4;
+    const uint4 w0 = q6_bytes(s.a, s.c, sh0);                // elements 128h + 32p + [0,16)
+    const uint4 w1 = q6_bytes(s.b, s.e, sh0);                // +16
+    const uint4 w2 = q6_bytes(hi_nib(s.a), s.c, sh1);        // +64
+    const uint4 w3 = q6_bytes(hi_nib(s.b), s.e, sh1);        // +80
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       const int bx = xb + m * nbx;
-      const uint8_t* e = lds + 256 * bx + 16 * l;
-      const uint4 x0 = *reinterpret_cast<const uint4*>(e);
-      const uint4 x1 = *reinterpret_cast<const uint4*>(e + 128);
-      int s0 = dot4(q0[0], x0.x, 0);
-      s0 = dot4(q0[1], x0.y, s0);
-      s0 = dot4(q0[2], x0.z, s0);
-      s0 = dot4(q0[3], x0.w, s0);
-      int s1 = dot4(q1[0], x1.x, 0);
-      s1 = dot4(q1[1], x1.y, s1);
-      s1 = dot4(q1[2], x1.z, s1);
-      s1 = dot4(q1[3], x1.w, s1);
-      const uint32_t bp = lb[8 * bx + l];
-      const int bs0 = (int)(int16_t)(bp & 0xffffu), bs1 = (int)bp >> 16;
-      const int is = sc0 * (s0 - 32 * bs0) + sc1 * (s1 - 32 * bs1);
+      const uint8_t* e = lds + 256 * bx;
+      const int sw = (l >> 1) | ((bx & 1) << 1);
+      const uint4 x0 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (0 ^ sw)));
+      const uint4 x1 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (1 ^ sw)));
+      const uint4 x2 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (2 ^ sw)));
+      const uint4 x3 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (3 ^ sw)));
+      const uint32_t b01 = lsum[8 * bx + 2 * l], b23 = lsum[8 * bx + 2 * l + 1];
+      const int t0 = dot16(w0, x0, 0) - 32 * (int)(int16_t)(b01 & 0xffffu);
+      const int t1 = dot16(w1, x1, 0) - 32 * ((int)b01 >> 16);
+      const int t2 = dot16(w2, x2, 0) - 32 * (int)(int16_t)(b23 & 0xffffu);
+      const int t3 = dot16(w3, x3, 0) - 32 * ((int)b23 >> 16);
+      const int is = sc0 * t0 + sc1 * t1 + sc2 * t2 + sc3 * t3;
       acc[m] += ok ? ld[bx] * (dw * (float)is) : 0.0f;
       ia[m] = is;
       ib[m] = 0;
@@ -230,11 +260,10 @@ __device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t*
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       const int bx = xb + m * nbx;
-      const uint4 x0 = *reinterpret_cast<const uint4*>(lds + 32 * bx + 16 * l);
-      int s0 = dot4(s.a.x, x0.x, 0);
-      s0 = dot4(s.a.y, x0.y, s0);
-      s0 = dot4(s.a.z, x0.z, s0);
-      s0 = dot4(s.a.w, x0.w, s0);
+      const int sw = (bx >> 2) & 1;
+      const uint4 x0 = *reinterpret_cast<const uint4*>(lds + 32 * bx + 16 * (0 ^ sw));
+      const uint4 x1 = *reinterpret_cast<const uint4*>(lds + 32 * bx + 16 * (1 ^ sw));
+      const int s0 = dot16(s.b, x1, dot16(s.a, x0, 0));
       acc[m] += ok ? (dw * ld[bx]) * (float)s0 : 0.0f;
       ia[m] = s0;
       ib[m] = 0;
@@ -242,32 +271,193 @@ __device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t*
   }
 }
 
-// y[m, n] = sum_b dot(W[n, b], X[m, b]) for m < M, n < N.
-//   wq: weight blocks (device layout), N rows of nb blocks; wd: separated f16
-//   scales (Q6_K, Q8_0) right after the bodies; xq: M rows of nb activation
-//   blocks (Q8_K or Q8_0, GGML bytes); dump (optional): int32 block dots.
-template <int FMT, int M, int R, int U>
-__device__ __forceinline__ void gemv(const uint8_t* __restrict__ wq, const uint8_t* __restrict__ xq,
-                                     float* __restrict__ y, int N, int K, int ldy,
+// Up to four weight matrices (same format and K) that share one activation;
+// rows of job j are global rows [sum_{i<j} rows[i], sum_{i<=j} rows[i]).
+struct GemvJobs {
+  const uint8_t* wq[4];  // device-layout blocks of each matrix
+  float* y[4];           // outputs, y[j][m * ldy[j] + row]
+  int rows[4];
+  int ldy[4];
+  int njobs;
+  int total;
+};
+
+// Where one global row lives.
+struct RowRef {
+  const uint8_t* wq;
+  const uint16_t* wd;
+  float* y;
+  int ldy;
+  int row;   // row within its matrix
+  int rows;  // rows of its matrix
+  bool ok;
+};
+
+// `gr` is wave-uniform, so the job lookup compiles to scalar selects.
+template <int FMT>
+__device__ __forceinline__ RowRef locate(const GemvJobs& jobs, int gr, int nb) {
+  RowRef r;
+  int base = 0;
+  const uint8_t* wq = jobs.wq[0];
+  float* y = jobs.y[0];
+  int rows = jobs.rows[0], ldy = jobs.ldy[0];
+  if (jobs.njobs > 1 && gr >= rows) {
+    base = rows;
+    wq = jobs.wq[1];
+    y = jobs.y[1];
+    rows = jobs.rows[1];
+    ldy = jobs.ldy[1];
+    if (jobs.njobs > 2 && gr >= base + rows) {
+      base += rows;
+      wq = jobs.wq[2];
+      y = jobs.y[2];
+      rows = jobs.rows[2];
+      ldy = jobs.ldy[2];
+      if (jobs.njobs > 3 && gr >= base + rows) {
+        base += rows;
+        wq = jobs.wq[3];
+        y = jobs.y[3];
+        rows = jobs.rows[3];
+        ldy = jobs.ldy[3];
+      }
+    }
+  }
+  r.wq = wq;
+  r.wd = FMT == kFmtQ4K ? nullptr
+                        : reinterpret_cast<const uint16_t*>(wq + (size_t)rows * nb * FmtInfo<FMT>::kBodyBytes);
+  r.y = y;
+  r.ldy = ldy;
+  r.row = gr - base;
+  r.rows = rows;
+  r.ok = gr < jobs.total;
+  return r;
+}
+
+template <int FMT, int R, int U>
+__device__ __forceinline__ void load_batch(WSlice (&ws)[R][U], const RowRef (&rr)[R], int it0, int nb, int g,
+                                           int l) {
+  constexpr int BPI = 64 / FmtInfo<FMT>::kLanesPerBlock;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int b = (it0 + u) * BPI + g;
+      ws[r][u] = WSlice{};
+      if (rr[r].ok && b < nb) load_slice<FMT>(ws[r][u], rr[r].wq, rr[r].wd, (size_t)rr[r].row * nb + b, l);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// In-kernel activation quantization (the prologue of the fused GEMV): the
+// same arithmetic as the standalone quantizers, written straight into the LDS
+// layout stage_act produces from GGML bytes.
+// ---------------------------------------------------------------------------
+
+// (lane l, chunk k) of the weight-side lane group that consumes 16-element
+// activation group c16 (inverse of act_chunk).
+template <int FMT>
+__device__ __forceinline__ void chunk_owner(int c16, int& l, int& k) {
+  if (FMT == kFmtQ4K) {
+    l = c16 >> 2;
+    k = c16 & 3;
+  } else {
+    const int rem = c16 & 7;
+    l = 2 * (c16 >> 3) + ((rem >> 1) & 1);
+    k = 2 * ((rem >> 2) & 1) + (rem & 1);
+  }
+}
+
+// Quantize mrows f32 rows (stride ldx) of nb blocks into the LDS layout.
+template <int FMT>
+__device__ __forceinline__ void quantize_act(const float* __restrict__ x, long long ldx, int mrows, int nb,
+                                             uint8_t* lds) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int nblk = mrows * nb;
+  if constexpr (FMT == kFmtQ80) {
+#pragma clang fp contract(off)
+    float* ld = reinterpret_cast<float*>(lds + 32 * nblk);
+    const int l8 = lane & 7;
+    for (int base = 8 * wave; base < nblk; base += 8 * nw) {
+      const int blk = base + (lane >> 3);
+      const bool valid = blk < nblk;
+      const int bc = valid ? blk : 0;
+      const float* xs = x + (bc / nb) * ldx + 32 * (bc % nb) + 4 * l8;
+      float e[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) e[j] = valid ? xs[j] : 0.0f;
+      float amax = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
+      amax = fmaxf(amax, dpp_f<0xb1>(amax));
+      amax = fmaxf(amax, dpp_f<0x4e>(amax));
+      amax = fmaxf(amax, dpp_f<0x141>(amax));
+      const float d = amax / 127.0f;
+      const float id = d != 0.0f ? 1.0f / d : 0.0f;
+      uint32_t q4 = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float v = roundf(e[j] * id);
+        v = fminf(fmaxf(v, -128.0f), 127.0f);
+        q4 |= (uint32_t)((int)v & 0xff) << (8 * j);
+      }
+      if (valid) {
+        *reinterpret_cast<uint32_t*>(lds + 32 * blk + 16 * q80_slot(blk, l8 >> 2) + 4 * (l8 & 3)) = q4;
+        if (l8 == 0) ld[blk] = h2f(f2h(d));
+      }
+    }
+  } else {
+    uint32_t* lsum = reinterpret_cast<uint32_t*>(lds + 256 * nblk);
+    float* ld = reinterpret_cast<float*>(lsum + 8 * nblk);
+    const int c16 = lane >> 2;
+    int lc, kc;
+    chunk_owner<FMT>(c16, lc, kc);
+    for (int blk = wave; blk < nblk; blk += nw) {
+      const Q8KLane q = q8k_lane(x + (blk / nb) * ldx + 256 * (blk % nb), lane);
+      *reinterpret_cast<uint32_t*>(lds + 256 * blk + 16 * kq_slot(blk, lc, kc) + 4 * (lane & 3)) = q.packed;
+      const int next = __shfl_down(q.sum16, 4);  // the following 16-group's sum
+      if (FMT == kFmtQ4K) {
+        const int s32 = q.sum16 + next;
+        const int s32n = __shfl_down(s32, 8);
+        if ((lane & 15) == 0) lsum[8 * blk + (lane >> 4)] = ((uint32_t)s32 & 0xffffu) | ((uint32_t)s32n << 16);
+      } else {
+        if ((lane & 7) == 0) lsum[8 * blk + 2 * lc + (kc >> 1)] = ((uint32_t)q.sum16 & 0xffffu) | ((uint32_t)next << 16);
+      }
+      if (lane == 0) ld[blk] = q.d;
+    }
+  }
+}
+
+// y_j[m, n] = sum_b dot(W_j[n, b], X[m, b]) for every job j, m < M, n < rows_j.
+//   act: M rows of nb activation blocks (Q8_K or Q8_0, GGML bytes), or, when
+//        FUSED, M rows of f32 (row stride ldx) quantized in the prologue;
+//   dump (optional, single job): int32 block dots [M][rows][nb](x2 for Q4_K).
+template <int FMT, int M, int R, int U, bool FUSED>
+__device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restrict__ act, long long ldx, int K,
                                      int* __restrict__ dump) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int LPB = FmtInfo<FMT>::kLanesPerBlock;
   constexpr int BPI = 64 / LPB;  // blocks per wave iteration
   const int nb = K / FmtInfo<FMT>::kBlockElems;
-  stage_act<FMT>(xq, M * nb, lds);
-  __syncthreads();
-
-  const uint16_t* wd =
-      FMT == kFmtQ4K ? nullptr
-                     : reinterpret_cast<const uint16_t*>(wq + (size_t)N * nb * FmtInfo<FMT>::kBodyBytes);
   const int lane = threadIdx.x & 63;
   const int nw = blockDim.x >> 6;
   const int l = lane % LPB;
   const int g = lane / LPB;
   const int niter = (nb + BPI - 1) / BPI;
   const int row_step = gridDim.x * nw * R;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int row0 = (blockIdx.x * nw + wave) * R;
 
-  for (int row0 = (blockIdx.x * nw + (threadIdx.x >> 6)) * R; row0 < N; row0 += row_step) {
+  // First weight batch in flight before the activation is staged.
+  RowRef rr[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) rr[r] = locate<FMT>(jobs, row0 + r, nb);
+  WSlice ws[R][U];
+  load_batch<FMT, R, U>(ws, rr, 0, nb, g, l);
+  if constexpr (FUSED)
+    quantize_act<FMT>(reinterpret_cast<const float*>(act), ldx, M, nb, lds);
+  else
+    stage_act<FMT>(reinterpret_cast<const uint8_t*>(act), M * nb, lds);
+  __syncthreads();
+
+  for (; row0 < jobs.total; row0 += row_step) {
     float acc[R][M];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -275,21 +465,13 @@ __device__ __forceinline__ void gemv(const uint8_t* __restrict__ wq, const uint8
       for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
 
     for (int it0 = 0; it0 < niter; it0 += U) {
-      WSlice ws[R][U];
+      if (it0 > 0) load_batch<FMT, R, U>(ws, rr, it0, nb, g, l);
 #pragma unroll
       for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           const int b = (it0 + u) * BPI + g;
-          ws[r][u] = WSlice{};
-          if (row0 + r < N && b < nb) load_slice<FMT>(ws[r][u], wq, wd, (size_t)(row0 + r) * nb + b, l);
-        }
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int b = (it0 + u) * BPI + g;
-          const bool ok = row0 + r < N && b < nb;
+          const bool ok = rr[r].ok && b < nb;
           int ia[M], ib[M];
           dot_slice<FMT, M>(ws[r][u], l, lds, M * nb, ok ? b : 0, nb, ok, acc[r], ia, ib);
           if (dump != nullptr) {
@@ -302,7 +484,7 @@ __device__ __forceinline__ void gemv(const uint8_t* __restrict__ wq, const uint8
                 vb += __shfl_xor(vb, off);
               }
               if (ok && l == 0) {
-                const size_t o = ((size_t)m * N + row0 + r) * nb + b;
+                const size_t o = ((size_t)m * rr[r].rows + rr[r].row) * nb + b;
                 if (FMT == kFmtQ4K) {
                   dump[2 * o] = va;
                   dump[2 * o + 1] = vb;
@@ -314,41 +496,103 @@ __device__ __forceinline__ void gemv(const uint8_t* __restrict__ wq, const uint8
           }
         }
     }
+    // The next row group's first batch goes out before this group's reduction.
+    RowRef cur[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      cur[r] = rr[r];
+      rr[r] = locate<FMT>(jobs, row0 + row_step + r, nb);
+    }
+    if (row0 + row_step < jobs.total) load_batch<FMT, R, U>(ws, rr, 0, nb, g, l);
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         const float v = wave_sum(acc[r][m]);
-        if (lane == 0 && row0 + r < N) y[(size_t)m * ldy + row0 + r] = v;
+        if (lane == 0 && cur[r].ok) cur[r].y[(size_t)m * cur[r].ldy + cur[r].row] = v;
       }
   }
 }
 
 }  // namespace qmm
 
-#define QMM_GEMV_KERNEL(FMT, NAME, M, R, U)                                                         \
-  extern "C" __global__ void __launch_bounds__(256)                                                \
-      qmm_gemv_##NAME##_m##M##_r##R##_u##U(const uint8_t* __restrict__ wq,                         \
-                                           const uint8_t* __restrict__ xq, float* __restrict__ y,  \
-                                           int N, int K, int ldy, int* __restrict__ dump) {        \
-    qmm::gemv<FMT, M, R, U>(wq, xq, y, N, K, ldy, dump);                                           \
+// Kernel arguments: the job table as plain scalars (a by-value struct would be
+// copied to scratch), then the activation, its row stride, K and the dump.
+#define QMM_GEMV_PARAMS                                                                                   \
+  const uint8_t *wq0, const uint8_t *wq1, const uint8_t *wq2, const uint8_t *wq3, float *y0, float *y1,   \
+      float *y2, float *y3, int rows0, int rows1, int rows2, int rows3, int ldy0, int ldy1, int ldy2,     \
+      int ldy3, int njobs, int total, const void *__restrict__ act, long long ldx, int K,                 \
+      int *__restrict__ dump
+#define QMM_GEMV_JOBS                                                                                     \
+  qmm::GemvJobs jobs;                                                                                     \
+  jobs.wq[0] = wq0;                                                                                       \
+  jobs.wq[1] = wq1;                                                                                       \
+  jobs.wq[2] = wq2;                                                                                       \
+  jobs.wq[3] = wq3;                                                                                       \
+  jobs.y[0] = y0;                                                                                         \
+  jobs.y[1] = y1;                                                                                         \
+  jobs.y[2] = y2;                                                                                         \
+  jobs.y[3] = y3;                                                                                         \
+  jobs.rows[0] = rows0;                                                                                   \
+  jobs.rows[1] = rows1;                                                                                   \
+  jobs.rows[2] = rows2;                                                                                   \
+  jobs.rows[3] = rows3;                                                                                   \
+  jobs.ldy[0] = ldy0;                                                                                     \
+  jobs.ldy[1] = ldy1;                                                                                     \
+  jobs.ldy[2] = ldy2;                                                                                     \
+  jobs.ldy[3] = ldy3;                                                                                     \
+  jobs.njobs = njobs;                                                                                     \
+  jobs.total = total;
+
+#define QMM_GEMV_KERNEL(FMT, NAME, M, W, R, U)                                                            \
+  extern "C" __global__ void __launch_bounds__(64 * W)                                                    \
+      qmm_gemv_##NAME##_m##M##_w##W##_r##R##_u##U(QMM_GEMV_PARAMS) {                                      \
+    QMM_GEMV_JOBS                                                                                         \
+    qmm::gemv<FMT, M, R, U, false>(jobs, act, ldx, K, dump);                                              \
   }
 
-#define QMM_GEMV_SHAPES(FMT, NAME, M) \
-  QMM_GEMV_KERNEL(FMT, NAME, M, 4, 2) \
-  QMM_GEMV_KERNEL(FMT, NAME, M, 2, 2) \
-  QMM_GEMV_KERNEL(FMT, NAME, M, 1, 4) \
-  QMM_GEMV_KERNEL(FMT, NAME, M, 1, 8)
+#define QMM_GEMVF_KERNEL(FMT, NAME, M, W, R, U)                                                           \
+  extern "C" __global__ void __launch_bounds__(64 * W)                                                    \
+      qmm_gemvf_##NAME##_m##M##_w##W##_r##R##_u##U(QMM_GEMV_PARAMS) {                                     \
+    QMM_GEMV_JOBS                                                                                         \
+    qmm::gemv<FMT, M, R, U, true>(jobs, act, ldx, K, dump);                                               \
+  }
+
+// Launch shapes: W waves per workgroup, R rows per wave, U load iterations per batch.
+#define QMM_GEMV_SHAPES_1(FMT, NAME)        \
+  QMM_GEMV_KERNEL(FMT, NAME, 1, 4, 1, 1)    \
+  QMM_GEMV_KERNEL(FMT, NAME, 1, 4, 2, 1)    \
+  QMM_GEMV_KERNEL(FMT, NAME, 1, 4, 1, 2)    \
+  QMM_GEMV_KERNEL(FMT, NAME, 1, 8, 1, 1)    \
+  QMM_GEMV_KERNEL(FMT, NAME, 1, 8, 2, 1)    \
+  QMM_GEMV_KERNEL(FMT, NAME, 1, 8, 1, 2)    \
+  QMM_GEMV_KERNEL(FMT, NAME, 1, 16, 1, 1)   \
+  QMM_GEMV_KERNEL(FMT, NAME, 1, 16, 1, 2)
+
+#define QMM_GEMV_SHAPES(FMT, NAME, M)       \
+  QMM_GEMV_KERNEL(FMT, NAME, M, 4, 1, 1)    \
+  QMM_GEMV_KERNEL(FMT, NAME, M, 4, 2, 1)    \
+  QMM_GEMV_KERNEL(FMT, NAME, M, 4, 1, 2)    \
+  QMM_GEMV_KERNEL(FMT, NAME, M, 8, 1, 1)    \
+  QMM_GEMV_KERNEL(FMT, NAME, M, 8, 1, 2)
+
+#define QMM_GEMVF_SHAPES(FMT, NAME, M)      \
+  QMM_GEMVF_KERNEL(FMT, NAME, M, 8, 1, 1)   \
+  QMM_GEMVF_KERNEL(FMT, NAME, M, 8, 1, 2)   \
+  QMM_GEMVF_KERNEL(FMT, NAME, M, 16, 1, 1)  \
+  QMM_GEMVF_KERNEL(FMT, NAME, M, 16, 1, 2)
 
 #define QMM_GEMV_ALL_M(FMT, NAME) \
-  QMM_GEMV_SHAPES(FMT, NAME, 1)   \
+  QMM_GEMV_SHAPES_1(FMT, NAME)    \
   QMM_GEMV_SHAPES(FMT, NAME, 2)   \
   QMM_GEMV_SHAPES(FMT, NAME, 3)   \
   QMM_GEMV_SHAPES(FMT, NAME, 4)   \
   QMM_GEMV_SHAPES(FMT, NAME, 5)   \
   QMM_GEMV_SHAPES(FMT, NAME, 6)   \
   QMM_GEMV_SHAPES(FMT, NAME, 7)   \
-  QMM_GEMV_SHAPES(FMT, NAME, 8)
+  QMM_GEMV_SHAPES(FMT, NAME, 8)   \
+  QMM_GEMVF_SHAPES(FMT, NAME, 1)  \
+  QMM_GEMVF_SHAPES(FMT, NAME, 2)
 
 QMM_GEMV_ALL_M(qmm::kFmtQ4K, q4k)
 QMM_GEMV_ALL_M(qmm::kFmtQ6K, q6k)

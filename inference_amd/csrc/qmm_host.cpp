@@ -69,16 +69,17 @@ std::mutex g_mu;
 Device* g_dev[64] = {};
 
 // Launch-shape overrides for tuning sweeps, read at every launch:
-// QMM_GEMV_RU="R,U" (rows per wave, loads per row in flight), QMM_GEMV_MAXWG=<workgroups>.
+// QMM_GEMV_CFG="W,R,U" (waves per workgroup, rows per wave, load iterations per
+// batch) and QMM_GEMV_WAVES_PER_CU (resident waves the grid is sized for).
 struct Tuning {
-  int r = 0, u = 0, max_wg = 0;
+  int w = 0, r = 0, u = 0, waves_per_cu = 0;
 };
 Tuning tuning() {
   Tuning t;
-  if (const char* s = getenv("QMM_GEMV_RU")) {
-    if (sscanf(s, "%d,%d", &t.r, &t.u) != 2) t.r = t.u = 0;
+  if (const char* s = getenv("QMM_GEMV_CFG")) {
+    if (sscanf(s, "%d,%d,%d", &t.w, &t.r, &t.u) != 3) t.w = t.r = t.u = 0;
   }
-  if (const char* s = getenv("QMM_GEMV_MAXWG")) t.max_wg = atoi(s);
+  if (const char* s = getenv("QMM_GEMV_WAVES_PER_CU")) t.waves_per_cu = atoi(s);
   return t;
 }
 
@@ -417,46 +418,80 @@ size_t qmm_matmul_workspace_size(const qmm_qtensor* w, int64_t m) {
   return (size_t)m * (size_t)(w->k / qmm_block_size(vt)) * qmm_type_size(vt);
 }
 
-// GEMV launch for m <= 8 activation rows.
-static int gemv(Device* d, const qmm_qtensor* w, const void* xq, int m, float* y, int64_t ldy, int* dump,
-                hipStream_t s) {
+// Job table of one GEMV launch (passed to the kernel as scalar arguments).
+struct GemvJobs {
+  const void* wq[4];
+  float* y[4];
+  int rows[4];
+  int ldy[4];
+  int njobs;
+  int total;
+};
+
+struct GemvTarget {
+  const qmm_qtensor* w;
+  float* y;
+  int64_t ldy;
+};
+
+// GEMV launch for m <= 8 activation rows over up to four weights (same dtype
+// and k) sharing one activation. `act` is m rows of quantized blocks, or f32
+// rows with stride ldx when `fused` (then the kernel quantizes in its prologue).
+static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, bool fused, int64_t ldx, int m,
+                int* dump, hipStream_t s) {
+  const qmm_qtensor* w = tg[0].w;
   const int fmt = fmt_of(w->dtype);
   const int nb = (int)(w->k / qmm_block_size(w->dtype));
-  const int lpb = fmt == kFmtQ80 ? 2 : 8;
-  const int bpi = 64 / lpb;
+  const int lpb = fmt == kFmtQ80 ? 1 : 4;  // lanes per weight block
+  const int bpi = 64 / lpb;                // blocks per wave iteration
   const int niter = (nb + bpi - 1) / bpi;
   const int xbb = fmt == kFmtQ80 ? 36 : 292;  // LDS bytes per staged activation block
   const unsigned lds = (unsigned)(m * nb * xbb);
   if ((int)lds > d->max_lds)
     return fail(QMM_ERR_UNSUPPORTED, "activation of %d rows x %lld needs %u B of LDS (> %d)", m, (long long)w->k, lds,
                 d->max_lds);
-  int r, u;
-  if (fmt == kFmtQ80) {
-    if (niter <= 2) { r = 4; u = 2; }
-    else if (niter <= 4) { r = 1; u = 4; }
-    else { r = 1; u = 8; }
-  } else if (fmt == kFmtQ4K) {
-    if (niter <= 2) { r = 4; u = 2; }
-    else if (niter <= 4) { r = 1; u = 4; }
-    else { r = 1; u = 8; }
-  } else {
-    if (niter <= 2) { r = 2; u = 2; }
-    else { r = 1; u = 4; }
+  GemvJobs jobs = {};
+  long long total = 0;
+  for (int j = 0; j < count; ++j) {
+    jobs.wq[j] = tg[j].w->data;
+    jobs.y[j] = tg[j].y;
+    jobs.rows[j] = (int)tg[j].w->n;
+    jobs.ldy[j] = (int)tg[j].ldy;
+    total += tg[j].w->n;
   }
-  if (m > 4 && r == 4) r = 2;
+  if (total > (1LL << 31) - 1) return fail(QMM_ERR_INVALID, "too many output rows in one launch");
+  jobs.njobs = count;
+  jobs.total = (int)total;
+  // Launch shape (from sweeps on MI355X at the Llama-3-8B shapes). Each wave
+  // keeps one or two 32-byte weight slices per lane in flight and prefetches
+  // its next row while finishing the current one; the grid is sized for ~20
+  // resident waves per CU so every wave walks several rows. 16-wave workgroups
+  // share the staged (or in-kernel quantized: one block per wave) activation
+  // over more rows; 8-wave ones are used where the 16-wave variant would
+  // exceed 128 VGPRs.
+  int wv = 16, r = 1, u = niter >= 2 ? 2 : 1;
+  if (fused) {
+    if (m == 2 && fmt == kFmtQ6K) u = 1;
+  } else if (m > 1 || nb * xbb <= 8192) {
+    wv = 8;
+  }
+  int waves_per_cu = 20;
   const Tuning tu = tuning();
-  if (tu.r > 0 && tu.u > 0) { r = tu.r; u = tu.u; }
-  char name[64];
-  snprintf(name, sizeof(name), "qmm_gemv_%s_m%d_r%d_u%d", fmt_name(fmt), m, r, u);
-  const int waves = 4;
-  long long wgs = ((long long)w->n + waves * r - 1) / (waves * r);
-  if (tu.max_wg > 0 && wgs > tu.max_wg) wgs = tu.max_wg;
-  const void* wq = w->data;
-  float* yy = y;
-  int N = (int)w->n, K = (int)w->k, ld = (int)ldy;
+  if (tu.w > 0 && tu.r > 0 && tu.u > 0) { wv = tu.w; r = tu.r; u = tu.u; }
+  if (tu.waves_per_cu > 0) waves_per_cu = tu.waves_per_cu;
+  char name[80];
+  snprintf(name, sizeof(name), "qmm_gemv%s_%s_m%d_w%d_r%d_u%d", fused ? "f" : "", fmt_name(fmt), m, wv, r, u);
+  long long wgs = (total + wv * r - 1) / (wv * r);
+  const long long cap = ((long long)d->num_cu * waves_per_cu + wv - 1) / wv;
+  if (wgs > cap) wgs = cap;
+  const void* a = act;
+  long long lx = ldx;
+  int K = (int)w->k;
   int* dp = dump;
-  void* args[] = {&wq, &xq, &yy, &N, &K, &ld, &dp};
-  return launch(d, name, (unsigned)wgs, 64 * waves, lds, s, args);
+  void* args[] = {&jobs.wq[0], &jobs.wq[1], &jobs.wq[2], &jobs.wq[3], &jobs.y[0], &jobs.y[1], &jobs.y[2],
+                  &jobs.y[3], &jobs.rows[0], &jobs.rows[1], &jobs.rows[2], &jobs.rows[3], &jobs.ldy[0],
+                  &jobs.ldy[1], &jobs.ldy[2], &jobs.ldy[3], &jobs.njobs, &jobs.total, &a, &lx, &K, &dp};
+  return launch(d, name, (unsigned)wgs, 64 * wv, lds, s, args);
 }
 
 static int check_matmul(const qmm_qtensor* w, int64_t m, const float* y, int64_t ldy) {
@@ -477,11 +512,38 @@ int qmm_matmul_q(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int6
   QMM_TRY(current_device(&d));
   const int vt = qmm_vec_dot_type(w->dtype);
   const size_t xrow = (size_t)(w->k / qmm_block_size(vt)) * qmm_type_size(vt);
-  // Rows are processed in groups of up to 8 by the GEMV (the GEMM path for
-  // large m is selected in qmm_matmul_q once available).
+  // Rows are processed in groups of up to 8 by the GEMV.
   for (int64_t m0 = 0; m0 < m; m0 += 8) {
     const int mm = (int)(m - m0 < 8 ? m - m0 : 8);
-    QMM_TRY(gemv(d, w, (const uint8_t*)xq + m0 * xrow, mm, y + m0 * ldy, ldy, nullptr, (hipStream_t)stream));
+    GemvTarget t = {w, y + m0 * ldy, ldy};
+    QMM_TRY(gemv(d, &t, 1, (const uint8_t*)xq + m0 * xrow, false, 0, mm, nullptr, (hipStream_t)stream));
+  }
+  return QMM_OK;
+}
+
+// Shared by qmm_matmul / qmm_matmul_multi: x f32 [m, k] against `count` weights.
+static int matmul_targets(const GemvTarget* tg, int count, const float* x, int64_t m, int64_t ldx, void* ws,
+                          size_t ws_bytes, void* stream) {
+  const qmm_qtensor* w = tg[0].w;
+  if (!x) return fail(QMM_ERR_INVALID, "null activation");
+  if (ldx < w->k) return fail(QMM_ERR_INVALID, "row stride %lld < k %lld", (long long)ldx, (long long)w->k);
+  Device* d;
+  QMM_TRY(current_device(&d));
+  hipStream_t s = (hipStream_t)stream;
+  if (m <= 2) {
+    // one launch: the activation is quantized in the GEMV prologue
+    return gemv(d, tg, count, x, true, ldx, (int)m, nullptr, s);
+  }
+  const size_t need = qmm_matmul_workspace_size(w, m);
+  if (!ws || ws_bytes < need) return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed", ws_bytes, need);
+  const int vt = qmm_vec_dot_type(w->dtype);
+  QMM_TRY(qmm_quantize_rows(vt, x, m, w->k, ldx, ws, stream));
+  const size_t xrow = (size_t)(w->k / qmm_block_size(vt)) * qmm_type_size(vt);
+  for (int64_t m0 = 0; m0 < m; m0 += 8) {
+    const int mm = (int)(m - m0 < 8 ? m - m0 : 8);
+    GemvTarget t[4];
+    for (int j = 0; j < count; ++j) t[j] = {tg[j].w, tg[j].y + m0 * tg[j].ldy, tg[j].ldy};
+    QMM_TRY(gemv(d, t, count, (const uint8_t*)ws + m0 * xrow, false, 0, mm, nullptr, s));
   }
   return QMM_OK;
 }
@@ -489,11 +551,21 @@ int qmm_matmul_q(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int6
 int qmm_matmul(const qmm_qtensor* w, const float* x, int64_t m, int64_t ldx, float* y, int64_t ldy, void* ws,
                size_t ws_bytes, void* stream) {
   QMM_TRY(check_matmul(w, m, y, ldy));
-  if (!x || !ws) return fail(QMM_ERR_INVALID, "null pointer");
-  const size_t need = qmm_matmul_workspace_size(w, m);
-  if (ws_bytes < need) return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed", ws_bytes, need);
-  QMM_TRY(qmm_quantize_rows(qmm_vec_dot_type(w->dtype), x, m, w->k, ldx, ws, stream));
-  return qmm_matmul_q(w, ws, m, y, ldy, stream);
+  GemvTarget t = {w, y, ldy};
+  return matmul_targets(&t, 1, x, m, ldx, ws, ws_bytes, stream);
+}
+
+int qmm_matmul_multi(const qmm_qtensor* const* w, int count, const float* x, int64_t m, int64_t ldx,
+                     float* const* y, const int64_t* ldy, void* ws, size_t ws_bytes, void* stream) {
+  if (!w || !y || !ldy || count < 1 || count > 4) return fail(QMM_ERR_INVALID, "need 1..4 weights with outputs");
+  GemvTarget t[4];
+  for (int j = 0; j < count; ++j) {
+    QMM_TRY(check_matmul(w[j], m, y[j], ldy[j]));
+    if (w[j]->dtype != w[0]->dtype || w[j]->k != w[0]->k)
+      return fail(QMM_ERR_INVALID, "weights of one multi-matmul must share dtype and k");
+    t[j] = {w[j], y[j], ldy[j]};
+  }
+  return matmul_targets(t, count, x, m, ldx, ws, ws_bytes, stream);
 }
 
 int qmm_block_dots(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int64_t ldy, int32_t* dots,
@@ -503,7 +575,8 @@ int qmm_block_dots(const qmm_qtensor* w, const void* xq, int64_t m, float* y, in
   if (m > 8) return fail(QMM_ERR_INVALID, "block dots are produced by the GEMV: m = %lld > 8", (long long)m);
   Device* d;
   QMM_TRY(current_device(&d));
-  return gemv(d, w, xq, (int)m, y, ldy, dots, (hipStream_t)stream);
+  GemvTarget t = {w, y, ldy};
+  return gemv(d, &t, 1, xq, false, 0, (int)m, dots, (hipStream_t)stream);
 }
 
 }  // extern "C"

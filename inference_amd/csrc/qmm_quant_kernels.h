@@ -22,60 +22,56 @@ namespace qmm {
 //   iscale = -128 / max, q = min(127, round(iscale * x)) (ties away from zero)
 //   bsums[j] = sum of q[16j .. 16j+16), d = 1 / iscale; an all-zero block is all zeros.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void q8k_block(const float* __restrict__ xs, uint8_t* __restrict__ blk,
-                                          int lane) {
+// Lane-local result of quantizing one 256-element block (lane owns elements
+// 4*lane .. 4*lane+3).
+struct Q8KLane {
+  uint32_t packed;  // its four int8 quants
+  int sum16;        // sum of the 16-element group it belongs to
+  float d;
+};
+
+__device__ __forceinline__ Q8KLane q8k_lane(const float* __restrict__ xs, int lane) {
 #pragma clang fp contract(off)
-  float e[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) e[j] = xs[4 * lane + j];
-  float amax = 0.0f;
-  int idx = 0x7fffffff;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float a = fabsf(e[j]);
-    if (amax < a) {
-      amax = a;
-      idx = 4 * lane + j;
-    }
-  }
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float oa = __shfl_xor(amax, off);
-    const int oi = __shfl_xor(idx, off);
-    if (oa > amax || (oa == amax && oi < idx)) {
-      amax = oa;
-      idx = oi;
-    }
-  }
-  uint32_t* qw = reinterpret_cast<uint32_t*>(blk + 4);
-  uint32_t* bw = reinterpret_cast<uint32_t*>(blk + 4 + 256);
+  const float e0 = xs[4 * lane], e1 = xs[4 * lane + 1], e2 = xs[4 * lane + 2], e3 = xs[4 * lane + 3];
+  const float amax = wave_max(fmaxf(fmaxf(fabsf(e0), fabsf(e1)), fmaxf(fabsf(e2), fabsf(e3))));
+  Q8KLane r;
   if (amax == 0.0f) {
-    qw[lane] = 0u;
-    if (lane < 8) bw[lane] = 0u;
-    if (lane == 0) *reinterpret_cast<float*>(blk) = 0.0f;
-    return;
+    r.packed = 0u;
+    r.sum16 = 0;
+    r.d = 0.0f;
+    return r;
   }
-  const int j0 = idx & 3;
-  const float mine = j0 == 0 ? e[0] : j0 == 1 ? e[1] : j0 == 2 ? e[2] : e[3];
-  const float mx = __shfl(mine, idx >> 2);
+  const int mine = fabsf(e0) == amax ? 0 : fabsf(e1) == amax ? 1 : fabsf(e2) == amax ? 2 : fabsf(e3) == amax ? 3 : 4;
+  const int idx = wave_min(mine < 4 ? 4 * lane + mine : 256);
+  const float cand = (idx & 3) == 0 ? e0 : (idx & 3) == 1 ? e1 : (idx & 3) == 2 ? e2 : e3;
+  const float mx = readlane_f(cand, idx >> 2);
   const float iscale = -128.0f / mx;
+  const float e[4] = {e0, e1, e2, e3};
   uint32_t packed = 0;
   int sum = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    float r = roundf(iscale * e[j]);
-    r = fminf(r, 127.0f);
-    int q = (int)r;
+    float v = roundf(iscale * e[j]);
+    v = fminf(v, 127.0f);
+    int q = (int)v;
     q = q < -128 ? -128 : q;
     sum += q;
     packed |= (uint32_t)(q & 0xff) << (8 * j);
   }
-  qw[lane] = packed;
-  sum += __shfl_xor(sum, 1);
-  sum += __shfl_xor(sum, 2);
-  const int next = __shfl_down(sum, 4);
-  if ((lane & 7) == 0) bw[lane >> 3] = ((uint32_t)sum & 0xffffu) | ((uint32_t)next << 16);
-  if (lane == 0) *reinterpret_cast<float*>(blk) = 1.0f / iscale;
+  r.packed = packed;
+  r.sum16 = quad_sum(sum);
+  r.d = 1.0f / iscale;
+  return r;
+}
+
+// Standalone form: one wave writes one GGML Q8_K block.
+__device__ __forceinline__ void q8k_block(const float* __restrict__ xs, uint8_t* __restrict__ blk, int lane) {
+  const Q8KLane q = q8k_lane(xs, lane);
+  reinterpret_cast<uint32_t*>(blk + 4)[lane] = q.packed;
+  const int next = __shfl_down(q.sum16, 4);
+  if ((lane & 7) == 0)
+    reinterpret_cast<uint32_t*>(blk + 4 + 256)[lane >> 3] = ((uint32_t)q.sum16 & 0xffffu) | ((uint32_t)next << 16);
+  if (lane == 0) *reinterpret_cast<float*>(blk) = q.d;
 }
 
 // ---------------------------------------------------------------------------
@@ -92,9 +88,9 @@ __device__ __forceinline__ void q80_block(const float* __restrict__ xs, uint8_t*
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(e[j]));
-  amax = fmaxf(amax, __shfl_xor(amax, 1));
-  amax = fmaxf(amax, __shfl_xor(amax, 2));
-  amax = fmaxf(amax, __shfl_xor(amax, 4));
+  amax = fmaxf(amax, dpp_f<0xb1>(amax));   // max over the 8 lanes of the block
+  amax = fmaxf(amax, dpp_f<0x4e>(amax));
+  amax = fmaxf(amax, dpp_f<0x141>(amax));
   const float d = amax / 127.0f;
   const float id = d != 0.0f ? 1.0f / d : 0.0f;
   if (!valid) return;

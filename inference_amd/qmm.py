@@ -44,7 +44,7 @@ EXPORTS = (
     "qmm_qtensor_from_ggml", "qmm_qtensor_quantize", "qmm_qtensor_dequantize",
     "qmm_qtensor_to_ggml", "qmm_qtensor_info", "qmm_qtensor_ggml_bytes", "qmm_qtensor_free",
     "qmm_quantize_rows", "qmm_matmul_workspace_size", "qmm_matmul", "qmm_matmul_q",
-    "qmm_block_dots",
+    "qmm_matmul_multi", "qmm_block_dots",
 )
 
 
@@ -79,6 +79,8 @@ def lib() -> ctypes.CDLL:
             "qmm_matmul_workspace_size": ([vp, i64], sz),
             "qmm_matmul": ([vp, vp, i64, i64, vp, i64, vp, sz, vp], i32),
             "qmm_matmul_q": ([vp, vp, i64, vp, i64, vp], i32),
+            "qmm_matmul_multi": ([ctypes.POINTER(vp), i32, vp, i64, i64, ctypes.POINTER(vp),
+                                  ctypes.POINTER(i64), vp, sz, vp], i32),
             "qmm_block_dots": ([vp, vp, i64, vp, i64, vp, vp], i32),
         }
         for name, (args, res) in sig.items():
@@ -283,6 +285,30 @@ class QMatMul:
     __call__ = forward
 
 
+def matmul_multi(qts: Sequence[QTensor], x: torch.Tensor) -> Tuple[torch.Tensor, ...]:
+    """Several QMatMul::forward on one input (same dtype and k) in one launch."""
+    if not 1 <= len(qts) <= 4:
+        raise QmmError(1, "matmul_multi takes 1..4 weights")
+    k = qts[0].shape[1]
+    if x.dtype != torch.float32 or x.shape[-1] != k:
+        raise QmmError(1, "matmul_multi expects float32 input with last dim k")
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    ys = [torch.empty((m, q.shape[0]), dtype=torch.float32, device=x.device) for q in qts]
+    L = lib()
+    ws_bytes = int(L.qmm_matmul_workspace_size(qts[0].handle, m))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    hs = (ctypes.c_void_p * len(qts))(*[q.handle.value for q in qts])
+    yp = (ctypes.c_void_p * len(qts))(*[y.data_ptr() for y in ys])
+    ld = (ctypes.c_int64 * len(qts))(*[q.shape[0] for q in qts])
+    with torch.cuda.device(x.device):
+        _check(L.qmm_matmul_multi(hs, len(qts), x2.data_ptr(), m, x2.stride(0), yp, ld, ws.data_ptr(),
+                                  ws_bytes, _stream(x.device)))
+    return tuple(y.reshape(*x.shape[:-1], y.shape[1]) for y in ys)
+
+
 def matmul_q(qt: QTensor, xq: torch.Tensor, m: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y[m, n] from pre-quantized activations (uint8 GGML vec-dot blocks on the GPU)."""
     n = qt.shape[0]
@@ -356,7 +382,7 @@ class QuantizedLinear:
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         y = self.inner.forward(x.to(torch.float32)).to(x.dtype)
         if self.bias is not None:
-            y = y + self.bias
+            y = y + self.bias.to(y.dtype)
         return y
 
     __call__ = forward

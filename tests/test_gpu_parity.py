@@ -149,16 +149,20 @@ def test_block_dots_bit_exact_and_outputs(dt, n, k, m):
     assert rel_err(y2, y_ref) <= TOL
 
 
-@pytest.mark.parametrize("ru", ["4,2", "2,2", "1,4", "1,8"])
+GENERIC_CFGS = ["4,1,1", "4,2,1", "4,1,2", "8,1,1", "8,1,2"]
+M1_ONLY_CFGS = ["8,2,1", "16,1,1", "16,1,2"]
+
+
+@pytest.mark.parametrize("cfg", GENERIC_CFGS + M1_ONLY_CFGS)
 @pytest.mark.parametrize("dt", WEIGHT_TYPES)
-def test_every_launch_shape_is_correct(dt, ru, monkeypatch):
-    """All compiled (rows/wave, loads/row) variants, on ragged row counts."""
-    monkeypatch.setenv("QMM_GEMV_RU", ru)
-    for n, k in ((1, 256), (13, 2048), (70, 4096)):
+def test_every_launch_shape_is_correct(dt, cfg, monkeypatch):
+    """All compiled (waves/workgroup, rows/wave, loads/row) variants, on ragged row counts."""
+    monkeypatch.setenv("QMM_GEMV_CFG", cfg)
+    for n, k in ((1, 256), (13, 2048), (70, 4096), (9, 14336)):
         w = normal(70 + n, (n, k), 0.02)
         wq = orc.quantize(ORC[dt], w)
         qt = QTensor.from_ggml(wq, dt, w.shape, device=DEV)
-        for m in (1, 2, 8):
+        for m in ((1, 2, 8) if cfg in GENERIC_CFGS else (1,)):
             x = normal(71, (m, k))
             xq = quantize_rows(dt.vec_dot_type(), torch.from_numpy(x).to(DEV))
             dots, y = block_dots(qt, xq, m)
@@ -166,16 +170,17 @@ def test_every_launch_shape_is_correct(dt, ru, monkeypatch):
             assert rel_err(y.cpu().numpy(), orc.matmul_prequant(ORC[dt], xq.cpu().numpy(), wq, k)) <= TOL
 
 
-def test_grid_cap_keeps_results(monkeypatch):
-    """A capped grid makes every wave loop over several row groups."""
-    monkeypatch.setenv("QMM_GEMV_MAXWG", "3")
-    n, k = 300, 4096
+@pytest.mark.parametrize("dt", WEIGHT_TYPES)
+def test_small_grid_walks_many_rows(dt, monkeypatch):
+    """A grid sized for one wave per CU makes every wave loop over ~10 rows."""
+    monkeypatch.setenv("QMM_GEMV_WAVES_PER_CU", "1")
+    n, k = 3000, 2048
     w = normal(80, (n, k), 0.02)
-    wq = orc.quantize(orc.Q4K, w)
-    qt = QTensor.from_ggml(wq, GgmlDType.Q4K, w.shape, device=DEV)
+    wq = orc.quantize(ORC[dt], w)
+    qt = QTensor.from_ggml(wq, dt, w.shape, device=DEV)
     x = normal(81, (2, k))
     y = QMatMul.from_qtensor(qt).forward(torch.from_numpy(x).to(DEV)).cpu().numpy()
-    assert rel_err(y, orc.matmul(orc.Q4K, x, wq, k)) <= TOL
+    assert rel_err(y, orc.matmul(ORC[dt], x, wq, k)) <= TOL
 
 
 CONFIG_SHAPES = [
@@ -272,3 +277,37 @@ def test_repeated_calls_are_deterministic():
     y0 = mm.forward(x)
     for _ in range(5):
         assert torch.equal(mm.forward(x), y0)
+
+
+FUSED_CFGS = ["8,1,1", "8,1,2", "16,1,1", "16,1,2"]
+
+
+@pytest.mark.parametrize("cfg", FUSED_CFGS)
+@pytest.mark.parametrize("dt", WEIGHT_TYPES)
+def test_fused_prologue_quantization_is_bit_identical(dt, cfg, monkeypatch):
+    """QMatMul.forward with m <= 2 quantizes x inside the GEMV; its outputs must equal,
+    bit for bit, the staged GEMV fed with the (CPU-identical) quantize_rows bytes."""
+    for n, k in ((37, 2048), (70, 4096), (9, 14336)):
+        w = normal(140 + n, (n, k), 0.02)
+        qt = QTensor.from_ggml(orc.quantize(ORC[dt], w), dt, w.shape, device=DEV)
+        for m in (1, 2):
+            x = np.concatenate([normal(141, (m, k)), special_activation_rows(k)])[-m:] if m == 2 else normal(142, (1, k))
+            xt = torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+            monkeypatch.setenv("QMM_GEMV_CFG", cfg)
+            y_fused = QMatMul.from_qtensor(qt).forward(xt)
+            monkeypatch.delenv("QMM_GEMV_CFG")  # staged reference with its default launch shape
+            y_staged = matmul_q(qt, quantize_rows(dt.vec_dot_type(), xt), m)
+            assert torch.equal(y_fused, y_staged), f"n={n} k={k} m={m}"
+
+
+@pytest.mark.parametrize("dt", WEIGHT_TYPES)
+@pytest.mark.parametrize("m", [1, 2, 5])
+def test_matmul_multi_equals_separate_forwards(dt, m):
+    from inference_amd import matmul_multi
+    k = 4096
+    qts = [QTensor.quantize(torch.from_numpy(normal(150 + i, (n, k), 0.02)).to(DEV), dt)
+           for i, n in enumerate((4096, 1024, 1000, 17))]
+    x = torch.from_numpy(normal(160, (m, k))).to(DEV)
+    ys = matmul_multi(qts, x)
+    for q, y in zip(qts, ys):
+        assert torch.equal(y, QMatMul.from_qtensor(q).forward(x))
