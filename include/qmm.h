@@ -127,15 +127,19 @@ int qmm_matmul_multi(const qmm_qtensor *const *w, int count, const float *x, int
                      float *const *y, const int64_t *ldy, void *ws, size_t ws_bytes, void *stream);
 
 /* The same with activations already quantized (xq: m rows of vec-dot blocks,
- * as produced by qmm_quantize_rows). */
+ * as produced by qmm_quantize_rows). For m > 8 the rows are rearranged for the
+ * GEMM in a scratch buffer the library keeps per device (calls on one device
+ * must then be ordered on one stream). */
 int qmm_matmul_q(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy, void *stream);
 
 /* Debug entry: exact int32 block dots of every (activation row, weight row,
- * super-block), computed by the same GEMV kernel that qmm_matmul_q runs.
+ * super-block), computed by the same kernel that qmm_matmul_q runs (the GEMV
+ * for m <= 8, the MFMA GEMM for m > 8).
  * dots: device int32 [m, n, k/block_size, per] with per = 2 for Q4K
  * (isum_d = sum_j sc_j*sum q4*q8, isum_m = sum_j m_j*(bsum_2j + bsum_2j+1))
  * and per = 1 for Q6K (sum_j sc_j*sum (q6-32)*q8) and Q8_0 (sum qw*qx).
- * y receives the f32 outputs as qmm_matmul_q would. m = 1..8. */
+ * y receives the f32 outputs as qmm_matmul_q would. For m > 8, k must be a
+ * multiple of 256. */
 int qmm_block_dots(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy,
                    int32_t *dots, void *stream);
 

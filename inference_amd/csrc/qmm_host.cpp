@@ -412,10 +412,32 @@ int qmm_quantize_rows(int vdtype, const float* x, int64_t m, int64_t k, int64_t 
   return launch(d, "qmm_quantize_q8_0", ceil_div(nblocks * 8, 256), 256, 0, (hipStream_t)stream, args);
 }
 
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Plane layout of m activation rows for the GEMM: int8 q8 [m][k], f32 scales
+// [m][k/block], int16 32-element sums [m][k/256][8] (k-quants).
+struct Planes {
+  size_t q8, d, s, total;
+};
+static Planes mmq_planes(int dtype, int64_t m, int64_t k) {
+  Planes p;
+  const int64_t nbd = dtype == QMM_Q8_0 ? k / 32 : k / 256;
+  p.q8 = 0;
+  p.d = align256((size_t)(m * k));
+  p.s = p.d + align256((size_t)(m * nbd) * 4);
+  p.total = p.s + (dtype == QMM_Q8_0 ? 0 : align256((size_t)(m * (k / 256)) * 16));
+  return p;
+}
+
+// The GEMM handles m > 8 rows when k is a whole number of 256-wide steps.
+static bool use_gemm(const qmm_qtensor* w, int64_t m) { return m > 8 && w->k % 256 == 0; }
+
 size_t qmm_matmul_workspace_size(const qmm_qtensor* w, int64_t m) {
   if (!w || m <= 0) return 0;
   const int vt = qmm_vec_dot_type(w->dtype);
-  return (size_t)m * (size_t)(w->k / qmm_block_size(vt)) * qmm_type_size(vt);
+  const size_t ggml = (size_t)m * (size_t)(w->k / qmm_block_size(vt)) * qmm_type_size(vt);
+  if (!use_gemm(w, m)) return ggml;
+  return mmq_planes(w->dtype, m, w->k).total;
 }
 
 // Job table of one GEMV launch (passed to the kernel as scalar arguments).
@@ -494,6 +516,81 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   return launch(d, name, (unsigned)wgs, 64 * wv, lds, s, args);
 }
 
+// Prefill GEMM over activation planes at `ws` (see mmq_planes).
+static int gemm(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, float* y, int64_t ldy, int* dump,
+                hipStream_t s) {
+  const Planes pl = mmq_planes(w->dtype, m, w->k);
+  const int fmt = fmt_of(w->dtype);
+  const char* name = fmt == kFmtQ4K ? "qmm_mmq_q4k" : fmt == kFmtQ6K ? "qmm_mmq_q6k" : "qmm_mmq_q8_0";
+  const void* wq = w->data;
+  const void* q8 = ws + pl.q8;
+  const void* dd = ws + pl.d;
+  const void* ss = ws + pl.s;
+  float* yy = y;
+  int M = (int)m, N = (int)w->n, K = (int)w->k, ld = (int)ldy;
+  int* dp = dump;
+  void* args[] = {&wq, &q8, &dd, &ss, &yy, &M, &N, &K, &ld, &dp};
+  hipFunction_t f;
+  QMM_TRY(kernel(d, name, &f));
+  const unsigned gx = (unsigned)((N + 127) / 128), gy = (unsigned)((M + 63) / 64);
+  QMM_HIP(hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, s, args, nullptr));
+  return QMM_OK;
+}
+
+// f32 activations -> planes (quantized as VecDotType::from_float).
+static int quantize_planes(Device* d, int wdtype, const float* x, int64_t m, int64_t k, int64_t ldx, uint8_t* ws,
+                           hipStream_t s) {
+  const Planes pl = mmq_planes(wdtype, m, k);
+  long long ld = ldx;
+  int kk = (int)k, mm = (int)m;
+  void* q8 = ws + pl.q8;
+  void* dd = ws + pl.d;
+  void* ss = ws + pl.s;
+  if (wdtype == QMM_Q8_0) {
+    void* args[] = {&x, &ld, &q8, &dd, &kk, &mm};
+    return launch(d, "qmm_quantize_q8_0_mmq", ceil_div(m * (k / 32) * 8, 256), 256, 0, s, args);
+  }
+  void* args[] = {&x, &ld, &q8, &dd, &ss, &kk, &mm};
+  return launch(d, "qmm_quantize_q8k_mmq", ceil_div(m * (k / 256), 4), 256, 0, s, args);
+}
+
+// GGML vec-dot blocks -> planes.
+static int blocks_to_planes(Device* d, int wdtype, const void* xq, int64_t m, int64_t k, uint8_t* ws,
+                            hipStream_t s) {
+  const Planes pl = mmq_planes(wdtype, m, k);
+  void* q8 = ws + pl.q8;
+  void* dd = ws + pl.d;
+  void* ss = ws + pl.s;
+  int kk = (int)k, mm = (int)m, is_q8k = wdtype == QMM_Q8_0 ? 0 : 1;
+  void* args[] = {&xq, &q8, &dd, &ss, &kk, &mm, &is_q8k};
+  const unsigned grid = is_q8k ? ceil_div(m * (k / 256), 4) : ceil_div(m * (k / 32), 256);
+  return launch(d, "qmm_q8_blocks_to_planes", grid, 256, 0, s, args);
+}
+
+// Scratch owned by the library for the prequantized GEMM entry points
+// (qmm_matmul_q / qmm_block_dots with m > 8), grown on demand per device.
+static int scratch(size_t bytes, uint8_t** out) {
+  static std::mutex mu;
+  static void* buf[64] = {};
+  static size_t cap[64] = {};
+  int dev = 0;
+  QMM_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(mu);
+  if (cap[dev] < bytes) {
+    if (buf[dev]) {
+      QMM_HIP(hipDeviceSynchronize());
+      QMM_HIP(hipFree(buf[dev]));
+      buf[dev] = nullptr;
+      cap[dev] = 0;
+    }
+    hipError_t e = hipMalloc(&buf[dev], bytes);
+    if (e != hipSuccess) return fail(QMM_ERR_OOM, "hipMalloc(scratch %zu): %s", bytes, hipGetErrorString(e));
+    cap[dev] = bytes;
+  }
+  *out = (uint8_t*)buf[dev];
+  return QMM_OK;
+}
+
 static int check_matmul(const qmm_qtensor* w, int64_t m, const float* y, int64_t ldy) {
   if (!w || !y) return fail(QMM_ERR_INVALID, "null pointer");
   if (m <= 0) return fail(QMM_ERR_INVALID, "m = %lld must be positive", (long long)m);
@@ -511,6 +608,12 @@ int qmm_matmul_q(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int6
   Device* d;
   QMM_TRY(current_device(&d));
   const int vt = qmm_vec_dot_type(w->dtype);
+  if (use_gemm(w, m)) {
+    uint8_t* ws;
+    QMM_TRY(scratch(mmq_planes(w->dtype, m, w->k).total, &ws));
+    QMM_TRY(blocks_to_planes(d, w->dtype, xq, m, w->k, ws, (hipStream_t)stream));
+    return gemm(d, w, ws, m, y, ldy, nullptr, (hipStream_t)stream);
+  }
   const size_t xrow = (size_t)(w->k / qmm_block_size(vt)) * qmm_type_size(vt);
   // Rows are processed in groups of up to 8 by the GEMV.
   for (int64_t m0 = 0; m0 < m; m0 += 8) {
@@ -536,6 +639,11 @@ static int matmul_targets(const GemvTarget* tg, int count, const float* x, int64
   }
   const size_t need = qmm_matmul_workspace_size(w, m);
   if (!ws || ws_bytes < need) return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed", ws_bytes, need);
+  if (use_gemm(w, m)) {
+    QMM_TRY(quantize_planes(d, w->dtype, x, m, w->k, ldx, (uint8_t*)ws, s));
+    for (int j = 0; j < count; ++j) QMM_TRY(gemm(d, tg[j].w, (const uint8_t*)ws, m, tg[j].y, tg[j].ldy, nullptr, s));
+    return QMM_OK;
+  }
   const int vt = qmm_vec_dot_type(w->dtype);
   QMM_TRY(qmm_quantize_rows(vt, x, m, w->k, ldx, ws, stream));
   const size_t xrow = (size_t)(w->k / qmm_block_size(vt)) * qmm_type_size(vt);
@@ -572,9 +680,15 @@ int qmm_block_dots(const qmm_qtensor* w, const void* xq, int64_t m, float* y, in
                    void* stream) {
   QMM_TRY(check_matmul(w, m, y, ldy));
   if (!xq || !dots) return fail(QMM_ERR_INVALID, "null pointer");
-  if (m > 8) return fail(QMM_ERR_INVALID, "block dots are produced by the GEMV: m = %lld > 8", (long long)m);
   Device* d;
   QMM_TRY(current_device(&d));
+  if (m > 8) {
+    if (!use_gemm(w, m)) return fail(QMM_ERR_UNSUPPORTED, "block dots for m > 8 need k %% 256 == 0");
+    uint8_t* ws;
+    QMM_TRY(scratch(mmq_planes(w->dtype, m, w->k).total, &ws));
+    QMM_TRY(blocks_to_planes(d, w->dtype, xq, m, w->k, ws, (hipStream_t)stream));
+    return gemm(d, w, ws, m, y, ldy, dots, (hipStream_t)stream);
+  }
   GemvTarget t = {w, y, ldy};
   return gemv(d, &t, 1, xq, false, 0, (int)m, dots, (hipStream_t)stream);
 }

@@ -5,3 +5,4 @@
 #include "qmm_common.h"
 #include "qmm_quant_kernels.h"
 #include "qmm_gemv_kernels.h"
+#include "qmm_mmq_kernels.h"

@@ -1,0 +1,453 @@
+// Prefill GEMM (M > 8 activation rows) on int8 MFMA (v_mfma_i32_32x32x32_i8).
+//
+// The contraction is split the way the GGML formats scale it:
+//   Q4_K: for each 32-element sub-block j, P_j = q8 . q4 is one MFMA (K = 32)
+//         per 32x32 tile; isum_d += sc_j * P_j (v_mad_i32_i24); the mins term
+//         isum_m = sum_j m_j * (bsum_2j + bsum_2j+1) is two zero-padded MFMAs
+//         (activation sums split into 6-bit low / signed high bytes);
+//         y += dx * (d * isum_d - dmin * isum_m) once per super-block.
+//   Q6_K: each 32-element chunk is two 16-element groups with their own int8
+//         scale; the activation operand is masked to one lane half (one group)
+//         per MFMA; isum += sc_g * P_g; y += dx * d * isum per super-block.
+//   Q8_0: one MFMA per 32-block, y += (dw * dx) * P.
+// Activations come from a plane layout written by qmm_quantize_*_mmq (int8
+// [M][K], f32 scales, int16 32-element sums), weights from the tensors'
+// device layout; both are staged in LDS per 256-wide K step, the weights
+// dequantized to int8 on the way.
+// Workgroup: 256 threads, tile 64 (M) x 128 (N); wave w owns rows
+// 32*(w&1) .. +32 and columns 64*(w>>1) .. +64 (two 32x32 MFMA tiles).
+// The next K step's global loads are issued before the current step's MFMAs.
+// The CUDA kernels this replaces are mul_mat_q (candle-kernels/src/mmq_gguf/mmq_gguf.cuh:3526-3778).
+#pragma once
+
+#include "qmm_common.h"
+#include "qmm_quant_kernels.h"
+
+namespace qmm {
+
+typedef char i8x16 __attribute__((ext_vector_type(16)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kMmqBM = 64;
+constexpr int kMmqBN = 128;
+constexpr int kMmqStride = 256 + 16;  // LDS row stride of the int8 tiles (16-byte skew per row)
+
+struct MmqLds {
+  int8_t a[kMmqBM * kMmqStride];   // activations, int8 [row][k]
+  int8_t b[kMmqBN * kMmqStride];   // weights, int8 [col][k]
+  float ad[kMmqBM * 8];            // activation scales: per row (k-quants) or per 32-block (Q8_0)
+  int8_t as[kMmqBM * 16];          // Q4_K: 32-element sums, low 6 bits [0..8) and high part [8..16)
+  int8_t bsc[kMmqBN * 16];         // Q4_K: sc[8] | m[8]; Q6_K: sc[16]
+  float bd[kMmqBN * 8];            // Q4_K: d, dmin; Q6_K: d; Q8_0: d of the 8 blocks
+};
+
+// Per-thread registers of one K step (256 elements) before they go to LDS.
+struct MmqRegs {
+  uint4 a[4];   // 64 activation bytes of one row
+  float ad[2];  // activation scale(s)
+  uint4 as;     // Q4_K activation sums (8 x int16)
+  uint4 w[8];   // weight bytes (format dependent)
+  uint32_t wd[4];
+};
+
+template <int FMT>
+__device__ __forceinline__ void mmq_load(MmqRegs& R, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                         const int16_t* __restrict__ xs, const uint8_t* __restrict__ wq,
+                                         const uint16_t* __restrict__ wd, int M, int N, int K, int m0, int n0,
+                                         int kb) {
+  const int t = threadIdx.x;
+  const int nbk = K / 256;
+  // activations: thread t -> row t/4, bytes [64*(t%4), +64) of this K step
+  {
+    const int row = m0 + (t >> 2);
+    const bool ok = row < M;
+    const uint4* p = reinterpret_cast<const uint4*>(xq + (size_t)(ok ? row : 0) * K + 256 * kb + 64 * (t & 3));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) R.a[i] = ok ? p[i] : make_uint4(0, 0, 0, 0);
+  }
+  if (FMT == kFmtQ80) {
+    // 8 scales per row per K step: thread t < 256 -> row t/4, blocks 2*(t%4), +1
+    const int row = m0 + (t >> 2);
+    const bool ok = row < M;
+    const float* p = xd + (size_t)(ok ? row : 0) * (K / 32) + 8 * kb + 2 * (t & 3);
+    R.ad[0] = ok ? p[0] : 0.0f;
+    R.ad[1] = ok ? p[1] : 0.0f;
+  } else if (t < kMmqBM) {
+    const int row = m0 + t;
+    const bool ok = row < M;
+    R.ad[0] = ok ? xd[(size_t)row * nbk + kb] : 0.0f;
+    if (FMT == kFmtQ4K)
+      R.as = ok ? *reinterpret_cast<const uint4*>(xs + ((size_t)row * nbk + kb) * 8) : make_uint4(0, 0, 0, 0);
+  }
+  // weights: thread t -> column t/2, half p = t%2 of the K step
+  const int col = n0 + (t >> 1), p = t & 1;
+  const bool okc = col < N;
+  const size_t blk = (size_t)(okc ? col : 0) * (FMT == kFmtQ80 ? K / 32 : nbk) + (FMT == kFmtQ80 ? 8 * kb : kb);
+  if (FMT == kFmtQ4K) {
+    const uint4* b = reinterpret_cast<const uint4*>(wq + blk * kQ4KBytes);
+    R.w[0] = b[0];  // d, dmin, scales
+#pragma unroll
+    for (int i = 0; i < 4; ++i) R.w[1 + i] = b[1 + 4 * p + i];  // qs[64p, 64p+64)
+  } else if (FMT == kFmtQ6K) {
+    const uint4* b = reinterpret_cast<const uint4*>(wq + blk * kQ6KBody);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) R.w[i] = b[4 * p + i];         // ql[64p, 64p+64)
+    R.w[4] = b[8 + 2 * p];                                      // qh[32p, 32p+32)
+    R.w[5] = b[9 + 2 * p];
+    R.w[6] = b[12];                                             // scales
+    R.wd[0] = wd[blk];
+  } else {
+    const uint4* b = reinterpret_cast<const uint4*>(wq + (blk + 4 * p) * kQ80Body);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) R.w[i] = b[i];  // blocks 4p .. 4p+3 of this K step
+    R.wd[0] = wd[blk + 4 * p];
+    R.wd[1] = wd[blk + 4 * p + 1];
+    R.wd[2] = wd[blk + 4 * p + 2];
+    R.wd[3] = wd[blk + 4 * p + 3];
+  }
+  if (!okc) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) R.w[i] = make_uint4(0, 0, 0, 0);
+    R.wd[0] = R.wd[1] = R.wd[2] = R.wd[3] = 0;
+  }
+}
+
+__device__ __forceinline__ uint32_t q6_sub32(uint32_t v) {
+  // bytes in [0, 63] minus 32, as int8, without borrows between bytes
+  return ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+}
+
+template <int FMT>
+__device__ __forceinline__ void mmq_store(const MmqRegs& R, MmqLds& L) {
+  const int t = threadIdx.x;
+  {
+    uint4* dst = reinterpret_cast<uint4*>(L.a + (t >> 2) * kMmqStride + 64 * (t & 3));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = R.a[i];
+  }
+  if (FMT == kFmtQ80) {
+    L.ad[(t >> 2) * 8 + 2 * (t & 3)] = R.ad[0];
+    L.ad[(t >> 2) * 8 + 2 * (t & 3) + 1] = R.ad[1];
+  } else if (t < kMmqBM) {
+    L.ad[t] = R.ad[0];
+    if (FMT == kFmtQ4K) {
+      // 32-element sums s (|s| <= 4096): s = 64*hi + lo, lo in [0,63], hi in [-64, 64]
+      const int16_t* s = reinterpret_cast<const int16_t*>(&R.as);
+      int8_t* d = L.as + 16 * t;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int v = s[j];
+        d[j] = (int8_t)(v & 63);
+        d[8 + j] = (int8_t)(v >> 6);
+      }
+    }
+  }
+  const int c = t >> 1, p = t & 1;
+  int8_t* brow = L.b + c * kMmqStride;
+  if (FMT == kFmtQ4K) {
+    // qs[64p + 16i ...] -> chunk cc = 2p + i/2: low nibbles at 64cc + 16(i%2), high at +32
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int cc = 2 * p + (i >> 1), off = 64 * cc + 16 * (i & 1);
+      const uint4 v = R.w[1 + i];
+      *reinterpret_cast<uint4*>(brow + off) =
+          make_uint4(v.x & 0x0f0f0f0fu, v.y & 0x0f0f0f0fu, v.z & 0x0f0f0f0fu, v.w & 0x0f0f0f0fu);
+      *reinterpret_cast<uint4*>(brow + off + 32) = make_uint4((v.x >> 4) & 0x0f0f0f0fu, (v.y >> 4) & 0x0f0f0f0fu,
+                                                             (v.z >> 4) & 0x0f0f0f0fu, (v.w >> 4) & 0x0f0f0f0fu);
+    }
+    if (p == 0) {
+      const uint8_t* hb = reinterpret_cast<const uint8_t*>(&R.w[0]);
+      int8_t* sc = L.bsc + 16 * c;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        int s, m;
+        q4k_scale_min(j, hb + 4, &s, &m);
+        sc[j] = (int8_t)s;
+        sc[8 + j] = (int8_t)m;
+      }
+      L.bd[8 * c] = h2f(R.w[0].x);
+      L.bd[8 * c + 1] = h2f(R.w[0].x >> 16);
+    }
+  } else if (FMT == kFmtQ6K) {
+    // half h = p: elements 128h + [0,128) from ql[64h, +64) and qh[32h, +32)
+    const uint32_t* ql = reinterpret_cast<const uint32_t*>(&R.w[0]);  // 16 dwords
+    const uint32_t* qh = reinterpret_cast<const uint32_t*>(&R.w[4]);  // 8 dwords
+    int8_t* base = brow + 128 * p;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint32_t l0 = ql[q], l1 = ql[8 + q], h = qh[q];
+      const uint32_t e0 = (l0 & 0x0f0f0f0fu) | ((h & 0x03030303u) << 4);                // elements 4q .. (+0)
+      const uint32_t e1 = (l1 & 0x0f0f0f0fu) | (((h >> 2) & 0x03030303u) << 4);         // +32
+      const uint32_t e2 = ((l0 >> 4) & 0x0f0f0f0fu) | (((h >> 4) & 0x03030303u) << 4);  // +64
+      const uint32_t e3 = ((l1 >> 4) & 0x0f0f0f0fu) | (((h >> 6) & 0x03030303u) << 4);  // +96
+      *reinterpret_cast<uint32_t*>(base + 4 * q) = q6_sub32(e0);
+      *reinterpret_cast<uint32_t*>(base + 32 + 4 * q) = q6_sub32(e1);
+      *reinterpret_cast<uint32_t*>(base + 64 + 4 * q) = q6_sub32(e2);
+      *reinterpret_cast<uint32_t*>(base + 96 + 4 * q) = q6_sub32(e3);
+    }
+    if (p == 0) {
+      *reinterpret_cast<uint4*>(L.bsc + 16 * c) = R.w[6];
+      L.bd[8 * c] = h2f(R.wd[0]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(brow + 128 * p + 16 * i) = R.w[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) L.bd[8 * c + 4 * p + i] = h2f(R.wd[i]);
+  }
+}
+
+__device__ __forceinline__ i32x16 mfma_i8(i8x16 a, i8x16 b, i32x16 c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+// y[m, n] = sum over K of x[m, :] . W[n, :] with the formats' scaling.
+template <int FMT>
+__device__ __forceinline__ void mmq(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,
+                                    const float* __restrict__ xd, const int16_t* __restrict__ xs,
+                                    float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump) {
+  __shared__ MmqLds L;
+  const int m0 = blockIdx.y * kMmqBM, n0 = blockIdx.x * kMmqBN;
+  const int nbk = K / 256;
+  const int nbw = FMT == kFmtQ80 ? K / 32 : nbk;  // weight blocks per row
+  const uint16_t* wd =
+      FMT == kFmtQ4K ? nullptr
+                     : reinterpret_cast<const uint16_t*>(wq + (size_t)N * nbw * FmtInfo<FMT>::kBodyBytes);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int wm = wave & 1, wn = wave >> 1;
+
+  i32x16 zero;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) zero[j] = 0;
+  float acc[2][16];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[t][j] = 0.0f;
+
+  MmqRegs R;
+  mmq_load<FMT>(R, xq, xd, xs, wq, wd, M, N, K, m0, n0, 0);
+  for (int kb = 0; kb < nbk; ++kb) {
+    __syncthreads();
+    mmq_store<FMT>(R, L);
+    __syncthreads();
+    if (kb + 1 < nbk) mmq_load<FMT>(R, xq, xd, xs, wq, wd, M, N, K, m0, n0, kb + 1);
+
+    const int8_t* arow = L.a + (32 * wm + r) * kMmqStride + 16 * h;
+    int isum[2][16];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) isum[t][j] = 0;
+
+    if (FMT == kFmtQ80) {
+#pragma unroll 1
+      for (int c = 0; c < 8; ++c) {
+        const i8x16 a = *reinterpret_cast<const i8x16*>(arow + 32 * c);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int col = 64 * wn + 32 * t + r;
+          const i8x16 b = *reinterpret_cast<const i8x16*>(L.b + col * kMmqStride + 32 * c + 16 * h);
+          const i32x16 P = mfma_i8(a, b, zero);
+          const float dw = L.bd[8 * col + c];
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int row = 32 * wm + 8 * (j >> 2) + 4 * h + (j & 3);
+            acc[t][j] += (dw * L.ad[8 * row + c]) * (float)P[j];
+            if (dump != nullptr && m0 + row < M && n0 + col < N)
+              dump[((size_t)(m0 + row) * N + n0 + col) * nbw + 8 * kb + c] = P[j];
+          }
+        }
+      }
+      continue;
+    }
+
+    if (FMT == kFmtQ4K) {
+#pragma unroll 1
+      for (int c = 0; c < 8; ++c) {
+        const i8x16 a = *reinterpret_cast<const i8x16*>(arow + 32 * c);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int col = 64 * wn + 32 * t + r;
+          const i8x16 b = *reinterpret_cast<const i8x16*>(L.b + col * kMmqStride + 32 * c + 16 * h);
+          const i32x16 P = mfma_i8(a, b, zero);
+          const int sc = L.bsc[16 * col + c];
+#pragma unroll
+          for (int j = 0; j < 16; ++j) isum[t][j] += sc * P[j];
+        }
+      }
+      // mins: two MFMAs over the 8 sub-block sums (only lane half 0 carries data)
+      i8x16 alo, ahi;
+      {
+        const int8_t* s = L.as + 16 * (32 * wm + r);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          alo[j] = (h == 0 && j < 8) ? s[j] : (char)0;
+          ahi[j] = (h == 0 && j < 8) ? s[8 + j] : (char)0;
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int col = 64 * wn + 32 * t + r;
+        i8x16 bm;
+        const int8_t* mn = L.bsc + 16 * col + 8;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) bm[j] = (h == 0 && j < 8) ? mn[j] : (char)0;
+        const i32x16 Plo = mfma_i8(alo, bm, zero);
+        const i32x16 Phi = mfma_i8(ahi, bm, zero);
+        const float dw = L.bd[8 * col], dmin = L.bd[8 * col + 1];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 dx = *reinterpret_cast<const float4*>(&L.ad[32 * wm + 8 * g + 4 * h]);
+          const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = 4 * g + i;
+            const int ism = Phi[j] * 64 + Plo[j];
+            acc[t][j] += dxs[i] * (dw * (float)isum[t][j] - dmin * (float)ism);
+            if (dump != nullptr) {
+              const int row = m0 + 32 * wm + 8 * g + 4 * h + i;
+              const int cl = n0 + col;
+              if (row < M && cl < N) {
+                const size_t o = ((size_t)row * N + cl) * nbk + kb;
+                dump[2 * o] = isum[t][j];
+                dump[2 * o + 1] = ism;
+              }
+            }
+          }
+        }
+      }
+    } else {  // Q6_K
+#pragma unroll 1
+      for (int c = 0; c < 8; ++c) {
+        const i8x16 a = *reinterpret_cast<const i8x16*>(arow + 32 * c);
+        i8x16 a0, a1;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          a0[j] = h == 0 ? a[j] : (char)0;
+          a1[j] = h == 1 ? a[j] : (char)0;
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int col = 64 * wn + 32 * t + r;
+          const i8x16 b = *reinterpret_cast<const i8x16*>(L.b + col * kMmqStride + 32 * c + 16 * h);
+          const i32x16 P0 = mfma_i8(a0, b, zero);
+          const i32x16 P1 = mfma_i8(a1, b, zero);
+          const int s0 = L.bsc[16 * col + 2 * c], s1 = L.bsc[16 * col + 2 * c + 1];
+#pragma unroll
+          for (int j = 0; j < 16; ++j) isum[t][j] += s0 * P0[j] + s1 * P1[j];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int col = 64 * wn + 32 * t + r;
+        const float dw = L.bd[8 * col];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 dx = *reinterpret_cast<const float4*>(&L.ad[32 * wm + 8 * g + 4 * h]);
+          const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = 4 * g + i;
+            acc[t][j] += dxs[i] * (dw * (float)isum[t][j]);
+            if (dump != nullptr) {
+              const int row = m0 + 32 * wm + 8 * g + 4 * h + i;
+              const int cl = n0 + col;
+              if (row < M && cl < N) dump[((size_t)row * N + cl) * nbk + kb] = isum[t][j];
+            }
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int row = m0 + 32 * wm + 8 * (j >> 2) + 4 * h + (j & 3);
+      const int col = n0 + 64 * wn + 32 * t + r;
+      if (row < M && col < N) y[(size_t)row * ldy + col] = acc[t][j];
+    }
+}
+
+}  // namespace qmm
+
+// Activation quantizers writing the GEMM's plane layout.
+//   Q8_K: q8 int8 [m][k], d f32 [m][k/256], 32-element sums int16 [m][k/256][8]
+extern "C" __global__ void __launch_bounds__(256) qmm_quantize_q8k_mmq(const float* __restrict__ x, long long ldx,
+                                                                       int8_t* __restrict__ q8,
+                                                                       float* __restrict__ d,
+                                                                       int16_t* __restrict__ s, int k, int m) {
+  const int nb = k / 256;
+  const long long w = (long long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (w >= (long long)m * nb) return;
+  const int row = (int)(w / nb), b = (int)(w % nb), lane = threadIdx.x & 63;
+  const qmm::Q8KLane q = qmm::q8k_lane(x + row * ldx + 256LL * b, lane);
+  reinterpret_cast<uint32_t*>(q8 + (size_t)row * k + 256 * b)[lane] = q.packed;
+  const int next = __shfl_down(q.sum16, 4);
+  if ((lane & 7) == 0) s[w * 8 + (lane >> 3)] = (int16_t)(q.sum16 + next);
+  if (lane == 0) d[w] = q.d;
+}
+
+//   Q8_0: q8 int8 [m][k], d f32 [m][k/32] (the f16-rounded block scale)
+extern "C" __global__ void __launch_bounds__(256) qmm_quantize_q8_0_mmq(const float* __restrict__ x, long long ldx,
+                                                                        int8_t* __restrict__ q8,
+                                                                        float* __restrict__ d, int k, int m) {
+  const int nb = k / 32;
+  const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long blk = t >> 3;
+  const bool valid = blk < (long long)m * nb;
+  const long long bc = valid ? blk : 0;
+  const int row = (int)(bc / nb), b = (int)(bc % nb), l = (int)(t & 7);
+  uint8_t tmp[qmm::kQ80Bytes];
+  qmm::q80_block(x + row * ldx + 32LL * b, tmp, l, valid);
+  if (!valid) return;
+  const uint16_t* p = reinterpret_cast<const uint16_t*>(tmp);
+  reinterpret_cast<uint16_t*>(q8 + (size_t)row * k + 32 * b)[2 * l] = p[1 + 2 * l];
+  reinterpret_cast<uint16_t*>(q8 + (size_t)row * k + 32 * b)[2 * l + 1] = p[2 + 2 * l];
+  if (l == 0) d[bc] = qmm::h2f(p[0]);
+}
+
+#define QMM_MMQ_KERNEL(FMT, NAME)                                                                          \
+  extern "C" __global__ void __launch_bounds__(256)                                                        \
+      qmm_mmq_##NAME(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                        \
+                     const float* __restrict__ xd, const int16_t* __restrict__ xs, float* __restrict__ y, \
+                     int M, int N, int K, int ldy, int* __restrict__ dump) {                               \
+    qmm::mmq<FMT>(wq, xq, xd, xs, y, M, N, K, ldy, dump);                                                  \
+  }
+
+QMM_MMQ_KERNEL(qmm::kFmtQ4K, q4k)
+QMM_MMQ_KERNEL(qmm::kFmtQ6K, q6k)
+QMM_MMQ_KERNEL(qmm::kFmtQ80, q8_0)
+
+// GGML activation blocks (m rows of Q8_K / Q8_0) -> the GEMM plane layout.
+// Q8_K: one wave per block; Q8_0: one thread per block.
+extern "C" __global__ void __launch_bounds__(256) qmm_q8_blocks_to_planes(const uint8_t* __restrict__ xq,
+                                                                          int8_t* __restrict__ q8,
+                                                                          float* __restrict__ d,
+                                                                          int16_t* __restrict__ s, int k, int m,
+                                                                          int is_q8k) {
+  if (is_q8k) {
+    const int nb = k / 256;
+    const long long w = (long long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (w >= (long long)m * nb) return;
+    const int row = (int)(w / nb), b = (int)(w % nb), lane = threadIdx.x & 63;
+    const uint8_t* blk = xq + w * qmm::kQ8KBytes;
+    reinterpret_cast<uint32_t*>(q8 + (size_t)row * k + 256 * b)[lane] = reinterpret_cast<const uint32_t*>(blk + 4)[lane];
+    if (lane < 8) {
+      const int16_t* bs = reinterpret_cast<const int16_t*>(blk + 4 + 256);
+      s[w * 8 + lane] = (int16_t)(bs[2 * lane] + bs[2 * lane + 1]);
+    }
+    if (lane == 0) d[w] = *reinterpret_cast<const float*>(blk);
+  } else {
+    const int nb = k / 32;
+    const long long b = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= (long long)m * nb) return;
+    const int row = (int)(b / nb), bb = (int)(b % nb);
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(xq + b * qmm::kQ80Bytes);
+    uint16_t* dst = reinterpret_cast<uint16_t*>(q8 + (size_t)row * k + 32 * bb);
+    for (int i = 0; i < 16; ++i) dst[i] = src[1 + i];
+    d[b] = qmm::h2f(src[0]);
+  }
+}

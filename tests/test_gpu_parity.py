@@ -311,3 +311,46 @@ def test_matmul_multi_equals_separate_forwards(dt, m):
     ys = matmul_multi(qts, x)
     for q, y in zip(qts, ys):
         assert torch.equal(y, QMatMul.from_qtensor(q).forward(x))
+
+
+# ---------------------------------------------------------------------------
+# prefill GEMM (m > 8): int8 MFMA path
+# ---------------------------------------------------------------------------
+
+GEMM_CASES = [(GgmlDType.Q4K, 100, 512), (GgmlDType.Q4K, 300, 1024), (GgmlDType.Q6K, 100, 512),
+              (GgmlDType.Q6K, 130, 1024), (GgmlDType.Q8_0, 130, 512), (GgmlDType.Q8_0, 64, 1024)]
+
+
+@pytest.mark.parametrize("dt,n,k", GEMM_CASES)
+@pytest.mark.parametrize("m", [9, 64, 100])
+def test_gemm_block_dots_bit_exact(dt, n, k, m):
+    w = np.concatenate([normal(170, (n, k), 0.02), special_weight_rows(k)[:4]])
+    wq = orc.quantize(ORC[dt], w)
+    qt = QTensor.from_ggml(wq, dt, w.shape, device=DEV)
+    x = normal(171 + m, (m, k))
+    x[1, : k // 2] *= 40.0
+    x[2] = 0.0  # an all-zero activation row
+    xq = quantize_rows(dt.vec_dot_type(), torch.from_numpy(x).to(DEV))
+    dots, y = block_dots(qt, xq, m)
+    ref = orc.block_dots(ORC[dt], wq, xq.cpu().numpy(), k)
+    assert np.array_equal(dots.cpu().numpy(), ref)
+    y_ref = orc.matmul_prequant(ORC[dt], xq.cpu().numpy(), wq, k)
+    assert rel_err(y.cpu().numpy(), y_ref) <= TOL
+    # f32 entry point (quantizes into the GEMM plane layout in one kernel)
+    y2 = QMatMul.from_qtensor(qt).forward(torch.from_numpy(x).to(DEV)).cpu().numpy()
+    assert rel_err(y2, orc.matmul(ORC[dt], x, wq, k)) <= TOL
+
+
+@pytest.mark.parametrize("dt,n,k,wseed", [(GgmlDType.Q4K, 14336, 4096, 6), (GgmlDType.Q4K, 4096, 14336, 6),
+                                          (GgmlDType.Q6K, 4096, 14336, 6)])
+def test_prefill_config_shapes_match_cpu_path(dt, n, k, wseed):
+    """Config 4: x 512 x k (seed 5) through QMatMul.forward; the CPU path is
+    evaluated on 48 of the 512 rows (spread over the batch)."""
+    w = normal(wseed, (n, k), 0.02)
+    wq = orc.quantize(ORC[dt], w)
+    qt = QTensor.from_ggml(wq, dt, (n, k), device=DEV)
+    x = normal(5, (512, k))
+    y = QMatMul.from_qtensor(qt).forward(torch.from_numpy(x).to(DEV)).cpu().numpy()
+    rows = np.linspace(0, 511, 48).astype(int)
+    y_ref = orc.matmul(ORC[dt], x[rows], wq, k)
+    assert rel_err(y[rows], y_ref) <= TOL
