@@ -521,7 +521,8 @@ static int gemm(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, f
                 hipStream_t s) {
   const Planes pl = mmq_planes(w->dtype, m, w->k);
   const int fmt = fmt_of(w->dtype);
-  const char* name = fmt == kFmtQ4K ? "qmm_mmq_q4k" : fmt == kFmtQ6K ? "qmm_mmq_q6k" : "qmm_mmq_q8_0";
+  char name[40];
+  snprintf(name, sizeof(name), "qmm_mmq_%s%s", fmt_name(fmt), dump ? "_dump" : "");
   const void* wq = w->data;
   const void* q8 = ws + pl.q8;
   const void* dd = ws + pl.d;

@@ -125,9 +125,9 @@ __device__ __forceinline__ void mmq_store(const MmqRegs& R, MmqLds& L) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) dst[i] = R.a[i];
   }
-  if (FMT == kFmtQ80) {
-    L.ad[(t >> 2) * 8 + 2 * (t & 3)] = R.ad[0];
-    L.ad[(t >> 2) * 8 + 2 * (t & 3) + 1] = R.ad[1];
+  if (FMT == kFmtQ80) {  // [block][row] so a lane's four consecutive rows are one float4
+    L.ad[(2 * (t & 3)) * kMmqBM + (t >> 2)] = R.ad[0];
+    L.ad[(2 * (t & 3) + 1) * kMmqBM + (t >> 2)] = R.ad[1];
   } else if (t < kMmqBM) {
     L.ad[t] = R.ad[0];
     if (FMT == kFmtQ4K) {
@@ -201,8 +201,14 @@ __device__ __forceinline__ i32x16 mfma_i8(i8x16 a, i8x16 b, i32x16 c) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
+__device__ __forceinline__ i8x16 as_i8x16(uint4 v) { return __builtin_bit_cast(i8x16, v); }
+
+// Byte `i` (0..7) of an 8-byte word pair.
+__device__ __forceinline__ uint32_t byte8(uint2 w, int i) { return ((i < 4 ? w.x : w.y) >> (8 * (i & 3))) & 0xffu; }
+
 // y[m, n] = sum over K of x[m, :] . W[n, :] with the formats' scaling.
-template <int FMT>
+// DUMP instantiations also write every integer block dot (debug entry point).
+template <int FMT, bool DUMP>
 __device__ __forceinline__ void mmq(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,
                                     const float* __restrict__ xd, const int16_t* __restrict__ xs,
                                     float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump) {
@@ -216,15 +222,15 @@ __device__ __forceinline__ void mmq(const uint8_t* __restrict__ wq, const int8_t
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 31, h = lane >> 5;
   const int wm = wave & 1, wn = wave >> 1;
+  const int col0 = 64 * wn + r, col1 = col0 + 32;  // this lane's output columns (tiles 0, 1)
+  const int rowb = 32 * wm + 4 * h;                  // + 8g + i: this lane's output rows
 
   i32x16 zero;
 #pragma unroll
   for (int j = 0; j < 16; ++j) zero[j] = 0;
-  float acc[2][16];
+  float acc0[16], acc1[16];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[t][j] = 0.0f;
+  for (int j = 0; j < 16; ++j) acc0[j] = acc1[j] = 0.0f;
 
   MmqRegs R;
   mmq_load<FMT>(R, xq, xd, xs, wq, wd, M, N, K, m0, n0, 0);
@@ -235,140 +241,142 @@ __device__ __forceinline__ void mmq(const uint8_t* __restrict__ wq, const int8_t
     if (kb + 1 < nbk) mmq_load<FMT>(R, xq, xd, xs, wq, wd, M, N, K, m0, n0, kb + 1);
 
     const int8_t* arow = L.a + (32 * wm + r) * kMmqStride + 16 * h;
-    int isum[2][16];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) isum[t][j] = 0;
+    const int8_t* b0row = L.b + col0 * kMmqStride + 16 * h;
+    const int8_t* b1row = L.b + col1 * kMmqStride + 16 * h;
 
-    if (FMT == kFmtQ80) {
+    if constexpr (FMT == kFmtQ80) {
 #pragma unroll 1
       for (int c = 0; c < 8; ++c) {
         const i8x16 a = *reinterpret_cast<const i8x16*>(arow + 32 * c);
+        const i32x16 P0 = mfma_i8(a, *reinterpret_cast<const i8x16*>(b0row + 32 * c), zero);
+        const i32x16 P1 = mfma_i8(a, *reinterpret_cast<const i8x16*>(b1row + 32 * c), zero);
+        const float dw0 = L.bd[8 * col0 + c], dw1 = L.bd[8 * col1 + c];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int col = 64 * wn + 32 * t + r;
-          const i8x16 b = *reinterpret_cast<const i8x16*>(L.b + col * kMmqStride + 32 * c + 16 * h);
-          const i32x16 P = mfma_i8(a, b, zero);
-          const float dw = L.bd[8 * col + c];
+        for (int g = 0; g < 4; ++g) {
+          const float4 dx = *reinterpret_cast<const float4*>(&L.ad[c * kMmqBM + rowb + 8 * g]);
+          const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            acc0[4 * g + i] += (dw0 * dxs[i]) * (float)P0[4 * g + i];
+            acc1[4 * g + i] += (dw1 * dxs[i]) * (float)P1[4 * g + i];
+          }
+        }
+        if (DUMP) {
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
-            const int row = 32 * wm + 8 * (j >> 2) + 4 * h + (j & 3);
-            acc[t][j] += (dw * L.ad[8 * row + c]) * (float)P[j];
-            if (dump != nullptr && m0 + row < M && n0 + col < N)
-              dump[((size_t)(m0 + row) * N + n0 + col) * nbw + 8 * kb + c] = P[j];
+            const int row = m0 + rowb + 8 * (j >> 2) + (j & 3);
+            if (row < M && n0 + col0 < N) dump[((size_t)row * N + n0 + col0) * nbw + 8 * kb + c] = P0[j];
+            if (row < M && n0 + col1 < N) dump[((size_t)row * N + n0 + col1) * nbw + 8 * kb + c] = P1[j];
           }
         }
       }
       continue;
     }
 
-    if (FMT == kFmtQ4K) {
+    int is0[16], is1[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) is0[j] = is1[j] = 0;
+
+    if constexpr (FMT == kFmtQ4K) {
+      const uint2 sc0 = *reinterpret_cast<const uint2*>(L.bsc + 16 * col0);
+      const uint2 sc1 = *reinterpret_cast<const uint2*>(L.bsc + 16 * col1);
 #pragma unroll 1
       for (int c = 0; c < 8; ++c) {
         const i8x16 a = *reinterpret_cast<const i8x16*>(arow + 32 * c);
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int col = 64 * wn + 32 * t + r;
-          const i8x16 b = *reinterpret_cast<const i8x16*>(L.b + col * kMmqStride + 32 * c + 16 * h);
-          const i32x16 P = mfma_i8(a, b, zero);
-          const int sc = L.bsc[16 * col + c];
-#pragma unroll
-          for (int j = 0; j < 16; ++j) isum[t][j] += sc * P[j];
-        }
-      }
-      // mins: two MFMAs over the 8 sub-block sums (only lane half 0 carries data)
-      i8x16 alo, ahi;
-      {
-        const int8_t* s = L.as + 16 * (32 * wm + r);
+        const i32x16 P0 = mfma_i8(a, *reinterpret_cast<const i8x16*>(b0row + 32 * c), zero);
+        const i32x16 P1 = mfma_i8(a, *reinterpret_cast<const i8x16*>(b1row + 32 * c), zero);
+        const int s0 = (int)byte8(sc0, c), s1 = (int)byte8(sc1, c);
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          alo[j] = (h == 0 && j < 8) ? s[j] : (char)0;
-          ahi[j] = (h == 0 && j < 8) ? s[8 + j] : (char)0;
+          is0[j] += __mul24(s0, P0[j]);  // |P| < 2^23: full-rate 24-bit multiply
+          is1[j] += __mul24(s1, P1[j]);
         }
       }
+      // mins: sum_j m_j * (32-element sum)_j as two zero-padded MFMAs
+      const uint4 sv = *reinterpret_cast<const uint4*>(L.as + 16 * (32 * wm + r));
+      const uint4 zero4 = make_uint4(0, 0, 0, 0);
+      const i8x16 alo = as_i8x16(h == 0 ? make_uint4(sv.x, sv.y, 0, 0) : zero4);
+      const i8x16 ahi = as_i8x16(h == 0 ? make_uint4(sv.z, sv.w, 0, 0) : zero4);
+      const uint2 mn0 = *reinterpret_cast<const uint2*>(L.bsc + 16 * col0 + 8);
+      const uint2 mn1 = *reinterpret_cast<const uint2*>(L.bsc + 16 * col1 + 8);
+      const i8x16 bm0 = as_i8x16(h == 0 ? make_uint4(mn0.x, mn0.y, 0, 0) : zero4);
+      const i8x16 bm1 = as_i8x16(h == 0 ? make_uint4(mn1.x, mn1.y, 0, 0) : zero4);
+      const i32x16 L0 = mfma_i8(alo, bm0, zero), H0 = mfma_i8(ahi, bm0, zero);
+      const i32x16 L1 = mfma_i8(alo, bm1, zero), H1 = mfma_i8(ahi, bm1, zero);
+      const float dw0 = L.bd[8 * col0], dm0 = L.bd[8 * col0 + 1];
+      const float dw1 = L.bd[8 * col1], dm1 = L.bd[8 * col1 + 1];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int col = 64 * wn + 32 * t + r;
-        i8x16 bm;
-        const int8_t* mn = L.bsc + 16 * col + 8;
+      for (int g = 0; g < 4; ++g) {
+        const float4 dx = *reinterpret_cast<const float4*>(&L.ad[rowb + 8 * g]);
+        const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
 #pragma unroll
-        for (int j = 0; j < 16; ++j) bm[j] = (h == 0 && j < 8) ? mn[j] : (char)0;
-        const i32x16 Plo = mfma_i8(alo, bm, zero);
-        const i32x16 Phi = mfma_i8(ahi, bm, zero);
-        const float dw = L.bd[8 * col], dmin = L.bd[8 * col + 1];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const float4 dx = *reinterpret_cast<const float4*>(&L.ad[32 * wm + 8 * g + 4 * h]);
-          const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int j = 4 * g + i;
-            const int ism = Phi[j] * 64 + Plo[j];
-            acc[t][j] += dxs[i] * (dw * (float)isum[t][j] - dmin * (float)ism);
-            if (dump != nullptr) {
-              const int row = m0 + 32 * wm + 8 * g + 4 * h + i;
-              const int cl = n0 + col;
-              if (row < M && cl < N) {
-                const size_t o = ((size_t)row * N + cl) * nbk + kb;
-                dump[2 * o] = isum[t][j];
-                dump[2 * o + 1] = ism;
-              }
+        for (int i = 0; i < 4; ++i) {
+          const int j = 4 * g + i;
+          const int im0 = H0[j] * 64 + L0[j], im1 = H1[j] * 64 + L1[j];
+          acc0[j] += dxs[i] * (dw0 * (float)is0[j] - dm0 * (float)im0);
+          acc1[j] += dxs[i] * (dw1 * (float)is1[j] - dm1 * (float)im1);
+          if (DUMP) {
+            const int row = m0 + rowb + 8 * g + i;
+            if (row < M && n0 + col0 < N) {
+              const size_t o = ((size_t)row * N + n0 + col0) * nbk + kb;
+              dump[2 * o] = is0[j];
+              dump[2 * o + 1] = im0;
+            }
+            if (row < M && n0 + col1 < N) {
+              const size_t o = ((size_t)row * N + n0 + col1) * nbk + kb;
+              dump[2 * o] = is1[j];
+              dump[2 * o + 1] = im1;
             }
           }
         }
       }
-    } else {  // Q6_K
+    } else {  // Q6_K: groups of 16 with their own scale; one MFMA per group (other half masked)
+      const uint4 sc0 = *reinterpret_cast<const uint4*>(L.bsc + 16 * col0);
+      const uint4 sc1 = *reinterpret_cast<const uint4*>(L.bsc + 16 * col1);
+      const uint4 zero4 = make_uint4(0, 0, 0, 0);
 #pragma unroll 1
       for (int c = 0; c < 8; ++c) {
-        const i8x16 a = *reinterpret_cast<const i8x16*>(arow + 32 * c);
-        i8x16 a0, a1;
+        const uint4 av = *reinterpret_cast<const uint4*>(arow + 32 * c);
+        const i8x16 alo = as_i8x16(h == 0 ? av : zero4), ahi = as_i8x16(h == 1 ? av : zero4);
+        const i8x16 b0 = *reinterpret_cast<const i8x16*>(b0row + 32 * c);
+        const i8x16 b1 = *reinterpret_cast<const i8x16*>(b1row + 32 * c);
+        const i32x16 P00 = mfma_i8(alo, b0, zero), P01 = mfma_i8(ahi, b0, zero);
+        const i32x16 P10 = mfma_i8(alo, b1, zero), P11 = mfma_i8(ahi, b1, zero);
+        const uint32_t w0 = (c < 2 ? sc0.x : c < 4 ? sc0.y : c < 6 ? sc0.z : sc0.w) >> (16 * (c & 1));
+        const uint32_t w1 = (c < 2 ? sc1.x : c < 4 ? sc1.y : c < 6 ? sc1.z : sc1.w) >> (16 * (c & 1));
+        const int s00 = (int)(int8_t)(w0 & 0xff), s01 = (int)(int8_t)((w0 >> 8) & 0xff);
+        const int s10 = (int)(int8_t)(w1 & 0xff), s11 = (int)(int8_t)((w1 >> 8) & 0xff);
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          a0[j] = h == 0 ? a[j] : (char)0;
-          a1[j] = h == 1 ? a[j] : (char)0;
-        }
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int col = 64 * wn + 32 * t + r;
-          const i8x16 b = *reinterpret_cast<const i8x16*>(L.b + col * kMmqStride + 32 * c + 16 * h);
-          const i32x16 P0 = mfma_i8(a0, b, zero);
-          const i32x16 P1 = mfma_i8(a1, b, zero);
-          const int s0 = L.bsc[16 * col + 2 * c], s1 = L.bsc[16 * col + 2 * c + 1];
-#pragma unroll
-          for (int j = 0; j < 16; ++j) isum[t][j] += s0 * P0[j] + s1 * P1[j];
+          is0[j] += __mul24(s00, P00[j]) + __mul24(s01, P01[j]);
+          is1[j] += __mul24(s10, P10[j]) + __mul24(s11, P11[j]);
         }
       }
+      const float dw0 = L.bd[8 * col0], dw1 = L.bd[8 * col1];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int col = 64 * wn + 32 * t + r;
-        const float dw = L.bd[8 * col];
+      for (int g = 0; g < 4; ++g) {
+        const float4 dx = *reinterpret_cast<const float4*>(&L.ad[rowb + 8 * g]);
+        const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const float4 dx = *reinterpret_cast<const float4*>(&L.ad[32 * wm + 8 * g + 4 * h]);
-          const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int j = 4 * g + i;
-            acc[t][j] += dxs[i] * (dw * (float)isum[t][j]);
-            if (dump != nullptr) {
-              const int row = m0 + 32 * wm + 8 * g + 4 * h + i;
-              const int cl = n0 + col;
-              if (row < M && cl < N) dump[((size_t)row * N + cl) * nbk + kb] = isum[t][j];
-            }
+        for (int i = 0; i < 4; ++i) {
+          const int j = 4 * g + i;
+          acc0[j] += dxs[i] * (dw0 * (float)is0[j]);
+          acc1[j] += dxs[i] * (dw1 * (float)is1[j]);
+          if (DUMP) {
+            const int row = m0 + rowb + 8 * g + i;
+            if (row < M && n0 + col0 < N) dump[((size_t)row * N + n0 + col0) * nbk + kb] = is0[j];
+            if (row < M && n0 + col1 < N) dump[((size_t)row * N + n0 + col1) * nbk + kb] = is1[j];
           }
         }
       }
     }
   }
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int row = m0 + 32 * wm + 8 * (j >> 2) + 4 * h + (j & 3);
-      const int col = n0 + 64 * wn + 32 * t + r;
-      if (row < M && col < N) y[(size_t)row * ldy + col] = acc[t][j];
-    }
+  for (int j = 0; j < 16; ++j) {
+    const int row = m0 + rowb + 8 * (j >> 2) + (j & 3);
+    if (row < M && n0 + col0 < N) y[(size_t)row * ldy + n0 + col0] = acc0[j];
+    if (row < M && n0 + col1 < N) y[(size_t)row * ldy + n0 + col1] = acc1[j];
+  }
 }
 
 }  // namespace qmm
@@ -409,12 +417,18 @@ extern "C" __global__ void __launch_bounds__(256) qmm_quantize_q8_0_mmq(const fl
   if (l == 0) d[bc] = qmm::h2f(p[0]);
 }
 
-#define QMM_MMQ_KERNEL(FMT, NAME)                                                                          \
-  extern "C" __global__ void __launch_bounds__(256)                                                        \
-      qmm_mmq_##NAME(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                        \
-                     const float* __restrict__ xd, const int16_t* __restrict__ xs, float* __restrict__ y, \
-                     int M, int N, int K, int ldy, int* __restrict__ dump) {                               \
-    qmm::mmq<FMT>(wq, xq, xd, xs, y, M, N, K, ldy, dump);                                                  \
+#define QMM_MMQ_KERNEL(FMT, NAME)                                                                            \
+  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))               \
+      qmm_mmq_##NAME(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                          \
+                     const float* __restrict__ xd, const int16_t* __restrict__ xs, float* __restrict__ y,   \
+                     int M, int N, int K, int ldy, int* __restrict__ dump) {                                 \
+    qmm::mmq<FMT, false>(wq, xq, xd, xs, y, M, N, K, ldy, dump);                                             \
+  }                                                                                                          \
+  extern "C" __global__ void __launch_bounds__(256)                                                          \
+      qmm_mmq_##NAME##_dump(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                   \
+                            const float* __restrict__ xd, const int16_t* __restrict__ xs,                    \
+                            float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump) {   \
+    qmm::mmq<FMT, true>(wq, xq, xd, xs, y, M, N, K, ldy, dump);                                              \
   }
 
 QMM_MMQ_KERNEL(qmm::kFmtQ4K, q4k)
