@@ -143,6 +143,39 @@ int qmm_matmul_q(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int6
 int qmm_block_dots(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy,
                    int32_t *dots, void *stream);
 
+/* ---- mixture of experts (MoeMlp::forward, crates/llm/candle-llm/src/models/llama.rs:1416-1487) ---- */
+
+/* Routing on the device: logits f32 [tokens, experts] -> softmax -> top-k
+ * (renormalised over the selected experts when `renormalize`). Outputs are
+ * device int32/f32 arrays: counts[experts], offsets[experts + 1] (exclusive
+ * prefix), and tokens*topk (token, weight) pairs grouped by expert in
+ * increasing expert order (pair_token, pair_weight); token_pairs[t*topk + s]
+ * lists token t's pairs in increasing expert order. Replaces the host-side
+ * top-k of llama.rs:1426-1451. Limits: tokens <= 4096, tokens*topk <= 8192. */
+int qmm_moe_route(const float *logits, int64_t tokens, int experts, int topk, int renormalize,
+                  int32_t *counts, int32_t *offsets, int32_t *pair_token, float *pair_weight,
+                  int32_t *token_pairs, void *stream);
+
+/* Expert-grouped GEMV (replaces moe_gemm_gguf, ffi.rs:25-39): w[j] (count 1..2)
+ * are stacked expert weights [experts*N, K] of one dtype; xq holds `pairs`
+ * rows of vec-dot blocks grouped by expert (counts/offsets as produced by
+ * qmm_moe_route); y[j] receives [pairs, N] f32. Each active expert's weights
+ * are streamed once; experts without tokens read nothing. */
+int qmm_moe_gemv(const qmm_qtensor *const *w, int count, int experts, const void *xq, int64_t pairs,
+                 const int32_t *counts, const int32_t *offsets, float *const *y, void *stream);
+
+/* The whole expert FFN at decode batch sizes: x f32 [tokens, hidden] (row
+ * stride ldx), router logits f32 [tokens, experts], stacked gate/up
+ * [experts*ffn, hidden] and down [experts*hidden, ffn] weights; out f32
+ * [tokens, hidden] (row stride ldo) = sum over each token's top-k experts, in
+ * increasing expert order, of weight * down(silu(gate(x)) * up(x)).
+ * ws: device scratch of qmm_moe_ffn_workspace_size() bytes. */
+size_t qmm_moe_ffn_workspace_size(const qmm_qtensor *gate, const qmm_qtensor *down, int64_t tokens,
+                                  int experts, int topk);
+int qmm_moe_ffn(const float *x, int64_t tokens, int64_t ldx, const float *logits, int experts, int topk,
+                const qmm_qtensor *gate, const qmm_qtensor *up, const qmm_qtensor *down, float *out,
+                int64_t ldo, void *ws, size_t ws_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

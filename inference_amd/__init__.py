@@ -14,6 +14,8 @@ from .qmm import (  # noqa: F401
     QuantSpec,
     block_dots,
     matmul_multi,
+    moe_ffn,
+    moe_route,
     matmul_q,
     quantize_rows,
 )

@@ -186,7 +186,7 @@ __device__ __forceinline__ uint4 q6_bytes(uint4 ql, uint4 qh, int sh) {
 template <int FMT, int M>
 __device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t* __restrict__ lds,
                                           int nblk, int xb, int nbx, bool ok, float (&acc)[M],
-                                          int (&ia)[M], int (&ib)[M]) {
+                                          int (&ia)[M], int (&ib)[M], int mrows) {
   if constexpr (FMT == kFmtQ4K) {
     const uint32_t* lsum = reinterpret_cast<const uint32_t*>(lds + 256 * nblk);
     const float* ld = reinterpret_cast<const float*>(lsum + 8 * nblk);
@@ -202,6 +202,7 @@ __device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t*
     const uint4 w0 = lo_nib(s.b), w1 = lo_nib(s.c), w2 = hi_nib(s.b), w3 = hi_nib(s.c);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
+      if (M > 1 && m >= mrows) break;  // wave-uniform
       const int bx = xb + m * nbx;
       const uint8_t* e = lds + 256 * bx;
       const int sw = (l >> 1) | ((bx & 1) << 1);
@@ -237,6 +238,7 @@ __device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t*
     const uint4 w3 = q6_bytes(hi_nib(s.b), s.e, sh1);        // +80
 #pragma unroll
     for (int m = 0; m < M; ++m) {
+      if (M > 1 && m >= mrows) break;  // wave-uniform
       const int bx = xb + m * nbx;
       const uint8_t* e = lds + 256 * bx;
       const int sw = (l >> 1) | ((bx & 1) << 1);
@@ -259,6 +261,7 @@ __device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t*
     const float dw = h2f(s.d);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
+      if (M > 1 && m >= mrows) break;  // wave-uniform
       const int bx = xb + m * nbx;
       const int sw = (bx >> 2) & 1;
       const uint4 x0 = *reinterpret_cast<const uint4*>(lds + 32 * bx + 16 * (0 ^ sw));
@@ -276,8 +279,10 @@ __device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t*
 struct GemvJobs {
   const uint8_t* wq[4];  // device-layout blocks of each matrix
   float* y[4];           // outputs, y[j][m * ldy[j] + row]
-  int rows[4];
+  int rows[4];           // rows computed for job j
   int ldy[4];
+  int row0[4];           // first row of job j within its tensor (stacked experts)
+  int trows[4];          // rows of the whole tensor (its f16 scales follow all of them)
   int njobs;
   int total;
 };
@@ -288,8 +293,9 @@ struct RowRef {
   const uint16_t* wd;
   float* y;
   int ldy;
-  int row;   // row within its matrix
-  int rows;  // rows of its matrix
+  int out;   // output row within the job
+  int row;   // row within the weight tensor
+  int rows;  // rows of the job
   bool ok;
 };
 
@@ -300,34 +306,41 @@ __device__ __forceinline__ RowRef locate(const GemvJobs& jobs, int gr, int nb) {
   int base = 0;
   const uint8_t* wq = jobs.wq[0];
   float* y = jobs.y[0];
-  int rows = jobs.rows[0], ldy = jobs.ldy[0];
+  int rows = jobs.rows[0], ldy = jobs.ldy[0], row0 = jobs.row0[0], trows = jobs.trows[0];
   if (jobs.njobs > 1 && gr >= rows) {
     base = rows;
     wq = jobs.wq[1];
     y = jobs.y[1];
     rows = jobs.rows[1];
     ldy = jobs.ldy[1];
+    row0 = jobs.row0[1];
+    trows = jobs.trows[1];
     if (jobs.njobs > 2 && gr >= base + rows) {
       base += rows;
       wq = jobs.wq[2];
       y = jobs.y[2];
       rows = jobs.rows[2];
       ldy = jobs.ldy[2];
+      row0 = jobs.row0[2];
+      trows = jobs.trows[2];
       if (jobs.njobs > 3 && gr >= base + rows) {
         base += rows;
         wq = jobs.wq[3];
         y = jobs.y[3];
         rows = jobs.rows[3];
         ldy = jobs.ldy[3];
+        row0 = jobs.row0[3];
+        trows = jobs.trows[3];
       }
     }
   }
   r.wq = wq;
   r.wd = FMT == kFmtQ4K ? nullptr
-                        : reinterpret_cast<const uint16_t*>(wq + (size_t)rows * nb * FmtInfo<FMT>::kBodyBytes);
+                        : reinterpret_cast<const uint16_t*>(wq + (size_t)trows * nb * FmtInfo<FMT>::kBodyBytes);
   r.y = y;
   r.ldy = ldy;
-  r.row = gr - base;
+  r.out = gr - base;   // output row
+  r.row = r.out + row0;  // row within the tensor
   r.rows = rows;
   r.ok = gr < jobs.total;
   return r;
@@ -431,7 +444,7 @@ __device__ __forceinline__ void quantize_act(const float* __restrict__ x, long l
 //   dump (optional, single job): int32 block dots [M][rows][nb](x2 for Q4_K).
 template <int FMT, int M, int R, int U, bool FUSED>
 __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restrict__ act, long long ldx, int K,
-                                     int* __restrict__ dump) {
+                                     int* __restrict__ dump, int mrows = M) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int LPB = FmtInfo<FMT>::kLanesPerBlock;
   constexpr int BPI = 64 / LPB;  // blocks per wave iteration
@@ -452,9 +465,9 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
   WSlice ws[R][U];
   load_batch<FMT, R, U>(ws, rr, 0, nb, g, l);
   if constexpr (FUSED)
-    quantize_act<FMT>(reinterpret_cast<const float*>(act), ldx, M, nb, lds);
+    quantize_act<FMT>(reinterpret_cast<const float*>(act), ldx, mrows, nb, lds);
   else
-    stage_act<FMT>(reinterpret_cast<const uint8_t*>(act), M * nb, lds);
+    stage_act<FMT>(reinterpret_cast<const uint8_t*>(act), mrows * nb, lds);
   __syncthreads();
 
   for (; row0 < jobs.total; row0 += row_step) {
@@ -473,7 +486,7 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
           const int b = (it0 + u) * BPI + g;
           const bool ok = rr[r].ok && b < nb;
           int ia[M], ib[M];
-          dot_slice<FMT, M>(ws[r][u], l, lds, M * nb, ok ? b : 0, nb, ok, acc[r], ia, ib);
+          dot_slice<FMT, M>(ws[r][u], l, lds, mrows * nb, ok ? b : 0, nb, ok, acc[r], ia, ib, mrows);
           if (dump != nullptr) {
 #pragma unroll
             for (int m = 0; m < M; ++m) {
@@ -483,8 +496,8 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
                 va += __shfl_xor(va, off);
                 vb += __shfl_xor(vb, off);
               }
-              if (ok && l == 0) {
-                const size_t o = ((size_t)m * rr[r].rows + rr[r].row) * nb + b;
+              if (ok && l == 0 && m < mrows) {
+                const size_t o = ((size_t)m * rr[r].rows + rr[r].out) * nb + b;
                 if (FMT == kFmtQ4K) {
                   dump[2 * o] = va;
                   dump[2 * o + 1] = vb;
@@ -508,8 +521,9 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int m = 0; m < M; ++m) {
+        if (M > 1 && m >= mrows) break;  // wave-uniform
         const float v = wave_sum(acc[r][m]);
-        if (lane == 0 && cur[r].ok) cur[r].y[(size_t)m * cur[r].ldy + cur[r].row] = v;
+        if (lane == 0 && cur[r].ok && m < mrows) cur[r].y[(size_t)m * cur[r].ldy + cur[r].out] = v;
       }
   }
 }
@@ -521,7 +535,8 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
 #define QMM_GEMV_PARAMS                                                                                   \
   const uint8_t *wq0, const uint8_t *wq1, const uint8_t *wq2, const uint8_t *wq3, float *y0, float *y1,   \
       float *y2, float *y3, int rows0, int rows1, int rows2, int rows3, int ldy0, int ldy1, int ldy2,     \
-      int ldy3, int njobs, int total, const void *__restrict__ act, long long ldx, int K,                 \
+      int ldy3, int row00, int row01, int row02, int row03, int trows0, int trows1, int trows2,           \
+      int trows3, int njobs, int total, const void *__restrict__ act, long long ldx, int K,               \
       int *__restrict__ dump
 #define QMM_GEMV_JOBS                                                                                     \
   qmm::GemvJobs jobs;                                                                                     \
@@ -541,6 +556,14 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
   jobs.ldy[1] = ldy1;                                                                                     \
   jobs.ldy[2] = ldy2;                                                                                     \
   jobs.ldy[3] = ldy3;                                                                                     \
+  jobs.row0[0] = row00;                                                                                   \
+  jobs.row0[1] = row01;                                                                                   \
+  jobs.row0[2] = row02;                                                                                   \
+  jobs.row0[3] = row03;                                                                                   \
+  jobs.trows[0] = trows0;                                                                                 \
+  jobs.trows[1] = trows1;                                                                                 \
+  jobs.trows[2] = trows2;                                                                                 \
+  jobs.trows[3] = trows3;                                                                                 \
   jobs.njobs = njobs;                                                                                     \
   jobs.total = total;
 

@@ -446,6 +446,8 @@ struct GemvJobs {
   float* y[4];
   int rows[4];
   int ldy[4];
+  int row0[4];
+  int trows[4];
   int njobs;
   int total;
 };
@@ -479,6 +481,8 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
     jobs.y[j] = tg[j].y;
     jobs.rows[j] = (int)tg[j].w->n;
     jobs.ldy[j] = (int)tg[j].ldy;
+    jobs.row0[j] = 0;
+    jobs.trows[j] = (int)tg[j].w->n;
     total += tg[j].w->n;
   }
   if (total > (1LL << 31) - 1) return fail(QMM_ERR_INVALID, "too many output rows in one launch");
@@ -510,9 +514,11 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   long long lx = ldx;
   int K = (int)w->k;
   int* dp = dump;
-  void* args[] = {&jobs.wq[0], &jobs.wq[1], &jobs.wq[2], &jobs.wq[3], &jobs.y[0], &jobs.y[1], &jobs.y[2],
-                  &jobs.y[3], &jobs.rows[0], &jobs.rows[1], &jobs.rows[2], &jobs.rows[3], &jobs.ldy[0],
-                  &jobs.ldy[1], &jobs.ldy[2], &jobs.ldy[3], &jobs.njobs, &jobs.total, &a, &lx, &K, &dp};
+  void* args[] = {&jobs.wq[0],    &jobs.wq[1],    &jobs.wq[2],    &jobs.wq[3],    &jobs.y[0],     &jobs.y[1],
+                  &jobs.y[2],     &jobs.y[3],     &jobs.rows[0],  &jobs.rows[1],  &jobs.rows[2],  &jobs.rows[3],
+                  &jobs.ldy[0],   &jobs.ldy[1],   &jobs.ldy[2],   &jobs.ldy[3],   &jobs.row0[0],  &jobs.row0[1],
+                  &jobs.row0[2],  &jobs.row0[3],  &jobs.trows[0], &jobs.trows[1], &jobs.trows[2], &jobs.trows[3],
+                  &jobs.njobs,    &jobs.total,    &a,             &lx,            &K,             &dp};
   return launch(d, name, (unsigned)wgs, 64 * wv, lds, s, args);
 }
 
@@ -692,6 +698,179 @@ int qmm_block_dots(const qmm_qtensor* w, const void* xq, int64_t m, float* y, in
   }
   GemvTarget t = {w, y, ldy};
   return gemv(d, &t, 1, xq, false, 0, (int)m, dots, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// mixture of experts
+// ---------------------------------------------------------------------------
+
+int qmm_moe_route(const float* logits, int64_t tokens, int experts, int topk, int renormalize, int32_t* counts,
+                  int32_t* offsets, int32_t* pair_token, float* pair_weight, int32_t* token_pairs, void* stream) {
+  if (!logits || !counts || !offsets || !pair_token || !pair_weight || !token_pairs)
+    return fail(QMM_ERR_INVALID, "null pointer");
+  if (tokens < 1 || tokens > 4096 || experts < 1 || experts > 256 || topk < 1 || topk > 8 || topk > experts ||
+      tokens * topk > 8192)
+    return fail(QMM_ERR_INVALID, "routing limits: 1 <= tokens <= 4096, tokens*topk <= 8192, topk <= min(8, experts)");
+  Device* d;
+  QMM_TRY(current_device(&d));
+  int T = (int)tokens, E = experts, k = topk, rn = renormalize ? 1 : 0;
+  void* args[] = {&logits, &T, &E, &k, &rn, &counts, &offsets, &pair_token, &pair_weight, &token_pairs};
+  return launch(d, "qmm_moe_route", 1, 256, 0, (hipStream_t)stream, args);
+}
+
+int qmm_moe_gemv(const qmm_qtensor* const* w, int count, int experts, const void* xq, int64_t pairs,
+                 const int32_t* counts, const int32_t* offsets, float* const* y, void* stream) {
+  if (!w || !y || !xq || !counts || !offsets || count < 1 || count > 2)
+    return fail(QMM_ERR_INVALID, "need 1..2 stacked weights, activations, routing arrays and outputs");
+  if (experts < 1 || experts > 65535) return fail(QMM_ERR_INVALID, "bad expert count %d", experts);
+  for (int j = 0; j < count; ++j) {
+    if (!w[j] || !y[j]) return fail(QMM_ERR_INVALID, "null weight or output");
+    if (w[j]->dtype != w[0]->dtype || w[j]->k != w[0]->k || w[j]->n != w[0]->n)
+      return fail(QMM_ERR_INVALID, "stacked expert weights must share dtype and shape");
+  }
+  if (w[0]->n % experts) return fail(QMM_ERR_INVALID, "rows %lld not divisible by %d experts", (long long)w[0]->n, experts);
+  Device* d;
+  QMM_TRY(current_device(&d));
+  const int fmt = fmt_of(w[0]->dtype);
+  const int nb = (int)(w[0]->k / qmm_block_size(w[0]->dtype));
+  const int bpi = fmt == kFmtQ80 ? 64 : 16;
+  const int niter = (nb + bpi - 1) / bpi;
+  const unsigned lds = (unsigned)(8 * nb * (fmt == kFmtQ80 ? 36 : 292));
+  if ((int)lds > d->max_lds) return fail(QMM_ERR_UNSUPPORTED, "expert activation needs %u B of LDS", lds);
+  char name[48];
+  snprintf(name, sizeof(name), "qmm_moe_gemv_%s_u%d", fmt_name(fmt), niter >= 2 ? 2 : 1);
+  const int vt = qmm_vec_dot_type(w[0]->dtype);
+  long long xrow = (w[0]->k / qmm_block_size(vt)) * qmm_type_size(vt);
+  int N = (int)(w[0]->n / experts), E = experts, nj = count, K = (int)w[0]->k, ld = N;
+  const void* w0 = w[0]->data;
+  const void* w1 = count > 1 ? w[1]->data : w[0]->data;
+  float* y0 = y[0];
+  float* y1 = count > 1 ? y[1] : y[0];
+  const void* xp = xq;
+  void* args[] = {&w0, &w1, &nj, &N, &E, &y0, &y1, &ld, &xp, &xrow, &counts, &offsets, &K};
+  // ~20 resident waves per CU spread over the experts (idle experts exit at once)
+  long long gx = ((long long)d->num_cu * 20 / 8 + E - 1) / E;
+  const long long need = ((long long)N * count + 7) / 8;
+  if (gx > need) gx = need;
+  if (gx < 1) gx = 1;
+  hipFunction_t f;
+  QMM_TRY(kernel(d, name, &f));
+  (void)pairs;
+  QMM_HIP(hipModuleLaunchKernel(f, (unsigned)gx, (unsigned)E, 1, 512, 1, 1, lds, (hipStream_t)stream, args, nullptr));
+  return QMM_OK;
+}
+
+// Workspace of qmm_moe_ffn, carved in this order.
+struct MoeWs {
+  size_t counts, offsets, pair_token, pair_weight, token_pairs, xg, xq, g, u, h, hq, yp, total;
+};
+static MoeWs moe_ws(const qmm_qtensor* gate, const qmm_qtensor* down, int64_t T, int E, int k) {
+  MoeWs w;
+  const int64_t P = T * k, H = gate->k, F = gate->n / E;
+  const int vg = qmm_vec_dot_type(gate->dtype), vd = qmm_vec_dot_type(down->dtype);
+  size_t o = 0;
+  auto take = [&o](size_t bytes) {
+    const size_t at = o;
+    o += align256(bytes);
+    return at;
+  };
+  w.counts = take(4 * E);
+  w.offsets = take(4 * (E + 1));
+  w.pair_token = take(4 * P);
+  w.pair_weight = take(4 * P);
+  w.token_pairs = take(4 * P);
+  w.xg = take(vg == QMM_Q8K ? 0 : 4 * P * H);
+  w.xq = take(P * (H / qmm_block_size(vg)) * qmm_type_size(vg));
+  w.g = take(4 * P * F);
+  w.u = take(4 * P * F);
+  w.h = take(4 * P * F);
+  w.hq = take(P * (F / qmm_block_size(vd)) * qmm_type_size(vd));
+  w.yp = take(4 * P * H);
+  w.total = o;
+  return w;
+}
+
+static int check_moe(const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* down, int E, int k) {
+  if (!gate || !up || !down) return fail(QMM_ERR_INVALID, "null expert weight");
+  if (E < 1 || k < 1 || k > 8 || k > E) return fail(QMM_ERR_INVALID, "bad experts/topk %d/%d", E, k);
+  if (gate->dtype != up->dtype || gate->n != up->n || gate->k != up->k)
+    return fail(QMM_ERR_INVALID, "gate and up must share dtype and shape");
+  if (gate->n % E || down->n % E) return fail(QMM_ERR_INVALID, "stacked rows not divisible by %d experts", E);
+  if (down->n / E != gate->k || down->k != gate->n / E)
+    return fail(QMM_ERR_INVALID, "down must be [E*hidden, ffn] for gate/up [E*ffn, hidden]");
+  return QMM_OK;
+}
+
+size_t qmm_moe_ffn_workspace_size(const qmm_qtensor* gate, const qmm_qtensor* down, int64_t tokens, int experts,
+                                  int topk) {
+  if (!gate || !down || tokens < 1 || experts < 1 || topk < 1) return 0;
+  return moe_ws(gate, down, tokens, experts, topk).total;
+}
+
+int qmm_moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* logits, int experts, int topk,
+                const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* down, float* out, int64_t ldo,
+                void* ws, size_t ws_bytes, void* stream) {
+  QMM_TRY(check_moe(gate, up, down, experts, topk));
+  if (!x || !logits || !out || !ws) return fail(QMM_ERR_INVALID, "null pointer");
+  const int64_t H = gate->k, F = gate->n / experts, P = tokens * topk;
+  if (ldx < H || ldo < H) return fail(QMM_ERR_INVALID, "row strides must be >= hidden size");
+  const MoeWs L = moe_ws(gate, down, tokens, experts, topk);
+  if (ws_bytes < L.total) return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed", ws_bytes, L.total);
+  Device* d;
+  QMM_TRY(current_device(&d));
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t* b = (uint8_t*)ws;
+  int32_t* counts = (int32_t*)(b + L.counts);
+  int32_t* offsets = (int32_t*)(b + L.offsets);
+  int32_t* ptok = (int32_t*)(b + L.pair_token);
+  float* pw = (float*)(b + L.pair_weight);
+  int32_t* tpairs = (int32_t*)(b + L.token_pairs);
+  QMM_TRY(qmm_moe_route(logits, tokens, experts, topk, 1, counts, offsets, ptok, pw, tpairs, stream));
+  // gather + quantize the routed token rows (expert order)
+  const int vg = qmm_vec_dot_type(gate->dtype);
+  {
+    const void* xp = x;
+    long long lx = ldx;
+    const int32_t* rows = ptok;
+    int kk = (int)H, nr = (int)P;
+    if (vg == QMM_Q8K) {
+      void* yq = b + L.xq;
+      void* args[] = {&xp, &lx, &rows, &yq, &kk, &nr};
+      QMM_TRY(launch(d, "qmm_quantize_q8k_gather", ceil_div(P * (H / 256), 4), 256, 0, s, args));
+    } else {
+      void* xg = b + L.xg;
+      void* args[] = {&xp, &lx, &rows, &xg, &kk, &nr};
+      QMM_TRY(launch(d, "qmm_gather_rows", ceil_div(P * H, 256), 256, 0, s, args));
+      QMM_TRY(qmm_quantize_rows(vg, (const float*)xg, P, H, H, b + L.xq, stream));
+    }
+  }
+  float* g = (float*)(b + L.g);
+  float* u = (float*)(b + L.u);
+  float* h = (float*)(b + L.h);
+  {
+    const qmm_qtensor* gw[2] = {gate, up};
+    float* gy[2] = {g, u};
+    QMM_TRY(qmm_moe_gemv(gw, 2, experts, b + L.xq, P, counts, offsets, gy, stream));
+  }
+  {
+    long long n = P * F;
+    void* args[] = {&g, &u, &h, &n};
+    QMM_TRY(launch(d, "qmm_silu_mul", ceil_div(n, 256), 256, 0, s, args));
+  }
+  const int vd = qmm_vec_dot_type(down->dtype);
+  QMM_TRY(qmm_quantize_rows(vd, h, P, F, F, b + L.hq, stream));
+  float* yp = (float*)(b + L.yp);
+  {
+    const qmm_qtensor* dw[1] = {down};
+    float* dy[1] = {yp};
+    QMM_TRY(qmm_moe_gemv(dw, 1, experts, b + L.hq, P, counts, offsets, dy, stream));
+  }
+  {
+    int T = (int)tokens, k = topk, N = (int)H, lo = (int)ldo;
+    void* args[] = {&yp, &pw, &tpairs, &T, &k, &N, &out, &lo};
+    QMM_TRY(launch(d, "qmm_moe_combine", ceil_div(tokens * H, 256), 256, 0, s, args));
+  }
+  return QMM_OK;
 }
 
 }  // extern "C"

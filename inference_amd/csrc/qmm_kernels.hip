@@ -6,3 +6,4 @@
 #include "qmm_quant_kernels.h"
 #include "qmm_gemv_kernels.h"
 #include "qmm_mmq_kernels.h"
+#include "qmm_moe_kernels.h"

@@ -1,0 +1,191 @@
+// Mixture-of-experts FFN at decode batch sizes (config 5 of the benchmark):
+// routing, per-expert gathered GEMVs over stacked expert weights, SiLU*mul
+// and the weighted scatter back to tokens, all on the device.
+//
+// Host semantics followed: MoeMlp::forward (crates/llm/candle-llm/src/models/llama.rs:1416-1487):
+// softmax over the router logits, top-k by probability, weights renormalised
+// over the selected experts, each expert's LlamaMlp (gate, up, silu(gate)*up,
+// down) on its tokens, outputs scaled by the weight and index_add-ed back in
+// increasing expert order. The CUDA kernel the expert GEMV replaces is
+// moe_gemm_gguf (candle-kernels/src/moe/moe_gguf.cu:56-216).
+#pragma once
+
+#include "qmm_common.h"
+#include "qmm_gemv_kernels.h"
+#include "qmm_quant_kernels.h"
+
+// Routing: logits f32 [T][E] -> per-expert lists of (token, weight) pairs,
+// experts in increasing order, tokens in increasing order within an expert.
+//   counts[e], offsets[e] (exclusive prefix, offsets[E] = T*k),
+//   pair_token[p], pair_weight[p] for p in [offsets[e], offsets[e] + counts[e]),
+//   token_pairs[t*k + s] = the pairs of token t in increasing expert order.
+// One workgroup; T <= 4096, T*k <= 8192, E <= 256, k <= 8.
+extern "C" __global__ void __launch_bounds__(256) qmm_moe_route(const float* __restrict__ logits, int T, int E,
+                                                                int k, int renorm, int* __restrict__ counts,
+                                                                int* __restrict__ offsets,
+                                                                int* __restrict__ pair_token,
+                                                                float* __restrict__ pair_weight,
+                                                                int* __restrict__ token_pairs) {
+#pragma clang fp contract(off)
+  __shared__ short sel_e[8192];
+  __shared__ float sel_w[8192];
+  __shared__ int cnt[4096];
+  for (int t = threadIdx.x; t < T; t += blockDim.x) {
+    const float* l = logits + (size_t)t * E;
+    float mx = l[0];
+    for (int e = 1; e < E; ++e) mx = fmaxf(mx, l[e]);
+    float sum = 0.0f;
+    for (int e = 0; e < E; ++e) sum += expf(l[e] - mx);
+    // top-k by probability (highest first, lowest expert index on ties)
+    unsigned long long taken[4] = {0, 0, 0, 0};
+    float denom = 0.0f;
+    float p[8];
+    int ids[8];
+    for (int s = 0; s < k; ++s) {
+      int best = -1;
+      float bp = 0.0f;
+      for (int e = 0; e < E; ++e) {
+        if ((taken[e >> 6] >> (e & 63)) & 1ull) continue;
+        const float pe = expf(l[e] - mx) / sum;
+        if (best < 0 || pe > bp) {
+          best = e;
+          bp = pe;
+        }
+      }
+      taken[best >> 6] |= 1ull << (best & 63);
+      ids[s] = best;
+      p[s] = bp;
+      denom += bp;
+    }
+    denom = fmaxf(denom, 1.17549435e-38f);
+    for (int s = 0; s < k; ++s) {
+      sel_e[t * k + s] = (short)ids[s];
+      sel_w[t * k + s] = renorm ? p[s] / denom : p[s];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int pos = 0;
+    for (int e = 0; e < E; ++e) {
+      offsets[e] = pos;
+      int c = 0;
+      for (int t = 0; t < T; ++t)
+        for (int s = 0; s < k; ++s)
+          if (sel_e[t * k + s] == e) {
+            pair_token[pos] = t;
+            pair_weight[pos] = sel_w[t * k + s];
+            ++pos;
+            ++c;
+          }
+      counts[e] = c;
+    }
+    offsets[E] = pos;
+    for (int t = 0; t < T; ++t) cnt[t] = 0;
+    for (int p = 0; p < pos; ++p) {  // pairs are in expert order, so each token's come in that order
+      const int t = pair_token[p];
+      token_pairs[t * k + cnt[t]++] = p;
+    }
+  }
+}
+
+// f32 row gather: out row i = x[rows[i]] (k columns).
+extern "C" __global__ void qmm_gather_rows(const float* __restrict__ x, long long ldx, const int* __restrict__ rows,
+                                           float* __restrict__ out, int k, int nrows) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)nrows * k) return;
+  const int r = (int)(i / k), c = (int)(i % k);
+  out[i] = x[(long long)rows[r] * ldx + c];
+}
+
+// Q8_K quantization of gathered rows: out row i = quantize(x[rows[i]]).
+extern "C" __global__ void __launch_bounds__(256) qmm_quantize_q8k_gather(const float* __restrict__ x,
+                                                                          long long ldx,
+                                                                          const int* __restrict__ rows,
+                                                                          uint8_t* __restrict__ y, int k,
+                                                                          int nrows) {
+  const int nb = k / 256;
+  const long long w = (long long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (w >= (long long)nrows * nb) return;
+  const int i = (int)(w / nb), b = (int)(w % nb);
+  qmm::q8k_block(x + (long long)rows[i] * ldx + 256LL * b, y + w * qmm::kQ8KBytes, threadIdx.x & 63);
+}
+
+// h = silu(g) * u, elementwise over [rows][k] (ld = row stride of g, u, h),
+// with silu(v) = v / (1 + exp(-v)) as the reference's f32 op.
+extern "C" __global__ void qmm_silu_mul(const float* __restrict__ g, const float* __restrict__ u,
+                                        float* __restrict__ h, long long n) {
+#pragma clang fp contract(off)
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float v = g[i];
+  h[i] = v / (1.0f + expf(-v)) * u[i];
+}
+
+// out[t][n] = sum over the pairs of token t (in increasing expert order) of
+// weight * y_pair[n], accumulated from zero like index_add.
+extern "C" __global__ void qmm_moe_combine(const float* __restrict__ yp, const float* __restrict__ pair_weight,
+                                           const int* __restrict__ token_pairs, int T, int k, int N,
+                                           float* __restrict__ out, int ldo) {
+#pragma clang fp contract(off)
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)T * N) return;
+  const int t = (int)(i / N), n = (int)(i % N);
+  float acc = 0.0f;
+  for (int s = 0; s < k; ++s) {
+    const int p = token_pairs[t * k + s];
+    const float v = yp[(size_t)p * N + n] * pair_weight[p];
+    acc = acc + v;
+  }
+  out[(size_t)t * ldo + n] = acc;
+}
+
+// Expert-grouped GEMV: blockIdx.y = expert e; its counts[e] token rows (up to
+// 8 per pass) of pre-quantized activations start at row offsets[e] of xq.
+// Weights are stacked [E*N, K] tensors (njobs of them, e.g. gate and up);
+// expert e uses rows [e*N, e*N + N). Outputs y_j[(offsets[e] + m) * ldy + n].
+// Experts without tokens exit before reading any weight.
+template <int FMT, int U>
+__device__ __forceinline__ void moe_gemv(const uint8_t* w0, const uint8_t* w1, int njobs, int N, int E, float* y0,
+                                         float* y1, int ldy, const uint8_t* __restrict__ xq, long long xrow,
+                                         const int* __restrict__ counts, const int* __restrict__ offsets, int K) {
+  const int e = blockIdx.y;
+  const int me = counts[e];
+  if (me == 0) return;
+  const int off = offsets[e];
+  for (int mc = 0; mc < me; mc += 8) {
+    if (mc > 0) __syncthreads();
+    qmm::GemvJobs jobs;
+    jobs.wq[0] = w0;
+    jobs.wq[1] = w1;
+    jobs.wq[2] = jobs.wq[3] = nullptr;
+    jobs.y[0] = y0 + (size_t)(off + mc) * ldy;
+    jobs.y[1] = y1 + (size_t)(off + mc) * ldy;
+    jobs.y[2] = jobs.y[3] = nullptr;
+    jobs.rows[0] = jobs.rows[1] = N;
+    jobs.rows[2] = jobs.rows[3] = 0;
+    jobs.ldy[0] = jobs.ldy[1] = jobs.ldy[2] = jobs.ldy[3] = ldy;
+    jobs.row0[0] = jobs.row0[1] = e * N;
+    jobs.row0[2] = jobs.row0[3] = 0;
+    jobs.trows[0] = jobs.trows[1] = E * N;
+    jobs.trows[2] = jobs.trows[3] = 0;
+    jobs.njobs = njobs;
+    jobs.total = njobs * N;
+    const int mrows = me - mc < 8 ? me - mc : 8;
+    qmm::gemv<FMT, 8, 1, U, false>(jobs, xq + (size_t)(off + mc) * xrow, 0, K, nullptr, mrows);
+  }
+}
+
+#define QMM_MOE_KERNEL(FMT, NAME, U)                                                                          \
+  extern "C" __global__ void __launch_bounds__(512)                                                           \
+      qmm_moe_gemv_##NAME##_u##U(const uint8_t* w0, const uint8_t* w1, int njobs, int N, int E, float* y0,  \
+                                 float* y1, int ldy, const uint8_t* __restrict__ xq, long long xrow,          \
+                                 const int* __restrict__ counts, const int* __restrict__ offsets, int K) {   \
+    moe_gemv<FMT, U>(w0, w1, njobs, N, E, y0, y1, ldy, xq, xrow, counts, offsets, K);                        \
+  }
+
+QMM_MOE_KERNEL(qmm::kFmtQ4K, q4k, 1)
+QMM_MOE_KERNEL(qmm::kFmtQ4K, q4k, 2)
+QMM_MOE_KERNEL(qmm::kFmtQ6K, q6k, 1)
+QMM_MOE_KERNEL(qmm::kFmtQ6K, q6k, 2)
+QMM_MOE_KERNEL(qmm::kFmtQ80, q8_0, 1)
+QMM_MOE_KERNEL(qmm::kFmtQ80, q8_0, 2)

@@ -44,7 +44,8 @@ EXPORTS = (
     "qmm_qtensor_from_ggml", "qmm_qtensor_quantize", "qmm_qtensor_dequantize",
     "qmm_qtensor_to_ggml", "qmm_qtensor_info", "qmm_qtensor_ggml_bytes", "qmm_qtensor_free",
     "qmm_quantize_rows", "qmm_matmul_workspace_size", "qmm_matmul", "qmm_matmul_q",
-    "qmm_matmul_multi", "qmm_block_dots",
+    "qmm_matmul_multi", "qmm_block_dots", "qmm_moe_route", "qmm_moe_gemv", "qmm_moe_ffn_workspace_size",
+    "qmm_moe_ffn",
 )
 
 
@@ -82,6 +83,10 @@ def lib() -> ctypes.CDLL:
             "qmm_matmul_multi": ([ctypes.POINTER(vp), i32, vp, i64, i64, ctypes.POINTER(vp),
                                   ctypes.POINTER(i64), vp, sz, vp], i32),
             "qmm_block_dots": ([vp, vp, i64, vp, i64, vp, vp], i32),
+            "qmm_moe_route": ([vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, vp], i32),
+            "qmm_moe_gemv": ([ctypes.POINTER(vp), i32, i32, vp, i64, vp, vp, ctypes.POINTER(vp), vp], i32),
+            "qmm_moe_ffn_workspace_size": ([vp, vp, i64, i32, i32], sz),
+            "qmm_moe_ffn": ([vp, i64, i64, vp, i32, i32, vp, vp, vp, vp, i64, vp, sz, vp], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -329,6 +334,40 @@ def block_dots(qt: QTensor, xq: torch.Tensor, m: int) -> Tuple[torch.Tensor, tor
         _check(lib().qmm_block_dots(qt.handle, xq.data_ptr(), m, y.data_ptr(), n, dots.data_ptr(),
                                     _stream(qt.device)))
     return (dots if per == 2 else dots[..., 0]), y
+
+
+def moe_route(logits: torch.Tensor, topk: int, renormalize: bool = True):
+    """Device routing: returns (counts, offsets, pair_token, pair_weight, token_pairs)."""
+    t, e = logits.shape
+    dev = logits.device
+    lg = logits.to(torch.float32).contiguous()
+    counts = torch.empty(e, dtype=torch.int32, device=dev)
+    offsets = torch.empty(e + 1, dtype=torch.int32, device=dev)
+    ptok = torch.empty(t * topk, dtype=torch.int32, device=dev)
+    pw = torch.empty(t * topk, dtype=torch.float32, device=dev)
+    tp = torch.empty(t * topk, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib().qmm_moe_route(lg.data_ptr(), t, e, topk, int(renormalize), counts.data_ptr(), offsets.data_ptr(),
+                                   ptok.data_ptr(), pw.data_ptr(), tp.data_ptr(), _stream(dev)))
+    return counts, offsets, ptok, pw, tp
+
+
+def moe_ffn(x: torch.Tensor, logits: torch.Tensor, gate: QTensor, up: QTensor, down: QTensor,
+            topk: int) -> torch.Tensor:
+    """Mixture-of-experts FFN (MoeMlp::forward with renormalised top-k) on stacked expert weights."""
+    t, hdim = x.shape
+    e = logits.shape[1]
+    dev = x.device
+    xx = x.to(torch.float32).contiguous()
+    lg = logits.to(torch.float32).contiguous()
+    out = torch.empty((t, hdim), dtype=torch.float32, device=dev)
+    L = lib()
+    wsb = int(L.qmm_moe_ffn_workspace_size(gate.handle, down.handle, t, e, topk))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _check(L.qmm_moe_ffn(xx.data_ptr(), t, hdim, lg.data_ptr(), e, topk, gate.handle, up.handle, down.handle,
+                             out.data_ptr(), hdim, ws.data_ptr(), wsb, _stream(dev)))
+    return out
 
 
 # ---------------------------------------------------------------------------

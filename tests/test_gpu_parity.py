@@ -354,3 +354,94 @@ def test_prefill_config_shapes_match_cpu_path(dt, n, k, wseed):
     rows = np.linspace(0, 511, 48).astype(int)
     y_ref = orc.matmul(ORC[dt], x[rows], wq, k)
     assert rel_err(y[rows], y_ref) <= TOL
+
+
+# ---------------------------------------------------------------------------
+# mixture of experts (config 5)
+# ---------------------------------------------------------------------------
+
+def _stacked_experts(E, H, F, seed, dt_gu=GgmlDType.Q4K, dt_down=GgmlDType.Q6K):
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+    mats = {}
+    for name, rows, cols, dt in (("gate", F, H, dt_gu), ("up", F, H, dt_gu), ("down", H, F, dt_down)):
+        w = torch.randn((E * rows, cols), generator=g, device=DEV) * 0.02
+        qt = QTensor.quantize(w, dt)
+        del w
+        raw = qt.to_ggml()
+        per = raw.size // E
+        mats[name] = (qt, [raw[e * per:(e + 1) * per] for e in range(E)])
+    return mats
+
+
+def test_moe_route_matches_oracle():
+    from inference_amd import moe_route
+    from oracle import moe
+    for T, E, k in ((8, 8, 2), (37, 16, 4), (1, 4, 1)):
+        logits = normal(200 + T, (T, E))
+        counts, offsets, ptok, pw, tp = [a.cpu().numpy() for a in moe_route(torch.from_numpy(logits).to(DEV), k)]
+        experts, weights = moe.route(logits, k)
+        assert counts.sum() == T * k and offsets[-1] == T * k
+        for e in range(E):
+            toks = [t for t in range(T) if e in experts[t]]
+            assert list(ptok[offsets[e]:offsets[e] + counts[e]]) == toks
+            for i, t in enumerate(toks):
+                assert abs(pw[offsets[e] + i] - weights[t][experts[t].index(e)]) < 1e-6
+        for t in range(T):
+            es = [int(np.searchsorted(offsets, p, side="right") - 1) for p in tp[t * k:(t + 1) * k]]
+            assert es == sorted(experts[t]) and all(ptok[p] == t for p in tp[t * k:(t + 1) * k])
+
+
+@pytest.mark.parametrize("E,H,F,T,k", [(8, 512, 1024, 8, 2), (4, 256, 512, 3, 2), (8, 512, 768, 16, 2)])
+def test_moe_ffn_matches_oracle_small(E, H, F, T, k):
+    from inference_amd import moe_ffn
+    from oracle import moe
+    mats = _stacked_experts(E, H, F, 210 + E + T)
+    x = normal(220, (T, H))
+    logits = normal(221, (T, E))
+    y = moe_ffn(torch.from_numpy(x).to(DEV), torch.from_numpy(logits).to(DEV), mats["gate"][0], mats["up"][0],
+                mats["down"][0], k).cpu().numpy()
+    y_ref = moe.moe_ffn(x, logits, mats["gate"][1], mats["up"][1], mats["down"][1], orc.Q4K, orc.Q6K, k)
+    assert rel_err(y, y_ref) <= TOL
+
+
+def test_moe_ffn_config5_matches_oracle():
+    """Config 5: 8 experts, Q4_K gate/up 14336x4096, Q6_K down 4096x14336, 8 tokens, top-2."""
+    from inference_amd import moe_ffn
+    from oracle import moe
+    E, H, F, T, k = 8, 4096, 14336, 8, 2
+    mats = _stacked_experts(E, H, F, 7)
+    x = normal(7, (T, H))
+    logits = normal(8, (T, E))
+    y = moe_ffn(torch.from_numpy(x).to(DEV), torch.from_numpy(logits).to(DEV), mats["gate"][0], mats["up"][0],
+                mats["down"][0], k).cpu().numpy()
+    y_ref = moe.moe_ffn(x, logits, mats["gate"][1], mats["up"][1], mats["down"][1], orc.Q4K, orc.Q6K, k)
+    assert rel_err(y, y_ref) <= TOL
+
+
+def test_moe_gemv_equals_per_expert_forward():
+    """The expert-grouped GEMV gives, bit for bit, each expert's own QMatMul on its gathered rows."""
+    from inference_amd import moe_route, qmm
+    E, H, F, T, k = 8, 1024, 2048, 8, 2
+    mats = _stacked_experts(E, H, F, 230)
+    x = torch.from_numpy(normal(231, (T, H))).to(DEV)
+    counts, offsets, ptok, pw, tp = moe_route(torch.from_numpy(normal(232, (T, E))).to(DEV), k)
+    P = T * k
+    xg = x[ptok.long()]
+    xq = quantize_rows(GgmlDType.Q8K, xg)
+    yg = torch.empty((P, F), device=DEV)
+    yu = torch.empty((P, F), device=DEV)
+    import ctypes
+    hs = (ctypes.c_void_p * 2)(mats["gate"][0].handle.value, mats["up"][0].handle.value)
+    ys = (ctypes.c_void_p * 2)(yg.data_ptr(), yu.data_ptr())
+    qmm._check(qmm.lib().qmm_moe_gemv(hs, 2, E, xq.data_ptr(), P, counts.data_ptr(), offsets.data_ptr(), ys,
+                                      qmm._stream(DEV)))
+    c, o = counts.cpu().numpy(), offsets.cpu().numpy()
+    gate_full = mats["gate"][0].dequantize()  # only for slicing per-expert tensors below
+    for e in range(E):
+        if c[e] == 0:
+            continue
+        qe = QTensor.from_ggml(mats["gate"][1][e], GgmlDType.Q4K, (F, H), device=DEV)
+        ref = matmul_q(qe, xq[o[e]:o[e] + c[e]].contiguous(), int(c[e]))
+        assert torch.equal(yg[o[e]:o[e] + c[e]], ref)
+    del gate_full
