@@ -212,6 +212,51 @@ def run_gemv_set(torch, dev, args):
     return result, sets
 
 
+def run_decode(torch, dev, args):
+    """Config 3: greedy decode of a random-init Llama-3-8B-shaped Q4_K_M model at batch 1.
+
+    Every token (prompt and generated) runs the same captured step; the
+    prompt's 128 tokens are fed one per step, then `decode_tokens` tokens are
+    generated. decode tok/s is timed over the generated tokens only.
+    """
+    from inference_amd.llama_decode import DecodeSession, LlamaConfig, LlamaWeights
+    cfg = LlamaConfig.llama3_8b()
+    log(f"[bench] decode: building the 8B-shape Q4_K_M model (seed 4)")
+    t0 = time.perf_counter()
+    w = LlamaWeights.random(cfg, 4, dev)
+    torch.cuda.synchronize()
+    log(f"[bench] decode: weights ready in {time.perf_counter() - t0:.1f} s")
+    prompt_len, gen = 128, args.decode_tokens
+    rng = np.random.default_rng(4)
+    prompt = [int(t) for t in rng.integers(0, cfg.vocab, prompt_len)]
+    sess = DecodeSession(w, prompt_len + gen)
+    sess.reset(prompt)
+    sess.capture()
+    # one untimed pass, then the timed pass from a fresh reset (same graph)
+    for timed in (False, True):
+        sess.reset(prompt)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        sess.run(prompt_len - 1)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        sess.run(gen)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+    toks = sess.generated(prompt_len + gen)
+    assert toks[:prompt_len] == prompt
+    tok_s = gen / (t2 - t1)
+    wb = cfg.weight_bytes_per_token()
+    return {"tok_s": round(tok_s, 2), "ms_per_token": round((t2 - t1) / gen * 1e3, 4),
+            "prompt_tokens": prompt_len, "generated_tokens": gen,
+            "prompt_ms_per_token": round((t1 - t0) / (prompt_len - 1) * 1e3, 4),
+            "weight_bytes_per_token": wb, "weight_GB_s": round(wb * tok_s / 1e9, 1),
+            "weight_hbm_frac": round(wb * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+            "model": "llama3-8b-shape Q4_K_M (q/k/o/gate/up Q4_K, v/down/head Q6_K), random init seed 4",
+            "schedule": "one HIP graph per token step, prompt fed token by token",
+            "first_generated": toks[prompt_len:prompt_len + 8]}
+
+
 def cpu_baseline(sets, budget_s):
     """Oracle restatement of Candle's CPU quantized matmul over the same GEMV set."""
     from oracle import oracle as orc
@@ -244,8 +289,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=24)
     ap.add_argument("--rotate-mb", type=int, default=640, help="distinct weight bytes rotated (MiB)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 = skip)")
-    ap.add_argument("--schedule", choices=("concurrent", "serial"), default="concurrent",
-                    help="run the set's independent GEMVs on 4 streams or one after another")
+    ap.add_argument("--schedule", choices=("concurrent", "serial"), default="serial",
+                    help="run the set's independent GEMVs one after another or on 4 streams")
+    ap.add_argument("--decode-tokens", type=int, default=256, help="config-3 generated tokens (0 = skip)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -257,6 +303,9 @@ def main():
     torch.cuda.set_device(dev)
     res, sets = run_gemv_set(torch, dev, args)
     cpu = cpu_baseline(sets, args.cpu_seconds) if args.cpu_seconds > 0 else None
+    del sets
+    torch.cuda.empty_cache()
+    dec = run_decode(torch, dev, args) if args.decode_tokens > 0 else None
     line = {
         "metric": METRIC,
         "value": round(res["value"], 1),
@@ -276,7 +325,8 @@ def main():
         "hbm_frac": round(res["value"] / HBM_PEAK_GBS, 4),
         "roofline": res["roofline"],
         "per_shape": res["per_shape"],
-        "decode_tok_s": None,
+        "decode_tok_s": dec["tok_s"] if dec else None,
+        "decode": dec,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

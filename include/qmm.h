@@ -132,6 +132,11 @@ int qmm_matmul_multi(const qmm_qtensor *const *w, int count, const float *x, int
  * must then be ordered on one stream). */
 int qmm_matmul_q(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy, void *stream);
 
+/* qmm_matmul_q with an optional residual add (accumulate != 0: y += result;
+ * then m <= 8). */
+int qmm_matmul_q_ex(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy, int accumulate,
+                    void *stream);
+
 /* Debug entry: exact int32 block dots of every (activation row, weight row,
  * super-block), computed by the same kernel that qmm_matmul_q runs (the GEMV
  * for m <= 8, the MFMA GEMM for m > 8).
@@ -142,6 +147,57 @@ int qmm_matmul_q(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int6
  * multiple of 256. */
 int qmm_block_dots(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy,
                    int32_t *dots, void *stream);
+
+/* QMatMul::forward for 1..4 weights (same dtype and k) on one input, with the
+ * decoder's neighbouring ops folded in: when norm_weight is non-NULL the input
+ * rows are first RMS-normalised, x / sqrt(mean(x^2) + eps) * norm_weight
+ * (rms_norm, crates/llm/candle-llm/src/primitives/nn.rs:22-31; fused into the
+ * quantization prologue for m <= 2), and when `accumulate` is set the result
+ * is added to y (the residual add of llama.rs:958-975). ws: device scratch of
+ * qmm_matmul_ex_workspace_size(w[0], m, norm_weight != NULL) bytes. */
+int qmm_matmul_ex(const qmm_qtensor *const *w, int count, const float *x, int64_t m, int64_t ldx,
+                  const float *norm_weight, float eps, int accumulate, float *const *y, const int64_t *ldy,
+                  void *ws, size_t ws_bytes, void *stream);
+size_t qmm_matmul_ex_workspace_size(const qmm_qtensor *w, int64_t m, int normalize);
+
+/* ---- decode step of a Llama-style decoder (f32 ops around the matmuls) ---- */
+
+/* RMSNorm of m rows: out = x / sqrt(mean(x^2) + eps) * w (nn.rs:22-31). */
+int qmm_rms_norm(const float *x, int64_t m, int64_t k, int64_t ldx, const float *w, float eps, float *out,
+                 int64_t ldo, void *stream);
+
+/* x[0:hidden) = table[tokens[pos[0]]] (dense f32 embedding rows, row stride ld). */
+int qmm_embed_rows(const float *table, int64_t ld, const int32_t *tokens, const int32_t *pos, float *x,
+                   int64_t hidden, void *stream);
+
+/* In place NeoX RoPE of q [heads][head_dim] and k [kv_heads][head_dim] at
+ * position pos[0] with cos/sin tables [max_seq][head_dim] (cat(freqs, freqs)),
+ * then k and v are appended to the caches [kv_heads][max_seq][head_dim]
+ * (apply_rope, rope.rs:289-323; KV concat, kv_cache.rs:107-111). */
+int qmm_rope_kv_append(float *q, float *k, const float *v, const float *cos_t, const float *sin_t,
+                       const int32_t *pos, float *kcache, float *vcache, int heads, int kv_heads, int head_dim,
+                       int max_seq, void *stream);
+
+/* One query per head against cache positions 0..pos[0]: out[h] =
+ * softmax(q[h] . K^T * scale) . V with kv head h / (heads / kv_heads)
+ * (repeat_kv + sdpa_eager, attention.rs:59-68, 154-186). max_seq <= 4096. */
+int qmm_decode_attention(const float *q, const float *kcache, const float *vcache, const int32_t *pos,
+                         float *out, int heads, int kv_heads, int head_dim, int max_seq, float scale,
+                         void *stream);
+
+/* hq = Q8_K(silu(g) * u) for rows x k (k a multiple of 256), the down
+ * projection's activation (LlamaMlp::forward, llama.rs:1386-1391). */
+int qmm_silu_mul_quantize(const float *g, const float *u, int64_t rows, int64_t k, int64_t ld, void *hq,
+                          void *stream);
+
+/* Greedy step end on the device: tokens[pos+1] = argmax(logits) (lowest index
+ * on ties, argmax_device, sampler.rs:216-219) unless pos+1 < prompt_len (the
+ * slot still holds a prompt token); then pos[0] += 1. `capacity` is the
+ * length of tokens (and of the KV cache): once pos+1 reaches it the call
+ * writes nothing and pos stays, so a step replayed too often never writes
+ * out of bounds. */
+int qmm_greedy_advance(const float *logits, int64_t n, int32_t *tokens, int64_t capacity, int32_t *pos,
+                       int prompt_len, void *stream);
 
 /* ---- mixture of experts (MoeMlp::forward, crates/llm/candle-llm/src/models/llama.rs:1416-1487) ---- */
 

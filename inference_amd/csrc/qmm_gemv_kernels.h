@@ -380,24 +380,58 @@ __device__ __forceinline__ void chunk_owner(int c16, int& l, int& k) {
   }
 }
 
-// Quantize mrows f32 rows (stride ldx) of nb blocks into the LDS layout.
+// RMSNorm denominators sqrt(mean(x^2) + eps) of mrows (<= 8) rows of k
+// elements, written to den[m] (LDS); the whole workgroup reduces.
+__device__ __forceinline__ void rms_denominators(const float* __restrict__ x, long long ldx, int mrows, int k,
+                                                 float eps, float* den, float* red) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  for (int m = 0; m < mrows; ++m) {
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < k; i += blockDim.x) {
+      const float v = x[m * ldx + i];
+      ss += v * v;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[m * 16 + wave] = ss;
+  }
+  __syncthreads();
+  if (threadIdx.x < mrows) {
+    float t = 0.0f;
+    for (int w = 0; w < nw; ++w) t += red[threadIdx.x * 16 + w];
+    den[threadIdx.x] = sqrtf(t / (float)k + eps);
+  }
+  __syncthreads();
+}
+
+// Quantize mrows f32 rows (stride ldx) of nb blocks into the LDS layout. With
+// norm_w, each row is first RMS-normalised: x / sqrt(mean(x^2) + eps) * w
+// (rms_norm, crates/llm/candle-llm/src/primitives/nn.rs:22-31).
 template <int FMT>
 __device__ __forceinline__ void quantize_act(const float* __restrict__ x, long long ldx, int mrows, int nb,
-                                             uint8_t* lds) {
+                                             uint8_t* lds, const float* __restrict__ norm_w, float eps) {
+#pragma clang fp contract(off)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int nblk = mrows * nb;
+  __shared__ float den[8];
+  __shared__ float red[8 * 16];
+  if (norm_w != nullptr)
+    rms_denominators(x, ldx, mrows, nb * FmtInfo<FMT>::kBlockElems, eps, den, red);
   if constexpr (FMT == kFmtQ80) {
-#pragma clang fp contract(off)
     float* ld = reinterpret_cast<float*>(lds + 32 * nblk);
     const int l8 = lane & 7;
     for (int base = 8 * wave; base < nblk; base += 8 * nw) {
       const int blk = base + (lane >> 3);
       const bool valid = blk < nblk;
       const int bc = valid ? blk : 0;
-      const float* xs = x + (bc / nb) * ldx + 32 * (bc % nb) + 4 * l8;
+      const int row = bc / nb, col = 32 * (bc % nb) + 4 * l8;
+      const float* xs = x + row * ldx + col;
       float e[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) e[j] = valid ? xs[j] : 0.0f;
+      for (int j = 0; j < 4; ++j) {
+        e[j] = valid ? xs[j] : 0.0f;
+        if (norm_w != nullptr) e[j] = e[j] / den[row] * norm_w[col + j];
+      }
       float amax = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
       amax = fmaxf(amax, dpp_f<0xb1>(amax));
       amax = fmaxf(amax, dpp_f<0x4e>(amax));
@@ -423,7 +457,17 @@ __device__ __forceinline__ void quantize_act(const float* __restrict__ x, long l
     int lc, kc;
     chunk_owner<FMT>(c16, lc, kc);
     for (int blk = wave; blk < nblk; blk += nw) {
-      const Q8KLane q = q8k_lane(x + (blk / nb) * ldx + 256 * (blk % nb), lane);
+      const int row = blk / nb, col = 256 * (blk % nb) + 4 * lane;
+      const float* xs = x + row * ldx + col;
+      float e0 = xs[0], e1 = xs[1], e2 = xs[2], e3 = xs[3];
+      if (norm_w != nullptr) {
+        const float dn = den[row];
+        e0 = e0 / dn * norm_w[col];
+        e1 = e1 / dn * norm_w[col + 1];
+        e2 = e2 / dn * norm_w[col + 2];
+        e3 = e3 / dn * norm_w[col + 3];
+      }
+      const Q8KLane q = q8k_lane_vals(e0, e1, e2, e3, lane);
       *reinterpret_cast<uint32_t*>(lds + 256 * blk + 16 * kq_slot(blk, lc, kc) + 4 * (lane & 3)) = q.packed;
       const int next = __shfl_down(q.sum16, 4);  // the following 16-group's sum
       if (FMT == kFmtQ4K) {
@@ -442,9 +486,13 @@ __device__ __forceinline__ void quantize_act(const float* __restrict__ x, long l
 //   act: M rows of nb activation blocks (Q8_K or Q8_0, GGML bytes), or, when
 //        FUSED, M rows of f32 (row stride ldx) quantized in the prologue;
 //   dump (optional, single job): int32 block dots [M][rows][nb](x2 for Q4_K).
+// With `accumulate`, outputs are added to y (y += result); norm_w (fused only)
+// RMS-normalises the activation rows before quantization.
 template <int FMT, int M, int R, int U, bool FUSED>
 __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restrict__ act, long long ldx, int K,
-                                     int* __restrict__ dump, int mrows = M) {
+                                     int* __restrict__ dump, int mrows = M,
+                                     const float* __restrict__ norm_w = nullptr, float eps = 0.0f,
+                                     int accumulate = 0) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int LPB = FmtInfo<FMT>::kLanesPerBlock;
   constexpr int BPI = 64 / LPB;  // blocks per wave iteration
@@ -465,7 +513,7 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
   WSlice ws[R][U];
   load_batch<FMT, R, U>(ws, rr, 0, nb, g, l);
   if constexpr (FUSED)
-    quantize_act<FMT>(reinterpret_cast<const float*>(act), ldx, mrows, nb, lds);
+    quantize_act<FMT>(reinterpret_cast<const float*>(act), ldx, mrows, nb, lds, norm_w, eps);
   else
     stage_act<FMT>(reinterpret_cast<const uint8_t*>(act), mrows * nb, lds);
   __syncthreads();
@@ -523,7 +571,10 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
       for (int m = 0; m < M; ++m) {
         if (M > 1 && m >= mrows) break;  // wave-uniform
         const float v = wave_sum(acc[r][m]);
-        if (lane == 0 && cur[r].ok && m < mrows) cur[r].y[(size_t)m * cur[r].ldy + cur[r].out] = v;
+        if (lane == 0 && cur[r].ok && m < mrows) {
+          float* yp = cur[r].y + (size_t)m * cur[r].ldy + cur[r].out;
+          *yp = accumulate ? *yp + v : v;
+        }
       }
   }
 }
@@ -537,7 +588,7 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
       float *y2, float *y3, int rows0, int rows1, int rows2, int rows3, int ldy0, int ldy1, int ldy2,     \
       int ldy3, int row00, int row01, int row02, int row03, int trows0, int trows1, int trows2,           \
       int trows3, int njobs, int total, const void *__restrict__ act, long long ldx, int K,               \
-      int *__restrict__ dump
+      int *__restrict__ dump, const float *__restrict__ norm_w, float eps, int accumulate
 #define QMM_GEMV_JOBS                                                                                     \
   qmm::GemvJobs jobs;                                                                                     \
   jobs.wq[0] = wq0;                                                                                       \
@@ -571,14 +622,14 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
   extern "C" __global__ void __launch_bounds__(64 * W)                                                    \
       qmm_gemv_##NAME##_m##M##_w##W##_r##R##_u##U(QMM_GEMV_PARAMS) {                                      \
     QMM_GEMV_JOBS                                                                                         \
-    qmm::gemv<FMT, M, R, U, false>(jobs, act, ldx, K, dump);                                              \
+    qmm::gemv<FMT, M, R, U, false>(jobs, act, ldx, K, dump, M, nullptr, 0.0f, accumulate);               \
   }
 
 #define QMM_GEMVF_KERNEL(FMT, NAME, M, W, R, U)                                                           \
   extern "C" __global__ void __launch_bounds__(64 * W)                                                    \
       qmm_gemvf_##NAME##_m##M##_w##W##_r##R##_u##U(QMM_GEMV_PARAMS) {                                     \
     QMM_GEMV_JOBS                                                                                         \
-    qmm::gemv<FMT, M, R, U, true>(jobs, act, ldx, K, dump);                                               \
+    qmm::gemv<FMT, M, R, U, true>(jobs, act, ldx, K, dump, M, norm_w, eps, accumulate);                  \
   }
 
 // Launch shapes: W waves per workgroup, R rows per wave, U load iterations per batch.

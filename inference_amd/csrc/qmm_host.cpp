@@ -462,7 +462,7 @@ struct GemvTarget {
 // and k) sharing one activation. `act` is m rows of quantized blocks, or f32
 // rows with stride ldx when `fused` (then the kernel quantizes in its prologue).
 static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, bool fused, int64_t ldx, int m,
-                int* dump, hipStream_t s) {
+                int* dump, hipStream_t s, const float* norm_w = nullptr, float eps = 0.0f, int accumulate = 0) {
   const qmm_qtensor* w = tg[0].w;
   const int fmt = fmt_of(w->dtype);
   const int nb = (int)(w->k / qmm_block_size(w->dtype));
@@ -518,13 +518,14 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
                   &jobs.y[2],     &jobs.y[3],     &jobs.rows[0],  &jobs.rows[1],  &jobs.rows[2],  &jobs.rows[3],
                   &jobs.ldy[0],   &jobs.ldy[1],   &jobs.ldy[2],   &jobs.ldy[3],   &jobs.row0[0],  &jobs.row0[1],
                   &jobs.row0[2],  &jobs.row0[3],  &jobs.trows[0], &jobs.trows[1], &jobs.trows[2], &jobs.trows[3],
-                  &jobs.njobs,    &jobs.total,    &a,             &lx,            &K,             &dp};
+                  &jobs.njobs,    &jobs.total,    &a,             &lx,            &K,             &dp,
+                  &norm_w,        &eps,           &accumulate};
   return launch(d, name, (unsigned)wgs, 64 * wv, lds, s, args);
 }
 
 // Prefill GEMM over activation planes at `ws` (see mmq_planes).
 static int gemm(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, float* y, int64_t ldy, int* dump,
-                hipStream_t s) {
+                hipStream_t s, int accumulate = 0) {
   const Planes pl = mmq_planes(w->dtype, m, w->k);
   const int fmt = fmt_of(w->dtype);
   char name[40];
@@ -536,7 +537,7 @@ static int gemm(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, f
   float* yy = y;
   int M = (int)m, N = (int)w->n, K = (int)w->k, ld = (int)ldy;
   int* dp = dump;
-  void* args[] = {&wq, &q8, &dd, &ss, &yy, &M, &N, &K, &ld, &dp};
+  void* args[] = {&wq, &q8, &dd, &ss, &yy, &M, &N, &K, &ld, &dp, &accumulate};
   hipFunction_t f;
   QMM_TRY(kernel(d, name, &f));
   const unsigned gx = (unsigned)((N + 127) / 128), gy = (unsigned)((M + 63) / 64);
@@ -631,9 +632,22 @@ int qmm_matmul_q(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int6
   return QMM_OK;
 }
 
+int qmm_matmul_q_ex(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int64_t ldy, int accumulate,
+                    void* stream) {
+  QMM_TRY(check_matmul(w, m, y, ldy));
+  if (!xq) return fail(QMM_ERR_INVALID, "null activation");
+  if (!accumulate) return qmm_matmul_q(w, xq, m, y, ldy, stream);
+  if (m > 8) return fail(QMM_ERR_UNSUPPORTED, "accumulating prequantized matmul is limited to m <= 8");
+  Device* d;
+  QMM_TRY(current_device(&d));
+  GemvTarget t = {w, y, ldy};
+  return gemv(d, &t, 1, xq, false, 0, (int)m, nullptr, (hipStream_t)stream, nullptr, 0.0f, 1);
+}
+
 // Shared by qmm_matmul / qmm_matmul_multi: x f32 [m, k] against `count` weights.
 static int matmul_targets(const GemvTarget* tg, int count, const float* x, int64_t m, int64_t ldx, void* ws,
-                          size_t ws_bytes, void* stream) {
+                          size_t ws_bytes, void* stream, const float* norm_w = nullptr, float eps = 0.0f,
+                          int accumulate = 0) {
   const qmm_qtensor* w = tg[0].w;
   if (!x) return fail(QMM_ERR_INVALID, "null activation");
   if (ldx < w->k) return fail(QMM_ERR_INVALID, "row stride %lld < k %lld", (long long)ldx, (long long)w->k);
@@ -641,14 +655,23 @@ static int matmul_targets(const GemvTarget* tg, int count, const float* x, int64
   QMM_TRY(current_device(&d));
   hipStream_t s = (hipStream_t)stream;
   if (m <= 2) {
-    // one launch: the activation is quantized in the GEMV prologue
-    return gemv(d, tg, count, x, true, ldx, (int)m, nullptr, s);
+    // one launch: the activation is (normalised and) quantized in the GEMV prologue
+    return gemv(d, tg, count, x, true, ldx, (int)m, nullptr, s, norm_w, eps, accumulate);
   }
-  const size_t need = qmm_matmul_workspace_size(w, m);
+  size_t need = qmm_matmul_workspace_size(w, m);
+  if (norm_w) need += align256((size_t)(m * w->k) * 4);
   if (!ws || ws_bytes < need) return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed", ws_bytes, need);
+  if (norm_w) {
+    // normalised rows go after the quantized activation in the workspace
+    float* xn = (float*)((uint8_t*)ws + qmm_matmul_workspace_size(w, m));
+    QMM_TRY(qmm_rms_norm(x, m, w->k, ldx, norm_w, eps, xn, w->k, stream));
+    x = xn;
+    ldx = w->k;
+  }
   if (use_gemm(w, m)) {
     QMM_TRY(quantize_planes(d, w->dtype, x, m, w->k, ldx, (uint8_t*)ws, s));
-    for (int j = 0; j < count; ++j) QMM_TRY(gemm(d, tg[j].w, (const uint8_t*)ws, m, tg[j].y, tg[j].ldy, nullptr, s));
+    for (int j = 0; j < count; ++j)
+      QMM_TRY(gemm(d, tg[j].w, (const uint8_t*)ws, m, tg[j].y, tg[j].ldy, nullptr, s, accumulate));
     return QMM_OK;
   }
   const int vt = qmm_vec_dot_type(w->dtype);
@@ -658,7 +681,7 @@ static int matmul_targets(const GemvTarget* tg, int count, const float* x, int64
     const int mm = (int)(m - m0 < 8 ? m - m0 : 8);
     GemvTarget t[4];
     for (int j = 0; j < count; ++j) t[j] = {tg[j].w, tg[j].y + m0 * tg[j].ldy, tg[j].ldy};
-    QMM_TRY(gemv(d, t, count, (const uint8_t*)ws + m0 * xrow, false, 0, mm, nullptr, s));
+    QMM_TRY(gemv(d, t, count, (const uint8_t*)ws + m0 * xrow, false, 0, mm, nullptr, s, nullptr, 0.0f, accumulate));
   }
   return QMM_OK;
 }
@@ -681,6 +704,99 @@ int qmm_matmul_multi(const qmm_qtensor* const* w, int count, const float* x, int
     t[j] = {w[j], y[j], ldy[j]};
   }
   return matmul_targets(t, count, x, m, ldx, ws, ws_bytes, stream);
+}
+
+int qmm_matmul_ex(const qmm_qtensor* const* w, int count, const float* x, int64_t m, int64_t ldx,
+                  const float* norm_weight, float eps, int accumulate, float* const* y, const int64_t* ldy, void* ws,
+                  size_t ws_bytes, void* stream) {
+  if (!w || !y || !ldy || count < 1 || count > 4) return fail(QMM_ERR_INVALID, "need 1..4 weights with outputs");
+  GemvTarget t[4];
+  for (int j = 0; j < count; ++j) {
+    QMM_TRY(check_matmul(w[j], m, y[j], ldy[j]));
+    if (w[j]->dtype != w[0]->dtype || w[j]->k != w[0]->k)
+      return fail(QMM_ERR_INVALID, "weights of one call must share dtype and k");
+    t[j] = {w[j], y[j], ldy[j]};
+  }
+  return matmul_targets(t, count, x, m, ldx, ws, ws_bytes, stream, norm_weight, eps, accumulate ? 1 : 0);
+}
+
+size_t qmm_matmul_ex_workspace_size(const qmm_qtensor* w, int64_t m, int normalize) {
+  if (!w || m <= 0) return 0;
+  size_t b = qmm_matmul_workspace_size(w, m);
+  if (normalize && m > 2) b += align256((size_t)(m * w->k) * 4);
+  return b;
+}
+
+// ---------------------------------------------------------------------------
+// decode-step kernels (f32, non-matmul)
+// ---------------------------------------------------------------------------
+
+int qmm_rms_norm(const float* x, int64_t m, int64_t k, int64_t ldx, const float* w, float eps, float* out,
+                 int64_t ldo, void* stream) {
+  if (!x || !w || !out || m < 1 || k < 1 || ldx < k || ldo < k) return fail(QMM_ERR_INVALID, "bad rms_norm arguments");
+  Device* d;
+  QMM_TRY(current_device(&d));
+  long long lx = ldx, lo = ldo;
+  int kk = (int)k;
+  void* args[] = {&x, &lx, &w, &eps, &kk, &out, &lo};
+  return launch(d, "qmm_rms_norm", (unsigned)m, 256, 0, (hipStream_t)stream, args);
+}
+
+int qmm_embed_rows(const float* table, int64_t ld, const int32_t* tokens, const int32_t* pos, float* x,
+                   int64_t hidden, void* stream) {
+  if (!table || !tokens || !pos || !x || hidden < 1 || ld < hidden) return fail(QMM_ERR_INVALID, "bad embed arguments");
+  Device* d;
+  QMM_TRY(current_device(&d));
+  long long l = ld;
+  int h = (int)hidden;
+  void* args[] = {&table, &l, &tokens, &pos, &x, &h};
+  return launch(d, "qmm_decode_embed", ceil_div(hidden, 256), 256, 0, (hipStream_t)stream, args);
+}
+
+int qmm_rope_kv_append(float* q, float* k, const float* v, const float* cos_t, const float* sin_t,
+                       const int32_t* pos, float* kcache, float* vcache, int heads, int kv_heads, int head_dim,
+                       int max_seq, void* stream) {
+  if (!q || !k || !v || !cos_t || !sin_t || !pos || !kcache || !vcache) return fail(QMM_ERR_INVALID, "null pointer");
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads || head_dim < 2 || head_dim > 1024 || head_dim % 2 || max_seq < 1)
+    return fail(QMM_ERR_INVALID, "bad attention geometry");
+  Device* d;
+  QMM_TRY(current_device(&d));
+  void* args[] = {&q, &k, &v, &cos_t, &sin_t, &pos, &kcache, &vcache, &heads, &kv_heads, &head_dim, &max_seq};
+  const unsigned threads = (unsigned)((head_dim + 63) / 64 * 64);
+  return launch(d, "qmm_decode_rope_kv", (unsigned)(heads + kv_heads), threads, 0, (hipStream_t)stream, args);
+}
+
+int qmm_decode_attention(const float* q, const float* kcache, const float* vcache, const int32_t* pos, float* out,
+                         int heads, int kv_heads, int head_dim, int max_seq, float scale, void* stream) {
+  if (!q || !kcache || !vcache || !pos || !out) return fail(QMM_ERR_INVALID, "null pointer");
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads || head_dim < 1 || head_dim > 256 || max_seq < 1 || max_seq > 4096)
+    return fail(QMM_ERR_INVALID, "bad attention geometry (head_dim <= 256, max_seq <= 4096)");
+  Device* d;
+  QMM_TRY(current_device(&d));
+  void* args[] = {&q, &kcache, &vcache, &pos, &out, &heads, &kv_heads, &head_dim, &max_seq, &scale};
+  return launch(d, "qmm_decode_attention", (unsigned)heads, 256, 0, (hipStream_t)stream, args);
+}
+
+int qmm_silu_mul_quantize(const float* g, const float* u, int64_t rows, int64_t k, int64_t ld, void* hq,
+                          void* stream) {
+  if (!g || !u || !hq || rows < 1 || k < 256 || k % 256 || ld < k) return fail(QMM_ERR_INVALID, "bad silu_mul arguments");
+  Device* d;
+  QMM_TRY(current_device(&d));
+  long long l = ld;
+  int kk = (int)k, rr = (int)rows;
+  void* args[] = {&g, &u, &l, &hq, &kk, &rr};
+  return launch(d, "qmm_silu_mul_q8k", ceil_div(rows * (k / 256), 4), 256, 0, (hipStream_t)stream, args);
+}
+
+int qmm_greedy_advance(const float* logits, int64_t n, int32_t* tokens, int64_t capacity, int32_t* pos,
+                       int prompt_len, void* stream) {
+  if (!logits || !tokens || !pos || n < 1 || n > INT32_MAX || capacity < 1 || capacity > INT32_MAX)
+    return fail(QMM_ERR_INVALID, "bad argmax arguments");
+  Device* d;
+  QMM_TRY(current_device(&d));
+  int nn = (int)n, cap = (int)capacity;
+  void* args[] = {&logits, &nn, &tokens, &cap, &pos, &prompt_len};
+  return launch(d, "qmm_decode_argmax", 1, 1024, 0, (hipStream_t)stream, args);
 }
 
 int qmm_block_dots(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int64_t ldy, int32_t* dots,

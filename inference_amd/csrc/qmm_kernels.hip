@@ -7,3 +7,4 @@
 #include "qmm_gemv_kernels.h"
 #include "qmm_mmq_kernels.h"
 #include "qmm_moe_kernels.h"
+#include "qmm_decode_kernels.h"

@@ -211,7 +211,8 @@ __device__ __forceinline__ uint32_t byte8(uint2 w, int i) { return ((i < 4 ? w.x
 template <int FMT, bool DUMP>
 __device__ __forceinline__ void mmq(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,
                                     const float* __restrict__ xd, const int16_t* __restrict__ xs,
-                                    float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump) {
+                                    float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,
+                                    int accumulate) {
   __shared__ MmqLds L;
   const int m0 = blockIdx.y * kMmqBM, n0 = blockIdx.x * kMmqBN;
   const int nbk = K / 256;
@@ -374,8 +375,14 @@ __device__ __forceinline__ void mmq(const uint8_t* __restrict__ wq, const int8_t
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     const int row = m0 + rowb + 8 * (j >> 2) + (j & 3);
-    if (row < M && n0 + col0 < N) y[(size_t)row * ldy + n0 + col0] = acc0[j];
-    if (row < M && n0 + col1 < N) y[(size_t)row * ldy + n0 + col1] = acc1[j];
+    if (row < M && n0 + col0 < N) {
+      float* yp = y + (size_t)row * ldy + n0 + col0;
+      *yp = accumulate ? *yp + acc0[j] : acc0[j];
+    }
+    if (row < M && n0 + col1 < N) {
+      float* yp = y + (size_t)row * ldy + n0 + col1;
+      *yp = accumulate ? *yp + acc1[j] : acc1[j];
+    }
   }
 }
 
@@ -421,14 +428,15 @@ extern "C" __global__ void __launch_bounds__(256) qmm_quantize_q8_0_mmq(const fl
   extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))               \
       qmm_mmq_##NAME(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                          \
                      const float* __restrict__ xd, const int16_t* __restrict__ xs, float* __restrict__ y,   \
-                     int M, int N, int K, int ldy, int* __restrict__ dump) {                                 \
-    qmm::mmq<FMT, false>(wq, xq, xd, xs, y, M, N, K, ldy, dump);                                             \
+                     int M, int N, int K, int ldy, int* __restrict__ dump, int accumulate) {                 \
+    qmm::mmq<FMT, false>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate);                                 \
   }                                                                                                          \
   extern "C" __global__ void __launch_bounds__(256)                                                          \
       qmm_mmq_##NAME##_dump(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                   \
                             const float* __restrict__ xd, const int16_t* __restrict__ xs,                    \
-                            float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump) {   \
-    qmm::mmq<FMT, true>(wq, xq, xd, xs, y, M, N, K, ldy, dump);                                              \
+                            float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,     \
+                            int accumulate) {                                                                \
+    qmm::mmq<FMT, true>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate);                                  \
   }
 
 QMM_MMQ_KERNEL(qmm::kFmtQ4K, q4k)

@@ -30,9 +30,8 @@ struct Q8KLane {
   float d;
 };
 
-__device__ __forceinline__ Q8KLane q8k_lane(const float* __restrict__ xs, int lane) {
+__device__ __forceinline__ Q8KLane q8k_lane_vals(float e0, float e1, float e2, float e3, int lane) {
 #pragma clang fp contract(off)
-  const float e0 = xs[4 * lane], e1 = xs[4 * lane + 1], e2 = xs[4 * lane + 2], e3 = xs[4 * lane + 3];
   const float amax = wave_max(fmaxf(fmaxf(fabsf(e0), fabsf(e1)), fmaxf(fabsf(e2), fabsf(e3))));
   Q8KLane r;
   if (amax == 0.0f) {
@@ -62,6 +61,10 @@ __device__ __forceinline__ Q8KLane q8k_lane(const float* __restrict__ xs, int la
   r.sum16 = quad_sum(sum);
   r.d = 1.0f / iscale;
   return r;
+}
+
+__device__ __forceinline__ Q8KLane q8k_lane(const float* __restrict__ xs, int lane) {
+  return q8k_lane_vals(xs[4 * lane], xs[4 * lane + 1], xs[4 * lane + 2], xs[4 * lane + 3], lane);
 }
 
 // Standalone form: one wave writes one GGML Q8_K block.

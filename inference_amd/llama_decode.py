@@ -1,0 +1,313 @@
+"""Greedy decode of a Llama-style decoder whose projections run on the quantized path.
+
+Mirrors the reference engine's decode for a Llama-3-shaped model
+(CausalLm::decode_logits -> run_decoder_stack -> LlamaLayer::forward,
+crates/llm/candle-llm/src/models/llama.rs:410-433, 654-725, 913-975, 1066-1120,
+1386-1391; the loop of decode/stream.rs:246-305) with the GGUF Q4_K_M tensor
+mix: Q4_K for attn_q/attn_k/attn_o/ffn_gate/ffn_up, Q6_K for attn_v/ffn_down
+and the output head, dense f32 embedding and RMSNorm weights.
+
+One token step is a fixed sequence of device launches (no host sync):
+embedding gather; per layer q/k and v projections with RMSNorm fused into
+their quantization prologue, RoPE + KV append, GQA attention, o projection
+added into the residual, gate/up projections (norm fused), SiLU*mul -> Q8_K,
+down projection added into the residual; final norm + head; greedy argmax
+that writes the next token and advances the position. The position and the
+token ids live in device memory, so the step is captured once into a HIP
+graph and replayed for every token (prompt tokens are fed through the same
+step: the argmax does not overwrite a slot that still holds a prompt token).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass, field
+from typing import Callable, Dict, List, Optional
+
+import numpy as np
+import torch
+
+from . import qmm
+from .qmm import GgmlDType, QTensor
+
+Q4K, Q6K = GgmlDType.Q4K, GgmlDType.Q6K
+
+
+@dataclass
+class LlamaConfig:
+    layers: int = 32
+    hidden: int = 4096
+    ffn: int = 14336
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    vocab: int = 128256
+    rope_theta: float = 500000.0
+    rope_factor: float = 8.0
+    rope_low: float = 1.0
+    rope_high: float = 4.0
+    rope_orig_ctx: float = 8192.0
+    eps: float = 1e-5
+    # Q4_K_M tensor types
+    dtypes: Dict[str, GgmlDType] = field(default_factory=lambda: {
+        "q": Q4K, "k": Q4K, "v": Q6K, "o": Q4K, "gate": Q4K, "up": Q4K, "down": Q6K, "head": Q6K})
+
+    @staticmethod
+    def llama3_8b() -> "LlamaConfig":
+        return LlamaConfig()
+
+    def shapes(self) -> Dict[str, tuple]:
+        return {"q": (self.heads * self.head_dim, self.hidden), "k": (self.kv_heads * self.head_dim, self.hidden),
+                "v": (self.kv_heads * self.head_dim, self.hidden), "o": (self.hidden, self.heads * self.head_dim),
+                "gate": (self.ffn, self.hidden), "up": (self.ffn, self.hidden), "down": (self.hidden, self.ffn),
+                "head": (self.vocab, self.hidden)}
+
+    def weight_bytes_per_token(self) -> int:
+        """Quantized weight bytes streamed per decoded token (all layers + head)."""
+        sh = self.shapes()
+        total = 0
+        for name, (n, k) in sh.items():
+            dt = self.dtypes[name]
+            b = n * (k // 256) * (144 if dt == Q4K else 210)
+            total += b * (1 if name == "head" else self.layers)
+        return total
+
+
+def llama3_inv_freq(cfg: LlamaConfig) -> np.ndarray:
+    """Rope::llama3 (crates/llm/candle-llm/src/primitives/rope.rs:117-150), f32 arithmetic."""
+    f32 = np.float32
+    dim = cfg.head_dim
+    low_wl = f32(cfg.rope_orig_ctx) / f32(cfg.rope_low)
+    high_wl = f32(cfg.rope_orig_ctx) / f32(cfg.rope_high)
+    out = np.empty(dim // 2, dtype=np.float32)
+    for i in range(dim // 2):
+        inv = f32(1.0) / np.power(f32(cfg.rope_theta), f32(2 * i) / f32(dim), dtype=np.float32)
+        wavelen = f32(2.0) * f32(math.pi) / inv
+        if wavelen > low_wl:
+            out[i] = inv / f32(cfg.rope_factor)
+        elif wavelen < high_wl:
+            out[i] = inv
+        else:
+            smooth = (f32(cfg.rope_orig_ctx) / wavelen - f32(cfg.rope_low)) / (f32(cfg.rope_high) - f32(cfg.rope_low))
+            out[i] = (f32(1.0) - smooth) * inv / f32(cfg.rope_factor) + smooth * inv
+    return out
+
+
+def rope_tables(cfg: LlamaConfig, max_seq: int):
+    """cos/sin [max_seq][head_dim] of Rope::cos_sin_at (NeoX: cat(freqs, freqs)), rope.rs:176-208."""
+    inv = llama3_inv_freq(cfg)
+    pos = np.arange(max_seq, dtype=np.float32)[:, None]
+    freqs = (pos * inv[None, :]).astype(np.float32)
+    emb = np.concatenate([freqs, freqs], axis=1)
+    return np.cos(emb).astype(np.float32), np.sin(emb).astype(np.float32)
+
+
+class LlamaWeights:
+    """Device weights: quantized projections per layer, dense f32 embedding and norms."""
+
+    def __init__(self, cfg: LlamaConfig, layers: List[Dict[str, QTensor]], head: QTensor, embed: torch.Tensor,
+                 attn_norm: List[torch.Tensor], ffn_norm: List[torch.Tensor], final_norm: torch.Tensor):
+        self.cfg = cfg
+        self.layers = layers
+        self.head = head
+        self.embed = embed
+        self.attn_norm = attn_norm
+        self.ffn_norm = ffn_norm
+        self.final_norm = final_norm
+
+    @classmethod
+    def random(cls, cfg: LlamaConfig, seed: int, device: torch.device, std: float = 0.02) -> "LlamaWeights":
+        """N(0, std^2) weights from a seeded device generator, quantized on the GPU; norms = 1."""
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        sh = cfg.shapes()
+
+        def q(name):
+            n, k = sh[name]
+            w = torch.randn((n, k), generator=g, device=device) * std
+            t = QTensor.quantize(w, cfg.dtypes[name])
+            del w
+            return t
+
+        layers = [{name: q(name) for name in ("q", "k", "v", "o", "gate", "up", "down")} for _ in range(cfg.layers)]
+        head = q("head")
+        embed = torch.randn((cfg.vocab, cfg.hidden), generator=g, device=device) * std
+        ones = lambda: torch.ones(cfg.hidden, dtype=torch.float32, device=device)  # noqa: E731
+        return cls(cfg, layers, head, embed, [ones() for _ in range(cfg.layers)],
+                   [ones() for _ in range(cfg.layers)], ones())
+
+    def export(self) -> dict:
+        """Host copies for the CPU reference: GGML bytes per tensor, f32 embedding and norms."""
+        return {"layers": [{n: t.to_ggml() for n, t in lw.items()} for lw in self.layers],
+                "head": self.head.to_ggml(), "embed": self.embed.cpu().numpy(),
+                "attn_norm": [w.cpu().numpy() for w in self.attn_norm],
+                "ffn_norm": [w.cpu().numpy() for w in self.ffn_norm], "final_norm": self.final_norm.cpu().numpy()}
+
+
+class DecodeSession:
+    """Device state and the launch sequence of one token step."""
+
+    def __init__(self, weights: LlamaWeights, max_seq: int):
+        cfg = weights.cfg
+        self.cfg, self.w, self.max_seq = cfg, weights, max_seq
+        if max_seq > 4096:
+            raise qmm.QmmError(1, "decode attention supports up to 4096 positions")
+        dev = weights.embed.device
+        self.dev = dev
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.x = torch.zeros(cfg.hidden, **f32)
+        self.q = torch.zeros(cfg.heads * cfg.head_dim, **f32)
+        self.k = torch.zeros(cfg.kv_heads * cfg.head_dim, **f32)
+        self.v = torch.zeros(cfg.kv_heads * cfg.head_dim, **f32)
+        self.attn = torch.zeros(cfg.heads * cfg.head_dim, **f32)
+        self.g = torch.zeros(cfg.ffn, **f32)
+        self.u = torch.zeros(cfg.ffn, **f32)
+        self.hq = torch.zeros(cfg.ffn // 256 * 292, dtype=torch.uint8, device=dev)
+        self.logits = torch.zeros(cfg.vocab, **f32)
+        self.tokens = torch.zeros(max_seq, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        kv = (cfg.layers, cfg.kv_heads, max_seq, cfg.head_dim)
+        self.kcache = torch.zeros(kv, **f32)
+        self.vcache = torch.zeros(kv, **f32)
+        cos, sin = rope_tables(cfg, max_seq)
+        self.cos = torch.from_numpy(cos).to(dev)
+        self.sin = torch.from_numpy(sin).to(dev)
+        self.scale = float(np.float32(cfg.head_dim) ** np.float32(-0.5))
+        self.prompt_len = 0
+        self.steps_done = 0
+        self._graph = None
+        L = qmm.lib()
+        self.L = L
+        # launch arguments prepared once (ctypes arrays of handles / outputs)
+        self._arr = []
+
+        def arr(ctype, vals):
+            a = (ctype * len(vals))(*vals)
+            self._arr.append(a)
+            return a
+
+        vp, i64 = ctypes.c_void_p, ctypes.c_int64
+        self._qk = [arr(vp, [lw["q"].handle.value, lw["k"].handle.value]) for lw in weights.layers]
+        self._qk_y = arr(vp, [self.q.data_ptr(), self.k.data_ptr()])
+        self._qk_ld = arr(i64, [self.q.numel(), self.k.numel()])
+        self._v = [arr(vp, [lw["v"].handle.value]) for lw in weights.layers]
+        self._v_y = arr(vp, [self.v.data_ptr()])
+        self._v_ld = arr(i64, [self.v.numel()])
+        self._o = [arr(vp, [lw["o"].handle.value]) for lw in weights.layers]
+        self._x_y = arr(vp, [self.x.data_ptr()])
+        self._x_ld = arr(i64, [cfg.hidden])
+        self._gu = [arr(vp, [lw["gate"].handle.value, lw["up"].handle.value]) for lw in weights.layers]
+        self._gu_y = arr(vp, [self.g.data_ptr(), self.u.data_ptr()])
+        self._gu_ld = arr(i64, [cfg.ffn, cfg.ffn])
+        self._head = arr(vp, [weights.head.handle.value])
+        self._lg_y = arr(vp, [self.logits.data_ptr()])
+        self._lg_ld = arr(i64, [cfg.vocab])
+
+    # -- one token step --------------------------------------------------
+    def step(self, trace: Optional[Callable[[str, int], None]] = None):
+        """Enqueue one token step on the current stream (no host synchronisation).
+
+        `trace(op, layer)`, when given, is called after each launch is enqueued (ops: embed, qk, v,
+        rope_kv, attention, o, gate_up, silu_mul, down, head, argmax); it lets a checker inspect the
+        session's buffers between launches. Captured steps take no trace.
+        """
+        cfg, L, w = self.cfg, self.L, self.w
+        s = qmm._stream(self.dev)
+        eps = ctypes.c_float(cfg.eps)
+        hd, H = cfg.head_dim, cfg.hidden
+        tr = trace if trace is not None else (lambda op, li: None)
+        qmm._check(L.qmm_embed_rows(w.embed.data_ptr(), H, self.tokens.data_ptr(), self.pos.data_ptr(),
+                                    self.x.data_ptr(), H, s))
+        tr("embed", -1)
+        kv_stride = cfg.kv_heads * self.max_seq * hd
+        for li in range(cfg.layers):
+            an, fn = w.attn_norm[li].data_ptr(), w.ffn_norm[li].data_ptr()
+            qmm._check(L.qmm_matmul_ex(self._qk[li], 2, self.x.data_ptr(), 1, H, an, eps, 0, self._qk_y,
+                                       self._qk_ld, None, 0, s))
+            tr("qk", li)
+            qmm._check(L.qmm_matmul_ex(self._v[li], 1, self.x.data_ptr(), 1, H, an, eps, 0, self._v_y, self._v_ld,
+                                       None, 0, s))
+            tr("v", li)
+            kc = self.kcache.data_ptr() + 4 * li * kv_stride
+            vc = self.vcache.data_ptr() + 4 * li * kv_stride
+            qmm._check(L.qmm_rope_kv_append(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                                            self.cos.data_ptr(), self.sin.data_ptr(), self.pos.data_ptr(), kc, vc,
+                                            cfg.heads, cfg.kv_heads, hd, self.max_seq, s))
+            tr("rope_kv", li)
+            qmm._check(L.qmm_decode_attention(self.q.data_ptr(), kc, vc, self.pos.data_ptr(), self.attn.data_ptr(),
+                                              cfg.heads, cfg.kv_heads, hd, self.max_seq,
+                                              ctypes.c_float(self.scale), s))
+            tr("attention", li)
+            qmm._check(L.qmm_matmul_ex(self._o[li], 1, self.attn.data_ptr(), 1, cfg.heads * hd, None, eps, 1,
+                                       self._x_y, self._x_ld, None, 0, s))
+            tr("o", li)
+            qmm._check(L.qmm_matmul_ex(self._gu[li], 2, self.x.data_ptr(), 1, H, fn, eps, 0, self._gu_y,
+                                       self._gu_ld, None, 0, s))
+            tr("gate_up", li)
+            qmm._check(L.qmm_silu_mul_quantize(self.g.data_ptr(), self.u.data_ptr(), 1, cfg.ffn, cfg.ffn,
+                                               self.hq.data_ptr(), s))
+            tr("silu_mul", li)
+            qmm._check(L.qmm_matmul_q_ex(w.layers[li]["down"].handle, self.hq.data_ptr(), 1, self.x.data_ptr(), H,
+                                         1, s))
+            tr("down", li)
+        qmm._check(L.qmm_matmul_ex(self._head, 1, self.x.data_ptr(), 1, H, w.final_norm.data_ptr(), eps, 0,
+                                   self._lg_y, self._lg_ld, None, 0, s))
+        tr("head", -1)
+        qmm._check(L.qmm_greedy_advance(self.logits.data_ptr(), cfg.vocab, self.tokens.data_ptr(), self.max_seq,
+                                        self.pos.data_ptr(), self.prompt_len, s))
+        tr("argmax", -1)
+
+    # -- driver ------------------------------------------------------------
+    def reset(self, prompt: List[int]):
+        """Load a prompt; the next step processes position 0."""
+        if len(prompt) < 1 or len(prompt) > self.max_seq:
+            raise qmm.QmmError(1, f"prompt length {len(prompt)} outside 1..{self.max_seq}")
+        if min(prompt) < 0 or max(prompt) >= self.cfg.vocab:
+            raise qmm.QmmError(1, f"prompt token ids must lie in [0, {self.cfg.vocab})")
+        if self.prompt_len != len(prompt):
+            self._graph = None  # the prompt length is a launch argument of the captured step
+        self.tokens.zero_()
+        self.tokens[: len(prompt)] = torch.tensor(prompt, dtype=torch.int32, device=self.dev)
+        self.pos.zero_()
+        self.kcache.zero_()
+        self.vcache.zero_()
+        self.prompt_len = len(prompt)
+        self.steps_done = 0
+
+    def capture(self):
+        """Capture one step into a HIP graph. Called at the state reset() leaves; an eager warm-up
+        step (which loads the kernels) runs first and its effect is undone."""
+        if self.steps_done != 0:
+            raise qmm.QmmError(1, "capture() needs the state reset() leaves")
+        prompt = self.tokens[: self.prompt_len].cpu().tolist()
+        self.step()
+        torch.cuda.synchronize()
+        self.reset(prompt)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step()
+        torch.cuda.synchronize()
+        self._graph = g
+
+    def run(self, steps: int, use_graph: bool = True, history: Optional[torch.Tensor] = None,
+            trace: Optional[Callable[[str, int], None]] = None):
+        """Run `steps` token steps from the current position; with `history`, row i receives the
+        logits of step i (copied between graph replays). A `trace` runs the steps eagerly."""
+        if self.prompt_len == 0:
+            raise qmm.QmmError(1, "reset() with a prompt before run()")
+        if self.steps_done + steps > self.max_seq:
+            raise qmm.QmmError(1, f"{self.steps_done} + {steps} steps exceed max_seq {self.max_seq}")
+        use_graph = use_graph and trace is None
+        if use_graph and self._graph is None:
+            self.capture()
+        self.steps_done += steps
+        for i in range(steps):
+            if use_graph:
+                self._graph.replay()
+            else:
+                self.step(trace)
+            if history is not None:
+                history[i].copy_(self.logits)
+
+    def generated(self, total: int) -> List[int]:
+        return self.tokens[:total].cpu().tolist()

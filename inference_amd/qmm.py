@@ -45,7 +45,9 @@ EXPORTS = (
     "qmm_qtensor_to_ggml", "qmm_qtensor_info", "qmm_qtensor_ggml_bytes", "qmm_qtensor_free",
     "qmm_quantize_rows", "qmm_matmul_workspace_size", "qmm_matmul", "qmm_matmul_q",
     "qmm_matmul_multi", "qmm_block_dots", "qmm_moe_route", "qmm_moe_gemv", "qmm_moe_ffn_workspace_size",
-    "qmm_moe_ffn",
+    "qmm_moe_ffn", "qmm_matmul_ex", "qmm_matmul_ex_workspace_size", "qmm_rms_norm", "qmm_embed_rows",
+    "qmm_rope_kv_append", "qmm_decode_attention", "qmm_silu_mul_quantize", "qmm_greedy_advance",
+    "qmm_matmul_q_ex",
 )
 
 
@@ -87,6 +89,16 @@ def lib() -> ctypes.CDLL:
             "qmm_moe_gemv": ([ctypes.POINTER(vp), i32, i32, vp, i64, vp, vp, ctypes.POINTER(vp), vp], i32),
             "qmm_moe_ffn_workspace_size": ([vp, vp, i64, i32, i32], sz),
             "qmm_moe_ffn": ([vp, i64, i64, vp, i32, i32, vp, vp, vp, vp, i64, vp, sz, vp], i32),
+            "qmm_matmul_ex": ([ctypes.POINTER(vp), i32, vp, i64, i64, vp, ctypes.c_float, i32, ctypes.POINTER(vp),
+                               ctypes.POINTER(i64), vp, sz, vp], i32),
+            "qmm_matmul_ex_workspace_size": ([vp, i64, i32], sz),
+            "qmm_rms_norm": ([vp, i64, i64, i64, vp, ctypes.c_float, vp, i64, vp], i32),
+            "qmm_embed_rows": ([vp, i64, vp, vp, vp, i64, vp], i32),
+            "qmm_rope_kv_append": ([vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp], i32),
+            "qmm_decode_attention": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp], i32),
+            "qmm_silu_mul_quantize": ([vp, vp, i64, i64, i64, vp, vp], i32),
+            "qmm_greedy_advance": ([vp, i64, vp, i64, vp, i32, vp], i32),
+            "qmm_matmul_q_ex": ([vp, vp, i64, vp, i64, i32, vp], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)

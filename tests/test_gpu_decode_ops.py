@@ -1,0 +1,208 @@
+"""Each decode-step launch of the C-ABI against the CPU decode oracle, one op at a time.
+
+Non-matmul ops are f32 like the reference's decode path and are held to a
+few ulp-scale tolerances stated per test; matmuls (with the RMSNorm prologue
+or the accumulate epilogue) to max|d| <= 1e-3 * rms.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from inference_amd import GgmlDType, QTensor, qmm
+from inference_amd.llama_decode import LlamaConfig, rope_tables
+from oracle import llama as ol
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def L():
+    return qmm.lib()
+
+
+def S():
+    return qmm._stream(DEV)
+
+
+def t(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV, dtype)
+
+
+def rel_err(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.abs(got - want).max() / np.sqrt((want ** 2).mean()))
+
+
+def test_rms_norm_kernel():
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal((3, 4096)) * 3).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 4096).astype(np.float32)
+    xd, wd, out = t(x), t(w), torch.zeros((3, 4096), device=DEV)
+    qmm._check(L().qmm_rms_norm(xd.data_ptr(), 3, 4096, 4096, wd.data_ptr(), ctypes.c_float(1e-5), out.data_ptr(),
+                                4096, S()))
+    np.testing.assert_allclose(out.cpu().numpy(), ol.rms_norm(x, w, 1e-5), rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("dt", [GgmlDType.Q4K, GgmlDType.Q6K])
+@pytest.mark.parametrize("m", [1, 2, 5])
+def test_matmul_ex_rms_norm_prologue(dt, m):
+    rng = np.random.default_rng(10 + m)
+    n, k = 640, 4096
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    qt = QTensor.quantize(t(w), dt)
+    x = (rng.standard_normal((m, k)) * 0.05).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, k).astype(np.float32)
+    xd, nwd = t(x), t(nw)
+    y = torch.zeros((m, n), device=DEV)
+    wsb = int(L().qmm_matmul_ex_workspace_size(qt.handle, m, 1))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    hs = (ctypes.c_void_p * 1)(qt.handle.value)
+    ys = (ctypes.c_void_p * 1)(y.data_ptr())
+    lds = (ctypes.c_int64 * 1)(n)
+    qmm._check(L().qmm_matmul_ex(hs, 1, xd.data_ptr(), m, k, nwd.data_ptr(), ctypes.c_float(1e-5), 0, ys, lds,
+                                 ws.data_ptr(), wsb, S()))
+    want = orc.matmul(int(dt), ol.rms_norm(x, nw, 1e-5), qt.to_ggml(), k)
+    assert rel_err(y.cpu().numpy(), want) <= 1e-3
+
+
+@pytest.mark.parametrize("m", [1, 2, 12])
+def test_matmul_ex_accumulate(m):
+    rng = np.random.default_rng(20 + m)
+    n, k = 384, 1024
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    qt = QTensor.quantize(t(w), GgmlDType.Q4K)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    xd, y = t(x), t(y0)
+    wsb = int(L().qmm_matmul_ex_workspace_size(qt.handle, m, 0))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    hs = (ctypes.c_void_p * 1)(qt.handle.value)
+    ys = (ctypes.c_void_p * 1)(y.data_ptr())
+    lds = (ctypes.c_int64 * 1)(n)
+    qmm._check(L().qmm_matmul_ex(hs, 1, xd.data_ptr(), m, k, None, ctypes.c_float(0), 1, ys, lds, ws.data_ptr(),
+                                 wsb, S()))
+    prod = orc.matmul(orc.Q4K, x, qt.to_ggml(), k)
+    assert rel_err(y.cpu().numpy() - y0, prod) <= 1e-3
+    np.testing.assert_allclose(y.cpu().numpy(), y0 + prod, rtol=0, atol=1e-3 * float(np.sqrt((prod ** 2).mean())))
+
+
+def test_matmul_q_ex_accumulate():
+    rng = np.random.default_rng(30)
+    n, k = 512, 2048
+    qt = QTensor.quantize(t((rng.standard_normal((n, k)) * 0.02).astype(np.float32)), GgmlDType.Q6K)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    xq = orc.quantize(orc.Q8K, x)
+    y0 = rng.standard_normal((1, n)).astype(np.float32)
+    y = t(y0)
+    xqd = t(xq, torch.uint8)
+    qmm._check(L().qmm_matmul_q_ex(qt.handle, xqd.data_ptr(), 1, y.data_ptr(), n, 1, S()))
+    prod = orc.matmul_prequant(orc.Q6K, xq, qt.to_ggml(), k)
+    assert rel_err(y.cpu().numpy() - y0, prod) <= 1e-3
+
+
+def test_embed_rows():
+    rng = np.random.default_rng(40)
+    table = rng.standard_normal((50, 96)).astype(np.float32)
+    toks = t(np.array([7, 3, 41, 0], np.int32), torch.int32)
+    td = t(table)
+    for p in range(4):
+        pos = t(np.array([p], np.int32), torch.int32)
+        x = torch.zeros(96, device=DEV)
+        qmm._check(L().qmm_embed_rows(td.data_ptr(), 96, toks.data_ptr(), pos.data_ptr(), x.data_ptr(), 96, S()))
+        np.testing.assert_array_equal(x.cpu().numpy(), table[[7, 3, 41, 0][p]])
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd", [(32, 8, 128), (8, 2, 64), (4, 1, 128)])
+@pytest.mark.parametrize("p", [0, 1, 37, 255])
+def test_rope_kv_append(heads, kv_heads, hd, p):
+    rng = np.random.default_rng(50 + p)
+    cfg = LlamaConfig(heads=heads, kv_heads=kv_heads, head_dim=hd)
+    max_seq = 256
+    cos, sin = rope_tables(cfg, max_seq)
+    q = rng.standard_normal((heads, hd)).astype(np.float32)
+    k = rng.standard_normal((kv_heads, hd)).astype(np.float32)
+    v = rng.standard_normal((kv_heads, hd)).astype(np.float32)
+    qd, kd, vd = t(q), t(k), t(v)
+    kc = torch.zeros((kv_heads, max_seq, hd), device=DEV)
+    vc = torch.zeros((kv_heads, max_seq, hd), device=DEV)
+    pos = t(np.array([p], np.int32), torch.int32)
+    cosd, sind = t(cos), t(sin)  # held: a temporary's memory could be reused before the kernel runs
+    qmm._check(L().qmm_rope_kv_append(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), cosd.data_ptr(),
+                                      sind.data_ptr(), pos.data_ptr(), kc.data_ptr(), vc.data_ptr(), heads,
+                                      kv_heads, hd, max_seq, S()))
+    inv = ol.llama3_inv_freq(hd, cfg.rope_theta, cfg.rope_factor, cfg.rope_low, cfg.rope_high, cfg.rope_orig_ctx)
+    c, s = ol.cos_sin(inv, p)
+    np.testing.assert_allclose(qd.cpu().numpy(), ol.apply_rope(q, c, s), rtol=0, atol=2e-6)
+    np.testing.assert_allclose(kd.cpu().numpy(), ol.apply_rope(k, c, s), rtol=0, atol=2e-6)
+    kcn, vcn = kc.cpu().numpy(), vc.cpu().numpy()
+    np.testing.assert_array_equal(kcn[:, p], kd.cpu().numpy())
+    np.testing.assert_array_equal(vcn[:, p], v)
+    others = np.ones(max_seq, bool)
+    others[p] = False
+    assert not kcn[:, others].any() and not vcn[:, others].any()
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd", [(32, 8, 128), (8, 2, 64), (4, 4, 256)])
+@pytest.mark.parametrize("p", [0, 1, 255, 300, 4095])
+def test_decode_attention(heads, kv_heads, hd, p):
+    rng = np.random.default_rng(60 + p)
+    max_seq = 4096
+    kc = rng.standard_normal((kv_heads, max_seq, hd)).astype(np.float32)
+    vc = rng.standard_normal((kv_heads, max_seq, hd)).astype(np.float32)
+    q = rng.standard_normal((heads, hd)).astype(np.float32)
+    out = torch.zeros((heads, hd), device=DEV)
+    pos = t(np.array([p], np.int32), torch.int32)
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    qd, kcd, vcd = t(q), t(kc), t(vc)
+    qmm._check(L().qmm_decode_attention(qd.data_ptr(), kcd.data_ptr(), vcd.data_ptr(), pos.data_ptr(),
+                                        out.data_ptr(), heads, kv_heads, hd, max_seq, ctypes.c_float(scale), S()))
+    g = heads // kv_heads
+    want = np.stack([ol.attend_one(q[h], kc[h // g, : p + 1], vc[h // g, : p + 1], scale) for h in range(heads)])
+    np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-4, atol=2e-5)
+
+
+def test_silu_mul_quantize():
+    rng = np.random.default_rng(70)
+    rows, k = 2, 1536
+    gt = (rng.standard_normal((rows, k)) * 2).astype(np.float32)
+    ut = rng.standard_normal((rows, k)).astype(np.float32)
+    hq = torch.zeros((rows, k // 256 * 292), dtype=torch.uint8, device=DEV)
+    gd, ud = t(gt), t(ut)
+    qmm._check(L().qmm_silu_mul_quantize(gd.data_ptr(), ud.data_ptr(), rows, k, k, hq.data_ptr(), S()))
+    h = (ol.silu(gt) * ut).astype(np.float32)
+    want = orc.quantize(orc.Q8K, h)
+    got = hq.cpu().numpy()
+    # expf may differ from numpy's exp by an ulp: a quant may move by one step at a rounding tie
+    dg = orc.dequantize(orc.Q8K, got, rows * k)
+    dw = orc.dequantize(orc.Q8K, want, rows * k)
+    d = np.abs(h).reshape(-1, 256).max(axis=1) / 127.0
+    assert np.all(np.abs(dg - dw).reshape(-1, 256) <= 1.01 * d[:, None] + 1e-12)
+    assert (got != want).mean() < 0.01
+
+
+def test_greedy_advance():
+    logits = t(np.array([0.5, 3.0, -1.0, 3.0, 2.0], np.float32))
+    toks = t(np.array([4, 4, 4, 0, 0, 0], np.int32), torch.int32)
+    pos = t(np.array([0], np.int32), torch.int32)
+
+    def adv(prompt_len, capacity=6):
+        qmm._check(L().qmm_greedy_advance(logits.data_ptr(), 5, toks.data_ptr(), capacity, pos.data_ptr(),
+                                          prompt_len, S()))
+        torch.cuda.synchronize()
+        return toks.cpu().tolist(), int(pos.item())
+
+    assert adv(3) == ([4, 4, 4, 0, 0, 0], 1)  # slot 1 holds a prompt token
+    assert adv(3) == ([4, 4, 4, 0, 0, 0], 2)
+    assert adv(3) == ([4, 4, 4, 1, 0, 0], 3)  # ties -> lowest index
+    adv(3)
+    assert adv(3) == ([4, 4, 4, 1, 1, 1], 5)
+    assert adv(3) == ([4, 4, 4, 1, 1, 1], 5)  # capacity reached: nothing written, pos stays
+    big = (np.random.default_rng(80).standard_normal(128256) * 3).astype(np.float32)
+    big[77777] = big.max() + 1.0
+    logits = t(big)
+    pos.zero_()
+    qmm._check(L().qmm_greedy_advance(logits.data_ptr(), 128256, toks.data_ptr(), 6, pos.data_ptr(), 1, S()))
+    assert toks[1].item() == 77777
