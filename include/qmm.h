@@ -178,17 +178,37 @@ int qmm_rope_kv_append(float *q, float *k, const float *v, const float *cos_t, c
                        const int32_t *pos, float *kcache, float *vcache, int heads, int kv_heads, int head_dim,
                        int max_seq, void *stream);
 
+/* Workspace bytes of the two attention calls below (0 for an unsupported
+ * geometry): heads % kv_heads == 0, heads / kv_heads <= 8, head_dim in
+ * {64, 128, 256}, max_seq <= 4096. The workspace holds per-chunk partial
+ * results between the call's two launches; calls that share a workspace
+ * must not run concurrently. */
+size_t qmm_decode_attention_workspace_size(int heads, int kv_heads, int head_dim, int max_seq);
+
 /* One query per head against cache positions 0..pos[0]: out[h] =
  * softmax(q[h] . K^T * scale) . V with kv head h / (heads / kv_heads)
- * (repeat_kv + sdpa_eager, attention.rs:59-68, 154-186). max_seq <= 4096. */
+ * (repeat_kv + sdpa_eager, attention.rs:59-68, 154-186). q is already
+ * rotated and the cache already holds position pos[0]. */
 int qmm_decode_attention(const float *q, const float *kcache, const float *vcache, const int32_t *pos,
-                         float *out, int heads, int kv_heads, int head_dim, int max_seq, float scale,
-                         void *stream);
+                         float *out, int heads, int kv_heads, int head_dim, int max_seq, float scale, void *ws,
+                         size_t ws_bytes, void *stream);
+
+/* qmm_rope_kv_append followed by qmm_decode_attention in one launch: q, k
+ * are the unrotated projections (left unchanged), the rotated k and v are
+ * written to position pos[0] of the caches, out as qmm_decode_attention. */
+int qmm_decode_rope_attention(const float *q, const float *k, const float *v, const float *cos_t,
+                              const float *sin_t, const int32_t *pos, float *kcache, float *vcache, float *out,
+                              int heads, int kv_heads, int head_dim, int max_seq, float scale, void *ws,
+                              size_t ws_bytes, void *stream);
 
 /* hq = Q8_K(silu(g) * u) for rows x k (k a multiple of 256), the down
  * projection's activation (LlamaMlp::forward, llama.rs:1386-1391). */
 int qmm_silu_mul_quantize(const float *g, const float *u, int64_t rows, int64_t k, int64_t ld, void *hq,
                           void *stream);
+
+/* Workspace bytes of qmm_greedy_advance; the first 256 bytes are a counter
+ * with the same zero-before-first-use contract as the attention workspace. */
+size_t qmm_greedy_workspace_size(int64_t n);
 
 /* Greedy step end on the device: tokens[pos+1] = argmax(logits) (lowest index
  * on ties, argmax_device, sampler.rs:216-219) unless pos+1 < prompt_len (the
@@ -197,7 +217,7 @@ int qmm_silu_mul_quantize(const float *g, const float *u, int64_t rows, int64_t 
  * writes nothing and pos stays, so a step replayed too often never writes
  * out of bounds. */
 int qmm_greedy_advance(const float *logits, int64_t n, int32_t *tokens, int64_t capacity, int32_t *pos,
-                       int prompt_len, void *stream);
+                       int prompt_len, void *ws, size_t ws_bytes, void *stream);
 
 /* ---- mixture of experts (MoeMlp::forward, crates/llm/candle-llm/src/models/llama.rs:1416-1487) ---- */
 

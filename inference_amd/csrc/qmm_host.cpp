@@ -118,9 +118,13 @@ int kernel(Device* d, const std::string& name, hipFunction_t* f) {
   }
   hipFunction_t fn = nullptr;
   hipError_t e = hipModuleGetFunction(&fn, d->module, name.c_str());
-  if (e != hipSuccess || !fn)
+  if (e != hipSuccess || !fn) {
+    // The failed lookup also sets the runtime's last error; clear it so the
+    // caller's next unrelated HIP call (e.g. a graph capture) does not report it.
+    (void)hipGetLastError();
     return fail(QMM_ERR_NO_KERNEL, "kernel %s missing from the code object: %s", name.c_str(),
                 hipGetErrorString(e));
+  }
   d->fns.emplace(name, fn);
   *f = fn;
   return QMM_OK;
@@ -488,20 +492,26 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   if (total > (1LL << 31) - 1) return fail(QMM_ERR_INVALID, "too many output rows in one launch");
   jobs.njobs = count;
   jobs.total = (int)total;
-  // Launch shape (from sweeps on MI355X at the Llama-3-8B shapes). Each wave
-  // keeps one or two 32-byte weight slices per lane in flight and prefetches
-  // its next row while finishing the current one; the grid is sized for ~20
-  // resident waves per CU so every wave walks several rows. 16-wave workgroups
-  // share the staged (or in-kernel quantized: one block per wave) activation
-  // over more rows; 8-wave ones are used where the 16-wave variant would
-  // exceed 128 VGPRs.
-  int wv = 16, r = 1, u = niter >= 2 ? 2 : 1;
-  if (fused) {
-    if (m == 2 && fmt == kFmtQ6K) u = 1;
-  } else if (m > 1 || nb * xbb <= 8192) {
-    wv = 8;
+  // Launch shape (from sweeps on MI355X at the Llama-3-8B decode shapes).
+  // Each wave keeps one or two weight slices per lane in flight and prefetches
+  // its next row while finishing the current one; 16 waves are resident per
+  // CU. Fused (in-kernel quantization) and long-K staged launches use one
+  // 16-wave workgroup per CU: the workgroup shares its activation over more
+  // rows, and a grid that leaves some CUs with one workgroup more than others
+  // finishes with those CUs (up to 35% slower at the gate/up and head shapes).
+  // Staged launches with a short activation (<= 8 KB in LDS) use 4-wave
+  // workgroups, so that even 1024-row weights spread over every CU. m > 1
+  // staged launches use 8 waves (the 16-wave variants would exceed 128 VGPRs).
+  int wv = 16, r = 1, u = 1;
+  if (!fused) {
+    if (m > 1) {
+      wv = 8;
+      if (niter >= 2) u = 2;
+    } else if (nb * xbb <= 8192) {
+      wv = 4;
+    }
   }
-  int waves_per_cu = 20;
+  int waves_per_cu = !fused && m > 1 ? 20 : 16;  // m > 1: the earlier sweep's optimum
   const Tuning tu = tuning();
   if (tu.w > 0 && tu.r > 0 && tu.u > 0) { wv = tu.w; r = tu.r; u = tu.u; }
   if (tu.waves_per_cu > 0) waves_per_cu = tu.waves_per_cu;
@@ -766,15 +776,59 @@ int qmm_rope_kv_append(float* q, float* k, const float* v, const float* cos_t, c
   return launch(d, "qmm_decode_rope_kv", (unsigned)(heads + kv_heads), threads, 0, (hipStream_t)stream, args);
 }
 
-int qmm_decode_attention(const float* q, const float* kcache, const float* vcache, const int32_t* pos, float* out,
-                         int heads, int kv_heads, int head_dim, int max_seq, float scale, void* stream) {
-  if (!q || !kcache || !vcache || !pos || !out) return fail(QMM_ERR_INVALID, "null pointer");
-  if (heads < 1 || kv_heads < 1 || heads % kv_heads || head_dim < 1 || head_dim > 256 || max_seq < 1 || max_seq > 4096)
-    return fail(QMM_ERR_INVALID, "bad attention geometry (head_dim <= 256, max_seq <= 4096)");
+// Workspace of the split attention: S chunks x heads x (m, l, o[head_dim]) floats.
+static const int kAttnSplits = 16;  // must equal the kernel's qmm::kAttnSplits
+
+static int check_attention(int heads, int kv_heads, int head_dim, int max_seq) {
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads || heads / kv_heads > 8)
+    return fail(QMM_ERR_INVALID, "attention needs heads %% kv_heads == 0 and heads / kv_heads <= 8");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(QMM_ERR_INVALID, "attention head_dim must be 64, 128 or 256 (got %d)", head_dim);
+  if (max_seq < 1 || max_seq > kAttnSplits * 256)
+    return fail(QMM_ERR_INVALID, "attention max_seq must be in [1, %d] (got %d)", kAttnSplits * 256, max_seq);
+  return QMM_OK;
+}
+
+size_t qmm_decode_attention_workspace_size(int heads, int kv_heads, int head_dim, int max_seq) {
+  if (check_attention(heads, kv_heads, head_dim, max_seq) != QMM_OK) return 0;
+  return (size_t)kAttnSplits * heads * (head_dim + 2) * sizeof(float);
+}
+
+static int attention(const float* q, const float* k, const float* v, const float* cos_t, const float* sin_t,
+                     const int32_t* pos, float* kcache, float* vcache, float* out, int heads, int kv_heads,
+                     int head_dim, int max_seq, float scale, void* ws, size_t ws_bytes, void* stream) {
+  QMM_TRY(check_attention(heads, kv_heads, head_dim, max_seq));
+  const size_t need = qmm_decode_attention_workspace_size(heads, kv_heads, head_dim, max_seq);
+  if (!ws || ws_bytes < need) return fail(QMM_ERR_INVALID, "attention workspace of %zu B < %zu B", ws_bytes, need);
   Device* d;
   QMM_TRY(current_device(&d));
-  void* args[] = {&q, &kcache, &vcache, &pos, &out, &heads, &kv_heads, &head_dim, &max_seq, &scale};
-  return launch(d, "qmm_decode_attention", (unsigned)heads, 256, 0, (hipStream_t)stream, args);
+  float* part = (float*)ws;
+  void* args[] = {&q, &k, &v, &cos_t, &sin_t, &pos, &kcache, &vcache, &part,
+                  &heads, &kv_heads, &head_dim, &max_seq, &scale};
+  hipFunction_t f;
+  QMM_TRY(kernel(d, "qmm_decode_attention_split", &f));
+  QMM_HIP(hipModuleLaunchKernel(f, (unsigned)kv_heads, (unsigned)kAttnSplits, 1, 256, 1, 1, 0,
+                                (hipStream_t)stream, args, nullptr));
+  void* margs[] = {&part, &out, &heads, &head_dim};
+  return launch(d, "qmm_decode_attention_merge", (unsigned)heads, (unsigned)head_dim, 0, (hipStream_t)stream, margs);
+}
+
+int qmm_decode_attention(const float* q, const float* kcache, const float* vcache, const int32_t* pos, float* out,
+                         int heads, int kv_heads, int head_dim, int max_seq, float scale, void* ws, size_t ws_bytes,
+                         void* stream) {
+  if (!q || !kcache || !vcache || !pos || !out) return fail(QMM_ERR_INVALID, "null pointer");
+  return attention(q, nullptr, nullptr, nullptr, nullptr, pos, const_cast<float*>(kcache),
+                   const_cast<float*>(vcache), out, heads, kv_heads, head_dim, max_seq, scale, ws, ws_bytes, stream);
+}
+
+int qmm_decode_rope_attention(const float* q, const float* k, const float* v, const float* cos_t,
+                              const float* sin_t, const int32_t* pos, float* kcache, float* vcache, float* out,
+                              int heads, int kv_heads, int head_dim, int max_seq, float scale, void* ws,
+                              size_t ws_bytes, void* stream) {
+  if (!q || !k || !v || !cos_t || !sin_t || !pos || !kcache || !vcache || !out)
+    return fail(QMM_ERR_INVALID, "null pointer");
+  return attention(q, k, v, cos_t, sin_t, pos, kcache, vcache, out, heads, kv_heads, head_dim, max_seq, scale, ws,
+                   ws_bytes, stream);
 }
 
 int qmm_silu_mul_quantize(const float* g, const float* u, int64_t rows, int64_t k, int64_t ld, void* hq,
@@ -788,15 +842,27 @@ int qmm_silu_mul_quantize(const float* g, const float* u, int64_t rows, int64_t 
   return launch(d, "qmm_silu_mul_q8k", ceil_div(rows * (k / 256), 4), 256, 0, (hipStream_t)stream, args);
 }
 
+static const int kArgmaxBlocks = 128;
+
+size_t qmm_greedy_workspace_size(int64_t n) {
+  (void)n;
+  return 256 + (size_t)kArgmaxBlocks * 8;
+}
+
 int qmm_greedy_advance(const float* logits, int64_t n, int32_t* tokens, int64_t capacity, int32_t* pos,
-                       int prompt_len, void* stream) {
+                       int prompt_len, void* ws, size_t ws_bytes, void* stream) {
   if (!logits || !tokens || !pos || n < 1 || n > INT32_MAX || capacity < 1 || capacity > INT32_MAX)
     return fail(QMM_ERR_INVALID, "bad argmax arguments");
+  const size_t need = qmm_greedy_workspace_size(n);
+  if (!ws || ws_bytes < need) return fail(QMM_ERR_INVALID, "argmax workspace of %zu B < %zu B", ws_bytes, need);
   Device* d;
   QMM_TRY(current_device(&d));
   int nn = (int)n, cap = (int)capacity;
-  void* args[] = {&logits, &nn, &tokens, &cap, &pos, &prompt_len};
-  return launch(d, "qmm_decode_argmax", 1, 1024, 0, (hipStream_t)stream, args);
+  unsigned* counter = (unsigned*)ws;
+  float* pval = (float*)((uint8_t*)ws + 256);
+  int* pidx = (int*)(pval + kArgmaxBlocks);
+  void* args[] = {&logits, &nn, &tokens, &cap, &pos, &prompt_len, &pval, &pidx, &counter};
+  return launch(d, "qmm_decode_argmax", kArgmaxBlocks, 256, 0, (hipStream_t)stream, args);
 }
 
 int qmm_block_dots(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int64_t ldy, int32_t* dots,

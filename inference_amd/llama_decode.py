@@ -150,8 +150,6 @@ class DecodeSession:
     def __init__(self, weights: LlamaWeights, max_seq: int):
         cfg = weights.cfg
         self.cfg, self.w, self.max_seq = cfg, weights, max_seq
-        if max_seq > 4096:
-            raise qmm.QmmError(1, "decode attention supports up to 4096 positions")
         dev = weights.embed.device
         self.dev = dev
         f32 = dict(dtype=torch.float32, device=dev)
@@ -178,6 +176,13 @@ class DecodeSession:
         self._graph = None
         L = qmm.lib()
         self.L = L
+        # workspaces of the split attention (chunk partials) and of the argmax (its counter
+        # starts at zero and every launch leaves it at zero)
+        wsa = int(L.qmm_decode_attention_workspace_size(cfg.heads, cfg.kv_heads, cfg.head_dim, max_seq))
+        if wsa == 0:
+            raise qmm.QmmError(1, "unsupported attention geometry: " + qmm.last_error())
+        self.ws_attn = torch.zeros(wsa, dtype=torch.uint8, device=dev)
+        self.ws_argmax = torch.zeros(int(L.qmm_greedy_workspace_size(cfg.vocab)), dtype=torch.uint8, device=dev)
         # launch arguments prepared once (ctypes arrays of handles / outputs)
         self._arr = []
 
@@ -208,8 +213,9 @@ class DecodeSession:
         """Enqueue one token step on the current stream (no host synchronisation).
 
         `trace(op, layer)`, when given, is called after each launch is enqueued (ops: embed, qk, v,
-        rope_kv, attention, o, gate_up, silu_mul, down, head, argmax); it lets a checker inspect the
-        session's buffers between launches. Captured steps take no trace.
+        attention (RoPE + KV append + attention in one launch), o, gate_up, silu_mul, down, head,
+        argmax); it lets a checker inspect the session's buffers between launches. Captured steps
+        take no trace.
         """
         cfg, L, w = self.cfg, self.L, self.w
         s = qmm._stream(self.dev)
@@ -230,13 +236,11 @@ class DecodeSession:
             tr("v", li)
             kc = self.kcache.data_ptr() + 4 * li * kv_stride
             vc = self.vcache.data_ptr() + 4 * li * kv_stride
-            qmm._check(L.qmm_rope_kv_append(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
-                                            self.cos.data_ptr(), self.sin.data_ptr(), self.pos.data_ptr(), kc, vc,
-                                            cfg.heads, cfg.kv_heads, hd, self.max_seq, s))
-            tr("rope_kv", li)
-            qmm._check(L.qmm_decode_attention(self.q.data_ptr(), kc, vc, self.pos.data_ptr(), self.attn.data_ptr(),
-                                              cfg.heads, cfg.kv_heads, hd, self.max_seq,
-                                              ctypes.c_float(self.scale), s))
+            qmm._check(L.qmm_decode_rope_attention(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                                                   self.cos.data_ptr(), self.sin.data_ptr(), self.pos.data_ptr(),
+                                                   kc, vc, self.attn.data_ptr(), cfg.heads, cfg.kv_heads, hd,
+                                                   self.max_seq, ctypes.c_float(self.scale),
+                                                   self.ws_attn.data_ptr(), self.ws_attn.numel(), s))
             tr("attention", li)
             qmm._check(L.qmm_matmul_ex(self._o[li], 1, self.attn.data_ptr(), 1, cfg.heads * hd, None, eps, 1,
                                        self._x_y, self._x_ld, None, 0, s))
@@ -254,7 +258,8 @@ class DecodeSession:
                                    self._lg_y, self._lg_ld, None, 0, s))
         tr("head", -1)
         qmm._check(L.qmm_greedy_advance(self.logits.data_ptr(), cfg.vocab, self.tokens.data_ptr(), self.max_seq,
-                                        self.pos.data_ptr(), self.prompt_len, s))
+                                        self.pos.data_ptr(), self.prompt_len, self.ws_argmax.data_ptr(),
+                                        self.ws_argmax.numel(), s))
         tr("argmax", -1)
 
     # -- driver ------------------------------------------------------------

@@ -47,7 +47,8 @@ EXPORTS = (
     "qmm_matmul_multi", "qmm_block_dots", "qmm_moe_route", "qmm_moe_gemv", "qmm_moe_ffn_workspace_size",
     "qmm_moe_ffn", "qmm_matmul_ex", "qmm_matmul_ex_workspace_size", "qmm_rms_norm", "qmm_embed_rows",
     "qmm_rope_kv_append", "qmm_decode_attention", "qmm_silu_mul_quantize", "qmm_greedy_advance",
-    "qmm_matmul_q_ex",
+    "qmm_matmul_q_ex", "qmm_decode_attention_workspace_size", "qmm_decode_rope_attention",
+    "qmm_greedy_workspace_size",
 )
 
 
@@ -95,9 +96,13 @@ def lib() -> ctypes.CDLL:
             "qmm_rms_norm": ([vp, i64, i64, i64, vp, ctypes.c_float, vp, i64, vp], i32),
             "qmm_embed_rows": ([vp, i64, vp, vp, vp, i64, vp], i32),
             "qmm_rope_kv_append": ([vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp], i32),
-            "qmm_decode_attention": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp], i32),
+            "qmm_decode_attention": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp, sz, vp], i32),
+            "qmm_decode_rope_attention": ([vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float,
+                                           vp, sz, vp], i32),
+            "qmm_decode_attention_workspace_size": ([i32, i32, i32, i32], sz),
+            "qmm_greedy_workspace_size": ([i64], sz),
             "qmm_silu_mul_quantize": ([vp, vp, i64, i64, i64, vp, vp], i32),
-            "qmm_greedy_advance": ([vp, i64, vp, i64, vp, i32, vp], i32),
+            "qmm_greedy_advance": ([vp, i64, vp, i64, vp, i32, vp, sz, vp], i32),
             "qmm_matmul_q_ex": ([vp, vp, i64, vp, i64, i32, vp], i32),
         }
         for name, (args, res) in sig.items():
@@ -108,10 +113,14 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+def last_error() -> str:
+    """The calling thread's last error message from the library."""
+    return lib().qmm_last_error().decode(errors="replace")
+
+
 def _check(status: int) -> None:
     if status != 0:
-        msg = lib().qmm_last_error().decode(errors="replace")
-        raise QmmError(status, msg)
+        raise QmmError(status, last_error())
 
 
 def _stream(device: torch.device) -> ctypes.c_void_p:

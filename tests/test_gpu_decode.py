@@ -5,9 +5,9 @@ Two levels of parity:
 * Op level (the gate). At every step, every launch of the step is checked
   against the oracle's operation applied to the device's own inputs to that
   launch: matmuls (with the fused RMSNorm prologue or the accumulate
-  epilogue) to max|d| <= 1e-3 * rms, embedding / KV append / argmax exactly,
-  RoPE and attention to f32 rounding, SiLU*mul -> Q8_K to one quantum (the
-  device's expf and numpy's exp may differ by an ulp).
+  epilogue) to max|d| <= 1e-3 * rms; embedding, the fused RoPE + KV append
+  and argmax exactly; attention to f32 rounding; SiLU*mul -> Q8_K to one
+  quantum (the device's expf and numpy's exp may differ by an ulp).
 * End to end. The oracle runs its own chain, fed the device's tokens. Its
   f32 values differ from the device's in the last bits (exp, accumulation
   order), and when such a difference lands on a Q8_K rounding tie the next
@@ -88,18 +88,18 @@ class OpChecker:
         elif op == "v":
             self.v0 = self.snap(s.v)
             self.note("v", rel_err(self.v0, self.mm("v", li, self.n, c.hidden)), MM_TOL)
-        elif op == "rope_kv":
-            cs, sn = ol.cos_sin(self.inv, self.p)
-            q1, k1 = self.snap(s.q), self.snap(s.k)
-            self.note("rope", rel_err(q1, ol.apply_rope(self.q0.reshape(-1, hd), cs, sn)), 1e-5)
-            self.note("rope", rel_err(k1, ol.apply_rope(self.k0.reshape(-1, hd), cs, sn)), 1e-5)
-            np.testing.assert_array_equal(self.snap(s.kcache[li, :, self.p]).reshape(-1), k1)
-            np.testing.assert_array_equal(self.snap(s.vcache[li, :, self.p]).reshape(-1), self.v0)
-            self.q1 = q1.reshape(-1, hd)
         elif op == "attention":
+            cs, sn = ol.cos_sin(self.inv, self.p)
+            q1 = ol.apply_rope(self.q0.reshape(-1, hd), cs, sn)
+            k1 = ol.apply_rope(self.k0.reshape(-1, hd), cs, sn)
             kc, vc, att = self.snap(s.kcache[li]), self.snap(s.vcache[li]), self.snap(s.attn)
+            # rotated k and v appended at p (same f32 operations as the oracle: bit-equal)
+            np.testing.assert_array_equal(kc[:, self.p], k1)
+            np.testing.assert_array_equal(vc[:, self.p], self.v0.reshape(-1, hd))
+            # q and k buffers keep the unrotated projections
+            np.testing.assert_array_equal(self.snap(s.q), self.q0)
             g = c.heads // c.kv_heads
-            want = np.stack([ol.attend_one(self.q1[h], kc[h // g, : self.p + 1], vc[h // g, : self.p + 1], s.scale)
+            want = np.stack([ol.attend_one(q1[h], kc[h // g, : self.p + 1], vc[h // g, : self.p + 1], s.scale)
                              for h in range(c.heads)])
             self.note("attention", rel_err(att, want), 1e-4)
             self.att = att
@@ -234,7 +234,7 @@ def test_decode_position_bounds(small_model):
     with pytest.raises(QmmError):
         sess.reset([cfg.vocab])
     with pytest.raises(QmmError):
-        DecodeSession(w, 5000)
+        DecodeSession(w, 5000)  # attention supports up to 4096 positions
 
 
 def test_decode_gqa_single_kv_head():

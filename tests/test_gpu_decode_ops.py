@@ -145,8 +145,17 @@ def test_rope_kv_append(heads, kv_heads, hd, p):
     assert not kcn[:, others].any() and not vcn[:, others].any()
 
 
-@pytest.mark.parametrize("heads,kv_heads,hd", [(32, 8, 128), (8, 2, 64), (4, 4, 256)])
-@pytest.mark.parametrize("p", [0, 1, 255, 300, 4095])
+def attn_ws(heads, kv_heads, hd, max_seq):
+    n = int(L().qmm_decode_attention_workspace_size(heads, kv_heads, hd, max_seq))
+    assert n > 0
+    return torch.zeros(n, dtype=torch.uint8, device=DEV)
+
+
+ATTN_GEOM = [(32, 8, 128), (8, 2, 64), (4, 4, 256), (32, 4, 128), (8, 1, 64)]
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd", ATTN_GEOM)
+@pytest.mark.parametrize("p", [0, 1, 17, 255, 300, 4095])
 def test_decode_attention(heads, kv_heads, hd, p):
     rng = np.random.default_rng(60 + p)
     max_seq = 4096
@@ -157,11 +166,61 @@ def test_decode_attention(heads, kv_heads, hd, p):
     pos = t(np.array([p], np.int32), torch.int32)
     scale = float(np.float32(hd) ** np.float32(-0.5))
     qd, kcd, vcd = t(q), t(kc), t(vc)
-    qmm._check(L().qmm_decode_attention(qd.data_ptr(), kcd.data_ptr(), vcd.data_ptr(), pos.data_ptr(),
-                                        out.data_ptr(), heads, kv_heads, hd, max_seq, ctypes.c_float(scale), S()))
+    ws = attn_ws(heads, kv_heads, hd, max_seq)
     g = heads // kv_heads
     want = np.stack([ol.attend_one(q[h], kc[h // g, : p + 1], vc[h // g, : p + 1], scale) for h in range(heads)])
+    for _ in range(2):  # the second call reuses the workspace
+        out.zero_()
+        qmm._check(L().qmm_decode_attention(qd.data_ptr(), kcd.data_ptr(), vcd.data_ptr(), pos.data_ptr(),
+                                            out.data_ptr(), heads, kv_heads, hd, max_seq, ctypes.c_float(scale),
+                                            ws.data_ptr(), ws.numel(), S()))
+        np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-4, atol=2e-5)
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd", ATTN_GEOM)
+@pytest.mark.parametrize("p", [0, 5, 130, 511])
+def test_decode_rope_attention(heads, kv_heads, hd, p):
+    """Fused RoPE + KV append + attention == rope_kv_append then attention (oracle on the same cache)."""
+    rng = np.random.default_rng(90 + p)
+    max_seq = 512
+    cfg = LlamaConfig(heads=heads, kv_heads=kv_heads, head_dim=hd)
+    cos, sin = rope_tables(cfg, max_seq)
+    kc = rng.standard_normal((kv_heads, max_seq, hd)).astype(np.float32)
+    vc = rng.standard_normal((kv_heads, max_seq, hd)).astype(np.float32)
+    q = rng.standard_normal((heads, hd)).astype(np.float32)
+    k = rng.standard_normal((kv_heads, hd)).astype(np.float32)
+    v = rng.standard_normal((kv_heads, hd)).astype(np.float32)
+    qd, kd, vd, kcd, vcd, cosd, sind = t(q), t(k), t(v), t(kc), t(vc), t(cos), t(sin)
+    pos = t(np.array([p], np.int32), torch.int32)
+    out = torch.zeros((heads, hd), device=DEV)
+    ws = attn_ws(heads, kv_heads, hd, max_seq)
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    qmm._check(L().qmm_decode_rope_attention(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), cosd.data_ptr(),
+                                             sind.data_ptr(), pos.data_ptr(), kcd.data_ptr(), vcd.data_ptr(),
+                                             out.data_ptr(), heads, kv_heads, hd, max_seq, ctypes.c_float(scale),
+                                             ws.data_ptr(), ws.numel(), S()))
+    inv = ol.llama3_inv_freq(hd, cfg.rope_theta, cfg.rope_factor, cfg.rope_low, cfg.rope_high, cfg.rope_orig_ctx)
+    c, s_ = ol.cos_sin(inv, p)
+    kref, vref = kc.copy(), vc.copy()
+    kref[:, p] = ol.apply_rope(k, c, s_)
+    vref[:, p] = v
+    np.testing.assert_array_equal(kcd.cpu().numpy(), kref)
+    np.testing.assert_array_equal(vcd.cpu().numpy(), vref)
+    np.testing.assert_array_equal(qd.cpu().numpy(), q)
+    qr = ol.apply_rope(q, c, s_)
+    g = heads // kv_heads
+    want = np.stack([ol.attend_one(qr[h], kref[h // g, : p + 1], vref[h // g, : p + 1], scale) for h in range(heads)])
     np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-4, atol=2e-5)
+
+
+def test_attention_geometry_errors():
+    for bad in [(32, 5, 128, 64), (32, 2, 128, 64), (8, 2, 96, 64), (8, 2, 128, 4097), (8, 2, 128, 0)]:
+        assert int(L().qmm_decode_attention_workspace_size(*bad)) == 0
+    ws = attn_ws(8, 2, 128, 64)
+    x = torch.zeros(16, device=DEV)
+    rc = L().qmm_decode_attention(x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(), 8, 2, 128,
+                                  64, ctypes.c_float(1.0), ws.data_ptr(), 16, S())
+    assert rc == 1 and "workspace" in qmm.last_error()
 
 
 def test_silu_mul_quantize():
@@ -187,10 +246,11 @@ def test_greedy_advance():
     logits = t(np.array([0.5, 3.0, -1.0, 3.0, 2.0], np.float32))
     toks = t(np.array([4, 4, 4, 0, 0, 0], np.int32), torch.int32)
     pos = t(np.array([0], np.int32), torch.int32)
+    ws = torch.zeros(int(L().qmm_greedy_workspace_size(128256)), dtype=torch.uint8, device=DEV)
 
-    def adv(prompt_len, capacity=6):
-        qmm._check(L().qmm_greedy_advance(logits.data_ptr(), 5, toks.data_ptr(), capacity, pos.data_ptr(),
-                                          prompt_len, S()))
+    def adv(prompt_len, capacity=6, n=5):
+        qmm._check(L().qmm_greedy_advance(logits.data_ptr(), n, toks.data_ptr(), capacity, pos.data_ptr(),
+                                          prompt_len, ws.data_ptr(), ws.numel(), S()))
         torch.cuda.synchronize()
         return toks.cpu().tolist(), int(pos.item())
 
@@ -200,9 +260,20 @@ def test_greedy_advance():
     adv(3)
     assert adv(3) == ([4, 4, 4, 1, 1, 1], 5)
     assert adv(3) == ([4, 4, 4, 1, 1, 1], 5)  # capacity reached: nothing written, pos stays
-    big = (np.random.default_rng(80).standard_normal(128256) * 3).astype(np.float32)
-    big[77777] = big.max() + 1.0
-    logits = t(big)
-    pos.zero_()
-    qmm._check(L().qmm_greedy_advance(logits.data_ptr(), 128256, toks.data_ptr(), 6, pos.data_ptr(), 1, S()))
-    assert toks[1].item() == 77777
+    rng = np.random.default_rng(80)
+    for trial in range(6):
+        big = (rng.standard_normal(128256) * 3).astype(np.float32)
+        win = int(rng.integers(0, 128256))
+        big[win] = big.max() + 1.0
+        if trial >= 3:  # exact ties across workgroup slices: the lowest index wins
+            other = int(rng.integers(0, 128256))
+            big[other] = big[win]
+            win = min(win, other)
+        logits = t(big)
+        pos.zero_()
+        adv(1, n=128256)
+        assert toks[1].item() == win
+    assert not ws[:256].any()
+    with pytest.raises(qmm.QmmError):
+        qmm._check(L().qmm_greedy_advance(logits.data_ptr(), 5, toks.data_ptr(), 6, pos.data_ptr(), 1,
+                                          ws.data_ptr(), 8, S()))
