@@ -14,9 +14,17 @@ Steps are captured into HIP graphs (torch.cuda.graph) and replayed; the timed
 region is bracketed by torch.cuda.synchronize(). `value` is algorithmic bytes
 (weights + f32 activations + f32 outputs) per second over the timed steps.
 The roofline object times the dominant kernel (the gate/up GEMV) alone with
-HIP events on the stream it runs on. The CPU baseline is the oracle's C
-restatement of Candle's CPU quantized matmul (k_quants::matmul with the
-generic vec_dot), run on this host's cores over a bounded sample.
+HIP events on the stream it runs on; its `traffic` (HBM bytes per launch) comes
+from the committed rocprofv3 counter summary profiles/gemv_q4k_gate_pmc.json
+(FETCH_SIZE / WRITE_SIZE of that kernel, each scaled by the counter's reading
+for a copy of known size), measured with `--kernel-only gate|copy`. The CPU
+baseline is the oracle's C restatement of Candle's CPU quantized matmul
+(k_quants::matmul with the generic vec_dot), run on this host's cores over a
+bounded sample.
+
+Further legs: config 3 (greedy decode tok/s of the Llama-3-8B-shape Q4_K_M
+model), config 4 (prefill GEMM, MFMA utilisation against the dense int8
+peak) and config 5 (MoE expert FFN, weight GB/s of the active experts).
 """
 from __future__ import annotations
 
@@ -203,8 +211,8 @@ def run_gemv_set(torch, dev, args):
         "ms_per_step": elapsed / steps * 1e3,
         "steps": steps,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "qmm_gemv_q4k_m1 (gate_proj 14336x4096)", "avg_us": round(gate_us, 3),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
+                     "kernel": "qmm_gemv_q4k_m1_w4_r1_u1 (gate_proj 14336x4096)", "avg_us": round(gate_us, 3),
                      "algorithmic_bytes": gate_bytes},
         "per_shape": per_shape,
         "weight_copies": copies,
@@ -257,6 +265,92 @@ def run_decode(torch, dev, args):
             "first_generated": toks[prompt_len:prompt_len + 8]}
 
 
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+
+
+def timed_graph(torch, fn, reps, per_graph):
+    """Average microseconds per fn() call over graph replays (fn launches on the current stream)."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(per_graph):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+
+
+def run_prefill(torch, dev):
+    """Config 4: M = 512 tokens x 4096 (N(0,1), seed 5) through Q4_K 14336x4096 and 4096x14336
+    (N(0, 0.02^2), seed 6, device generator). qmm_matmul: activation quantization to Q8_K planes +
+    the int8-MFMA GEMM. MFMA utilisation = 2*M*N*K / time / dense int8 peak."""
+    from inference_amd import GgmlDType, QTensor, qmm
+    from inference_amd.synth import normal
+    L = qmm.lib()
+    m = 512
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    out = {}
+    for name, n, k in (("gate_up_shape", 14336, 4096), ("down_shape", 4096, 14336)):
+        qt = QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
+        x = torch.from_numpy(normal(5, (m, k))).to(dev)
+        y = torch.empty((m, n), dtype=torch.float32, device=dev)
+        wsb = int(L.qmm_matmul_workspace_size(qt.handle, m))
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+
+        def fn(qt=qt, x=x, y=y, ws=ws, wsb=wsb, n=n, k=k):
+            qmm._check(L.qmm_matmul(qt.handle, x.data_ptr(), m, k, y.data_ptr(), n, ws.data_ptr(), wsb,
+                                    qmm._stream(dev)))
+        us = timed_graph(torch, fn, 10, 4)
+        tops = 2.0 * m * n * k / us / 1e6
+        out[name] = {"m_n_k": [m, n, k], "us": round(us, 2), "TOPS": round(tops, 1),
+                     "mfma_util": round(tops / INT8_PEAK_TOPS, 4)}
+        del qt
+    return out
+
+
+def run_moe(torch, dev):
+    """Config 5: 8 experts (Q4_K gate/up 14336x4096, Q6_K down 4096x14336, N(0, 0.02^2) seed 7 on the
+    device generator), 8 tokens N(0,1), router logits N(0,1) seed 8, top-2. One qmm_moe_ffn call:
+    routing, gathered Q8_K activations, expert GEMVs streaming each active expert once, SiLU*mul, combine."""
+    from inference_amd import GgmlDType, QTensor, qmm
+    from inference_amd.synth import normal
+    L = qmm.lib()
+    E, H, F, T, k = 8, 4096, 14336, 8, 2
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    gate = QTensor.quantize(torch.randn((E * F, H), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
+    up = QTensor.quantize(torch.randn((E * F, H), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
+    down = QTensor.quantize(torch.randn((E * H, F), generator=g, device=dev) * 0.02, GgmlDType.Q6K)
+    x = torch.from_numpy(normal(7, (T, H))).to(dev)
+    logits_np = normal(8, (T, E))
+    logits = torch.from_numpy(logits_np).to(dev)
+    y = torch.empty((T, H), dtype=torch.float32, device=dev)
+    wsb = int(L.qmm_moe_ffn_workspace_size(gate.handle, down.handle, T, E, k))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+
+    def fn():
+        qmm._check(L.qmm_moe_ffn(x.data_ptr(), T, H, logits.data_ptr(), E, k, gate.handle, up.handle, down.handle,
+                                 y.data_ptr(), H, ws.data_ptr(), wsb, qmm._stream(dev)))
+    us = timed_graph(torch, fn, 10, 4)
+    # active experts: those in some token's top-k
+    active = set()
+    for row in logits_np:
+        active.update(np.argsort(-row, kind="stable")[:k].tolist())
+    per_expert = F * (H // 256) * 144 * 2 + H * (F // 256) * 210
+    wbytes = per_expert * len(active)
+    return {"us": round(us, 2), "active_experts": len(active), "weight_bytes": wbytes,
+            "GB/s": round(wbytes / us / 1e3, 1), "hbm_frac": round(wbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "tokens": T, "topk": k}
+
+
 def cpu_baseline(sets, budget_s):
     """Oracle restatement of Candle's CPU quantized matmul over the same GEMV set."""
     from oracle import oracle as orc
@@ -282,6 +376,47 @@ def cpu_baseline(sets, budget_s):
                       f"vec_dot, {threads} OpenMP threads, {el:.1f} s"}
 
 
+def kernel_only(torch, dev, which, launches):
+    """Launch one kernel `launches` times, eagerly (every dispatch visible to a counter run):
+    `gate` = the Q4_K gate GEMV (14336x4096, M = 1, rotated weight copies), `copy` = a 256 MiB
+    device copy (the calibration for FETCH_SIZE / WRITE_SIZE)."""
+    from inference_amd import GgmlDType, QTensor, qmm
+    if which == "copy":
+        a = torch.ones(64 * 2 ** 20, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(launches):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel_only": "copy", "bytes_read": a.numel() * 4, "bytes_written": b.numel() * 4,
+                          "launches": launches}), flush=True)
+        return
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    ws = [QTensor.quantize(torch.randn((14336, 4096), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
+          for _ in range(8)]
+    L = qmm.lib()
+    xq = torch.zeros(16 * 292, dtype=torch.uint8, device=dev)
+    x = torch.randn(4096, device=dev)
+    qmm._check(L.qmm_quantize_rows(15, x.data_ptr(), 1, 4096, 4096, xq.data_ptr(), qmm._stream(dev)))
+    y = torch.empty(14336, dtype=torch.float32, device=dev)
+    for i in range(launches):
+        qmm._check(L.qmm_matmul_q(ws[i % 8].handle, xq.data_ptr(), 1, y.data_ptr(), 14336, qmm._stream(dev)))
+    torch.cuda.synchronize()
+    print(json.dumps({"kernel_only": "gate", "algorithmic_bytes": gemv_bytes(12, 14336, 4096),
+                      "launches": launches}), flush=True)
+
+
+def traffic_from_profile():
+    """HBM bytes per gate-GEMV launch from the committed counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", "gemv_q4k_gate_pmc.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        return int(d["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -292,6 +427,8 @@ def main():
     ap.add_argument("--schedule", choices=("concurrent", "serial"), default="serial",
                     help="run the set's independent GEMVs one after another or on 4 streams")
     ap.add_argument("--decode-tokens", type=int, default=256, help="config-3 generated tokens (0 = skip)")
+    ap.add_argument("--kernel-only", choices=("gate", "copy"), default=None,
+                    help="launch only the gate GEMV or a calibration copy --steps times (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -301,11 +438,20 @@ def main():
     import torch
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.kernel_only:
+        kernel_only(torch, dev, args.kernel_only, args.steps)
+        return
     res, sets = run_gemv_set(torch, dev, args)
     cpu = cpu_baseline(sets, args.cpu_seconds) if args.cpu_seconds > 0 else None
     del sets
     torch.cuda.empty_cache()
     dec = run_decode(torch, dev, args) if args.decode_tokens > 0 else None
+    torch.cuda.empty_cache()
+    log("[bench] prefill GEMM (config 4)")
+    pre = run_prefill(torch, dev)
+    torch.cuda.empty_cache()
+    log("[bench] MoE expert FFN (config 5)")
+    moe = run_moe(torch, dev)
     line = {
         "metric": METRIC,
         "value": round(res["value"], 1),
@@ -327,6 +473,8 @@ def main():
         "per_shape": res["per_shape"],
         "decode_tok_s": dec["tok_s"] if dec else None,
         "decode": dec,
+        "prefill_gemm": pre,
+        "moe_ffn": moe,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
