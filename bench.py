@@ -29,6 +29,7 @@ peak) and config 5 (MoE expert FFN, weight GB/s of the active experts).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -81,6 +82,9 @@ def build_set(torch, dev, dt, copies):
     return sets
 
 
+QKVGU = ("q_proj", "k_proj", "v_proj", "gate_proj", "up_proj")  # the K = 4096 projections
+
+
 def run_gemv_set(torch, dev, args):
     from inference_amd import GgmlDType, qmm
     from inference_amd.synth import normal
@@ -99,6 +103,7 @@ def run_gemv_set(torch, dev, args):
     xq14336 = torch.empty((1, 56 * 292), dtype=torch.uint8, device=dev)
     outs = {name: torch.empty((1, n), dtype=torch.float32, device=dev) for name, n, _ in GEMV_SET}
     L = qmm.lib()
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
 
     def q8k(x, xq, k):
         qmm._check(L.qmm_quantize_rows(int(vt), x.data_ptr(), 1, k, k, xq.data_ptr(), qmm._stream(dev)))
@@ -108,41 +113,50 @@ def run_gemv_set(torch, dev, args):
         xq = xq4096 if k == 4096 else xq14336
         qmm._check(L.qmm_matmul_q(layer[name].handle, xq.data_ptr(), 1, outs[name].data_ptr(), n, qmm._stream(dev)))
 
+    # job tables of the one-launch schedules (handles per weight copy)
+    hs5 = [(vp * 5)(*[layer[nm].handle.value for nm in QKVGU]) for layer in sets]
+    y5 = (vp * 5)(*[outs[nm].data_ptr() for nm in QKVGU])
+    ld5 = (i64 * 5)(*[shapes[nm][0] for nm in QKVGU])
+    hsd = [(vp * 1)(layer["down_proj"].handle.value) for layer in sets]
+    yd = (vp * 1)(outs["down_proj"].data_ptr())
+    ldd = (i64 * 1)(4096)
+    cidx = {id(layer): c for c, layer in enumerate(sets)}
+
+    def qkvgu(layer, fused):
+        c = cidx[id(layer)]
+        if fused:
+            qmm._check(L.qmm_matmul_ex(hs5[c], 5, x4096.data_ptr(), 1, 4096, None, ctypes.c_float(0), 0, y5, ld5,
+                                       None, 0, qmm._stream(dev)))
+        else:
+            qmm._check(L.qmm_matmul_multi_q(hs5[c], 5, xq4096.data_ptr(), 1, y5, ld5, qmm._stream(dev)))
+
+    def down_fused(layer):
+        c = cidx[id(layer)]
+        qmm._check(L.qmm_matmul_ex(hsd[c], 1, x14336.data_ptr(), 1, 14336, None, ctypes.c_float(0), 0, yd, ldd,
+                                   None, 0, qmm._stream(dev)))
+
     def step_serial(layer):
         q8k(x4096, xq4096, 4096)
-        for name in ("q_proj", "k_proj", "v_proj", "gate_proj", "up_proj"):
+        for name in QKVGU:
             gemv(layer, name)
         q8k(x14336, xq14336, 14336)
         gemv(layer, "down_proj")
 
-    # The six GEMVs of the set are independent given their activations, so a
-    # step can also run them on four streams (fork/join inside the graph), the
-    # way a decode layer overlaps q/k/v and gate/up.
-    side = [torch.cuda.Stream(device=dev) for _ in range(3)]
-    branches = [("q_proj", "k_proj"), ("v_proj", "gate_proj"), ("up_proj",), ("down_proj",)]
-
-    def step_concurrent(layer):
-        main = torch.cuda.current_stream(dev)
+    def step_staged(layer):
         q8k(x4096, xq4096, 4096)
+        qkvgu(layer, False)
         q8k(x14336, xq14336, 14336)
-        for sb in side:
-            sb.wait_stream(main)
-        for br, st in zip(branches, [main] + side):
-            with torch.cuda.stream(st):
-                for name in br:
-                    gemv(layer, name)
-        for sb in side:
-            main.wait_stream(sb)
+        gemv(layer, "down_proj")
 
-    step = step_concurrent if args.schedule == "concurrent" else step_serial
+    def step_fused(layer):
+        qkvgu(layer, True)
+        down_fused(layer)
 
-    def gate_only(layer):
-        s = qmm._stream(dev)
-        qmm._check(L.qmm_matmul_q(layer["gate_proj"].handle, xq4096.data_ptr(), 1, outs["gate_proj"].data_ptr(),
-                                  14336, s))
+    step = {"serial": step_serial, "staged": step_staged, "fused": step_fused}[args.schedule]
 
     # warm up eagerly (module load, kernel lookup), then capture graphs
     for c in range(copies):
+        step_serial(sets[c])
         step(sets[c])
     torch.cuda.synchronize()
 
@@ -169,51 +183,48 @@ def run_gemv_set(torch, dev, args):
     step_bytes = sum(gemv_bytes(dt, n, k) for _, n, k in GEMV_SET)
     value = step_bytes * steps / elapsed / 1e9
 
-    # dominant kernel alone: gate/up GEMV, HIP events on the capture/replay stream
-    g_gate = capture(gate_only, per_graph)
-    g_gate.replay()
-    torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    gate_reps = max(4, args.steps // per_graph)
-    e0.record(stream)
-    for _ in range(gate_reps):
-        g_gate.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    gate_us = e0.elapsed_time(e1) * 1e3 / (gate_reps * per_graph)
-    gate_bytes = gemv_bytes(dt, 14336, 4096)
-    achieved = gate_bytes / (gate_us * 1e-6) / 1e9
+    timing_reps = max(4, args.steps // per_graph)
 
-    # per-shape figures (same method)
-    per_shape = {}
-    for name, n, k in GEMV_SET:
-        xq = xq4096 if k == 4096 else xq14336
-        y = outs[name]
-
-        def one(layer, name=name, n=n, xq=xq, y=y):
-            qmm._check(L.qmm_matmul_q(layer[name].handle, xq.data_ptr(), 1, y.data_ptr(), n, qmm._stream(dev)))
-        g = capture(one, per_graph)
+    def time_launch(fn):
+        """Average us of fn(layer) alone: graph replays over the rotated copies, HIP events on its stream."""
+        g = capture(fn, per_graph)
         g.replay()
         torch.cuda.synchronize()
         e0.record(stream)
-        for _ in range(gate_reps):
+        for _ in range(timing_reps):
             g.replay()
         e1.record(stream)
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (gate_reps * per_graph)
+        return e0.elapsed_time(e1) * 1e3 / (timing_reps * per_graph)
+
+    # per-shape single launches (pre-quantized activation)
+    per_shape = {}
+    for name, n, k in GEMV_SET:
+        us = time_launch(lambda layer, name=name: gemv(layer, name))
         b = gemv_bytes(dt, n, k)
         per_shape[name] = {"shape": [n, k], "us": round(us, 3), "GB/s": round(b / us / 1e3, 1),
                            "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
 
+    # dominant launch of the step
+    if args.schedule == "serial":
+        kernel, rb = "qmm_gemv_q4k_m1_w4_r1_u1 (gate_proj 14336x4096, one launch)", gemv_bytes(dt, 14336, 4096)
+        rus = per_shape["gate_proj"]["us"]
+    else:
+        fused = args.schedule == "fused"
+        rus = time_launch(lambda layer: qkvgu(layer, fused))
+        rb = sum(gemv_bytes(dt, *shapes[nm]) for nm in QKVGU) - 4 * 4096 * (len(QKVGU) - 1)  # x read once
+        kernel = ("qmm_gemvf_q4k_m1_w16_r1_u1_j8" if fused else "qmm_gemv_q4k_m1_w4_r1_u1_j8") + \
+            " (q, k, v, gate, up: 5 weights, one launch" + (", Q8_K in the prologue)" if fused else ")")
+    achieved = rb / (rus * 1e-6) / 1e9
     result = {
         "value": value,
         "ms_per_step": elapsed / steps * 1e3,
         "steps": steps,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
-                     "kernel": "qmm_gemv_q4k_m1_w4_r1_u1 (gate_proj 14336x4096)", "avg_us": round(gate_us, 3),
-                     "algorithmic_bytes": gate_bytes},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(args.schedule),
+                     "kernel": kernel, "avg_us": round(rus, 3), "algorithmic_bytes": rb},
         "per_shape": per_shape,
         "weight_copies": copies,
     }
@@ -378,8 +389,9 @@ def cpu_baseline(sets, budget_s):
 
 def kernel_only(torch, dev, which, launches):
     """Launch one kernel `launches` times, eagerly (every dispatch visible to a counter run):
-    `gate` = the Q4_K gate GEMV (14336x4096, M = 1, rotated weight copies), `copy` = a 256 MiB
-    device copy (the calibration for FETCH_SIZE / WRITE_SIZE)."""
+    `gate` = the Q4_K gate GEMV (14336x4096, M = 1, rotated weight copies); `qkvgu` / `qkvgu_staged`
+    = the q/k/v/gate/up set in one launch (Q8_K in the prologue / pre-quantized activation);
+    `copy` = a 256 MiB device copy (the calibration for FETCH_SIZE / WRITE_SIZE)."""
     from inference_amd import GgmlDType, QTensor, qmm
     if which == "copy":
         a = torch.ones(64 * 2 ** 20, dtype=torch.float32, device=dev)
@@ -392,23 +404,45 @@ def kernel_only(torch, dev, which, launches):
         return
     g = torch.Generator(device=dev)
     g.manual_seed(2)
-    ws = [QTensor.quantize(torch.randn((14336, 4096), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
-          for _ in range(8)]
     L = qmm.lib()
-    xq = torch.zeros(16 * 292, dtype=torch.uint8, device=dev)
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
     x = torch.randn(4096, device=dev)
+    xq = torch.zeros(16 * 292, dtype=torch.uint8, device=dev)
     qmm._check(L.qmm_quantize_rows(15, x.data_ptr(), 1, 4096, 4096, xq.data_ptr(), qmm._stream(dev)))
-    y = torch.empty(14336, dtype=torch.float32, device=dev)
-    for i in range(launches):
-        qmm._check(L.qmm_matmul_q(ws[i % 8].handle, xq.data_ptr(), 1, y.data_ptr(), 14336, qmm._stream(dev)))
+    if which == "gate":
+        ws = [QTensor.quantize(torch.randn((14336, 4096), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
+              for _ in range(8)]
+        y = torch.empty(14336, dtype=torch.float32, device=dev)
+        for i in range(launches):
+            qmm._check(L.qmm_matmul_q(ws[i % 8].handle, xq.data_ptr(), 1, y.data_ptr(), 14336, qmm._stream(dev)))
+        alg = gemv_bytes(12, 14336, 4096)
+    else:
+        names = [nm for nm, _, _ in GEMV_SET if nm != "down_proj"]
+        shp = {nm: (n, k) for nm, n, k in GEMV_SET}
+        copies = [[QTensor.quantize(torch.randn(shp[nm], generator=g, device=dev) * 0.02, GgmlDType.Q4K)
+                   for nm in names] for _ in range(6)]
+        hs = [(vp * 5)(*[t.handle.value for t in c]) for c in copies]
+        ys = [torch.empty(shp[nm][0], dtype=torch.float32, device=dev) for nm in names]
+        yp = (vp * 5)(*[y.data_ptr() for y in ys])
+        ld = (i64 * 5)(*[shp[nm][0] for nm in names])
+        for i in range(launches):
+            if which == "qkvgu":
+                qmm._check(L.qmm_matmul_ex(hs[i % 6], 5, x.data_ptr(), 1, 4096, None, ctypes.c_float(0), 0, yp, ld,
+                                           None, 0, qmm._stream(dev)))
+            else:
+                qmm._check(L.qmm_matmul_multi_q(hs[i % 6], 5, xq.data_ptr(), 1, yp, ld, qmm._stream(dev)))
+        alg = sum(gemv_bytes(12, *shp[nm]) for nm in names) - 4 * 4096 * (len(names) - 1)
     torch.cuda.synchronize()
-    print(json.dumps({"kernel_only": "gate", "algorithmic_bytes": gemv_bytes(12, 14336, 4096),
-                      "launches": launches}), flush=True)
+    print(json.dumps({"kernel_only": which, "algorithmic_bytes": alg, "launches": launches}), flush=True)
 
 
-def traffic_from_profile():
-    """HBM bytes per gate-GEMV launch from the committed counter summary, or None."""
-    path = os.path.join(ROOT, "profiles", "gemv_q4k_gate_pmc.json")
+PMC_PROFILES = {"serial": "gemv_q4k_gate_pmc.json", "staged": "gemv_q4k_qkvgu_staged_pmc.json",
+                "fused": "gemv_q4k_qkvgu_fused_pmc.json"}
+
+
+def traffic_from_profile(schedule):
+    """HBM bytes per launch of the schedule's roofline kernel from the committed counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", PMC_PROFILES[schedule])
     try:
         with open(path) as f:
             d = json.load(f)
@@ -424,11 +458,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=24)
     ap.add_argument("--rotate-mb", type=int, default=640, help="distinct weight bytes rotated (MiB)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 = skip)")
-    ap.add_argument("--schedule", choices=("concurrent", "serial"), default="serial",
-                    help="run the set's independent GEMVs one after another or on 4 streams")
+    ap.add_argument("--schedule", choices=("fused", "staged", "serial"), default="staged",
+                    help="staged: quantize x (Q8_K), q/k/v/gate/up in one launch, quantize, down; fused: the "
+                         "same two GEMV launches with Q8_K quantization in their prologues; serial: one launch "
+                         "per projection")
     ap.add_argument("--decode-tokens", type=int, default=256, help="config-3 generated tokens (0 = skip)")
-    ap.add_argument("--kernel-only", choices=("gate", "copy"), default=None,
-                    help="launch only the gate GEMV or a calibration copy --steps times (counter runs)")
+    ap.add_argument("--kernel-only", choices=("gate", "qkvgu", "qkvgu_staged", "copy"), default=None,
+                    help="launch only one GEMV launch kind or a calibration copy --steps times (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "

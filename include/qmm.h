@@ -118,8 +118,8 @@ size_t qmm_matmul_workspace_size(const qmm_qtensor *w, int64_t m);
 int qmm_matmul(const qmm_qtensor *w, const float *x, int64_t m, int64_t ldx, float *y, int64_t ldy,
                void *ws, size_t ws_bytes, void *stream);
 
-/* `count` (1..4) QMatMul::forward calls on one input in a single launch:
- * y[j] = x . W[j]^T for weights of one dtype and k (e.g. a layer's q/k or
+/* `count` (1..8) QMatMul::forward calls on one input in a single launch:
+ * y[j] = x . W[j]^T for weights of one dtype and k (e.g. a layer's q/k/v and
  * gate/up projections, which the reference engine runs as separate
  * QuantizedLinear::forward calls on the same activation, llama.rs:1066-1092,
  * 1386-1391). ldy[j] is the row stride of y[j]; ws as for qmm_matmul. */
@@ -131,6 +131,12 @@ int qmm_matmul_multi(const qmm_qtensor *const *w, int count, const float *x, int
  * GEMM in a scratch buffer the library keeps per device (calls on one device
  * must then be ordered on one stream). */
 int qmm_matmul_q(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy, void *stream);
+
+/* qmm_matmul_multi with activations already quantized (xq as for
+ * qmm_matmul_q): `count` (1..8) weights of one dtype and k in one launch for
+ * m <= 8 (one GEMM per weight for larger m). */
+int qmm_matmul_multi_q(const qmm_qtensor *const *w, int count, const void *xq, int64_t m, float *const *y,
+                       const int64_t *ldy, void *stream);
 
 /* qmm_matmul_q with an optional residual add (accumulate != 0: y += result;
  * then m <= 8). */
@@ -148,7 +154,7 @@ int qmm_matmul_q_ex(const qmm_qtensor *w, const void *xq, int64_t m, float *y, i
 int qmm_block_dots(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy,
                    int32_t *dots, void *stream);
 
-/* QMatMul::forward for 1..4 weights (same dtype and k) on one input, with the
+/* QMatMul::forward for 1..8 weights (same dtype and k) on one input, with the
  * decoder's neighbouring ops folded in: when norm_weight is non-NULL the input
  * rows are first RMS-normalised, x / sqrt(mean(x^2) + eps) * norm_weight
  * (rms_norm, crates/llm/candle-llm/src/primitives/nn.rs:22-31; fused into the

@@ -274,15 +274,17 @@ __device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t*
   }
 }
 
-// Up to four weight matrices (same format and K) that share one activation;
+// Up to kMaxJobs weight matrices (same format and K) that share one activation;
 // rows of job j are global rows [sum_{i<j} rows[i], sum_{i<=j} rows[i]).
+constexpr int kMaxJobs = 8;
+
 struct GemvJobs {
-  const uint8_t* wq[4];  // device-layout blocks of each matrix
-  float* y[4];           // outputs, y[j][m * ldy[j] + row]
-  int rows[4];           // rows computed for job j
-  int ldy[4];
-  int row0[4];           // first row of job j within its tensor (stacked experts)
-  int trows[4];          // rows of the whole tensor (its f16 scales follow all of them)
+  const uint8_t* wq[kMaxJobs];  // device-layout blocks of each matrix
+  float* y[kMaxJobs];           // outputs, y[j][m * ldy[j] + row]
+  int rows[kMaxJobs];           // rows computed for job j
+  int ldy[kMaxJobs];
+  int row0[kMaxJobs];           // first row of job j within its tensor (stacked experts)
+  int trows[kMaxJobs];          // rows of the whole tensor (its f16 scales follow all of them)
   int njobs;
   int total;
 };
@@ -293,45 +295,33 @@ struct RowRef {
   const uint16_t* wd;
   float* y;
   int ldy;
-  int out;   // output row within the job
-  int row;   // row within the weight tensor
-  int rows;  // rows of the job
+  int out;   // output row within its job
+  int row;   // row within its tensor
+  int rows;
   bool ok;
 };
 
-// `gr` is wave-uniform, so the job lookup compiles to scalar selects.
-template <int FMT>
+// Global row gr -> (job, row). Jobs are laid out back to back in job order.
+// `gr` is wave-uniform and every job index below is a constant, so the lookup
+// compiles to a chain of scalar selects (no indexed access into the table).
+// J is the kernel's job capacity (its launch arguments carry J jobs).
+template <int FMT, int J>
 __device__ __forceinline__ RowRef locate(const GemvJobs& jobs, int gr, int nb) {
   RowRef r;
   int base = 0;
   const uint8_t* wq = jobs.wq[0];
   float* y = jobs.y[0];
   int rows = jobs.rows[0], ldy = jobs.ldy[0], row0 = jobs.row0[0], trows = jobs.trows[0];
-  if (jobs.njobs > 1 && gr >= rows) {
-    base = rows;
-    wq = jobs.wq[1];
-    y = jobs.y[1];
-    rows = jobs.rows[1];
-    ldy = jobs.ldy[1];
-    row0 = jobs.row0[1];
-    trows = jobs.trows[1];
-    if (jobs.njobs > 2 && gr >= base + rows) {
+#pragma unroll
+  for (int j = 1; j < J; ++j) {
+    if (j < jobs.njobs && gr >= base + rows) {
       base += rows;
-      wq = jobs.wq[2];
-      y = jobs.y[2];
-      rows = jobs.rows[2];
-      ldy = jobs.ldy[2];
-      row0 = jobs.row0[2];
-      trows = jobs.trows[2];
-      if (jobs.njobs > 3 && gr >= base + rows) {
-        base += rows;
-        wq = jobs.wq[3];
-        y = jobs.y[3];
-        rows = jobs.rows[3];
-        ldy = jobs.ldy[3];
-        row0 = jobs.row0[3];
-        trows = jobs.trows[3];
-      }
+      wq = jobs.wq[j];
+      y = jobs.y[j];
+      rows = jobs.rows[j];
+      ldy = jobs.ldy[j];
+      row0 = jobs.row0[j];
+      trows = jobs.trows[j];
     }
   }
   r.wq = wq;
@@ -488,7 +478,7 @@ __device__ __forceinline__ void quantize_act(const float* __restrict__ x, long l
 //   dump (optional, single job): int32 block dots [M][rows][nb](x2 for Q4_K).
 // With `accumulate`, outputs are added to y (y += result); norm_w (fused only)
 // RMS-normalises the activation rows before quantization.
-template <int FMT, int M, int R, int U, bool FUSED>
+template <int FMT, int M, int R, int U, bool FUSED, int J = 4>
 __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restrict__ act, long long ldx, int K,
                                      int* __restrict__ dump, int mrows = M,
                                      const float* __restrict__ norm_w = nullptr, float eps = 0.0f,
@@ -509,7 +499,7 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
   // First weight batch in flight before the activation is staged.
   RowRef rr[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) rr[r] = locate<FMT>(jobs, row0 + r, nb);
+  for (int r = 0; r < R; ++r) rr[r] = locate<FMT, J>(jobs, row0 + r, nb);
   WSlice ws[R][U];
   load_batch<FMT, R, U>(ws, rr, 0, nb, g, l);
   if constexpr (FUSED)
@@ -562,7 +552,7 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       cur[r] = rr[r];
-      rr[r] = locate<FMT>(jobs, row0 + row_step + r, nb);
+      rr[r] = locate<FMT, J>(jobs, row0 + row_step + r, nb);
     }
     if (row0 + row_step < jobs.total) load_batch<FMT, R, U>(ws, rr, 0, nb, g, l);
 #pragma unroll
@@ -583,40 +573,37 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
 
 // Kernel arguments: the job table as plain scalars (a by-value struct would be
 // copied to scratch), then the activation, its row stride, K and the dump.
-#define QMM_GEMV_PARAMS                                                                                   \
-  const uint8_t *wq0, const uint8_t *wq1, const uint8_t *wq2, const uint8_t *wq3, float *y0, float *y1,   \
-      float *y2, float *y3, int rows0, int rows1, int rows2, int rows3, int ldy0, int ldy1, int ldy2,     \
-      int ldy3, int row00, int row01, int row02, int row03, int trows0, int trows1, int trows2,           \
-      int trows3, int njobs, int total, const void *__restrict__ act, long long ldx, int K,               \
-      int *__restrict__ dump, const float *__restrict__ norm_w, float eps, int accumulate
-#define QMM_GEMV_JOBS                                                                                     \
-  qmm::GemvJobs jobs;                                                                                     \
-  jobs.wq[0] = wq0;                                                                                       \
-  jobs.wq[1] = wq1;                                                                                       \
-  jobs.wq[2] = wq2;                                                                                       \
-  jobs.wq[3] = wq3;                                                                                       \
-  jobs.y[0] = y0;                                                                                         \
-  jobs.y[1] = y1;                                                                                         \
-  jobs.y[2] = y2;                                                                                         \
-  jobs.y[3] = y3;                                                                                         \
-  jobs.rows[0] = rows0;                                                                                   \
-  jobs.rows[1] = rows1;                                                                                   \
-  jobs.rows[2] = rows2;                                                                                   \
-  jobs.rows[3] = rows3;                                                                                   \
-  jobs.ldy[0] = ldy0;                                                                                     \
-  jobs.ldy[1] = ldy1;                                                                                     \
-  jobs.ldy[2] = ldy2;                                                                                     \
-  jobs.ldy[3] = ldy3;                                                                                     \
-  jobs.row0[0] = row00;                                                                                   \
-  jobs.row0[1] = row01;                                                                                   \
-  jobs.row0[2] = row02;                                                                                   \
-  jobs.row0[3] = row03;                                                                                   \
-  jobs.trows[0] = trows0;                                                                                 \
-  jobs.trows[1] = trows1;                                                                                 \
-  jobs.trows[2] = trows2;                                                                                 \
-  jobs.trows[3] = trows3;                                                                                 \
-  jobs.njobs = njobs;                                                                                     \
+#define QMM_JOB_PARAMS(i) \
+  const uint8_t *wq##i, float *y##i, int rows##i, int ldy##i, int row0##i, int trows##i
+#define QMM_GEMV_TAIL_PARAMS                                                                  \
+  int njobs, int total, const void *__restrict__ act, long long ldx, int K, int *__restrict__ dump, \
+      const float *__restrict__ norm_w, float eps, int accumulate
+#define QMM_GEMV_PARAMS \
+  QMM_JOB_PARAMS(0), QMM_JOB_PARAMS(1), QMM_JOB_PARAMS(2), QMM_JOB_PARAMS(3), QMM_GEMV_TAIL_PARAMS
+#define QMM_GEMV_PARAMS8                                                                              \
+  QMM_JOB_PARAMS(0), QMM_JOB_PARAMS(1), QMM_JOB_PARAMS(2), QMM_JOB_PARAMS(3), QMM_JOB_PARAMS(4),    \
+      QMM_JOB_PARAMS(5), QMM_JOB_PARAMS(6), QMM_JOB_PARAMS(7), QMM_GEMV_TAIL_PARAMS
+#define QMM_JOB_SET(i)   \
+  jobs.wq[i] = wq##i;    \
+  jobs.y[i] = y##i;      \
+  jobs.rows[i] = rows##i; \
+  jobs.ldy[i] = ldy##i;  \
+  jobs.row0[i] = row0##i; \
+  jobs.trows[i] = trows##i;
+#define QMM_GEMV_JOBS \
+  qmm::GemvJobs jobs; \
+  QMM_JOB_SET(0)      \
+  QMM_JOB_SET(1)      \
+  QMM_JOB_SET(2)      \
+  QMM_JOB_SET(3)      \
+  jobs.njobs = njobs; \
   jobs.total = total;
+#define QMM_GEMV_JOBS8 \
+  QMM_GEMV_JOBS        \
+  QMM_JOB_SET(4)       \
+  QMM_JOB_SET(5)       \
+  QMM_JOB_SET(6)       \
+  QMM_JOB_SET(7)
 
 #define QMM_GEMV_KERNEL(FMT, NAME, M, W, R, U)                                                            \
   extern "C" __global__ void __launch_bounds__(64 * W)                                                    \
@@ -630,6 +617,23 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
       qmm_gemvf_##NAME##_m##M##_w##W##_r##R##_u##U(QMM_GEMV_PARAMS) {                                     \
     QMM_GEMV_JOBS                                                                                         \
     qmm::gemv<FMT, M, R, U, true>(jobs, act, ldx, K, dump, M, norm_w, eps, accumulate);                  \
+  }
+
+// Eight-job variants (M = 1 only): one launch over up to eight weights that
+// share the activation (e.g. a layer's q, k, v, gate and up). The longer
+// argument list costs scalar registers, so four-job launches keep their own
+// kernels.
+#define QMM_GEMV_KERNEL8(FMT, NAME, W, R, U)                                                           \
+  extern "C" __global__ void __launch_bounds__(64 * W)                                                 \
+      qmm_gemv_##NAME##_m1_w##W##_r##R##_u##U##_j8(QMM_GEMV_PARAMS8) {                                 \
+    QMM_GEMV_JOBS8                                                                                     \
+    qmm::gemv<FMT, 1, R, U, false, 8>(jobs, act, ldx, K, dump, 1, nullptr, 0.0f, accumulate);          \
+  }
+#define QMM_GEMVF_KERNEL8(FMT, NAME, W, R, U)                                                          \
+  extern "C" __global__ void __launch_bounds__(64 * W)                                                 \
+      qmm_gemvf_##NAME##_m1_w##W##_r##R##_u##U##_j8(QMM_GEMV_PARAMS8) {                                \
+    QMM_GEMV_JOBS8                                                                                     \
+    qmm::gemv<FMT, 1, R, U, true, 8>(jobs, act, ldx, K, dump, 1, norm_w, eps, accumulate);             \
   }
 
 // Launch shapes: W waves per workgroup, R rows per wave, U load iterations per batch.
@@ -653,11 +657,23 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
 #define QMM_GEMVF_SHAPES(FMT, NAME, M)      \
   QMM_GEMVF_KERNEL(FMT, NAME, M, 8, 1, 1)   \
   QMM_GEMVF_KERNEL(FMT, NAME, M, 8, 1, 2)   \
+  QMM_GEMVF_KERNEL(FMT, NAME, M, 8, 2, 1)   \
   QMM_GEMVF_KERNEL(FMT, NAME, M, 16, 1, 1)  \
-  QMM_GEMVF_KERNEL(FMT, NAME, M, 16, 1, 2)
+  QMM_GEMVF_KERNEL(FMT, NAME, M, 16, 1, 2)  \
+  QMM_GEMVF_KERNEL(FMT, NAME, M, 16, 2, 1)
 
 #define QMM_GEMV_ALL_M(FMT, NAME) \
   QMM_GEMV_SHAPES_1(FMT, NAME)    \
+  QMM_GEMV_KERNEL8(FMT, NAME, 4, 1, 1)  \
+  QMM_GEMV_KERNEL8(FMT, NAME, 4, 2, 1)  \
+  QMM_GEMV_KERNEL8(FMT, NAME, 8, 1, 1)  \
+  QMM_GEMV_KERNEL8(FMT, NAME, 8, 2, 1)  \
+  QMM_GEMV_KERNEL8(FMT, NAME, 16, 1, 1) \
+  QMM_GEMV_KERNEL8(FMT, NAME, 16, 2, 1) \
+  QMM_GEMVF_KERNEL8(FMT, NAME, 8, 1, 1) \
+  QMM_GEMVF_KERNEL8(FMT, NAME, 8, 2, 1) \
+  QMM_GEMVF_KERNEL8(FMT, NAME, 16, 1, 1) \
+  QMM_GEMVF_KERNEL8(FMT, NAME, 16, 2, 1) \
   QMM_GEMV_SHAPES(FMT, NAME, 2)   \
   QMM_GEMV_SHAPES(FMT, NAME, 3)   \
   QMM_GEMV_SHAPES(FMT, NAME, 4)   \

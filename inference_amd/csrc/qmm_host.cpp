@@ -445,13 +445,15 @@ size_t qmm_matmul_workspace_size(const qmm_qtensor* w, int64_t m) {
 }
 
 // Job table of one GEMV launch (passed to the kernel as scalar arguments).
+constexpr int kMaxJobs = 8;  // the kernels' qmm::kMaxJobs
+
 struct GemvJobs {
-  const void* wq[4];
-  float* y[4];
-  int rows[4];
-  int ldy[4];
-  int row0[4];
-  int trows[4];
+  const void* wq[kMaxJobs];
+  float* y[kMaxJobs];
+  int rows[kMaxJobs];
+  int ldy[kMaxJobs];
+  int row0[kMaxJobs];
+  int trows[kMaxJobs];
   int njobs;
   int total;
 };
@@ -462,11 +464,15 @@ struct GemvTarget {
   int64_t ldy;
 };
 
-// GEMV launch for m <= 8 activation rows over up to four weights (same dtype
+// GEMV launch for m <= 8 activation rows over up to kMaxJobs weights (same dtype
 // and k) sharing one activation. `act` is m rows of quantized blocks, or f32
 // rows with stride ldx when `fused` (then the kernel quantizes in its prologue).
 static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, bool fused, int64_t ldx, int m,
                 int* dump, hipStream_t s, const float* norm_w = nullptr, float eps = 0.0f, int accumulate = 0) {
+  if (count > 4 && m != 1) {  // eight-job kernels exist for m == 1 only: two launches
+    QMM_TRY(gemv(d, tg, 4, act, fused, ldx, m, dump, s, norm_w, eps, accumulate));
+    return gemv(d, tg + 4, count - 4, act, fused, ldx, m, dump, s, norm_w, eps, accumulate);
+  }
   const qmm_qtensor* w = tg[0].w;
   const int fmt = fmt_of(w->dtype);
   const int nb = (int)(w->k / qmm_block_size(w->dtype));
@@ -515,8 +521,16 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   const Tuning tu = tuning();
   if (tu.w > 0 && tu.r > 0 && tu.u > 0) { wv = tu.w; r = tu.r; u = tu.u; }
   if (tu.waves_per_cu > 0) waves_per_cu = tu.waves_per_cu;
+  // more than four weights: the eight-job kernels (M = 1; r = u = 1 shapes)
+  const int jcap = count > 4 ? kMaxJobs : 4;
+  if (jcap > 4) {  // instantiated: staged w4/w8/w16, fused w8/w16; r 1..2, u 1
+    u = 1;
+    if (r > 2) r = 2;
+    if (fused && wv < 8) wv = 8;
+  }
   char name[80];
-  snprintf(name, sizeof(name), "qmm_gemv%s_%s_m%d_w%d_r%d_u%d", fused ? "f" : "", fmt_name(fmt), m, wv, r, u);
+  snprintf(name, sizeof(name), "qmm_gemv%s_%s_m%d_w%d_r%d_u%d%s", fused ? "f" : "", fmt_name(fmt), m, wv, r, u,
+           jcap > 4 ? "_j8" : "");
   long long wgs = (total + wv * r - 1) / (wv * r);
   const long long cap = ((long long)d->num_cu * waves_per_cu + wv - 1) / wv;
   if (wgs > cap) wgs = cap;
@@ -524,12 +538,25 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   long long lx = ldx;
   int K = (int)w->k;
   int* dp = dump;
-  void* args[] = {&jobs.wq[0],    &jobs.wq[1],    &jobs.wq[2],    &jobs.wq[3],    &jobs.y[0],     &jobs.y[1],
-                  &jobs.y[2],     &jobs.y[3],     &jobs.rows[0],  &jobs.rows[1],  &jobs.rows[2],  &jobs.rows[3],
-                  &jobs.ldy[0],   &jobs.ldy[1],   &jobs.ldy[2],   &jobs.ldy[3],   &jobs.row0[0],  &jobs.row0[1],
-                  &jobs.row0[2],  &jobs.row0[3],  &jobs.trows[0], &jobs.trows[1], &jobs.trows[2], &jobs.trows[3],
-                  &jobs.njobs,    &jobs.total,    &a,             &lx,            &K,             &dp,
-                  &norm_w,        &eps,           &accumulate};
+  void* args[6 * kMaxJobs + 9];
+  int na = 0;
+  for (int j = 0; j < jcap; ++j) {
+    args[na++] = &jobs.wq[j];
+    args[na++] = &jobs.y[j];
+    args[na++] = &jobs.rows[j];
+    args[na++] = &jobs.ldy[j];
+    args[na++] = &jobs.row0[j];
+    args[na++] = &jobs.trows[j];
+  }
+  args[na++] = &jobs.njobs;
+  args[na++] = &jobs.total;
+  args[na++] = &a;
+  args[na++] = &lx;
+  args[na++] = &K;
+  args[na++] = &dp;
+  args[na++] = &norm_w;
+  args[na++] = &eps;
+  args[na++] = &accumulate;
   return launch(d, name, (unsigned)wgs, 64 * wv, lds, s, args);
 }
 
@@ -642,6 +669,26 @@ int qmm_matmul_q(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int6
   return QMM_OK;
 }
 
+int qmm_matmul_multi_q(const qmm_qtensor* const* w, int count, const void* xq, int64_t m, float* const* y,
+                       const int64_t* ldy, void* stream) {
+  if (!w || !y || !ldy || !xq || count < 1 || count > kMaxJobs)
+    return fail(QMM_ERR_INVALID, "need 1..%d weights with outputs and an activation", kMaxJobs);
+  GemvTarget tg[kMaxJobs];
+  for (int j = 0; j < count; ++j) {
+    QMM_TRY(check_matmul(w[j], m, y[j], ldy[j]));
+    if (w[j]->dtype != w[0]->dtype || w[j]->k != w[0]->k)
+      return fail(QMM_ERR_INVALID, "weights of one launch must share dtype and k");
+    tg[j] = {w[j], y[j], ldy[j]};
+  }
+  if (m > 8) {  // the GEMM runs one weight at a time
+    for (int j = 0; j < count; ++j) QMM_TRY(qmm_matmul_q(w[j], xq, m, y[j], ldy[j], stream));
+    return QMM_OK;
+  }
+  Device* d;
+  QMM_TRY(current_device(&d));
+  return gemv(d, tg, count, xq, false, 0, (int)m, nullptr, (hipStream_t)stream);
+}
+
 int qmm_matmul_q_ex(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int64_t ldy, int accumulate,
                     void* stream) {
   QMM_TRY(check_matmul(w, m, y, ldy));
@@ -689,7 +736,7 @@ static int matmul_targets(const GemvTarget* tg, int count, const float* x, int64
   const size_t xrow = (size_t)(w->k / qmm_block_size(vt)) * qmm_type_size(vt);
   for (int64_t m0 = 0; m0 < m; m0 += 8) {
     const int mm = (int)(m - m0 < 8 ? m - m0 : 8);
-    GemvTarget t[4];
+    GemvTarget t[kMaxJobs];
     for (int j = 0; j < count; ++j) t[j] = {tg[j].w, tg[j].y + m0 * tg[j].ldy, tg[j].ldy};
     QMM_TRY(gemv(d, t, count, (const uint8_t*)ws + m0 * xrow, false, 0, mm, nullptr, s, nullptr, 0.0f, accumulate));
   }
@@ -705,8 +752,9 @@ int qmm_matmul(const qmm_qtensor* w, const float* x, int64_t m, int64_t ldx, flo
 
 int qmm_matmul_multi(const qmm_qtensor* const* w, int count, const float* x, int64_t m, int64_t ldx,
                      float* const* y, const int64_t* ldy, void* ws, size_t ws_bytes, void* stream) {
-  if (!w || !y || !ldy || count < 1 || count > 4) return fail(QMM_ERR_INVALID, "need 1..4 weights with outputs");
-  GemvTarget t[4];
+  if (!w || !y || !ldy || count < 1 || count > kMaxJobs)
+    return fail(QMM_ERR_INVALID, "need 1..%d weights with outputs", kMaxJobs);
+  GemvTarget t[kMaxJobs];
   for (int j = 0; j < count; ++j) {
     QMM_TRY(check_matmul(w[j], m, y[j], ldy[j]));
     if (w[j]->dtype != w[0]->dtype || w[j]->k != w[0]->k)
@@ -719,8 +767,9 @@ int qmm_matmul_multi(const qmm_qtensor* const* w, int count, const float* x, int
 int qmm_matmul_ex(const qmm_qtensor* const* w, int count, const float* x, int64_t m, int64_t ldx,
                   const float* norm_weight, float eps, int accumulate, float* const* y, const int64_t* ldy, void* ws,
                   size_t ws_bytes, void* stream) {
-  if (!w || !y || !ldy || count < 1 || count > 4) return fail(QMM_ERR_INVALID, "need 1..4 weights with outputs");
-  GemvTarget t[4];
+  if (!w || !y || !ldy || count < 1 || count > kMaxJobs)
+    return fail(QMM_ERR_INVALID, "need 1..%d weights with outputs", kMaxJobs);
+  GemvTarget t[kMaxJobs];
   for (int j = 0; j < count; ++j) {
     QMM_TRY(check_matmul(w[j], m, y[j], ldy[j]));
     if (w[j]->dtype != w[0]->dtype || w[j]->k != w[0]->k)

@@ -155,19 +155,15 @@ __device__ __forceinline__ void moe_gemv(const uint8_t* w0, const uint8_t* w1, i
   for (int mc = 0; mc < me; mc += 8) {
     if (mc > 0) __syncthreads();
     qmm::GemvJobs jobs;
-    jobs.wq[0] = w0;
-    jobs.wq[1] = w1;
-    jobs.wq[2] = jobs.wq[3] = nullptr;
-    jobs.y[0] = y0 + (size_t)(off + mc) * ldy;
-    jobs.y[1] = y1 + (size_t)(off + mc) * ldy;
-    jobs.y[2] = jobs.y[3] = nullptr;
-    jobs.rows[0] = jobs.rows[1] = N;
-    jobs.rows[2] = jobs.rows[3] = 0;
-    jobs.ldy[0] = jobs.ldy[1] = jobs.ldy[2] = jobs.ldy[3] = ldy;
-    jobs.row0[0] = jobs.row0[1] = e * N;
-    jobs.row0[2] = jobs.row0[3] = 0;
-    jobs.trows[0] = jobs.trows[1] = E * N;
-    jobs.trows[2] = jobs.trows[3] = 0;
+#pragma unroll
+    for (int j = 0; j < qmm::kMaxJobs; ++j) {
+      jobs.wq[j] = j == 0 ? w0 : j == 1 ? w1 : nullptr;
+      jobs.y[j] = j == 0 ? y0 + (size_t)(off + mc) * ldy : j == 1 ? y1 + (size_t)(off + mc) * ldy : nullptr;
+      jobs.rows[j] = j < 2 ? N : 0;
+      jobs.ldy[j] = ldy;
+      jobs.row0[j] = j < 2 ? e * N : 0;
+      jobs.trows[j] = j < 2 ? E * N : 0;
+    }
     jobs.njobs = njobs;
     jobs.total = njobs * N;
     const int mrows = me - mc < 8 ? me - mc : 8;

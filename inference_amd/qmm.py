@@ -48,7 +48,7 @@ EXPORTS = (
     "qmm_moe_ffn", "qmm_matmul_ex", "qmm_matmul_ex_workspace_size", "qmm_rms_norm", "qmm_embed_rows",
     "qmm_rope_kv_append", "qmm_decode_attention", "qmm_silu_mul_quantize", "qmm_greedy_advance",
     "qmm_matmul_q_ex", "qmm_decode_attention_workspace_size", "qmm_decode_rope_attention",
-    "qmm_greedy_workspace_size",
+    "qmm_greedy_workspace_size", "qmm_matmul_multi_q",
 )
 
 
@@ -104,6 +104,8 @@ def lib() -> ctypes.CDLL:
             "qmm_silu_mul_quantize": ([vp, vp, i64, i64, i64, vp, vp], i32),
             "qmm_greedy_advance": ([vp, i64, vp, i64, vp, i32, vp, sz, vp], i32),
             "qmm_matmul_q_ex": ([vp, vp, i64, vp, i64, i32, vp], i32),
+            "qmm_matmul_multi_q": ([ctypes.POINTER(vp), i32, vp, i64, ctypes.POINTER(vp), ctypes.POINTER(i64), vp],
+                                   i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -313,8 +315,8 @@ class QMatMul:
 
 def matmul_multi(qts: Sequence[QTensor], x: torch.Tensor) -> Tuple[torch.Tensor, ...]:
     """Several QMatMul::forward on one input (same dtype and k) in one launch."""
-    if not 1 <= len(qts) <= 4:
-        raise QmmError(1, "matmul_multi takes 1..4 weights")
+    if not 1 <= len(qts) <= 8:
+        raise QmmError(1, "matmul_multi takes 1..8 weights")
     k = qts[0].shape[1]
     if x.dtype != torch.float32 or x.shape[-1] != k:
         raise QmmError(1, "matmul_multi expects float32 input with last dim k")

@@ -8,6 +8,8 @@ Bars (from the task's parity contract):
 Sizes: small shapes where the oracle's per-block dump is cheap, and the
 BASELINE configuration shapes for the f32 outputs.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -311,6 +313,31 @@ def test_matmul_multi_equals_separate_forwards(dt, m):
     ys = matmul_multi(qts, x)
     for q, y in zip(qts, ys):
         assert torch.equal(y, QMatMul.from_qtensor(q).forward(x))
+
+
+@pytest.mark.parametrize("dt", WEIGHT_TYPES)
+@pytest.mark.parametrize("m", [1, 2, 3])
+@pytest.mark.parametrize("count", [5, 8])
+def test_matmul_multi_eight_jobs(dt, m, count):
+    """More than four weights in one call (the eight-job kernels at m = 1, two launches otherwise):
+    bit-identical to separate forwards, fused prologue and pre-quantized activation alike."""
+    from inference_amd import matmul_multi, qmm
+    k = 1024
+    rows = (4096, 1024, 1024, 700, 33, 512, 256, 1)[:count]
+    qts = [QTensor.quantize(torch.from_numpy(normal(240 + i, (n, k), 0.02)).to(DEV), dt)
+           for i, n in enumerate(rows)]
+    x = torch.from_numpy(normal(250 + m, (m, k))).to(DEV)
+    ys = matmul_multi(qts, x)
+    xq = quantize_rows(dt.vec_dot_type(), x)
+    yq = [torch.empty((m, n), dtype=torch.float32, device=DEV) for n in rows]
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    qmm._check(qmm.lib().qmm_matmul_multi_q((vp * count)(*[q.handle.value for q in qts]), count, xq.data_ptr(), m,
+                                            (vp * count)(*[y.data_ptr() for y in yq]), (i64 * count)(*rows),
+                                            qmm._stream(DEV)))
+    for q, y, y2 in zip(qts, ys, yq):
+        ref = QMatMul.from_qtensor(q).forward(x)
+        assert torch.equal(y, ref)
+        assert torch.equal(y2, ref)
 
 
 # ---------------------------------------------------------------------------
