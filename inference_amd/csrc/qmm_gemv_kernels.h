@@ -173,6 +173,12 @@ __device__ __forceinline__ uint4 hi_nib(uint4 v) {
   return make_uint4((v.x >> 4) & 0x0f0f0f0fu, (v.y >> 4) & 0x0f0f0f0fu, (v.z >> 4) & 0x0f0f0f0fu,
                     (v.w >> 4) & 0x0f0f0f0fu);
 }
+// High nibbles left in place with the sign bit flipped: byte = 16*q ^ 0x80,
+// read as a signed byte 16*q - 128.
+__device__ __forceinline__ uint4 hi_nib_x80(uint4 v) {
+  return make_uint4((v.x & 0xf0f0f0f0u) ^ 0x80808080u, (v.y & 0xf0f0f0f0u) ^ 0x80808080u,
+                    (v.z & 0xf0f0f0f0u) ^ 0x80808080u, (v.w & 0xf0f0f0f0u) ^ 0x80808080u);
+}
 // 6-bit Q6_K quants (0..63) of 16 elements: 4 low bits from `ql` (already
 // shifted to the low nibble), 2 high bits at bit `sh` of `qh`.
 __device__ __forceinline__ uint4 q6_bytes(uint4 ql, uint4 qh, int sh) {
@@ -199,7 +205,11 @@ __device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t*
     const uint32_t mnp = upper ? (((C >> 4) & 0x0f0fu) | ((B >> 2) & 0x3030u)) : (B & 0x3f3fu);
     const int sc0 = scp & 0xff, sc1 = (scp >> 8) & 0xff;
     const int m0 = mnp & 0xff, m1 = (mnp >> 8) & 0xff;
-    const uint4 w0 = lo_nib(s.b), w1 = lo_nib(s.c), w2 = hi_nib(s.b), w3 = hi_nib(s.c);
+    // Low nibbles as bytes 0..15; high nibbles kept in place with the top bit
+    // flipped, i.e. signed bytes 16*q - 128 (one mask-and-xor per dword instead
+    // of shift-and-mask); their dot is corrected below with the sub-block's
+    // activation sum: sum(q*x) = (dot + 128*sum(x)) / 16, exactly.
+    const uint4 w0 = lo_nib(s.b), w1 = lo_nib(s.c), w2 = hi_nib_x80(s.b), w3 = hi_nib_x80(s.c);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       if (M > 1 && m >= mrows) break;  // wave-uniform
@@ -210,14 +220,16 @@ __device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t*
       const uint4 x1 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (1 ^ sw)));
       const uint4 x2 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (2 ^ sw)));
       const uint4 x3 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (3 ^ sw)));
-      const int s0 = dot16(w1, x1, dot16(w0, x0, 0));
-      const int s1 = dot16(w3, x3, dot16(w2, x2, 0));
       const uint32_t bp = lsum[8 * bx + l];
       const int bs0 = (int)(int16_t)(bp & 0xffffu), bs1 = (int)bp >> 16;
-      const int isd = sc0 * s0 + sc1 * s1;
-      const int ism = m0 * bs0 + m1 * bs1;
+      const int s0 = dot16(w1, x1, dot16(w0, x0, 0));
+      const int s1 = (dot16(w3, x3, dot16(w2, x2, 0)) + 128 * bs1) >> 4;
+      // |s0|, |s1| <= 32*15*128 < 2^23 and scales/mins < 64: full-rate 24-bit products
+      const int isd = __mul24(sc0, s0) + __mul24(sc1, s1);
+      const int ism = __mul24(m0, bs0) + __mul24(m1, bs1);
       const float t = dw * (float)isd - dm * (float)ism;
-      acc[m] += ok ? ld[bx] * t : 0.0f;
+      const float prod = ld[bx] * t;  // computed on every lane: no branch around the dot
+      acc[m] += ok ? prod : 0.0f;
       ia[m] = isd;
       ib[m] = ism;
     }
@@ -252,7 +264,8 @@ __device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t*
       const int t2 = dot16(w2, x2, 0) - 32 * (int)(int16_t)(b23 & 0xffffu);
       const int t3 = dot16(w3, x3, 0) - 32 * ((int)b23 >> 16);
       const int is = sc0 * t0 + sc1 * t1 + sc2 * t2 + sc3 * t3;
-      acc[m] += ok ? ld[bx] * (dw * (float)is) : 0.0f;
+      const float prod = ld[bx] * (dw * (float)is);
+      acc[m] += ok ? prod : 0.0f;
       ia[m] = is;
       ib[m] = 0;
     }
@@ -267,7 +280,8 @@ __device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t*
       const uint4 x0 = *reinterpret_cast<const uint4*>(lds + 32 * bx + 16 * (0 ^ sw));
       const uint4 x1 = *reinterpret_cast<const uint4*>(lds + 32 * bx + 16 * (1 ^ sw));
       const int s0 = dot16(s.b, x1, dot16(s.a, x0, 0));
-      acc[m] += ok ? (dw * ld[bx]) * (float)s0 : 0.0f;
+      const float prod = (dw * ld[bx]) * (float)s0;
+      acc[m] += ok ? prod : 0.0f;
       ia[m] = s0;
       ib[m] = 0;
     }
@@ -336,6 +350,76 @@ __device__ __forceinline__ RowRef locate(const GemvJobs& jobs, int gr, int nb) {
   return r;
 }
 
+// Job cursor: a wave visits its rows in increasing order, so instead of a
+// lookup over the whole table per row it keeps the current job in scalar
+// registers and steps forward when a row passes the job's end. The job fields
+// are read from the kernel-argument segment, where each job's arguments
+// (QMM_JOB_PARAMS) form one 32-byte record.
+struct JobArg {
+  const uint8_t* wq;
+  float* y;
+  int rows, ldy, row0, trows;
+};
+static_assert(sizeof(JobArg) == 32, "job argument record");
+
+struct JobCursor {
+  int j, base, end;  // current job, its first global row, one past its last
+  const uint8_t* wq;
+  float* y;
+  int ldy, row0, trows;
+};
+
+__device__ __forceinline__ const JobArg* job_args() {
+  return reinterpret_cast<const JobArg*>(__builtin_amdgcn_kernarg_segment_ptr());
+}
+
+__device__ __forceinline__ void cursor_load(JobCursor& c, const JobArg* ja) {
+  const JobArg& a = ja[c.j];
+  c.wq = a.wq;
+  c.y = a.y;
+  c.end = c.base + a.rows;
+  c.ldy = a.ldy;
+  c.row0 = a.row0;
+  c.trows = a.trows;
+}
+
+__device__ __forceinline__ void cursor_init(JobCursor& c, const JobArg* ja) {
+  c.j = 0;
+  c.base = 0;
+  cursor_load(c, ja);
+}
+
+// RowRef of global row gr (wave-uniform, not below the previous call's row).
+template <int FMT>
+__device__ __forceinline__ RowRef cursor_row(JobCursor& c, const JobArg* ja, int njobs, int total, int gr, int nb) {
+  while (gr >= c.end && c.j + 1 < njobs) {
+    c.base = c.end;
+    ++c.j;
+    cursor_load(c, ja);
+  }
+  RowRef r;
+  r.wq = c.wq;
+  r.wd = FMT == kFmtQ4K ? nullptr
+                        : reinterpret_cast<const uint16_t*>(c.wq + (size_t)c.trows * nb * FmtInfo<FMT>::kBodyBytes);
+  r.y = c.y;
+  r.ldy = c.ldy;
+  r.out = gr - c.base;
+  r.row = r.out + c.row0;
+  r.rows = c.end - c.base;
+  r.ok = gr < total;
+  return r;
+}
+
+// Row lookup of gemv(): the job cursor when the job table is the kernel's own
+// arguments (KARG), else the select chain over a table built in the kernel.
+template <int FMT, int J, bool KARG>
+__device__ __forceinline__ RowRef row_ref(JobCursor& c, const JobArg* ja, const GemvJobs& jobs, int gr, int nb) {
+  if constexpr (KARG)
+    return cursor_row<FMT>(c, ja, jobs.njobs, jobs.total, gr, nb);
+  else
+    return locate<FMT, J>(jobs, gr, nb);
+}
+
 template <int FMT, int R, int U>
 __device__ __forceinline__ void load_batch(WSlice (&ws)[R][U], const RowRef (&rr)[R], int it0, int nb, int g,
                                            int l) {
@@ -347,6 +431,25 @@ __device__ __forceinline__ void load_batch(WSlice (&ws)[R][U], const RowRef (&rr
       const int b = (it0 + u) * BPI + g;
       ws[r][u] = WSlice{};
       if (rr[r].ok && b < nb) load_slice<FMT>(ws[r][u], rr[r].wq, rr[r].wd, (size_t)rr[r].row * nb + b, l);
+    }
+}
+
+// Unconditional variant for the pipelined kernel: every lane issues its loads
+// (a branch around them would make the compiler wait for all outstanding
+// loads before the next dot products). Lanes past the row's last block read
+// the last block again, rows past the end read the group's first row; the
+// caller masks their results with RowRef::ok and b < nb. rr[0] must be valid.
+template <int FMT, int R, int U>
+__device__ __forceinline__ void load_batch_nc(WSlice (&ws)[R][U], const RowRef (&rr)[R], int it0, int nb, int g,
+                                              int l) {
+  constexpr int BPI = 64 / FmtInfo<FMT>::kLanesPerBlock;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int b = min((it0 + u) * BPI + g, nb - 1);
+      const RowRef& q = rr[r].ok ? rr[r] : rr[0];
+      load_slice<FMT>(ws[r][u], q.wq, q.wd, (size_t)q.row * nb + b, l);
     }
 }
 
@@ -478,7 +581,7 @@ __device__ __forceinline__ void quantize_act(const float* __restrict__ x, long l
 //   dump (optional, single job): int32 block dots [M][rows][nb](x2 for Q4_K).
 // With `accumulate`, outputs are added to y (y += result); norm_w (fused only)
 // RMS-normalises the activation rows before quantization.
-template <int FMT, int M, int R, int U, bool FUSED, int J = 4>
+template <int FMT, int M, int R, int U, bool FUSED, int J = 4, bool KARG = true>
 __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restrict__ act, long long ldx, int K,
                                      int* __restrict__ dump, int mrows = M,
                                      const float* __restrict__ norm_w = nullptr, float eps = 0.0f,
@@ -497,9 +600,12 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
   int row0 = (blockIdx.x * nw + wave) * R;
 
   // First weight batch in flight before the activation is staged.
+  const JobArg* ja = KARG ? job_args() : nullptr;
+  JobCursor jc;
+  if constexpr (KARG) cursor_init(jc, ja);
   RowRef rr[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) rr[r] = locate<FMT, J>(jobs, row0 + r, nb);
+  for (int r = 0; r < R; ++r) rr[r] = row_ref<FMT, J, KARG>(jc, ja, jobs, row0 + r, nb);
   WSlice ws[R][U];
   load_batch<FMT, R, U>(ws, rr, 0, nb, g, l);
   if constexpr (FUSED)
@@ -552,7 +658,7 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       cur[r] = rr[r];
-      rr[r] = locate<FMT, J>(jobs, row0 + row_step + r, nb);
+      rr[r] = row_ref<FMT, J, KARG>(jc, ja, jobs, row0 + row_step + r, nb);
     }
     if (row0 + row_step < jobs.total) load_batch<FMT, R, U>(ws, rr, 0, nb, g, l);
 #pragma unroll
@@ -567,6 +673,152 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
         }
       }
   }
+}
+
+// Software-pipelined GEMV: the weight slices of the next (row group,
+// iteration) step are requested into a second register buffer before the
+// current step's dot products, so every wave keeps a batch in flight while it
+// computes (gemv() issues the next batch only after its dot products). Same
+// work split, arithmetic and outputs as gemv(); no block-dot dump (a store of
+// dump data would make the next batch's loads wait for it).
+// Writes the outputs kept by the lanes with `valid` (lane i holds one output of
+// global row keep_row); `accumulate` adds them with a no-return atomic (one add
+// per output, so the result is exactly y + v).
+template <int FMT, int J>
+__device__ __forceinline__ void flush_outputs(const GemvJobs& jobs, int nb, float keep_v, int keep_row, bool valid,
+                                              int accumulate) {
+  if (!valid) return;
+  const RowRef q = locate<FMT, J>(jobs, keep_row, nb);
+  float* yp = q.y + q.out;
+  if (accumulate)
+    __hip_atomic_fetch_add(yp, keep_v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *yp = keep_v;
+}
+
+template <int FMT, int M, int R, int U, bool FUSED, int J = 4>
+__device__ __forceinline__ void gemv_pipe(const GemvJobs& jobs, const void* __restrict__ act, long long ldx,
+                                          int K, int* __restrict__ dump, int mrows = M,
+                                          const float* __restrict__ norm_w = nullptr, float eps = 0.0f,
+                                          int accumulate = 0) {
+  static_assert(M == 1, "the pipelined GEMV keeps one output per lane (M = 1)");
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int LPB = FmtInfo<FMT>::kLanesPerBlock;
+  constexpr int BPI = 64 / LPB;  // blocks per wave iteration
+  const int nb = K / FmtInfo<FMT>::kBlockElems;
+  const int lane = threadIdx.x & 63;
+  const int nw = blockDim.x >> 6;
+  const int l = lane % LPB;
+  const int g = lane / LPB;
+  const int niter = (nb + BPI - 1) / BPI;
+  const int row_step = gridDim.x * nw * R;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int row = (blockIdx.x * nw + wave) * R;
+  int it = 0;
+
+  WSlice ws0[R][U], ws1[R][U];
+  const JobArg* ja = job_args();
+  JobCursor lcur, ccur;  // rows of the batches being loaded / consumed
+  cursor_init(lcur, ja);
+  cursor_init(ccur, ja);
+  {
+    // waves without rows still load (row total-1) so that no load is conditional
+    RowRef rr[R];
+    const int lr = min(row, jobs.total - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) rr[r] = cursor_row<FMT>(lcur, ja, jobs.njobs, jobs.total, lr + r, nb);
+    load_batch_nc<FMT, R, U>(ws0, rr, 0, nb, g, l);
+  }
+  if constexpr (FUSED)
+    quantize_act<FMT>(reinterpret_cast<const float*>(act), ldx, mrows, nb, lds, norm_w, eps);
+  else
+    stage_act<FMT>(reinterpret_cast<const uint8_t*>(act), mrows * nb, lds);
+  // Every load of the prologue has landed by now (the staging waited for them);
+  // saying so explicitly clears the compiler's wait bookkeeping of the staging
+  // loop, whose exit paths would otherwise leave loads "pending" into the main
+  // loop and force full waits there. vmcnt(0) expcnt(7) lgkmcnt(15).
+  __builtin_amdgcn_s_waitcnt(0x0f70);
+  __syncthreads();
+  if (row >= jobs.total) return;
+
+  float acc[R][M];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+  // Finished outputs wait in registers, one per lane, and are written 64 at a
+  // time: a store inside the loop would make the next batch's loads wait for
+  // it (its data register is reused by the following step).
+  float keep_v = 0.0f;
+  int keep_row = 0;
+  int slot = 0;
+
+  // Each step requests the next batch into one buffer, then consumes the
+  // other; the two buffers alternate (the phase loop is unrolled, so both stay
+  // in registers). Row references are recomputed from `row` (scalar work).
+  // Two phases per loop trip, both unconditional, one exit test after phase 1:
+  // the loop head is then reachable only from the end of phase 1, so the
+  // compiler's wait counting sees each phase's batch consumed before it is
+  // reloaded (an exit inside the trip adds merge paths that force full waits).
+  // A wave whose rows end in phase 0 runs phase 1 with every result masked.
+  // Loads always target a valid batch: past the wave's last one, the last
+  // valid batch is requested again (an L2 hit).
+  int ldrow = row, ldit = 0;
+  do {
+#pragma unroll
+    for (int ph = 0; ph < 2; ++ph) {
+      WSlice(&cur)[R][U] = ph ? ws1 : ws0;
+      WSlice(&nxt)[R][U] = ph ? ws0 : ws1;
+      int nit = it + U, nrow = row;
+      const bool newrow = nit >= niter;
+      if (newrow) {
+        nit = 0;
+        nrow = row + row_step;
+      }
+      if (nrow < jobs.total) {  // scalar selects only
+        ldrow = nrow;
+        ldit = nit;
+      }
+      {
+        RowRef nr[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) nr[r] = cursor_row<FMT>(lcur, ja, jobs.njobs, jobs.total, ldrow + r, nb);
+        load_batch_nc<FMT, R, U>(nxt, nr, ldit, nb, g, l);
+      }
+      RowRef cr[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) cr[r] = cursor_row<FMT>(ccur, ja, jobs.njobs, jobs.total, row + r, nb);
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int b = (it + u) * BPI + g;
+          const bool ok = cr[r].ok && b < nb;
+          int ia[M], ib[M];
+          dot_slice<FMT, M>(cur[r][u], l, lds, mrows * nb, ok ? b : 0, nb, ok, acc[r], ia, ib, mrows);
+        }
+      if (newrow) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const float v = wave_sum(acc[r][0]);
+          acc[r][0] = 0.0f;
+          // lane `slot` keeps this output (rows past the end are dropped)
+          if (cr[r].ok && lane == slot) {
+            keep_v = v;
+            keep_row = row + r;
+          }
+          slot += cr[r].ok ? 1 : 0;
+        }
+        if (slot > 64 - R) {
+          flush_outputs<FMT, J>(jobs, nb, keep_v, keep_row, lane < slot, accumulate);
+          slot = 0;
+        }
+      }
+      row = nrow;
+      it = nit;
+    }
+  } while (row < jobs.total);
+  if (slot > 0) flush_outputs<FMT, J>(jobs, nb, keep_v, keep_row, lane < slot, accumulate);
 }
 
 }  // namespace qmm
@@ -636,6 +888,48 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
     qmm::gemv<FMT, 1, R, U, true, 8>(jobs, act, ldx, K, dump, 1, norm_w, eps, accumulate);             \
   }
 
+// Pipelined variants (suffix _p), M = 1: four-job and eight-job tables.
+#define QMM_GEMVP_KERNEL(FMT, NAME, W, R, U)                                                          \
+  extern "C" __global__ void __launch_bounds__(64 * W)                                                \
+      qmm_gemv_##NAME##_m1_w##W##_r##R##_u##U##_p(QMM_GEMV_PARAMS) {                                  \
+    QMM_GEMV_JOBS                                                                                     \
+    qmm::gemv_pipe<FMT, 1, R, U, false>(jobs, act, ldx, K, dump, 1, nullptr, 0.0f, accumulate);       \
+  }
+#define QMM_GEMVFP_KERNEL(FMT, NAME, W, R, U)                                                         \
+  extern "C" __global__ void __launch_bounds__(64 * W)                                                \
+      qmm_gemvf_##NAME##_m1_w##W##_r##R##_u##U##_p(QMM_GEMV_PARAMS) {                                 \
+    QMM_GEMV_JOBS                                                                                     \
+    qmm::gemv_pipe<FMT, 1, R, U, true>(jobs, act, ldx, K, dump, 1, norm_w, eps, accumulate);          \
+  }
+#define QMM_GEMVP_KERNEL8(FMT, NAME, W, R, U)                                                         \
+  extern "C" __global__ void __launch_bounds__(64 * W)                                                \
+      qmm_gemv_##NAME##_m1_w##W##_r##R##_u##U##_j8_p(QMM_GEMV_PARAMS8) {                              \
+    QMM_GEMV_JOBS8                                                                                    \
+    qmm::gemv_pipe<FMT, 1, R, U, false, 8>(jobs, act, ldx, K, dump, 1, nullptr, 0.0f, accumulate);    \
+  }
+#define QMM_GEMVFP_KERNEL8(FMT, NAME, W, R, U)                                                        \
+  extern "C" __global__ void __launch_bounds__(64 * W)                                                \
+      qmm_gemvf_##NAME##_m1_w##W##_r##R##_u##U##_j8_p(QMM_GEMV_PARAMS8) {                             \
+    QMM_GEMV_JOBS8                                                                                    \
+    qmm::gemv_pipe<FMT, 1, R, U, true, 8>(jobs, act, ldx, K, dump, 1, norm_w, eps, accumulate);       \
+  }
+#define QMM_GEMV_PIPE_SHAPES(FMT, NAME) \
+  QMM_GEMVP_KERNEL(FMT, NAME, 4, 1, 1)  \
+  QMM_GEMVP_KERNEL(FMT, NAME, 8, 1, 1)  \
+  QMM_GEMVP_KERNEL(FMT, NAME, 16, 1, 1) \
+  QMM_GEMVP_KERNEL(FMT, NAME, 8, 2, 1)  \
+  QMM_GEMVP_KERNEL(FMT, NAME, 8, 1, 2)  \
+  QMM_GEMVP_KERNEL(FMT, NAME, 16, 1, 2) \
+  QMM_GEMVFP_KERNEL(FMT, NAME, 8, 1, 1)  \
+  QMM_GEMVFP_KERNEL(FMT, NAME, 16, 1, 1) \
+  QMM_GEMVFP_KERNEL(FMT, NAME, 8, 1, 2)  \
+  QMM_GEMVFP_KERNEL(FMT, NAME, 16, 1, 2) \
+  QMM_GEMVP_KERNEL8(FMT, NAME, 4, 1, 1)  \
+  QMM_GEMVP_KERNEL8(FMT, NAME, 8, 1, 1)  \
+  QMM_GEMVP_KERNEL8(FMT, NAME, 16, 1, 1) \
+  QMM_GEMVFP_KERNEL8(FMT, NAME, 8, 1, 1)  \
+  QMM_GEMVFP_KERNEL8(FMT, NAME, 16, 1, 1)
+
 // Launch shapes: W waves per workgroup, R rows per wave, U load iterations per batch.
 #define QMM_GEMV_SHAPES_1(FMT, NAME)        \
   QMM_GEMV_KERNEL(FMT, NAME, 1, 4, 1, 1)    \
@@ -682,7 +976,8 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
   QMM_GEMV_SHAPES(FMT, NAME, 7)   \
   QMM_GEMV_SHAPES(FMT, NAME, 8)   \
   QMM_GEMVF_SHAPES(FMT, NAME, 1)  \
-  QMM_GEMVF_SHAPES(FMT, NAME, 2)
+  QMM_GEMVF_SHAPES(FMT, NAME, 2)  \
+  QMM_GEMV_PIPE_SHAPES(FMT, NAME)
 
 QMM_GEMV_ALL_M(qmm::kFmtQ4K, q4k)
 QMM_GEMV_ALL_M(qmm::kFmtQ6K, q6k)
