@@ -42,6 +42,10 @@ __device__ __forceinline__ float dpp_f(float v) {
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
 }
 
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
 // Sum over the 64 lanes of a wave; every lane receives the total.
 // Rows of 16 lanes are reduced with DPP (quad swaps, half-row and row
 // mirrors), the four rows with two cross-row exchanges.
@@ -55,8 +59,15 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ float readlane_f(float v, int lane) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+// Sum over the 64 lanes of a wave as a wave-uniform value: DPP inside rows of
+// 16 lanes, then the four row sums are read with v_readlane (no LDS round
+// trip). Summation order: rows, then (row 0 + row 1) + (row 2 + row 3).
+__device__ __forceinline__ float wave_total(float v) {
+  v += dpp_f<0xb1>(v);
+  v += dpp_f<0x4e>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
 }
 
 // Max over the 64 lanes of a wave (every lane receives it): DPP inside rows

@@ -134,28 +134,32 @@ struct WSlice {
   uint32_t d;  // Q6_K / Q8_0: f16 scale
 };
 
-// `wq` = block bodies (N rows x nb blocks), `wd` = separated f16 scales.
+// Block b of a row: `wrow` = the row's first block body, `drow` = its first
+// separated f16 scale (both wave-uniform), so a lane's address is a scalar base
+// plus a 32-bit offset.
 template <int FMT>
-__device__ __forceinline__ void load_slice(WSlice& s, const uint8_t* __restrict__ wq,
-                                           const uint16_t* __restrict__ wd, size_t blk, int l) {
+__device__ __forceinline__ void load_slice(WSlice& s, const uint8_t* __restrict__ wrow,
+                                           const uint16_t* __restrict__ drow, uint32_t b, int l) {
+  // 32-bit offsets from the uniform row base (global_load with a scalar base)
+  auto ld16 = [wrow](uint32_t o) { return *reinterpret_cast<const uint4*>(wrow + o); };
   if constexpr (FMT == kFmtQ4K) {
-    const uint8_t* p = wq + blk * kQ4KBytes;
-    s.a = *reinterpret_cast<const uint4*>(p);
-    s.b = *reinterpret_cast<const uint4*>(p + 16 + 32 * l);
-    s.c = *reinterpret_cast<const uint4*>(p + 32 + 32 * l);
+    const uint32_t o = b * (uint32_t)kQ4KBytes, ol = o + 32u * (uint32_t)l;
+    s.a = ld16(o);
+    s.b = ld16(ol + 16u);
+    s.c = ld16(ol + 32u);
   } else if constexpr (FMT == kFmtQ6K) {
-    const uint8_t* p = wq + blk * kQ6KBody;
-    s.a = *reinterpret_cast<const uint4*>(p + 32 * l);
-    s.b = *reinterpret_cast<const uint4*>(p + 32 * l + 16);
-    s.c = *reinterpret_cast<const uint4*>(p + 128 + 32 * (l >> 1));
-    s.e = *reinterpret_cast<const uint4*>(p + 128 + 32 * (l >> 1) + 16);
-    s.f = *reinterpret_cast<const uint4*>(p + 192);
-    s.d = wd[blk];
+    const uint32_t o = b * (uint32_t)kQ6KBody, ol = o + 32u * (uint32_t)l, oh = o + 128u + 32u * (uint32_t)(l >> 1);
+    s.a = ld16(ol);
+    s.b = ld16(ol + 16u);
+    s.c = ld16(oh);
+    s.e = ld16(oh + 16u);
+    s.f = ld16(o + 192u);
+    s.d = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(drow) + 2u * b);
   } else {
-    const uint8_t* p = wq + blk * kQ80Body;
-    s.a = *reinterpret_cast<const uint4*>(p);
-    s.b = *reinterpret_cast<const uint4*>(p + 16);
-    s.d = wd[blk];
+    const uint32_t o = b * (uint32_t)kQ80Body;
+    s.a = ld16(o);
+    s.b = ld16(o + 16u);
+    s.d = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(drow) + 2u * b);
   }
 }
 
@@ -186,105 +190,148 @@ __device__ __forceinline__ uint4 q6_bytes(uint4 ql, uint4 qh, int sh) {
   return make_uint4(one(ql.x, qh.x), one(ql.y, qh.y), one(ql.z, qh.z), one(ql.w, qh.w));
 }
 
-// Multiply one lane's slice with the staged activation block `xb` of each of
-// the M rows (row stride `nbx` blocks in LDS). Adds to acc (when ok) and
-// returns the lane's integer partials in ia / ib.
-template <int FMT, int M>
-__device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t* __restrict__ lds,
-                                          int nblk, int xb, int nbx, bool ok, float (&acc)[M],
-                                          int (&ia)[M], int (&ib)[M], int mrows) {
+// Weight-side values of one lane's slice of one block (unpacked quants, scales),
+// shared by every activation row the slice meets.
+struct WPrep {
+  uint4 w0, w1, w2, w3;
+  int c0, c1, c2, c3;  // Q4_K: sc0, sc1, m0, m1; Q6_K: the four group scales
+  float dw, dm;
+};
+
+template <int FMT>
+__device__ __forceinline__ WPrep prep_w(const WSlice& s, int l) {
+  WPrep w;
   if constexpr (FMT == kFmtQ4K) {
-    const uint32_t* lsum = reinterpret_cast<const uint32_t*>(lds + 256 * nblk);
-    const float* ld = reinterpret_cast<const float*>(lsum + 8 * nblk);
-    const float dw = h2f(s.a.x), dm = h2f(s.a.x >> 16);
+    w.dw = h2f(s.a.x);
+    w.dm = h2f(s.a.x >> 16);
     // 6-bit scale/min of sub-blocks 2l and 2l+1 (get_scale_min_k4).
     const int sh = (l & 1) * 16;
     const uint32_t A = s.a.y >> sh, B = s.a.z >> sh, C = s.a.w >> sh;
     const bool upper = l >= 2;
     const uint32_t scp = upper ? ((C & 0x0f0fu) | ((A >> 2) & 0x3030u)) : (A & 0x3f3fu);
     const uint32_t mnp = upper ? (((C >> 4) & 0x0f0fu) | ((B >> 2) & 0x3030u)) : (B & 0x3f3fu);
-    const int sc0 = scp & 0xff, sc1 = (scp >> 8) & 0xff;
-    const int m0 = mnp & 0xff, m1 = (mnp >> 8) & 0xff;
+    w.c0 = scp & 0xff;
+    w.c1 = (scp >> 8) & 0xff;
+    w.c2 = mnp & 0xff;
+    w.c3 = (mnp >> 8) & 0xff;
     // Low nibbles as bytes 0..15; high nibbles kept in place with the top bit
     // flipped, i.e. signed bytes 16*q - 128 (one mask-and-xor per dword instead
-    // of shift-and-mask); their dot is corrected below with the sub-block's
+    // of shift-and-mask); their dot is corrected with the sub-block's
     // activation sum: sum(q*x) = (dot + 128*sum(x)) / 16, exactly.
-    const uint4 w0 = lo_nib(s.b), w1 = lo_nib(s.c), w2 = hi_nib_x80(s.b), w3 = hi_nib_x80(s.c);
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      if (M > 1 && m >= mrows) break;  // wave-uniform
-      const int bx = xb + m * nbx;
-      const uint8_t* e = lds + 256 * bx;
-      const int sw = (l >> 1) | ((bx & 1) << 1);
-      const uint4 x0 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (0 ^ sw)));
-      const uint4 x1 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (1 ^ sw)));
-      const uint4 x2 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (2 ^ sw)));
-      const uint4 x3 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (3 ^ sw)));
-      const uint32_t bp = lsum[8 * bx + l];
-      const int bs0 = (int)(int16_t)(bp & 0xffffu), bs1 = (int)bp >> 16;
-      const int s0 = dot16(w1, x1, dot16(w0, x0, 0));
-      const int s1 = (dot16(w3, x3, dot16(w2, x2, 0)) + 128 * bs1) >> 4;
-      // |s0|, |s1| <= 32*15*128 < 2^23 and scales/mins < 64: full-rate 24-bit products
-      const int isd = __mul24(sc0, s0) + __mul24(sc1, s1);
-      const int ism = __mul24(m0, bs0) + __mul24(m1, bs1);
-      const float t = dw * (float)isd - dm * (float)ism;
-      const float prod = ld[bx] * t;  // computed on every lane: no branch around the dot
-      acc[m] += ok ? prod : 0.0f;
-      ia[m] = isd;
-      ib[m] = ism;
-    }
+    w.w0 = lo_nib(s.b);
+    w.w1 = lo_nib(s.c);
+    w.w2 = hi_nib_x80(s.b);
+    w.w3 = hi_nib_x80(s.c);
   } else if constexpr (FMT == kFmtQ6K) {
-    const uint32_t* lsum = reinterpret_cast<const uint32_t*>(lds + 256 * nblk);
-    const float* ld = reinterpret_cast<const float*>(lsum + 8 * nblk);
-    const float dw = h2f(s.d);
+    w.dw = h2f(s.d);
+    w.dm = 0.0f;
     const int h = l >> 1, p = l & 1;
     // scales of the lane's four 16-element groups: 8h + 2p + {0, 1} and +4.
     const uint32_t wlo = h ? s.f.z : s.f.x, whi = h ? s.f.w : s.f.y;
     const uint32_t sl = wlo >> (16 * p), shh = whi >> (16 * p);
-    const int sc0 = (int)(int8_t)(sl & 0xff), sc1 = (int)(int8_t)((sl >> 8) & 0xff);
-    const int sc2 = (int)(int8_t)(shh & 0xff), sc3 = (int)(int8_t)((shh >> 8) & 0xff);
+    w.c0 = (int)(int8_t)(sl & 0xff);
+    w.c1 = (int)(int8_t)((sl >> 8) & 0xff);
+    w.c2 = (int)(int8_t)(shh & 0xff);
+    w.c3 = (int)(int8_t)((shh >> 8) & 0xff);
     const int sh0 = 2 * p, sh1 = 2 * p + 4;
-    const uint4 w0 = q6_bytes(s.a, s.c, sh0);                // elements 128h + 32p + [0,16)
-    const uint4 w1 = q6_bytes(s.b, s.e, sh0);                // +16
-    const uint4 w2 = q6_bytes(hi_nib(s.a), s.c, sh1);        // +64
-    const uint4 w3 = q6_bytes(hi_nib(s.b), s.e, sh1);        // +80
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      if (M > 1 && m >= mrows) break;  // wave-uniform
-      const int bx = xb + m * nbx;
-      const uint8_t* e = lds + 256 * bx;
-      const int sw = (l >> 1) | ((bx & 1) << 1);
-      const uint4 x0 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (0 ^ sw)));
-      const uint4 x1 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (1 ^ sw)));
-      const uint4 x2 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (2 ^ sw)));
-      const uint4 x3 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (3 ^ sw)));
-      const uint32_t b01 = lsum[8 * bx + 2 * l], b23 = lsum[8 * bx + 2 * l + 1];
-      const int t0 = dot16(w0, x0, 0) - 32 * (int)(int16_t)(b01 & 0xffffu);
-      const int t1 = dot16(w1, x1, 0) - 32 * ((int)b01 >> 16);
-      const int t2 = dot16(w2, x2, 0) - 32 * (int)(int16_t)(b23 & 0xffffu);
-      const int t3 = dot16(w3, x3, 0) - 32 * ((int)b23 >> 16);
-      const int is = sc0 * t0 + sc1 * t1 + sc2 * t2 + sc3 * t3;
-      const float prod = ld[bx] * (dw * (float)is);
-      acc[m] += ok ? prod : 0.0f;
-      ia[m] = is;
-      ib[m] = 0;
-    }
+    w.w0 = q6_bytes(s.a, s.c, sh0);          // elements 128h + 32p + [0,16)
+    w.w1 = q6_bytes(s.b, s.e, sh0);          // +16
+    w.w2 = q6_bytes(hi_nib(s.a), s.c, sh1);  // +64
+    w.w3 = q6_bytes(hi_nib(s.b), s.e, sh1);  // +80
   } else {
+    w.dw = h2f(s.d);
+    w.dm = 0.0f;
+    w.w0 = s.a;
+    w.w1 = s.b;
+    w.c0 = w.c1 = w.c2 = w.c3 = 0;
+  }
+  return w;
+}
+
+// Activation-side values of one lane for one staged block: its 16-element
+// chunks, their precombined sums and the block scale.
+struct XSlice {
+  uint4 x0, x1, x2, x3;
+  uint32_t s0, s1;  // Q4_K: sums of sub-blocks 2l | 2l+1; Q6_K: (chunks 0,1) and (2,3)
+  float d;
+};
+
+// LDS layouts written by stage_act / quantize_act (nblk staged blocks).
+template <int FMT>
+__device__ __forceinline__ void load_x(XSlice& x, const uint8_t* __restrict__ lds, int nblk, int bx, int l) {
+  if constexpr (FMT == kFmtQ80) {
     const float* ld = reinterpret_cast<const float*>(lds + 32 * nblk);
-    const float dw = h2f(s.d);
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      if (M > 1 && m >= mrows) break;  // wave-uniform
-      const int bx = xb + m * nbx;
-      const int sw = (bx >> 2) & 1;
-      const uint4 x0 = *reinterpret_cast<const uint4*>(lds + 32 * bx + 16 * (0 ^ sw));
-      const uint4 x1 = *reinterpret_cast<const uint4*>(lds + 32 * bx + 16 * (1 ^ sw));
-      const int s0 = dot16(s.b, x1, dot16(s.a, x0, 0));
-      const float prod = (dw * ld[bx]) * (float)s0;
-      acc[m] += ok ? prod : 0.0f;
-      ia[m] = s0;
-      ib[m] = 0;
+    const int sw = (bx >> 2) & 1;
+    x.x0 = *reinterpret_cast<const uint4*>(lds + 32 * bx + 16 * (0 ^ sw));
+    x.x1 = *reinterpret_cast<const uint4*>(lds + 32 * bx + 16 * (1 ^ sw));
+    x.d = ld[bx];
+  } else {
+    const uint32_t* lsum = reinterpret_cast<const uint32_t*>(lds + 256 * nblk);
+    const float* ld = reinterpret_cast<const float*>(lsum + 8 * nblk);
+    const uint8_t* e = lds + 256 * bx;
+    const int sw = (l >> 1) | ((bx & 1) << 1);
+    x.x0 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (0 ^ sw)));
+    x.x1 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (1 ^ sw)));
+    x.x2 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (2 ^ sw)));
+    x.x3 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (3 ^ sw)));
+    if constexpr (FMT == kFmtQ4K) {
+      x.s0 = lsum[8 * bx + l];
+    } else {
+      x.s0 = lsum[8 * bx + 2 * l];
+      x.s1 = lsum[8 * bx + 2 * l + 1];
     }
+    x.d = ld[bx];
+  }
+}
+
+// One lane's f32 contribution for one block; its integer partials go to ia / ib.
+template <int FMT>
+__device__ __forceinline__ float dot_wx(const WPrep& w, const XSlice& x, int& ia, int& ib) {
+  if constexpr (FMT == kFmtQ4K) {
+    const int bs0 = (int)(int16_t)(x.s0 & 0xffffu), bs1 = (int)x.s0 >> 16;
+    const int s0 = dot16(w.w1, x.x1, dot16(w.w0, x.x0, 0));
+    const int s1 = (dot16(w.w3, x.x3, dot16(w.w2, x.x2, 0)) + 128 * bs1) >> 4;
+    // |s0|, |s1| <= 32*15*128 < 2^23 and scales/mins < 64: full-rate 24-bit products
+    const int isd = __mul24(w.c0, s0) + __mul24(w.c1, s1);
+    const int ism = __mul24(w.c2, bs0) + __mul24(w.c3, bs1);
+    const float t = w.dw * (float)isd - w.dm * (float)ism;
+    ia = isd;
+    ib = ism;
+    return x.d * t;
+  } else if constexpr (FMT == kFmtQ6K) {
+    const int t0 = dot16(w.w0, x.x0, 0) - 32 * (int)(int16_t)(x.s0 & 0xffffu);
+    const int t1 = dot16(w.w1, x.x1, 0) - 32 * ((int)x.s0 >> 16);
+    const int t2 = dot16(w.w2, x.x2, 0) - 32 * (int)(int16_t)(x.s1 & 0xffffu);
+    const int t3 = dot16(w.w3, x.x3, 0) - 32 * ((int)x.s1 >> 16);
+    // |t| < 2^18 and int8 scales: exact 24-bit products
+    const int is = __mul24(w.c0, t0) + __mul24(w.c1, t1) + __mul24(w.c2, t2) + __mul24(w.c3, t3);
+    ia = is;
+    ib = 0;
+    return x.d * (w.dw * (float)is);
+  } else {
+    const int s0 = dot16(w.w1, x.x1, dot16(w.w0, x.x0, 0));
+    ia = s0;
+    ib = 0;
+    return (w.dw * x.d) * (float)s0;
+  }
+}
+
+// Multiply one lane's slice with the staged activation block `xb` of each of
+// the M rows (row stride `nbx` blocks in LDS). Adds to acc (when ok; the
+// product is computed on every lane, so there is no branch around the dot)
+// and returns the lane's integer partials in ia / ib.
+template <int FMT, int M>
+__device__ __forceinline__ void dot_slice(const WSlice& s, int l, const uint8_t* __restrict__ lds,
+                                          int nblk, int xb, int nbx, bool ok, float (&acc)[M],
+                                          int (&ia)[M], int (&ib)[M], int mrows) {
+  const WPrep w = prep_w<FMT>(s, l);
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    if (M > 1 && m >= mrows) break;  // wave-uniform
+    XSlice x;
+    load_x<FMT>(x, lds, nblk, xb + m * nbx, l);
+    const float prod = dot_wx<FMT>(w, x, ia[m], ib[m]);
+    acc[m] += ok ? prod : 0.0f;
   }
 }
 
@@ -307,6 +354,8 @@ struct GemvJobs {
 struct RowRef {
   const uint8_t* wq;
   const uint16_t* wd;
+  const uint8_t* wrow;   // first block body of the row (wave-uniform)
+  const uint16_t* drow;  // first separated f16 scale of the row (Q6_K / Q8_0)
   float* y;
   int ldy;
   int out;   // output row within its job
@@ -347,6 +396,8 @@ __device__ __forceinline__ RowRef locate(const GemvJobs& jobs, int gr, int nb) {
   r.row = r.out + row0;  // row within the tensor
   r.rows = rows;
   r.ok = gr < jobs.total;
+  r.wrow = wq + (size_t)r.row * nb * FmtInfo<FMT>::kBodyBytes;
+  r.drow = r.wd + (size_t)r.row * nb;
   return r;
 }
 
@@ -407,6 +458,8 @@ __device__ __forceinline__ RowRef cursor_row(JobCursor& c, const JobArg* ja, int
   r.row = r.out + c.row0;
   r.rows = c.end - c.base;
   r.ok = gr < total;
+  r.wrow = c.wq + (size_t)r.row * nb * FmtInfo<FMT>::kBodyBytes;
+  r.drow = r.wd + (size_t)r.row * nb;
   return r;
 }
 
@@ -420,25 +473,10 @@ __device__ __forceinline__ RowRef row_ref(JobCursor& c, const JobArg* ja, const 
     return locate<FMT, J>(jobs, gr, nb);
 }
 
-template <int FMT, int R, int U>
-__device__ __forceinline__ void load_batch(WSlice (&ws)[R][U], const RowRef (&rr)[R], int it0, int nb, int g,
-                                           int l) {
-  constexpr int BPI = 64 / FmtInfo<FMT>::kLanesPerBlock;
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int b = (it0 + u) * BPI + g;
-      ws[r][u] = WSlice{};
-      if (rr[r].ok && b < nb) load_slice<FMT>(ws[r][u], rr[r].wq, rr[r].wd, (size_t)rr[r].row * nb + b, l);
-    }
-}
-
-// Unconditional variant for the pipelined kernel: every lane issues its loads
-// (a branch around them would make the compiler wait for all outstanding
-// loads before the next dot products). Lanes past the row's last block read
-// the last block again, rows past the end read the group's first row; the
-// caller masks their results with RowRef::ok and b < nb. rr[0] must be valid.
+// One batch of weight slices: U iterations of R rows. Every lane issues its
+// loads (no zero-fill and branch around them): lanes past the row's last block
+// read the last block again and rows past the end read the group's first row;
+// the dot products mask those with RowRef::ok and b < nb. rr[0] must be valid.
 template <int FMT, int R, int U>
 __device__ __forceinline__ void load_batch_nc(WSlice (&ws)[R][U], const RowRef (&rr)[R], int it0, int nb, int g,
                                               int l) {
@@ -449,7 +487,7 @@ __device__ __forceinline__ void load_batch_nc(WSlice (&ws)[R][U], const RowRef (
     for (int u = 0; u < U; ++u) {
       const int b = min((it0 + u) * BPI + g, nb - 1);
       const RowRef& q = rr[r].ok ? rr[r] : rr[0];
-      load_slice<FMT>(ws[r][u], q.wq, q.wd, (size_t)q.row * nb + b, l);
+      load_slice<FMT>(ws[r][u], q.wrow, q.drow, (uint32_t)b, l);
     }
 }
 
@@ -575,6 +613,21 @@ __device__ __forceinline__ void quantize_act(const float* __restrict__ x, long l
   }
 }
 
+// Writes the outputs kept by the lanes with `valid` (lane i holds one output of
+// global row keep_row); `accumulate` adds them with a no-return atomic (one add
+// per output, so the result is exactly y + v).
+template <int FMT, int J>
+__device__ __forceinline__ void flush_outputs(const GemvJobs& jobs, int nb, float keep_v, int keep_row, bool valid,
+                                              int accumulate) {
+  if (!valid) return;
+  const RowRef q = locate<FMT, J>(jobs, keep_row, nb);
+  float* yp = q.y + q.out;
+  if (accumulate)
+    __hip_atomic_fetch_add(yp, keep_v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *yp = keep_v;
+}
+
 // y_j[m, n] = sum_b dot(W_j[n, b], X[m, b]) for every job j, m < M, n < rows_j.
 //   act: M rows of nb activation blocks (Q8_K or Q8_0, GGML bytes), or, when
 //        FUSED, M rows of f32 (row stride ldx) quantized in the prologue;
@@ -604,16 +657,24 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
   JobCursor jc;
   if constexpr (KARG) cursor_init(jc, ja);
   RowRef rr[R];
+  WSlice ws[R][U];
+  {
+    // a wave without rows still loads (row total-1) so that no load is conditional
+    const int lr = min(row0, jobs.total - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) rr[r] = row_ref<FMT, J, KARG>(jc, ja, jobs, lr + r, nb);
+    load_batch_nc<FMT, R, U>(ws, rr, 0, nb, g, l);
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r) rr[r] = row_ref<FMT, J, KARG>(jc, ja, jobs, row0 + r, nb);
-  WSlice ws[R][U];
-  load_batch<FMT, R, U>(ws, rr, 0, nb, g, l);
   if constexpr (FUSED)
     quantize_act<FMT>(reinterpret_cast<const float*>(act), ldx, mrows, nb, lds, norm_w, eps);
   else
     stage_act<FMT>(reinterpret_cast<const uint8_t*>(act), mrows * nb, lds);
   __syncthreads();
 
+  float keep_v = 0.0f;  // M = 1: this lane's kept output (global row keep_row)
+  int keep_row = 0, slot = 0;
   for (; row0 < jobs.total; row0 += row_step) {
     float acc[R][M];
 #pragma unroll
@@ -622,7 +683,7 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
       for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
 
     for (int it0 = 0; it0 < niter; it0 += U) {
-      if (it0 > 0) load_batch<FMT, R, U>(ws, rr, it0, nb, g, l);
+      if (it0 > 0) load_batch_nc<FMT, R, U>(ws, rr, it0, nb, g, l);
 #pragma unroll
       for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -660,48 +721,55 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
       cur[r] = rr[r];
       rr[r] = row_ref<FMT, J, KARG>(jc, ja, jobs, row0 + row_step + r, nb);
     }
-    if (row0 + row_step < jobs.total) load_batch<FMT, R, U>(ws, rr, 0, nb, g, l);
+    if (row0 + row_step < jobs.total) load_batch_nc<FMT, R, U>(ws, rr, 0, nb, g, l);
+    if constexpr (M == 1 && KARG) {
+      // One output per row: lane `slot` keeps it and the wave writes 64 at a
+      // time (a store per row would sit in the same in-order memory counter
+      // that the next row's loads are waited on).
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        if (M > 1 && m >= mrows) break;  // wave-uniform
-        const float v = wave_sum(acc[r][m]);
-        if (lane == 0 && cur[r].ok && m < mrows) {
-          float* yp = cur[r].y + (size_t)m * cur[r].ldy + cur[r].out;
-          *yp = accumulate ? *yp + v : v;
+      for (int r = 0; r < R; ++r) {
+        const float v = wave_sum(acc[r][0]);
+        if (cur[r].ok && lane == slot) {
+          keep_v = v;
+          keep_row = row0 + r;
         }
+        slot += cur[r].ok ? 1 : 0;
       }
+      if (slot > 64 - R) {
+        flush_outputs<FMT, J>(jobs, nb, keep_v, keep_row, lane < slot, accumulate);
+        slot = 0;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          if (M > 1 && m >= mrows) break;  // wave-uniform
+          const float v = wave_sum(acc[r][m]);
+          if (lane == 0 && cur[r].ok && m < mrows) {
+            float* yp = cur[r].y + (size_t)m * cur[r].ldy + cur[r].out;
+            *yp = accumulate ? *yp + v : v;
+          }
+        }
+    }
+  }
+  if constexpr (M == 1 && KARG) {
+    if (slot > 0) flush_outputs<FMT, J>(jobs, nb, keep_v, keep_row, lane < slot, accumulate);
   }
 }
 
-// Software-pipelined GEMV: the weight slices of the next (row group,
-// iteration) step are requested into a second register buffer before the
-// current step's dot products, so every wave keeps a batch in flight while it
-// computes (gemv() issues the next batch only after its dot products). Same
-// work split, arithmetic and outputs as gemv(); no block-dot dump (a store of
-// dump data would make the next batch's loads wait for it).
-// Writes the outputs kept by the lanes with `valid` (lane i holds one output of
-// global row keep_row); `accumulate` adds them with a no-return atomic (one add
-// per output, so the result is exactly y + v).
-template <int FMT, int J>
-__device__ __forceinline__ void flush_outputs(const GemvJobs& jobs, int nb, float keep_v, int keep_row, bool valid,
-                                              int accumulate) {
-  if (!valid) return;
-  const RowRef q = locate<FMT, J>(jobs, keep_row, nb);
-  float* yp = q.y + q.out;
-  if (accumulate)
-    __hip_atomic_fetch_add(yp, keep_v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else
-    *yp = keep_v;
-}
-
-template <int FMT, int M, int R, int U, bool FUSED, int J = 4>
-__device__ __forceinline__ void gemv_pipe(const GemvJobs& jobs, const void* __restrict__ act, long long ldx,
-                                          int K, int* __restrict__ dump, int mrows = M,
-                                          const float* __restrict__ norm_w = nullptr, float eps = 0.0f,
-                                          int accumulate = 0) {
-  static_assert(M == 1, "the pipelined GEMV keeps one output per lane (M = 1)");
+// Decode GEMV for one activation row (M = 1), one row per wave at a time:
+// the leanest per-row instruction stream, because a wave's row time is its
+// memory latency plus its own instruction issue. Against gemv():
+//   * the activation slice of the first wave iteration (the whole row's when
+//     K <= 64/LPB blocks, e.g. K = 4096 for k-quants) is read from LDS once
+//     and kept in registers for every row;
+//   * the row sum is reduced with DPP and v_readlane (no LDS round trip);
+//   * outputs are kept one per lane and written 64 at a time.
+// Same per-block arithmetic (prep_w / dot_wx) as gemv(); no block-dot dump.
+template <int FMT, bool FUSED, int J>
+__device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restrict__ act, long long ldx, int K,
+                                      const float* __restrict__ norm_w, float eps, int accumulate) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int LPB = FmtInfo<FMT>::kLanesPerBlock;
   constexpr int BPI = 64 / LPB;  // blocks per wave iteration
@@ -711,113 +779,62 @@ __device__ __forceinline__ void gemv_pipe(const GemvJobs& jobs, const void* __re
   const int l = lane % LPB;
   const int g = lane / LPB;
   const int niter = (nb + BPI - 1) / BPI;
-  const int row_step = gridDim.x * nw * R;
+  const int row_step = gridDim.x * nw;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  int row = (blockIdx.x * nw + wave) * R;
-  int it = 0;
+  int row = blockIdx.x * nw + wave;
 
-  WSlice ws0[R][U], ws1[R][U];
   const JobArg* ja = job_args();
-  JobCursor lcur, ccur;  // rows of the batches being loaded / consumed
-  cursor_init(lcur, ja);
-  cursor_init(ccur, ja);
-  {
-    // waves without rows still load (row total-1) so that no load is conditional
-    RowRef rr[R];
-    const int lr = min(row, jobs.total - 1);
-#pragma unroll
-    for (int r = 0; r < R; ++r) rr[r] = cursor_row<FMT>(lcur, ja, jobs.njobs, jobs.total, lr + r, nb);
-    load_batch_nc<FMT, R, U>(ws0, rr, 0, nb, g, l);
-  }
+  JobCursor jc;
+  cursor_init(jc, ja);
+  WSlice ws;
+  const uint32_t b0 = (uint32_t)min(g, nb - 1);  // clamped: every lane loads
+  RowRef rr = cursor_row<FMT>(jc, ja, jobs.njobs, jobs.total, min(row, jobs.total - 1), nb);
+  load_slice<FMT>(ws, rr.wrow, rr.drow, b0, l);  // first row in flight before staging
   if constexpr (FUSED)
-    quantize_act<FMT>(reinterpret_cast<const float*>(act), ldx, mrows, nb, lds, norm_w, eps);
+    quantize_act<FMT>(reinterpret_cast<const float*>(act), ldx, 1, nb, lds, norm_w, eps);
   else
-    stage_act<FMT>(reinterpret_cast<const uint8_t*>(act), mrows * nb, lds);
-  // Every load of the prologue has landed by now (the staging waited for them);
-  // saying so explicitly clears the compiler's wait bookkeeping of the staging
-  // loop, whose exit paths would otherwise leave loads "pending" into the main
-  // loop and force full waits there. vmcnt(0) expcnt(7) lgkmcnt(15).
-  __builtin_amdgcn_s_waitcnt(0x0f70);
+    stage_act<FMT>(reinterpret_cast<const uint8_t*>(act), nb, lds);
   __syncthreads();
   if (row >= jobs.total) return;
+  rr = cursor_row<FMT>(jc, ja, jobs.njobs, jobs.total, row, nb);
 
-  float acc[R][M];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
-  // Finished outputs wait in registers, one per lane, and are written 64 at a
-  // time: a store inside the loop would make the next batch's loads wait for
-  // it (its data register is reused by the following step).
-  float keep_v = 0.0f;
-  int keep_row = 0;
-  int slot = 0;
-
-  // Each step requests the next batch into one buffer, then consumes the
-  // other; the two buffers alternate (the phase loop is unrolled, so both stay
-  // in registers). Row references are recomputed from `row` (scalar work).
-  // Two phases per loop trip, both unconditional, one exit test after phase 1:
-  // the loop head is then reachable only from the end of phase 1, so the
-  // compiler's wait counting sees each phase's batch consumed before it is
-  // reloaded (an exit inside the trip adds merge paths that force full waits).
-  // A wave whose rows end in phase 0 runs phase 1 with every result masked.
-  // Loads always target a valid batch: past the wave's last one, the last
-  // valid batch is requested again (an L2 hit).
-  int ldrow = row, ldit = 0;
-  do {
-#pragma unroll
-    for (int ph = 0; ph < 2; ++ph) {
-      WSlice(&cur)[R][U] = ph ? ws1 : ws0;
-      WSlice(&nxt)[R][U] = ph ? ws0 : ws1;
-      int nit = it + U, nrow = row;
-      const bool newrow = nit >= niter;
-      if (newrow) {
-        nit = 0;
-        nrow = row + row_step;
-      }
-      if (nrow < jobs.total) {  // scalar selects only
-        ldrow = nrow;
-        ldit = nit;
-      }
-      {
-        RowRef nr[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) nr[r] = cursor_row<FMT>(lcur, ja, jobs.njobs, jobs.total, ldrow + r, nb);
-        load_batch_nc<FMT, R, U>(nxt, nr, ldit, nb, g, l);
-      }
-      RowRef cr[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) cr[r] = cursor_row<FMT>(ccur, ja, jobs.njobs, jobs.total, row + r, nb);
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int b = (it + u) * BPI + g;
-          const bool ok = cr[r].ok && b < nb;
-          int ia[M], ib[M];
-          dot_slice<FMT, M>(cur[r][u], l, lds, mrows * nb, ok ? b : 0, nb, ok, acc[r], ia, ib, mrows);
-        }
-      if (newrow) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const float v = wave_sum(acc[r][0]);
-          acc[r][0] = 0.0f;
-          // lane `slot` keeps this output (rows past the end are dropped)
-          if (cr[r].ok && lane == slot) {
-            keep_v = v;
-            keep_row = row + r;
-          }
-          slot += cr[r].ok ? 1 : 0;
-        }
-        if (slot > 64 - R) {
-          flush_outputs<FMT, J>(jobs, nb, keep_v, keep_row, lane < slot, accumulate);
-          slot = 0;
-        }
-      }
-      row = nrow;
-      it = nit;
+  XSlice x0;  // loop-invariant activation of the first iteration
+  load_x<FMT>(x0, lds, nb, (int)b0, l);
+  const bool ok0 = g < nb;
+  float keep_v = 0.0f;  // this lane's kept output (global row keep_row)
+  int keep_row = 0, slot = 0;
+  for (;;) {
+    int ia, ib;
+    float acc;
+    {
+      const float p = dot_wx<FMT>(prep_w<FMT>(ws, l), x0, ia, ib);
+      acc = ok0 ? p : 0.0f;
     }
-  } while (row < jobs.total);
+    for (int it = 1; it < niter; ++it) {
+      const int b = it * BPI + g;
+      load_slice<FMT>(ws, rr.wrow, rr.drow, (uint32_t)min(b, nb - 1), l);
+      XSlice x;
+      load_x<FMT>(x, lds, nb, b < nb ? b : 0, l);
+      const float p = dot_wx<FMT>(prep_w<FMT>(ws, l), x, ia, ib);
+      acc += b < nb ? p : 0.0f;
+    }
+    const int nrow = row + row_step;
+    if (nrow < jobs.total) {  // next row's first batch before this row's reduction
+      rr = cursor_row<FMT>(jc, ja, jobs.njobs, jobs.total, nrow, nb);
+      load_slice<FMT>(ws, rr.wrow, rr.drow, b0, l);
+    }
+    const float v = wave_total(acc);
+    if (lane == slot) {
+      keep_v = v;
+      keep_row = row;
+    }
+    if (++slot == 64) {
+      flush_outputs<FMT, J>(jobs, nb, keep_v, keep_row, true, accumulate);
+      slot = 0;
+    }
+    row = nrow;
+    if (row >= jobs.total) break;
+  }
   if (slot > 0) flush_outputs<FMT, J>(jobs, nb, keep_v, keep_row, lane < slot, accumulate);
 }
 
@@ -888,47 +905,29 @@ __device__ __forceinline__ void gemv_pipe(const GemvJobs& jobs, const void* __re
     qmm::gemv<FMT, 1, R, U, true, 8>(jobs, act, ldx, K, dump, 1, norm_w, eps, accumulate);             \
   }
 
-// Pipelined variants (suffix _p), M = 1: four-job and eight-job tables.
-#define QMM_GEMVP_KERNEL(FMT, NAME, W, R, U)                                                          \
-  extern "C" __global__ void __launch_bounds__(64 * W)                                                \
-      qmm_gemv_##NAME##_m1_w##W##_r##R##_u##U##_p(QMM_GEMV_PARAMS) {                                  \
-    QMM_GEMV_JOBS                                                                                     \
-    qmm::gemv_pipe<FMT, 1, R, U, false>(jobs, act, ldx, K, dump, 1, nullptr, 0.0f, accumulate);       \
+// One-row decode kernels (gemv1): four-job and eight-job tables, staged
+// (pre-quantized activation) and fused (quantized in the prologue).
+#define QMM_GEMV1_KERNELS(FMT, NAME, W)                                                              \
+  extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1_##NAME##_w##W(QMM_GEMV_PARAMS) {    \
+    QMM_GEMV_JOBS                                                                                    \
+    qmm::gemv1<FMT, false, 4>(jobs, act, ldx, K, nullptr, 0.0f, accumulate);                         \
+  }                                                                                                  \
+  extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1f_##NAME##_w##W(QMM_GEMV_PARAMS) {   \
+    QMM_GEMV_JOBS                                                                                    \
+    qmm::gemv1<FMT, true, 4>(jobs, act, ldx, K, norm_w, eps, accumulate);                            \
+  }                                                                                                  \
+  extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1_##NAME##_w##W##_j8(QMM_GEMV_PARAMS8) { \
+    QMM_GEMV_JOBS8                                                                                   \
+    qmm::gemv1<FMT, false, 8>(jobs, act, ldx, K, nullptr, 0.0f, accumulate);                         \
+  }                                                                                                  \
+  extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1f_##NAME##_w##W##_j8(QMM_GEMV_PARAMS8) { \
+    QMM_GEMV_JOBS8                                                                                   \
+    qmm::gemv1<FMT, true, 8>(jobs, act, ldx, K, norm_w, eps, accumulate);                            \
   }
-#define QMM_GEMVFP_KERNEL(FMT, NAME, W, R, U)                                                         \
-  extern "C" __global__ void __launch_bounds__(64 * W)                                                \
-      qmm_gemvf_##NAME##_m1_w##W##_r##R##_u##U##_p(QMM_GEMV_PARAMS) {                                 \
-    QMM_GEMV_JOBS                                                                                     \
-    qmm::gemv_pipe<FMT, 1, R, U, true>(jobs, act, ldx, K, dump, 1, norm_w, eps, accumulate);          \
-  }
-#define QMM_GEMVP_KERNEL8(FMT, NAME, W, R, U)                                                         \
-  extern "C" __global__ void __launch_bounds__(64 * W)                                                \
-      qmm_gemv_##NAME##_m1_w##W##_r##R##_u##U##_j8_p(QMM_GEMV_PARAMS8) {                              \
-    QMM_GEMV_JOBS8                                                                                    \
-    qmm::gemv_pipe<FMT, 1, R, U, false, 8>(jobs, act, ldx, K, dump, 1, nullptr, 0.0f, accumulate);    \
-  }
-#define QMM_GEMVFP_KERNEL8(FMT, NAME, W, R, U)                                                        \
-  extern "C" __global__ void __launch_bounds__(64 * W)                                                \
-      qmm_gemvf_##NAME##_m1_w##W##_r##R##_u##U##_j8_p(QMM_GEMV_PARAMS8) {                             \
-    QMM_GEMV_JOBS8                                                                                    \
-    qmm::gemv_pipe<FMT, 1, R, U, true, 8>(jobs, act, ldx, K, dump, 1, norm_w, eps, accumulate);       \
-  }
-#define QMM_GEMV_PIPE_SHAPES(FMT, NAME) \
-  QMM_GEMVP_KERNEL(FMT, NAME, 4, 1, 1)  \
-  QMM_GEMVP_KERNEL(FMT, NAME, 8, 1, 1)  \
-  QMM_GEMVP_KERNEL(FMT, NAME, 16, 1, 1) \
-  QMM_GEMVP_KERNEL(FMT, NAME, 8, 2, 1)  \
-  QMM_GEMVP_KERNEL(FMT, NAME, 8, 1, 2)  \
-  QMM_GEMVP_KERNEL(FMT, NAME, 16, 1, 2) \
-  QMM_GEMVFP_KERNEL(FMT, NAME, 8, 1, 1)  \
-  QMM_GEMVFP_KERNEL(FMT, NAME, 16, 1, 1) \
-  QMM_GEMVFP_KERNEL(FMT, NAME, 8, 1, 2)  \
-  QMM_GEMVFP_KERNEL(FMT, NAME, 16, 1, 2) \
-  QMM_GEMVP_KERNEL8(FMT, NAME, 4, 1, 1)  \
-  QMM_GEMVP_KERNEL8(FMT, NAME, 8, 1, 1)  \
-  QMM_GEMVP_KERNEL8(FMT, NAME, 16, 1, 1) \
-  QMM_GEMVFP_KERNEL8(FMT, NAME, 8, 1, 1)  \
-  QMM_GEMVFP_KERNEL8(FMT, NAME, 16, 1, 1)
+#define QMM_GEMV1_SHAPES(FMT, NAME) \
+  QMM_GEMV1_KERNELS(FMT, NAME, 4)   \
+  QMM_GEMV1_KERNELS(FMT, NAME, 8)   \
+  QMM_GEMV1_KERNELS(FMT, NAME, 16)
 
 // Launch shapes: W waves per workgroup, R rows per wave, U load iterations per batch.
 #define QMM_GEMV_SHAPES_1(FMT, NAME)        \
@@ -977,7 +976,7 @@ __device__ __forceinline__ void gemv_pipe(const GemvJobs& jobs, const void* __re
   QMM_GEMV_SHAPES(FMT, NAME, 8)   \
   QMM_GEMVF_SHAPES(FMT, NAME, 1)  \
   QMM_GEMVF_SHAPES(FMT, NAME, 2)  \
-  QMM_GEMV_PIPE_SHAPES(FMT, NAME)
+  QMM_GEMV1_SHAPES(FMT, NAME)
 
 QMM_GEMV_ALL_M(qmm::kFmtQ4K, q4k)
 QMM_GEMV_ALL_M(qmm::kFmtQ6K, q6k)

@@ -70,13 +70,14 @@ Device* g_dev[64] = {};
 
 // Launch-shape overrides for tuning sweeps, read at every launch:
 // QMM_GEMV_CFG="W,R,U" (waves per workgroup, rows per wave, load iterations per
-// batch) and QMM_GEMV_WAVES_PER_CU (resident waves the grid is sized for).
+// batch), QMM_GEMV_WAVES_PER_CU (resident waves the grid is sized for) and
+// QMM_GEMV1=0 (use the general kernel for one activation row too).
 struct Tuning {
-  int w = 0, r = 0, u = 0, waves_per_cu = 0, pipe = -1;
+  int w = 0, r = 0, u = 0, waves_per_cu = 0, gemv1 = 1;
 };
 Tuning tuning() {
   Tuning t;
-  if (const char* s = getenv("QMM_GEMV_PIPE")) t.pipe = atoi(s);
+  if (const char* s = getenv("QMM_GEMV1")) t.gemv1 = atoi(s);
   if (const char* s = getenv("QMM_GEMV_CFG")) {
     if (sscanf(s, "%d,%d,%d", &t.w, &t.r, &t.u) != 3) t.w = t.r = t.u = 0;
   }
@@ -529,12 +530,16 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
     if (r > 2) r = 2;
     if (fused && wv < 8) wv = 8;
   }
-  // pipelined kernels (M = 1): the next batch is in flight while the current one is consumed
-  bool pipe = false;
-  if (tu.pipe >= 0) pipe = tu.pipe > 0 && m == 1 && dump == nullptr;
+  // One activation row without a block-dot dump: the lean one-row kernels
+  // (gemv1: activation slice kept in registers, one row per wave at a time).
+  const bool one = m == 1 && dump == nullptr && r == 1 && u == 1 && (wv == 4 || wv == 8 || wv == 16) &&
+                   tu.gemv1 != 0;
   char name[80];
-  snprintf(name, sizeof(name), "qmm_gemv%s_%s_m%d_w%d_r%d_u%d%s%s", fused ? "f" : "", fmt_name(fmt), m, wv, r, u,
-           jcap > 4 ? "_j8" : "", pipe ? "_p" : "");
+  if (one)
+    snprintf(name, sizeof(name), "qmm_gemv1%s_%s_w%d%s", fused ? "f" : "", fmt_name(fmt), wv, jcap > 4 ? "_j8" : "");
+  else
+    snprintf(name, sizeof(name), "qmm_gemv%s_%s_m%d_w%d_r%d_u%d%s", fused ? "f" : "", fmt_name(fmt), m, wv, r, u,
+             jcap > 4 ? "_j8" : "");
   long long wgs = (total + wv * r - 1) / (wv * r);
   const long long cap = ((long long)d->num_cu * waves_per_cu + wv - 1) / wv;
   if (wgs > cap) wgs = cap;
