@@ -86,7 +86,7 @@ QKVGU = ("q_proj", "k_proj", "v_proj", "gate_proj", "up_proj")  # the K = 4096 p
 
 
 def run_gemv_set(torch, dev, args):
-    from inference_amd import GgmlDType, qmm
+    from inference_amd import GgmlDType, QTensor, qmm
     from inference_amd.synth import normal
 
     dt = GgmlDType.Q4K
@@ -199,13 +199,36 @@ def run_gemv_set(torch, dev, args):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / (timing_reps * per_graph)
 
-    # per-shape single launches (pre-quantized activation)
+    # per-shape single launches (pre-quantized activation); each shape rotates
+    # its own copies over >= rotate_mb MiB, so no launch reads from the MALL
     per_shape = {}
     for name, n, k in GEMV_SET:
-        us = time_launch(lambda layer, name=name: gemv(layer, name))
+        wb = n * (k // 256) * 144
+        nc = max(2, -(-args.rotate_mb * 2 ** 20 // wb))
+        g = torch.Generator(device=dev)
+        g.manual_seed(7000 + n + k)
+        own = [{name: QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, dt)} for _ in range(nc)]
+        per = nc * max(1, 24 // nc)
+        gph = torch.cuda.CUDAGraph()
+        gemv(own[0], name)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(gph):
+            for r in range(per):
+                gemv(own[r % nc], name)
+        gph.replay()
+        torch.cuda.synchronize()
+        reps = max(2, 240 // per)
+        e0.record(stream)
+        for _ in range(reps):
+            gph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * per)
         b = gemv_bytes(dt, n, k)
         per_shape[name] = {"shape": [n, k], "us": round(us, 3), "GB/s": round(b / us / 1e3, 1),
-                           "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+                           "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "copies": nc}
+        del own, gph
+        torch.cuda.empty_cache()
 
     # dominant launch of the step
     if args.schedule == "serial":

@@ -212,6 +212,15 @@ int qmm_decode_rope_attention(const float *q, const float *k, const float *v, co
 int qmm_silu_mul_quantize(const float *g, const float *u, int64_t rows, int64_t k, int64_t ld, void *hq,
                           void *stream);
 
+/* The down projection of one token with its activation formed in the same
+ * launch: y (+)= QMatMul::forward(silu(g) * u), i.e. qmm_silu_mul_quantize
+ * followed by qmm_matmul_q_ex, with the Q8_K quantization done in the GEMV
+ * prologue (LlamaMlp::forward, llama.rs:1386-1391: down(silu(gate) * up)).
+ * g, u: f32 [w->k] (k-quant weights, k a multiple of 256); y: f32 [w->n];
+ * accumulate != 0 adds to y. Results are identical to the two-call form. */
+int qmm_silu_mul_matmul(const qmm_qtensor *w, const float *g, const float *u, float *y, int accumulate,
+                        void *stream);
+
 /* Workspace bytes of qmm_greedy_advance; the first 256 bytes are a counter
  * with the same zero-before-first-use contract as the attention workspace. */
 size_t qmm_greedy_workspace_size(int64_t n);

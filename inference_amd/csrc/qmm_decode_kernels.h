@@ -367,10 +367,7 @@ extern "C" __global__ void __launch_bounds__(256) qmm_silu_mul_q8k(const float* 
   const long long o = row * ld + 256LL * b + 4 * lane;
   float e[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float v = g[o + j];
-    e[j] = v / (1.0f + expf(-v)) * u[o + j];
-  }
+  for (int j = 0; j < 4; ++j) e[j] = qmm::silu_mul(g[o + j], u[o + j]);
   const qmm::Q8KLane q = qmm::q8k_lane_vals(e[0], e[1], e[2], e[3], lane);
   uint8_t* blk = hq + w * qmm::kQ8KBytes;
   reinterpret_cast<uint32_t*>(blk + 4)[lane] = q.packed;

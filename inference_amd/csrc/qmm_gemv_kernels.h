@@ -538,7 +538,10 @@ __device__ __forceinline__ void rms_denominators(const float* __restrict__ x, lo
 // Quantize mrows f32 rows (stride ldx) of nb blocks into the LDS layout. With
 // norm_w, each row is first RMS-normalised: x / sqrt(mean(x^2) + eps) * w
 // (rms_norm, crates/llm/candle-llm/src/primitives/nn.rs:22-31).
-template <int FMT>
+// With SILU, `x` is the gate row g and `norm_w` the up row u, and the
+// quantized activation is silu(g) * u (silu_mul, the same arithmetic as the
+// standalone qmm_silu_mul_q8k); no RMSNorm then.
+template <int FMT, bool SILU = false>
 __device__ __forceinline__ void quantize_act(const float* __restrict__ x, long long ldx, int mrows, int nb,
                                              uint8_t* lds, const float* __restrict__ norm_w, float eps) {
 #pragma clang fp contract(off)
@@ -546,7 +549,7 @@ __device__ __forceinline__ void quantize_act(const float* __restrict__ x, long l
   const int nblk = mrows * nb;
   __shared__ float den[8];
   __shared__ float red[8 * 16];
-  if (norm_w != nullptr)
+  if (!SILU && norm_w != nullptr)
     rms_denominators(x, ldx, mrows, nb * FmtInfo<FMT>::kBlockElems, eps, den, red);
   if constexpr (FMT == kFmtQ80) {
     float* ld = reinterpret_cast<float*>(lds + 32 * nblk);
@@ -560,8 +563,12 @@ __device__ __forceinline__ void quantize_act(const float* __restrict__ x, long l
       float e[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        e[j] = valid ? xs[j] : 0.0f;
-        if (norm_w != nullptr) e[j] = e[j] / den[row] * norm_w[col + j];
+        if (SILU) {
+          e[j] = valid ? silu_mul(xs[j], norm_w[row * ldx + col + j]) : 0.0f;
+        } else {
+          e[j] = valid ? xs[j] : 0.0f;
+          if (norm_w != nullptr) e[j] = e[j] / den[row] * norm_w[col + j];
+        }
       }
       float amax = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
       amax = fmaxf(amax, dpp_f<0xb1>(amax));
@@ -591,7 +598,13 @@ __device__ __forceinline__ void quantize_act(const float* __restrict__ x, long l
       const int row = blk / nb, col = 256 * (blk % nb) + 4 * lane;
       const float* xs = x + row * ldx + col;
       float e0 = xs[0], e1 = xs[1], e2 = xs[2], e3 = xs[3];
-      if (norm_w != nullptr) {
+      if (SILU) {
+        const float* us = norm_w + row * ldx + col;
+        e0 = silu_mul(e0, us[0]);
+        e1 = silu_mul(e1, us[1]);
+        e2 = silu_mul(e2, us[2]);
+        e3 = silu_mul(e3, us[3]);
+      } else if (norm_w != nullptr) {
         const float dn = den[row];
         e0 = e0 / dn * norm_w[col];
         e1 = e1 / dn * norm_w[col + 1];
@@ -626,6 +639,95 @@ __device__ __forceinline__ void flush_outputs(const GemvJobs& jobs, int nb, floa
     __hip_atomic_fetch_add(yp, keep_v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   else
     *yp = keep_v;
+}
+
+// One-row prologue of the fused one-row GEMV (k-quant weights): every load
+// of the activation row goes out before any block is quantized, so the
+// prologue costs one memory round trip instead of one per block a wave owns.
+// Wave w owns blocks w, w + nw, ... (up to kActPF of them; longer rows take
+// quantize_act). RMSNorm (norm_w, not SILU) sums the squares from the same
+// registers: lanes, then DPP rows and v_readlane, then waves in order.
+constexpr int kActPF = 4;
+
+template <int FMT, bool SILU>
+__device__ __forceinline__ void quantize_act1(const float* __restrict__ x, int nb, uint8_t* lds,
+                                              const float* __restrict__ norm_w, float eps) {
+#pragma clang fp contract(off)
+  static_assert(FMT != kFmtQ80, "k-quant activations");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if (nb > kActPF * nw) {
+    quantize_act<FMT, SILU>(x, 0, 1, nb, lds, norm_w, eps);
+    return;
+  }
+  __shared__ float red[16];
+  __shared__ float den1;
+  float4 e[kActPF], a[kActPF];
+  const bool aux = SILU || norm_w != nullptr;
+#pragma unroll
+  for (int i = 0; i < kActPF; ++i) {
+    const int blk = wave + i * nw;
+    e[i] = a[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (blk < nb) {
+      e[i] = *reinterpret_cast<const float4*>(x + 256 * blk + 4 * lane);
+      if (aux) a[i] = *reinterpret_cast<const float4*>(norm_w + 256 * blk + 4 * lane);
+    }
+  }
+  if (!SILU && norm_w != nullptr) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kActPF; ++i) {
+      ss += e[i].x * e[i].x;
+      ss += e[i].y * e[i].y;
+      ss += e[i].z * e[i].z;
+      ss += e[i].w * e[i].w;
+    }
+    ss = wave_total(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float t = 0.0f;
+      for (int w = 0; w < nw; ++w) t += red[w];
+      den1 = sqrtf(t / (float)(256 * nb) + eps);
+    }
+    __syncthreads();
+    const float dn = den1;
+#pragma unroll
+    for (int i = 0; i < kActPF; ++i) {
+      e[i].x = e[i].x / dn * a[i].x;
+      e[i].y = e[i].y / dn * a[i].y;
+      e[i].z = e[i].z / dn * a[i].z;
+      e[i].w = e[i].w / dn * a[i].w;
+    }
+  } else if (SILU) {
+#pragma unroll
+    for (int i = 0; i < kActPF; ++i) {
+      e[i].x = silu_mul(e[i].x, a[i].x);
+      e[i].y = silu_mul(e[i].y, a[i].y);
+      e[i].z = silu_mul(e[i].z, a[i].z);
+      e[i].w = silu_mul(e[i].w, a[i].w);
+    }
+  }
+  uint32_t* lsum = reinterpret_cast<uint32_t*>(lds + 256 * nb);
+  float* ld = reinterpret_cast<float*>(lsum + 8 * nb);
+  const int c16 = lane >> 2;
+  int lc, kc;
+  chunk_owner<FMT>(c16, lc, kc);
+#pragma unroll
+  for (int i = 0; i < kActPF; ++i) {
+    const int blk = wave + i * nw;
+    if (blk >= nb) break;  // wave-uniform
+    const Q8KLane q = q8k_lane_vals(e[i].x, e[i].y, e[i].z, e[i].w, lane);
+    *reinterpret_cast<uint32_t*>(lds + 256 * blk + 16 * kq_slot(blk, lc, kc) + 4 * (lane & 3)) = q.packed;
+    const int next = __shfl_down(q.sum16, 4);  // the following 16-group's sum
+    if (FMT == kFmtQ4K) {
+      const int s32 = q.sum16 + next;
+      const int s32n = __shfl_down(s32, 8);
+      if ((lane & 15) == 0) lsum[8 * blk + (lane >> 4)] = ((uint32_t)s32 & 0xffffu) | ((uint32_t)s32n << 16);
+    } else {
+      if ((lane & 7) == 0) lsum[8 * blk + 2 * lc + (kc >> 1)] = ((uint32_t)q.sum16 & 0xffffu) | ((uint32_t)next << 16);
+    }
+    if (lane == 0) ld[blk] = q.d;
+  }
 }
 
 // y_j[m, n] = sum_b dot(W_j[n, b], X[m, b]) for every job j, m < M, n < rows_j.
@@ -767,7 +869,7 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
 //   * the row sum is reduced with DPP and v_readlane (no LDS round trip);
 //   * outputs are kept one per lane and written 64 at a time.
 // Same per-block arithmetic (prep_w / dot_wx) as gemv(); no block-dot dump.
-template <int FMT, bool FUSED, int J>
+template <int FMT, bool FUSED, int J, bool SILU = false>
 __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restrict__ act, long long ldx, int K,
                                       const float* __restrict__ norm_w, float eps, int accumulate) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -790,8 +892,12 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
   const uint32_t b0 = (uint32_t)min(g, nb - 1);  // clamped: every lane loads
   RowRef rr = cursor_row<FMT>(jc, ja, jobs.njobs, jobs.total, min(row, jobs.total - 1), nb);
   load_slice<FMT>(ws, rr.wrow, rr.drow, b0, l);  // first row in flight before staging
-  if constexpr (FUSED)
-    quantize_act<FMT>(reinterpret_cast<const float*>(act), ldx, 1, nb, lds, norm_w, eps);
+  if constexpr (FUSED) {
+    if constexpr (FMT == kFmtQ80)
+      quantize_act<FMT, SILU>(reinterpret_cast<const float*>(act), ldx, 1, nb, lds, norm_w, eps);
+    else
+      quantize_act1<FMT, SILU>(reinterpret_cast<const float*>(act), nb, lds, norm_w, eps);
+  }
   else
     stage_act<FMT>(reinterpret_cast<const uint8_t*>(act), nb, lds);
   __syncthreads();
@@ -924,10 +1030,18 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
     QMM_GEMV_JOBS8                                                                                   \
     qmm::gemv1<FMT, true, 8>(jobs, act, ldx, K, norm_w, eps, accumulate);                            \
   }
+// silu(g) * u quantized in the prologue (act = g, norm_w = u).
+#define QMM_GEMV1S_KERNEL(FMT, NAME, W)                                                              \
+  extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1s_##NAME##_w##W(QMM_GEMV_PARAMS) {   \
+    QMM_GEMV_JOBS                                                                                    \
+    qmm::gemv1<FMT, true, 4, true>(jobs, act, ldx, K, norm_w, 0.0f, accumulate);                     \
+  }
 #define QMM_GEMV1_SHAPES(FMT, NAME) \
   QMM_GEMV1_KERNELS(FMT, NAME, 4)   \
   QMM_GEMV1_KERNELS(FMT, NAME, 8)   \
-  QMM_GEMV1_KERNELS(FMT, NAME, 16)
+  QMM_GEMV1_KERNELS(FMT, NAME, 16)  \
+  QMM_GEMV1S_KERNEL(FMT, NAME, 8)   \
+  QMM_GEMV1S_KERNEL(FMT, NAME, 16)
 
 // Launch shapes: W waves per workgroup, R rows per wave, U load iterations per batch.
 #define QMM_GEMV_SHAPES_1(FMT, NAME)        \

@@ -470,7 +470,8 @@ struct GemvTarget {
 // and k) sharing one activation. `act` is m rows of quantized blocks, or f32
 // rows with stride ldx when `fused` (then the kernel quantizes in its prologue).
 static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, bool fused, int64_t ldx, int m,
-                int* dump, hipStream_t s, const float* norm_w = nullptr, float eps = 0.0f, int accumulate = 0) {
+                int* dump, hipStream_t s, const float* norm_w = nullptr, float eps = 0.0f, int accumulate = 0,
+                bool silu = false) {
   if (count > 4 && m != 1) {  // eight-job kernels exist for m == 1 only: two launches
     QMM_TRY(gemv(d, tg, 4, act, fused, ldx, m, dump, s, norm_w, eps, accumulate));
     return gemv(d, tg + 4, count - 4, act, fused, ldx, m, dump, s, norm_w, eps, accumulate);
@@ -535,7 +536,13 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   const bool one = m == 1 && dump == nullptr && r == 1 && u == 1 && (wv == 4 || wv == 8 || wv == 16) &&
                    tu.gemv1 != 0;
   char name[80];
-  if (one)
+  if (silu) {
+    // silu(g) * u in the prologue: one-row kernels with a four-job table, 8 or 16 waves
+    if (!fused || m != 1 || dump || count > 4) return fail(QMM_ERR_INVALID, "silu prologue needs one fused row");
+    wv = wv >= 16 ? 16 : 8;
+    r = u = 1;
+    snprintf(name, sizeof(name), "qmm_gemv1s_%s_w%d", fmt_name(fmt), wv);
+  } else if (one)
     snprintf(name, sizeof(name), "qmm_gemv1%s_%s_w%d%s", fused ? "f" : "", fmt_name(fmt), wv, jcap > 4 ? "_j8" : "");
   else
     snprintf(name, sizeof(name), "qmm_gemv%s_%s_m%d_w%d_r%d_u%d%s", fused ? "f" : "", fmt_name(fmt), m, wv, r, u,
@@ -696,6 +703,17 @@ int qmm_matmul_multi_q(const qmm_qtensor* const* w, int count, const void* xq, i
   Device* d;
   QMM_TRY(current_device(&d));
   return gemv(d, tg, count, xq, false, 0, (int)m, nullptr, (hipStream_t)stream);
+}
+
+int qmm_silu_mul_matmul(const qmm_qtensor* w, const float* g, const float* u, float* y, int accumulate,
+                        void* stream) {
+  QMM_TRY(check_matmul(w, 1, y, w ? w->n : 0));
+  if (!g || !u) return fail(QMM_ERR_INVALID, "null activation");
+  if (w->dtype != QMM_Q4K && w->dtype != QMM_Q6K) return fail(QMM_ERR_UNSUPPORTED, "silu prologue needs a k-quant weight");
+  Device* d;
+  QMM_TRY(current_device(&d));
+  GemvTarget t = {w, y, w->n};
+  return gemv(d, &t, 1, g, true, w->k, 1, nullptr, (hipStream_t)stream, u, 0.0f, accumulate ? 1 : 0, true);
 }
 
 int qmm_matmul_q_ex(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int64_t ldy, int accumulate,

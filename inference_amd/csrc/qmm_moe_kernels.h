@@ -117,8 +117,7 @@ extern "C" __global__ void qmm_silu_mul(const float* __restrict__ g, const float
 #pragma clang fp contract(off)
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const float v = g[i];
-  h[i] = v / (1.0f + expf(-v)) * u[i];
+  h[i] = qmm::silu_mul(g[i], u[i]);
 }
 
 // out[t][n] = sum over the pairs of token t (in increasing expert order) of

@@ -24,6 +24,13 @@ namespace qmm {
 // ---------------------------------------------------------------------------
 // Lane-local result of quantizing one 256-element block (lane owns elements
 // 4*lane .. 4*lane+3).
+// silu(g) * u as LlamaMlp::forward computes it (crates/llm/candle-llm/src/models/llama.rs:1386-1391):
+// g / (1 + exp(-g)) * u, each operation rounded on its own.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+#pragma clang fp contract(off)
+  return g / (1.0f + expf(-g)) * u;
+}
+
 struct Q8KLane {
   uint32_t packed;  // its four int8 quants
   int sum16;        // sum of the 16-element group it belongs to

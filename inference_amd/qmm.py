@@ -48,7 +48,7 @@ EXPORTS = (
     "qmm_moe_ffn", "qmm_matmul_ex", "qmm_matmul_ex_workspace_size", "qmm_rms_norm", "qmm_embed_rows",
     "qmm_rope_kv_append", "qmm_decode_attention", "qmm_silu_mul_quantize", "qmm_greedy_advance",
     "qmm_matmul_q_ex", "qmm_decode_attention_workspace_size", "qmm_decode_rope_attention",
-    "qmm_greedy_workspace_size", "qmm_matmul_multi_q",
+    "qmm_greedy_workspace_size", "qmm_matmul_multi_q", "qmm_silu_mul_matmul",
 )
 
 
@@ -104,6 +104,7 @@ def lib() -> ctypes.CDLL:
             "qmm_silu_mul_quantize": ([vp, vp, i64, i64, i64, vp, vp], i32),
             "qmm_greedy_advance": ([vp, i64, vp, i64, vp, i32, vp, sz, vp], i32),
             "qmm_matmul_q_ex": ([vp, vp, i64, vp, i64, i32, vp], i32),
+            "qmm_silu_mul_matmul": ([vp, vp, vp, vp, i32, vp], i32),
             "qmm_matmul_multi_q": ([ctypes.POINTER(vp), i32, vp, i64, ctypes.POINTER(vp), ctypes.POINTER(i64), vp],
                                    i32),
         }

@@ -126,6 +126,15 @@ class OpChecker:
                                        self.hq[None], ex["layers"][li]["down"], c.ffn)[0]
             self.note("down", rel_err(x2 - self.x, want), MM_TOL)
             self.x = x2
+        elif op == "silu_down":
+            # the activation is quantized inside the launch: the oracle quantizes silu(g) * u itself
+            # (exp vs expf may move one quantum at a rounding tie, far inside the matmul tolerance)
+            x2 = self.snap(s.x)
+            h = (ol.silu(self.g) * self.u).astype(np.float32)
+            hq = orc.quantize(orc.Q8K, h[None])
+            want = orc.matmul_prequant(int(c.dtypes["down"]), hq, ex["layers"][li]["down"], c.ffn)[0]
+            self.note("down", rel_err(x2 - self.x, want), MM_TOL)
+            self.x = x2
         elif op == "head":
             self.lg = self.snap(s.logits)
             self.note("head", rel_err(self.lg, self.mm("head", 0, ol.rms_norm(self.x, ex["final_norm"], c.eps),

@@ -242,6 +242,38 @@ def test_silu_mul_quantize():
     assert (got != want).mean() < 0.01
 
 
+@pytest.mark.parametrize("dt,n,k", [(GgmlDType.Q6K, 4096, 14336), (GgmlDType.Q4K, 1000, 3072),
+                                    (GgmlDType.Q6K, 777, 1536)])
+@pytest.mark.parametrize("accumulate", [0, 1])
+def test_silu_mul_matmul_equals_two_calls(dt, n, k, accumulate):
+    # the fused down projection (Q8_K of silu(g) * u formed in the GEMV prologue) against the
+    # two-call form (qmm_silu_mul_quantize + qmm_matmul_q_ex): bit-identical outputs
+    rng = np.random.default_rng(90 + n)
+    qt = QTensor.quantize(t((rng.standard_normal((n, k)) * 0.02).astype(np.float32)), dt)
+    g = t((rng.standard_normal(k) * 2).astype(np.float32))
+    u = t(rng.standard_normal(k).astype(np.float32))
+    y0 = rng.standard_normal(n).astype(np.float32)
+    ya, yb = t(y0), t(y0)
+    hq = torch.zeros(k // 256 * 292, dtype=torch.uint8, device=DEV)
+    qmm._check(L().qmm_silu_mul_quantize(g.data_ptr(), u.data_ptr(), 1, k, k, hq.data_ptr(), S()))
+    qmm._check(L().qmm_matmul_q_ex(qt.handle, hq.data_ptr(), 1, ya.data_ptr(), n, accumulate, S()))
+    qmm._check(L().qmm_silu_mul_matmul(qt.handle, g.data_ptr(), u.data_ptr(), yb.data_ptr(), accumulate, S()))
+    torch.cuda.synchronize()
+    assert torch.equal(ya, yb)
+    # and the oracle on the device's own activation bytes
+    want = orc.matmul_prequant(int(dt), hq.cpu().numpy()[None], qt.to_ggml(), k)[0]
+    got = yb.cpu().numpy() - (y0 if accumulate else 0)
+    assert rel_err(got, want) <= 1e-3
+
+
+def test_silu_mul_matmul_rejects_q8_0():
+    qt = QTensor.quantize(torch.zeros((64, 256), device=DEV), GgmlDType.Q8_0)
+    x = torch.zeros(256, device=DEV)
+    y = torch.zeros(64, device=DEV)
+    rc = L().qmm_silu_mul_matmul(qt.handle, x.data_ptr(), x.data_ptr(), y.data_ptr(), 0, S())
+    assert rc != 0 and "k-quant" in qmm.last_error()
+
+
 def test_greedy_advance():
     logits = t(np.array([0.5, 3.0, -1.0, 3.0, 2.0], np.float32))
     toks = t(np.array([4, 4, 4, 0, 0, 0], np.int32), torch.int32)
