@@ -592,6 +592,25 @@ static int gemm(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, f
   int* dp = dump;
   void* args[] = {&wq, &q8, &dd, &ss, &yy, &M, &N, &K, &ld, &dp, &accumulate};
   hipFunction_t f;
+  // Q4_K: the second-generation kernel, 128x128 tiles (one workgroup of 512
+  // threads per CU, double-buffered LDS of 2 x 58 KB). QMM_MMQ2="BM,BN" picks
+  // 64-row tiles instead.
+  int bm = 128, bn = 128;
+  if (const char* e = getenv("QMM_MMQ2")) {
+    int a = 0, b = 0;
+    if (sscanf(e, "%d,%d", &a, &b) == 2 && (a == 64 || a == 128) && (b == 64 || b == 128) && !(a == 128 && b == 64)) {
+      bm = a;
+      bn = b;
+    }
+  }
+  const unsigned lds2 = (unsigned)(2 * (bm * 272 + bn * 160 + bm * 4 + bm * 16));
+  if (fmt == kFmtQ4K && (int)lds2 <= d->max_lds && getenv("QMM_MMQ1") == nullptr) {
+    snprintf(name, sizeof(name), "qmm_mmq2_q4k_m%d_n%d%s", bm, bn, dump ? "_dump" : "");
+    QMM_TRY(kernel(d, name, &f));
+    QMM_HIP(hipModuleLaunchKernel(f, (unsigned)((N + bn - 1) / bn), (unsigned)((M + bm - 1) / bm), 1,
+                                  (unsigned)(bm * bn / 32), 1, 1, lds2, s, args, nullptr));
+    return QMM_OK;
+  }
   QMM_TRY(kernel(d, name, &f));
   const unsigned gx = (unsigned)((N + 127) / 128), gy = (unsigned)((M + 63) / 64);
   QMM_HIP(hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, s, args, nullptr));

@@ -473,3 +473,236 @@ extern "C" __global__ void __launch_bounds__(256) qmm_q8_blocks_to_planes(const 
     d[b] = qmm::h2f(src[0]);
   }
 }
+
+// ---------------------------------------------------------------------------
+// Q4_K prefill GEMM, second generation: larger tiles, raw weight blocks in LDS.
+//   * workgroup tile BM (64 or 128) rows x BN (64 or 128) columns; waves of
+//     64 x 32 outputs (two v_mfma_i32_32x32x32_i8 tiles), BM/64 x BN/32 of
+//     them; 64-row tiles keep a workgroup's LDS small enough for two per CU,
+//     so one workgroup's MFMAs cover the other's loads;
+//   * per 256-wide K step the activation rows (int8 planes) and the weight
+//     columns' Q4_K blocks are copied to LDS unchanged (double-buffered, the
+//     next step's global loads in flight during this step's MFMAs); a lane's
+//     16-byte read of a block's quants yields the B operands of two
+//     sub-blocks (low and high nibbles), and the scales/mins of all eight
+//     sub-blocks are unpacked byte-parallel from the block header;
+//   * per sub-block j: P = MFMA(x, q4) and isd += sc_j * P (24-bit); the mins
+//     term ism = sum_j m_j * (32-sums)_j is two zero-padded MFMAs (sums split
+//     into a 6-bit low byte and a signed high byte); then
+//     y += dx * (d * isd - dmin * ism) once per step.
+// The integer block dots are the same as mmq()'s (DUMP writes them).
+// ---------------------------------------------------------------------------
+namespace qmm {
+
+constexpr int kM2AStride = 256 + 16;  // activation row in LDS (16-byte skew)
+constexpr int kM2BStride = 144 + 16;  // weight block in LDS
+
+template <int BM, int BN>
+struct M2 {
+  static constexpr int kWM = BM / 64, kWN = BN / 32;  // waves along M and N
+  static constexpr int kThreads = 64 * kWM * kWN;
+  static constexpr int kA = BM * kM2AStride;
+  static constexpr int kB = BN * kM2BStride;
+  static constexpr int kDx = BM * 4;
+  static constexpr int kSum = BM * 16;
+  static constexpr int kStage = kA + kB + kDx + kSum;  // bytes of one buffer
+  static constexpr int kBytes = 2 * kStage;
+  static constexpr int kAPer = BM * 16 / kThreads;                  // activation uint4 per thread
+  static constexpr int kBPer = (BN * 9 + kThreads - 1) / kThreads;  // weight uint4 per thread
+  static_assert(BM * 16 % kThreads == 0 && BM <= kThreads, "tile / thread count");
+};
+
+// Global loads of one K step into registers.
+template <int BM, int BN>
+struct M2Regs {
+  uint4 a[M2<BM, BN>::kAPer];
+  uint4 b[M2<BM, BN>::kBPer];
+  float dx;  // t < BM: activation scale of row t
+  uint4 s;   // t < BM: eight int16 32-element sums of row t
+};
+
+template <int BM, int BN>
+__device__ __forceinline__ void m2_load(M2Regs<BM, BN>& R, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                        const int16_t* __restrict__ xs, const uint8_t* __restrict__ wq, int M, int N,
+                                        int K, int m0, int n0, int kb) {
+  using C = M2<BM, BN>;
+  const int t = threadIdx.x, nbk = K / 256;
+#pragma unroll
+  for (int u = 0; u < C::kAPer; ++u) {
+    const int idx = t + C::kThreads * u, row = m0 + (idx >> 4);
+    const bool ok = row < M;
+    R.a[u] = ok ? reinterpret_cast<const uint4*>(xq + (size_t)row * K + 256 * kb)[idx & 15] : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int u = 0; u < C::kBPer; ++u) {
+    const int idx = t + C::kThreads * u, col = idx / 9, piece = idx % 9;
+    R.b[u] = make_uint4(0, 0, 0, 0);
+    if (idx < BN * 9 && n0 + col < N)
+      R.b[u] = reinterpret_cast<const uint4*>(wq + ((size_t)(n0 + col) * nbk + kb) * kQ4KBytes)[piece];
+  }
+  if (t < BM) {
+    const int row = m0 + t;
+    const bool ok = row < M;
+    R.dx = ok ? xd[(size_t)row * nbk + kb] : 0.0f;
+    R.s = ok ? *reinterpret_cast<const uint4*>(xs + ((size_t)row * nbk + kb) * 8) : make_uint4(0, 0, 0, 0);
+  }
+}
+
+template <int BM, int BN>
+__device__ __forceinline__ void m2_store(const M2Regs<BM, BN>& R, uint8_t* buf) {
+  using C = M2<BM, BN>;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < C::kAPer; ++u) {
+    const int idx = t + C::kThreads * u;
+    *reinterpret_cast<uint4*>(buf + (idx >> 4) * kM2AStride + 16 * (idx & 15)) = R.a[u];
+  }
+#pragma unroll
+  for (int u = 0; u < C::kBPer; ++u) {
+    const int idx = t + C::kThreads * u, col = idx / 9, piece = idx % 9;
+    if (idx < BN * 9) *reinterpret_cast<uint4*>(buf + C::kA + col * kM2BStride + 16 * piece) = R.b[u];
+  }
+  if (t < BM) {
+    reinterpret_cast<float*>(buf + C::kA + C::kB)[t] = R.dx;
+    // 32-element sums s (|s| <= 4096) as s = 64 * hi + lo: lo in [0, 63], hi in [-64, 64]
+    const int16_t* sv = reinterpret_cast<const int16_t*>(&R.s);
+    uint32_t lo[2] = {0, 0}, hi[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int v = sv[j];
+      lo[j >> 2] |= (uint32_t)(v & 63) << (8 * (j & 3));
+      hi[j >> 2] |= (uint32_t)((v >> 6) & 0xff) << (8 * (j & 3));
+    }
+    *reinterpret_cast<uint4*>(buf + C::kA + C::kB + C::kDx + 16 * t) = make_uint4(lo[0], lo[1], hi[0], hi[1]);
+  }
+}
+
+template <int BM, int BN, bool DUMP>
+__device__ __forceinline__ void mmq2_q4k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,
+                                         const float* __restrict__ xd, const int16_t* __restrict__ xs,
+                                         float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,
+                                         int accumulate) {
+  using C = M2<BM, BN>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int nbk = K / 256;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int wm = wave % C::kWM, wn = wave / C::kWM;
+  const int arow0 = 64 * wm + r;  // + 32 i: A operand row of tile i
+  const int bcol = 32 * wn + r;   // B operand column within the workgroup tile
+  const int col = n0 + bcol;      // this lane's output column
+
+  i32x16 zero;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) zero[j] = 0;
+  float acc[2][16];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[i][j] = 0.0f;
+
+  M2Regs<BM, BN> R;
+  m2_load<BM, BN>(R, xq, xd, xs, wq, M, N, K, m0, n0, 0);
+  m2_store<BM, BN>(R, lds);
+  __syncthreads();
+  for (int kb = 0; kb < nbk; ++kb) {
+    uint8_t* buf = lds + (kb & 1) * C::kStage;
+    if (kb + 1 < nbk) m2_load<BM, BN>(R, xq, xd, xs, wq, M, N, K, m0, n0, kb + 1);
+    const int8_t* A = reinterpret_cast<const int8_t*>(buf);
+    const uint8_t* Bc = buf + C::kA + bcol * kM2BStride;  // this lane's weight block
+    const float* DX = reinterpret_cast<const float*>(buf + C::kA + C::kB);
+    const uint8_t* SUM = buf + C::kA + C::kB + C::kDx;
+
+    // scales / mins of the lane's column: byte j of (lo, hi) is sub-block j
+    const uint4 hd = *reinterpret_cast<const uint4*>(Bc);
+    const float dw = h2f(hd.x), dm = h2f(hd.x >> 16);
+    const uint32_t sclo = hd.y & 0x3f3f3f3fu, schi = (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u);
+    const uint32_t mnlo = hd.z & 0x3f3f3f3fu, mnhi = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
+
+    int isd[2][16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) isd[i][j] = 0;
+#pragma unroll 1
+    for (int c2 = 0; c2 < 4; ++c2) {
+      const uint4 qv = *reinterpret_cast<const uint4*>(Bc + 16 + 32 * c2 + 16 * h);
+      const uint4 blo = make_uint4(qv.x & 0x0f0f0f0fu, qv.y & 0x0f0f0f0fu, qv.z & 0x0f0f0f0fu, qv.w & 0x0f0f0f0fu);
+      const uint4 bhi = make_uint4((qv.x >> 4) & 0x0f0f0f0fu, (qv.y >> 4) & 0x0f0f0f0fu, (qv.z >> 4) & 0x0f0f0f0fu,
+                                   (qv.w >> 4) & 0x0f0f0f0fu);
+      const uint32_t scw = c2 < 2 ? sclo : schi;
+      const int s0 = (int)((scw >> (16 * (c2 & 1))) & 0xffu), s1 = (int)((scw >> (16 * (c2 & 1) + 8)) & 0xffu);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int8_t* ar = A + (arow0 + 32 * i) * kM2AStride + 64 * c2 + 16 * h;
+        const i32x16 P0 = mfma_i8(*reinterpret_cast<const i8x16*>(ar), as_i8x16(blo), zero);
+        const i32x16 P1 = mfma_i8(*reinterpret_cast<const i8x16*>(ar + 32), as_i8x16(bhi), zero);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) isd[i][e] += __mul24(s0, P0[e]) + __mul24(s1, P1[e]);  // |P| < 2^23
+      }
+    }
+    // mins term and the float update
+    const uint4 zero4 = make_uint4(0, 0, 0, 0);
+    const i8x16 bm = as_i8x16(h == 0 ? make_uint4(mnlo, mnhi, 0, 0) : zero4);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint4 sv = *reinterpret_cast<const uint4*>(SUM + 16 * (arow0 + 32 * i));
+      const i8x16 alo = as_i8x16(h == 0 ? make_uint4(sv.x, sv.y, 0, 0) : zero4);
+      const i8x16 ahi = as_i8x16(h == 0 ? make_uint4(sv.z, sv.w, 0, 0) : zero4);
+      const i32x16 Lo = mfma_i8(alo, bm, zero), Hi = mfma_i8(ahi, bm, zero);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 dx = *reinterpret_cast<const float4*>(DX + 64 * wm + 32 * i + 8 * g + 4 * h);
+        const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int e = 4 * g + q;
+          const int ism = Hi[e] * 64 + Lo[e];
+          acc[i][e] += dxs[q] * (dw * (float)isd[i][e] - dm * (float)ism);
+          if (DUMP) {
+            const int row = m0 + 64 * wm + 32 * i + 8 * g + 4 * h + q;
+            if (row < M && col < N) {
+              const size_t o = ((size_t)row * N + col) * nbk + kb;
+              dump[2 * o] = isd[i][e];
+              dump[2 * o + 1] = ism;
+            }
+          }
+        }
+      }
+    }
+    if (kb + 1 < nbk) m2_store<BM, BN>(R, lds + ((kb + 1) & 1) * C::kStage);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int row = m0 + 64 * wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+      if (row < M && col < N) {
+        float* yp = y + (size_t)row * ldy + col;
+        *yp = accumulate ? *yp + acc[i][e] : acc[i][e];
+      }
+    }
+}
+
+}  // namespace qmm
+
+#define QMM_MMQ2_KERNEL(BM, BN)                                                                                \
+  extern "C" __global__ void __launch_bounds__(BM * BN / 32) __attribute__((amdgpu_waves_per_eu(2 * 64 / BM)))     \
+      qmm_mmq2_q4k_m##BM##_n##BN(                                                                            \
+      const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq, const float* __restrict__ xd,           \
+      const int16_t* __restrict__ xs, float* __restrict__ y, int M, int N, int K, int ldy,                   \
+      int* __restrict__ dump, int accumulate) {                                                              \
+    qmm::mmq2_q4k<BM, BN, false>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate);                         \
+  }                                                                                                          \
+  extern "C" __global__ void __launch_bounds__(BM * BN / 32) qmm_mmq2_q4k_m##BM##_n##BN##_dump(              \
+      const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq, const float* __restrict__ xd,           \
+      const int16_t* __restrict__ xs, float* __restrict__ y, int M, int N, int K, int ldy,                   \
+      int* __restrict__ dump, int accumulate) {                                                              \
+    qmm::mmq2_q4k<BM, BN, true>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate);                          \
+  }
+
+QMM_MMQ2_KERNEL(128, 128)
+QMM_MMQ2_KERNEL(64, 128)
+QMM_MMQ2_KERNEL(64, 64)

@@ -349,7 +349,7 @@ GEMM_CASES = [(GgmlDType.Q4K, 100, 512), (GgmlDType.Q4K, 300, 1024), (GgmlDType.
 
 
 @pytest.mark.parametrize("dt,n,k", GEMM_CASES)
-@pytest.mark.parametrize("m", [9, 64, 100])
+@pytest.mark.parametrize("m", [9, 64, 100, 257])
 def test_gemm_block_dots_bit_exact(dt, n, k, m):
     w = np.concatenate([normal(170, (n, k), 0.02), special_weight_rows(k)[:4]])
     wq = orc.quantize(ORC[dt], w)
