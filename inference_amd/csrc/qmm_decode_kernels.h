@@ -58,72 +58,98 @@ extern "C" __global__ void qmm_decode_rope_kv(float* __restrict__ q, float* __re
   }
 }
 
-// One query token against positions 0..p of the cache (p = pos[0]),
-// split over positions ("flash decoding") in two launches.
+// One query token against positions 0..p of the cache (p = pos[0]) in one
+// launch ("flash decoding" with the merge done by the last workgroup).
 //
-// qmm_decode_attention_split: workgroup (g, c) of a kv_heads x S grid takes
-// the G = heads / kv_heads query heads of kv head g (repeat_kv maps query
-// head h to kv head h / G) and the c-th of S contiguous chunks of the
-// n = p + 1 positions, and writes per head the chunk's softmax state:
-// m = max_j s_j, l = sum_j exp(s_j - m), o = sum_j exp(s_j - m) v_j, with
-// s_j = (q . k_j) * scale (m = -inf, l = 0, o = 0 for an empty chunk).
-// qmm_decode_attention_merge then forms, per head,
-// out = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c, M = max_c m_c,
-// adding the chunks in chunk order. The launch boundary orders the two.
+// Workgroup (g, c) of a kv_heads x S grid takes the G = heads / kv_heads
+// query heads of kv head g (repeat_kv maps query head h to kv head h / G)
+// and the c-th of S contiguous chunks of the n = p + 1 positions. Its four
+// waves scan the chunk's positions round-robin straight from the cache: lane
+// l holds dims [l * dim/64, (l+1) * dim/64) of q, k_j and v_j, so a score
+// s_j = (q . k_j) * scale is a wave-wide sum (DPP + v_readlane) and the
+// softmax runs online per wave, a batch of positions at a time (m = running
+// max, l = sum exp(s - m), o = sum exp(s - m) v). The next batch's k/v rows
+// are loaded while the current batch is scored. The waves' states are combined through LDS into the
+// chunk's record (m, l, o[dim]) per head. Records are stored with
+// device-scope (agent) atomic stores, which write through the XCD's L2 to
+// the device-coherent level; after s_waitcnt vmcnt(0) and a barrier, one
+// thread bumps the kv head's counter with a device-scope atomic. The
+// workgroup that brings it to S is the last of its kv head: it reads the S
+// records back with device-scope atomic loads (coherent, not served from a
+// stale L2 line), forms out = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c
+// (M = max_c m_c, chunks in order) and resets the counter to zero, so the
+// workspace is ready for the next launch.
 //
 // With cos/sin (fused RoPE + KV append), q and k are the unrotated
-// projections: q is rotated in LDS; the workgroup whose chunk holds p
-// rotates k, appends k and v at position p of the cache and uses them for
-// that position. Without cos/sin, q is already rotated and the cache already
-// holds position p.
-//
-// The kernel is a chain of memory latencies, so its loads go out in two
-// batches: pos, q and the new k/v rows (independent of each other), then
-// the chunk's first K tile, its first v rows and the cos/sin rows (all
-// functions of p only). K tiles sit in LDS rows padded to dim + 1 floats
-// (conflict-free column reads); scores are one (position, head) per thread;
-// v rows are read once per workgroup, each thread accumulating one float4
-// column over a slot of rows. dim is 64, 128 or 256, G <= 8, chunk length
-// <= 256 (max_seq <= 256 S).
+// projections: q is rotated in registers (the partner of dim d is in lane
+// l ^ 32); the workgroup whose chunk holds p rotates k, appends k and v at
+// position p of the cache and uses them for that position. Without cos/sin,
+// q is already rotated and the cache already holds position p.
+// dim = 64 * DPL (64, 128, 256); G <= GT (1, 2, 4, 8).
 namespace qmm {
-constexpr int kAttnMaxG = 8;
-constexpr int kAttnMaxChunk = 256;
-constexpr int kAttnTileFloats = 8192;
-constexpr int kAttnSplits = 16;  // S
-}  // namespace qmm
+constexpr int kAttnSplits = 16;  // S; chunk length <= 256 for max_seq <= 4096
 
-extern "C" __global__ void __launch_bounds__(256) qmm_decode_attention_split(
-    const float* __restrict__ q, const float* __restrict__ k_new, const float* __restrict__ v_new,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t, const int* __restrict__ pos,
-    float* __restrict__ kcache, float* __restrict__ vcache, float* __restrict__ part, int heads, int kv_heads,
-    int dim, int max_seq, float scale) {
+template <int DPL>
+__device__ __forceinline__ void attn_row(float (&dst)[DPL], const float* __restrict__ row, int lane) {
+  if constexpr (DPL == 1) {
+    dst[0] = row[lane];
+  } else if constexpr (DPL == 2) {
+    const float2 v = reinterpret_cast<const float2*>(row)[lane];
+    dst[0] = v.x;
+    dst[1] = v.y;
+  } else {
+    const float4 v = reinterpret_cast<const float4*>(row)[lane];
+    dst[0] = v.x;
+    dst[1] = v.y;
+    dst[2] = v.z;
+    dst[3] = v.w;
+  }
+}
+
+// x * cos + rotate_half(x) * sin with rotate_half = cat(-x2, x1): lanes < 32
+// hold the first half of the dims, their partners are lanes ^ 32.
+template <int DPL>
+__device__ __forceinline__ void attn_rope(float (&x)[DPL], const float (&cs)[DPL], const float (&sn)[DPL],
+                                          int lane) {
 #pragma clang fp contract(off)
-  using namespace qmm;
-  constexpr int S = kAttnSplits;
-  __shared__ float qs[kAttnMaxG * 256];
-  __shared__ float sc[kAttnMaxG * kAttnMaxChunk];
-  __shared__ __attribute__((aligned(16))) float kt[kAttnTileFloats + 128];  // padded K tile, then V partials
-  __shared__ float knew[256];
-  __shared__ float stat[2 * kAttnMaxG];
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) {
+    const float other = __shfl_xor(x[e], 32);
+    const float rot = lane < 32 ? -other : other;
+    x[e] = x[e] * cs[e] + rot * sn[e];
+  }
+}
+
+template <int DPL, int GT, int NW>
+__device__ __forceinline__ void decode_attention(const float* __restrict__ q, const float* __restrict__ k_new,
+                                                 const float* __restrict__ v_new, const float* __restrict__ cos_t,
+                                                 const float* __restrict__ sin_t, const int* __restrict__ pos,
+                                                 float* __restrict__ kcache, float* __restrict__ vcache,
+                                                 float* __restrict__ part, unsigned* __restrict__ counters,
+                                                 float* __restrict__ out, int heads, int kv_heads, int max_seq,
+                                                 float scale) {
+#pragma clang fp contract(off)
+  constexpr int dim = 64 * DPL;
+  constexpr int B = 16 / DPL;  // positions per wave batch
+  constexpr int NT = 64 * NW;
+  __shared__ float wst[NW][2 * GT];
+  __shared__ __attribute__((aligned(16))) float wo[NW][GT * dim];
+  __shared__ int last;
   const int g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const int G = heads / kv_heads;
+  constexpr int S = kAttnSplits;
   const bool rope = cos_t != nullptr;
-  const int half = dim >> 1, d4 = dim >> 2;
-  const int gd = G * dim;
 
-  // loads, batch 1: pos, q of the group's heads (contiguous rows), new k / v rows
+  // loads, batch 1: pos, q of the group's heads, new k / v rows
   const int p = min(max(pos[0], 0), max_seq - 1);
-  float qv[8];
+  float qv[GT][DPL];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int i = t + 256 * u;
-    if (i < gd) qv[u] = q[(size_t)g * gd + i];
-  }
-  float kn = 0.0f, vn = 0.0f;
-  if (rope && t < dim) {
-    kn = k_new[(size_t)g * dim + t];
-    vn = v_new[(size_t)g * dim + t];
+  for (int h = 0; h < GT; ++h) attn_row<DPL>(qv[h], q + (size_t)(g * G + min(h, G - 1)) * dim, lane);
+  float kn[DPL], vn[DPL];
+  if (rope) {
+    attn_row<DPL>(kn, k_new + (size_t)g * dim, lane);
+    attn_row<DPL>(vn, v_new + (size_t)g * dim, lane);
   }
 
   const int n = p + 1;
@@ -133,227 +159,195 @@ extern "C" __global__ void __launch_bounds__(256) qmm_decode_attention_split(
   const bool own = j0 <= p && p < j1;
   const float* kc = kcache + (size_t)g * max_seq * dim;
   const float* vc = vcache + (size_t)g * max_seq * dim;
-  const int TJ = kAttnTileFloats / dim;  // positions per K tile
-  const int RS = 256 / d4;              // v row slots
-  const int c4 = t % d4, rs = t / d4;
+  const int npos = nc > wave ? (nc - wave + NW - 1) / NW : 0;  // this wave's positions j0 + wave + NW i
 
-  // loads, batch 2: first K tile, first v rows, cos / sin rows
-  float4 r[8];
-  {
-    const int nt = min(TJ, nc);
+  // loads, batch 2: the wave's first k / v rows (clamped into the chunk), cos / sin at p
+  float kr[B][DPL], vr[B][DPL];
+  const int jlast = max(j1 - 1, 0);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int i = t + 256 * u, jj = i / d4;
-      if (jj < nt) r[u] = reinterpret_cast<const float4*>(kc + (size_t)(j0 + jj) * dim)[i % d4];
-    }
+  for (int b = 0; b < B; ++b) {
+    const int j = min(j0 + wave + NW * b, jlast);
+    attn_row<DPL>(kr[b], kc + (size_t)j * dim, lane);
+    attn_row<DPL>(vr[b], vc + (size_t)j * dim, lane);
   }
-  float4 vv[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int j = j0 + rs + u * RS;
-    if (j < j1) {
-      const float* row = (rope && j == p) ? v_new + (size_t)g * dim : vc + (size_t)j * dim;
-      vv[u] = reinterpret_cast<const float4*>(row)[c4];
-    }
-  }
-  float csv[8], snv[8], ck = 0.0f, sk = 0.0f;
   if (rope) {
-    const float* cs = cos_t + (size_t)p * dim;
-    const float* sn = sin_t + (size_t)p * dim;
+    float cs[DPL], sn[DPL];
+    attn_row<DPL>(cs, cos_t + (size_t)p * dim, lane);
+    attn_row<DPL>(sn, sin_t + (size_t)p * dim, lane);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int i = t + 256 * u;
-      if (i < gd) {
-        csv[u] = cs[i % dim];
-        snv[u] = sn[i % dim];
+    for (int h = 0; h < GT; ++h) attn_rope<DPL>(qv[h], cs, sn, lane);
+    attn_rope<DPL>(kn, cs, sn, lane);
+    if (own && wave == 0) {
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        kcache[((size_t)g * max_seq + p) * dim + lane * DPL + e] = kn[e];
+        vcache[((size_t)g * max_seq + p) * dim + lane * DPL + e] = vn[e];
       }
-    }
-    if (t < dim) {
-      ck = cs[t];
-      sk = sn[t];
     }
   }
 
-  // q (and k at p) into LDS, rotated when fused: x * cos + cat(-x2, x1) * sin
+  float m[GT], l[GT], o[GT][DPL];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int i = t + 256 * u;
-    if (i < gd) qs[i] = qv[u];
+  for (int h = 0; h < GT; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) o[h][e] = 0.0f;
   }
-  if (rope && t < dim) knew[t] = kn;
-  __syncthreads();
-  if (rope) {
-    float rq[8], rk = 0.0f;
+  // One batch of B positions (i0 .. i0 + B - 1 of this wave; those past npos
+  // are clamped duplicates and weigh nothing): all B x GT scores first (their
+  // wave sums are independent), then one online-softmax update per head.
+  auto scan = [&](const float (&kb)[B][DPL], const float (&vb)[B][DPL], int i0) {
+    const int nv = min(B, npos - i0);
+    float sc[B][GT];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int i = t + 256 * u;
-      if (i < gd) {
-        const int d = i % dim;
-        const float rot = d < half ? -qs[i + half] : qs[i - half];
-        rq[u] = qv[u] * csv[u] + rot * snv[u];
+    for (int b = 0; b < B; ++b) {
+      const bool at_p = rope && j0 + wave + NW * (i0 + b) == p;
+#pragma unroll
+      for (int h = 0; h < GT; ++h) {
+        float d = 0.0f;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) d += qv[h][e] * (at_p ? kn[e] : kb[b][e]);
+        sc[b][h] = d;
       }
     }
-    if (t < dim) {
-      const float rot = t < half ? -knew[t + half] : knew[t - half];
-      rk = kn * ck + rot * sk;
-    }
-    __syncthreads();
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int i = t + 256 * u;
-      if (i < gd) qs[i] = rq[u];
-    }
-    if (t < dim) {
-      knew[t] = rk;
-      if (own) {
-        kcache[((size_t)g * max_seq + p) * dim + t] = rk;
-        vcache[((size_t)g * max_seq + p) * dim + t] = vn;
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+      for (int h = 0; h < GT; ++h) sc[b][h] = wave_total(sc[b][h]) * scale;
+#pragma unroll
+    for (int h = 0; h < GT; ++h) {
+      float mx = m[h];
+#pragma unroll
+      for (int b = 0; b < B; ++b) mx = b < nv ? fmaxf(mx, sc[b][h]) : mx;
+      const float a = expf(m[h] - mx);  // 0 while m = -inf
+      float ls = l[h] * a;
+      float acc[DPL];
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) acc[e] = o[h][e] * a;
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const bool at_p = rope && j0 + wave + NW * (i0 + b) == p;
+        const float w = b < nv ? expf(sc[b][h] - mx) : 0.0f;
+        ls += w;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[e] += w * (at_p ? vn[e] : vb[b][e]);
       }
-    }
-  }
-  const int ld = dim + 1;
-
-  // scores s_j = (q_h . k_j) * scale for the chunk, one K tile at a time
-  for (int jt = j0; jt < j1; jt += TJ) {
-    const int nt = min(TJ, j1 - jt);
-    if (jt != j0) {
+      m[h] = mx;
+      l[h] = ls;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int i = t + 256 * u, jj = i / d4;
-        if (jj < nt) r[u] = reinterpret_cast<const float4*>(kc + (size_t)(jt + jj) * dim)[i % d4];
+      for (int e = 0; e < DPL; ++e) o[h][e] = acc[e];
+    }
+  };
+  if (npos > 0) {
+    int i0 = 0;
+    for (; i0 + B < npos; i0 += B) {
+      // next batch in flight (clamped, unconditional) while this one is scored
+      float kx[B][DPL], vx[B][DPL];
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const int j = min(j0 + wave + NW * (i0 + B + b), jlast);
+        attn_row<DPL>(kx[b], kc + (size_t)j * dim, lane);
+        attn_row<DPL>(vx[b], vc + (size_t)j * dim, lane);
       }
-    }
-    __syncthreads();  // q / knew staged; the previous tile consumed
+      scan(kr, vr, i0);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int i = t + 256 * u, jj = i / d4;
-      if (jj < nt) {
-        float* dst = kt + jj * ld + 4 * (i % d4);
-        dst[0] = r[u].x;
-        dst[1] = r[u].y;
-        dst[2] = r[u].z;
-        dst[3] = r[u].w;
-      }
-    }
-    __syncthreads();
-    if (rope && own && p >= jt && p < jt + nt) {  // the appended position comes from LDS, not the cache
-      for (int d = t; d < dim; d += 256) kt[(p - jt) * ld + d] = knew[d];
-      __syncthreads();
-    }
-    const int jj = t % TJ;
-    if (jj < nt) {
-      const float* kr = kt + jj * ld;
-      for (int hl = t / TJ; hl < G; hl += 256 / TJ) {
-        const float* qh = qs + hl * dim;
-        float acc = 0.0f;
-        for (int d = 0; d < dim; ++d) acc += qh[d] * kr[d];
-        sc[hl * kAttnMaxChunk + (jt - j0) + jj] = acc * scale;
-      }
-    }
-  }
-  __syncthreads();
-
-  // chunk softmax state per head (one wave per head)
-  for (int hl = wave; hl < G; hl += 4) {
-    float* sh = sc + hl * kAttnMaxChunk;
-    float mx = -INFINITY;
-    for (int j = lane; j < nc; j += 64) mx = fmaxf(mx, sh[j]);
-    mx = wave_max(mx);
-    float sum = 0.0f;
-    for (int j = lane; j < nc; j += 64) {
-      const float e = expf(sh[j] - mx);
-      sh[j] = e;
-      sum += e;
-    }
-    sum = wave_sum(sum);
-    if (lane == 0) {
-      stat[2 * hl] = mx;
-      stat[2 * hl + 1] = sum;
-    }
-  }
-  __syncthreads();
-
-  // o_h = sum_j e_hj v_j: thread (column c4, row slot rs) over rows j0 + rs + RS*k
-  float4 acc[kAttnMaxG];
+      for (int b = 0; b < B; ++b)
 #pragma unroll
-  for (int hl = 0; hl < kAttnMaxG; ++hl) acc[hl] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  for (int jb = j0 + rs; jb < j1; jb += 4 * RS) {
-    if (jb != j0 + rs) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int j = jb + u * RS;
-        if (j < j1) {
-          const float* row = (rope && j == p) ? v_new + (size_t)g * dim : vc + (size_t)j * dim;
-          vv[u] = reinterpret_cast<const float4*>(row)[c4];
+        for (int e = 0; e < DPL; ++e) {
+          kr[b][e] = kx[b][e];
+          vr[b][e] = vx[b][e];
         }
-      }
     }
+    scan(kr, vr, i0);
+  }
+
+  // the waves' states -> the chunk's record per head
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int j = jb + u * RS;
-      if (j < j1) {
+  for (int h = 0; h < GT; ++h)
 #pragma unroll
-        for (int hl = 0; hl < kAttnMaxG; ++hl) {
-          if (hl < G) {
-            const float e = sc[hl * kAttnMaxChunk + (j - j0)];
-            acc[hl].x += e * vv[u].x;
-            acc[hl].y += e * vv[u].y;
-            acc[hl].z += e * vv[u].z;
-            acc[hl].w += e * vv[u].w;
-          }
-        }
-      }
+    for (int e = 0; e < DPL; ++e) wo[wave][h * dim + lane * DPL + e] = o[h][e];
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < GT; ++h) {
+      wst[wave][2 * h] = m[h];
+      wst[wave][2 * h + 1] = l[h];
     }
   }
-  float* red = kt;  // RS x G x dim partial sums (1024 * G floats)
-#pragma unroll
-  for (int hl = 0; hl < kAttnMaxG; ++hl)
-    if (hl < G) reinterpret_cast<float4*>(red + (rs * G + hl) * dim)[c4] = acc[hl];
   __syncthreads();
   const size_t rec = (size_t)dim + 2;  // per (chunk, head): m, l, o[dim]
-  for (int i = t; i < gd; i += 256) {
-    const int hl = i / dim, dd = i % dim;
-    float o = 0.0f;
-    for (int q2 = 0; q2 < RS; ++q2) o += red[(q2 * G + hl) * dim + dd];
-    part[((size_t)c * heads + g * G + hl) * rec + 2 + dd] = o;
-  }
-  if (t < G) {
-    part[((size_t)c * heads + g * G + t) * rec] = nc > 0 ? stat[2 * t] : -INFINITY;
-    part[((size_t)c * heads + g * G + t) * rec + 1] = nc > 0 ? stat[2 * t + 1] : 0.0f;
-  }
-}
-
-// out[h] = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c over the S chunk
-// records of head h (chunk order). One workgroup of dim threads per head.
-extern "C" __global__ void __launch_bounds__(256) qmm_decode_attention_merge(const float* __restrict__ part,
-                                                                            float* __restrict__ out, int heads,
-                                                                            int dim) {
-#pragma clang fp contract(off)
-  constexpr int S = qmm::kAttnSplits;
-  const int h = blockIdx.x, d = threadIdx.x;
-  const size_t rec = (size_t)dim + 2;
-  float mc[S], lc[S], oc[S];
+  for (int i = t; i < G * dim; i += NT) {
+    const int h = i / dim, d = i % dim;
+    float M = -INFINITY;
 #pragma unroll
-  for (int c = 0; c < S; ++c) {
-    const float* r = part + ((size_t)c * heads + h) * rec;
-    mc[c] = r[0];
-    lc[c] = r[1];
-    oc[c] = r[2 + d];
-  }
-  float M = -INFINITY;
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, wst[w][2 * h]);
+    float lsum = 0.0f, osum = 0.0f;
 #pragma unroll
-  for (int c = 0; c < S; ++c) M = fmaxf(M, mc[c]);
-  float lsum = 0.0f, o = 0.0f;
-#pragma unroll
-  for (int c = 0; c < S; ++c) {
-    if (mc[c] != -INFINITY) {
-      const float w = expf(mc[c] - M);
-      lsum += lc[c] * w;
-      o += oc[c] * w;
+    for (int w = 0; w < NW; ++w) {
+      if (wst[w][2 * h] != -INFINITY) {
+        const float a = expf(wst[w][2 * h] - M);
+        lsum += wst[w][2 * h + 1] * a;
+        osum += wo[w][i] * a;
+      }
+    }
+    float* r = part + ((size_t)c * heads + g * G + h) * rec;
+    __hip_atomic_store(r + 2 + d, osum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d == 0) {
+      __hip_atomic_store(r, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(r + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  out[(size_t)h * dim + d] = o / lsum;
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this thread's record stores are acknowledged
+  __syncthreads();
+  if (t == 0)
+    last = __hip_atomic_fetch_add(counters + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+  __syncthreads();
+  if (!last) return;
+
+  // last workgroup of kv head g: merge the S chunk records of its G heads
+  for (int i = t; i < G * dim; i += NT) {
+    const int h = g * G + i / dim, d = i % dim;
+    float mc[S], lc[S], oc[S];
+#pragma unroll
+    for (int cc = 0; cc < S; ++cc) {
+      const float* r = part + ((size_t)cc * heads + h) * rec;
+      mc[cc] = __hip_atomic_load(r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      lc[cc] = __hip_atomic_load(r + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      oc[cc] = __hip_atomic_load(r + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int cc = 0; cc < S; ++cc) M = fmaxf(M, mc[cc]);
+    float lsum = 0.0f, osum = 0.0f;
+#pragma unroll
+    for (int cc = 0; cc < S; ++cc) {
+      if (mc[cc] != -INFINITY) {
+        const float w = expf(mc[cc] - M);
+        lsum += lc[cc] * w;
+        osum += oc[cc] * w;
+      }
+    }
+    out[(size_t)h * dim + d] = osum / lsum;
+  }
+  if (t == 0) __hip_atomic_store(counters + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+}  // namespace qmm
+
+#define QMM_ATTN_KERNEL(DPL, GT, NW)                                                                             \
+  extern "C" __global__ void __launch_bounds__(64 * NW) qmm_decode_attention_d##DPL##_g##GT##_w##NW(             \
+      const float* __restrict__ q, const float* __restrict__ k_new, const float* __restrict__ v_new,            \
+      const float* __restrict__ cos_t, const float* __restrict__ sin_t, const int* __restrict__ pos,            \
+      float* __restrict__ kcache, float* __restrict__ vcache, float* __restrict__ part,                         \
+      unsigned* __restrict__ counters, float* __restrict__ out, int heads, int kv_heads, int max_seq,           \
+      float scale) {                                                                                             \
+    qmm::decode_attention<DPL, GT, NW>(q, k_new, v_new, cos_t, sin_t, pos, kcache, vcache, part, counters, out, \
+                                       heads, kv_heads, max_seq, scale);                                        \
+  }
+#define QMM_ATTN_KERNELS(DPL) \
+  QMM_ATTN_KERNEL(DPL, 1, 4) QMM_ATTN_KERNEL(DPL, 2, 4) QMM_ATTN_KERNEL(DPL, 4, 4) QMM_ATTN_KERNEL(DPL, 8, 4)
+QMM_ATTN_KERNELS(1)
+QMM_ATTN_KERNELS(2)
+QMM_ATTN_KERNELS(4)
 
 // hq = Q8_K(silu(g) * u) for `rows` rows of k elements (one wave per block).
 extern "C" __global__ void __launch_bounds__(256) qmm_silu_mul_q8k(const float* __restrict__ g,

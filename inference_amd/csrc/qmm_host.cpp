@@ -871,7 +871,8 @@ int qmm_rope_kv_append(float* q, float* k, const float* v, const float* cos_t, c
   return launch(d, "qmm_decode_rope_kv", (unsigned)(heads + kv_heads), threads, 0, (hipStream_t)stream, args);
 }
 
-// Workspace of the split attention: S chunks x heads x (m, l, o[head_dim]) floats.
+// Workspace of the attention: one counter per kv head (a 256-byte-aligned
+// region), then S chunks x heads x (m, l, o[head_dim]) floats.
 static const int kAttnSplits = 16;  // must equal the kernel's qmm::kAttnSplits
 
 static int check_attention(int heads, int kv_heads, int head_dim, int max_seq) {
@@ -884,9 +885,11 @@ static int check_attention(int heads, int kv_heads, int head_dim, int max_seq) {
   return QMM_OK;
 }
 
+static size_t attn_counter_bytes(int kv_heads) { return ((size_t)kv_heads * 4 + 255) / 256 * 256; }
+
 size_t qmm_decode_attention_workspace_size(int heads, int kv_heads, int head_dim, int max_seq) {
   if (check_attention(heads, kv_heads, head_dim, max_seq) != QMM_OK) return 0;
-  return (size_t)kAttnSplits * heads * (head_dim + 2) * sizeof(float);
+  return attn_counter_bytes(kv_heads) + (size_t)kAttnSplits * heads * (head_dim + 2) * sizeof(float);
 }
 
 static int attention(const float* q, const float* k, const float* v, const float* cos_t, const float* sin_t,
@@ -897,15 +900,20 @@ static int attention(const float* q, const float* k, const float* v, const float
   if (!ws || ws_bytes < need) return fail(QMM_ERR_INVALID, "attention workspace of %zu B < %zu B", ws_bytes, need);
   Device* d;
   QMM_TRY(current_device(&d));
-  float* part = (float*)ws;
-  void* args[] = {&q, &k, &v, &cos_t, &sin_t, &pos, &kcache, &vcache, &part,
-                  &heads, &kv_heads, &head_dim, &max_seq, &scale};
+  unsigned* counters = (unsigned*)ws;
+  float* part = (float*)((uint8_t*)ws + attn_counter_bytes(kv_heads));
+  const int G = heads / kv_heads;
+  const int gt = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;
+  const int splits = kAttnSplits, nw = 4;
+  char name[64];
+  snprintf(name, sizeof(name), "qmm_decode_attention_d%d_g%d_w%d", head_dim / 64, gt, nw);
+  void* args[] = {&q, &k, &v, &cos_t, &sin_t, &pos, &kcache, &vcache, &part, &counters, &out,
+                  &heads, &kv_heads, &max_seq, &scale};
   hipFunction_t f;
-  QMM_TRY(kernel(d, "qmm_decode_attention_split", &f));
-  QMM_HIP(hipModuleLaunchKernel(f, (unsigned)kv_heads, (unsigned)kAttnSplits, 1, 256, 1, 1, 0,
+  QMM_TRY(kernel(d, name, &f));
+  QMM_HIP(hipModuleLaunchKernel(f, (unsigned)kv_heads, (unsigned)splits, 1, (unsigned)(64 * nw), 1, 1, 0,
                                 (hipStream_t)stream, args, nullptr));
-  void* margs[] = {&part, &out, &heads, &head_dim};
-  return launch(d, "qmm_decode_attention_merge", (unsigned)heads, (unsigned)head_dim, 0, (hipStream_t)stream, margs);
+  return QMM_OK;
 }
 
 int qmm_decode_attention(const float* q, const float* kcache, const float* vcache, const int32_t* pos, float* out,

@@ -176,8 +176,8 @@ class DecodeSession:
         self._graph = None
         L = qmm.lib()
         self.L = L
-        # workspaces of the split attention (chunk partials) and of the argmax (its counter
-        # starts at zero and every launch leaves it at zero)
+        # workspaces of the attention (per-kv-head counters, then chunk partials) and of the
+        # argmax; their counters start at zero and every launch leaves them at zero
         wsa = int(L.qmm_decode_attention_workspace_size(cfg.heads, cfg.kv_heads, cfg.head_dim, max_seq))
         if wsa == 0:
             raise qmm.QmmError(1, "unsupported attention geometry: " + qmm.last_error())
