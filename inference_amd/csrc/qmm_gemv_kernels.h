@@ -647,16 +647,41 @@ __device__ __forceinline__ void flush_outputs(const GemvJobs& jobs, int nb, floa
 // Wave w owns blocks w, w + nw, ... (up to kActPF of them; longer rows take
 // quantize_act). RMSNorm (norm_w, not SILU) sums the squares from the same
 // registers: lanes, then DPP rows and v_readlane, then waves in order.
+// MIX (FMT = Q4_K) also writes the Q6_K layout of the same quantized row at
+// lds + 292 * nb, for launches whose jobs mix the two formats.
 constexpr int kActPF = 4;
 
-template <int FMT, bool SILU>
+template <int FMT>
+__device__ __forceinline__ void put_q8k_lane(uint8_t* lds, int nb, int blk, const Q8KLane& q, int lane) {
+  uint32_t* lsum = reinterpret_cast<uint32_t*>(lds + 256 * nb);
+  float* ld = reinterpret_cast<float*>(lsum + 8 * nb);
+  int lc, kc;
+  chunk_owner<FMT>(lane >> 2, lc, kc);
+  *reinterpret_cast<uint32_t*>(lds + 256 * blk + 16 * kq_slot(blk, lc, kc) + 4 * (lane & 3)) = q.packed;
+  const int next = __shfl_down(q.sum16, 4);  // the following 16-group's sum
+  if (FMT == kFmtQ4K) {
+    const int s32 = q.sum16 + next;
+    const int s32n = __shfl_down(s32, 8);
+    if ((lane & 15) == 0) lsum[8 * blk + (lane >> 4)] = ((uint32_t)s32 & 0xffffu) | ((uint32_t)s32n << 16);
+  } else {
+    if ((lane & 7) == 0) lsum[8 * blk + 2 * lc + (kc >> 1)] = ((uint32_t)q.sum16 & 0xffffu) | ((uint32_t)next << 16);
+  }
+  if (lane == 0) ld[blk] = q.d;
+}
+
+template <int FMT, bool SILU, bool MIX = false>
 __device__ __forceinline__ void quantize_act1(const float* __restrict__ x, int nb, uint8_t* lds,
                                               const float* __restrict__ norm_w, float eps) {
 #pragma clang fp contract(off)
   static_assert(FMT != kFmtQ80, "k-quant activations");
+  static_assert(!MIX || FMT == kFmtQ4K, "mixed layouts: Q4_K then Q6_K");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   if (nb > kActPF * nw) {
     quantize_act<FMT, SILU>(x, 0, 1, nb, lds, norm_w, eps);
+    if constexpr (MIX) {
+      __syncthreads();  // quantize_act's LDS scratch is reused
+      quantize_act<kFmtQ6K, SILU>(x, 0, 1, nb, lds + kQ8KBytes * nb, norm_w, eps);
+    }
     return;
   }
   __shared__ float red[16];
@@ -707,26 +732,13 @@ __device__ __forceinline__ void quantize_act1(const float* __restrict__ x, int n
       e[i].w = silu_mul(e[i].w, a[i].w);
     }
   }
-  uint32_t* lsum = reinterpret_cast<uint32_t*>(lds + 256 * nb);
-  float* ld = reinterpret_cast<float*>(lsum + 8 * nb);
-  const int c16 = lane >> 2;
-  int lc, kc;
-  chunk_owner<FMT>(c16, lc, kc);
 #pragma unroll
   for (int i = 0; i < kActPF; ++i) {
     const int blk = wave + i * nw;
     if (blk >= nb) break;  // wave-uniform
     const Q8KLane q = q8k_lane_vals(e[i].x, e[i].y, e[i].z, e[i].w, lane);
-    *reinterpret_cast<uint32_t*>(lds + 256 * blk + 16 * kq_slot(blk, lc, kc) + 4 * (lane & 3)) = q.packed;
-    const int next = __shfl_down(q.sum16, 4);  // the following 16-group's sum
-    if (FMT == kFmtQ4K) {
-      const int s32 = q.sum16 + next;
-      const int s32n = __shfl_down(s32, 8);
-      if ((lane & 15) == 0) lsum[8 * blk + (lane >> 4)] = ((uint32_t)s32 & 0xffffu) | ((uint32_t)s32n << 16);
-    } else {
-      if ((lane & 7) == 0) lsum[8 * blk + 2 * lc + (kc >> 1)] = ((uint32_t)q.sum16 & 0xffffu) | ((uint32_t)next << 16);
-    }
-    if (lane == 0) ld[blk] = q.d;
+    put_q8k_lane<FMT>(lds, nb, blk, q, lane);
+    if constexpr (MIX) put_q8k_lane<kFmtQ6K>(lds + kQ8KBytes * nb, nb, blk, q, lane);
   }
 }
 
@@ -868,47 +880,18 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
 //     and kept in registers for every row;
 //   * the row sum is reduced with DPP and v_readlane (no LDS round trip);
 //   * outputs are kept one per lane and written 64 at a time.
-// Same per-block arithmetic (prep_w / dot_wx) as gemv(); no block-dot dump.
-template <int FMT, bool FUSED, int J, bool SILU = false>
-__device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restrict__ act, long long ldx, int K,
-                                      const float* __restrict__ norm_w, float eps, int accumulate) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  constexpr int LPB = FmtInfo<FMT>::kLanesPerBlock;
-  constexpr int BPI = 64 / LPB;  // blocks per wave iteration
-  const int nb = K / FmtInfo<FMT>::kBlockElems;
-  const int lane = threadIdx.x & 63;
-  const int nw = blockDim.x >> 6;
-  const int l = lane % LPB;
-  const int g = lane / LPB;
+// Rows row, row + row_step, ... below `end` of one format (gemv1's row loop):
+// each row's dot, the next row's first slice loaded before this row's
+// reduction, outputs kept one per lane (keep_v / keep_row, `slot` lanes
+// filled) and flushed 64 at a time. ws holds row `row`'s first slice on entry.
+template <int FMT, int J>
+__device__ __forceinline__ void gemv1_rows(const GemvJobs& jobs, JobCursor& jc, const JobArg* ja, RowRef& rr,
+                                           WSlice& ws, const XSlice& x0, const uint8_t* __restrict__ lds, int nb,
+                                           int& row, int end, int row_step, uint32_t b0, int g, int l, int lane,
+                                           float& keep_v, int& keep_row, int& slot, int accumulate) {
+  constexpr int BPI = 64 / FmtInfo<FMT>::kLanesPerBlock;
   const int niter = (nb + BPI - 1) / BPI;
-  const int row_step = gridDim.x * nw;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  int row = blockIdx.x * nw + wave;
-
-  const JobArg* ja = job_args();
-  JobCursor jc;
-  cursor_init(jc, ja);
-  WSlice ws;
-  const uint32_t b0 = (uint32_t)min(g, nb - 1);  // clamped: every lane loads
-  RowRef rr = cursor_row<FMT>(jc, ja, jobs.njobs, jobs.total, min(row, jobs.total - 1), nb);
-  load_slice<FMT>(ws, rr.wrow, rr.drow, b0, l);  // first row in flight before staging
-  if constexpr (FUSED) {
-    if constexpr (FMT == kFmtQ80)
-      quantize_act<FMT, SILU>(reinterpret_cast<const float*>(act), ldx, 1, nb, lds, norm_w, eps);
-    else
-      quantize_act1<FMT, SILU>(reinterpret_cast<const float*>(act), nb, lds, norm_w, eps);
-  }
-  else
-    stage_act<FMT>(reinterpret_cast<const uint8_t*>(act), nb, lds);
-  __syncthreads();
-  if (row >= jobs.total) return;
-  rr = cursor_row<FMT>(jc, ja, jobs.njobs, jobs.total, row, nb);
-
-  XSlice x0;  // loop-invariant activation of the first iteration
-  load_x<FMT>(x0, lds, nb, (int)b0, l);
   const bool ok0 = g < nb;
-  float keep_v = 0.0f;  // this lane's kept output (global row keep_row)
-  int keep_row = 0, slot = 0;
   for (;;) {
     int ia, ib;
     float acc;
@@ -925,7 +908,7 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
       acc += b < nb ? p : 0.0f;
     }
     const int nrow = row + row_step;
-    if (nrow < jobs.total) {  // next row's first batch before this row's reduction
+    if (nrow < end) {  // next row's first batch before this row's reduction
       rr = cursor_row<FMT>(jc, ja, jobs.njobs, jobs.total, nrow, nb);
       load_slice<FMT>(ws, rr.wrow, rr.drow, b0, l);
     }
@@ -939,7 +922,81 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
       slot = 0;
     }
     row = nrow;
-    if (row >= jobs.total) break;
+    if (row >= end) break;
+  }
+}
+
+// Same per-block arithmetic (prep_w / dot_wx) as gemv(); no block-dot dump.
+// MIX (FMT = Q4_K): global rows >= mix_row belong to Q6_K jobs (the host
+// orders the jobs Q4_K first); the activation is staged in both layouts and
+// a wave runs its Q4_K rows, then its Q6_K rows.
+template <int FMT, bool FUSED, int J, bool SILU = false, bool MIX = false>
+__device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restrict__ act, long long ldx, int K,
+                                      const float* __restrict__ norm_w, float eps, int accumulate,
+                                      int mix_row = 0x7fffffff) {
+  static_assert(!MIX || FMT == kFmtQ4K, "mixed launches: Q4_K rows, then Q6_K rows");
+  constexpr int F6 = kFmtQ6K;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int LPB = FmtInfo<FMT>::kLanesPerBlock;
+  const int nb = K / FmtInfo<FMT>::kBlockElems;
+  const int lane = threadIdx.x & 63;
+  const int nw = blockDim.x >> 6;
+  const int l = lane % LPB;
+  const int g = lane / LPB;
+  const int row_step = gridDim.x * nw;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int row = blockIdx.x * nw + wave;
+  uint8_t* lds6 = lds + (MIX ? kQ8KBytes * nb : 0);  // Q6_K layout (MIX)
+  const int end4 = MIX ? min(mix_row, jobs.total) : jobs.total;
+
+  const JobArg* ja = job_args();
+  JobCursor jc;
+  cursor_init(jc, ja);
+  WSlice ws;
+  const uint32_t b0 = (uint32_t)min(g, nb - 1);  // clamped: every lane loads
+  RowRef rr;
+  const bool first6 = MIX && min(row, jobs.total - 1) >= end4;  // the wave starts in the Q6_K rows
+  {
+    // first row in flight before staging
+    const int r0 = min(row, jobs.total - 1);
+    if (first6) {
+      rr = cursor_row<F6>(jc, ja, jobs.njobs, jobs.total, r0, nb);
+      load_slice<F6>(ws, rr.wrow, rr.drow, b0, l);
+    } else {
+      rr = cursor_row<FMT>(jc, ja, jobs.njobs, jobs.total, r0, nb);
+      load_slice<FMT>(ws, rr.wrow, rr.drow, b0, l);
+    }
+  }
+  if constexpr (FUSED) {
+    if constexpr (FMT == kFmtQ80)
+      quantize_act<FMT, SILU>(reinterpret_cast<const float*>(act), ldx, 1, nb, lds, norm_w, eps);
+    else
+      quantize_act1<FMT, SILU, MIX>(reinterpret_cast<const float*>(act), nb, lds, norm_w, eps);
+  } else {
+    stage_act<FMT>(reinterpret_cast<const uint8_t*>(act), nb, lds);
+    if constexpr (MIX) stage_act<F6>(reinterpret_cast<const uint8_t*>(act), nb, lds6);
+  }
+  __syncthreads();
+  if (row >= jobs.total) return;
+
+  float keep_v = 0.0f;  // this lane's kept output (global row keep_row)
+  int keep_row = 0, slot = 0;
+  if (row < end4) {
+    rr = cursor_row<FMT>(jc, ja, jobs.njobs, jobs.total, row, nb);
+    XSlice x0;  // loop-invariant activation of the first iteration
+    load_x<FMT>(x0, lds, nb, (int)b0, l);
+    gemv1_rows<FMT, J>(jobs, jc, ja, rr, ws, x0, lds, nb, row, end4, row_step, b0, g, l, lane, keep_v, keep_row,
+                       slot, accumulate);
+  }
+  if constexpr (MIX) {
+    if (row < jobs.total) {
+      rr = cursor_row<F6>(jc, ja, jobs.njobs, jobs.total, row, nb);
+      if (!first6) load_slice<F6>(ws, rr.wrow, rr.drow, b0, l);  // after Q4_K rows: not prefetched
+      XSlice x06;
+      load_x<F6>(x06, lds6, nb, (int)b0, l);
+      gemv1_rows<F6, J>(jobs, jc, ja, rr, ws, x06, lds6, nb, row, jobs.total, row_step, b0, g, l, lane, keep_v,
+                        keep_row, slot, accumulate);
+    }
   }
   if (slot > 0) flush_outputs<FMT, J>(jobs, nb, keep_v, keep_row, lane < slot, accumulate);
 }
@@ -1036,6 +1093,25 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
     QMM_GEMV_JOBS                                                                                    \
     qmm::gemv1<FMT, true, 4, true>(jobs, act, ldx, K, norm_w, 0.0f, accumulate);                     \
   }
+// Mixed Q4_K / Q6_K jobs (e.g. a layer's q, k and v projections in one
+// launch); rows >= mix_row are the Q6_K jobs'.
+#define QMM_GEMV1_MIX_KERNELS(W)                                                                               \
+  extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1_q4k6k_w##W(QMM_GEMV_PARAMS, int mix_row) {    \
+    QMM_GEMV_JOBS                                                                                              \
+    qmm::gemv1<qmm::kFmtQ4K, false, 4, false, true>(jobs, act, ldx, K, nullptr, 0.0f, accumulate, mix_row);     \
+  }                                                                                                            \
+  extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1f_q4k6k_w##W(QMM_GEMV_PARAMS, int mix_row) {   \
+    QMM_GEMV_JOBS                                                                                              \
+    qmm::gemv1<qmm::kFmtQ4K, true, 4, false, true>(jobs, act, ldx, K, norm_w, eps, accumulate, mix_row);        \
+  }                                                                                                            \
+  extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1_q4k6k_w##W##_j8(QMM_GEMV_PARAMS8, int mix_row) { \
+    QMM_GEMV_JOBS8                                                                                             \
+    qmm::gemv1<qmm::kFmtQ4K, false, 8, false, true>(jobs, act, ldx, K, nullptr, 0.0f, accumulate, mix_row);     \
+  }                                                                                                            \
+  extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1f_q4k6k_w##W##_j8(QMM_GEMV_PARAMS8, int mix_row) { \
+    QMM_GEMV_JOBS8                                                                                             \
+    qmm::gemv1<qmm::kFmtQ4K, true, 8, false, true>(jobs, act, ldx, K, norm_w, eps, accumulate, mix_row);        \
+  }
 #define QMM_GEMV1_SHAPES(FMT, NAME) \
   QMM_GEMV1_KERNELS(FMT, NAME, 4)   \
   QMM_GEMV1_KERNELS(FMT, NAME, 8)   \
@@ -1095,3 +1171,6 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
 QMM_GEMV_ALL_M(qmm::kFmtQ4K, q4k)
 QMM_GEMV_ALL_M(qmm::kFmtQ6K, q6k)
 QMM_GEMV_ALL_M(qmm::kFmtQ80, q8_0)
+QMM_GEMV1_MIX_KERNELS(4)
+QMM_GEMV1_MIX_KERNELS(8)
+QMM_GEMV1_MIX_KERNELS(16)

@@ -476,6 +476,35 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
     QMM_TRY(gemv(d, tg, 4, act, fused, ldx, m, dump, s, norm_w, eps, accumulate));
     return gemv(d, tg + 4, count - 4, act, fused, ldx, m, dump, s, norm_w, eps, accumulate);
   }
+  // Q4_K and Q6_K jobs together (both take Q8_K activations): one launch of
+  // the mixed one-row kernels, Q4_K jobs first (global rows >= mix_row are
+  // Q6_K); other shapes take one launch per format.
+  int n4 = 0, n6 = 0;
+  for (int j = 0; j < count; ++j) {
+    const int f = fmt_of(tg[j].w->dtype);
+    n4 += f == kFmtQ4K;
+    n6 += f == kFmtQ6K;
+  }
+  const bool mixed = n4 > 0 && n6 > 0;
+  if (mixed && n4 + n6 != count) return fail(QMM_ERR_INVALID, "only Q4_K and Q6_K weights share a launch");
+  GemvTarget sorted[kMaxJobs];
+  int mix_row = 0;
+  if (mixed) {
+    int a = 0, b = n4;
+    for (int j = 0; j < count; ++j) {
+      if (fmt_of(tg[j].w->dtype) == kFmtQ4K) {
+        sorted[a++] = tg[j];
+        mix_row += (int)tg[j].w->n;
+      } else {
+        sorted[b++] = tg[j];
+      }
+    }
+    if (m != 1 || dump || silu) {
+      QMM_TRY(gemv(d, sorted, n4, act, fused, ldx, m, dump, s, norm_w, eps, accumulate, silu));
+      return gemv(d, sorted + n4, n6, act, fused, ldx, m, dump, s, norm_w, eps, accumulate, silu);
+    }
+    tg = sorted;
+  }
   const qmm_qtensor* w = tg[0].w;
   const int fmt = fmt_of(w->dtype);
   const int nb = (int)(w->k / qmm_block_size(w->dtype));
@@ -483,7 +512,7 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   const int bpi = 64 / lpb;                // blocks per wave iteration
   const int niter = (nb + bpi - 1) / bpi;
   const int xbb = fmt == kFmtQ80 ? 36 : 292;  // LDS bytes per staged activation block
-  const unsigned lds = (unsigned)(m * nb * xbb);
+  const unsigned lds = (unsigned)(m * nb * xbb * (mixed ? 2 : 1));  // mixed: Q4_K and Q6_K layouts
   if ((int)lds > d->max_lds)
     return fail(QMM_ERR_UNSUPPORTED, "activation of %d rows x %lld needs %u B of LDS (> %d)", m, (long long)w->k, lds,
                 d->max_lds);
@@ -543,8 +572,12 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
     r = u = 1;
     snprintf(name, sizeof(name), "qmm_gemv1s_%s_w%d", fmt_name(fmt), wv);
   } else if (one)
-    snprintf(name, sizeof(name), "qmm_gemv1%s_%s_w%d%s", fused ? "f" : "", fmt_name(fmt), wv, jcap > 4 ? "_j8" : "");
-  else
+    snprintf(name, sizeof(name), "qmm_gemv1%s_%s_w%d%s", fused ? "f" : "", mixed ? "q4k6k" : fmt_name(fmt), wv,
+             jcap > 4 ? "_j8" : "");
+  else if (mixed) {  // tuned to a shape without mixed kernels: one launch per format
+    QMM_TRY(gemv(d, tg, n4, act, fused, ldx, m, dump, s, norm_w, eps, accumulate, silu));
+    return gemv(d, tg + n4, n6, act, fused, ldx, m, dump, s, norm_w, eps, accumulate, silu);
+  } else
     snprintf(name, sizeof(name), "qmm_gemv%s_%s_m%d_w%d_r%d_u%d%s", fused ? "f" : "", fmt_name(fmt), m, wv, r, u,
              jcap > 4 ? "_j8" : "");
   long long wgs = (total + wv * r - 1) / (wv * r);
@@ -554,7 +587,7 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   long long lx = ldx;
   int K = (int)w->k;
   int* dp = dump;
-  void* args[6 * kMaxJobs + 9];
+  void* args[6 * kMaxJobs + 10];
   int na = 0;
   for (int j = 0; j < jcap; ++j) {
     args[na++] = &jobs.wq[j];
@@ -573,6 +606,7 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   args[na++] = &norm_w;
   args[na++] = &eps;
   args[na++] = &accumulate;
+  if (mixed) args[na++] = &mix_row;
   return launch(d, name, (unsigned)wgs, 64 * wv, lds, s, args);
 }
 
@@ -704,6 +738,15 @@ int qmm_matmul_q(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int6
   return QMM_OK;
 }
 
+// Weights that can share one activation in a call: the same k, and the same
+// dtype or both Q4_K / Q6_K (whose activations are both Q8_K).
+static bool same_act(const qmm_qtensor* a, const qmm_qtensor* b) {
+  if (a->k != b->k) return false;
+  if (a->dtype == b->dtype) return true;
+  const bool ka = a->dtype == QMM_Q4K || a->dtype == QMM_Q6K, kb = b->dtype == QMM_Q4K || b->dtype == QMM_Q6K;
+  return ka && kb;
+}
+
 int qmm_matmul_multi_q(const qmm_qtensor* const* w, int count, const void* xq, int64_t m, float* const* y,
                        const int64_t* ldy, void* stream) {
   if (!w || !y || !ldy || !xq || count < 1 || count > kMaxJobs)
@@ -711,8 +754,7 @@ int qmm_matmul_multi_q(const qmm_qtensor* const* w, int count, const void* xq, i
   GemvTarget tg[kMaxJobs];
   for (int j = 0; j < count; ++j) {
     QMM_TRY(check_matmul(w[j], m, y[j], ldy[j]));
-    if (w[j]->dtype != w[0]->dtype || w[j]->k != w[0]->k)
-      return fail(QMM_ERR_INVALID, "weights of one launch must share dtype and k");
+    if (!same_act(w[j], w[0])) return fail(QMM_ERR_INVALID, "weights of one launch must share k and dtype (or be Q4_K/Q6_K)");
     tg[j] = {w[j], y[j], ldy[j]};
   }
   if (m > 8) {  // the GEMM runs one weight at a time
@@ -818,9 +860,17 @@ int qmm_matmul_ex(const qmm_qtensor* const* w, int count, const float* x, int64_
   GemvTarget t[kMaxJobs];
   for (int j = 0; j < count; ++j) {
     QMM_TRY(check_matmul(w[j], m, y[j], ldy[j]));
-    if (w[j]->dtype != w[0]->dtype || w[j]->k != w[0]->k)
-      return fail(QMM_ERR_INVALID, "weights of one call must share dtype and k");
+    if (!same_act(w[j], w[0])) return fail(QMM_ERR_INVALID, "weights of one call must share k and dtype (or be Q4_K/Q6_K)");
     t[j] = {w[j], y[j], ldy[j]};
+  }
+  if (m > 2) {  // quantized activation planes are per format: one pass per dtype
+    GemvTarget a[kMaxJobs], b[kMaxJobs];
+    int na = 0, nb = 0;
+    for (int j = 0; j < count; ++j) (w[j]->dtype == w[0]->dtype ? a[na++] : b[nb++]) = t[j];
+    if (nb > 0) {
+      QMM_TRY(matmul_targets(a, na, x, m, ldx, ws, ws_bytes, stream, norm_weight, eps, accumulate ? 1 : 0));
+      return matmul_targets(b, nb, x, m, ldx, ws, ws_bytes, stream, norm_weight, eps, accumulate ? 1 : 0);
+    }
   }
   return matmul_targets(t, count, x, m, ldx, ws, ws_bytes, stream, norm_weight, eps, accumulate ? 1 : 0);
 }

@@ -192,12 +192,11 @@ class DecodeSession:
             return a
 
         vp, i64 = ctypes.c_void_p, ctypes.c_int64
-        self._qk = [arr(vp, [lw["q"].handle.value, lw["k"].handle.value]) for lw in weights.layers]
-        self._qk_y = arr(vp, [self.q.data_ptr(), self.k.data_ptr()])
-        self._qk_ld = arr(i64, [self.q.numel(), self.k.numel()])
-        self._v = [arr(vp, [lw["v"].handle.value]) for lw in weights.layers]
-        self._v_y = arr(vp, [self.v.data_ptr()])
-        self._v_ld = arr(i64, [self.v.numel()])
+        # q, k (Q4_K) and v (Q6_K) share the normalised activation: one launch
+        self._qkv = [arr(vp, [lw["q"].handle.value, lw["k"].handle.value, lw["v"].handle.value])
+                     for lw in weights.layers]
+        self._qkv_y = arr(vp, [self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr()])
+        self._qkv_ld = arr(i64, [self.q.numel(), self.k.numel(), self.v.numel()])
         self._o = [arr(vp, [lw["o"].handle.value]) for lw in weights.layers]
         self._x_y = arr(vp, [self.x.data_ptr()])
         self._x_ld = arr(i64, [cfg.hidden])
@@ -212,7 +211,7 @@ class DecodeSession:
     def step(self, trace: Optional[Callable[[str, int], None]] = None):
         """Enqueue one token step on the current stream (no host synchronisation).
 
-        `trace(op, layer)`, when given, is called after each launch is enqueued (ops: embed, qk, v,
+        `trace(op, layer)`, when given, is called after each launch is enqueued (ops: embed, qkv,
         attention (RoPE + KV append + attention in one launch), o, gate_up, silu_mul, down, head,
         argmax); it lets a checker inspect the session's buffers between launches. Captured steps
         take no trace.
@@ -228,12 +227,9 @@ class DecodeSession:
         kv_stride = cfg.kv_heads * self.max_seq * hd
         for li in range(cfg.layers):
             an, fn = w.attn_norm[li].data_ptr(), w.ffn_norm[li].data_ptr()
-            qmm._check(L.qmm_matmul_ex(self._qk[li], 2, self.x.data_ptr(), 1, H, an, eps, 0, self._qk_y,
-                                       self._qk_ld, None, 0, s))
-            tr("qk", li)
-            qmm._check(L.qmm_matmul_ex(self._v[li], 1, self.x.data_ptr(), 1, H, an, eps, 0, self._v_y, self._v_ld,
-                                       None, 0, s))
-            tr("v", li)
+            qmm._check(L.qmm_matmul_ex(self._qkv[li], 3, self.x.data_ptr(), 1, H, an, eps, 0, self._qkv_y,
+                                       self._qkv_ld, None, 0, s))
+            tr("qkv", li)
             kc = self.kcache.data_ptr() + 4 * li * kv_stride
             vc = self.vcache.data_ptr() + 4 * li * kv_stride
             qmm._check(L.qmm_decode_rope_attention(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),

@@ -80,13 +80,11 @@ class OpChecker:
             self.p = int(s.pos.item())
             self.x = self.snap(s.x)
             np.testing.assert_array_equal(self.x, ex["embed"][int(s.tokens[self.p].item())])
-        elif op == "qk":
+        elif op == "qkv":
             self.n = ol.rms_norm(self.x, ex["attn_norm"][li], c.eps)
-            self.q0, self.k0 = self.snap(s.q), self.snap(s.k)
+            self.q0, self.k0, self.v0 = self.snap(s.q), self.snap(s.k), self.snap(s.v)
             self.note("q", rel_err(self.q0, self.mm("q", li, self.n, c.hidden)), MM_TOL)
             self.note("k", rel_err(self.k0, self.mm("k", li, self.n, c.hidden)), MM_TOL)
-        elif op == "v":
-            self.v0 = self.snap(s.v)
             self.note("v", rel_err(self.v0, self.mm("v", li, self.n, c.hidden)), MM_TOL)
         elif op == "attention":
             cs, sn = ol.cos_sin(self.inv, self.p)

@@ -68,6 +68,69 @@ def test_matmul_ex_rms_norm_prologue(dt, m):
     assert rel_err(y.cpu().numpy(), want) <= 1e-3
 
 
+MIXES = [(GgmlDType.Q4K, GgmlDType.Q4K, GgmlDType.Q6K), (GgmlDType.Q6K, GgmlDType.Q4K),
+         (GgmlDType.Q4K, GgmlDType.Q6K, GgmlDType.Q4K, GgmlDType.Q6K, GgmlDType.Q4K)]
+
+
+@pytest.mark.parametrize("dts", MIXES)
+@pytest.mark.parametrize("m", [1, 2, 5])
+@pytest.mark.parametrize("norm", [False, True])
+@pytest.mark.parametrize("k", [4096, 20480])
+def test_matmul_ex_mixed_q4k_q6k_equals_separate_calls(dts, m, norm, k):
+    """Q4_K and Q6_K weights in one qmm_matmul_ex call (one mixed launch at m = 1; per-format launches
+    otherwise): bit-identical to one call per weight. k = 20480 takes the long-row prologue."""
+    rng = np.random.default_rng(40 + m + len(dts))
+    rows = [700, 256, 300, 1000, 33][:len(dts)]
+    qts = [QTensor.quantize(t((rng.standard_normal((n, k)) * 0.02).astype(np.float32)), dt)
+           for n, dt in zip(rows, dts)]
+    x = t((rng.standard_normal((m, k)) * 0.5).astype(np.float32))
+    nw = t(rng.uniform(0.5, 1.5, k).astype(np.float32)) if norm else None
+    nwp = nw.data_ptr() if norm else None
+    wsb = max(int(L().qmm_matmul_ex_workspace_size(q.handle, m, int(norm))) for q in qts)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    ys = [torch.full((m, n), float("nan"), device=DEV) for n in rows]
+    qmm._check(L().qmm_matmul_ex((vp * len(qts))(*[q.handle.value for q in qts]), len(qts), x.data_ptr(), m, k, nwp,
+                                 ctypes.c_float(1e-5), 0, (vp * len(qts))(*[y.data_ptr() for y in ys]),
+                                 (i64 * len(qts))(*rows), ws.data_ptr(), wsb, S()))
+    for q, n, y in zip(qts, rows, ys):
+        want = torch.full((m, n), float("nan"), device=DEV)
+        qmm._check(L().qmm_matmul_ex((vp * 1)(q.handle.value), 1, x.data_ptr(), m, k, nwp, ctypes.c_float(1e-5), 0,
+                                     (vp * 1)(want.data_ptr()), (i64 * 1)(n), ws.data_ptr(), wsb, S()))
+        assert torch.equal(y, want)
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_matmul_multi_q_mixed_q4k_q6k(m):
+    """Pre-quantized Q8_K activation shared by Q4_K and Q6_K weights: bit-identical to qmm_matmul_q."""
+    rng = np.random.default_rng(50 + m)
+    k, rows, dts = 2048, [513, 1024, 77], [GgmlDType.Q6K, GgmlDType.Q4K, GgmlDType.Q6K]
+    qts = [QTensor.quantize(t((rng.standard_normal((n, k)) * 0.02).astype(np.float32)), dt)
+           for n, dt in zip(rows, dts)]
+    xq = t(orc.quantize(orc.Q8K, rng.standard_normal((m, k)).astype(np.float32)), torch.uint8)
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    ys = [torch.full((m, n), float("nan"), device=DEV) for n in rows]
+    qmm._check(L().qmm_matmul_multi_q((vp * 3)(*[q.handle.value for q in qts]), 3, xq.data_ptr(), m,
+                                      (vp * 3)(*[y.data_ptr() for y in ys]), (i64 * 3)(*rows), S()))
+    for q, n, y in zip(qts, rows, ys):
+        want = torch.full((m, n), float("nan"), device=DEV)
+        qmm._check(L().qmm_matmul_q(q.handle, xq.data_ptr(), m, want.data_ptr(), n, S()))
+        assert torch.equal(y, want)
+
+
+def test_mixed_formats_other_than_k_quants_are_rejected():
+    rng = np.random.default_rng(60)
+    k = 1024
+    a = QTensor.quantize(t((rng.standard_normal((64, k)) * 0.02).astype(np.float32)), GgmlDType.Q4K)
+    b = QTensor.quantize(t((rng.standard_normal((64, k)) * 0.02).astype(np.float32)), GgmlDType.Q8_0)
+    x = t(rng.standard_normal((1, k)).astype(np.float32))
+    y = torch.zeros((2, 64), device=DEV)
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    rc = L().qmm_matmul_ex((vp * 2)(a.handle.value, b.handle.value), 2, x.data_ptr(), 1, k, None, ctypes.c_float(0), 0,
+                           (vp * 2)(y.data_ptr(), y.data_ptr() + 256), (i64 * 2)(64, 64), None, 0, S())
+    assert rc == 1 and "Q4_K/Q6_K" in qmm.last_error()
+
+
 @pytest.mark.parametrize("m", [1, 2, 12])
 def test_matmul_ex_accumulate(m):
     rng = np.random.default_rng(20 + m)
