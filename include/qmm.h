@@ -133,8 +133,10 @@ int qmm_matmul_multi(const qmm_qtensor *const *w, int count, const float *x, int
 int qmm_matmul_q(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy, void *stream);
 
 /* qmm_matmul_multi with activations already quantized (xq as for
- * qmm_matmul_q): `count` (1..8) weights of one dtype and k in one launch for
- * m <= 8 (one GEMM per weight for larger m). */
+ * qmm_matmul_q): `count` (1..8) weights of one k in one launch for m <= 8
+ * (one GEMM per weight for larger m). The weights share one dtype, or mix
+ * Q4_K and Q6_K (both multiply Q8_K activations): one launch at m = 1, one
+ * per dtype otherwise. */
 int qmm_matmul_multi_q(const qmm_qtensor *const *w, int count, const void *xq, int64_t m, float *const *y,
                        const int64_t *ldy, void *stream);
 
@@ -154,13 +156,15 @@ int qmm_matmul_q_ex(const qmm_qtensor *w, const void *xq, int64_t m, float *y, i
 int qmm_block_dots(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy,
                    int32_t *dots, void *stream);
 
-/* QMatMul::forward for 1..8 weights (same dtype and k) on one input, with the
- * decoder's neighbouring ops folded in: when norm_weight is non-NULL the input
- * rows are first RMS-normalised, x / sqrt(mean(x^2) + eps) * norm_weight
+/* QMatMul::forward for 1..8 weights (same k; one dtype, or Q4_K and Q6_K
+ * together as for qmm_matmul_multi_q, e.g. a Q4_K_M layer's q, k and v) on
+ * one input, with the decoder's neighbouring ops folded in: when norm_weight
+ * is non-NULL the input rows are first RMS-normalised, x / sqrt(mean(x^2) + eps) * norm_weight
  * (rms_norm, crates/llm/candle-llm/src/primitives/nn.rs:22-31; fused into the
  * quantization prologue for m <= 2), and when `accumulate` is set the result
  * is added to y (the residual add of llama.rs:958-975). ws: device scratch of
- * qmm_matmul_ex_workspace_size(w[0], m, norm_weight != NULL) bytes. */
+ * qmm_matmul_ex_workspace_size(w[j], m, norm_weight != NULL) bytes, the
+ * largest over the weights (m > 2 runs one pass per dtype). */
 int qmm_matmul_ex(const qmm_qtensor *const *w, int count, const float *x, int64_t m, int64_t ldx,
                   const float *norm_weight, float eps, int accumulate, float *const *y, const int64_t *ldy,
                   void *ws, size_t ws_bytes, void *stream);
