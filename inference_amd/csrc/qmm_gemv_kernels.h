@@ -60,6 +60,17 @@ struct FmtInfo<kFmtQ6K> {
 //        (chunks 0,1), high nibbles 64l + 32 + [0,32) (chunks 2,3).
 //   Q6_K lane l holds ql[64h + 32p, +32) (h = l/2, p = l%2): low nibbles are
 //        elements 128h + 32p + [0,32) (chunks 0,1), high nibbles 64 further (2,3).
+// Waves per workgroup: the kernel's compile-time size when it has one (NW >
+// 0), else blockDim (which costs a vector-memory load of the dispatch's
+// implicit arguments before anything else can be issued).
+template <int NW>
+__device__ __forceinline__ int block_waves() {
+  if constexpr (NW > 0)
+    return NW;
+  else
+    return blockDim.x >> 6;
+}
+
 template <int FMT>
 __device__ __forceinline__ int act_chunk(int l, int k) {
   return FMT == kFmtQ4K ? 64 * l + 16 * k : 128 * (l >> 1) + 32 * (l & 1) + 64 * (k >> 1) + 16 * (k & 1);
@@ -76,11 +87,12 @@ __device__ __forceinline__ int q80_slot(int b, int k) { return k ^ ((b >> 2) & 1
 //     Q4_K sums: lane l -> (bsum_4l + bsum_4l+1) | (bsum_4l+2 + bsum_4l+3) << 16
 //     Q6_K sums: lane l -> two u32: bsums of its chunks (0,1) and (2,3)
 //   Q8_0: q8 [blk][32] (swizzled halves), d f32 [blk]
-template <int FMT>
+template <int FMT, int NW = 0>
 __device__ __forceinline__ void stage_act(const uint8_t* __restrict__ xq, int nblk, uint8_t* lds) {
+  const int nthr = 64 * block_waves<NW>();
   if constexpr (FMT == kFmtQ80) {
     float* ld = reinterpret_cast<float*>(lds + 32 * nblk);
-    for (int t = threadIdx.x; t < 2 * nblk; t += blockDim.x) {
+    for (int t = threadIdx.x; t < 2 * nblk; t += nthr) {
       const int blk = t >> 1, half = t & 1;
       const uint16_t* s = reinterpret_cast<const uint16_t*>(xq + (size_t)kQ80Bytes * blk);
       const uint16_t* q = s + 1 + 8 * half;
@@ -95,7 +107,7 @@ __device__ __forceinline__ void stage_act(const uint8_t* __restrict__ xq, int nb
   } else {
     uint32_t* lsum = reinterpret_cast<uint32_t*>(lds + 256 * nblk);
     float* ld = reinterpret_cast<float*>(lsum + 8 * nblk);
-    for (int t = threadIdx.x; t < 16 * nblk; t += blockDim.x) {
+    for (int t = threadIdx.x; t < 16 * nblk; t += nthr) {
       const int blk = t >> 4, l = (t >> 2) & 3, k = t & 3;
       const uint8_t* s = xq + (size_t)kQ8KBytes * blk;
       const uint32_t* q = reinterpret_cast<const uint32_t*>(s + 4 + act_chunk<FMT>(l, k));
@@ -513,13 +525,14 @@ __device__ __forceinline__ void chunk_owner(int c16, int& l, int& k) {
 
 // RMSNorm denominators sqrt(mean(x^2) + eps) of mrows (<= 8) rows of k
 // elements, written to den[m] (LDS); the whole workgroup reduces.
+template <int NW = 0>
 __device__ __forceinline__ void rms_denominators(const float* __restrict__ x, long long ldx, int mrows, int k,
                                                  float eps, float* den, float* red) {
 #pragma clang fp contract(off)
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = block_waves<NW>();
   for (int m = 0; m < mrows; ++m) {
     float ss = 0.0f;
-    for (int i = threadIdx.x; i < k; i += blockDim.x) {
+    for (int i = threadIdx.x; i < k; i += 64 * nw) {
       const float v = x[m * ldx + i];
       ss += v * v;
     }
@@ -541,16 +554,16 @@ __device__ __forceinline__ void rms_denominators(const float* __restrict__ x, lo
 // With SILU, `x` is the gate row g and `norm_w` the up row u, and the
 // quantized activation is silu(g) * u (silu_mul, the same arithmetic as the
 // standalone qmm_silu_mul_q8k); no RMSNorm then.
-template <int FMT, bool SILU = false>
+template <int FMT, bool SILU = false, int NW = 0>
 __device__ __forceinline__ void quantize_act(const float* __restrict__ x, long long ldx, int mrows, int nb,
                                              uint8_t* lds, const float* __restrict__ norm_w, float eps) {
 #pragma clang fp contract(off)
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = block_waves<NW>();
   const int nblk = mrows * nb;
   __shared__ float den[8];
   __shared__ float red[8 * 16];
   if (!SILU && norm_w != nullptr)
-    rms_denominators(x, ldx, mrows, nb * FmtInfo<FMT>::kBlockElems, eps, den, red);
+    rms_denominators<NW>(x, ldx, mrows, nb * FmtInfo<FMT>::kBlockElems, eps, den, red);
   if constexpr (FMT == kFmtQ80) {
     float* ld = reinterpret_cast<float*>(lds + 32 * nblk);
     const int l8 = lane & 7;
@@ -669,34 +682,44 @@ __device__ __forceinline__ void put_q8k_lane(uint8_t* lds, int nb, int blk, cons
   if (lane == 0) ld[blk] = q.d;
 }
 
-template <int FMT, bool SILU, bool MIX = false>
-__device__ __forceinline__ void quantize_act1(const float* __restrict__ x, int nb, uint8_t* lds,
-                                              const float* __restrict__ norm_w, float eps) {
-#pragma clang fp contract(off)
-  static_assert(FMT != kFmtQ80, "k-quant activations");
-  static_assert(!MIX || FMT == kFmtQ4K, "mixed layouts: Q4_K then Q6_K");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  if (nb > kActPF * nw) {
-    quantize_act<FMT, SILU>(x, 0, 1, nb, lds, norm_w, eps);
-    if constexpr (MIX) {
-      __syncthreads();  // quantize_act's LDS scratch is reused
-      quantize_act<kFmtQ6K, SILU>(x, 0, 1, nb, lds + kQ8KBytes * nb, norm_w, eps);
-    }
-    return;
-  }
-  __shared__ float red[16];
-  __shared__ float den1;
+// The prologue's registers: wave w's blocks w, w + nw, ... of the f32 row
+// (e) and of the RMSNorm weight or the up row (a).
+struct Act1Regs {
   float4 e[kActPF], a[kActPF];
+};
+
+// First half of the one-row prologue: the loads only, so that a caller can
+// issue its weight loads behind them and still use the activation first.
+// `nw` = waves per workgroup (a constant in kernels that know their size:
+// blockDim costs a vector-memory load of the dispatch's implicit arguments).
+template <bool SILU>
+__device__ __forceinline__ void act1_load(Act1Regs& r, const float* __restrict__ x, int nb,
+                                          const float* __restrict__ norm_w, int nw) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const bool aux = SILU || norm_w != nullptr;
 #pragma unroll
   for (int i = 0; i < kActPF; ++i) {
     const int blk = wave + i * nw;
-    e[i] = a[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    r.e[i] = r.a[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (blk < nb) {
-      e[i] = *reinterpret_cast<const float4*>(x + 256 * blk + 4 * lane);
-      if (aux) a[i] = *reinterpret_cast<const float4*>(norm_w + 256 * blk + 4 * lane);
+      r.e[i] = *reinterpret_cast<const float4*>(x + 256 * blk + 4 * lane);
+      if (aux) r.a[i] = *reinterpret_cast<const float4*>(norm_w + 256 * blk + 4 * lane);
     }
   }
+}
+
+// Second half: RMSNorm or silu(g) * u, Q8_K quantization, LDS layout(s).
+template <int FMT, bool SILU, bool MIX = false>
+__device__ __forceinline__ void act1_finish(Act1Regs& r, int nb, uint8_t* lds, const float* __restrict__ norm_w,
+                                            float eps, int nw) {
+#pragma clang fp contract(off)
+  static_assert(FMT != kFmtQ80, "k-quant activations");
+  static_assert(!MIX || FMT == kFmtQ4K, "mixed layouts: Q4_K then Q6_K");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ float red[16];
+  __shared__ float den1;
+  float4* e = r.e;
+  const float4* a = r.a;
   if (!SILU && norm_w != nullptr) {
     float ss = 0.0f;
 #pragma unroll
@@ -742,13 +765,30 @@ __device__ __forceinline__ void quantize_act1(const float* __restrict__ x, int n
   }
 }
 
+template <int FMT, bool SILU, bool MIX = false, int NW = 0>
+__device__ __forceinline__ void quantize_act1(const float* __restrict__ x, int nb, uint8_t* lds,
+                                              const float* __restrict__ norm_w, float eps) {
+  const int nw = block_waves<NW>();
+  if (nb > kActPF * nw) {
+    quantize_act<FMT, SILU, NW>(x, 0, 1, nb, lds, norm_w, eps);
+    if constexpr (MIX) {
+      __syncthreads();  // quantize_act's LDS scratch is reused
+      quantize_act<kFmtQ6K, SILU, NW>(x, 0, 1, nb, lds + kQ8KBytes * nb, norm_w, eps);
+    }
+    return;
+  }
+  Act1Regs r;
+  act1_load<SILU>(r, x, nb, norm_w, nw);
+  act1_finish<FMT, SILU, MIX>(r, nb, lds, norm_w, eps, nw);
+}
+
 // y_j[m, n] = sum_b dot(W_j[n, b], X[m, b]) for every job j, m < M, n < rows_j.
 //   act: M rows of nb activation blocks (Q8_K or Q8_0, GGML bytes), or, when
 //        FUSED, M rows of f32 (row stride ldx) quantized in the prologue;
 //   dump (optional, single job): int32 block dots [M][rows][nb](x2 for Q4_K).
 // With `accumulate`, outputs are added to y (y += result); norm_w (fused only)
 // RMS-normalises the activation rows before quantization.
-template <int FMT, int M, int R, int U, bool FUSED, int J = 4, bool KARG = true>
+template <int FMT, int M, int R, int U, bool FUSED, int J = 4, bool KARG = true, int NW = 0>
 __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restrict__ act, long long ldx, int K,
                                      int* __restrict__ dump, int mrows = M,
                                      const float* __restrict__ norm_w = nullptr, float eps = 0.0f,
@@ -758,7 +798,7 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
   constexpr int BPI = 64 / LPB;  // blocks per wave iteration
   const int nb = K / FmtInfo<FMT>::kBlockElems;
   const int lane = threadIdx.x & 63;
-  const int nw = blockDim.x >> 6;
+  const int nw = block_waves<NW>();
   const int l = lane % LPB;
   const int g = lane / LPB;
   const int niter = (nb + BPI - 1) / BPI;
@@ -782,9 +822,9 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
 #pragma unroll
   for (int r = 0; r < R; ++r) rr[r] = row_ref<FMT, J, KARG>(jc, ja, jobs, row0 + r, nb);
   if constexpr (FUSED)
-    quantize_act<FMT>(reinterpret_cast<const float*>(act), ldx, mrows, nb, lds, norm_w, eps);
+    quantize_act<FMT, false, NW>(reinterpret_cast<const float*>(act), ldx, mrows, nb, lds, norm_w, eps);
   else
-    stage_act<FMT>(reinterpret_cast<const uint8_t*>(act), mrows * nb, lds);
+    stage_act<FMT, NW>(reinterpret_cast<const uint8_t*>(act), mrows * nb, lds);
   __syncthreads();
 
   float keep_v = 0.0f;  // M = 1: this lane's kept output (global row keep_row)
@@ -930,7 +970,7 @@ __device__ __forceinline__ void gemv1_rows(const GemvJobs& jobs, JobCursor& jc, 
 // MIX (FMT = Q4_K): global rows >= mix_row belong to Q6_K jobs (the host
 // orders the jobs Q4_K first); the activation is staged in both layouts and
 // a wave runs its Q4_K rows, then its Q6_K rows.
-template <int FMT, bool FUSED, int J, bool SILU = false, bool MIX = false>
+template <int FMT, bool FUSED, int J, bool SILU = false, bool MIX = false, int NW = 0>
 __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restrict__ act, long long ldx, int K,
                                       const float* __restrict__ norm_w, float eps, int accumulate,
                                       int mix_row = 0x7fffffff) {
@@ -940,7 +980,7 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
   constexpr int LPB = FmtInfo<FMT>::kLanesPerBlock;
   const int nb = K / FmtInfo<FMT>::kBlockElems;
   const int lane = threadIdx.x & 63;
-  const int nw = blockDim.x >> 6;
+  const int nw = block_waves<NW>();
   const int l = lane % LPB;
   const int g = lane / LPB;
   const int row_step = gridDim.x * nw;
@@ -969,12 +1009,12 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
   }
   if constexpr (FUSED) {
     if constexpr (FMT == kFmtQ80)
-      quantize_act<FMT, SILU>(reinterpret_cast<const float*>(act), ldx, 1, nb, lds, norm_w, eps);
+      quantize_act<FMT, SILU, NW>(reinterpret_cast<const float*>(act), ldx, 1, nb, lds, norm_w, eps);
     else
-      quantize_act1<FMT, SILU, MIX>(reinterpret_cast<const float*>(act), nb, lds, norm_w, eps);
+      quantize_act1<FMT, SILU, MIX, NW>(reinterpret_cast<const float*>(act), nb, lds, norm_w, eps);
   } else {
-    stage_act<FMT>(reinterpret_cast<const uint8_t*>(act), nb, lds);
-    if constexpr (MIX) stage_act<F6>(reinterpret_cast<const uint8_t*>(act), nb, lds6);
+    stage_act<FMT, NW>(reinterpret_cast<const uint8_t*>(act), nb, lds);
+    if constexpr (MIX) stage_act<F6, NW>(reinterpret_cast<const uint8_t*>(act), nb, lds6);
   }
   __syncthreads();
   if (row >= jobs.total) return;
@@ -1041,14 +1081,14 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
   extern "C" __global__ void __launch_bounds__(64 * W)                                                    \
       qmm_gemv_##NAME##_m##M##_w##W##_r##R##_u##U(QMM_GEMV_PARAMS) {                                      \
     QMM_GEMV_JOBS                                                                                         \
-    qmm::gemv<FMT, M, R, U, false>(jobs, act, ldx, K, dump, M, nullptr, 0.0f, accumulate);               \
+    qmm::gemv<FMT, M, R, U, false, 4, true, W>(jobs, act, ldx, K, dump, M, nullptr, 0.0f, accumulate);               \
   }
 
 #define QMM_GEMVF_KERNEL(FMT, NAME, M, W, R, U)                                                           \
   extern "C" __global__ void __launch_bounds__(64 * W)                                                    \
       qmm_gemvf_##NAME##_m##M##_w##W##_r##R##_u##U(QMM_GEMV_PARAMS) {                                     \
     QMM_GEMV_JOBS                                                                                         \
-    qmm::gemv<FMT, M, R, U, true>(jobs, act, ldx, K, dump, M, norm_w, eps, accumulate);                  \
+    qmm::gemv<FMT, M, R, U, true, 4, true, W>(jobs, act, ldx, K, dump, M, norm_w, eps, accumulate);                  \
   }
 
 // Eight-job variants (M = 1 only): one launch over up to eight weights that
@@ -1059,13 +1099,13 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
   extern "C" __global__ void __launch_bounds__(64 * W)                                                 \
       qmm_gemv_##NAME##_m1_w##W##_r##R##_u##U##_j8(QMM_GEMV_PARAMS8) {                                 \
     QMM_GEMV_JOBS8                                                                                     \
-    qmm::gemv<FMT, 1, R, U, false, 8>(jobs, act, ldx, K, dump, 1, nullptr, 0.0f, accumulate);          \
+    qmm::gemv<FMT, 1, R, U, false, 8, true, W>(jobs, act, ldx, K, dump, 1, nullptr, 0.0f, accumulate);          \
   }
 #define QMM_GEMVF_KERNEL8(FMT, NAME, W, R, U)                                                          \
   extern "C" __global__ void __launch_bounds__(64 * W)                                                 \
       qmm_gemvf_##NAME##_m1_w##W##_r##R##_u##U##_j8(QMM_GEMV_PARAMS8) {                                \
     QMM_GEMV_JOBS8                                                                                     \
-    qmm::gemv<FMT, 1, R, U, true, 8>(jobs, act, ldx, K, dump, 1, norm_w, eps, accumulate);             \
+    qmm::gemv<FMT, 1, R, U, true, 8, true, W>(jobs, act, ldx, K, dump, 1, norm_w, eps, accumulate);             \
   }
 
 // One-row decode kernels (gemv1): four-job and eight-job tables, staged
@@ -1073,44 +1113,44 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
 #define QMM_GEMV1_KERNELS(FMT, NAME, W)                                                              \
   extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1_##NAME##_w##W(QMM_GEMV_PARAMS) {    \
     QMM_GEMV_JOBS                                                                                    \
-    qmm::gemv1<FMT, false, 4>(jobs, act, ldx, K, nullptr, 0.0f, accumulate);                         \
+    qmm::gemv1<FMT, false, 4, false, false, W>(jobs, act, ldx, K, nullptr, 0.0f, accumulate);                         \
   }                                                                                                  \
   extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1f_##NAME##_w##W(QMM_GEMV_PARAMS) {   \
     QMM_GEMV_JOBS                                                                                    \
-    qmm::gemv1<FMT, true, 4>(jobs, act, ldx, K, norm_w, eps, accumulate);                            \
+    qmm::gemv1<FMT, true, 4, false, false, W>(jobs, act, ldx, K, norm_w, eps, accumulate);                            \
   }                                                                                                  \
   extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1_##NAME##_w##W##_j8(QMM_GEMV_PARAMS8) { \
     QMM_GEMV_JOBS8                                                                                   \
-    qmm::gemv1<FMT, false, 8>(jobs, act, ldx, K, nullptr, 0.0f, accumulate);                         \
+    qmm::gemv1<FMT, false, 8, false, false, W>(jobs, act, ldx, K, nullptr, 0.0f, accumulate);                         \
   }                                                                                                  \
   extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1f_##NAME##_w##W##_j8(QMM_GEMV_PARAMS8) { \
     QMM_GEMV_JOBS8                                                                                   \
-    qmm::gemv1<FMT, true, 8>(jobs, act, ldx, K, norm_w, eps, accumulate);                            \
+    qmm::gemv1<FMT, true, 8, false, false, W>(jobs, act, ldx, K, norm_w, eps, accumulate);                            \
   }
 // silu(g) * u quantized in the prologue (act = g, norm_w = u).
 #define QMM_GEMV1S_KERNEL(FMT, NAME, W)                                                              \
   extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1s_##NAME##_w##W(QMM_GEMV_PARAMS) {   \
     QMM_GEMV_JOBS                                                                                    \
-    qmm::gemv1<FMT, true, 4, true>(jobs, act, ldx, K, norm_w, 0.0f, accumulate);                     \
+    qmm::gemv1<FMT, true, 4, true, false, W>(jobs, act, ldx, K, norm_w, 0.0f, accumulate);                     \
   }
 // Mixed Q4_K / Q6_K jobs (e.g. a layer's q, k and v projections in one
 // launch); rows >= mix_row are the Q6_K jobs'.
 #define QMM_GEMV1_MIX_KERNELS(W)                                                                               \
   extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1_q4k6k_w##W(QMM_GEMV_PARAMS, int mix_row) {    \
     QMM_GEMV_JOBS                                                                                              \
-    qmm::gemv1<qmm::kFmtQ4K, false, 4, false, true>(jobs, act, ldx, K, nullptr, 0.0f, accumulate, mix_row);     \
+    qmm::gemv1<qmm::kFmtQ4K, false, 4, false, true, W>(jobs, act, ldx, K, nullptr, 0.0f, accumulate, mix_row);     \
   }                                                                                                            \
   extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1f_q4k6k_w##W(QMM_GEMV_PARAMS, int mix_row) {   \
     QMM_GEMV_JOBS                                                                                              \
-    qmm::gemv1<qmm::kFmtQ4K, true, 4, false, true>(jobs, act, ldx, K, norm_w, eps, accumulate, mix_row);        \
+    qmm::gemv1<qmm::kFmtQ4K, true, 4, false, true, W>(jobs, act, ldx, K, norm_w, eps, accumulate, mix_row);        \
   }                                                                                                            \
   extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1_q4k6k_w##W##_j8(QMM_GEMV_PARAMS8, int mix_row) { \
     QMM_GEMV_JOBS8                                                                                             \
-    qmm::gemv1<qmm::kFmtQ4K, false, 8, false, true>(jobs, act, ldx, K, nullptr, 0.0f, accumulate, mix_row);     \
+    qmm::gemv1<qmm::kFmtQ4K, false, 8, false, true, W>(jobs, act, ldx, K, nullptr, 0.0f, accumulate, mix_row);     \
   }                                                                                                            \
   extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1f_q4k6k_w##W##_j8(QMM_GEMV_PARAMS8, int mix_row) { \
     QMM_GEMV_JOBS8                                                                                             \
-    qmm::gemv1<qmm::kFmtQ4K, true, 8, false, true>(jobs, act, ldx, K, norm_w, eps, accumulate, mix_row);        \
+    qmm::gemv1<qmm::kFmtQ4K, true, 8, false, true, W>(jobs, act, ldx, K, norm_w, eps, accumulate, mix_row);        \
   }
 #define QMM_GEMV1_SHAPES(FMT, NAME) \
   QMM_GEMV1_KERNELS(FMT, NAME, 4)   \

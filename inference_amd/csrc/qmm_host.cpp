@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -73,11 +74,12 @@ Device* g_dev[64] = {};
 // batch), QMM_GEMV_WAVES_PER_CU (resident waves the grid is sized for) and
 // QMM_GEMV1=0 (use the general kernel for one activation row too).
 struct Tuning {
-  int w = 0, r = 0, u = 0, waves_per_cu = 0, gemv1 = 1;
+  int w = 0, r = 0, u = 0, waves_per_cu = 0, gemv1 = 1, gemv1p = -1;
 };
 Tuning tuning() {
   Tuning t;
   if (const char* s = getenv("QMM_GEMV1")) t.gemv1 = atoi(s);
+  if (const char* s = getenv("QMM_GEMV1P")) t.gemv1p = atoi(s);
   if (const char* s = getenv("QMM_GEMV_CFG")) {
     if (sscanf(s, "%d,%d,%d", &t.w, &t.r, &t.u) != 3) t.w = t.r = t.u = 0;
   }
@@ -564,8 +566,29 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   // (gemv1: activation slice kept in registers, one row per wave at a time).
   const bool one = m == 1 && dump == nullptr && r == 1 && u == 1 && (wv == 4 || wv == 8 || wv == 16) &&
                    tu.gemv1 != 0;
+  // k-quant weights with an activation of at most 64 blocks (K <= 16384):
+  // the prefetch-ring kernels (gemv1p), one 16-wave workgroup per CU; their
+  // prologue stages one activation item per thread. From sweeps at the decode
+  // shapes they beat gemv1 for Q6_K rows of several slices (down 4096x14336:
+  // 13.2 vs 13.9 us staged, 15.4 vs 16.1 fused, two slices in flight) and for
+  // staged Q4_K launches of one row per wave (q 4096x4096: 4.8 vs 5.1 us);
+  // gemv1 keeps the rest. QMM_GEMV1P=<P> forces them (0: never).
+  const long long rows_cu = (long long)d->num_cu * 16;
+  bool ring = m == 1 && dump == nullptr && fmt != kFmtQ80 && nb <= 64 && tu.gemv1p != 0 && !silu &&
+              !(tu.w > 0 && tu.r > 0 && tu.u > 0);
+  if (ring && tu.gemv1p < 0)
+    ring = !mixed && ((fmt == kFmtQ6K && niter >= 2) ||
+                      (fmt == kFmtQ4K && !fused && total > rows_cu / 4 && total <= rows_cu));
   char name[80];
-  if (silu) {
+  if (ring) {
+    wv = 16;
+    waves_per_cu = 16;
+    // prefetch depth (instantiated: 1, 2)
+    int pd = fmt == kFmtQ4K ? 1 : 2;
+    if (tu.gemv1p > 0) pd = std::min(tu.gemv1p, 2);
+    snprintf(name, sizeof(name), "qmm_gemv1p%s_%s_w16_p%d%s", fused ? "f" : "", mixed ? "q4k6k" : fmt_name(fmt), pd,
+             jcap > 4 ? "_j8" : "");
+  } else if (silu) {
     // silu(g) * u in the prologue: one-row kernels with a four-job table, 8 or 16 waves
     if (!fused || m != 1 || dump || count > 4) return fail(QMM_ERR_INVALID, "silu prologue needs one fused row");
     wv = wv >= 16 ? 16 : 8;

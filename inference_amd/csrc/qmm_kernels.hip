@@ -5,6 +5,7 @@
 #include "qmm_common.h"
 #include "qmm_quant_kernels.h"
 #include "qmm_gemv_kernels.h"
+#include "qmm_gemv1p_kernels.h"
 #include "qmm_mmq_kernels.h"
 #include "qmm_moe_kernels.h"
 #include "qmm_decode_kernels.h"

@@ -166,7 +166,7 @@ __device__ __forceinline__ void moe_gemv(const uint8_t* w0, const uint8_t* w1, i
     jobs.njobs = njobs;
     jobs.total = njobs * N;
     const int mrows = me - mc < 8 ? me - mc : 8;
-    qmm::gemv<FMT, 8, 1, U, false, qmm::kMaxJobs, false>(jobs, xq + (size_t)(off + mc) * xrow, 0, K, nullptr, mrows);
+    qmm::gemv<FMT, 8, 1, U, false, qmm::kMaxJobs, false, 8>(jobs, xq + (size_t)(off + mc) * xrow, 0, K, nullptr, mrows);
   }
 }
 
