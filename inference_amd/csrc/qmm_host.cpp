@@ -1095,8 +1095,16 @@ int qmm_moe_gemv(const qmm_qtensor* const* w, int count, int experts, const void
   const int niter = (nb + bpi - 1) / bpi;
   const unsigned lds = (unsigned)(8 * nb * (fmt == kFmtQ80 ? 36 : 292));
   if ((int)lds > d->max_lds) return fail(QMM_ERR_UNSUPPORTED, "expert activation needs %u B of LDS", lds);
+  // k-quants: the one-row ring kernels (16 waves, two workgroups per CU when
+  // every expert is active); QMM_MOE_GEMV=0 selects the generic M = 8 GEMV,
+  // QMM_MOE_GEMV=<P> the ring depth.
+  int ring = fmt == kFmtQ4K ? 2 : fmt == kFmtQ6K ? 1 : 0;
+  if (const char* e = getenv("QMM_MOE_GEMV")) ring = fmt != kFmtQ80 ? std::min(std::max(atoi(e), 0), 2) : 0;
   char name[48];
-  snprintf(name, sizeof(name), "qmm_moe_gemv_%s_u%d", fmt_name(fmt), niter >= 2 ? 2 : 1);
+  if (ring)
+    snprintf(name, sizeof(name), "qmm_moe_gemv1_%s_p%d", fmt_name(fmt), ring);
+  else
+    snprintf(name, sizeof(name), "qmm_moe_gemv_%s_u%d", fmt_name(fmt), niter >= 2 ? 2 : 1);
   const int vt = qmm_vec_dot_type(w[0]->dtype);
   long long xrow = (w[0]->k / qmm_block_size(vt)) * qmm_type_size(vt);
   int N = (int)(w[0]->n / experts), E = experts, nj = count, K = (int)w[0]->k, ld = N;
@@ -1106,15 +1114,18 @@ int qmm_moe_gemv(const qmm_qtensor* const* w, int count, int experts, const void
   float* y1 = count > 1 ? y[1] : y[0];
   const void* xp = xq;
   void* args[] = {&w0, &w1, &nj, &N, &E, &y0, &y1, &ld, &xp, &xrow, &counts, &offsets, &K};
-  // ~20 resident waves per CU spread over the experts (idle experts exit at once)
-  long long gx = ((long long)d->num_cu * 20 / 8 + E - 1) / E;
-  const long long need = ((long long)N * count + 7) / 8;
+  // generic: ~20 resident waves per CU spread over the experts; ring: two
+  // 16-wave workgroups per CU over the experts (idle experts exit at once)
+  const int wpg = ring ? 16 : 8;
+  long long gx = ring ? ((long long)d->num_cu * 2 + E - 1) / E : ((long long)d->num_cu * 20 / 8 + E - 1) / E;
+  const long long need = ((long long)N * count + wpg - 1) / wpg;
   if (gx > need) gx = need;
   if (gx < 1) gx = 1;
   hipFunction_t f;
   QMM_TRY(kernel(d, name, &f));
   (void)pairs;
-  QMM_HIP(hipModuleLaunchKernel(f, (unsigned)gx, (unsigned)E, 1, 512, 1, 1, lds, (hipStream_t)stream, args, nullptr));
+  QMM_HIP(hipModuleLaunchKernel(f, (unsigned)gx, (unsigned)E, 1, 64 * wpg, 1, 1, lds, (hipStream_t)stream, args,
+                                nullptr));
   return QMM_OK;
 }
 

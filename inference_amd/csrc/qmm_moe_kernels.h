@@ -12,6 +12,7 @@
 
 #include "qmm_common.h"
 #include "qmm_gemv_kernels.h"
+#include "qmm_gemv1p_kernels.h"
 #include "qmm_quant_kernels.h"
 
 // Routing: logits f32 [T][E] -> per-expert lists of (token, weight) pairs,
@@ -169,6 +170,116 @@ __device__ __forceinline__ void moe_gemv(const uint8_t* w0, const uint8_t* w1, i
     qmm::gemv<FMT, 8, 1, U, false, qmm::kMaxJobs, false, 8>(jobs, xq + (size_t)(off + mc) * xrow, 0, K, nullptr, mrows);
   }
 }
+
+// Expert-grouped GEMV for k-quant weights, one row per wave at a time with a
+// prefetch ring (the gemv1p structure): blockIdx.y = expert e, whose
+// counts[e] token rows (8 per pass) are staged in LDS once per workgroup; a
+// wave's weight slice is unpacked once (prep_w) and multiplied with each
+// token row, and each row's outputs are stored by lanes 0..rows-1 together.
+// The per-token accumulators are eight scalars, so register use stays at the
+// one-row kernels' level (the generic M = 8 GEMV keeps eight activation
+// slices live and spills at these shapes). Experts without tokens exit at once.
+template <int FMT, int P, int NW>
+__device__ __forceinline__ void moe_gemv1(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, int njobs,
+                                          int N, int E, float* __restrict__ y0, float* __restrict__ y1, int ldy,
+                                          const uint8_t* __restrict__ xq, long long xrow,
+                                          const int* __restrict__ counts, const int* __restrict__ offsets, int K) {
+  using namespace qmm;
+  static_assert(FMT != kFmtQ80, "k-quant weights");
+  constexpr int BPI = 16;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int e = blockIdx.y;
+  const int me = counts[e];
+  if (me == 0) return;
+  const int off = offsets[e];
+  const int nb = K / 256, niter = (nb + BPI - 1) / BPI;
+  const int lane = threadIdx.x & 63, l = lane & 3, g = lane >> 2;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int total = njobs * N;
+  const int row_step = gridDim.x * NW;
+  const int row0 = blockIdx.x * NW + wave;
+  const int nrows = row0 < total ? (total - 1 - row0) / row_step + 1 : 0;
+  const int nslices = nrows * niter;
+  const size_t rowb = (size_t)nb * FmtInfo<FMT>::kBodyBytes;
+  const size_t trows = (size_t)E * N;
+  for (int mc = 0; mc < me; mc += 8) {
+    const int mr = min(8, me - mc);
+    int is_s = 0, is_k = 0, is_it = 0;
+    WSlice ring[P];
+    auto issue = [&](WSlice& w) {
+      const int gr = row0 + is_k * row_step;  // < total while is_s < nslices
+      const int j = gr >= N ? 1 : 0;
+      const uint8_t* wq = j ? w1 : w0;
+      const size_t trow = (size_t)e * N + (gr - j * N);
+      const uint8_t* wrow = wq + trow * rowb;
+      const uint16_t* drow = reinterpret_cast<const uint16_t*>(wq + trows * rowb) + trow * nb;
+      load_slice<FMT>(w, wrow, drow, (uint32_t)min(is_it * BPI + g, nb - 1), l);
+      if (++is_it == niter) {
+        is_it = 0;
+        ++is_k;
+      }
+      ++is_s;
+    };
+#pragma unroll
+    for (int u = 0; u < P; ++u)
+      if (is_s < nslices) issue(ring[u]);
+    if (mc > 0) __syncthreads();  // the previous pass's LDS reads are done
+    stage_act<FMT, NW>(xq + (size_t)(off + mc) * xrow, mr * nb, lds);
+    __syncthreads();
+    float acc[8];
+    int c_k = 0, c_it = 0;
+    for (int s0 = 0; s0 < nslices; s0 += P) {
+#pragma unroll
+      for (int u = 0; u < P; ++u) {
+        if (s0 + u < nslices) {
+          const int b = c_it * BPI + g;
+          const bool okb = b < nb;
+          const int bx = okb ? b : 0;
+          const WPrep wp = prep_w<FMT>(ring[u], l);
+#pragma unroll
+          for (int m = 0; m < 8; ++m) {
+            if (m < mr) {  // wave-uniform
+              XSlice x;
+              load_x<FMT>(x, lds, mr * nb, m * nb + bx, l);
+              int ia, ib;
+              float p = dot_wx<FMT>(wp, x, ia, ib);
+              p = okb ? p : 0.0f;
+              acc[m] = c_it == 0 ? p : acc[m] + p;
+            }
+          }
+          if (++c_it == niter) {
+            const int gr = row0 + c_k * row_step;
+            const int j = gr >= N ? 1 : 0;
+            float out = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+              if (m < mr) {
+                const float v = wave_total(acc[m]);
+                out = lane == m ? v : out;
+              }
+            }
+            if (lane < mr) (j ? y1 : y0)[(size_t)(off + mc + lane) * ldy + (gr - j * N)] = out;
+            c_it = 0;
+            ++c_k;
+          }
+        }
+        if (is_s < nslices) issue(ring[u]);
+      }
+    }
+  }
+}
+
+#define QMM_MOE1_KERNEL(FMT, NAME, P)                                                                           \
+  extern "C" __global__ void __launch_bounds__(1024)                                                            \
+      qmm_moe_gemv1_##NAME##_p##P(const uint8_t* w0, const uint8_t* w1, int njobs, int N, int E, float* y0,   \
+                                  float* y1, int ldy, const uint8_t* __restrict__ xq, long long xrow,           \
+                                  const int* __restrict__ counts, const int* __restrict__ offsets, int K) {    \
+    moe_gemv1<FMT, P, 16>(w0, w1, njobs, N, E, y0, y1, ldy, xq, xrow, counts, offsets, K);                     \
+  }
+QMM_MOE1_KERNEL(qmm::kFmtQ4K, q4k, 1)
+QMM_MOE1_KERNEL(qmm::kFmtQ4K, q4k, 2)
+QMM_MOE1_KERNEL(qmm::kFmtQ6K, q6k, 1)
+QMM_MOE1_KERNEL(qmm::kFmtQ6K, q6k, 2)
 
 #define QMM_MOE_KERNEL(FMT, NAME, U)                                                                          \
   extern "C" __global__ void __launch_bounds__(512)                                                           \

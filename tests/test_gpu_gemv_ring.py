@@ -154,3 +154,39 @@ def test_default_policy_uses_ring_for_q6k_long_rows():
     finally:
         del os.environ["QMM_GEMV1P"]
     assert torch.equal(got, ref)
+
+
+def _moe_gemv(qts, E, xq, P, counts, offsets, F):
+    ys = [torch.full((P, F), float("nan"), device=DEV) for _ in qts]
+    qmm._check(L().qmm_moe_gemv((vp * len(qts))(*[q.handle.value for q in qts]), len(qts), E, xq.data_ptr(), P,
+                                counts.data_ptr(), offsets.data_ptr(), (vp * len(qts))(*[y.data_ptr() for y in ys]),
+                                S()))
+    torch.cuda.synchronize()
+    return ys
+
+
+@pytest.mark.parametrize("dt,K", [(GgmlDType.Q4K, 4096), (GgmlDType.Q6K, 5120), (GgmlDType.Q4K, 5120)])
+@pytest.mark.parametrize("skew", [False, True])
+def test_moe_ring_gemv_equals_generic(monkeypatch, dt, K, skew):
+    """The expert ring GEMV (QMM_MOE_GEMV=P) against the generic M = 8 expert GEMV: bit-identical, including
+    experts with more than eight tokens (skew: every token routes to experts 0 and 1)."""
+    from inference_amd import moe_route
+    E, F, T, k = 4, 768, 10, 2
+    rng = np.random.default_rng(K + int(skew))
+    qts = [QTensor.quantize(t((rng.standard_normal((E * F, K)) * 0.02).astype(np.float32)), dt) for _ in range(2)]
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    if skew:
+        logits[:, :2] += 10.0
+    counts, offsets, ptok, pw, tp = moe_route(t(logits), k)
+    P = T * k
+    xg = t(rng.standard_normal((T, K)).astype(np.float32))[ptok.long()]
+    xq = t(orc.quantize(orc.Q8K, xg.cpu().numpy()), torch.uint8)
+    monkeypatch.setenv("QMM_MOE_GEMV", "0")
+    ref = _moe_gemv(qts, E, xq, P, counts, offsets, F)
+    for p in ("1", "2"):
+        monkeypatch.setenv("QMM_MOE_GEMV", p)
+        got = _moe_gemv(qts, E, xq, P, counts, offsets, F)
+        for a, b in zip(got, ref):
+            assert torch.equal(a, b), f"P={p}"
+    if skew:
+        assert int(counts[0]) > 8
