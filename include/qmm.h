@@ -272,6 +272,66 @@ int qmm_moe_ffn(const float *x, int64_t tokens, int64_t ldx, const float *logits
                 const qmm_qtensor *gate, const qmm_qtensor *up, const qmm_qtensor *down, float *out,
                 int64_t ldo, void *ws, size_t ws_bytes, void *stream);
 
+/* ---------------------------------------------------------------------------
+ * GGUF files (llama.cpp's single-file model container, spec v2/v3).
+ * Replaces the reference's GgufFile (crates/llm/mlx-llm/src/gguf/reader.rs:
+ * GgufFile::open/parse :188-278, meta/meta_str/meta_u64/meta_f64 :281-303,
+ * tensor_data :307-328; MetaValue::as_u64/as_i64/as_f64/as_str :73-131) and
+ * candle's gguf_file::Content::{read, tensor} at the engine's call sites
+ * (crates/llm/candle-llm/src/gguf.rs:68, 101-103). Unlike the engine, which
+ * dequantizes every tensor and re-quantizes it, qmm_gguf_load_qtensor puts
+ * a quantized tensor's blocks straight into a device QTensor.
+ * ------------------------------------------------------------------------- */
+typedef struct qmm_gguf qmm_gguf;
+
+/* Open a file (memory-mapped, read only) or an in-memory image (copied).
+ * Errors: bad magic, version other than 2 or 3 (QMM_ERR_UNSUPPORTED), counts
+ * above 2^20, truncated tables, tensors of 0 or more than 4 dims, nested
+ * arrays, unknown value types, a data section past the end of the file. */
+int qmm_gguf_open(const char *path, qmm_gguf **out);
+int qmm_gguf_open_memory(const void *bytes, size_t len, qmm_gguf **out);
+void qmm_gguf_close(qmm_gguf *g);
+
+int qmm_gguf_version(const qmm_gguf *g);
+/* general.alignment when it is an integer (>= 1), else 32. */
+uint64_t qmm_gguf_alignment(const qmm_gguf *g);
+int64_t qmm_gguf_tensor_count(const qmm_gguf *g);
+int64_t qmm_gguf_metadata_count(const qmm_gguf *g);
+
+/* Index of a tensor / metadata key (-1 if absent; a repeated key keeps its last value). */
+int64_t qmm_gguf_find_tensor(const qmm_gguf *g, const char *name);
+int64_t qmm_gguf_meta_find(const qmm_gguf *g, const char *key);
+
+/* Tensor i: name (owned by g), dims, shape in torch order (the GGML ne order
+ * reversed: [out, in] for a linear weight; unused entries 0), GGML type tag
+ * and byte offset within the data section. */
+int qmm_gguf_tensor_info(const qmm_gguf *g, int64_t i, const char **name, int *ndims, int64_t *shape,
+                         int *ggml_type, uint64_t *offset);
+/* (elements, bytes) per block of a GGML type tag (dequant.rs:86-140). */
+int qmm_gguf_type_size(int ggml_type, uint64_t *block_elems, uint64_t *block_bytes);
+/* Host pointer to tensor i's bytes inside the file and their length
+ * (elements / block_elems * block_bytes); out-of-range data is an error. */
+int qmm_gguf_tensor_data(const qmm_gguf *g, int64_t i, const void **data, size_t *bytes);
+
+/* Metadata entry i: key, value type (GGUF tags 0..12; 9 = array), element
+ * type (arrays) and count (1 for scalars). Values: elem = -1 for a scalar,
+ * else the array element. u64 takes unsigned integers, non-negative signed
+ * ones and bools; i64 any integer; f64 f32/f64; string a pointer into the
+ * file (not NUL-terminated) and its length. A type mismatch is an error. */
+int qmm_gguf_meta_info(const qmm_gguf *g, int64_t i, const char **key, int *type, int *elem_type,
+                       uint64_t *count);
+int qmm_gguf_meta_u64(const qmm_gguf *g, int64_t i, int64_t elem, uint64_t *v);
+int qmm_gguf_meta_i64(const qmm_gguf *g, int64_t i, int64_t elem, int64_t *v);
+int qmm_gguf_meta_f64(const qmm_gguf *g, int64_t i, int64_t elem, double *v);
+int qmm_gguf_meta_string(const qmm_gguf *g, int64_t i, int64_t elem, const char **s, uint64_t *len);
+
+/* Resident load of a 2-D Q8_0 / Q4_K / Q6_K tensor into a device QTensor
+ * (QStorage::from_data + QTensor::new, candle-gen/src/quant/repack.rs:202-203),
+ * on the current device, synchronous. unpermute_heads > 0 undoes llama.cpp's
+ * q/k row order per head on the quantized rows (unpermute_qk, candle-llm
+ * gguf.rs:333-356: torch row k * hd/2 + j of a head is GGUF row 2j + k). */
+int qmm_gguf_load_qtensor(const qmm_gguf *g, int64_t i, int unpermute_heads, void *stream, qmm_qtensor **out);
+
 #ifdef __cplusplus
 }
 #endif

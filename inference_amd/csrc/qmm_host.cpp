@@ -34,6 +34,13 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+}  // namespace
+
+// Error reporting for the library's other translation units (qmm_gguf.cpp).
+__attribute__((visibility("hidden"))) int qmm_internal_fail(int code, const char* msg) { return fail(code, "%s", msg); }
+
+namespace {
+
 #define QMM_HIP(expr)                                                                 \
   do {                                                                                \
     hipError_t e_ = (expr);                                                           \

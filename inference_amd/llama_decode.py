@@ -136,6 +136,75 @@ class LlamaWeights:
         return cls(cfg, layers, head, embed, [ones() for _ in range(cfg.layers)],
                    [ones() for _ in range(cfg.layers)], ones())
 
+    @classmethod
+    def from_gguf(cls, path, device: torch.device) -> "LlamaWeights":
+        """Resident load of a llama-architecture GGUF file (the engine's GgufCheckpoint::open,
+        crates/llm/candle-llm/src/gguf.rs:63-170, without its dequantize -> re-quantize): projections
+        go straight into device QTensors (q/k rows un-permuted from llama.cpp's order on the quantized
+        rows), the token embedding is dequantized to f32 on the device, norms are read as f32, and a
+        missing output.weight ties the head to the embedding's quantized tensor. The configuration
+        follows reconstruct_config (gguf.rs:361-428): absent llama3 RoPE-scaling keys mean standard
+        RoPE (factor 1)."""
+        from .gguf import GgufFile, GGML_Q4K, GGML_Q6K
+        f = path if isinstance(path, GgufFile) else GgufFile.open(path)
+        arch = f.meta_str("general.architecture")
+        if arch != "llama":
+            raise qmm.QmmError(qmm.QMM_ERR_UNSUPPORTED, f"gguf: architecture {arch!r} (llama only)")
+
+        def req(k):
+            v = f.meta_u64(f"{arch}.{k}")
+            if v is None:
+                raise qmm.QmmError(qmm.QMM_ERR_INVALID, f"gguf: missing metadata {arch}.{k}")
+            return v
+
+        heads = req("attention.head_count")
+        kv = f.meta_u64(f"{arch}.attention.head_count_kv") or heads
+        hidden = req("embedding_length")
+        head_dim = f.meta_u64(f"{arch}.attention.key_length") or hidden // heads
+        infos = {t.name: t for t in f.tensors}
+        if "token_embd.weight" not in infos:
+            raise qmm.QmmError(qmm.QMM_ERR_INVALID, "gguf: no token embedding tensor")
+        low = f.meta_f64(f"{arch}.rope.scaling.low_freq_factor")
+        high = f.meta_f64(f"{arch}.rope.scaling.high_freq_factor")
+        llama3 = f.meta_str(f"{arch}.rope.scaling.type") == "llama3" or low is not None or high is not None
+        cfg = LlamaConfig(
+            layers=req("block_count"), hidden=hidden, ffn=req("feed_forward_length"), heads=heads, kv_heads=kv,
+            head_dim=head_dim, vocab=infos["token_embd.weight"].shape[0],
+            rope_theta=f.meta_f64(f"{arch}.rope.freq_base") or 10000.0,
+            rope_factor=(f.meta_f64(f"{arch}.rope.scaling.factor") or 8.0) if llama3 else 1.0,
+            rope_low=low if low is not None else 1.0, rope_high=high if high is not None else 4.0,
+            rope_orig_ctx=float(f.meta_u64(f"{arch}.rope.scaling.original_context_length") or 8192),
+            eps=f.meta_f64(f"{arch}.attention.layer_norm_rms_epsilon") or 1e-5)
+
+        def tensor(name):
+            if name not in infos:
+                raise qmm.QmmError(qmm.QMM_ERR_INVALID, f"gguf: missing tensor {name}")
+            return infos[name]
+
+        names = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate",
+                 "up": "ffn_up", "down": "ffn_down"}
+        layers, attn_norm, ffn_norm = [], [], []
+        for li in range(cfg.layers):
+            lw = {}
+            for key, gname in names.items():
+                info = tensor(f"blk.{li}.{gname}.weight")
+                if info.ggml_type not in (GGML_Q4K, GGML_Q6K):
+                    raise qmm.QmmError(qmm.QMM_ERR_UNSUPPORTED,
+                                       f"gguf: {info.name} has GGML type {info.ggml_type} (Q4_K / Q6_K projections)")
+                unperm = cfg.heads if key == "q" else cfg.kv_heads if key == "k" else 0
+                lw[key] = f.load_qtensor(info, device, unperm)
+            layers.append(lw)
+            attn_norm.append(f.load_dense(tensor(f"blk.{li}.attn_norm.weight"), device).float())
+            ffn_norm.append(f.load_dense(tensor(f"blk.{li}.ffn_norm.weight"), device).float())
+        emb_info = infos["token_embd.weight"]
+        embed = f.load_dense(emb_info, device).float().contiguous()
+        head_info = infos.get("output.weight", emb_info)
+        head = f.load_qtensor(head_info, device)
+        cfg.dtypes = {k: v.dtype() for k, v in layers[0].items()}
+        cfg.dtypes["head"] = head.dtype()
+        return cls(cfg, layers, head, embed, attn_norm, ffn_norm,
+                   f.load_dense(tensor("output_norm.weight"), device).float())
+
     def export(self) -> dict:
         """Host copies for the CPU reference: GGML bytes per tensor, f32 embedding and norms."""
         return {"layers": [{n: t.to_ggml() for n, t in lw.items()} for lw in self.layers],

@@ -36,6 +36,9 @@ class QmmError(RuntimeError):
         self.status = status
 
 
+# status codes of the C ABI (include/qmm.h)
+QMM_OK, QMM_ERR_INVALID, QMM_ERR_HIP, QMM_ERR_NO_KERNEL, QMM_ERR_UNSUPPORTED, QMM_ERR_OOM = range(6)
+
 _lib = None
 _lib_lock = threading.Lock()
 
@@ -49,6 +52,11 @@ EXPORTS = (
     "qmm_rope_kv_append", "qmm_decode_attention", "qmm_silu_mul_quantize", "qmm_greedy_advance",
     "qmm_matmul_q_ex", "qmm_decode_attention_workspace_size", "qmm_decode_rope_attention",
     "qmm_greedy_workspace_size", "qmm_matmul_multi_q", "qmm_silu_mul_matmul",
+    "qmm_gguf_open", "qmm_gguf_open_memory", "qmm_gguf_close", "qmm_gguf_version", "qmm_gguf_alignment",
+    "qmm_gguf_tensor_count", "qmm_gguf_metadata_count", "qmm_gguf_find_tensor", "qmm_gguf_meta_find",
+    "qmm_gguf_tensor_info", "qmm_gguf_type_size", "qmm_gguf_tensor_data", "qmm_gguf_meta_info",
+    "qmm_gguf_meta_u64", "qmm_gguf_meta_i64", "qmm_gguf_meta_f64", "qmm_gguf_meta_string",
+    "qmm_gguf_load_qtensor",
 )
 
 
@@ -107,6 +115,26 @@ def lib() -> ctypes.CDLL:
             "qmm_silu_mul_matmul": ([vp, vp, vp, vp, i32, vp], i32),
             "qmm_matmul_multi_q": ([ctypes.POINTER(vp), i32, vp, i64, ctypes.POINTER(vp), ctypes.POINTER(i64), vp],
                                    i32),
+            "qmm_gguf_open": ([ctypes.c_char_p, pp], i32),
+            "qmm_gguf_open_memory": ([ctypes.c_char_p, sz, pp], i32),
+            "qmm_gguf_close": ([vp], None),
+            "qmm_gguf_version": ([vp], i32),
+            "qmm_gguf_alignment": ([vp], ctypes.c_uint64),
+            "qmm_gguf_tensor_count": ([vp], i64),
+            "qmm_gguf_metadata_count": ([vp], i64),
+            "qmm_gguf_find_tensor": ([vp, ctypes.c_char_p], i64),
+            "qmm_gguf_meta_find": ([vp, ctypes.c_char_p], i64),
+            "qmm_gguf_tensor_info": ([vp, i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(i32),
+                                      ctypes.POINTER(i64), ctypes.POINTER(i32), ctypes.POINTER(ctypes.c_uint64)], i32),
+            "qmm_gguf_type_size": ([i32, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)], i32),
+            "qmm_gguf_tensor_data": ([vp, i64, pp, ctypes.POINTER(sz)], i32),
+            "qmm_gguf_meta_info": ([vp, i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(i32), ctypes.POINTER(i32),
+                                    ctypes.POINTER(ctypes.c_uint64)], i32),
+            "qmm_gguf_meta_u64": ([vp, i64, i64, ctypes.POINTER(ctypes.c_uint64)], i32),
+            "qmm_gguf_meta_i64": ([vp, i64, i64, ctypes.POINTER(i64)], i32),
+            "qmm_gguf_meta_f64": ([vp, i64, i64, ctypes.POINTER(ctypes.c_double)], i32),
+            "qmm_gguf_meta_string": ([vp, i64, i64, pp, ctypes.POINTER(ctypes.c_uint64)], i32),
+            "qmm_gguf_load_qtensor": ([vp, i64, i32, vp, pp], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
