@@ -668,6 +668,24 @@ static int gemm(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, f
     }
   }
   const unsigned lds2 = (unsigned)(2 * (bm * 272 + bn * 160 + bm * 4 + bm * 16));
+  // Q4_K: mmq2 (128x128 tiles, 8 waves, VALU sub-block scaling) when its grid
+  // covers every CU; otherwise (e.g. N = 4096 at M = 512: 128 tiles) the
+  // split-scale mmq4 with 128x64 tiles (4 waves, one per SIMD), which gives
+  // twice the workgroups (4096x14336 at M = 512: 144 vs 194 us).
+  // QMM_MMQ=2 / QMM_MMQ=4 force one; QMM_MMQ4_BN=128 picks 128x128 mmq4 tiles.
+  const char* gen = getenv("QMM_MMQ");
+  const long long tiles2 = (long long)((N + bn - 1) / bn) * ((M + bm - 1) / bm);
+  const bool use4 = gen ? atoi(gen) == 4 : tiles2 < d->num_cu;
+  if (fmt == kFmtQ4K && use4) {
+    int b4 = 64;
+    if (const char* e = getenv("QMM_MMQ4_BN")) b4 = atoi(e) == 128 ? 128 : 64;
+    const unsigned lds4 = (unsigned)(2 * (128 * 272 + b4 * 160 + 128 * 4 + 128 * 16));
+    snprintf(name, sizeof(name), "qmm_mmq4_q4k_n%d%s", b4, dump ? "_dump" : "");
+    QMM_TRY(kernel(d, name, &f));
+    QMM_HIP(hipModuleLaunchKernel(f, (unsigned)((N + b4 - 1) / b4), (unsigned)((M + 127) / 128), 1, 256, 1, 1, lds4,
+                                  s, args, nullptr));
+    return QMM_OK;
+  }
   if (fmt == kFmtQ4K && (int)lds2 <= d->max_lds && getenv("QMM_MMQ1") == nullptr) {
     snprintf(name, sizeof(name), "qmm_mmq2_q4k_m%d_n%d%s", bm, bn, dump ? "_dump" : "");
     QMM_TRY(kernel(d, name, &f));

@@ -497,10 +497,11 @@ namespace qmm {
 constexpr int kM2AStride = 256 + 16;  // activation row in LDS (16-byte skew)
 constexpr int kM2BStride = 144 + 16;  // weight block in LDS
 
-template <int BM, int BN>
+// NT = threads of the workgroup (mmq2: one wave per 64 x 32 outputs).
+template <int BM, int BN, int NT = 64 * (BM / 64) * (BN / 32)>
 struct M2 {
-  static constexpr int kWM = BM / 64, kWN = BN / 32;  // waves along M and N
-  static constexpr int kThreads = 64 * kWM * kWN;
+  static constexpr int kWM = BM / 64, kWN = BN / 32;  // mmq2's waves along M and N
+  static constexpr int kThreads = NT;
   static constexpr int kA = BM * kM2AStride;
   static constexpr int kB = BN * kM2BStride;
   static constexpr int kDx = BM * 4;
@@ -513,19 +514,19 @@ struct M2 {
 };
 
 // Global loads of one K step into registers.
-template <int BM, int BN>
+template <int BM, int BN, int NT = M2<BM, BN>::kThreads>
 struct M2Regs {
-  uint4 a[M2<BM, BN>::kAPer];
-  uint4 b[M2<BM, BN>::kBPer];
+  uint4 a[M2<BM, BN, NT>::kAPer];
+  uint4 b[M2<BM, BN, NT>::kBPer];
   float dx;  // t < BM: activation scale of row t
   uint4 s;   // t < BM: eight int16 32-element sums of row t
 };
 
-template <int BM, int BN>
-__device__ __forceinline__ void m2_load(M2Regs<BM, BN>& R, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+template <int BM, int BN, int NT = M2<BM, BN>::kThreads>
+__device__ __forceinline__ void m2_load(M2Regs<BM, BN, NT>& R, const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                         const int16_t* __restrict__ xs, const uint8_t* __restrict__ wq, int M, int N,
                                         int K, int m0, int n0, int kb) {
-  using C = M2<BM, BN>;
+  using C = M2<BM, BN, NT>;
   const int t = threadIdx.x, nbk = K / 256;
 #pragma unroll
   for (int u = 0; u < C::kAPer; ++u) {
@@ -548,9 +549,9 @@ __device__ __forceinline__ void m2_load(M2Regs<BM, BN>& R, const int8_t* __restr
   }
 }
 
-template <int BM, int BN>
-__device__ __forceinline__ void m2_store(const M2Regs<BM, BN>& R, uint8_t* buf) {
-  using C = M2<BM, BN>;
+template <int BM, int BN, int NT = M2<BM, BN>::kThreads>
+__device__ __forceinline__ void m2_store(const M2Regs<BM, BN, NT>& R, uint8_t* buf) {
+  using C = M2<BM, BN, NT>;
   const int t = threadIdx.x;
 #pragma unroll
   for (int u = 0; u < C::kAPer; ++u) {
@@ -686,7 +687,196 @@ __device__ __forceinline__ void mmq2_q4k(const uint8_t* __restrict__ wq, const i
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K prefill GEMM, split-scale form (mmq4): the sub-block scales move into
+// the MFMA operands, so a super-block's contraction accumulates inside the
+// matrix cores instead of one VALU scale-and-add per sub-block and output.
+//   * each 6-bit scale is split as sc = 8 * sh + sl (sh, sl in [0, 7]); the
+//     weight operand of sub-block j is taken twice, as sl_j * q4 and
+//     sh_j * q4 (both <= 105: still int8), and
+//       isd = sum_j sc_j (q8 . q4)_j = MFMA_acc(x, sl q4) + 8 MFMA_acc(x, sh q4)
+//     exactly in int32 (|isd| <= 63 * 15 * 127 * 256 < 2^31); the per-byte
+//     products are one packed 16-bit multiply per dword (q * s < 256, so no
+//     carry crosses a byte);
+//   * workgroup tile 128 x BN with four waves, one per SIMD, each owning
+//     64 x BN/2 outputs (two M tiles x BN/64 N tiles of 32 x 32): a wave has
+//     the whole register file, so the 2 x 2 x BN/64 accumulators, the f32
+//     outputs and the next step's global loads fit without spilling, and
+//     its MFMAs overlap its own VALU work;
+//   * staging (double-buffered LDS, next step's loads in registers during
+//     this step's MFMAs), the mins term (two zero-padded MFMAs) and the f32
+//     update y += dx * (d * isd - dmin * ism) are mmq2's, so the integer
+//     block dots are the same (DUMP writes them).
+// ---------------------------------------------------------------------------
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Bytes of v times s (each product < 256): one packed 16-bit multiply.
+__device__ __forceinline__ uint32_t bytes_times(uint32_t v, uint32_t s) {
+  const u16x2 a = __builtin_bit_cast(u16x2, v);
+  const u16x2 b = {(unsigned short)s, (unsigned short)s};
+  return __builtin_bit_cast(uint32_t, a * b);
+}
+__device__ __forceinline__ i8x16 bytes_times4(uint4 v, uint32_t s) {
+  return as_i8x16(make_uint4(bytes_times(v.x, s), bytes_times(v.y, s), bytes_times(v.z, s), bytes_times(v.w, s)));
+}
+
+template <int BN, bool DUMP>
+__device__ __forceinline__ void mmq4_q4k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,
+                                         const float* __restrict__ xd, const int16_t* __restrict__ xs,
+                                         float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,
+                                         int accumulate) {
+  constexpr int BM = 128, NT = 256;
+  constexpr int TN = BN / 64;  // N tiles per wave
+  using C = M2<BM, BN, NT>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int nbk = K / 256;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int arow0 = 64 * wm + r;  // + 32 i: A operand row of M tile i
+
+  i32x16 zero;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) zero[j] = 0;
+  float acc[2][TN][16];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[i][t][j] = 0.0f;
+
+  M2Regs<BM, BN, NT> R;
+  m2_load<BM, BN, NT>(R, xq, xd, xs, wq, M, N, K, m0, n0, 0);
+  m2_store<BM, BN, NT>(R, lds);
+  __syncthreads();
+  for (int kb = 0; kb < nbk; ++kb) {
+    uint8_t* buf = lds + (kb & 1) * C::kStage;
+    if (kb + 1 < nbk) m2_load<BM, BN, NT>(R, xq, xd, xs, wq, M, N, K, m0, n0, kb + 1);
+    const int8_t* A = reinterpret_cast<const int8_t*>(buf);
+    const float* DX = reinterpret_cast<const float*>(buf + C::kA + C::kB);
+    const uint8_t* SUM = buf + C::kA + C::kB + C::kDx;
+
+    // per N tile: this lane's column block, its scales (split) and mins
+    const uint8_t* Bc[TN];
+    float dw[TN], dm[TN];
+    uint32_t sl[TN][2], sh[TN][2], mn[TN][2];
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      Bc[t] = buf + C::kA + (BN / 2 * wn + 32 * t + r) * kM2BStride;
+      const uint4 hd = *reinterpret_cast<const uint4*>(Bc[t]);
+      dw[t] = h2f(hd.x);
+      dm[t] = h2f(hd.x >> 16);
+      const uint32_t sclo = hd.y & 0x3f3f3f3fu, schi = (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u);
+      sl[t][0] = sclo & 0x07070707u;
+      sl[t][1] = schi & 0x07070707u;
+      sh[t][0] = (sclo >> 3) & 0x07070707u;
+      sh[t][1] = (schi >> 3) & 0x07070707u;
+      mn[t][0] = hd.z & 0x3f3f3f3fu;
+      mn[t][1] = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
+    }
+    i32x16 accl[2][TN], acch[2][TN];
+#pragma unroll
+    for (int c2 = 0; c2 < 4; ++c2) {
+      const int sel = c2 >> 1, sb = 16 * (c2 & 1);
+      i8x16 b0l[TN], b0h[TN], b1l[TN], b1h[TN];
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const uint4 qv = *reinterpret_cast<const uint4*>(Bc[t] + 16 + 32 * c2 + 16 * h);
+        const uint4 blo = make_uint4(qv.x & 0x0f0f0f0fu, qv.y & 0x0f0f0f0fu, qv.z & 0x0f0f0f0fu, qv.w & 0x0f0f0f0fu);
+        const uint4 bhi = make_uint4((qv.x >> 4) & 0x0f0f0f0fu, (qv.y >> 4) & 0x0f0f0f0fu,
+                                     (qv.z >> 4) & 0x0f0f0f0fu, (qv.w >> 4) & 0x0f0f0f0fu);
+        b0l[t] = bytes_times4(blo, (sl[t][sel] >> sb) & 0xffu);
+        b0h[t] = bytes_times4(blo, (sh[t][sel] >> sb) & 0xffu);
+        b1l[t] = bytes_times4(bhi, (sl[t][sel] >> (sb + 8)) & 0xffu);
+        b1h[t] = bytes_times4(bhi, (sh[t][sel] >> (sb + 8)) & 0xffu);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int8_t* ar = A + (arow0 + 32 * i) * kM2AStride + 64 * c2 + 16 * h;
+        const i8x16 a0 = *reinterpret_cast<const i8x16*>(ar);
+        const i8x16 a1 = *reinterpret_cast<const i8x16*>(ar + 32);
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+          accl[i][t] = mfma_i8(a0, b0l[t], c2 == 0 ? zero : accl[i][t]);  // first: inline-zero accumulator
+          acch[i][t] = mfma_i8(a0, b0h[t], c2 == 0 ? zero : acch[i][t]);
+          accl[i][t] = mfma_i8(a1, b1l[t], accl[i][t]);
+          acch[i][t] = mfma_i8(a1, b1h[t], acch[i][t]);
+        }
+      }
+    }
+    // mins term and the float update
+    const uint4 zero4 = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint4 sv = *reinterpret_cast<const uint4*>(SUM + 16 * (arow0 + 32 * i));
+      const i8x16 alo = as_i8x16(h == 0 ? make_uint4(sv.x, sv.y, 0, 0) : zero4);
+      const i8x16 ahi = as_i8x16(h == 0 ? make_uint4(sv.z, sv.w, 0, 0) : zero4);
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const i8x16 bm = as_i8x16(h == 0 ? make_uint4(mn[t][0], mn[t][1], 0, 0) : zero4);
+        const i32x16 Lo = mfma_i8(alo, bm, zero), Hi = mfma_i8(ahi, bm, zero);
+        const int col = n0 + BN / 2 * wn + 32 * t + r;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 dx = *reinterpret_cast<const float4*>(DX + 64 * wm + 32 * i + 8 * g + 4 * h);
+          const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int e = 4 * g + q;
+            const int isd = accl[i][t][e] + 8 * acch[i][t][e];
+            const int ism = Hi[e] * 64 + Lo[e];
+            acc[i][t][e] += dxs[q] * (dw[t] * (float)isd - dm[t] * (float)ism);
+            if (DUMP) {
+              const int row = m0 + 64 * wm + 32 * i + 8 * g + 4 * h + q;
+              if (row < M && col < N) {
+                const size_t o = ((size_t)row * N + col) * nbk + kb;
+                dump[2 * o] = isd;
+                dump[2 * o + 1] = ism;
+              }
+            }
+          }
+        }
+      }
+    }
+    if (kb + 1 < nbk) m2_store<BM, BN, NT>(R, lds + ((kb + 1) & 1) * C::kStage);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const int col = n0 + BN / 2 * wn + 32 * t + r;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = m0 + 64 * wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (row < M && col < N) {
+          float* yp = y + (size_t)row * ldy + col;
+          *yp = accumulate ? *yp + acc[i][t][e] : acc[i][t][e];
+        }
+      }
+    }
+}
+
 }  // namespace qmm
+
+#define QMM_MMQ4_KERNEL(BN)                                                                                    \
+  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))                 \
+      qmm_mmq4_q4k_n##BN(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                        \
+                         const float* __restrict__ xd, const int16_t* __restrict__ xs, float* __restrict__ y,   \
+                         int M, int N, int K, int ldy, int* __restrict__ dump, int accumulate) {                \
+    qmm::mmq4_q4k<BN, false>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate);                               \
+  }                                                                                                            \
+  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))                 \
+      qmm_mmq4_q4k_n##BN##_dump(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                 \
+                                const float* __restrict__ xd, const int16_t* __restrict__ xs,                  \
+                                float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,    \
+                                int accumulate) {                                                              \
+    qmm::mmq4_q4k<BN, true>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate);                                \
+  }
+QMM_MMQ4_KERNEL(128)
+QMM_MMQ4_KERNEL(64)
 
 #define QMM_MMQ2_KERNEL(BM, BN)                                                                                \
   extern "C" __global__ void __launch_bounds__(BM * BN / 32) __attribute__((amdgpu_waves_per_eu(2 * 64 / BM)))     \

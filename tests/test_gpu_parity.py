@@ -368,6 +368,27 @@ def test_gemm_block_dots_bit_exact(dt, n, k, m):
     assert rel_err(y2, orc.matmul(ORC[dt], x, wq, k)) <= TOL
 
 
+@pytest.mark.parametrize("gen", [{"QMM_MMQ": "2"}, {"QMM_MMQ": "4"}, {"QMM_MMQ": "4", "QMM_MMQ4_BN": "128"}])
+@pytest.mark.parametrize("n,k,m", [(300, 1024, 9), (130, 512, 257), (64, 256, 130)])
+def test_gemm_q4k_generations_bit_exact(monkeypatch, gen, n, k, m):
+    """Both Q4_K GEMM generations (mmq2: per-sub-block VALU scaling; mmq4: split-scale MFMA operands, 128x64
+    and 128x128 tiles) give the oracle's integer block dots and f32 outputs within TOL."""
+    for key, val in gen.items():
+        monkeypatch.setenv(key, val)
+    w = np.concatenate([normal(180 + n, (n, k), 0.02), special_weight_rows(k)[:4]])
+    wq = orc.quantize(orc.Q4K, w)
+    qt = QTensor.from_ggml(wq, GgmlDType.Q4K, w.shape, device=DEV)
+    x = normal(181 + m, (m, k))
+    x[1, : k // 2] *= 40.0
+    x[2] = 0.0
+    xq = quantize_rows(GgmlDType.Q8K, torch.from_numpy(x).to(DEV))
+    dots, y = block_dots(qt, xq, m)
+    assert np.array_equal(dots.cpu().numpy(), orc.block_dots(orc.Q4K, wq, xq.cpu().numpy(), k))
+    assert rel_err(y.cpu().numpy(), orc.matmul_prequant(orc.Q4K, xq.cpu().numpy(), wq, k)) <= TOL
+    y2 = QMatMul.from_qtensor(qt).forward(torch.from_numpy(x).to(DEV)).cpu().numpy()
+    assert rel_err(y2, orc.matmul(orc.Q4K, x, wq, k)) <= TOL
+
+
 @pytest.mark.parametrize("dt,n,k,wseed", [(GgmlDType.Q4K, 14336, 4096, 6), (GgmlDType.Q4K, 4096, 14336, 6),
                                           (GgmlDType.Q6K, 4096, 14336, 6)])
 def test_prefill_config_shapes_match_cpu_path(dt, n, k, wseed):
