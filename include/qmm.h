@@ -49,6 +49,8 @@ enum {
 /* GGML dtype tags (GGUF numbering, crates/llm/mlx-llm/src/gguf/dequant.rs:87-113). */
 enum {
     QMM_F32 = 0,
+    QMM_F16 = 1,   /* dense outputs of qmm_qtensor_dequantize_to */
+    QMM_BF16 = 30,
     QMM_Q8_0 = 8,  /* 34 B / 32:   f16 d, i8 qs[32]                          */
     QMM_Q4K = 12,  /* 144 B / 256: f16 d, f16 dmin, u8 scales[12], u8 qs[128] */
     QMM_Q6K = 14,  /* 210 B / 256: u8 ql[128], u8 qh[64], i8 scales[16], f16 d */
@@ -86,6 +88,14 @@ int qmm_qtensor_quantize(int dtype, int64_t n, int64_t k, const float *w, void *
 
 /* QTensor::dequantize: n*k f32 into the device buffer `dst`. */
 int qmm_qtensor_dequantize(const qmm_qtensor *t, float *dst, void *stream);
+
+/* qmm_qtensor_dequantize to a dense [n, k] of out_dtype QMM_F32, QMM_F16 or
+ * QMM_BF16 (each value rounded to nearest even from its f32 dequantization):
+ * candle's QTensor::dequantize_f16 and the dequant-dense matmul strategy's
+ * weight.dequantize(device).to_dtype(x.dtype) (candle-gen/src/quant/mod.rs:
+ * 515-533; QMatMul::forward_via_f16 at candle-gen-lens/src/text_encoder.rs:
+ * 518-529). */
+int qmm_qtensor_dequantize_to(const qmm_qtensor *t, void *dst, int out_dtype, void *stream);
 
 /* Export the tensor as GGML block bytes (qmm_qtensor_ggml_bytes() of them) into
  * `dst` on the host (dst_on_device = 0, synchronous) or the device (= 1). */

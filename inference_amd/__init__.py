@@ -6,6 +6,8 @@ reference engine's QTensor / QMatMul / QuantizedLinear surface over it.
 """
 from .qmm import (  # noqa: F401
     GgmlDType,
+    MatmulStrategy,
+    QLinear,
     Projection,
     QMatMul,
     QmmError,

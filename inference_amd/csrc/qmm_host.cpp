@@ -339,18 +339,27 @@ int qmm_qtensor_quantize(int dtype, int64_t n, int64_t k, const float* w, void* 
   return QMM_OK;
 }
 
-int qmm_qtensor_dequantize(const qmm_qtensor* t, float* dst, void* stream) {
+int qmm_qtensor_dequantize_to(const qmm_qtensor* t, void* dst, int out_dtype, void* stream) {
   if (!t || !dst) return fail(QMM_ERR_INVALID, "null pointer");
+  const char* name = out_dtype == QMM_F32    ? "qmm_dequantize"
+                     : out_dtype == QMM_F16  ? "qmm_dequantize_f16"
+                     : out_dtype == QMM_BF16 ? "qmm_dequantize_bf16"
+                                             : nullptr;
+  if (!name) return fail(QMM_ERR_INVALID, "dequantize: output dtype %d (F32 = 0, F16 = 1, BF16 = 30)", out_dtype);
   Device* d;
   QMM_TRY(current_device(&d));
   const int fmt = fmt_of(t->dtype);
   long long nblocks = t->n * (t->k / qmm_block_size(t->dtype));
   const void* a0 = t->data;
-  float* a1 = dst;
+  void* a1 = dst;
   int f = fmt;
   void* args[] = {&a0, &a1, &nblocks, &f};
   const long long threads = fmt == kFmtQ80 ? nblocks : nblocks * 8;
-  return launch(d, "qmm_dequantize", ceil_div(threads, 256), 256, 0, (hipStream_t)stream, args);
+  return launch(d, name, ceil_div(threads, 256), 256, 0, (hipStream_t)stream, args);
+}
+
+int qmm_qtensor_dequantize(const qmm_qtensor* t, float* dst, void* stream) {
+  return qmm_qtensor_dequantize_to(t, dst, QMM_F32, stream);
 }
 
 int qmm_qtensor_to_ggml(const qmm_qtensor* t, void* dst, int dst_on_device, void* stream) {

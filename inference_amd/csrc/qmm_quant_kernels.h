@@ -440,36 +440,47 @@ extern "C" __global__ void qmm_dev_to_ggml(const uint8_t* __restrict__ src, uint
   }
 }
 
-// Dequantize a device-layout tensor to f32 (QTensor::dequantize). One thread
-// per 32 consecutive outputs; formulas of crates/llm/mlx-llm/src/gguf/dequant.rs
-// :284-290 (Q8_0), :391-416 (Q4_K), :452-474 (Q6_K), one rounding per operation.
-extern "C" __global__ void qmm_dequantize(const uint8_t* __restrict__ src, float* __restrict__ y,
-                                          long long nblocks, int fmt) {
+// Dequantize a device-layout tensor (QTensor::dequantize). One thread per 32
+// consecutive outputs; formulas of crates/llm/mlx-llm/src/gguf/dequant.rs
+// :284-290 (Q8_0), :391-416 (Q4_K), :452-474 (Q6_K), one rounding per f32
+// operation; the f16 / bf16 outputs round the f32 value once more, to
+// nearest even (the f32 dequantize followed by to_dtype).
+namespace qmm {
+__device__ __forceinline__ void put_val(float* y, long long i, float v) { y[i] = v; }
+__device__ __forceinline__ void put_val(_Float16* y, long long i, float v) { y[i] = (_Float16)v; }
+__device__ __forceinline__ void put_val(uint16_t* y, long long i, float v) {  // bf16, round to nearest even
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  y[i] = (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
+template <class T>
+__device__ __forceinline__ void dequantize_blocks(const uint8_t* __restrict__ src, T* __restrict__ y,
+                                                  long long nblocks, int fmt) {
 #pragma clang fp contract(off)
   const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (fmt == qmm::kFmtQ80) {
+  if (fmt == kFmtQ80) {
     if (t >= nblocks) return;
-    const int8_t* q = reinterpret_cast<const int8_t*>(src + qmm::kQ80Body * t);
-    const float d = qmm::h2f(reinterpret_cast<const uint16_t*>(src + qmm::kQ80Body * nblocks)[t]);
-    for (int j = 0; j < 32; ++j) y[32 * t + j] = (float)q[j] * d;
+    const int8_t* q = reinterpret_cast<const int8_t*>(src + kQ80Body * t);
+    const float d = h2f(reinterpret_cast<const uint16_t*>(src + kQ80Body * nblocks)[t]);
+    for (int j = 0; j < 32; ++j) put_val(y, 32 * t + j, (float)q[j] * d);
     return;
   }
   const long long b = t >> 3;
   const int part = (int)(t & 7);
   if (b >= nblocks) return;
-  float* out = y + 256 * b + 32 * part;
-  if (fmt == qmm::kFmtQ4K) {
-    const uint8_t* blk = src + qmm::kQ4KBytes * b;
-    const float d = qmm::h2f(blk[0] | (blk[1] << 8)), dmin = qmm::h2f(blk[2] | (blk[3] << 8));
+  const long long o = 256 * b + 32 * part;
+  if (fmt == kFmtQ4K) {
+    const uint8_t* blk = src + kQ4KBytes * b;
+    const float d = h2f(blk[0] | (blk[1] << 8)), dmin = h2f(blk[2] | (blk[3] << 8));
     int sc, m;
-    qmm::q4k_scale_min(part, blk + 4, &sc, &m);
+    q4k_scale_min(part, blk + 4, &sc, &m);
     const float d1 = d * (float)sc, m1 = dmin * (float)m;
     const uint8_t* qs = blk + 16 + 32 * (part >> 1);
     const int sh = (part & 1) * 4;
-    for (int l = 0; l < 32; ++l) out[l] = d1 * (float)((qs[l] >> sh) & 0xf) - m1;
+    for (int l = 0; l < 32; ++l) put_val(y, o + l, d1 * (float)((qs[l] >> sh) & 0xf) - m1);
   } else {
-    const uint8_t* body = src + qmm::kQ6KBody * b;
-    const float d = qmm::h2f(reinterpret_cast<const uint16_t*>(src + qmm::kQ6KBody * nblocks)[b]);
+    const uint8_t* body = src + kQ6KBody * b;
+    const float d = h2f(reinterpret_cast<const uint16_t*>(src + kQ6KBody * nblocks)[b]);
     const int8_t* sc = reinterpret_cast<const int8_t*>(body + 192);
     // outputs 128h + 32s + [0, 32): ql low/high nibble and 2 bits of qh.
     const int h = part >> 2, s = part & 3;
@@ -478,7 +489,21 @@ extern "C" __global__ void qmm_dequantize(const uint8_t* __restrict__ src, float
     const int nsh = (s >> 1) * 4, hsh = 2 * s;
     for (int l = 0; l < 32; ++l) {
       const int q = (((ql[l] >> nsh) & 0xf) | (((qh[l] >> hsh) & 3) << 4)) - 32;
-      out[l] = d * (float)sc[8 * h + 2 * s + l / 16] * (float)q;
+      put_val(y, o + l, d * (float)sc[8 * h + 2 * s + l / 16] * (float)q);
     }
   }
+}
+}  // namespace qmm
+
+extern "C" __global__ void qmm_dequantize(const uint8_t* __restrict__ src, float* __restrict__ y, long long nblocks,
+                                          int fmt) {
+  qmm::dequantize_blocks(src, y, nblocks, fmt);
+}
+extern "C" __global__ void qmm_dequantize_f16(const uint8_t* __restrict__ src, _Float16* __restrict__ y,
+                                              long long nblocks, int fmt) {
+  qmm::dequantize_blocks(src, y, nblocks, fmt);
+}
+extern "C" __global__ void qmm_dequantize_bf16(const uint8_t* __restrict__ src, uint16_t* __restrict__ y,
+                                               long long nblocks, int fmt) {
+  qmm::dequantize_blocks(src, y, nblocks, fmt);
 }

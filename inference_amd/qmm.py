@@ -56,7 +56,7 @@ EXPORTS = (
     "qmm_gguf_tensor_count", "qmm_gguf_metadata_count", "qmm_gguf_find_tensor", "qmm_gguf_meta_find",
     "qmm_gguf_tensor_info", "qmm_gguf_type_size", "qmm_gguf_tensor_data", "qmm_gguf_meta_info",
     "qmm_gguf_meta_u64", "qmm_gguf_meta_i64", "qmm_gguf_meta_f64", "qmm_gguf_meta_string",
-    "qmm_gguf_load_qtensor",
+    "qmm_gguf_load_qtensor", "qmm_qtensor_dequantize_to",
 )
 
 
@@ -135,6 +135,7 @@ def lib() -> ctypes.CDLL:
             "qmm_gguf_meta_f64": ([vp, i64, i64, ctypes.POINTER(ctypes.c_double)], i32),
             "qmm_gguf_meta_string": ([vp, i64, i64, pp, ctypes.POINTER(ctypes.c_uint64)], i32),
             "qmm_gguf_load_qtensor": ([vp, i64, i32, vp, pp], i32),
+            "qmm_qtensor_dequantize_to": ([vp, vp, i32, vp], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -280,12 +281,19 @@ class QTensor:
     def storage_size_in_bytes(self) -> int:
         return int(lib().qmm_qtensor_ggml_bytes(self._h))
 
-    def dequantize(self) -> torch.Tensor:
-        """QTensor::dequantize -> f32 [n, k] on the tensor's GPU."""
-        out = torch.empty(self.shape, dtype=torch.float32, device=self.device)
+    def dequantize(self, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        """QTensor::dequantize -> [n, k] on the tensor's GPU: f32, or f16 / bf16 rounded once from it
+        (QTensor::dequantize_f16; the dequant-dense strategy's to_dtype)."""
+        tag = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 30}.get(dtype)
+        if tag is None:
+            raise QmmError(1, f"dequantize to {dtype}: float32, float16 or bfloat16")
+        out = torch.empty(self.shape, dtype=dtype, device=self.device)
         with torch.cuda.device(self.device):
-            _check(lib().qmm_qtensor_dequantize(self._h, out.data_ptr(), _stream(self.device)))
+            _check(lib().qmm_qtensor_dequantize_to(self._h, out.data_ptr(), tag, _stream(self.device)))
         return out
+
+    def dequantize_f16(self) -> torch.Tensor:
+        return self.dequantize(torch.float16)
 
     def to_ggml(self) -> np.ndarray:
         """GGML block bytes of the tensor (host, uint8)."""
@@ -338,6 +346,46 @@ class QMatMul:
             _check(L.qmm_matmul(self.qtensor.handle, x2.data_ptr(), m, x2.stride(0), y.data_ptr(), n,
                                 ws.data_ptr(), ws_bytes, _stream(x.device)))
         return y.reshape(*lead, n)
+
+    def forward_via_f16(self, x: torch.Tensor) -> torch.Tensor:
+        """QMatMul::forward_via_f16: the weight dequantized to a dense f16 tile, x cast to f16, a dense
+        matmul (a plain library GEMM), the result cast back to x's dtype
+        (candle-gen-lens/src/text_encoder.rs:518-529)."""
+        n, k = self.qtensor.shape
+        if x.shape[-1] != k:
+            raise QmmError(1, f"shape mismatch: input last dim {x.shape[-1]} vs weight in-dim {k}")
+        w = self.qtensor.dequantize(torch.float16)
+        return torch.matmul(x.to(torch.float16), w.t()).to(x.dtype)
+
+    __call__ = forward
+
+
+class MatmulStrategy(enum.Enum):
+    """How a quantized QLinear computes x @ W^T (candle-gen/src/quant/mod.rs:202-227)."""
+    DEQUANT_DENSE = "dequant_dense"  # weight dequantized to x's dtype, dense matmul (outlier-safe)
+    INT8_FAST = "int8_fast"          # QMatMul::forward: activation quantized to Q8_K / Q8_0
+
+
+class QLinear:
+    """Quantized linear of the media models (candle-gen/src/quant/mod.rs:515-568): x @ W^T (+ b) over a
+    QTensor with either strategy. DEQUANT_DENSE keeps the activation full precision (the weight is
+    dequantized per call, the QTensor stays resident); INT8_FAST flattens the leading dims, runs the
+    f32 activation through QMatMul::forward and casts back to x's dtype."""
+
+    def __init__(self, weight: QTensor, bias: Optional[torch.Tensor] = None,
+                 strategy: MatmulStrategy = MatmulStrategy.DEQUANT_DENSE):
+        self.weight, self.bias, self.strategy = weight, bias, strategy
+        self._mm = QMatMul(weight)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.strategy == MatmulStrategy.DEQUANT_DENSE:
+            w = self.weight.dequantize(torch.float32).to(x.dtype)
+            b = self.bias.to(x.dtype) if self.bias is not None else None
+            return torch.nn.functional.linear(x, w, b)
+        y = self._mm.forward(x.to(torch.float32).contiguous())
+        if self.bias is not None:
+            y = y + self.bias
+        return y.to(x.dtype)
 
     __call__ = forward
 
