@@ -222,6 +222,31 @@ int qmm_decode_rope_attention(const float *q, const float *k, const float *v, co
                               int heads, int kv_heads, int head_dim, int max_seq, float scale, void *ws,
                               size_t ws_bytes, void *stream);
 
+/* Batched prefill: the same per-layer operations over `count` prompt rows at
+ * positions first .. first + count - 1 (CausalLm::forward over a prompt with
+ * seq_len > 1 and the causal mask, llama.rs:410-433, 654-725; causal sdpa,
+ * attention.rs:154-186). Rows are row-major with the given strides. */
+
+/* x[i] = table[tokens[first + i]] for i < count (CausalLm embed, llama.rs:397-408). */
+int qmm_embed_rows_n(const float *table, int64_t ld, const int32_t *tokens, int64_t first, int64_t count, float *x,
+                     int64_t hidden, void *stream);
+
+/* qmm_rope_kv_append for rows i < count at positions first + i: q and k
+ * rows rotated in place, k and v written to the caches at those positions. */
+int qmm_rope_kv_append_n(float *q, float *k, const float *v, int64_t ldq, int64_t ldk, int64_t ldv,
+                         const float *cos_t, const float *sin_t, int64_t first, int64_t count, float *kcache,
+                         float *vcache, int heads, int kv_heads, int head_dim, int max_seq, void *stream);
+
+/* Causal GQA attention of rows i < count: query row i (already rotated, at
+ * position first + i) against cache positions 0 ..= first + i, out row i =
+ * softmax(q . K^T * scale) . V per head (geometry as qmm_decode_attention). */
+int qmm_prefill_attention(const float *q, int64_t ldq, const float *kcache, const float *vcache, int64_t first,
+                          int64_t count, float *out, int64_t ldo, int heads, int kv_heads, int head_dim, int max_seq,
+                          float scale, void *stream);
+
+/* h = silu(g) * u over n elements, f32 (LlamaMlp::forward, llama.rs:1386-1391). */
+int qmm_silu_mul(const float *g, const float *u, float *h, int64_t n, void *stream);
+
 /* hq = Q8_K(silu(g) * u) for rows x k (k a multiple of 256), the down
  * projection's activation (LlamaMlp::forward, llama.rs:1386-1391). */
 int qmm_silu_mul_quantize(const float *g, const float *u, int64_t rows, int64_t k, int64_t ld, void *hq,

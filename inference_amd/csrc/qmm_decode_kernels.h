@@ -12,6 +12,17 @@
 #include "qmm_common.h"
 #include "qmm_quant_kernels.h"
 
+// x[i][0 : hidden) = table[tokens[first + i]][0 : hidden) for i < gridDim.y
+// (the prompt rows of a batched prefill).
+extern "C" __global__ void qmm_prefill_embed(const float* __restrict__ table, long long ld,
+                                             const int* __restrict__ tokens, int first, float* __restrict__ x,
+                                             int hidden) {
+  const int i = blockIdx.y;
+  const int tok = tokens[first + i];
+  for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < hidden; c += gridDim.x * blockDim.x)
+    x[(long long)i * hidden + c] = table[(long long)tok * ld + c];
+}
+
 // x[0 : hidden) = table[tokens[pos[0]]][0 : hidden)
 extern "C" __global__ void qmm_decode_embed(const float* __restrict__ table, long long ld,
                                             const int* __restrict__ tokens, const int* __restrict__ pos,
@@ -26,13 +37,12 @@ extern "C" __global__ void qmm_decode_embed(const float* __restrict__ table, lon
 // place, and appends k, v to the layer's cache [kv_heads][max_seq][dim].
 // One workgroup per head (q heads first, then kv heads). A position outside
 // [0, max_seq) writes nothing.
-extern "C" __global__ void qmm_decode_rope_kv(float* __restrict__ q, float* __restrict__ k,
-                                              const float* __restrict__ v, const float* __restrict__ cos_t,
-                                              const float* __restrict__ sin_t, const int* __restrict__ pos,
-                                              float* __restrict__ kcache, float* __restrict__ vcache, int heads,
-                                              int kv_heads, int dim, int max_seq) {
+namespace qmm {
+__device__ __forceinline__ void rope_kv_row(float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
+                                            const float* __restrict__ cos_t, const float* __restrict__ sin_t, int p,
+                                            float* __restrict__ kcache, float* __restrict__ vcache, int heads,
+                                            int dim, int max_seq) {
 #pragma clang fp contract(off)
-  const int p = pos[0];
   if (p < 0 || p >= max_seq) return;
   const int h = blockIdx.x;
   const int half = dim / 2;
@@ -56,6 +66,29 @@ extern "C" __global__ void qmm_decode_rope_kv(float* __restrict__ q, float* __re
       vcache[((size_t)g * max_seq + p) * dim + i] = v[(size_t)g * dim + i];
     }
   }
+}
+}  // namespace qmm
+
+extern "C" __global__ void qmm_decode_rope_kv(float* __restrict__ q, float* __restrict__ k,
+                                              const float* __restrict__ v, const float* __restrict__ cos_t,
+                                              const float* __restrict__ sin_t, const int* __restrict__ pos,
+                                              float* __restrict__ kcache, float* __restrict__ vcache, int heads,
+                                              int kv_heads, int dim, int max_seq) {
+  (void)kv_heads;
+  qmm::rope_kv_row(q, k, v, cos_t, sin_t, pos[0], kcache, vcache, heads, dim, max_seq);
+}
+
+// Prompt rows i < gridDim.y at positions first + i: row i of q / k / v starts
+// at q + i * ldq (k, v likewise).
+extern "C" __global__ void qmm_prefill_rope_kv(float* __restrict__ q, float* __restrict__ k,
+                                               const float* __restrict__ v, long long ldq, long long ldk,
+                                               long long ldv, const float* __restrict__ cos_t,
+                                               const float* __restrict__ sin_t, int first,
+                                               float* __restrict__ kcache, float* __restrict__ vcache, int heads,
+                                               int dim, int max_seq) {
+  const int i = blockIdx.y;
+  qmm::rope_kv_row(q + i * ldq, k + i * ldk, v + i * ldv, cos_t, sin_t, first + i, kcache, vcache, heads, dim,
+                   max_seq);
 }
 
 // One query token against positions 0..p of the cache (p = pos[0]) in one
@@ -120,14 +153,21 @@ __device__ __forceinline__ void attn_rope(float (&x)[DPL], const float (&cs)[DPL
   }
 }
 
-template <int DPL, int GT, int NW>
+// PREFILL: one query per workgroup row, all its positions in one chunk: query
+// row i = blockIdx.y (position first + i, q row at q + i * ldq) attends to
+// positions 0 ..= first + i of the cache (which already holds them, rotated;
+// q is already rotated) and writes its normalised output to out + i * ldo.
+// The arithmetic is the S = 1 case of the chunked form (the merge of one
+// record multiplies by e^0 = 1).
+template <int DPL, int GT, int NW, bool PREFILL = false>
 __device__ __forceinline__ void decode_attention(const float* __restrict__ q, const float* __restrict__ k_new,
                                                  const float* __restrict__ v_new, const float* __restrict__ cos_t,
                                                  const float* __restrict__ sin_t, const int* __restrict__ pos,
                                                  float* __restrict__ kcache, float* __restrict__ vcache,
                                                  float* __restrict__ part, unsigned* __restrict__ counters,
                                                  float* __restrict__ out, int heads, int kv_heads, int max_seq,
-                                                 float scale) {
+                                                 float scale, int first = 0, long long ldq = 0,
+                                                 long long ldo = 0) {
 #pragma clang fp contract(off)
   constexpr int dim = 64 * DPL;
   constexpr int B = 16 / DPL;  // positions per wave batch
@@ -135,14 +175,18 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
   __shared__ float wst[NW][2 * GT];
   __shared__ __attribute__((aligned(16))) float wo[NW][GT * dim];
   __shared__ int last;
-  const int g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
+  const int g = blockIdx.x, c = PREFILL ? 0 : blockIdx.y, t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const int G = heads / kv_heads;
-  constexpr int S = kAttnSplits;
-  const bool rope = cos_t != nullptr;
+  constexpr int S = PREFILL ? 1 : kAttnSplits;
+  const bool rope = !PREFILL && cos_t != nullptr;
+  if constexpr (PREFILL) {
+    q += blockIdx.y * ldq;
+    out += blockIdx.y * ldo;
+  }
 
   // loads, batch 1: pos, q of the group's heads, new k / v rows
-  const int p = min(max(pos[0], 0), max_seq - 1);
+  const int p = PREFILL ? min(first + (int)blockIdx.y, max_seq - 1) : min(max(pos[0], 0), max_seq - 1);
   float qv[GT][DPL];
 #pragma unroll
   for (int h = 0; h < GT; ++h) attn_row<DPL>(qv[h], q + (size_t)(g * G + min(h, G - 1)) * dim, lane);
@@ -290,6 +334,10 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
         osum += wo[w][i] * a;
       }
     }
+    if constexpr (PREFILL) {
+      out[(size_t)(g * G + h) * dim + d] = osum / lsum;
+      continue;
+    }
     float* r = part + ((size_t)c * heads + g * G + h) * rec;
     __hip_atomic_store(r + 2 + d, osum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (d == 0) {
@@ -297,6 +345,7 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
       __hip_atomic_store(r + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  if constexpr (PREFILL) return;
   __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this thread's record stores are acknowledged
   __syncthreads();
   if (t == 0)
@@ -348,6 +397,22 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
 QMM_ATTN_KERNELS(1)
 QMM_ATTN_KERNELS(2)
 QMM_ATTN_KERNELS(4)
+
+// Causal attention of a prompt's rows (batched prefill): grid kv_heads x rows.
+#define QMM_PREFILL_ATTN_KERNEL(DPL, GT)                                                                         \
+  extern "C" __global__ void __launch_bounds__(256) qmm_prefill_attention_d##DPL##_g##GT(                        \
+      const float* __restrict__ q, long long ldq, const float* __restrict__ kcache,                              \
+      const float* __restrict__ vcache, int first, float* __restrict__ out, long long ldo, int heads,            \
+      int kv_heads, int max_seq, float scale) {                                                                  \
+    qmm::decode_attention<DPL, GT, 4, true>(q, nullptr, nullptr, nullptr, nullptr, nullptr,                      \
+                                            const_cast<float*>(kcache), const_cast<float*>(vcache), nullptr,     \
+                                            nullptr, out, heads, kv_heads, max_seq, scale, first, ldq, ldo);     \
+  }
+#define QMM_PREFILL_ATTN_KERNELS(DPL) \
+  QMM_PREFILL_ATTN_KERNEL(DPL, 1) QMM_PREFILL_ATTN_KERNEL(DPL, 2) QMM_PREFILL_ATTN_KERNEL(DPL, 4) QMM_PREFILL_ATTN_KERNEL(DPL, 8)
+QMM_PREFILL_ATTN_KERNELS(1)
+QMM_PREFILL_ATTN_KERNELS(2)
+QMM_PREFILL_ATTN_KERNELS(4)
 
 // hq = Q8_K(silu(g) * u) for `rows` rows of k elements (one wave per block).
 extern "C" __global__ void __launch_bounds__(256) qmm_silu_mul_q8k(const float* __restrict__ g,

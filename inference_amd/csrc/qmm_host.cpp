@@ -1041,6 +1041,89 @@ int qmm_decode_rope_attention(const float* q, const float* k, const float* v, co
                    ws_bytes, stream);
 }
 
+// ---------------------------------------------------------------------------
+// batched prefill (the prompt's rows through one pass per layer)
+// ---------------------------------------------------------------------------
+
+int qmm_embed_rows_n(const float* table, int64_t ld, const int32_t* tokens, int64_t first, int64_t count, float* x,
+                     int64_t hidden, void* stream) {
+  if (!table || !tokens || !x || hidden < 1 || ld < hidden || first < 0 || count < 0 || count > 65535)
+    return fail(QMM_ERR_INVALID, "bad embed arguments");
+  if (count == 0) return QMM_OK;
+  Device* d;
+  QMM_TRY(current_device(&d));
+  long long l = ld;
+  int h = (int)hidden, f = (int)first;
+  void* args[] = {&table, &l, &tokens, &f, &x, &h};
+  hipFunction_t fn;
+  QMM_TRY(kernel(d, "qmm_prefill_embed", &fn));
+  QMM_HIP(hipModuleLaunchKernel(fn, std::min(ceil_div(hidden, 256), 64u), (unsigned)count, 1, 256, 1, 1, 0,
+                                (hipStream_t)stream, args, nullptr));
+  return QMM_OK;
+}
+
+int qmm_rope_kv_append_n(float* q, float* k, const float* v, int64_t ldq, int64_t ldk, int64_t ldv,
+                         const float* cos_t, const float* sin_t, int64_t first, int64_t count, float* kcache,
+                         float* vcache, int heads, int kv_heads, int head_dim, int max_seq, void* stream) {
+  if (!q || !k || !v || !cos_t || !sin_t || !kcache || !vcache) return fail(QMM_ERR_INVALID, "null pointer");
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads || head_dim < 2 || head_dim > 1024 || head_dim % 2 || max_seq < 1)
+    return fail(QMM_ERR_INVALID, "bad attention geometry");
+  if (first < 0 || count < 0 || first + count > max_seq || count > 65535)
+    return fail(QMM_ERR_INVALID, "positions [%lld, %lld) outside the cache of %d", (long long)first,
+                (long long)(first + count), max_seq);
+  if (ldq < (int64_t)heads * head_dim || ldk < (int64_t)kv_heads * head_dim || ldv < (int64_t)kv_heads * head_dim)
+    return fail(QMM_ERR_INVALID, "row strides below the row widths");
+  if (count == 0) return QMM_OK;
+  Device* d;
+  QMM_TRY(current_device(&d));
+  long long a = ldq, b = ldk, c = ldv;
+  int f = (int)first;
+  void* args[] = {&q, &k, &v, &a, &b, &c, &cos_t, &sin_t, &f, &kcache, &vcache, &heads, &head_dim, &max_seq};
+  hipFunction_t fn;
+  QMM_TRY(kernel(d, "qmm_prefill_rope_kv", &fn));
+  const unsigned threads = (unsigned)((head_dim + 63) / 64 * 64);
+  QMM_HIP(hipModuleLaunchKernel(fn, (unsigned)(heads + kv_heads), (unsigned)count, 1, threads, 1, 1, 0,
+                                (hipStream_t)stream, args, nullptr));
+  return QMM_OK;
+}
+
+int qmm_prefill_attention(const float* q, int64_t ldq, const float* kcache, const float* vcache, int64_t first,
+                          int64_t count, float* out, int64_t ldo, int heads, int kv_heads, int head_dim, int max_seq,
+                          float scale, void* stream) {
+  if (!q || !kcache || !vcache || !out) return fail(QMM_ERR_INVALID, "null pointer");
+  QMM_TRY(check_attention(heads, kv_heads, head_dim, max_seq));
+  if (first < 0 || count < 0 || first + count > max_seq || count > 65535)
+    return fail(QMM_ERR_INVALID, "positions [%lld, %lld) outside the cache of %d", (long long)first,
+                (long long)(first + count), max_seq);
+  if (ldq < (int64_t)heads * head_dim || ldo < (int64_t)heads * head_dim)
+    return fail(QMM_ERR_INVALID, "row strides below heads * head_dim");
+  if (count == 0) return QMM_OK;
+  Device* d;
+  QMM_TRY(current_device(&d));
+  const int G = heads / kv_heads;
+  const int gt = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;
+  char name[64];
+  snprintf(name, sizeof(name), "qmm_prefill_attention_d%d_g%d", head_dim / 64, gt);
+  long long a = ldq, o = ldo;
+  int f = (int)first;
+  void* args[] = {&q, &a, &kcache, &vcache, &f, &out, &o, &heads, &kv_heads, &max_seq, &scale};
+  hipFunction_t fn;
+  QMM_TRY(kernel(d, name, &fn));
+  QMM_HIP(hipModuleLaunchKernel(fn, (unsigned)kv_heads, (unsigned)count, 1, 256, 1, 1, 0, (hipStream_t)stream, args,
+                                nullptr));
+  return QMM_OK;
+}
+
+int qmm_silu_mul(const float* g, const float* u, float* h, int64_t n, void* stream) {
+  if (!g || !u || !h || n < 0) return fail(QMM_ERR_INVALID, "bad silu_mul arguments");
+  if (n == 0) return QMM_OK;
+  Device* d;
+  QMM_TRY(current_device(&d));
+  long long nn = n;
+  void* args[] = {&g, &u, &h, &nn};
+  return launch(d, "qmm_silu_mul", ceil_div(n, 256), 256, 0, (hipStream_t)stream, args);
+}
+
 int qmm_silu_mul_quantize(const float* g, const float* u, int64_t rows, int64_t k, int64_t ld, void* hq,
                           void* stream) {
   if (!g || !u || !hq || rows < 1 || k < 256 || k % 256 || ld < k) return fail(QMM_ERR_INVALID, "bad silu_mul arguments");

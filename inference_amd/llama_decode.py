@@ -329,6 +329,67 @@ class DecodeSession:
                                         self.ws_argmax.numel(), s))
         tr("argmax", -1)
 
+    # -- batched prefill -----------------------------------------------------
+    def prefill(self) -> int:
+        """Run the prompt's positions 0 .. prompt_len - 2 in one pass per layer (matmuls with m = rows on
+        the MFMA GEMM path, batched RoPE + KV append, causal attention over the prompt), then leave the
+        session at position prompt_len - 1, where the captured step takes over: it processes the last
+        prompt token and produces the first generated one. Same operations and order per row as the
+        token-by-token steps, so the KV cache and the following logits match them to f32 accumulation
+        order. Returns the number of rows run. Call right after reset()."""
+        if self.prompt_len == 0 or self.steps_done != 0:
+            raise qmm.QmmError(1, "prefill() needs the state reset() leaves")
+        cfg, L, w = self.cfg, self.L, self.w
+        rows = self.prompt_len - 1
+        if rows == 0:
+            return 0
+        dev, s = self.dev, qmm._stream(self.dev)
+        H, F, hd = cfg.hidden, cfg.ffn, cfg.head_dim
+        nq, nkv = cfg.heads * hd, cfg.kv_heads * hd
+        f32 = dict(dtype=torch.float32, device=dev)
+        x = torch.empty((rows, H), **f32)
+        q = torch.empty((rows, nq), **f32)
+        k = torch.empty((rows, nkv), **f32)
+        v = torch.empty((rows, nkv), **f32)
+        att = torch.empty((rows, nq), **f32)
+        g = torch.empty((rows, F), **f32)
+        u = torch.empty((rows, F), **f32)
+        hh = torch.empty((rows, F), **f32)
+        wsb = 0
+        for lw in w.layers:
+            for t in lw.values():
+                wsb = max(wsb, int(L.qmm_matmul_ex_workspace_size(t.handle, rows, 1)))
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        vp, i64 = ctypes.c_void_p, ctypes.c_int64
+        eps = ctypes.c_float(cfg.eps)
+        qkv_y = (vp * 3)(q.data_ptr(), k.data_ptr(), v.data_ptr())
+        qkv_ld = (i64 * 3)(nq, nkv, nkv)
+        x_y, x_ld = (vp * 1)(x.data_ptr()), (i64 * 1)(H)
+        gu_y, gu_ld = (vp * 2)(g.data_ptr(), u.data_ptr()), (i64 * 2)(F, F)
+        kv_stride = cfg.kv_heads * self.max_seq * hd
+        qmm._check(L.qmm_embed_rows_n(w.embed.data_ptr(), H, self.tokens.data_ptr(), 0, rows, x.data_ptr(), H, s))
+        for li in range(cfg.layers):
+            lw = w.layers[li]
+            qmm._check(L.qmm_matmul_ex(self._qkv[li], 3, x.data_ptr(), rows, H, w.attn_norm[li].data_ptr(), eps, 0,
+                                       qkv_y, qkv_ld, ws.data_ptr(), ws.numel(), s))
+            kc = self.kcache.data_ptr() + 4 * li * kv_stride
+            vc = self.vcache.data_ptr() + 4 * li * kv_stride
+            qmm._check(L.qmm_rope_kv_append_n(q.data_ptr(), k.data_ptr(), v.data_ptr(), nq, nkv, nkv,
+                                              self.cos.data_ptr(), self.sin.data_ptr(), 0, rows, kc, vc, cfg.heads,
+                                              cfg.kv_heads, hd, self.max_seq, s))
+            qmm._check(L.qmm_prefill_attention(q.data_ptr(), nq, kc, vc, 0, rows, att.data_ptr(), nq, cfg.heads,
+                                               cfg.kv_heads, hd, self.max_seq, ctypes.c_float(self.scale), s))
+            qmm._check(L.qmm_matmul_ex((vp * 1)(lw["o"].handle.value), 1, att.data_ptr(), rows, nq, None, eps, 1,
+                                       x_y, x_ld, ws.data_ptr(), ws.numel(), s))
+            qmm._check(L.qmm_matmul_ex(self._gu[li], 2, x.data_ptr(), rows, H, w.ffn_norm[li].data_ptr(), eps, 0,
+                                       gu_y, gu_ld, ws.data_ptr(), ws.numel(), s))
+            qmm._check(L.qmm_silu_mul(g.data_ptr(), u.data_ptr(), hh.data_ptr(), rows * F, s))
+            qmm._check(L.qmm_matmul_ex((vp * 1)(lw["down"].handle.value), 1, hh.data_ptr(), rows, F, None, eps, 1,
+                                       x_y, x_ld, ws.data_ptr(), ws.numel(), s))
+        self.pos.fill_(rows)
+        self.steps_done = rows
+        return rows
+
     # -- driver ------------------------------------------------------------
     def reset(self, prompt: List[int]):
         """Load a prompt; the next step processes position 0."""
@@ -347,14 +408,18 @@ class DecodeSession:
         self.steps_done = 0
 
     def capture(self):
-        """Capture one step into a HIP graph. Called at the state reset() leaves; an eager warm-up
-        step (which loads the kernels) runs first and its effect is undone."""
-        if self.steps_done != 0:
-            raise qmm.QmmError(1, "capture() needs the state reset() leaves")
-        prompt = self.tokens[: self.prompt_len].cpu().tolist()
+        """Capture one step into a HIP graph, from any state. An eager warm-up step (which loads the
+        kernels) runs first and its effect is undone: the position and the token slot after it are
+        restored; the KV rows it wrote at the position are written again, identically, by the next
+        real step."""
+        p = int(self.pos.item())
+        nxt = self.tokens[p + 1].clone() if p + 1 < self.max_seq else None
         self.step()
         torch.cuda.synchronize()
-        self.reset(prompt)
+        self.pos.fill_(p)
+        if nxt is not None:
+            self.tokens[p + 1] = nxt
+        torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             self.step()

@@ -56,7 +56,8 @@ EXPORTS = (
     "qmm_gguf_tensor_count", "qmm_gguf_metadata_count", "qmm_gguf_find_tensor", "qmm_gguf_meta_find",
     "qmm_gguf_tensor_info", "qmm_gguf_type_size", "qmm_gguf_tensor_data", "qmm_gguf_meta_info",
     "qmm_gguf_meta_u64", "qmm_gguf_meta_i64", "qmm_gguf_meta_f64", "qmm_gguf_meta_string",
-    "qmm_gguf_load_qtensor", "qmm_qtensor_dequantize_to",
+    "qmm_gguf_load_qtensor", "qmm_qtensor_dequantize_to", "qmm_embed_rows_n", "qmm_rope_kv_append_n",
+    "qmm_prefill_attention", "qmm_silu_mul",
 )
 
 
@@ -136,6 +137,12 @@ def lib() -> ctypes.CDLL:
             "qmm_gguf_meta_string": ([vp, i64, i64, pp, ctypes.POINTER(ctypes.c_uint64)], i32),
             "qmm_gguf_load_qtensor": ([vp, i64, i32, vp, pp], i32),
             "qmm_qtensor_dequantize_to": ([vp, vp, i32, vp], i32),
+            "qmm_embed_rows_n": ([vp, i64, vp, i64, i64, vp, i64, vp], i32),
+            "qmm_rope_kv_append_n": ([vp, vp, vp, i64, i64, i64, vp, vp, i64, i64, vp, vp, i32, i32, i32, i32, vp],
+                                     i32),
+            "qmm_prefill_attention": ([vp, i64, vp, vp, i64, i64, vp, i64, i32, i32, i32, i32, ctypes.c_float, vp],
+                                      i32),
+            "qmm_silu_mul": ([vp, vp, vp, i64, vp], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)

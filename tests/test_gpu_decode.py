@@ -154,17 +154,22 @@ def op_level(cfg, weights, prompt, steps, max_seq):
     return sess.generated(steps + 1)
 
 
-def end_to_end(cfg, weights, prompt, steps, max_seq):
+def end_to_end(cfg, weights, prompt, steps, max_seq, prefill=False):
+    """Logits of every step against the oracle run token by token. With prefill, the prompt's first
+    len(prompt) - 1 positions run as one batched pass (no logits) and steps count from there."""
     sess = DecodeSession(weights, max_seq)
     sess.reset(prompt)
-    hist = torch.zeros((steps, cfg.vocab), dtype=torch.float32, device=weights.embed.device)
-    sess.run(steps, use_graph=True, history=hist)
+    first = sess.prefill() if prefill else 0
+    hist = torch.zeros((steps - first, cfg.vocab), dtype=torch.float32, device=weights.embed.device)
+    sess.run(steps - first, use_graph=True, history=hist)
     toks = sess.generated(steps + 1)
-    H = hist.cpu().numpy()
+    H = np.concatenate([np.zeros((first, cfg.vocab), np.float32), hist.cpu().numpy()])
     orl = ol.LlamaOracle(cfg, weights.export(), max_seq)
     errs, coss, flips = [], [], 0
     for p in range(steps):
         lg = orl.step(toks[p], p)
+        if p < first:
+            continue
         errs.append(rel_err(H[p], lg))
         coss.append(cosine(H[p], lg))
         if p + 1 >= len(prompt):
@@ -196,6 +201,38 @@ def test_decode_small_end_to_end(small_model):
     cfg, w = small_model
     prompt = [int(t) for t in np.random.default_rng(3).integers(0, cfg.vocab, 8)]
     end_to_end(cfg, w, prompt, 40, 64)
+
+
+def test_decode_small_prefill_end_to_end(small_model):
+    """Batched prefill of a 17-token prompt (16 rows through the GEMM path and causal attention), then
+    decode: every following step's logits against the token-by-token oracle."""
+    cfg, w = small_model
+    prompt = [int(t) for t in np.random.default_rng(5).integers(0, cfg.vocab, 17)]
+    end_to_end(cfg, w, prompt, 40, 64, prefill=True)
+
+
+def test_prefill_kv_cache_matches_token_steps(small_model):
+    """The caches a batched prefill writes against those of token-by-token steps over the same prompt
+    (per layer, cosine >= 0.9999; the first layer's keys and values to 1e-4 relative)."""
+    cfg, w = small_model
+    prompt = [int(t) for t in np.random.default_rng(6).integers(0, cfg.vocab, 30)]
+    a, b = DecodeSession(w, 64), DecodeSession(w, 64)
+    a.reset(prompt)
+    assert a.prefill() == 29 and int(a.pos.item()) == 29
+    b.reset(prompt)
+    b.run(29)
+    assert int(b.pos.item()) == 29
+    for name in ("kcache", "vcache"):
+        ca, cb = getattr(a, name)[:, :, :29].cpu().numpy(), getattr(b, name)[:, :, :29].cpu().numpy()
+        for li in range(cfg.layers):
+            assert cosine(ca[li].ravel(), cb[li].ravel()) >= 0.9999, (name, li)
+        assert rel_err(ca[0], cb[0]) <= 1e-4, name
+    # the next step from either state: logits agree closely
+    ha = torch.zeros((1, cfg.vocab), device=a.dev)
+    hb = torch.zeros((1, cfg.vocab), device=b.dev)
+    a.run(1, history=ha)
+    b.run(1, history=hb)
+    assert cosine(ha.cpu().numpy().ravel(), hb.cpu().numpy().ravel()) >= 0.9999
 
 
 def test_decode_graph_equals_eager_and_traced(small_model):
