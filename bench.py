@@ -359,7 +359,8 @@ def run_prefill(torch, dev):
 def run_moe(torch, dev):
     """Config 5: 8 experts (Q4_K gate/up 14336x4096, Q6_K down 4096x14336, N(0, 0.02^2) seed 7 on the
     device generator), 8 tokens N(0,1), router logits N(0,1) seed 8, top-2. One qmm_moe_ffn call:
-    routing, gathered Q8_K activations, expert GEMVs streaming each active expert once, SiLU*mul, combine."""
+    routing, gathered Q8_K activations, expert GEMVs streaming each active expert once, SiLU*mul, combine.
+    Then MoE prefill on the same experts (512 tokens through the grouped MFMA GEMMs)."""
     from inference_amd import GgmlDType, QTensor, qmm
     from inference_amd.synth import normal
     L = qmm.lib()
@@ -386,9 +387,28 @@ def run_moe(torch, dev):
         active.update(np.argsort(-row, kind="stable")[:k].tolist())
     per_expert = F * (H // 256) * 144 * 2 + H * (F // 256) * 210
     wbytes = per_expert * len(active)
-    return {"us": round(us, 2), "active_experts": len(active), "weight_bytes": wbytes,
-            "GB/s": round(wbytes / us / 1e3, 1), "hbm_frac": round(wbytes / us / 1e3 / HBM_PEAK_GBS, 4),
-            "tokens": T, "topk": k}
+    out = {"us": round(us, 2), "active_experts": len(active), "weight_bytes": wbytes,
+           "GB/s": round(wbytes / us / 1e3, 1), "hbm_frac": round(wbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+           "tokens": T, "topk": k}
+
+    # MoE prefill on the same experts: 512 tokens N(0,1) seed 9, router logits seed 10, top-2; the
+    # routed pairs average 128 rows per expert, so qmm_moe_ffn takes the grouped MFMA GEMMs.
+    Tp = 512
+    xp = torch.from_numpy(normal(9, (Tp, H))).to(dev)
+    lp = torch.from_numpy(normal(10, (Tp, E))).to(dev)
+    yp = torch.empty((Tp, H), dtype=torch.float32, device=dev)
+    wsp = int(L.qmm_moe_ffn_workspace_size(gate.handle, down.handle, Tp, E, k))
+    wsv = torch.empty(wsp, dtype=torch.uint8, device=dev)
+
+    def fnp():
+        qmm._check(L.qmm_moe_ffn(xp.data_ptr(), Tp, H, lp.data_ptr(), E, k, gate.handle, up.handle, down.handle,
+                                 yp.data_ptr(), H, wsv.data_ptr(), wsp, qmm._stream(dev)))
+    usp = timed_graph(torch, fnp, 4, 2)
+    ops = 2 * Tp * k * 3 * F * H  # int8 ops of the three projections over every routed pair
+    out["prefill"] = {"tokens": Tp, "us": round(usp, 2), "TOPS": round(ops / usp / 1e6, 1),
+                      "mfma_util": round(ops / usp / 1e6 / INT8_PEAK_TOPS, 4),
+                      "schedule": "route, gather, grouped MFMA GEMM gate/up, SiLU*mul, grouped GEMM down, combine"}
+    return out
 
 
 def cpu_baseline(sets, budget_s):

@@ -295,6 +295,21 @@ int qmm_moe_route(const float *logits, int64_t tokens, int experts, int topk, in
 int qmm_moe_gemv(const qmm_qtensor *const *w, int count, int experts, const void *xq, int64_t pairs,
                  const int32_t *counts, const int32_t *offsets, float *const *y, void *stream);
 
+/* Expert-grouped prefill GEMM (replaces the grouped prefill launcher
+ * moe/moe_wmma_gguf.cu:124-354 and the per-expert QMatMul::forward over
+ * gathered rows of MoeMlp::forward, llama.rs:1455-1474): x holds `pairs` f32
+ * rows (stride ldx) grouped by expert (counts/offsets as from
+ * qmm_moe_route); y[j] receives [pairs, N] f32 with N = rows / experts. The
+ * rows are quantized once (Q8_K / Q8_0, as QMatMul::forward does), then each
+ * expert's rows go through the int8 MFMA GEMM against its weight slice.
+ * max_rows bounds every count (e.g. the token count for top-k routing).
+ * Outputs equal qmm_matmul's GEMM path on each expert's rows bit for bit.
+ * ws: qmm_moe_gemm_workspace_size(w[0], pairs) bytes; k % 256 == 0. */
+size_t qmm_moe_gemm_workspace_size(const qmm_qtensor *w, int64_t pairs);
+int qmm_moe_gemm(const qmm_qtensor *const *w, int count, int experts, const float *x, int64_t pairs, int64_t ldx,
+                 int64_t max_rows, const int32_t *counts, const int32_t *offsets, float *const *y, void *ws,
+                 size_t ws_bytes, void *stream);
+
 /* The whole expert FFN at decode batch sizes: x f32 [tokens, hidden] (row
  * stride ldx), router logits f32 [tokens, experts], stacked gate/up
  * [experts*ffn, hidden] and down [experts*hidden, ffn] weights; out f32

@@ -663,7 +663,10 @@ static int gemm(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, f
   float* yy = y;
   int M = (int)m, N = (int)w->n, K = (int)w->k, ld = (int)ldy;
   int* dp = dump;
-  void* args[] = {&wq, &q8, &dd, &ss, &yy, &M, &N, &K, &ld, &dp, &accumulate};
+  // XCD-aware tile order (QMM_MMQ_XCD=0: plain blockIdx order)
+  int remap = 1;
+  if (const char* e = getenv("QMM_MMQ_XCD")) remap = atoi(e) != 0;
+  void* args[] = {&wq, &q8, &dd, &ss, &yy, &M, &N, &K, &ld, &dp, &accumulate, &remap};
   hipFunction_t f;
   // Q4_K: the second-generation kernel, 128x128 tiles (one workgroup of 512
   // threads per CU, double-buffered LDS of 2 x 58 KB). QMM_MMQ2="BM,BN" picks
@@ -1246,9 +1249,83 @@ int qmm_moe_gemv(const qmm_qtensor* const* w, int count, int experts, const void
   return QMM_OK;
 }
 
+// Grouped prefill GEMM over expert-ordered f32 rows: the rows are quantized
+// into GEMM planes in `ws`, then one launch per weight runs every expert's
+// M tiles (grid z = expert; tiles past an expert's rows exit at once).
+size_t qmm_moe_gemm_workspace_size(const qmm_qtensor* w, int64_t pairs) {
+  if (!w || pairs < 1) return 0;
+  return mmq_planes(w->dtype, pairs, w->k).total;
+}
+
+int qmm_moe_gemm(const qmm_qtensor* const* w, int count, int experts, const float* x, int64_t pairs, int64_t ldx,
+                 int64_t max_rows, const int32_t* counts, const int32_t* offsets, float* const* y, void* ws,
+                 size_t ws_bytes, void* stream) {
+  if (!w || !y || !x || !counts || !offsets || !ws || count < 1 || count > 2)
+    return fail(QMM_ERR_INVALID, "need 1..2 stacked weights, rows, routing arrays, outputs and a workspace");
+  if (experts < 1 || experts > 65535) return fail(QMM_ERR_INVALID, "bad expert count %d", experts);
+  for (int j = 0; j < count; ++j) {
+    if (!w[j] || !y[j]) return fail(QMM_ERR_INVALID, "null weight or output");
+    if (w[j]->dtype != w[0]->dtype || w[j]->k != w[0]->k || w[j]->n != w[0]->n)
+      return fail(QMM_ERR_INVALID, "stacked expert weights must share dtype and shape");
+  }
+  const qmm_qtensor* w0 = w[0];
+  if (w0->n % experts) return fail(QMM_ERR_INVALID, "rows %lld not divisible by %d experts", (long long)w0->n, experts);
+  if (w0->k % 256) return fail(QMM_ERR_UNSUPPORTED, "grouped GEMM needs k %% 256 == 0 (k = %lld)", (long long)w0->k);
+  if (pairs < 1 || pairs > (1LL << 24) || ldx < w0->k)
+    return fail(QMM_ERR_INVALID, "pairs must be 1..2^24 and ldx >= k");
+  if (max_rows < 1 || max_rows > pairs) return fail(QMM_ERR_INVALID, "max_rows must be 1..pairs");
+  if (ws_bytes < qmm_moe_gemm_workspace_size(w0, pairs))
+    return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed", ws_bytes, qmm_moe_gemm_workspace_size(w0, pairs));
+  Device* d;
+  QMM_TRY(current_device(&d));
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t* b = (uint8_t*)ws;
+  QMM_TRY(quantize_planes(d, w0->dtype, x, pairs, w0->k, ldx, b, s));
+  const Planes pl = mmq_planes(w0->dtype, pairs, w0->k);
+  const int fmt = fmt_of(w0->dtype);
+  const void* q8 = b + pl.q8;
+  const void* dd = b + pl.d;
+  const void* ss = b + pl.s;
+  int N = (int)(w0->n / experts), K = (int)w0->k, ld = N, E = experts;
+  // Q4_K: 128-row tiles (QMM_MOE_BM=64: 64-row tiles, less padding when an
+  // expert's row count sits just above a multiple of 128)
+  int bm = 64;
+  if (fmt == kFmtQ4K) {
+    bm = 128;
+    if (const char* e = getenv("QMM_MOE_BM")) bm = atoi(e) == 64 ? 64 : 128;
+  }
+  const int bn = 128;
+  const unsigned lds = fmt == kFmtQ4K ? (unsigned)(2 * (bm * 272 + 128 * 160 + bm * 4 + bm * 16)) : 0u;
+  char name[40];
+  if (fmt == kFmtQ4K)
+    snprintf(name, sizeof(name), "qmm_moe_mmq2_q4k%s", bm == 64 ? "_m64" : "");
+  else
+    snprintf(name, sizeof(name), "qmm_moe_mmq_%s", fmt_name(fmt));
+  hipFunction_t f;
+  QMM_TRY(kernel(d, name, &f));
+  for (int j = 0; j < count; ++j) {
+    const void* wq = w[j]->data;
+    float* yy = y[j];
+    void* args[] = {&wq, &q8, &dd, &ss, &yy, &N, &K, &ld, &E, &counts, &offsets};
+    QMM_HIP(hipModuleLaunchKernel(f, (unsigned)((N + bn - 1) / bn), (unsigned)((max_rows + bm - 1) / bm),
+                                  (unsigned)experts, fmt == kFmtQ4K ? (unsigned)(bm * 4) : 256u, 1, 1, lds, s, args,
+                                  nullptr));
+  }
+  return QMM_OK;
+}
+
+// qmm_moe_ffn runs the grouped GEMMs (prefill) instead of the expert GEMVs
+// when the routed pairs average more than this many rows per expert: the
+// GEMV streams an expert's weights once per eight rows, the GEMM once per
+// 128-row tile. QMM_MOE_GROUPED=0/1 forces the choice.
+static bool moe_grouped(int64_t pairs, int experts) {
+  if (const char* e = getenv("QMM_MOE_GROUPED")) return atoi(e) != 0;
+  return pairs > 16LL * experts;
+}
+
 // Workspace of qmm_moe_ffn, carved in this order.
 struct MoeWs {
-  size_t counts, offsets, pair_token, pair_weight, token_pairs, xg, xq, g, u, h, hq, yp, total;
+  size_t counts, offsets, pair_token, pair_weight, token_pairs, xg, xq, g, u, h, hq, yp, planes, total;
 };
 static MoeWs moe_ws(const qmm_qtensor* gate, const qmm_qtensor* down, int64_t T, int E, int k) {
   MoeWs w;
@@ -1265,13 +1342,14 @@ static MoeWs moe_ws(const qmm_qtensor* gate, const qmm_qtensor* down, int64_t T,
   w.pair_token = take(4 * P);
   w.pair_weight = take(4 * P);
   w.token_pairs = take(4 * P);
-  w.xg = take(vg == QMM_Q8K ? 0 : 4 * P * H);
+  w.xg = take(4 * P * H);  // f32 gathered rows (Q8_0 experts, grouped GEMMs)
   w.xq = take(P * (H / qmm_block_size(vg)) * qmm_type_size(vg));
   w.g = take(4 * P * F);
   w.u = take(4 * P * F);
   w.h = take(4 * P * F);
   w.hq = take(P * (F / qmm_block_size(vd)) * qmm_type_size(vd));
   w.yp = take(4 * P * H);
+  w.planes = take(std::max(mmq_planes(gate->dtype, P, H).total, mmq_planes(down->dtype, P, F).total));
   w.total = o;
   return w;
 }
@@ -1293,26 +1371,11 @@ size_t qmm_moe_ffn_workspace_size(const qmm_qtensor* gate, const qmm_qtensor* do
   return moe_ws(gate, down, tokens, experts, topk).total;
 }
 
-int qmm_moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* logits, int experts, int topk,
-                const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* down, float* out, int64_t ldo,
-                void* ws, size_t ws_bytes, void* stream) {
-  QMM_TRY(check_moe(gate, up, down, experts, topk));
-  if (!x || !logits || !out || !ws) return fail(QMM_ERR_INVALID, "null pointer");
-  const int64_t H = gate->k, F = gate->n / experts, P = tokens * topk;
-  if (ldx < H || ldo < H) return fail(QMM_ERR_INVALID, "row strides must be >= hidden size");
-  const MoeWs L = moe_ws(gate, down, tokens, experts, topk);
-  if (ws_bytes < L.total) return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed", ws_bytes, L.total);
-  Device* d;
-  QMM_TRY(current_device(&d));
-  hipStream_t s = (hipStream_t)stream;
-  uint8_t* b = (uint8_t*)ws;
-  int32_t* counts = (int32_t*)(b + L.counts);
-  int32_t* offsets = (int32_t*)(b + L.offsets);
-  int32_t* ptok = (int32_t*)(b + L.pair_token);
-  float* pw = (float*)(b + L.pair_weight);
-  int32_t* tpairs = (int32_t*)(b + L.token_pairs);
-  QMM_TRY(qmm_moe_route(logits, tokens, experts, topk, 1, counts, offsets, ptok, pw, tpairs, stream));
-  // gather + quantize the routed token rows (expert order)
+// Decode-sized MoE: gathered Q8_K rows through the expert GEMVs.
+static int moe_gemv_path(Device* d, const MoeWs& L, uint8_t* b, const float* x, int64_t ldx, const int32_t* ptok,
+                         int64_t P, int64_t H, int64_t F, int experts, const int32_t* counts, const int32_t* offsets,
+                         const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* down, hipStream_t s) {
+  void* stream = s;
   const int vg = qmm_vec_dot_type(gate->dtype);
   {
     const void* xp = x;
@@ -1346,10 +1409,61 @@ int qmm_moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* logits
   const int vd = qmm_vec_dot_type(down->dtype);
   QMM_TRY(qmm_quantize_rows(vd, h, P, F, F, b + L.hq, stream));
   float* yp = (float*)(b + L.yp);
-  {
+  const qmm_qtensor* dw[1] = {down};
+  float* dy[1] = {yp};
+  return qmm_moe_gemv(dw, 1, experts, b + L.hq, P, counts, offsets, dy, stream);
+}
+
+int qmm_moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* logits, int experts, int topk,
+                const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* down, float* out, int64_t ldo,
+                void* ws, size_t ws_bytes, void* stream) {
+  QMM_TRY(check_moe(gate, up, down, experts, topk));
+  if (!x || !logits || !out || !ws) return fail(QMM_ERR_INVALID, "null pointer");
+  const int64_t H = gate->k, F = gate->n / experts, P = tokens * topk;
+  if (ldx < H || ldo < H) return fail(QMM_ERR_INVALID, "row strides must be >= hidden size");
+  const MoeWs L = moe_ws(gate, down, tokens, experts, topk);
+  if (ws_bytes < L.total) return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed", ws_bytes, L.total);
+  Device* d;
+  QMM_TRY(current_device(&d));
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t* b = (uint8_t*)ws;
+  int32_t* counts = (int32_t*)(b + L.counts);
+  int32_t* offsets = (int32_t*)(b + L.offsets);
+  int32_t* ptok = (int32_t*)(b + L.pair_token);
+  float* pw = (float*)(b + L.pair_weight);
+  int32_t* tpairs = (int32_t*)(b + L.token_pairs);
+  QMM_TRY(qmm_moe_route(logits, tokens, experts, topk, 1, counts, offsets, ptok, pw, tpairs, stream));
+  float* g = (float*)(b + L.g);
+  float* u = (float*)(b + L.u);
+  float* h = (float*)(b + L.h);
+  float* yp = (float*)(b + L.yp);
+  if (moe_grouped(P, experts) && H % 256 == 0 && F % 256 == 0) {
+    // prefill: gathered f32 rows -> grouped GEMMs (an expert holds at most
+    // `tokens` pairs: a token's top-k experts are distinct)
+    float* xg = (float*)(b + L.xg);
+    {
+      const void* xp = x;
+      long long lx = ldx;
+      const int32_t* rows = ptok;
+      int kk = (int)H, nr = (int)P;
+      void* args[] = {&xp, &lx, &rows, &xg, &kk, &nr};
+      QMM_TRY(launch(d, "qmm_gather_rows", ceil_div(P * H, 256), 256, 0, s, args));
+    }
+    const qmm_qtensor* gw[2] = {gate, up};
+    float* gy[2] = {g, u};
+    QMM_TRY(qmm_moe_gemm(gw, 2, experts, xg, P, H, tokens, counts, offsets, gy, b + L.planes,
+                         L.total - L.planes, stream));
+    {
+      long long n = P * F;
+      void* args[] = {&g, &u, &h, &n};
+      QMM_TRY(launch(d, "qmm_silu_mul", ceil_div(n, 256), 256, 0, s, args));
+    }
     const qmm_qtensor* dw[1] = {down};
     float* dy[1] = {yp};
-    QMM_TRY(qmm_moe_gemv(dw, 1, experts, b + L.hq, P, counts, offsets, dy, stream));
+    QMM_TRY(qmm_moe_gemm(dw, 1, experts, h, P, F, tokens, counts, offsets, dy, b + L.planes, L.total - L.planes,
+                         stream));
+  } else {
+    QMM_TRY(moe_gemv_path(d, L, b, x, ldx, ptok, P, H, F, experts, counts, offsets, gate, up, down, s));
   }
   {
     int T = (int)tokens, k = topk, N = (int)H, lo = (int)ldo;

@@ -206,20 +206,49 @@ __device__ __forceinline__ i8x16 as_i8x16(uint4 v) { return __builtin_bit_cast(i
 // Byte `i` (0..7) of an 8-byte word pair.
 __device__ __forceinline__ uint32_t byte8(uint2 w, int i) { return ((i < 4 ? w.x : w.y) >> (8 * (i & 3))) & 0xffu; }
 
-// y[m, n] = sum over K of x[m, :] . W[n, :] with the formats' scaling.
-// DUMP instantiations also write every integer block dot (debug entry point).
+// This workgroup's (M tile, N tile). With remap, the grid's tiles are dealt
+// so that the workgroups of one XCD take consecutive tiles in M-major order:
+// the dispatcher hands workgroups to the eight XCDs round-robin by linear id
+// and every XCD has its own L2, so an XCD's workgroups then share a few M
+// tiles' activation rows in that L2 instead of each XCD streaming all of them.
+// The map is a bijection of the grid; without remap, tile = (blockIdx.y, .x).
+__device__ __forceinline__ void gemm_tile(int remap, int& mt, int& nt) {
+  if (!remap) {
+    mt = blockIdx.y;
+    nt = blockIdx.x;
+    return;
+  }
+  const int gx = gridDim.x, g = gx * gridDim.y;
+  const int lin = blockIdx.y * gx + blockIdx.x;
+  const int xcd = lin & 7, slot = lin >> 3, q = g >> 3, r = g & 7;
+  const int t = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
+  mt = t / gx;
+  nt = t - mt * gx;
+}
+
+// f16 block scales of a scale-split Q6_K / Q8_0 weight of `rows` rows (they
+// follow all block bodies); Q4_K keeps its scales inside the blocks.
+template <int FMT>
+__device__ __forceinline__ const uint16_t* split_scales(const uint8_t* wq, long long rows, int K) {
+  const int nbw = FMT == kFmtQ80 ? K / 32 : K / 256;
+  return FMT == kFmtQ4K ? nullptr
+                        : reinterpret_cast<const uint16_t*>(wq + (size_t)rows * nbw * FmtInfo<FMT>::kBodyBytes);
+}
+
+// y[m, n] = sum over K of x[m, :] . W[n, :] with the formats' scaling; wd =
+// the weight's block scales (split_scales). DUMP instantiations also write
+// every integer block dot (debug entry point).
 template <int FMT, bool DUMP>
-__device__ __forceinline__ void mmq(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,
-                                    const float* __restrict__ xd, const int16_t* __restrict__ xs,
-                                    float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,
-                                    int accumulate) {
+__device__ __forceinline__ void mmq(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                    const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                    const int16_t* __restrict__ xs, float* __restrict__ y, int M, int N, int K,
+                                    int ldy, int* __restrict__ dump, int accumulate, int remap) {
   __shared__ MmqLds L;
-  const int m0 = blockIdx.y * kMmqBM, n0 = blockIdx.x * kMmqBN;
+  int mt, nt;
+  gemm_tile(remap, mt, nt);
+  const int m0 = mt * kMmqBM, n0 = nt * kMmqBN;
   const int nbk = K / 256;
   const int nbw = FMT == kFmtQ80 ? K / 32 : nbk;  // weight blocks per row
-  const uint16_t* wd =
-      FMT == kFmtQ4K ? nullptr
-                     : reinterpret_cast<const uint16_t*>(wq + (size_t)N * nbw * FmtInfo<FMT>::kBodyBytes);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 31, h = lane >> 5;
   const int wm = wave & 1, wn = wave >> 1;
@@ -428,15 +457,17 @@ extern "C" __global__ void __launch_bounds__(256) qmm_quantize_q8_0_mmq(const fl
   extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))               \
       qmm_mmq_##NAME(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                          \
                      const float* __restrict__ xd, const int16_t* __restrict__ xs, float* __restrict__ y,   \
-                     int M, int N, int K, int ldy, int* __restrict__ dump, int accumulate) {                 \
-    qmm::mmq<FMT, false>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate);                                 \
+                     int M, int N, int K, int ldy, int* __restrict__ dump, int accumulate, int remap) {     \
+    qmm::mmq<FMT, false>(wq, qmm::split_scales<FMT>(wq, N, K), xq, xd, xs, y, M, N, K, ldy, dump, accumulate,  \
+                         remap);                                                                              \
   }                                                                                                          \
   extern "C" __global__ void __launch_bounds__(256)                                                          \
       qmm_mmq_##NAME##_dump(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                   \
                             const float* __restrict__ xd, const int16_t* __restrict__ xs,                    \
                             float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,     \
-                            int accumulate) {                                                                \
-    qmm::mmq<FMT, true>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate);                                  \
+                            int accumulate, int remap) {                                                     \
+    qmm::mmq<FMT, true>(wq, qmm::split_scales<FMT>(wq, N, K), xq, xd, xs, y, M, N, K, ldy, dump, accumulate,   \
+                        remap);                                                                               \
   }
 
 QMM_MMQ_KERNEL(qmm::kFmtQ4K, q4k)
@@ -582,10 +613,12 @@ template <int BM, int BN, bool DUMP>
 __device__ __forceinline__ void mmq2_q4k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,
                                          const float* __restrict__ xd, const int16_t* __restrict__ xs,
                                          float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,
-                                         int accumulate) {
+                                         int accumulate, int remap) {
   using C = M2<BM, BN>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  int mt, nt;
+  gemm_tile(remap, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
   const int nbk = K / 256;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 31, h = lane >> 5;
@@ -724,12 +757,14 @@ template <int BN, bool DUMP>
 __device__ __forceinline__ void mmq4_q4k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,
                                          const float* __restrict__ xd, const int16_t* __restrict__ xs,
                                          float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,
-                                         int accumulate) {
+                                         int accumulate, int remap) {
   constexpr int BM = 128, NT = 256;
   constexpr int TN = BN / 64;  // N tiles per wave
   using C = M2<BM, BN, NT>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  int mt, nt;
+  gemm_tile(remap, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
   const int nbk = K / 256;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 31, h = lane >> 5;
@@ -751,9 +786,8 @@ __device__ __forceinline__ void mmq4_q4k(const uint8_t* __restrict__ wq, const i
   m2_load<BM, BN, NT>(R, xq, xd, xs, wq, M, N, K, m0, n0, 0);
   m2_store<BM, BN, NT>(R, lds);
   __syncthreads();
-  for (int kb = 0; kb < nbk; ++kb) {
-    uint8_t* buf = lds + (kb & 1) * C::kStage;
-    if (kb + 1 < nbk) m2_load<BM, BN, NT>(R, xq, xd, xs, wq, M, N, K, m0, n0, kb + 1);
+  // one K step from LDS buffer `buf` (the next step's loads are in flight)
+  auto step = [&](const uint8_t* buf, int kb) {
     const int8_t* A = reinterpret_cast<const int8_t*>(buf);
     const float* DX = reinterpret_cast<const float*>(buf + C::kA + C::kB);
     const uint8_t* SUM = buf + C::kA + C::kB + C::kDx;
@@ -840,6 +874,10 @@ __device__ __forceinline__ void mmq4_q4k(const uint8_t* __restrict__ wq, const i
         }
       }
     }
+  };
+  for (int kb = 0; kb < nbk; ++kb) {
+    if (kb + 1 < nbk) m2_load<BM, BN, NT>(R, xq, xd, xs, wq, M, N, K, m0, n0, kb + 1);
+    step(lds + (kb & 1) * C::kStage, kb);
     if (kb + 1 < nbk) m2_store<BM, BN, NT>(R, lds + ((kb + 1) & 1) * C::kStage);
     __syncthreads();
   }
@@ -865,15 +903,15 @@ __device__ __forceinline__ void mmq4_q4k(const uint8_t* __restrict__ wq, const i
   extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))                 \
       qmm_mmq4_q4k_n##BN(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                        \
                          const float* __restrict__ xd, const int16_t* __restrict__ xs, float* __restrict__ y,   \
-                         int M, int N, int K, int ldy, int* __restrict__ dump, int accumulate) {                \
-    qmm::mmq4_q4k<BN, false>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate);                               \
+                         int M, int N, int K, int ldy, int* __restrict__ dump, int accumulate, int remap) {     \
+    qmm::mmq4_q4k<BN, false>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate, remap);                        \
   }                                                                                                            \
   extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))                 \
       qmm_mmq4_q4k_n##BN##_dump(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                 \
                                 const float* __restrict__ xd, const int16_t* __restrict__ xs,                  \
                                 float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,    \
-                                int accumulate) {                                                              \
-    qmm::mmq4_q4k<BN, true>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate);                                \
+                                int accumulate, int remap) {                                                   \
+    qmm::mmq4_q4k<BN, true>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate, remap);                         \
   }
 QMM_MMQ4_KERNEL(128)
 QMM_MMQ4_KERNEL(64)
@@ -883,14 +921,14 @@ QMM_MMQ4_KERNEL(64)
       qmm_mmq2_q4k_m##BM##_n##BN(                                                                            \
       const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq, const float* __restrict__ xd,           \
       const int16_t* __restrict__ xs, float* __restrict__ y, int M, int N, int K, int ldy,                   \
-      int* __restrict__ dump, int accumulate) {                                                              \
-    qmm::mmq2_q4k<BM, BN, false>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate);                         \
+      int* __restrict__ dump, int accumulate, int remap) {                                                   \
+    qmm::mmq2_q4k<BM, BN, false>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate, remap);                  \
   }                                                                                                          \
   extern "C" __global__ void __launch_bounds__(BM * BN / 32) qmm_mmq2_q4k_m##BM##_n##BN##_dump(              \
       const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq, const float* __restrict__ xd,           \
       const int16_t* __restrict__ xs, float* __restrict__ y, int M, int N, int K, int ldy,                   \
-      int* __restrict__ dump, int accumulate) {                                                              \
-    qmm::mmq2_q4k<BM, BN, true>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate);                          \
+      int* __restrict__ dump, int accumulate, int remap) {                                                   \
+    qmm::mmq2_q4k<BM, BN, true>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate, remap);                   \
   }
 
 QMM_MMQ2_KERNEL(128, 128)

@@ -20,7 +20,12 @@
 //   counts[e], offsets[e] (exclusive prefix, offsets[E] = T*k),
 //   pair_token[p], pair_weight[p] for p in [offsets[e], offsets[e] + counts[e]),
 //   token_pairs[t*k + s] = the pairs of token t in increasing expert order.
-// One workgroup; T <= 4096, T*k <= 8192, E <= 256, k <= 8.
+// One workgroup of four waves; T <= 4096, T*k <= 8192, E <= 256, k <= 8.
+// Pass 1: each thread routes tokens (softmax, top-k) into LDS and counts the
+// selections per expert; the offsets are the exclusive prefix of the counts.
+// Pass 2: each wave takes experts e = wave, wave + 4, ... and walks the tokens
+// 64 at a time: a ballot of the lanes whose token selected e ranks them, so
+// pair p = offsets[e] + (pairs of e so far) + (selecting lanes below).
 extern "C" __global__ void __launch_bounds__(256) qmm_moe_route(const float* __restrict__ logits, int T, int E,
                                                                 int k, int renorm, int* __restrict__ counts,
                                                                 int* __restrict__ offsets,
@@ -28,10 +33,14 @@ extern "C" __global__ void __launch_bounds__(256) qmm_moe_route(const float* __r
                                                                 float* __restrict__ pair_weight,
                                                                 int* __restrict__ token_pairs) {
 #pragma clang fp contract(off)
+  constexpr int kThreads = 256, kWaves = kThreads / 64;
   __shared__ short sel_e[8192];
   __shared__ float sel_w[8192];
-  __shared__ int cnt[4096];
-  for (int t = threadIdx.x; t < T; t += blockDim.x) {
+  __shared__ int ecount[256];
+  __shared__ int eoff[257];
+  for (int e = threadIdx.x; e < E; e += kThreads) ecount[e] = 0;
+  __syncthreads();
+  for (int t = threadIdx.x; t < T; t += kThreads) {
     const float* l = logits + (size_t)t * E;
     float mx = l[0];
     for (int e = 1; e < E; ++e) mx = fmaxf(mx, l[e]);
@@ -62,29 +71,43 @@ extern "C" __global__ void __launch_bounds__(256) qmm_moe_route(const float* __r
     for (int s = 0; s < k; ++s) {
       sel_e[t * k + s] = (short)ids[s];
       sel_w[t * k + s] = renorm ? p[s] / denom : p[s];
+      atomicAdd(&ecount[ids[s]], 1);
     }
   }
   __syncthreads();
   if (threadIdx.x == 0) {
     int pos = 0;
     for (int e = 0; e < E; ++e) {
-      offsets[e] = pos;
-      int c = 0;
-      for (int t = 0; t < T; ++t)
-        for (int s = 0; s < k; ++s)
-          if (sel_e[t * k + s] == e) {
-            pair_token[pos] = t;
-            pair_weight[pos] = sel_w[t * k + s];
-            ++pos;
-            ++c;
-          }
-      counts[e] = c;
+      eoff[e] = pos;
+      pos += ecount[e];
     }
-    offsets[E] = pos;
-    for (int t = 0; t < T; ++t) cnt[t] = 0;
-    for (int p = 0; p < pos; ++p) {  // pairs are in expert order, so each token's come in that order
-      const int t = pair_token[p];
-      token_pairs[t * k + cnt[t]++] = p;
+    eoff[E] = pos;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e <= E; e += kThreads) {
+    offsets[e] = eoff[e];
+    if (e < E) counts[e] = ecount[e];
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int e = wave; e < E; e += kWaves) {
+    int base = eoff[e];
+    for (int t0 = 0; t0 < T; t0 += 64) {
+      const int t = t0 + lane;
+      int slot = -1, before = 0;
+      if (t < T)
+        for (int s = 0; s < k; ++s) {
+          const int es = sel_e[t * k + s];
+          if (es == e) slot = s;
+          before += es < e;
+        }
+      const unsigned long long m = __ballot(slot >= 0);
+      if (slot >= 0) {
+        const int pr = base + __popcll(m & ((1ull << lane) - 1ull));
+        pair_token[pr] = t;
+        pair_weight[pr] = sel_w[t * k + slot];
+        token_pairs[t * k + before] = pr;  // the token's pairs in increasing expert order
+      }
+      base += __popcll(m);
     }
   }
 }
@@ -295,3 +318,74 @@ QMM_MOE_KERNEL(qmm::kFmtQ6K, q6k, 1)
 QMM_MOE_KERNEL(qmm::kFmtQ6K, q6k, 2)
 QMM_MOE_KERNEL(qmm::kFmtQ80, q8_0, 1)
 QMM_MOE_KERNEL(qmm::kFmtQ80, q8_0, 2)
+
+// ---------------------------------------------------------------------------
+// MoE prefill: grouped GEMM over the expert-ordered pair rows (the grouped
+// prefill of moe/moe_wmma_gguf.cu:124-354, here on the int8 MFMA GEMM tiles).
+// blockIdx.z is the expert e; its rows are pairs offsets[e] ..
+// offsets[e] + counts[e] - 1 of the activation planes and of y (row stride
+// ldy), its weight rows e*N .. e*N + N - 1 of the stacked [E*N, K] tensor. An
+// M tile past the expert's rows exits before any load, so every workgroup
+// that runs computes exactly what the per-expert GEMM over that expert's
+// gathered rows computes, in the same order.
+// ---------------------------------------------------------------------------
+namespace qmm {
+
+// Planes of the expert's first row: int8 [row][K], scales [row][K/256] (Q8_K)
+// or [row][K/32] (Q8_0), Q8_K 32-element sums [row][K/256][8].
+struct GroupRows {
+  const int8_t* xq;
+  const float* xd;
+  const int16_t* xs;
+  float* y;
+  int m;
+};
+
+template <int BM, bool Q80>
+__device__ __forceinline__ bool group_rows(GroupRows& g, const int8_t* xq, const float* xd, const int16_t* xs,
+                                           float* y, int K, int ldy, const int* __restrict__ counts,
+                                           const int* __restrict__ offsets) {
+  const int e = blockIdx.z;
+  g.m = counts[e];
+  if ((int)blockIdx.y * BM >= g.m) return false;
+  const long long off = offsets[e];
+  g.xq = xq + off * K;
+  g.xd = xd + off * (Q80 ? K / 32 : K / 256);
+  g.xs = xs + off * (K / 256) * 8;
+  g.y = y + off * ldy;
+  return true;
+}
+
+}  // namespace qmm
+
+#define QMM_MOE_MMQ2_KERNEL(BM, SUFFIX)                                                                         \
+  extern "C" __global__ void __launch_bounds__(BM * 4) __attribute__((amdgpu_waves_per_eu(2 * 64 / BM)))         \
+      qmm_moe_mmq2_q4k##SUFFIX(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                   \
+                               const float* __restrict__ xd, const int16_t* __restrict__ xs,                    \
+                               float* __restrict__ y, int N, int K, int ldy, int E,                             \
+                               const int* __restrict__ counts, const int* __restrict__ offsets) {               \
+    qmm::GroupRows g;                                                                                           \
+    if (!qmm::group_rows<BM, false>(g, xq, xd, xs, y, K, ldy, counts, offsets)) return;                         \
+    const uint8_t* we = wq + (size_t)blockIdx.z * N * (K / 256) * qmm::kQ4KBytes;                               \
+    qmm::mmq2_q4k<BM, 128, false>(we, g.xq, g.xd, g.xs, g.y, g.m, N, K, ldy, nullptr, 0, 0);                    \
+    (void)E;                                                                                                    \
+  }
+QMM_MOE_MMQ2_KERNEL(128, )
+QMM_MOE_MMQ2_KERNEL(64, _m64)
+
+#define QMM_MOE_MMQ_KERNEL(FMT, NAME)                                                                          \
+  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))                 \
+      qmm_moe_mmq_##NAME(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                        \
+                         const float* __restrict__ xd, const int16_t* __restrict__ xs, float* __restrict__ y,   \
+                         int N, int K, int ldy, int E, const int* __restrict__ counts,                          \
+                         const int* __restrict__ offsets) {                                                    \
+    qmm::GroupRows g;                                                                                          \
+    if (!qmm::group_rows<qmm::kMmqBM, FMT == qmm::kFmtQ80>(g, xq, xd, xs, y, K, ldy, counts, offsets)) return; \
+    const int nbw = FMT == qmm::kFmtQ80 ? K / 32 : K / 256;                                                    \
+    const size_t rows0 = (size_t)blockIdx.z * N;                                                               \
+    const uint16_t* wd = qmm::split_scales<FMT>(wq, (long long)E * N, K) + rows0 * nbw;                        \
+    const uint8_t* we = wq + rows0 * nbw * qmm::FmtInfo<FMT>::kBodyBytes;                                      \
+    qmm::mmq<FMT, false>(we, wd, g.xq, g.xd, g.xs, g.y, g.m, N, K, ldy, nullptr, 0, 0);                        \
+  }
+QMM_MOE_MMQ_KERNEL(qmm::kFmtQ6K, q6k)
+QMM_MOE_MMQ_KERNEL(qmm::kFmtQ80, q8_0)

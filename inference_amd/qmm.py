@@ -47,7 +47,8 @@ EXPORTS = (
     "qmm_qtensor_from_ggml", "qmm_qtensor_quantize", "qmm_qtensor_dequantize",
     "qmm_qtensor_to_ggml", "qmm_qtensor_info", "qmm_qtensor_ggml_bytes", "qmm_qtensor_free",
     "qmm_quantize_rows", "qmm_matmul_workspace_size", "qmm_matmul", "qmm_matmul_q",
-    "qmm_matmul_multi", "qmm_block_dots", "qmm_moe_route", "qmm_moe_gemv", "qmm_moe_ffn_workspace_size",
+    "qmm_matmul_multi", "qmm_block_dots", "qmm_moe_route", "qmm_moe_gemv", "qmm_moe_gemm_workspace_size", "qmm_moe_gemm",
+    "qmm_moe_ffn_workspace_size",
     "qmm_moe_ffn", "qmm_matmul_ex", "qmm_matmul_ex_workspace_size", "qmm_rms_norm", "qmm_embed_rows",
     "qmm_rope_kv_append", "qmm_decode_attention", "qmm_silu_mul_quantize", "qmm_greedy_advance",
     "qmm_matmul_q_ex", "qmm_decode_attention_workspace_size", "qmm_decode_rope_attention",
@@ -97,6 +98,9 @@ def lib() -> ctypes.CDLL:
             "qmm_block_dots": ([vp, vp, i64, vp, i64, vp, vp], i32),
             "qmm_moe_route": ([vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, vp], i32),
             "qmm_moe_gemv": ([ctypes.POINTER(vp), i32, i32, vp, i64, vp, vp, ctypes.POINTER(vp), vp], i32),
+            "qmm_moe_gemm_workspace_size": ([vp, i64], ctypes.c_size_t),
+            "qmm_moe_gemm": ([ctypes.POINTER(vp), i32, i32, vp, i64, i64, i64, vp, vp, ctypes.POINTER(vp), vp,
+                              ctypes.c_size_t, vp], i32),
             "qmm_moe_ffn_workspace_size": ([vp, vp, i64, i32, i32], sz),
             "qmm_moe_ffn": ([vp, i64, i64, vp, i32, i32, vp, vp, vp, vp, i64, vp, sz, vp], i32),
             "qmm_matmul_ex": ([ctypes.POINTER(vp), i32, vp, i64, i64, vp, ctypes.c_float, i32, ctypes.POINTER(vp),

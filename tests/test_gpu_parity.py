@@ -425,7 +425,8 @@ def _stacked_experts(E, H, F, seed, dt_gu=GgmlDType.Q4K, dt_down=GgmlDType.Q6K):
 def test_moe_route_matches_oracle():
     from inference_amd import moe_route
     from oracle import moe
-    for T, E, k in ((8, 8, 2), (37, 16, 4), (1, 4, 1)):
+    # decode sizes, prefill sizes, the limits (T*k = 8192, E = 256, k = 8) and ragged token counts
+    for T, E, k in ((8, 8, 2), (37, 16, 4), (1, 4, 1), (512, 8, 2), (4096, 8, 2), (1000, 256, 8), (130, 64, 3)):
         logits = normal(200 + T, (T, E))
         counts, offsets, ptok, pw, tp = [a.cpu().numpy() for a in moe_route(torch.from_numpy(logits).to(DEV), k)]
         experts, weights = moe.route(logits, k)
