@@ -115,7 +115,9 @@ void qmm_qtensor_free(qmm_qtensor *t);
 int qmm_quantize_rows(int vdtype, const float *x, int64_t m, int64_t k, int64_t ldx, void *xq,
                       void *stream);
 
-/* Bytes of workspace qmm_matmul needs for m activation rows. */
+/* Bytes of workspace qmm_matmul needs for m activation rows (for m > 8: the
+ * GEMM's quantized activation planes plus, when the weight's output tiles
+ * cover fewer than half the CUs, f32 split-K partials). */
 size_t qmm_matmul_workspace_size(const qmm_qtensor *w, int64_t m);
 
 /* QMatMul::forward: y[i, j] = sum_k x[i, k] * W[j, k] for i < m, j < n, with x
@@ -132,7 +134,12 @@ int qmm_matmul(const qmm_qtensor *w, const float *x, int64_t m, int64_t ldx, flo
  * y[j] = x . W[j]^T for weights of one dtype and k (e.g. a layer's q/k/v and
  * gate/up projections, which the reference engine runs as separate
  * QuantizedLinear::forward calls on the same activation, llama.rs:1066-1092,
- * 1386-1391). ldy[j] is the row stride of y[j]; ws as for qmm_matmul. */
+ * 1386-1391). ldy[j] is the row stride of y[j]; ws: at least
+ * qmm_matmul_workspace_size(w[0], m) bytes. For m > 8 the GEMMs of narrow
+ * weights split K over more workgroups and need room for f32 partials: a
+ * job whose split does not fit the workspace runs unsplit (same block dots,
+ * another f32 summation order), so size ws as the largest over the weights
+ * for the same results as separate qmm_matmul calls. */
 int qmm_matmul_multi(const qmm_qtensor *const *w, int count, const float *x, int64_t m, int64_t ldx,
                      float *const *y, const int64_t *ldy, void *ws, size_t ws_bytes, void *stream);
 

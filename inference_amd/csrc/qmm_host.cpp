@@ -456,12 +456,15 @@ static Planes mmq_planes(int dtype, int64_t m, int64_t k) {
 // The GEMM handles m > 8 rows when k is a whole number of 256-wide steps.
 static bool use_gemm(const qmm_qtensor* w, int64_t m) { return m > 8 && w->k % 256 == 0; }
 
+static size_t gemm_split_bytes(const qmm_qtensor* w, int64_t m);
+
 size_t qmm_matmul_workspace_size(const qmm_qtensor* w, int64_t m) {
   if (!w || m <= 0) return 0;
   const int vt = qmm_vec_dot_type(w->dtype);
   const size_t ggml = (size_t)m * (size_t)(w->k / qmm_block_size(vt)) * qmm_type_size(vt);
   if (!use_gemm(w, m)) return ggml;
-  return mmq_planes(w->dtype, m, w->k).total;
+  // activation planes, then the split-K partials
+  return mmq_planes(w->dtype, m, w->k).total + gemm_split_bytes(w, m);
 }
 
 // Job table of one GEMV launch (passed to the kernel as scalar arguments).
@@ -649,25 +652,35 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   return launch(d, name, (unsigned)wgs, 64 * wv, lds, s, args);
 }
 
-// Prefill GEMM over activation planes at `ws` (see mmq_planes).
-static int gemm(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, float* y, int64_t ldy, int* dump,
-                hipStream_t s, int accumulate = 0) {
-  const Planes pl = mmq_planes(w->dtype, m, w->k);
-  const int fmt = fmt_of(w->dtype);
+// Kernel, tile and split-K plan of one prefill GEMM.
+struct GemmPlan {
   char name[40];
-  snprintf(name, sizeof(name), "qmm_mmq_%s%s", fmt_name(fmt), dump ? "_dump" : "");
-  const void* wq = w->data;
-  const void* q8 = ws + pl.q8;
-  const void* dd = ws + pl.d;
-  const void* ss = ws + pl.s;
-  float* yy = y;
-  int M = (int)m, N = (int)w->n, K = (int)w->k, ld = (int)ldy;
-  int* dp = dump;
-  // XCD-aware tile order (QMM_MMQ_XCD=0: plain blockIdx order)
-  int remap = 1;
-  if (const char* e = getenv("QMM_MMQ_XCD")) remap = atoi(e) != 0;
-  void* args[] = {&wq, &q8, &dd, &ss, &yy, &M, &N, &K, &ld, &dp, &accumulate, &remap};
-  hipFunction_t f;
+  unsigned gx, gy, threads, lds;
+  int splits, kc;  // K steps per split
+};
+
+// Split-K: a grid of fewer than half as many tiles as CUs (e.g. m = 127
+// against N = 4096: 32-64 tiles) leaves most CUs idle for the whole K loop;
+// splitting the K steps over blockIdx.z fills them, and a small kernel sums
+// the splits' f32 partials in split order. QMM_SPLITK=0 disables it,
+// QMM_SPLITK=<S> forces S splits.
+static void plan_splits(const Device* d, GemmPlan& p, int nbk) {
+  const long long tiles = (long long)p.gx * p.gy;
+  int sp = 1;
+  if (const char* e = getenv("QMM_SPLITK")) {
+    sp = atoi(e);
+  } else if (tiles * 2 <= d->num_cu) {
+    sp = (int)((d->num_cu + tiles - 1) / tiles);
+  }
+  sp = std::max(1, std::min(std::min(sp, 16), nbk));
+  p.kc = (nbk + sp - 1) / sp;
+  p.splits = (nbk + p.kc - 1) / p.kc;
+}
+
+static GemmPlan gemm_plan(const Device* d, const qmm_qtensor* w, int64_t m, bool dump) {
+  GemmPlan p;
+  const int fmt = fmt_of(w->dtype);
+  const int M = (int)m, N = (int)w->n;
   // Q4_K: the second-generation kernel, 128x128 tiles (one workgroup of 512
   // threads per CU, double-buffered LDS of 2 x 58 KB). QMM_MMQ2="BM,BN" picks
   // 64-row tiles instead.
@@ -691,23 +704,73 @@ static int gemm(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, f
   if (fmt == kFmtQ4K && use4) {
     int b4 = 64;
     if (const char* e = getenv("QMM_MMQ4_BN")) b4 = atoi(e) == 128 ? 128 : 64;
-    const unsigned lds4 = (unsigned)(2 * (128 * 272 + b4 * 160 + 128 * 4 + 128 * 16));
-    snprintf(name, sizeof(name), "qmm_mmq4_q4k_n%d%s", b4, dump ? "_dump" : "");
-    QMM_TRY(kernel(d, name, &f));
-    QMM_HIP(hipModuleLaunchKernel(f, (unsigned)((N + b4 - 1) / b4), (unsigned)((M + 127) / 128), 1, 256, 1, 1, lds4,
-                                  s, args, nullptr));
-    return QMM_OK;
+    snprintf(p.name, sizeof(p.name), "qmm_mmq4_q4k_n%d%s", b4, dump ? "_dump" : "");
+    p.gx = (unsigned)((N + b4 - 1) / b4);
+    p.gy = (unsigned)((M + 127) / 128);
+    p.threads = 256;
+    p.lds = (unsigned)(2 * (128 * 272 + b4 * 160 + 128 * 4 + 128 * 16));
+  } else if (fmt == kFmtQ4K && (int)lds2 <= d->max_lds && getenv("QMM_MMQ1") == nullptr) {
+    snprintf(p.name, sizeof(p.name), "qmm_mmq2_q4k_m%d_n%d%s", bm, bn, dump ? "_dump" : "");
+    p.gx = (unsigned)((N + bn - 1) / bn);
+    p.gy = (unsigned)((M + bm - 1) / bm);
+    p.threads = (unsigned)(bm * bn / 32);
+    p.lds = lds2;
+  } else {
+    snprintf(p.name, sizeof(p.name), "qmm_mmq_%s%s", fmt_name(fmt), dump ? "_dump" : "");
+    p.gx = (unsigned)((N + 127) / 128);
+    p.gy = (unsigned)((M + 63) / 64);
+    p.threads = 256;
+    p.lds = 0;
   }
-  if (fmt == kFmtQ4K && (int)lds2 <= d->max_lds && getenv("QMM_MMQ1") == nullptr) {
-    snprintf(name, sizeof(name), "qmm_mmq2_q4k_m%d_n%d%s", bm, bn, dump ? "_dump" : "");
-    QMM_TRY(kernel(d, name, &f));
-    QMM_HIP(hipModuleLaunchKernel(f, (unsigned)((N + bn - 1) / bn), (unsigned)((M + bm - 1) / bm), 1,
-                                  (unsigned)(bm * bn / 32), 1, 1, lds2, s, args, nullptr));
-    return QMM_OK;
+  plan_splits(d, p, (int)(w->k / 256));
+  return p;
+}
+
+// Bytes of f32 split partials a GEMM of w at m rows uses (0 without split-K).
+static size_t gemm_split_bytes(const qmm_qtensor* w, int64_t m) {
+  Device* d;
+  if (current_device(&d) != QMM_OK) return 0;
+  const GemmPlan p = gemm_plan(d, w, m, false);
+  return p.splits > 1 ? align256((size_t)p.splits * (size_t)m * (size_t)w->n * 4) : 0;
+}
+
+// Prefill GEMM over activation planes at `ws` (see mmq_planes); `part` holds
+// part_bytes of scratch for split partials (a split plan that does not fit
+// runs as one split).
+static int gemm(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, float* y, int64_t ldy, int* dump,
+                hipStream_t s, int accumulate, float* part, size_t part_bytes) {
+  const Planes pl = mmq_planes(w->dtype, m, w->k);
+  GemmPlan p = gemm_plan(d, w, m, dump != nullptr);
+  const size_t need = (size_t)p.splits * (size_t)m * (size_t)w->n * 4;
+  if (p.splits > 1 && (part == nullptr || need > part_bytes)) {
+    p.splits = 1;
+    p.kc = (int)(w->k / 256);
   }
-  QMM_TRY(kernel(d, name, &f));
-  const unsigned gx = (unsigned)((N + 127) / 128), gy = (unsigned)((M + 63) / 64);
-  QMM_HIP(hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, s, args, nullptr));
+  const bool split = p.splits > 1;
+  const void* wq = w->data;
+  const void* q8 = ws + pl.q8;
+  const void* dd = ws + pl.d;
+  const void* ss = ws + pl.s;
+  float* yy = split ? part : y;
+  int M = (int)m, N = (int)w->n, K = (int)w->k, ld = split ? N : (int)ldy;
+  int* dp = dump;
+  int acc = split ? 0 : accumulate;
+  // XCD-aware tile order (QMM_MMQ_XCD=0: plain blockIdx order); split
+  // launches keep the plain order
+  int remap = split ? 0 : 1;
+  if (const char* e = getenv("QMM_MMQ_XCD")) remap = remap && atoi(e) != 0;
+  int kc = p.kc;
+  long long ysplit = split ? (long long)M * N : 0;
+  void* args[] = {&wq, &q8, &dd, &ss, &yy, &M, &N, &K, &ld, &dp, &acc, &remap, &kc, &ysplit};
+  hipFunction_t f;
+  QMM_TRY(kernel(d, p.name, &f));
+  QMM_HIP(hipModuleLaunchKernel(f, p.gx, p.gy, (unsigned)p.splits, p.threads, 1, 1, p.lds, s, args, nullptr));
+  if (split) {
+    const float* pp = part;
+    int sp = p.splits, lo = (int)ldy;
+    void* a2[] = {&pp, &sp, &M, &N, &y, &lo, &accumulate};
+    QMM_TRY(launch(d, "qmm_splitk_sum", ceil_div((int64_t)M * N, 256), 256, 0, s, a2));
+  }
   return QMM_OK;
 }
 
@@ -784,9 +847,10 @@ int qmm_matmul_q(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int6
   const int vt = qmm_vec_dot_type(w->dtype);
   if (use_gemm(w, m)) {
     uint8_t* ws;
-    QMM_TRY(scratch(mmq_planes(w->dtype, m, w->k).total, &ws));
+    const size_t pb = mmq_planes(w->dtype, m, w->k).total, sb = gemm_split_bytes(w, m);
+    QMM_TRY(scratch(pb + sb, &ws));
     QMM_TRY(blocks_to_planes(d, w->dtype, xq, m, w->k, ws, (hipStream_t)stream));
-    return gemm(d, w, ws, m, y, ldy, nullptr, (hipStream_t)stream);
+    return gemm(d, w, ws, m, y, ldy, nullptr, (hipStream_t)stream, 0, (float*)(ws + pb), sb);
   }
   const size_t xrow = (size_t)(w->k / qmm_block_size(vt)) * qmm_type_size(vt);
   // Rows are processed in groups of up to 8 by the GEMV.
@@ -864,19 +928,26 @@ static int matmul_targets(const GemvTarget* tg, int count, const float* x, int64
     return gemv(d, tg, count, x, true, ldx, (int)m, nullptr, s, norm_w, eps, accumulate);
   }
   size_t need = qmm_matmul_workspace_size(w, m);
-  if (norm_w) need += align256((size_t)(m * w->k) * 4);
+  const size_t nrm = norm_w ? align256((size_t)(m * w->k) * 4) : 0;
+  need += nrm;
   if (!ws || ws_bytes < need) return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed", ws_bytes, need);
+  // layout: quantized activation (GGML rows or GEMM planes), normalised rows,
+  // then (GEMM) split-K partials in the rest
+  const size_t base = use_gemm(w, m) ? mmq_planes(w->dtype, m, w->k).total : qmm_matmul_workspace_size(w, m);
   if (norm_w) {
-    // normalised rows go after the quantized activation in the workspace
-    float* xn = (float*)((uint8_t*)ws + qmm_matmul_workspace_size(w, m));
+    float* xn = (float*)((uint8_t*)ws + base);
     QMM_TRY(qmm_rms_norm(x, m, w->k, ldx, norm_w, eps, xn, w->k, stream));
     x = xn;
     ldx = w->k;
   }
   if (use_gemm(w, m)) {
     QMM_TRY(quantize_planes(d, w->dtype, x, m, w->k, ldx, (uint8_t*)ws, s));
+    // a job whose split plan needs more than the rest of the workspace runs
+    // unsplit (size ws for the largest weight to split every job)
+    float* part = (float*)((uint8_t*)ws + base + nrm);
+    const size_t sb = ws_bytes - base - nrm;
     for (int j = 0; j < count; ++j)
-      QMM_TRY(gemm(d, tg[j].w, (const uint8_t*)ws, m, tg[j].y, tg[j].ldy, nullptr, s, accumulate));
+      QMM_TRY(gemm(d, tg[j].w, (const uint8_t*)ws, m, tg[j].y, tg[j].ldy, nullptr, s, accumulate, part, sb));
     return QMM_OK;
   }
   const int vt = qmm_vec_dot_type(w->dtype);
@@ -1170,9 +1241,10 @@ int qmm_block_dots(const qmm_qtensor* w, const void* xq, int64_t m, float* y, in
   if (m > 8) {
     if (!use_gemm(w, m)) return fail(QMM_ERR_UNSUPPORTED, "block dots for m > 8 need k %% 256 == 0");
     uint8_t* ws;
-    QMM_TRY(scratch(mmq_planes(w->dtype, m, w->k).total, &ws));
+    const size_t pb = mmq_planes(w->dtype, m, w->k).total, sb = gemm_split_bytes(w, m);
+    QMM_TRY(scratch(pb + sb, &ws));
     QMM_TRY(blocks_to_planes(d, w->dtype, xq, m, w->k, ws, (hipStream_t)stream));
-    return gemm(d, w, ws, m, y, ldy, dots, (hipStream_t)stream);
+    return gemm(d, w, ws, m, y, ldy, dots, (hipStream_t)stream, 0, (float*)(ws + pb), sb);
   }
   GemvTarget t = {w, y, ldy};
   return gemv(d, &t, 1, xq, false, 0, (int)m, dots, (hipStream_t)stream);

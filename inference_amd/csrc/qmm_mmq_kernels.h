@@ -226,6 +226,17 @@ __device__ __forceinline__ void gemm_tile(int remap, int& mt, int& nt) {
   nt = t - mt * gx;
 }
 
+// Split-K: the K steps [kb0, kb1) of split blockIdx.z (kc steps each); the
+// split's f32 partial goes to y + blockIdx.z * ysplit (the host sums the
+// splits in order). One split: kc = K / 256, ysplit = 0.
+struct KRange {
+  int kb0, kb1;
+};
+__device__ __forceinline__ KRange split_range(int K, int kc) {
+  const int kb0 = (int)blockIdx.z * kc, nbk = K / 256;
+  return {kb0, kb0 + kc < nbk ? kb0 + kc : nbk};
+}
+
 // f16 block scales of a scale-split Q6_K / Q8_0 weight of `rows` rows (they
 // follow all block bodies); Q4_K keeps its scales inside the blocks.
 template <int FMT>
@@ -242,7 +253,7 @@ template <int FMT, bool DUMP>
 __device__ __forceinline__ void mmq(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                     const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                     const int16_t* __restrict__ xs, float* __restrict__ y, int M, int N, int K,
-                                    int ldy, int* __restrict__ dump, int accumulate, int remap) {
+                                    int ldy, int* __restrict__ dump, int accumulate, int remap, int kb0, int kb1) {
   __shared__ MmqLds L;
   int mt, nt;
   gemm_tile(remap, mt, nt);
@@ -263,12 +274,12 @@ __device__ __forceinline__ void mmq(const uint8_t* __restrict__ wq, const uint16
   for (int j = 0; j < 16; ++j) acc0[j] = acc1[j] = 0.0f;
 
   MmqRegs R;
-  mmq_load<FMT>(R, xq, xd, xs, wq, wd, M, N, K, m0, n0, 0);
-  for (int kb = 0; kb < nbk; ++kb) {
+  mmq_load<FMT>(R, xq, xd, xs, wq, wd, M, N, K, m0, n0, kb0);
+  for (int kb = kb0; kb < kb1; ++kb) {
     __syncthreads();
     mmq_store<FMT>(R, L);
     __syncthreads();
-    if (kb + 1 < nbk) mmq_load<FMT>(R, xq, xd, xs, wq, wd, M, N, K, m0, n0, kb + 1);
+    if (kb + 1 < kb1) mmq_load<FMT>(R, xq, xd, xs, wq, wd, M, N, K, m0, n0, kb + 1);
 
     const int8_t* arow = L.a + (32 * wm + r) * kMmqStride + 16 * h;
     const int8_t* b0row = L.b + col0 * kMmqStride + 16 * h;
@@ -457,17 +468,20 @@ extern "C" __global__ void __launch_bounds__(256) qmm_quantize_q8_0_mmq(const fl
   extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))               \
       qmm_mmq_##NAME(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                          \
                      const float* __restrict__ xd, const int16_t* __restrict__ xs, float* __restrict__ y,   \
-                     int M, int N, int K, int ldy, int* __restrict__ dump, int accumulate, int remap) {     \
-    qmm::mmq<FMT, false>(wq, qmm::split_scales<FMT>(wq, N, K), xq, xd, xs, y, M, N, K, ldy, dump, accumulate,  \
-                         remap);                                                                              \
+                     int M, int N, int K, int ldy, int* __restrict__ dump, int accumulate, int remap,       \
+                     int kc, long long ysplit) {                                                             \
+    const qmm::KRange kr = qmm::split_range(K, kc);                                                          \
+    qmm::mmq<FMT, false>(wq, qmm::split_scales<FMT>(wq, N, K), xq, xd, xs, y + blockIdx.z * ysplit, M, N, K,  \
+                         ldy, dump, accumulate, remap, kr.kb0, kr.kb1);                                       \
   }                                                                                                          \
   extern "C" __global__ void __launch_bounds__(256)                                                          \
       qmm_mmq_##NAME##_dump(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                   \
                             const float* __restrict__ xd, const int16_t* __restrict__ xs,                    \
                             float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,     \
-                            int accumulate, int remap) {                                                     \
-    qmm::mmq<FMT, true>(wq, qmm::split_scales<FMT>(wq, N, K), xq, xd, xs, y, M, N, K, ldy, dump, accumulate,   \
-                        remap);                                                                               \
+                            int accumulate, int remap, int kc, long long ysplit) {                           \
+    const qmm::KRange kr = qmm::split_range(K, kc);                                                          \
+    qmm::mmq<FMT, true>(wq, qmm::split_scales<FMT>(wq, N, K), xq, xd, xs, y + blockIdx.z * ysplit, M, N, K,   \
+                        ldy, dump, accumulate, remap, kr.kb0, kr.kb1);                                        \
   }
 
 QMM_MMQ_KERNEL(qmm::kFmtQ4K, q4k)
@@ -613,7 +627,7 @@ template <int BM, int BN, bool DUMP>
 __device__ __forceinline__ void mmq2_q4k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,
                                          const float* __restrict__ xd, const int16_t* __restrict__ xs,
                                          float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,
-                                         int accumulate, int remap) {
+                                         int accumulate, int remap, int kb0, int kb1) {
   using C = M2<BM, BN>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   int mt, nt;
@@ -637,12 +651,12 @@ __device__ __forceinline__ void mmq2_q4k(const uint8_t* __restrict__ wq, const i
     for (int j = 0; j < 16; ++j) acc[i][j] = 0.0f;
 
   M2Regs<BM, BN> R;
-  m2_load<BM, BN>(R, xq, xd, xs, wq, M, N, K, m0, n0, 0);
+  m2_load<BM, BN>(R, xq, xd, xs, wq, M, N, K, m0, n0, kb0);
   m2_store<BM, BN>(R, lds);
   __syncthreads();
-  for (int kb = 0; kb < nbk; ++kb) {
-    uint8_t* buf = lds + (kb & 1) * C::kStage;
-    if (kb + 1 < nbk) m2_load<BM, BN>(R, xq, xd, xs, wq, M, N, K, m0, n0, kb + 1);
+  for (int kb = kb0; kb < kb1; ++kb) {
+    uint8_t* buf = lds + ((kb - kb0) & 1) * C::kStage;
+    if (kb + 1 < kb1) m2_load<BM, BN>(R, xq, xd, xs, wq, M, N, K, m0, n0, kb + 1);
     const int8_t* A = reinterpret_cast<const int8_t*>(buf);
     const uint8_t* Bc = buf + C::kA + bcol * kM2BStride;  // this lane's weight block
     const float* DX = reinterpret_cast<const float*>(buf + C::kA + C::kB);
@@ -705,7 +719,7 @@ __device__ __forceinline__ void mmq2_q4k(const uint8_t* __restrict__ wq, const i
         }
       }
     }
-    if (kb + 1 < nbk) m2_store<BM, BN>(R, lds + ((kb + 1) & 1) * C::kStage);
+    if (kb + 1 < kb1) m2_store<BM, BN>(R, lds + ((kb + 1 - kb0) & 1) * C::kStage);
     __syncthreads();
   }
 #pragma unroll
@@ -757,7 +771,7 @@ template <int BN, bool DUMP>
 __device__ __forceinline__ void mmq4_q4k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,
                                          const float* __restrict__ xd, const int16_t* __restrict__ xs,
                                          float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,
-                                         int accumulate, int remap) {
+                                         int accumulate, int remap, int kb0, int kb1) {
   constexpr int BM = 128, NT = 256;
   constexpr int TN = BN / 64;  // N tiles per wave
   using C = M2<BM, BN, NT>;
@@ -783,7 +797,7 @@ __device__ __forceinline__ void mmq4_q4k(const uint8_t* __restrict__ wq, const i
       for (int j = 0; j < 16; ++j) acc[i][t][j] = 0.0f;
 
   M2Regs<BM, BN, NT> R;
-  m2_load<BM, BN, NT>(R, xq, xd, xs, wq, M, N, K, m0, n0, 0);
+  m2_load<BM, BN, NT>(R, xq, xd, xs, wq, M, N, K, m0, n0, kb0);
   m2_store<BM, BN, NT>(R, lds);
   __syncthreads();
   // one K step from LDS buffer `buf` (the next step's loads are in flight)
@@ -875,10 +889,10 @@ __device__ __forceinline__ void mmq4_q4k(const uint8_t* __restrict__ wq, const i
       }
     }
   };
-  for (int kb = 0; kb < nbk; ++kb) {
-    if (kb + 1 < nbk) m2_load<BM, BN, NT>(R, xq, xd, xs, wq, M, N, K, m0, n0, kb + 1);
-    step(lds + (kb & 1) * C::kStage, kb);
-    if (kb + 1 < nbk) m2_store<BM, BN, NT>(R, lds + ((kb + 1) & 1) * C::kStage);
+  for (int kb = kb0; kb < kb1; ++kb) {
+    if (kb + 1 < kb1) m2_load<BM, BN, NT>(R, xq, xd, xs, wq, M, N, K, m0, n0, kb + 1);
+    step(lds + ((kb - kb0) & 1) * C::kStage, kb);
+    if (kb + 1 < kb1) m2_store<BM, BN, NT>(R, lds + ((kb + 1 - kb0) & 1) * C::kStage);
     __syncthreads();
   }
 #pragma unroll
@@ -903,15 +917,20 @@ __device__ __forceinline__ void mmq4_q4k(const uint8_t* __restrict__ wq, const i
   extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))                 \
       qmm_mmq4_q4k_n##BN(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                        \
                          const float* __restrict__ xd, const int16_t* __restrict__ xs, float* __restrict__ y,   \
-                         int M, int N, int K, int ldy, int* __restrict__ dump, int accumulate, int remap) {     \
-    qmm::mmq4_q4k<BN, false>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate, remap);                        \
+                         int M, int N, int K, int ldy, int* __restrict__ dump, int accumulate, int remap,       \
+                         int kc, long long ysplit) {                                                            \
+    const qmm::KRange kr = qmm::split_range(K, kc);                                                            \
+    qmm::mmq4_q4k<BN, false>(wq, xq, xd, xs, y + blockIdx.z * ysplit, M, N, K, ldy, dump, accumulate, remap,   \
+                             kr.kb0, kr.kb1);                                                                  \
   }                                                                                                            \
   extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))                 \
       qmm_mmq4_q4k_n##BN##_dump(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                 \
                                 const float* __restrict__ xd, const int16_t* __restrict__ xs,                  \
                                 float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,    \
-                                int accumulate, int remap) {                                                   \
-    qmm::mmq4_q4k<BN, true>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate, remap);                         \
+                                int accumulate, int remap, int kc, long long ysplit) {                         \
+    const qmm::KRange kr = qmm::split_range(K, kc);                                                            \
+    qmm::mmq4_q4k<BN, true>(wq, xq, xd, xs, y + blockIdx.z * ysplit, M, N, K, ldy, dump, accumulate, remap,    \
+                            kr.kb0, kr.kb1);                                                                   \
   }
 QMM_MMQ4_KERNEL(128)
 QMM_MMQ4_KERNEL(64)
@@ -921,16 +940,35 @@ QMM_MMQ4_KERNEL(64)
       qmm_mmq2_q4k_m##BM##_n##BN(                                                                            \
       const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq, const float* __restrict__ xd,           \
       const int16_t* __restrict__ xs, float* __restrict__ y, int M, int N, int K, int ldy,                   \
-      int* __restrict__ dump, int accumulate, int remap) {                                                   \
-    qmm::mmq2_q4k<BM, BN, false>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate, remap);                  \
+      int* __restrict__ dump, int accumulate, int remap, int kc, long long ysplit) {                         \
+    const qmm::KRange kr = qmm::split_range(K, kc);                                                          \
+    qmm::mmq2_q4k<BM, BN, false>(wq, xq, xd, xs, y + blockIdx.z * ysplit, M, N, K, ldy, dump, accumulate,    \
+                                 remap, kr.kb0, kr.kb1);                                                      \
   }                                                                                                          \
   extern "C" __global__ void __launch_bounds__(BM * BN / 32) qmm_mmq2_q4k_m##BM##_n##BN##_dump(              \
       const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq, const float* __restrict__ xd,           \
       const int16_t* __restrict__ xs, float* __restrict__ y, int M, int N, int K, int ldy,                   \
-      int* __restrict__ dump, int accumulate, int remap) {                                                   \
-    qmm::mmq2_q4k<BM, BN, true>(wq, xq, xd, xs, y, M, N, K, ldy, dump, accumulate, remap);                   \
+      int* __restrict__ dump, int accumulate, int remap, int kc, long long ysplit) {                         \
+    const qmm::KRange kr = qmm::split_range(K, kc);                                                          \
+    qmm::mmq2_q4k<BM, BN, true>(wq, xq, xd, xs, y + blockIdx.z * ysplit, M, N, K, ldy, dump, accumulate,     \
+                                remap, kr.kb0, kr.kb1);                                                       \
   }
 
 QMM_MMQ2_KERNEL(128, 128)
 QMM_MMQ2_KERNEL(64, 128)
 QMM_MMQ2_KERNEL(64, 64)
+
+// Split-K sum: y[m, n] (+)= part[0][m, n] + ... + part[splits - 1][m, n], in
+// split order (partials [splits][M][N], row stride N).
+extern "C" __global__ void __launch_bounds__(256) qmm_splitk_sum(const float* __restrict__ part, int splits, int M,
+                                                                 int N, float* __restrict__ y, int ldy,
+                                                                 int accumulate) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long long)M * N) return;
+  const int m = (int)(i / N), n = (int)(i - (long long)m * N);
+  const size_t plane = (size_t)M * N;
+  float s = part[i];
+  for (int k = 1; k < splits; ++k) s += part[i + k * plane];
+  float* yp = y + (size_t)m * ldy + n;
+  *yp = accumulate ? *yp + s : s;
+}

@@ -367,7 +367,7 @@ __device__ __forceinline__ bool group_rows(GroupRows& g, const int8_t* xq, const
     qmm::GroupRows g;                                                                                           \
     if (!qmm::group_rows<BM, false>(g, xq, xd, xs, y, K, ldy, counts, offsets)) return;                         \
     const uint8_t* we = wq + (size_t)blockIdx.z * N * (K / 256) * qmm::kQ4KBytes;                               \
-    qmm::mmq2_q4k<BM, 128, false>(we, g.xq, g.xd, g.xs, g.y, g.m, N, K, ldy, nullptr, 0, 0);                    \
+    qmm::mmq2_q4k<BM, 128, false>(we, g.xq, g.xd, g.xs, g.y, g.m, N, K, ldy, nullptr, 0, 0, 0, K / 256);        \
     (void)E;                                                                                                    \
   }
 QMM_MOE_MMQ2_KERNEL(128, )
@@ -385,7 +385,7 @@ QMM_MOE_MMQ2_KERNEL(64, _m64)
     const size_t rows0 = (size_t)blockIdx.z * N;                                                               \
     const uint16_t* wd = qmm::split_scales<FMT>(wq, (long long)E * N, K) + rows0 * nbw;                        \
     const uint8_t* we = wq + rows0 * nbw * qmm::FmtInfo<FMT>::kBodyBytes;                                      \
-    qmm::mmq<FMT, false>(we, wd, g.xq, g.xd, g.xs, g.y, g.m, N, K, ldy, nullptr, 0, 0);                        \
+    qmm::mmq<FMT, false>(we, wd, g.xq, g.xd, g.xs, g.y, g.m, N, K, ldy, nullptr, 0, 0, 0, K / 256);            \
   }
 QMM_MOE_MMQ_KERNEL(qmm::kFmtQ6K, q6k)
 QMM_MOE_MMQ_KERNEL(qmm::kFmtQ80, q8_0)

@@ -414,7 +414,7 @@ def matmul_multi(qts: Sequence[QTensor], x: torch.Tensor) -> Tuple[torch.Tensor,
     m = x2.shape[0]
     ys = [torch.empty((m, q.shape[0]), dtype=torch.float32, device=x.device) for q in qts]
     L = lib()
-    ws_bytes = int(L.qmm_matmul_workspace_size(qts[0].handle, m))
+    ws_bytes = max(int(L.qmm_matmul_workspace_size(q.handle, m)) for q in qts)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
     hs = (ctypes.c_void_p * len(qts))(*[q.handle.value for q in qts])
     yp = (ctypes.c_void_p * len(qts))(*[y.data_ptr() for y in ys])

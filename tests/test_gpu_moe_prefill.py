@@ -84,6 +84,7 @@ def test_grouped_gemm_equals_per_expert_gemm(monkeypatch, dt, E, N, K, T, mode):
     if mode == "skew":
         assert c[0] == T and c[1] == T and c[2:].sum() == 0
     monkeypatch.setenv("QMM_MMQ", "2")  # per-expert Q4_K on the same 128x128 kernel as the grouped launch
+    monkeypatch.setenv("QMM_SPLITK", "1")  # and unsplit, as the grouped launch is
     for e in range(E):
         if c[e] == 0:
             continue
