@@ -694,13 +694,14 @@ static GemmPlan gemm_plan(const Device* d, const qmm_qtensor* w, int64_t m, bool
   }
   const unsigned lds2 = (unsigned)(2 * (bm * 272 + bn * 160 + bm * 4 + bm * 16));
   // Q4_K: mmq2 (128x128 tiles, 8 waves, VALU sub-block scaling) when its grid
-  // covers every CU; otherwise (e.g. N = 4096 at M = 512: 128 tiles) the
-  // split-scale mmq4 with 128x64 tiles (4 waves, one per SIMD), which gives
-  // twice the workgroups (4096x14336 at M = 512: 144 vs 194 us).
+  // covers at least half the CUs (split-K fills the rest: 4096x14336 at
+  // M = 512, 128 tiles x 2 splits: 120 us); below that (the prefill's
+  // M = 127) the split-scale mmq4 with 128x64 tiles (4 waves, one per SIMD),
+  // twice the workgroups (14336x4096 at M = 127: 41 vs 52 us).
   // QMM_MMQ=2 / QMM_MMQ=4 force one; QMM_MMQ4_BN=128 picks 128x128 mmq4 tiles.
   const char* gen = getenv("QMM_MMQ");
   const long long tiles2 = (long long)((N + bn - 1) / bn) * ((M + bm - 1) / bm);
-  const bool use4 = gen ? atoi(gen) == 4 : tiles2 < d->num_cu;
+  const bool use4 = gen ? atoi(gen) == 4 : tiles2 * 2 < d->num_cu;
   if (fmt == kFmtQ4K && use4) {
     int b4 = 64;
     if (const char* e = getenv("QMM_MMQ4_BN")) b4 = atoi(e) == 128 ? 128 : 64;
