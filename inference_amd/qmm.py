@@ -247,6 +247,20 @@ class QTensor:
         return cls(h, dev)
 
     @classmethod
+    def quantize_onto(cls, tensor: torch.Tensor, dtype: GgmlDType, device: torch.device) -> "QTensor":
+        """QTensor::quantize_onto (candle-gen/src/quant/mod.rs:693-728): a host, contiguous, zero-offset
+        f32 source quantized straight into a QTensor on `device` (here: copied up, then quantized there).
+        Any other source is an error, as in the reference."""
+        if tensor.device.type != "cpu":
+            raise QmmError(1, f"quantize_onto expects a CPU source tensor, got {tensor.device}")
+        if not tensor.is_contiguous() or tensor.storage_offset() != 0:
+            raise QmmError(1, "quantize_onto expects a contiguous source with zero offset")
+        dev = torch.device(device)
+        if dev.type != "cuda":
+            raise QmmError(1, f"quantize_onto targets a GPU device, got {dev}")
+        return cls.quantize(tensor.to(dev), dtype)
+
+    @classmethod
     def from_ggml(cls, data, dtype: GgmlDType, shape: Sequence[int],
                   device: Optional[torch.device] = None) -> "QTensor":
         """QTensor::new(QStorage::from_data(GGML bytes), shape).

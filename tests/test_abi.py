@@ -81,3 +81,17 @@ def test_python_api_validates_on_host():
     with pytest.raises(QmmError):
         from inference_amd import quantize_rows
         quantize_rows(GgmlDType.Q8K, torch.zeros(1, 256))  # CPU tensor: rejected, no fallback
+
+
+def test_quantize_onto_source_rules():
+    """QTensor::quantize_onto takes a host, contiguous, zero-offset source (candle-gen/src/quant/mod.rs:693-717)
+    and a GPU target; everything else is rejected before any device work."""
+    import torch
+    from inference_amd import GgmlDType, QmmError, QTensor
+    w = torch.zeros(8, 512)
+    with pytest.raises(QmmError, match="contiguous"):
+        QTensor.quantize_onto(w.t(), GgmlDType.Q4K, torch.device("cuda:0"))
+    with pytest.raises(QmmError, match="contiguous"):
+        QTensor.quantize_onto(w[1:], GgmlDType.Q4K, torch.device("cuda:0"))  # nonzero offset
+    with pytest.raises(QmmError, match="GPU"):
+        QTensor.quantize_onto(w, GgmlDType.Q4K, torch.device("cpu"))

@@ -107,3 +107,12 @@ def test_dequant_dense_survives_outlier_activations(dt):
     q8 = cosine(QLinear(qt, None, MatmulStrategy.INT8_FAST).forward(xd).cpu().numpy(), ref)
     assert dq > 0.99, dq
     assert dq > q8 + 0.05, (dq, q8)
+
+
+def test_quantize_onto_equals_device_quantize():
+    """QTensor::quantize_onto from a host weight gives the same blocks as QTensor::quantize on the device."""
+    w = torch.from_numpy(np.random.default_rng(31).standard_normal((300, 512)).astype(np.float32) * 0.02)
+    for dt in (GgmlDType.Q4K, GgmlDType.Q6K, GgmlDType.Q8_0):
+        a = QTensor.quantize_onto(w, dt, DEV)
+        b = QTensor.quantize(w.to(DEV), dt)
+        assert a.device == DEV and np.array_equal(a.to_ggml(), b.to_ggml())
