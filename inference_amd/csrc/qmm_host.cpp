@@ -1293,6 +1293,7 @@ int qmm_moe_gemv(const qmm_qtensor* const* w, int count, int experts, const void
   // QMM_MOE_GEMV=<P> the ring depth.
   int ring = fmt == kFmtQ4K ? 2 : fmt == kFmtQ6K ? 1 : 0;
   if (const char* e = getenv("QMM_MOE_GEMV")) ring = fmt != kFmtQ80 ? std::min(std::max(atoi(e), 0), 2) : 0;
+  if (experts > 256) ring = 0;  // the ring kernel lists the active experts in a 256-entry LDS table
   char name[48];
   if (ring)
     snprintf(name, sizeof(name), "qmm_moe_gemv1_%s_p%d", fmt_name(fmt), ring);
@@ -1307,16 +1308,22 @@ int qmm_moe_gemv(const qmm_qtensor* const* w, int count, int experts, const void
   float* y1 = count > 1 ? y[1] : y[0];
   const void* xp = xq;
   void* args[] = {&w0, &w1, &nj, &N, &E, &y0, &y1, &ld, &xp, &xrow, &counts, &offsets, &K};
-  // generic: ~20 resident waves per CU spread over the experts; ring: two
-  // 16-wave workgroups per CU over the experts (idle experts exit at once)
+  // generic: ~20 resident waves per CU spread over the experts (grid y =
+  // expert, idle experts exit at once); ring: two 16-wave workgroups per CU
+  // shared out over the active experts inside the kernel (grid >= E)
   const int wpg = ring ? 16 : 8;
-  long long gx = ring ? ((long long)d->num_cu * 2 + E - 1) / E : ((long long)d->num_cu * 20 / 8 + E - 1) / E;
-  const long long need = ((long long)N * count + wpg - 1) / wpg;
-  if (gx > need) gx = need;
-  if (gx < 1) gx = 1;
   hipFunction_t f;
   QMM_TRY(kernel(d, name, &f));
   (void)pairs;
+  if (ring) {
+    const long long gr = std::max<long long>((long long)d->num_cu * 2, E);
+    QMM_HIP(hipModuleLaunchKernel(f, (unsigned)gr, 1, 1, 64 * wpg, 1, 1, lds, (hipStream_t)stream, args, nullptr));
+    return QMM_OK;
+  }
+  long long gx = ((long long)d->num_cu * 20 / 8 + E - 1) / E;
+  const long long need = ((long long)N * count + wpg - 1) / wpg;
+  if (gx > need) gx = need;
+  if (gx < 1) gx = 1;
   QMM_HIP(hipModuleLaunchKernel(f, (unsigned)gx, (unsigned)E, 1, 64 * wpg, 1, 1, lds, (hipStream_t)stream, args,
                                 nullptr));
   return QMM_OK;

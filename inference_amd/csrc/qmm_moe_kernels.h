@@ -211,16 +211,38 @@ __device__ __forceinline__ void moe_gemv1(const uint8_t* __restrict__ w0, const 
   static_assert(FMT != kFmtQ80, "k-quant weights");
   constexpr int BPI = 16;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int e = blockIdx.y;
+  // The grid is shared out over the experts that have tokens: active
+  // expert s (in expert order) gets workgroups [ceil(s G / na), ceil((s + 1) G / na))
+  // of the G in the grid (G >= E), so every workgroup streams weights, however
+  // many experts are idle.
+  __shared__ int act[256];
+  __shared__ int nact;
+  const int lane = threadIdx.x & 63, l = lane & 3, g = lane >> 2;
+  if (threadIdx.x < 64) {
+    int base = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const bool a = e0 + lane < E && counts[e0 + lane] > 0;
+      const unsigned long long msk = __ballot(a);
+      if (a) act[base + __popcll(msk & ((1ull << lane) - 1ull))] = e0 + lane;
+      base += __popcll(msk);
+    }
+    if (lane == 0) nact = base;
+  }
+  __syncthreads();
+  const int na = nact;
+  if (na == 0) return;
+  const long long G = gridDim.x;
+  const int slot = (int)((long long)blockIdx.x * na / G);
+  const int first = (int)(((long long)slot * G + na - 1) / na);
+  const int next = (int)(((long long)(slot + 1) * G + na - 1) / na);
+  const int e = act[slot], bx = (int)blockIdx.x - first, gx = next - first;
   const int me = counts[e];
-  if (me == 0) return;
   const int off = offsets[e];
   const int nb = K / 256, niter = (nb + BPI - 1) / BPI;
-  const int lane = threadIdx.x & 63, l = lane & 3, g = lane >> 2;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int total = njobs * N;
-  const int row_step = gridDim.x * NW;
-  const int row0 = blockIdx.x * NW + wave;
+  const int row_step = gx * NW;
+  const int row0 = bx * NW + wave;
   const int nrows = row0 < total ? (total - 1 - row0) / row_step + 1 : 0;
   const int nslices = nrows * niter;
   const size_t rowb = (size_t)nb * FmtInfo<FMT>::kBodyBytes;
