@@ -76,9 +76,13 @@ __device__ __forceinline__ int act_chunk(int l, int k) {
   return FMT == kFmtQ4K ? 64 * l + 16 * k : 128 * (l >> 1) + 32 * (l & 1) + 64 * (k >> 1) + 16 * (k & 1);
 }
 
-// LDS position (16-byte slot) of chunk k of lane l in block b.
+// LDS position (16-byte slot) of chunk k of lane l in block b. Blocks are
+// 256 B apart, so without a swizzle the same (l, k) of every block falls on
+// the same banks; XOR-ing k with the block's low two bits spreads four
+// consecutive blocks (the 16 lanes of a ds_read_b128 pass over 64 banks), and
+// the lane-pair bit keeps lanes l and l + 2 apart within 128 B.
 __device__ __forceinline__ int kq_slot(int b, int l, int k) {
-  return 4 * l + (k ^ ((l >> 1) | ((b & 1) << 1)));
+  return 4 * l + (k ^ ((b & 3) ^ ((l >> 1) << 1)));
 }
 __device__ __forceinline__ int q80_slot(int b, int k) { return k ^ ((b >> 2) & 1); }
 
@@ -281,7 +285,7 @@ __device__ __forceinline__ void load_x(XSlice& x, const uint8_t* __restrict__ ld
     const uint32_t* lsum = reinterpret_cast<const uint32_t*>(lds + 256 * nblk);
     const float* ld = reinterpret_cast<const float*>(lsum + 8 * nblk);
     const uint8_t* e = lds + 256 * bx;
-    const int sw = (l >> 1) | ((bx & 1) << 1);
+    const int sw = (bx & 3) ^ ((l >> 1) << 1);  // kq_slot's swizzle
     x.x0 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (0 ^ sw)));
     x.x1 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (1 ^ sw)));
     x.x2 = *reinterpret_cast<const uint4*>(e + 16 * (4 * l + (2 ^ sw)));
