@@ -440,8 +440,10 @@ def kernel_only(torch, dev, which, launches):
     """Launch one kernel `launches` times, eagerly (every dispatch visible to a counter run):
     `gate` = the Q4_K gate GEMV (14336x4096, M = 1, rotated weight copies); `qkvgu` / `qkvgu_staged`
     = the q/k/v/gate/up set in one launch (Q8_K in the prologue / pre-quantized activation);
-    `copy` = a 256 MiB device copy (the calibration for FETCH_SIZE / WRITE_SIZE)."""
+    `copy` = a 256 MiB device copy (the calibration for FETCH_SIZE / WRITE_SIZE); `gemm_gate` / `gemm_down` =
+    the config-4 GEMMs (M = 512); `moe` = the config-5 expert FFN."""
     from inference_amd import GgmlDType, QTensor, qmm
+    from inference_amd.synth import normal
     if which == "copy":
         a = torch.ones(64 * 2 ** 20, dtype=torch.float32, device=dev)
         b = torch.empty_like(a)
@@ -450,6 +452,43 @@ def kernel_only(torch, dev, which, launches):
         torch.cuda.synchronize()
         print(json.dumps({"kernel_only": "copy", "bytes_read": a.numel() * 4, "bytes_written": b.numel() * 4,
                           "launches": launches}), flush=True)
+        return
+    if which in ("gemm_gate", "gemm_down"):
+        # config-4 GEMM: 512 rows N(0,1) seed 5 against a Q4_K weight N(0, 0.02^2) seed 6
+        n, k = (14336, 4096) if which == "gemm_gate" else (4096, 14336)
+        g = torch.Generator(device=dev)
+        g.manual_seed(6)
+        w = QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
+        x = torch.from_numpy(normal(5, (512, k))).to(dev)
+        y = torch.empty((512, n), dtype=torch.float32, device=dev)
+        L = qmm.lib()
+        wsb = int(L.qmm_matmul_workspace_size(w.handle, 512))
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        for _ in range(launches):
+            qmm._check(L.qmm_matmul(w.handle, x.data_ptr(), 512, k, y.data_ptr(), n, ws.data_ptr(), wsb,
+                                    qmm._stream(dev)))
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel_only": which, "int8_ops": 2 * 512 * n * k, "launches": launches}), flush=True)
+        return
+    if which == "moe":
+        # config 5: one qmm_moe_ffn call per launch (route, gather, expert GEMVs, SiLU*mul, combine)
+        E, H, F, T, k = 8, 4096, 14336, 8, 2
+        g = torch.Generator(device=dev)
+        g.manual_seed(7)
+        gate = QTensor.quantize(torch.randn((E * F, H), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
+        up = QTensor.quantize(torch.randn((E * F, H), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
+        down = QTensor.quantize(torch.randn((E * H, F), generator=g, device=dev) * 0.02, GgmlDType.Q6K)
+        x = torch.from_numpy(normal(7, (T, H))).to(dev)
+        lg = torch.from_numpy(normal(8, (T, E))).to(dev)
+        y = torch.empty((T, H), dtype=torch.float32, device=dev)
+        L = qmm.lib()
+        wsb = int(L.qmm_moe_ffn_workspace_size(gate.handle, down.handle, T, E, k))
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        for _ in range(launches):
+            qmm._check(L.qmm_moe_ffn(x.data_ptr(), T, H, lg.data_ptr(), E, k, gate.handle, up.handle, down.handle,
+                                     y.data_ptr(), H, ws.data_ptr(), wsb, qmm._stream(dev)))
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel_only": "moe", "launches": launches}), flush=True)
         return
     g = torch.Generator(device=dev)
     g.manual_seed(2)
@@ -512,7 +551,8 @@ def main():
                          "same two GEMV launches with Q8_K quantization in their prologues; serial: one launch "
                          "per projection")
     ap.add_argument("--decode-tokens", type=int, default=256, help="config-3 generated tokens (0 = skip)")
-    ap.add_argument("--kernel-only", choices=("gate", "qkvgu", "qkvgu_staged", "copy"), default=None,
+    ap.add_argument("--kernel-only", choices=("gate", "qkvgu", "qkvgu_staged", "copy", "gemm_gate", "gemm_down", "moe"),
+                    default=None,
                     help="launch only one GEMV launch kind or a calibration copy --steps times (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
