@@ -692,7 +692,7 @@ static GemmPlan gemm_plan(const Device* d, const qmm_qtensor* w, int64_t m, bool
       bn = b;
     }
   }
-  const unsigned lds2 = (unsigned)(2 * (bm * 272 + bn * 160 + bm * 4 + bm * 16));
+  const unsigned lds2 = (unsigned)(2 * (bm * 272 + bn * 144 + bm * 4 + bm * 16));
   // Q4_K: mmq2 (128x128 tiles, 8 waves, VALU sub-block scaling) when its grid
   // covers at least half the CUs (split-K fills the rest: 4096x14336 at
   // M = 512, 128 tiles x 2 splits: 120 us); below that (the prefill's
@@ -709,7 +709,7 @@ static GemmPlan gemm_plan(const Device* d, const qmm_qtensor* w, int64_t m, bool
     p.gx = (unsigned)((N + b4 - 1) / b4);
     p.gy = (unsigned)((M + 127) / 128);
     p.threads = 256;
-    p.lds = (unsigned)(2 * (128 * 272 + b4 * 160 + 128 * 4 + 128 * 16));
+    p.lds = (unsigned)(2 * (128 * 272 + b4 * 144 + 128 * 4 + 128 * 16));
   } else if (fmt == kFmtQ4K && (int)lds2 <= d->max_lds && getenv("QMM_MMQ1") == nullptr) {
     snprintf(p.name, sizeof(p.name), "qmm_mmq2_q4k_m%d_n%d%s", bm, bn, dump ? "_dump" : "");
     p.gx = (unsigned)((N + bn - 1) / bn);
@@ -1375,7 +1375,7 @@ int qmm_moe_gemm(const qmm_qtensor* const* w, int count, int experts, const floa
     if (const char* e = getenv("QMM_MOE_BM")) bm = atoi(e) == 64 ? 64 : 128;
   }
   const int bn = 128;
-  const unsigned lds = fmt == kFmtQ4K ? (unsigned)(2 * (bm * 272 + 128 * 160 + bm * 4 + bm * 16)) : 0u;
+  const unsigned lds = fmt == kFmtQ4K ? (unsigned)(2 * (bm * 272 + 128 * 144 + bm * 4 + bm * 16)) : 0u;
   char name[40];
   if (fmt == kFmtQ4K)
     snprintf(name, sizeof(name), "qmm_moe_mmq2_q4k%s", bm == 64 ? "_m64" : "");

@@ -540,7 +540,10 @@ extern "C" __global__ void __launch_bounds__(256) qmm_q8_blocks_to_planes(const 
 namespace qmm {
 
 constexpr int kM2AStride = 256 + 16;  // activation row in LDS (16-byte skew)
-constexpr int kM2BStride = 144 + 16;  // weight block in LDS
+// Weight blocks in LDS at their own 144 B (9 x 16 B): an odd number of
+// 16-byte units, so the 16 lanes of a ds_read_b128 pass (one block each) land
+// on 16 distinct 4-bank groups, and the staging stores are contiguous.
+constexpr int kM2BStride = 144;
 
 // NT = threads of the workgroup (mmq2: one wave per 64 x 32 outputs).
 template <int BM, int BN, int NT = 64 * (BM / 64) * (BN / 32)>
