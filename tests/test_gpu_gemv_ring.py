@@ -166,16 +166,20 @@ def _moe_gemv(qts, E, xq, P, counts, offsets, F):
 
 
 @pytest.mark.parametrize("dt,K", [(GgmlDType.Q4K, 4096), (GgmlDType.Q6K, 5120), (GgmlDType.Q4K, 5120)])
-@pytest.mark.parametrize("skew", [False, True])
+@pytest.mark.parametrize("skew", [False, True, "single"])
 def test_moe_ring_gemv_equals_generic(monkeypatch, dt, K, skew):
     """The expert ring GEMV (QMM_MOE_GEMV=P) against the generic M = 8 expert GEMV: bit-identical, including
-    experts with more than eight tokens (skew: every token routes to experts 0 and 1)."""
+    experts with more than eight tokens (skew: every token routes to experts 0 and 1) and one active expert
+    taking the whole grid (single: top-1 routing, every token to expert 3)."""
     from inference_amd import moe_route
-    E, F, T, k = 4, 768, 10, 2
-    rng = np.random.default_rng(K + int(skew))
+    E, F, T = 4, 768, 10
+    k = 1 if skew == "single" else 2
+    rng = np.random.default_rng(K + (2 if skew == "single" else int(skew)))
     qts = [QTensor.quantize(t((rng.standard_normal((E * F, K)) * 0.02).astype(np.float32)), dt) for _ in range(2)]
     logits = rng.standard_normal((T, E)).astype(np.float32)
-    if skew:
+    if skew == "single":
+        logits[:, 3] += 10.0
+    elif skew:
         logits[:, :2] += 10.0
     counts, offsets, ptok, pw, tp = moe_route(t(logits), k)
     P = T * k
@@ -188,5 +192,7 @@ def test_moe_ring_gemv_equals_generic(monkeypatch, dt, K, skew):
         got = _moe_gemv(qts, E, xq, P, counts, offsets, F)
         for a, b in zip(got, ref):
             assert torch.equal(a, b), f"P={p}"
-    if skew:
+    if skew == "single":
+        assert int(counts[3]) == T and int(counts.sum()) == T
+    elif skew:
         assert int(counts[0]) > 8
