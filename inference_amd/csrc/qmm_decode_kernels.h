@@ -509,15 +509,38 @@ extern "C" __global__ void __launch_bounds__(256) qmm_rms_norm(const float* __re
                                                                const float* __restrict__ w, float eps, int k,
                                                                float* __restrict__ out, long long ldo) {
 #pragma clang fp contract(off)
-  __shared__ float red[4];
+  // 256 threads (the launch's); each thread walks i = t, t + 256, ... with
+  // eight loads in flight per step (the order of its partial sum is the
+  // same as one element at a time)
+  constexpr int NT = 256, U = 8;
+  __shared__ float red[NT / 64];
   const float* xr = x + blockIdx.x * ldx;
   float ss = 0.0f;
-  for (int i = threadIdx.x; i < k; i += blockDim.x) ss += xr[i] * xr[i];
+  for (int i0 = threadIdx.x; i0 < k; i0 += U * NT) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = i0 + u * NT < k ? xr[i0 + u * NT] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) ss += v[u] * v[u];
+  }
   ss = qmm::wave_sum(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
   float t = 0.0f;
-  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) t += red[i];
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i) t += red[i];
   const float den = sqrtf(t / (float)k + eps);
-  for (int i = threadIdx.x; i < k; i += blockDim.x) out[blockIdx.x * ldo + i] = xr[i] / den * w[i];
+  float* orow = out + blockIdx.x * ldo;
+  for (int i0 = threadIdx.x; i0 < k; i0 += U * NT) {
+    float v[U], g[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * NT;
+      v[u] = i < k ? xr[i] : 0.0f;
+      g[u] = i < k ? w[i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i0 + u * NT < k) orow[i0 + u * NT] = v[u] / den * g[u];
+  }
 }
