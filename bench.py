@@ -111,7 +111,8 @@ def run_gemv_set(torch, dev, args):
     def gemv(layer, name):
         n, k = shapes[name]
         xq = xq4096 if k == 4096 else xq14336
-        qmm._check(L.qmm_matmul_q(layer[name].handle, xq.data_ptr(), 1, outs[name].data_ptr(), n, qmm._stream(dev)))
+        qmm._check(L.qmm_matmul_q(layer[name].handle, xq.data_ptr(), 1, outs[name].data_ptr(), n, None, 0,
+                                  qmm._stream(dev)))
 
     # job tables of the one-launch schedules (handles per weight copy)
     hs5 = [(vp * 5)(*[layer[nm].handle.value for nm in QKVGU]) for layer in sets]
@@ -128,7 +129,7 @@ def run_gemv_set(torch, dev, args):
             qmm._check(L.qmm_matmul_ex(hs5[c], 5, x4096.data_ptr(), 1, 4096, None, ctypes.c_float(0), 0, y5, ld5,
                                        None, 0, qmm._stream(dev)))
         else:
-            qmm._check(L.qmm_matmul_multi_q(hs5[c], 5, xq4096.data_ptr(), 1, y5, ld5, qmm._stream(dev)))
+            qmm._check(L.qmm_matmul_multi_q(hs5[c], 5, xq4096.data_ptr(), 1, y5, ld5, None, 0, qmm._stream(dev)))
 
     def down_fused(layer):
         c = cidx[id(layer)]
@@ -502,7 +503,8 @@ def kernel_only(torch, dev, which, launches):
               for _ in range(8)]
         y = torch.empty(14336, dtype=torch.float32, device=dev)
         for i in range(launches):
-            qmm._check(L.qmm_matmul_q(ws[i % 8].handle, xq.data_ptr(), 1, y.data_ptr(), 14336, qmm._stream(dev)))
+            qmm._check(L.qmm_matmul_q(ws[i % 8].handle, xq.data_ptr(), 1, y.data_ptr(), 14336, None, 0,
+                                      qmm._stream(dev)))
         alg = gemv_bytes(12, 14336, 4096)
     else:
         names = [nm for nm, _, _ in GEMV_SET if nm != "down_proj"]
@@ -518,7 +520,7 @@ def kernel_only(torch, dev, which, launches):
                 qmm._check(L.qmm_matmul_ex(hs[i % 6], 5, x.data_ptr(), 1, 4096, None, ctypes.c_float(0), 0, yp, ld,
                                            None, 0, qmm._stream(dev)))
             else:
-                qmm._check(L.qmm_matmul_multi_q(hs[i % 6], 5, xq.data_ptr(), 1, yp, ld, qmm._stream(dev)))
+                qmm._check(L.qmm_matmul_multi_q(hs[i % 6], 5, xq.data_ptr(), 1, yp, ld, None, 0, qmm._stream(dev)))
         alg = sum(gemv_bytes(12, *shp[nm]) for nm in names) - 4 * 4096 * (len(names) - 1)
     torch.cuda.synchronize()
     print(json.dumps({"kernel_only": which, "algorithmic_bytes": alg, "launches": launches}), flush=True)

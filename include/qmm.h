@@ -143,24 +143,35 @@ int qmm_matmul(const qmm_qtensor *w, const float *x, int64_t m, int64_t ldx, flo
 int qmm_matmul_multi(const qmm_qtensor *const *w, int count, const float *x, int64_t m, int64_t ldx,
                      float *const *y, const int64_t *ldy, void *ws, size_t ws_bytes, void *stream);
 
+/* Bytes of workspace the pre-quantized entry points below need for m
+ * activation rows: 0 for m <= 8 (the GEMV reads the GGML blocks as they are);
+ * for m > 8 the GEMM's activation planes plus, when the weight's output tiles
+ * cover fewer than half the CUs, f32 split-K partials. The workspace is the
+ * caller's: calls on different streams need different workspaces. */
+size_t qmm_matmul_q_workspace_size(const qmm_qtensor *w, int64_t m);
+
 /* The same with activations already quantized (xq: m rows of vec-dot blocks,
- * as produced by qmm_quantize_rows). For m > 8 the rows are rearranged for the
- * GEMM in a scratch buffer the library keeps per device (calls on one device
- * must then be ordered on one stream). */
-int qmm_matmul_q(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy, void *stream);
+ * as produced by qmm_quantize_rows). For m > 8 the rows are rearranged for
+ * the GEMM into `ws` (qmm_matmul_q_workspace_size(w, m) bytes; NULL allowed
+ * for m <= 8). A workspace smaller than the planes is an error; one that holds
+ * the planes but not the split-K partials runs the GEMM unsplit (same block
+ * dots, another f32 summation order). */
+int qmm_matmul_q(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy, void *ws, size_t ws_bytes,
+                 void *stream);
 
 /* qmm_matmul_multi with activations already quantized (xq as for
  * qmm_matmul_q): `count` (1..8) weights of one k in one launch for m <= 8
- * (one GEMM per weight for larger m). The weights share one dtype, or mix
- * Q4_K and Q6_K (both multiply Q8_K activations): one launch at m = 1, one
- * per dtype otherwise. */
+ * (one GEMM per weight for larger m, all using `ws`, sized as the largest
+ * qmm_matmul_q_workspace_size over the weights). The weights share one
+ * dtype, or mix Q4_K and Q6_K (both multiply Q8_K activations): one launch at
+ * m = 1, one per dtype otherwise. */
 int qmm_matmul_multi_q(const qmm_qtensor *const *w, int count, const void *xq, int64_t m, float *const *y,
-                       const int64_t *ldy, void *stream);
+                       const int64_t *ldy, void *ws, size_t ws_bytes, void *stream);
 
 /* qmm_matmul_q with an optional residual add (accumulate != 0: y += result;
  * then m <= 8). */
 int qmm_matmul_q_ex(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy, int accumulate,
-                    void *stream);
+                    void *ws, size_t ws_bytes, void *stream);
 
 /* Debug entry: exact int32 block dots of every (activation row, weight row,
  * super-block), computed by the same kernel that qmm_matmul_q runs (the GEMV
@@ -169,9 +180,9 @@ int qmm_matmul_q_ex(const qmm_qtensor *w, const void *xq, int64_t m, float *y, i
  * (isum_d = sum_j sc_j*sum q4*q8, isum_m = sum_j m_j*(bsum_2j + bsum_2j+1))
  * and per = 1 for Q6K (sum_j sc_j*sum (q6-32)*q8) and Q8_0 (sum qw*qx).
  * y receives the f32 outputs as qmm_matmul_q would. For m > 8, k must be a
- * multiple of 256. */
+ * multiple of 256 and ws holds qmm_matmul_q_workspace_size(w, m) bytes. */
 int qmm_block_dots(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy,
-                   int32_t *dots, void *stream);
+                   int32_t *dots, void *ws, size_t ws_bytes, void *stream);
 
 /* QMatMul::forward for 1..8 weights (same k; one dtype, or Q4_K and Q6_K
  * together as for qmm_matmul_multi_q, e.g. a Q4_K_M layer's q, k and v) on
@@ -193,9 +204,10 @@ size_t qmm_matmul_ex_workspace_size(const qmm_qtensor *w, int64_t m, int normali
 int qmm_rms_norm(const float *x, int64_t m, int64_t k, int64_t ldx, const float *w, float eps, float *out,
                  int64_t ldo, void *stream);
 
-/* x[0:hidden) = table[tokens[pos[0]]] (dense f32 embedding rows, row stride ld). */
-int qmm_embed_rows(const float *table, int64_t ld, const int32_t *tokens, const int32_t *pos, float *x,
-                   int64_t hidden, void *stream);
+/* x[0:hidden) = table[tokens[pos[0]]] (dense f32 embedding rows [vocab][ld]).
+ * A token id outside [0, vocab) reads no table row and writes a NaN row. */
+int qmm_embed_rows(const float *table, int64_t ld, int64_t vocab, const int32_t *tokens, const int32_t *pos,
+                   float *x, int64_t hidden, void *stream);
 
 /* In place NeoX RoPE of q [heads][head_dim] and k [kv_heads][head_dim] at
  * position pos[0] with cos/sin tables [max_seq][head_dim] (cat(freqs, freqs)),
@@ -234,9 +246,10 @@ int qmm_decode_rope_attention(const float *q, const float *k, const float *v, co
  * seq_len > 1 and the causal mask, llama.rs:410-433, 654-725; causal sdpa,
  * attention.rs:154-186). Rows are row-major with the given strides. */
 
-/* x[i] = table[tokens[first + i]] for i < count (CausalLm embed, llama.rs:397-408). */
-int qmm_embed_rows_n(const float *table, int64_t ld, const int32_t *tokens, int64_t first, int64_t count, float *x,
-                     int64_t hidden, void *stream);
+/* x[i] = table[tokens[first + i]] for i < count (CausalLm embed, llama.rs:397-408);
+ * token ids outside [0, vocab) give NaN rows as in qmm_embed_rows. */
+int qmm_embed_rows_n(const float *table, int64_t ld, int64_t vocab, const int32_t *tokens, int64_t first,
+                     int64_t count, float *x, int64_t hidden, void *stream);
 
 /* qmm_rope_kv_append for rows i < count at positions first + i: q and k
  * rows rotated in place, k and v written to the caches at those positions. */
@@ -273,7 +286,8 @@ int qmm_silu_mul_matmul(const qmm_qtensor *w, const float *g, const float *u, fl
 size_t qmm_greedy_workspace_size(int64_t n);
 
 /* Greedy step end on the device: tokens[pos+1] = argmax(logits) (lowest index
- * on ties, argmax_device, sampler.rs:216-219) unless pos+1 < prompt_len (the
+ * on ties, argmax_device, sampler.rs:216-219; a NaN counts as the largest
+ * value, the first NaN wins, as torch.argmax) unless pos+1 < prompt_len (the
  * slot still holds a prompt token); then pos[0] += 1. `capacity` is the
  * length of tokens (and of the KV cache): once pos+1 reaches it the call
  * writes nothing and pos stays, so a step replayed too often never writes

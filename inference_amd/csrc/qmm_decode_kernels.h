@@ -12,24 +12,32 @@
 #include "qmm_common.h"
 #include "qmm_quant_kernels.h"
 
+// Row `tok` of the embedding table into x[0 : hidden); a token id outside
+// [0, vocab) reads nothing and writes a NaN row, so the step's logits show it.
+namespace qmm {
+__device__ __forceinline__ void embed_row(const float* __restrict__ table, long long ld, int tok, int vocab,
+                                          float* __restrict__ x, int hidden) {
+  const bool ok = tok >= 0 && tok < vocab;
+  const float* row = table + (long long)(ok ? tok : 0) * ld;
+  for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < hidden; c += gridDim.x * blockDim.x)
+    x[c] = ok ? row[c] : __builtin_nanf("");
+}
+}  // namespace qmm
+
 // x[i][0 : hidden) = table[tokens[first + i]][0 : hidden) for i < gridDim.y
 // (the prompt rows of a batched prefill).
-extern "C" __global__ void qmm_prefill_embed(const float* __restrict__ table, long long ld,
+extern "C" __global__ void qmm_prefill_embed(const float* __restrict__ table, long long ld, int vocab,
                                              const int* __restrict__ tokens, int first, float* __restrict__ x,
                                              int hidden) {
   const int i = blockIdx.y;
-  const int tok = tokens[first + i];
-  for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < hidden; c += gridDim.x * blockDim.x)
-    x[(long long)i * hidden + c] = table[(long long)tok * ld + c];
+  qmm::embed_row(table, ld, tokens[first + i], vocab, x + (long long)i * hidden, hidden);
 }
 
 // x[0 : hidden) = table[tokens[pos[0]]][0 : hidden)
-extern "C" __global__ void qmm_decode_embed(const float* __restrict__ table, long long ld,
+extern "C" __global__ void qmm_decode_embed(const float* __restrict__ table, long long ld, int vocab,
                                             const int* __restrict__ tokens, const int* __restrict__ pos,
                                             float* __restrict__ x, int hidden) {
-  const int tok = tokens[pos[0]];
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x)
-    x[i] = table[(long long)tok * ld + i];
+  qmm::embed_row(table, ld, tokens[pos[0]], vocab, x, hidden);
 }
 
 // Rotates q (heads x dim) and k (kv_heads x dim) at position p = pos[0] with
@@ -444,8 +452,14 @@ extern "C" __global__ void __launch_bounds__(256) qmm_silu_mul_q8k(const float* 
 // in the workspace; the last one to finish (a counter it resets to zero)
 // reduces the slices in order and advances the step.
 namespace qmm {
+// (value, index) order of the reduction: NaN above every number (torch.argmax's
+// rule, so a NaN logit is reported rather than skipped), then the larger value,
+// then the lower index. Every element therefore claims its slot and the
+// result is always an index the reduction saw.
 __device__ __forceinline__ void argmax_merge(float& best, int& idx, float ov, int oi) {
-  if (ov > best || (ov == best && oi < idx)) {
+  const bool on = ov != ov, bn = best != best;
+  const bool take = on ? (!bn || oi < idx) : (!bn && (ov > best || (ov == best && oi < idx)));
+  if (take) {
     best = ov;
     idx = oi;
   }
@@ -496,7 +510,7 @@ extern "C" __global__ void __launch_bounds__(256) qmm_decode_argmax(const float*
   if (threadIdx.x == 0) {
     const int p = pos[0];
     if (p + 1 < capacity) {
-      if (p + 1 >= prompt) tokens[p + 1] = idx;
+      if (p + 1 >= prompt) tokens[p + 1] = idx < n ? idx : 0;  // n >= 1: some slice holds an element
       pos[0] = p + 1;
     }
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -236,10 +236,15 @@ int parse(qmm_gguf* g) {
     // a non-integer general.alignment keeps the default (as_u64 gives none)
   }
   if (g->alignment == 0) g->alignment = 1;
-  const uint64_t end = c.pos;
-  const uint64_t start = (end + g->alignment - 1) / g->alignment * g->alignment;
+  // data start = end of the tensor infos rounded up to the alignment, without
+  // wrapping: a rounding that would pass 2^64 (a huge general.alignment)
+  // lands past the end of any file
+  const uint64_t end = c.pos, rem = end % g->alignment;
+  const uint64_t pad = rem ? g->alignment - rem : 0;
+  const bool wraps = pad > UINT64_MAX - end;
+  const uint64_t start = wraps ? UINT64_MAX : end + pad;
   if (!g->tensors.empty() && start > g->size) return fail(QMM_ERR_INVALID, "gguf: data section starts past end of file");
-  g->data_start = (size_t)start;
+  g->data_start = (size_t)(start > g->size ? g->size : start);
   return QMM_OK;
 }
 
@@ -473,6 +478,8 @@ int qmm_gguf_load_qtensor(const qmm_gguf* g, int64_t i, int unpermute_heads, voi
   if (t.ndims != 2) return fail(QMM_ERR_UNSUPPORTED, "gguf: tensor \"%s\" is %d-D (resident loads take 2-D weights)",
                                 t.name.c_str(), t.ndims);
   const int64_t n = t.shape[0], k = t.shape[1];
+  if (n < 1 || k < 1) return fail(QMM_ERR_INVALID, "gguf: tensor \"%s\" has an empty dimension (%lld x %lld)",
+                                  t.name.c_str(), (long long)n, (long long)k);
   if (unpermute_heads <= 0) return qmm_qtensor_from_ggml(dtype, n, k, src, 0, stream, out);
   if (n % unpermute_heads) return fail(QMM_ERR_INVALID, "gguf: q/k permute: out %lld not divisible by n_head %d",
                                        (long long)n, unpermute_heads);

@@ -805,30 +805,6 @@ static int blocks_to_planes(Device* d, int wdtype, const void* xq, int64_t m, in
   return launch(d, "qmm_q8_blocks_to_planes", grid, 256, 0, s, args);
 }
 
-// Scratch owned by the library for the prequantized GEMM entry points
-// (qmm_matmul_q / qmm_block_dots with m > 8), grown on demand per device.
-static int scratch(size_t bytes, uint8_t** out) {
-  static std::mutex mu;
-  static void* buf[64] = {};
-  static size_t cap[64] = {};
-  int dev = 0;
-  QMM_HIP(hipGetDevice(&dev));
-  std::lock_guard<std::mutex> lk(mu);
-  if (cap[dev] < bytes) {
-    if (buf[dev]) {
-      QMM_HIP(hipDeviceSynchronize());
-      QMM_HIP(hipFree(buf[dev]));
-      buf[dev] = nullptr;
-      cap[dev] = 0;
-    }
-    hipError_t e = hipMalloc(&buf[dev], bytes);
-    if (e != hipSuccess) return fail(QMM_ERR_OOM, "hipMalloc(scratch %zu): %s", bytes, hipGetErrorString(e));
-    cap[dev] = bytes;
-  }
-  *out = (uint8_t*)buf[dev];
-  return QMM_OK;
-}
-
 static int check_matmul(const qmm_qtensor* w, int64_t m, const float* y, int64_t ldy) {
   if (!w || !y) return fail(QMM_ERR_INVALID, "null pointer");
   if (m <= 0) return fail(QMM_ERR_INVALID, "m = %lld must be positive", (long long)m);
@@ -840,19 +816,34 @@ static int check_matmul(const qmm_qtensor* w, int64_t m, const float* y, int64_t
   return QMM_OK;
 }
 
-int qmm_matmul_q(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int64_t ldy, void* stream) {
+size_t qmm_matmul_q_workspace_size(const qmm_qtensor* w, int64_t m) {
+  if (!w || m <= 0 || !use_gemm(w, m)) return 0;
+  return mmq_planes(w->dtype, m, w->k).total + gemm_split_bytes(w, m);
+}
+
+// m > 8 rows of GGML vec-dot blocks -> GEMM planes in the caller's
+// workspace, then the GEMM (dump != nullptr: the block-dot variant).
+static int gemm_from_blocks(Device* d, const qmm_qtensor* w, const void* xq, int64_t m, float* y, int64_t ldy,
+                            int* dump, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (!use_gemm(w, m)) return fail(QMM_ERR_UNSUPPORTED, "the GEMM path (m > 8) needs k %% 256 == 0");
+  const size_t pb = mmq_planes(w->dtype, m, w->k).total;
+  if (!ws || ws_bytes < pb)
+    return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed (qmm_matmul_q_workspace_size)", ws ? ws_bytes : 0,
+                qmm_matmul_q_workspace_size(w, m));
+  uint8_t* b = (uint8_t*)ws;
+  QMM_TRY(blocks_to_planes(d, w->dtype, xq, m, w->k, b, s));
+  // split-K partials in the rest (a plan that does not fit runs unsplit)
+  return gemm(d, w, b, m, y, ldy, dump, s, 0, (float*)(b + pb), ws_bytes - pb);
+}
+
+int qmm_matmul_q(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int64_t ldy, void* ws, size_t ws_bytes,
+                 void* stream) {
   QMM_TRY(check_matmul(w, m, y, ldy));
   if (!xq) return fail(QMM_ERR_INVALID, "null activation");
   Device* d;
   QMM_TRY(current_device(&d));
   const int vt = qmm_vec_dot_type(w->dtype);
-  if (use_gemm(w, m)) {
-    uint8_t* ws;
-    const size_t pb = mmq_planes(w->dtype, m, w->k).total, sb = gemm_split_bytes(w, m);
-    QMM_TRY(scratch(pb + sb, &ws));
-    QMM_TRY(blocks_to_planes(d, w->dtype, xq, m, w->k, ws, (hipStream_t)stream));
-    return gemm(d, w, ws, m, y, ldy, nullptr, (hipStream_t)stream, 0, (float*)(ws + pb), sb);
-  }
+  if (use_gemm(w, m)) return gemm_from_blocks(d, w, xq, m, y, ldy, nullptr, ws, ws_bytes, (hipStream_t)stream);
   const size_t xrow = (size_t)(w->k / qmm_block_size(vt)) * qmm_type_size(vt);
   // Rows are processed in groups of up to 8 by the GEMV.
   for (int64_t m0 = 0; m0 < m; m0 += 8) {
@@ -873,7 +864,7 @@ static bool same_act(const qmm_qtensor* a, const qmm_qtensor* b) {
 }
 
 int qmm_matmul_multi_q(const qmm_qtensor* const* w, int count, const void* xq, int64_t m, float* const* y,
-                       const int64_t* ldy, void* stream) {
+                       const int64_t* ldy, void* ws, size_t ws_bytes, void* stream) {
   if (!w || !y || !ldy || !xq || count < 1 || count > kMaxJobs)
     return fail(QMM_ERR_INVALID, "need 1..%d weights with outputs and an activation", kMaxJobs);
   GemvTarget tg[kMaxJobs];
@@ -883,7 +874,7 @@ int qmm_matmul_multi_q(const qmm_qtensor* const* w, int count, const void* xq, i
     tg[j] = {w[j], y[j], ldy[j]};
   }
   if (m > 8) {  // the GEMM runs one weight at a time
-    for (int j = 0; j < count; ++j) QMM_TRY(qmm_matmul_q(w[j], xq, m, y[j], ldy[j], stream));
+    for (int j = 0; j < count; ++j) QMM_TRY(qmm_matmul_q(w[j], xq, m, y[j], ldy[j], ws, ws_bytes, stream));
     return QMM_OK;
   }
   Device* d;
@@ -903,10 +894,10 @@ int qmm_silu_mul_matmul(const qmm_qtensor* w, const float* g, const float* u, fl
 }
 
 int qmm_matmul_q_ex(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int64_t ldy, int accumulate,
-                    void* stream) {
+                    void* ws, size_t ws_bytes, void* stream) {
   QMM_TRY(check_matmul(w, m, y, ldy));
   if (!xq) return fail(QMM_ERR_INVALID, "null activation");
-  if (!accumulate) return qmm_matmul_q(w, xq, m, y, ldy, stream);
+  if (!accumulate) return qmm_matmul_q(w, xq, m, y, ldy, ws, ws_bytes, stream);
   if (m > 8) return fail(QMM_ERR_UNSUPPORTED, "accumulating prequantized matmul is limited to m <= 8");
   Device* d;
   QMM_TRY(current_device(&d));
@@ -1029,14 +1020,15 @@ int qmm_rms_norm(const float* x, int64_t m, int64_t k, int64_t ldx, const float*
   return launch(d, "qmm_rms_norm", (unsigned)m, 256, 0, (hipStream_t)stream, args);
 }
 
-int qmm_embed_rows(const float* table, int64_t ld, const int32_t* tokens, const int32_t* pos, float* x,
+int qmm_embed_rows(const float* table, int64_t ld, int64_t vocab, const int32_t* tokens, const int32_t* pos, float* x,
                    int64_t hidden, void* stream) {
-  if (!table || !tokens || !pos || !x || hidden < 1 || ld < hidden) return fail(QMM_ERR_INVALID, "bad embed arguments");
+  if (!table || !tokens || !pos || !x || hidden < 1 || ld < hidden || vocab < 1 || vocab > (1LL << 31) - 1)
+    return fail(QMM_ERR_INVALID, "bad embed arguments");
   Device* d;
   QMM_TRY(current_device(&d));
   long long l = ld;
-  int h = (int)hidden;
-  void* args[] = {&table, &l, &tokens, &pos, &x, &h};
+  int h = (int)hidden, v = (int)vocab;
+  void* args[] = {&table, &l, &v, &tokens, &pos, &x, &h};
   return launch(d, "qmm_decode_embed", ceil_div(hidden, 256), 256, 0, (hipStream_t)stream, args);
 }
 
@@ -1120,16 +1112,17 @@ int qmm_decode_rope_attention(const float* q, const float* k, const float* v, co
 // batched prefill (the prompt's rows through one pass per layer)
 // ---------------------------------------------------------------------------
 
-int qmm_embed_rows_n(const float* table, int64_t ld, const int32_t* tokens, int64_t first, int64_t count, float* x,
-                     int64_t hidden, void* stream) {
-  if (!table || !tokens || !x || hidden < 1 || ld < hidden || first < 0 || count < 0 || count > 65535)
+int qmm_embed_rows_n(const float* table, int64_t ld, int64_t vocab, const int32_t* tokens, int64_t first,
+                     int64_t count, float* x, int64_t hidden, void* stream) {
+  if (!table || !tokens || !x || hidden < 1 || ld < hidden || first < 0 || count < 0 || count > 65535 ||
+      first + count > (1LL << 31) - 1 || vocab < 1 || vocab > (1LL << 31) - 1)
     return fail(QMM_ERR_INVALID, "bad embed arguments");
   if (count == 0) return QMM_OK;
   Device* d;
   QMM_TRY(current_device(&d));
   long long l = ld;
-  int h = (int)hidden, f = (int)first;
-  void* args[] = {&table, &l, &tokens, &f, &x, &h};
+  int h = (int)hidden, f = (int)first, v = (int)vocab;
+  void* args[] = {&table, &l, &v, &tokens, &f, &x, &h};
   hipFunction_t fn;
   QMM_TRY(kernel(d, "qmm_prefill_embed", &fn));
   QMM_HIP(hipModuleLaunchKernel(fn, std::min(ceil_div(hidden, 256), 64u), (unsigned)count, 1, 256, 1, 1, 0,
@@ -1233,20 +1226,13 @@ int qmm_greedy_advance(const float* logits, int64_t n, int32_t* tokens, int64_t 
   return launch(d, "qmm_decode_argmax", kArgmaxBlocks, 256, 0, (hipStream_t)stream, args);
 }
 
-int qmm_block_dots(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int64_t ldy, int32_t* dots,
-                   void* stream) {
+int qmm_block_dots(const qmm_qtensor* w, const void* xq, int64_t m, float* y, int64_t ldy, int32_t* dots, void* ws,
+                   size_t ws_bytes, void* stream) {
   QMM_TRY(check_matmul(w, m, y, ldy));
   if (!xq || !dots) return fail(QMM_ERR_INVALID, "null pointer");
   Device* d;
   QMM_TRY(current_device(&d));
-  if (m > 8) {
-    if (!use_gemm(w, m)) return fail(QMM_ERR_UNSUPPORTED, "block dots for m > 8 need k %% 256 == 0");
-    uint8_t* ws;
-    const size_t pb = mmq_planes(w->dtype, m, w->k).total, sb = gemm_split_bytes(w, m);
-    QMM_TRY(scratch(pb + sb, &ws));
-    QMM_TRY(blocks_to_planes(d, w->dtype, xq, m, w->k, ws, (hipStream_t)stream));
-    return gemm(d, w, ws, m, y, ldy, dots, (hipStream_t)stream, 0, (float*)(ws + pb), sb);
-  }
+  if (m > 8) return gemm_from_blocks(d, w, xq, m, y, ldy, dots, ws, ws_bytes, (hipStream_t)stream);
   GemvTarget t = {w, y, ldy};
   return gemv(d, &t, 1, xq, false, 0, (int)m, dots, (hipStream_t)stream);
 }

@@ -290,7 +290,7 @@ class DecodeSession:
         eps = ctypes.c_float(cfg.eps)
         hd, H = cfg.head_dim, cfg.hidden
         tr = trace if trace is not None else (lambda op, li: None)
-        qmm._check(L.qmm_embed_rows(w.embed.data_ptr(), H, self.tokens.data_ptr(), self.pos.data_ptr(),
+        qmm._check(L.qmm_embed_rows(w.embed.data_ptr(), H, cfg.vocab, self.tokens.data_ptr(), self.pos.data_ptr(),
                                     self.x.data_ptr(), H, s))
         tr("embed", -1)
         kv_stride = cfg.kv_heads * self.max_seq * hd
@@ -319,7 +319,7 @@ class DecodeSession:
                                                self.hq.data_ptr(), s))
             tr("silu_mul", li)
             qmm._check(L.qmm_matmul_q_ex(w.layers[li]["down"].handle, self.hq.data_ptr(), 1, self.x.data_ptr(), H,
-                                         1, s))
+                                         1, None, 0, s))
             tr("down", li)
         qmm._check(L.qmm_matmul_ex(self._head, 1, self.x.data_ptr(), 1, H, w.final_norm.data_ptr(), eps, 0,
                                    self._lg_y, self._lg_ld, None, 0, s))
@@ -367,7 +367,8 @@ class DecodeSession:
         x_y, x_ld = (vp * 1)(x.data_ptr()), (i64 * 1)(H)
         gu_y, gu_ld = (vp * 2)(g.data_ptr(), u.data_ptr()), (i64 * 2)(F, F)
         kv_stride = cfg.kv_heads * self.max_seq * hd
-        qmm._check(L.qmm_embed_rows_n(w.embed.data_ptr(), H, self.tokens.data_ptr(), 0, rows, x.data_ptr(), H, s))
+        qmm._check(L.qmm_embed_rows_n(w.embed.data_ptr(), H, cfg.vocab, self.tokens.data_ptr(), 0, rows, x.data_ptr(),
+                                      H, s))
         for li in range(cfg.layers):
             lw = w.layers[li]
             qmm._check(L.qmm_matmul_ex(self._qkv[li], 3, x.data_ptr(), rows, H, w.attn_norm[li].data_ptr(), eps, 0,

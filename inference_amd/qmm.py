@@ -58,7 +58,7 @@ EXPORTS = (
     "qmm_gguf_tensor_info", "qmm_gguf_type_size", "qmm_gguf_tensor_data", "qmm_gguf_meta_info",
     "qmm_gguf_meta_u64", "qmm_gguf_meta_i64", "qmm_gguf_meta_f64", "qmm_gguf_meta_string",
     "qmm_gguf_load_qtensor", "qmm_qtensor_dequantize_to", "qmm_embed_rows_n", "qmm_rope_kv_append_n",
-    "qmm_prefill_attention", "qmm_silu_mul",
+    "qmm_prefill_attention", "qmm_silu_mul", "qmm_matmul_q_workspace_size",
 )
 
 
@@ -92,10 +92,11 @@ def lib() -> ctypes.CDLL:
             "qmm_quantize_rows": ([i32, vp, i64, i64, i64, vp, vp], i32),
             "qmm_matmul_workspace_size": ([vp, i64], sz),
             "qmm_matmul": ([vp, vp, i64, i64, vp, i64, vp, sz, vp], i32),
-            "qmm_matmul_q": ([vp, vp, i64, vp, i64, vp], i32),
+            "qmm_matmul_q": ([vp, vp, i64, vp, i64, vp, sz, vp], i32),
+            "qmm_matmul_q_workspace_size": ([vp, i64], sz),
             "qmm_matmul_multi": ([ctypes.POINTER(vp), i32, vp, i64, i64, ctypes.POINTER(vp),
                                   ctypes.POINTER(i64), vp, sz, vp], i32),
-            "qmm_block_dots": ([vp, vp, i64, vp, i64, vp, vp], i32),
+            "qmm_block_dots": ([vp, vp, i64, vp, i64, vp, vp, sz, vp], i32),
             "qmm_moe_route": ([vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, vp], i32),
             "qmm_moe_gemv": ([ctypes.POINTER(vp), i32, i32, vp, i64, vp, vp, ctypes.POINTER(vp), vp], i32),
             "qmm_moe_gemm_workspace_size": ([vp, i64], ctypes.c_size_t),
@@ -107,7 +108,7 @@ def lib() -> ctypes.CDLL:
                                ctypes.POINTER(i64), vp, sz, vp], i32),
             "qmm_matmul_ex_workspace_size": ([vp, i64, i32], sz),
             "qmm_rms_norm": ([vp, i64, i64, i64, vp, ctypes.c_float, vp, i64, vp], i32),
-            "qmm_embed_rows": ([vp, i64, vp, vp, vp, i64, vp], i32),
+            "qmm_embed_rows": ([vp, i64, i64, vp, vp, vp, i64, vp], i32),
             "qmm_rope_kv_append": ([vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp], i32),
             "qmm_decode_attention": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp, sz, vp], i32),
             "qmm_decode_rope_attention": ([vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float,
@@ -116,10 +117,10 @@ def lib() -> ctypes.CDLL:
             "qmm_greedy_workspace_size": ([i64], sz),
             "qmm_silu_mul_quantize": ([vp, vp, i64, i64, i64, vp, vp], i32),
             "qmm_greedy_advance": ([vp, i64, vp, i64, vp, i32, vp, sz, vp], i32),
-            "qmm_matmul_q_ex": ([vp, vp, i64, vp, i64, i32, vp], i32),
+            "qmm_matmul_q_ex": ([vp, vp, i64, vp, i64, i32, vp, sz, vp], i32),
             "qmm_silu_mul_matmul": ([vp, vp, vp, vp, i32, vp], i32),
-            "qmm_matmul_multi_q": ([ctypes.POINTER(vp), i32, vp, i64, ctypes.POINTER(vp), ctypes.POINTER(i64), vp],
-                                   i32),
+            "qmm_matmul_multi_q": ([ctypes.POINTER(vp), i32, vp, i64, ctypes.POINTER(vp), ctypes.POINTER(i64), vp,
+                                    sz, vp], i32),
             "qmm_gguf_open": ([ctypes.c_char_p, pp], i32),
             "qmm_gguf_open_memory": ([ctypes.c_char_p, sz, pp], i32),
             "qmm_gguf_close": ([vp], None),
@@ -141,7 +142,7 @@ def lib() -> ctypes.CDLL:
             "qmm_gguf_meta_string": ([vp, i64, i64, pp, ctypes.POINTER(ctypes.c_uint64)], i32),
             "qmm_gguf_load_qtensor": ([vp, i64, i32, vp, pp], i32),
             "qmm_qtensor_dequantize_to": ([vp, vp, i32, vp], i32),
-            "qmm_embed_rows_n": ([vp, i64, vp, i64, i64, vp, i64, vp], i32),
+            "qmm_embed_rows_n": ([vp, i64, i64, vp, i64, i64, vp, i64, vp], i32),
             "qmm_rope_kv_append_n": ([vp, vp, vp, i64, i64, i64, vp, vp, i64, i64, vp, vp, i32, i32, i32, i32, vp],
                                      i32),
             "qmm_prefill_attention": ([vp, i64, vp, vp, i64, i64, vp, i64, i32, i32, i32, i32, ctypes.c_float, vp],
@@ -439,12 +440,27 @@ def matmul_multi(qts: Sequence[QTensor], x: torch.Tensor) -> Tuple[torch.Tensor,
     return tuple(y.reshape(*x.shape[:-1], y.shape[1]) for y in ys)
 
 
+def q_workspace(qts: Sequence[QTensor], m: int) -> Tuple[Optional[torch.Tensor], int]:
+    """A device workspace for the pre-quantized entry points (None when m <= 8)."""
+    L = lib()
+    nbytes = max(int(L.qmm_matmul_q_workspace_size(q.handle, m)) for q in qts)
+    if nbytes == 0:
+        return None, 0
+    return torch.empty(nbytes, dtype=torch.uint8, device=qts[0].device), nbytes
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
 def matmul_q(qt: QTensor, xq: torch.Tensor, m: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y[m, n] from pre-quantized activations (uint8 GGML vec-dot blocks on the GPU)."""
     n = qt.shape[0]
     y = out if out is not None else torch.empty((m, n), dtype=torch.float32, device=qt.device)
+    ws, nbytes = q_workspace([qt], m)
     with torch.cuda.device(qt.device):
-        _check(lib().qmm_matmul_q(qt.handle, xq.data_ptr(), m, y.data_ptr(), y.stride(0), _stream(qt.device)))
+        _check(lib().qmm_matmul_q(qt.handle, xq.data_ptr(), m, y.data_ptr(), y.stride(0), _ptr(ws), nbytes,
+                                  _stream(qt.device)))
     return y
 
 
@@ -455,8 +471,9 @@ def block_dots(qt: QTensor, xq: torch.Tensor, m: int) -> Tuple[torch.Tensor, tor
     per = 2 if qt.dtype() == GgmlDType.Q4K else 1
     dots = torch.zeros((m, n, nb, per), dtype=torch.int32, device=qt.device)
     y = torch.empty((m, n), dtype=torch.float32, device=qt.device)
+    ws, nbytes = q_workspace([qt], m)
     with torch.cuda.device(qt.device):
-        _check(lib().qmm_block_dots(qt.handle, xq.data_ptr(), m, y.data_ptr(), n, dots.data_ptr(),
+        _check(lib().qmm_block_dots(qt.handle, xq.data_ptr(), m, y.data_ptr(), n, dots.data_ptr(), _ptr(ws), nbytes,
                                     _stream(qt.device)))
     return (dots if per == 2 else dots[..., 0]), y
 

@@ -232,3 +232,27 @@ def test_errors():
     # metadata-only files may end before the aligned data boundary
     assert GgufFile.parse(W.build([("x", W.T_UINT8, 1)], [])[:-1] if len(W.build([("x", W.T_UINT8, 1)], [])) % 32
                           else W.build([("x", W.T_UINT8, 1)], [])).meta_u64("x") == 1
+
+
+def test_huge_alignment_is_rejected_not_wrapped():
+    # general.alignment near 2^64: rounding the data start up must not wrap to
+    # a small offset (the reference's div_ceil rejects such a file as a data
+    # section past the end of the file)
+    for a in (2 ** 64 - 1, 2 ** 63 + 1, 1 << 40):
+        img = W.build([("general.alignment", W.T_UINT64, a)], [("t", (256,), 12, bytes(144))])
+        with pytest.raises(qmm.QmmError) as e:
+            GgufFile.parse(img)
+        assert "past end of file" in str(e.value)
+
+
+def test_resident_load_rejects_an_empty_dimension_before_any_device_work():
+    # a 0 x 256 Q4_K tensor with a q/k un-permute: refused by the shape check
+    # (the per-row byte count would otherwise divide by zero)
+    import ctypes
+    img = W.build([], [("t", (0, 256), 12, b"")])
+    g = GgufFile.parse(img)
+    out = ctypes.c_void_p()
+    for heads in (0, 4):
+        rc = qmm.lib().qmm_gguf_load_qtensor(g.handle, 0, heads, None, ctypes.byref(out))
+        assert rc == qmm.QMM_ERR_INVALID and "empty dimension" in qmm.last_error()
+        assert not out.value

@@ -111,10 +111,10 @@ def test_matmul_multi_q_mixed_q4k_q6k(m):
     vp, i64 = ctypes.c_void_p, ctypes.c_int64
     ys = [torch.full((m, n), float("nan"), device=DEV) for n in rows]
     qmm._check(L().qmm_matmul_multi_q((vp * 3)(*[q.handle.value for q in qts]), 3, xq.data_ptr(), m,
-                                      (vp * 3)(*[y.data_ptr() for y in ys]), (i64 * 3)(*rows), S()))
+                                      (vp * 3)(*[y.data_ptr() for y in ys]), (i64 * 3)(*rows), None, 0, S()))
     for q, n, y in zip(qts, rows, ys):
         want = torch.full((m, n), float("nan"), device=DEV)
-        qmm._check(L().qmm_matmul_q(q.handle, xq.data_ptr(), m, want.data_ptr(), n, S()))
+        qmm._check(L().qmm_matmul_q(q.handle, xq.data_ptr(), m, want.data_ptr(), n, None, 0, S()))
         assert torch.equal(y, want)
 
 
@@ -161,7 +161,7 @@ def test_matmul_q_ex_accumulate():
     y0 = rng.standard_normal((1, n)).astype(np.float32)
     y = t(y0)
     xqd = t(xq, torch.uint8)
-    qmm._check(L().qmm_matmul_q_ex(qt.handle, xqd.data_ptr(), 1, y.data_ptr(), n, 1, S()))
+    qmm._check(L().qmm_matmul_q_ex(qt.handle, xqd.data_ptr(), 1, y.data_ptr(), n, 1, None, 0, S()))
     prod = orc.matmul_prequant(orc.Q6K, xq, qt.to_ggml(), k)
     assert rel_err(y.cpu().numpy() - y0, prod) <= 1e-3
 
@@ -169,13 +169,27 @@ def test_matmul_q_ex_accumulate():
 def test_embed_rows():
     rng = np.random.default_rng(40)
     table = rng.standard_normal((50, 96)).astype(np.float32)
-    toks = t(np.array([7, 3, 41, 0], np.int32), torch.int32)
+    ids = [7, 3, 41, 0, 50, -1, 2 ** 31 - 1]
+    toks = t(np.array(ids, np.int32), torch.int32)
     td = t(table)
-    for p in range(4):
+    for p, tok in enumerate(ids):
         pos = t(np.array([p], np.int32), torch.int32)
         x = torch.zeros(96, device=DEV)
-        qmm._check(L().qmm_embed_rows(td.data_ptr(), 96, toks.data_ptr(), pos.data_ptr(), x.data_ptr(), 96, S()))
-        np.testing.assert_array_equal(x.cpu().numpy(), table[[7, 3, 41, 0][p]])
+        qmm._check(L().qmm_embed_rows(td.data_ptr(), 96, 50, toks.data_ptr(), pos.data_ptr(), x.data_ptr(), 96,
+                                      S()))
+        if 0 <= tok < 50:
+            np.testing.assert_array_equal(x.cpu().numpy(), table[tok])
+        else:  # outside the vocabulary: no table read, a NaN row
+            assert torch.isnan(x).all()
+    # the batched gather: the same rule per row
+    xs = torch.zeros((len(ids), 96), device=DEV)
+    qmm._check(L().qmm_embed_rows_n(td.data_ptr(), 96, 50, toks.data_ptr(), 0, len(ids), xs.data_ptr(), 96, S()))
+    got = xs.cpu().numpy()
+    for i, tok in enumerate(ids):
+        if 0 <= tok < 50:
+            np.testing.assert_array_equal(got[i], table[tok])
+        else:
+            assert np.isnan(got[i]).all()
 
 
 @pytest.mark.parametrize("heads,kv_heads,hd", [(32, 8, 128), (8, 2, 64), (4, 1, 128)])
@@ -319,7 +333,7 @@ def test_silu_mul_matmul_equals_two_calls(dt, n, k, accumulate):
     ya, yb = t(y0), t(y0)
     hq = torch.zeros(k // 256 * 292, dtype=torch.uint8, device=DEV)
     qmm._check(L().qmm_silu_mul_quantize(g.data_ptr(), u.data_ptr(), 1, k, k, hq.data_ptr(), S()))
-    qmm._check(L().qmm_matmul_q_ex(qt.handle, hq.data_ptr(), 1, ya.data_ptr(), n, accumulate, S()))
+    qmm._check(L().qmm_matmul_q_ex(qt.handle, hq.data_ptr(), 1, ya.data_ptr(), n, accumulate, None, 0, S()))
     qmm._check(L().qmm_silu_mul_matmul(qt.handle, g.data_ptr(), u.data_ptr(), yb.data_ptr(), accumulate, S()))
     torch.cuda.synchronize()
     assert torch.equal(ya, yb)
@@ -368,6 +382,18 @@ def test_greedy_advance():
         pos.zero_()
         adv(1, n=128256)
         assert toks[1].item() == win
+    assert not ws[:256].any()
+    # NaN logits count as the largest value (the first NaN wins, torch.argmax's
+    # rule): the written token is always an index of the logits
+    for nan_at in ([], [77], [70000, 5]):
+        big = np.full(128256, np.nan if not nan_at else 0.0, np.float32)
+        for i in nan_at:
+            big[i] = np.nan
+        logits = t(big)
+        pos.zero_()
+        adv(1, n=128256)
+        assert toks[1].item() == (min(nan_at) if nan_at else 0)
+        assert int(torch.argmax(logits).item()) == toks[1].item()
     assert not ws[:256].any()
     with pytest.raises(qmm.QmmError):
         qmm._check(L().qmm_greedy_advance(logits.data_ptr(), 5, toks.data_ptr(), 6, pos.data_ptr(), 1,

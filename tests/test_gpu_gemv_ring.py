@@ -60,7 +60,8 @@ def run_multi_q(qts, xq):
     rows = [qt_rows(q) for q in qts]
     ys = [torch.full((1, n), float("nan"), device=DEV) for n in rows]
     qmm._check(L().qmm_matmul_multi_q((vp * len(qts))(*[q.handle.value for q in qts]), len(qts), xq.data_ptr(), 1,
-                                      (vp * len(qts))(*[y.data_ptr() for y in ys]), (i64 * len(qts))(*rows), S()))
+                                      (vp * len(qts))(*[y.data_ptr() for y in ys]), (i64 * len(qts))(*rows), None, 0,
+                                      S()))
     torch.cuda.synchronize()
     return ys
 

@@ -330,10 +330,11 @@ def test_matmul_multi_eight_jobs(dt, m, count):
     ys = matmul_multi(qts, x)
     xq = quantize_rows(dt.vec_dot_type(), x)
     yq = [torch.empty((m, n), dtype=torch.float32, device=DEV) for n in rows]
+    ws, ws_bytes = qmm.q_workspace(qts, m)
     vp, i64 = ctypes.c_void_p, ctypes.c_int64
     qmm._check(qmm.lib().qmm_matmul_multi_q((vp * count)(*[q.handle.value for q in qts]), count, xq.data_ptr(), m,
                                             (vp * count)(*[y.data_ptr() for y in yq]), (i64 * count)(*rows),
-                                            qmm._stream(DEV)))
+                                            qmm._ptr(ws), ws_bytes, qmm._stream(DEV)))
     for q, y, y2 in zip(qts, ys, yq):
         ref = QMatMul.from_qtensor(q).forward(x)
         assert torch.equal(y, ref)
