@@ -130,6 +130,20 @@ size_t qmm_matmul_workspace_size(const qmm_qtensor *w, int64_t m);
 int qmm_matmul(const qmm_qtensor *w, const float *x, int64_t m, int64_t ldx, float *y, int64_t ldy,
                void *ws, size_t ws_bytes, void *stream);
 
+/* qmm_matmul without a caller workspace, for callers that cannot allocate
+ * (code under stream capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference: its launchers take caller
+ * buffers or allocate their own (moe_gguf.cu:172-174). The workspace is a
+ * library-held device array of QMM_NOALLOC_SCRATCH_BYTES per GPU, resolved at
+ * set-up (qmm_init(device), else the first call on a device); the call itself
+ * allocates nothing. Calls whose qmm_matmul_workspace_size(w, m) exceeds it
+ * fail with QMM_ERR_INVALID. All calls on one GPU share the array: calls that
+ * overlap on one GPU (other streams, other threads) race, so order them on
+ * one stream. Results equal qmm_matmul's with a workspace of that size. */
+#define QMM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int qmm_matmul_noalloc(const qmm_qtensor *w, const float *x, int64_t m, int64_t ldx, float *y, int64_t ldy,
+                       void *stream);
+
 /* `count` (1..8) QMatMul::forward calls on one input in a single launch:
  * y[j] = x . W[j]^T for weights of one dtype and k (e.g. a layer's q/k/v and
  * gate/up projections, which the reference engine runs as separate

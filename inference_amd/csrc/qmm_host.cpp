@@ -166,12 +166,17 @@ extern "C" {
 
 const char* qmm_last_error(void) { return g_err.c_str(); }
 
+// qmm_noalloc.hip: resolves the allocation-free entry point's device scratch
+// on the current device (set-up, once per device).
+__attribute__((visibility("hidden"))) int qmm_internal_noalloc_setup(void** out);
+
 int qmm_init(int device) {
   int prev = 0;
   QMM_HIP(hipGetDevice(&prev));
   QMM_HIP(hipSetDevice(device));
   Device* d;
   int rc = current_device(&d);
+  if (rc == QMM_OK) rc = qmm_internal_noalloc_setup(nullptr);
   (void)hipSetDevice(prev);
   return rc;
 }

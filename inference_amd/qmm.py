@@ -58,7 +58,7 @@ EXPORTS = (
     "qmm_gguf_tensor_info", "qmm_gguf_type_size", "qmm_gguf_tensor_data", "qmm_gguf_meta_info",
     "qmm_gguf_meta_u64", "qmm_gguf_meta_i64", "qmm_gguf_meta_f64", "qmm_gguf_meta_string",
     "qmm_gguf_load_qtensor", "qmm_qtensor_dequantize_to", "qmm_embed_rows_n", "qmm_rope_kv_append_n",
-    "qmm_prefill_attention", "qmm_silu_mul", "qmm_matmul_q_workspace_size",
+    "qmm_prefill_attention", "qmm_silu_mul", "qmm_matmul_q_workspace_size", "qmm_matmul_noalloc",
 )
 
 
@@ -94,6 +94,7 @@ def lib() -> ctypes.CDLL:
             "qmm_matmul": ([vp, vp, i64, i64, vp, i64, vp, sz, vp], i32),
             "qmm_matmul_q": ([vp, vp, i64, vp, i64, vp, sz, vp], i32),
             "qmm_matmul_q_workspace_size": ([vp, i64], sz),
+            "qmm_matmul_noalloc": ([vp, vp, i64, i64, vp, i64, vp], i32),
             "qmm_matmul_multi": ([ctypes.POINTER(vp), i32, vp, i64, i64, ctypes.POINTER(vp),
                                   ctypes.POINTER(i64), vp, sz, vp], i32),
             "qmm_block_dots": ([vp, vp, i64, vp, i64, vp, vp, sz, vp], i32),
