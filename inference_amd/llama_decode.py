@@ -330,13 +330,17 @@ class DecodeSession:
         tr("argmax", -1)
 
     # -- batched prefill -----------------------------------------------------
-    def prefill(self) -> int:
+    def prefill(self, trace: Optional[Callable[[str, int, Dict[str, torch.Tensor]], None]] = None) -> int:
         """Run the prompt's positions 0 .. prompt_len - 2 in one pass per layer (matmuls with m = rows on
         the MFMA GEMM path, batched RoPE + KV append, causal attention over the prompt), then leave the
         session at position prompt_len - 1, where the captured step takes over: it processes the last
         prompt token and produces the first generated one. Same operations and order per row as the
         token-by-token steps, so the KV cache and the following logits match them to f32 accumulation
-        order. Returns the number of rows run. Call right after reset()."""
+        order. Returns the number of rows run. Call right after reset().
+
+        `trace(op, layer, bufs)`, when given, is called after each launch is enqueued (ops: embed, qkv,
+        rope_kv, attention, o, gate_up, silu_mul, down); `bufs` holds the pass's row buffers (x, q, k, v,
+        att, g, u, h), so a checker can read them between launches."""
         if self.prompt_len == 0 or self.steps_done != 0:
             raise qmm.QmmError(1, "prefill() needs the state reset() leaves")
         cfg, L, w = self.cfg, self.L, self.w
@@ -367,26 +371,36 @@ class DecodeSession:
         x_y, x_ld = (vp * 1)(x.data_ptr()), (i64 * 1)(H)
         gu_y, gu_ld = (vp * 2)(g.data_ptr(), u.data_ptr()), (i64 * 2)(F, F)
         kv_stride = cfg.kv_heads * self.max_seq * hd
+        bufs = {"x": x, "q": q, "k": k, "v": v, "att": att, "g": g, "u": u, "h": hh}
+        tr = (lambda op, li: trace(op, li, bufs)) if trace is not None else (lambda op, li: None)
         qmm._check(L.qmm_embed_rows_n(w.embed.data_ptr(), H, cfg.vocab, self.tokens.data_ptr(), 0, rows, x.data_ptr(),
                                       H, s))
+        tr("embed", -1)
         for li in range(cfg.layers):
             lw = w.layers[li]
             qmm._check(L.qmm_matmul_ex(self._qkv[li], 3, x.data_ptr(), rows, H, w.attn_norm[li].data_ptr(), eps, 0,
                                        qkv_y, qkv_ld, ws.data_ptr(), ws.numel(), s))
+            tr("qkv", li)
             kc = self.kcache.data_ptr() + 4 * li * kv_stride
             vc = self.vcache.data_ptr() + 4 * li * kv_stride
             qmm._check(L.qmm_rope_kv_append_n(q.data_ptr(), k.data_ptr(), v.data_ptr(), nq, nkv, nkv,
                                               self.cos.data_ptr(), self.sin.data_ptr(), 0, rows, kc, vc, cfg.heads,
                                               cfg.kv_heads, hd, self.max_seq, s))
+            tr("rope_kv", li)
             qmm._check(L.qmm_prefill_attention(q.data_ptr(), nq, kc, vc, 0, rows, att.data_ptr(), nq, cfg.heads,
                                                cfg.kv_heads, hd, self.max_seq, ctypes.c_float(self.scale), s))
+            tr("attention", li)
             qmm._check(L.qmm_matmul_ex((vp * 1)(lw["o"].handle.value), 1, att.data_ptr(), rows, nq, None, eps, 1,
                                        x_y, x_ld, ws.data_ptr(), ws.numel(), s))
+            tr("o", li)
             qmm._check(L.qmm_matmul_ex(self._gu[li], 2, x.data_ptr(), rows, H, w.ffn_norm[li].data_ptr(), eps, 0,
                                        gu_y, gu_ld, ws.data_ptr(), ws.numel(), s))
+            tr("gate_up", li)
             qmm._check(L.qmm_silu_mul(g.data_ptr(), u.data_ptr(), hh.data_ptr(), rows * F, s))
+            tr("silu_mul", li)
             qmm._check(L.qmm_matmul_ex((vp * 1)(lw["down"].handle.value), 1, hh.data_ptr(), rows, F, None, eps, 1,
                                        x_y, x_ld, ws.data_ptr(), ws.numel(), s))
+            tr("down", li)
         self.pos.fill_(rows)
         self.steps_done = rows
         return rows

@@ -759,6 +759,11 @@ int orc_matmul_prequant(int dtype, int64_t m, int64_t k, int64_t n, const void *
 
 int orc_matmul(int dtype, int64_t m, int64_t k, int64_t n, const float *lhs, const void *rhs,
                float *dst, int nthreads) {
+    return orc_matmul_impl(dtype, m, k, n, lhs, rhs, dst, nthreads, ORC_IMPL_GENERIC);
+}
+
+int orc_matmul_impl(int dtype, int64_t m, int64_t k, int64_t n, const float *lhs, const void *rhs,
+                    float *dst, int nthreads, int impl) {
     int vt = orc_vec_dot_type(dtype);
     if (vt < 0) return -1;
     int vbe = orc_block_elems(vt), vbb = orc_block_bytes(vt);
@@ -767,7 +772,7 @@ int orc_matmul(int dtype, int64_t m, int64_t k, int64_t n, const float *lhs, con
     uint8_t *xq = (uint8_t *)calloc((size_t)(m * xrow), 1);
     if (!xq) return -1;
     for (int64_t r = 0; r < m; r++) orc_quantize(vt, lhs + r * k, k, xq + r * xrow);
-    int rc = orc_matmul_prequant(dtype, m, k, n, xq, rhs, dst, nthreads);
+    int rc = orc_matmul_prequant_impl(dtype, m, k, n, xq, rhs, dst, nthreads, impl);
     free(xq);
     return rc;
 }

@@ -61,6 +61,20 @@ int orc_matmul(int dtype, int64_t m, int64_t k, int64_t n, const float *lhs,
 int orc_matmul_prequant(int dtype, int64_t m, int64_t k, int64_t n, const void *xq,
                         const void *rhs, float *dst, int nthreads);
 
+/* vec_dot implementations: candle's generic bodies (the default build of the
+ * reference) or its x86 AVX2 + FMA bodies (ggml_oracle_avx2.c).  Both give the
+ * same integer block dots; they differ only in f32 accumulation order. */
+enum { ORC_IMPL_GENERIC = 0, ORC_IMPL_AVX2 = 1 };
+/* 1 when this CPU runs the AVX2 + FMA bodies. */
+int orc_simd_supported(void);
+float orc_vec_dot_avx2(int dtype, int64_t k, const void *w_row, const void *x_row);
+/* orc_matmul_prequant / orc_matmul with a chosen implementation; -1 for an
+ * unknown one or AVX2 on a CPU without it. */
+int orc_matmul_prequant_impl(int dtype, int64_t m, int64_t k, int64_t n, const void *xq,
+                             const void *rhs, float *dst, int nthreads, int impl);
+int orc_matmul_impl(int dtype, int64_t m, int64_t k, int64_t n, const float *lhs,
+                    const void *rhs, float *dst, int nthreads, int impl);
+
 #ifdef __cplusplus
 }
 #endif

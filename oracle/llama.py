@@ -98,8 +98,10 @@ class LlamaOracle:
     projection name) and the Llama-3 RoPE parameters.
     """
 
-    def __init__(self, cfg, ex: dict, max_seq: int):
-        self.cfg, self.ex, self.max_seq = cfg, ex, max_seq
+    def __init__(self, cfg, ex: dict, max_seq: int, impl: int = orc.GENERIC):
+        """impl picks the vec_dot bodies (orc.GENERIC: candle's generic ones, the reference's default
+        build; orc.AVX2: its AVX2 + FMA ones). Both give the same integer block dots."""
+        self.cfg, self.ex, self.max_seq, self.impl = cfg, ex, max_seq, impl
         self.inv_freq = llama3_inv_freq(cfg.head_dim, cfg.rope_theta, cfg.rope_factor, cfg.rope_low,
                                         cfg.rope_high, cfg.rope_orig_ctx)
         self.scale = float(f32(cfg.head_dim) ** f32(-0.5))
@@ -109,10 +111,13 @@ class LlamaOracle:
 
     def _mm(self, name: str, li: int, x: np.ndarray, k: int) -> np.ndarray:
         w = self.ex["head"] if name == "head" else self.ex["layers"][li][name]
-        return orc.matmul(int(self.cfg.dtypes[name]), x.reshape(1, k), w, k)[0]
+        return orc.matmul(int(self.cfg.dtypes[name]), x.reshape(1, k), w, k, impl=self.impl)[0]
 
-    def step(self, token: int, pos: int) -> np.ndarray:
-        """Logits of the token at `pos` (the cache holds positions < pos)."""
+    def step(self, token: int, pos: int, record: dict = None) -> np.ndarray:
+        """Logits of the token at `pos` (the cache holds positions < pos). With `record`, record[layer]
+        receives the f32 inputs of the layer's four activation quantizations: "n_attn" (normalised
+        x before q/k/v), "att" (attention output before o), "n_ffn" (normalised x before gate/up) and
+        "hmid" (silu(gate) * up before down), plus "x_attn" / "x_ffn" (the residual before each norm)."""
         c = self.cfg
         hd, H = c.head_dim, c.hidden
         x = self.ex["embed"][token].astype(np.float32).copy()
@@ -120,6 +125,8 @@ class LlamaOracle:
         groups = c.heads // c.kv_heads
         for li in range(c.layers):
             n = rms_norm(x, self.ex["attn_norm"][li], c.eps)
+            rec = record.setdefault(li, {}) if record is not None else {}
+            rec["x_attn"], rec["n_attn"] = x, n
             q = self._mm("q", li, n, H).reshape(c.heads, hd)
             k = self._mm("k", li, n, H).reshape(c.kv_heads, hd)
             v = self._mm("v", li, n, H).reshape(c.kv_heads, hd)
@@ -128,9 +135,12 @@ class LlamaOracle:
             self.vc[li, :, pos] = v
             att = np.stack([attend_one(q[h], self.kc[li, h // groups, : pos + 1],
                                        self.vc[li, h // groups, : pos + 1], self.scale) for h in range(c.heads)])
+            rec["att"] = att.reshape(-1)
             x = (x + self._mm("o", li, att.reshape(-1), c.heads * hd)).astype(np.float32)
             n = rms_norm(x, self.ex["ffn_norm"][li], c.eps)
+            rec["x_ffn"], rec["n_ffn"] = x, n
             hmid = (silu(self._mm("gate", li, n, H)) * self._mm("up", li, n, H)).astype(np.float32)
+            rec["hmid"] = hmid
             x = (x + self._mm("down", li, hmid, c.ffn)).astype(np.float32)
         return self._mm("head", 0, rms_norm(x, self.ex["final_norm"], c.eps), H)
 

@@ -19,6 +19,8 @@ F32, F16, Q8_0, Q4K, Q6K, Q8K = 0, 1, 8, 12, 14, 15
 _ELEMS = {Q8_0: 32, Q4K: 256, Q6K: 256, Q8K: 256}
 _BYTES = {Q8_0: 34, Q4K: 144, Q6K: 210, Q8K: 292}
 VEC_DOT_TYPE = {Q8_0: Q8_0, Q4K: Q8K, Q6K: Q8K}
+# vec_dot bodies: candle's generic ones (the reference's default build) or its AVX2 + FMA ones
+GENERIC, AVX2 = 0, 1
 
 _lib = None
 
@@ -46,6 +48,10 @@ def lib() -> ctypes.CDLL:
         L.orc_block_dots.argtypes = [i32, i64, vp, vp, vp]
         L.orc_matmul.argtypes = [i32, i64, i64, i64, vp, vp, vp, i32]
         L.orc_matmul_prequant.argtypes = [i32, i64, i64, i64, vp, vp, vp, i32]
+        L.orc_matmul_impl.argtypes = [i32, i64, i64, i64, vp, vp, vp, i32, i32]
+        L.orc_matmul_prequant_impl.argtypes = [i32, i64, i64, i64, vp, vp, vp, i32, i32]
+        L.orc_vec_dot_avx2.argtypes = [i32, i64, vp, vp]
+        L.orc_vec_dot_avx2.restype = ctypes.c_float
         for f in ("orc_block_elems", "orc_block_bytes", "orc_vec_dot_type"):
             getattr(L, f).argtypes = [i32]
         _lib = L
@@ -124,23 +130,33 @@ def block_dots(dt: int, w: np.ndarray, xq: np.ndarray, k: int) -> np.ndarray:
     return out
 
 
-def matmul(dt: int, x: np.ndarray, w: np.ndarray, k: int, nthreads: int = 0) -> np.ndarray:
-    """Candle k_quants::matmul: y[m, n] = vec_dot(W[n], quant(x[m]))."""
+def simd_supported() -> bool:
+    return bool(lib().orc_simd_supported())
+
+
+def vec_dot_avx2(dt: int, k: int, w_row: np.ndarray, x_row: np.ndarray) -> float:
+    return lib().orc_vec_dot_avx2(dt, k, _ptr(np.ascontiguousarray(w_row)), _ptr(np.ascontiguousarray(x_row)))
+
+
+def matmul(dt: int, x: np.ndarray, w: np.ndarray, k: int, nthreads: int = 0, impl: int = GENERIC) -> np.ndarray:
+    """Candle k_quants::matmul: y[m, n] = vec_dot(W[n], quant(x[m])) with the chosen vec_dot bodies."""
     x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, k)
     w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1, row_bytes(dt, k))
     y = np.zeros((x.shape[0], w.shape[0]), dtype=np.float32)
-    rc = lib().orc_matmul(dt, x.shape[0], k, w.shape[0], _ptr(x), _ptr(w), _ptr(y), nthreads)
+    rc = lib().orc_matmul_impl(dt, x.shape[0], k, w.shape[0], _ptr(x), _ptr(w), _ptr(y), nthreads, impl)
     if rc != 0:
         raise ValueError("oracle matmul failed")
     return y
 
 
-def matmul_prequant(dt: int, xq: np.ndarray, w: np.ndarray, k: int, nthreads: int = 0) -> np.ndarray:
+def matmul_prequant(dt: int, xq: np.ndarray, w: np.ndarray, k: int, nthreads: int = 0,
+                    impl: int = GENERIC) -> np.ndarray:
     vt = VEC_DOT_TYPE[dt]
     xq = np.ascontiguousarray(xq, dtype=np.uint8).reshape(-1, row_bytes(vt, k))
     w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1, row_bytes(dt, k))
     y = np.zeros((xq.shape[0], w.shape[0]), dtype=np.float32)
-    rc = lib().orc_matmul_prequant(dt, xq.shape[0], k, w.shape[0], _ptr(xq), _ptr(w), _ptr(y), nthreads)
+    rc = lib().orc_matmul_prequant_impl(dt, xq.shape[0], k, w.shape[0], _ptr(xq), _ptr(w), _ptr(y), nthreads,
+                                        impl)
     if rc != 0:
         raise ValueError("oracle matmul failed")
     return y

@@ -22,13 +22,12 @@ import numpy as np
 import pytest
 import torch
 
+from decode_check import OpChecker, cosine, rel_err
 from inference_amd.llama_decode import DecodeSession, LlamaConfig, LlamaWeights
 from inference_amd.qmm import QmmError
 from oracle import llama as ol
-from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
-MM_TOL = 1e-3
 COS_MIN = 0.999
 
 
@@ -36,112 +35,6 @@ def small_cfg(**kw):
     base = dict(layers=2, hidden=512, ffn=1024, heads=8, kv_heads=2, head_dim=64, vocab=1000)
     base.update(kw)
     return LlamaConfig(**base)
-
-
-def rel_err(got, want):
-    got = np.asarray(got, np.float64).reshape(-1)
-    want = np.asarray(want, np.float64).reshape(-1)
-    return float(np.abs(got - want).max() / np.sqrt((want ** 2).mean()))
-
-
-def cosine(a, b):
-    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
-    return float(a @ b / np.sqrt((a @ a) * (b @ b)))
-
-
-class OpChecker:
-    """DecodeSession trace callback: checks each launch against the oracle on the device's inputs."""
-
-    def __init__(self, sess, ex):
-        self.s, self.ex, self.cfg = sess, ex, sess.cfg
-        c = sess.cfg
-        self.inv = ol.llama3_inv_freq(c.head_dim, c.rope_theta, c.rope_factor, c.rope_low, c.rope_high,
-                                      c.rope_orig_ctx)
-        self.worst = {}
-        self.steps = 0
-
-    @staticmethod
-    def snap(t):
-        torch.cuda.synchronize()
-        return t.detach().cpu().numpy().copy()
-
-    def note(self, op, err, tol):
-        self.worst[op] = max(self.worst.get(op, 0.0), err)
-        assert err <= tol, (op, self.p, err)
-
-    def mm(self, name, li, x, k):
-        w = self.ex["head"] if name == "head" else self.ex["layers"][li][name]
-        return orc.matmul(int(self.cfg.dtypes[name]), np.asarray(x, np.float32).reshape(1, k), w, k)[0]
-
-    def __call__(self, op, li):
-        s, c, ex = self.s, self.cfg, self.ex
-        hd = c.head_dim
-        if op == "embed":
-            self.p = int(s.pos.item())
-            self.x = self.snap(s.x)
-            np.testing.assert_array_equal(self.x, ex["embed"][int(s.tokens[self.p].item())])
-        elif op == "qkv":
-            self.n = ol.rms_norm(self.x, ex["attn_norm"][li], c.eps)
-            self.q0, self.k0, self.v0 = self.snap(s.q), self.snap(s.k), self.snap(s.v)
-            self.note("q", rel_err(self.q0, self.mm("q", li, self.n, c.hidden)), MM_TOL)
-            self.note("k", rel_err(self.k0, self.mm("k", li, self.n, c.hidden)), MM_TOL)
-            self.note("v", rel_err(self.v0, self.mm("v", li, self.n, c.hidden)), MM_TOL)
-        elif op == "attention":
-            cs, sn = ol.cos_sin(self.inv, self.p)
-            q1 = ol.apply_rope(self.q0.reshape(-1, hd), cs, sn)
-            k1 = ol.apply_rope(self.k0.reshape(-1, hd), cs, sn)
-            kc, vc, att = self.snap(s.kcache[li]), self.snap(s.vcache[li]), self.snap(s.attn)
-            # rotated k and v appended at p (same f32 operations as the oracle: bit-equal)
-            np.testing.assert_array_equal(kc[:, self.p], k1)
-            np.testing.assert_array_equal(vc[:, self.p], self.v0.reshape(-1, hd))
-            # q and k buffers keep the unrotated projections
-            np.testing.assert_array_equal(self.snap(s.q), self.q0)
-            g = c.heads // c.kv_heads
-            want = np.stack([ol.attend_one(q1[h], kc[h // g, : self.p + 1], vc[h // g, : self.p + 1], s.scale)
-                             for h in range(c.heads)])
-            self.note("attention", rel_err(att, want), 1e-4)
-            self.att = att
-        elif op == "o":
-            x1 = self.snap(s.x)
-            self.note("o", rel_err(x1 - self.x, self.mm("o", li, self.att, c.heads * hd)), MM_TOL)
-            self.x = x1
-        elif op == "gate_up":
-            n2 = ol.rms_norm(self.x, ex["ffn_norm"][li], c.eps)
-            self.g, self.u = self.snap(s.g), self.snap(s.u)
-            self.note("gate", rel_err(self.g, self.mm("gate", li, n2, c.hidden)), MM_TOL)
-            self.note("up", rel_err(self.u, self.mm("up", li, n2, c.hidden)), MM_TOL)
-        elif op == "silu_mul":
-            self.hq = self.snap(s.hq)
-            h = (ol.silu(self.g) * self.u).astype(np.float32)
-            want = orc.quantize(orc.Q8K, h[None]).reshape(-1)
-            dg = orc.dequantize(orc.Q8K, self.hq, c.ffn).reshape(-1, 256)
-            dw = orc.dequantize(orc.Q8K, want, c.ffn).reshape(-1, 256)
-            quantum = np.abs(h).reshape(-1, 256).max(axis=1, keepdims=True) / 127.0
-            self.note("silu_mul_quanta", float((np.abs(dg - dw) / (quantum + 1e-30)).max()), 1.01)
-        elif op == "down":
-            x2 = self.snap(s.x)
-            want = orc.matmul_prequant(orc.Q6K if c.dtypes["down"] == orc.Q6K else int(c.dtypes["down"]),
-                                       self.hq[None], ex["layers"][li]["down"], c.ffn)[0]
-            self.note("down", rel_err(x2 - self.x, want), MM_TOL)
-            self.x = x2
-        elif op == "silu_down":
-            # the activation is quantized inside the launch: the oracle quantizes silu(g) * u itself
-            # (exp vs expf may move one quantum at a rounding tie, far inside the matmul tolerance)
-            x2 = self.snap(s.x)
-            h = (ol.silu(self.g) * self.u).astype(np.float32)
-            hq = orc.quantize(orc.Q8K, h[None])
-            want = orc.matmul_prequant(int(c.dtypes["down"]), hq, ex["layers"][li]["down"], c.ffn)[0]
-            self.note("down", rel_err(x2 - self.x, want), MM_TOL)
-            self.x = x2
-        elif op == "head":
-            self.lg = self.snap(s.logits)
-            self.note("head", rel_err(self.lg, self.mm("head", 0, ol.rms_norm(self.x, ex["final_norm"], c.eps),
-                                                       c.hidden)), MM_TOL)
-        elif op == "argmax":
-            assert int(s.pos.item()) == self.p + 1
-            if self.p + 1 >= s.prompt_len:
-                assert int(s.tokens[self.p + 1].item()) == ol.argmax_first(self.lg)
-            self.steps += 1
 
 
 def op_level(cfg, weights, prompt, steps, max_seq):

@@ -402,3 +402,23 @@ def test_matmul_equals_sum_of_block_terms(dt):
         ref = np.einsum("nb,mb,mnb->mn", dw, dx, dots)
     rms = np.sqrt(np.mean(ref ** 2))
     assert np.max(np.abs(y - ref)) / rms < 1e-5
+
+
+@pytest.mark.skipif(not orc.simd_supported(), reason="needs an AVX2 + FMA host")
+@pytest.mark.parametrize("dt,k", [(orc.Q8_0, 4096), (orc.Q4K, 4096), (orc.Q4K, 14336), (orc.Q6K, 14336)])
+def test_avx2_vec_dot_equals_generic(dt, k):
+    """The AVX2 + FMA bodies (candle's x86 SIMD vec_dot) against the generic ones: the integer block dots
+    are the same, so the f32 results agree to summation-order rounding; extreme codes (all-max weights
+    against -128/+127 activations) included, where a saturating pair sum would show."""
+    rng = np.random.default_rng(k + dt)
+    n = 64
+    w = orc.quantize(dt, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((3, k)).astype(np.float32)
+    x[1] = np.where(np.arange(k) % 2 == 0, -1.0, 0.9921875).astype(np.float32)  # codes -128 / +127 (Q8_K)
+    ext = np.ones((n, k), np.float32) * np.where(np.arange(k) % 3 == 0, -1.0, 1.0).astype(np.float32)
+    we = orc.quantize(dt, ext * 0.05)
+    for wq in (w, we):
+        a = orc.matmul(dt, x, wq, k, impl=orc.GENERIC)
+        b = orc.matmul(dt, x, wq, k, impl=orc.AVX2)
+        scale = np.abs(a.astype(np.float64)).max() + 1e-30
+        assert np.abs(a - b).max() <= 1e-5 * scale * np.sqrt(k / 256), (dt, k, np.abs(a - b).max(), scale)

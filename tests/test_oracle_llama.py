@@ -167,3 +167,54 @@ def test_generate_is_deterministic_and_keeps_prompt():
     b = ol.LlamaOracle(cfg, ex, 16).generate([3, 1, 4], 5)
     assert a == b and a[:3] == [3, 1, 4] and len(a) == 8
     assert all(0 <= t < cfg.vocab for t in a)
+
+
+@pytest.mark.skipif(not orc.simd_supported(), reason="needs an AVX2 + FMA host")
+def test_two_reference_builds_part_at_a_q8k_tie():
+    """Candle's generic and AVX2 vec_dot bodies give the same integer block dots and differ only in f32
+    summation order. Their decode chains agree to f32 noise until one activation's Q8_K code sits on a
+    rounding tie; there the two round apart by one quantum, and the layers after amplify it. Shown on an
+    8-layer Llama-shaped model: the first K/V rows to leave noise are preceded, within the same
+    position, by a quantization whose inputs still agree to f32 noise but whose codes differ by one at
+    tie elements; the logits then differ far beyond f32 noise."""
+    from decode_check import assert_tie, first_flip, kv_rel, quant_inputs_from_record, rel_err
+    cfg = SimpleNamespace(layers=8, hidden=1024, ffn=2816, heads=8, kv_heads=2, head_dim=128, vocab=2048,
+                          rope_theta=500000.0, rope_factor=8.0, rope_low=1.0, rope_high=4.0, rope_orig_ctx=8192.0,
+                          eps=1e-5, dtypes={"q": orc.Q4K, "k": orc.Q4K, "v": orc.Q6K, "o": orc.Q4K, "gate": orc.Q4K,
+                                            "up": orc.Q4K, "down": orc.Q6K, "head": orc.Q6K})
+    rng = np.random.default_rng(1)
+    hd = cfg.heads * cfg.head_dim
+    sh = {"q": (hd, cfg.hidden), "k": (cfg.kv_heads * cfg.head_dim, cfg.hidden),
+          "v": (cfg.kv_heads * cfg.head_dim, cfg.hidden), "o": (cfg.hidden, hd), "gate": (cfg.ffn, cfg.hidden),
+          "up": (cfg.ffn, cfg.hidden), "down": (cfg.hidden, cfg.ffn)}
+
+    def q(n, k, dt):
+        return orc.quantize(dt, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+
+    ex = {"layers": [{nm: q(*sh[nm], cfg.dtypes[nm]) for nm in sh} for _ in range(cfg.layers)],
+          "head": q(cfg.vocab, cfg.hidden, orc.Q6K),
+          "embed": (rng.standard_normal((cfg.vocab, cfg.hidden)) * 0.02).astype(np.float32),
+          "attn_norm": [np.ones(cfg.hidden, np.float32)] * cfg.layers,
+          "ffn_norm": [np.ones(cfg.hidden, np.float32)] * cfg.layers, "final_norm": np.ones(cfg.hidden, np.float32)}
+    T = 24
+    toks = [int(t) for t in np.random.default_rng(2).integers(0, cfg.vocab, T)]
+    og, oa = ol.LlamaOracle(cfg, ex, T, orc.GENERIC), ol.LlamaOracle(cfg, ex, T, orc.AVX2)
+    first, errs = None, []
+    for p in range(T):
+        rg, ra = {}, {}
+        lg, la = og.step(toks[p], p, rg), oa.step(toks[p], p, ra)
+        errs.append(rel_err(la, lg))
+        if first is None:
+            for li in range(cfg.layers):
+                if kv_rel(oa.kc, oa.vc, og.kc, og.vc, li, p) > 5e-5:
+                    first, rec = (p, li), (rg, ra)
+                    break
+            if first is None:
+                assert errs[-1] < 1e-4, (p, errs[-1])  # before the chains part: f32 noise
+    assert first is not None
+    p, li = first
+    rg, ra = rec
+    lays = range(max(0, li - 1), li + 1)
+    assert_tie("AVX2 vs generic chain", first_flip({l: quant_inputs_from_record(ra, l) for l in lays},
+                                                   {l: quant_inputs_from_record(rg, l) for l in lays}, li))
+    assert max(errs[p + 1:]) > 1e-2
