@@ -17,12 +17,16 @@ The roofline object times the dominant kernel (the gate/up GEMV) alone with
 HIP events on the stream it runs on; its `traffic` (HBM bytes per launch) comes
 from the committed rocprofv3 counter summary profiles/gemv_q4k_gate_pmc.json
 (FETCH_SIZE / WRITE_SIZE of that kernel, each scaled by the counter's reading
-for a copy of known size), measured with `--kernel-only gate|copy`. The CPU
+for a copy of known size), measured with `--kernel-only gate|copy`. Every
+timing reports mean / median / p10 / p90 over 120 HIP-event samples. The CPU
 baseline is the oracle's C restatement of Candle's CPU quantized matmul
-(k_quants::matmul with the generic vec_dot), run on this host's cores over a
-bounded sample.
+(k_quants::matmul), with candle's generic vec_dot bodies (the reference's
+default build) and with its AVX2 + FMA bodies, on the host's CPU share for
+one GPU (16 threads) over bounded samples of configs 1, 2, 4 and one config-3
+token; `value` is config 2 with the faster build.
 
-Further legs: config 3 (greedy decode tok/s of the Llama-3-8B-shape Q4_K_M
+Further legs: config 1 (the Q8_0 4096x4096 matvec, GB/s, checked against
+the oracle), config 3 (greedy decode tok/s of the Llama-3-8B-shape Q4_K_M
 model), config 4 (prefill GEMM, MFMA utilisation against the dense int8
 peak) and config 5 (MoE expert FFN, weight GB/s of the active experts).
 """
@@ -58,6 +62,29 @@ def gemv_bytes(dt, n, k):
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+SPREAD_SAMPLES = 120  # HIP-event samples behind every median / p10 / p90
+
+
+def replay_samples(torch, g, n, stream):
+    """Replay graph g n times with a HIP event between consecutive replays on `stream` (where the graph
+    runs); returns the milliseconds of each replay."""
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    evs[0].record(stream)
+    for i in range(n):
+        g.replay()
+        evs[i + 1].record(stream)
+    torch.cuda.synchronize()
+    return np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(n)])
+
+
+def spread(us):
+    """mean / median / p10 / p90 of per-unit microseconds."""
+    us = np.asarray(us, dtype=np.float64)
+    return {"mean": round(float(us.mean()), 3), "median": round(float(np.median(us)), 3),
+            "p10": round(float(np.percentile(us, 10)), 3), "p90": round(float(np.percentile(us, 90)), 3),
+            "samples": int(us.size)}
 
 
 def build_set(torch, dev, dt, copies):
@@ -168,39 +195,45 @@ def run_gemv_set(torch, dev, args):
                 fn(sets[r % copies])
         return g
 
+    # the timed region runs exactly args.steps steps: whole graphs of per_graph steps, then a graph of
+    # the remaining steps (each graph walks the copies from the first, so a copy's weights are never
+    # re-read from the MALL by the step after it)
     per_graph = copies * max(1, 24 // copies)
     g_step = capture(step, per_graph)
-    reps = max(1, -(-args.steps // per_graph))
-    steps = reps * per_graph
-    for _ in range(max(1, args.warmup // per_graph)):
+    reps, rem = divmod(args.steps, per_graph)
+    g_rem = capture(step, rem) if rem else None
+    for _ in range(max(1, -(-args.warmup // per_graph))):
         g_step.replay()
+    if g_rem is not None:
+        g_rem.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(reps):
         g_step.replay()
+    if g_rem is not None:
+        g_rem.replay()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    steps = args.steps
 
     step_bytes = sum(gemv_bytes(dt, n, k) for _, n, k in GEMV_SET)
     value = step_bytes * steps / elapsed / 1e9
 
     stream = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    timing_reps = max(4, args.steps // per_graph)
+
+    # spread of the step time: SPREAD_SAMPLES replays of the step graph, a HIP event between consecutive
+    # replays
+    replay_samples(torch, g_step, 4, stream)
+    step_spread = spread(replay_samples(torch, g_step, SPREAD_SAMPLES, stream) * 1e3 / per_graph)
 
     def time_launch(fn):
-        """Average us of fn(layer) alone: graph replays over the rotated copies, HIP events on its stream,
-        after as many untimed replays (the first pass over the copies runs a few % slower)."""
+        """us per launch of fn(layer) alone: SPREAD_SAMPLES replays of a graph of per_graph launches over the
+        rotated copies, HIP events between replays on the stream the graph runs on, after untimed replays
+        (the first pass over the copies runs a few % slower). Returns the spread of the per-launch time;
+        its mean is the average launch."""
         g = capture(fn, per_graph)
-        for _ in range(timing_reps):
-            g.replay()
-        torch.cuda.synchronize()
-        e0.record(stream)
-        for _ in range(timing_reps):
-            g.replay()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / (timing_reps * per_graph)
+        replay_samples(torch, g, 4, stream)
+        return spread(replay_samples(torch, g, SPREAD_SAMPLES, stream) * 1e3 / per_graph)
 
     # per-shape single launches (pre-quantized activation); each shape rotates
     # its own copies over >= rotate_mb MiB, so no launch reads from the MALL
@@ -211,54 +244,95 @@ def run_gemv_set(torch, dev, args):
         g = torch.Generator(device=dev)
         g.manual_seed(7000 + n + k)
         own = [{name: QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, dt)} for _ in range(nc)]
-        per = nc * max(1, 24 // nc)
         gph = torch.cuda.CUDAGraph()
         gemv(own[0], name)
         torch.cuda.synchronize()
         with torch.cuda.graph(gph):
-            for r in range(per):
-                gemv(own[r % nc], name)
-        reps = max(2, 240 // per)
-        for _ in range(reps):  # untimed pass over the copies
-            gph.replay()
-        torch.cuda.synchronize()
-        e0.record(stream)
-        for _ in range(reps):
-            gph.replay()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (reps * per)
+            for r in range(nc):
+                gemv(own[r], name)
+        replay_samples(torch, gph, 4, stream)  # untimed passes over the copies
+        sp = spread(replay_samples(torch, gph, SPREAD_SAMPLES, stream) * 1e3 / nc)
+        us = sp["mean"]
         b = gemv_bytes(dt, n, k)
         per_shape[name] = {"shape": [n, k], "us": round(us, 3), "GB/s": round(b / us / 1e3, 1),
-                           "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "copies": nc}
+                           "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "copies": nc, "us_spread": sp}
         del own, gph
         torch.cuda.empty_cache()
 
     # dominant launch of the step
     if args.schedule == "serial":
         kernel, rb = "qmm_gemv1_q4k_w4 (gate_proj 14336x4096, one launch)", gemv_bytes(dt, 14336, 4096)
-        rus = per_shape["gate_proj"]["us"]
+        rsp = time_launch(lambda layer: gemv(layer, "gate_proj"))
     else:
         fused = args.schedule == "fused"
-        rus = time_launch(lambda layer: qkvgu(layer, fused))
+        rsp = time_launch(lambda layer: qkvgu(layer, fused))
         rb = sum(gemv_bytes(dt, *shapes[nm]) for nm in QKVGU) - 4 * 4096 * (len(QKVGU) - 1)  # x read once
         kernel = ("qmm_gemv1f_q4k_w16_j8" if fused else "qmm_gemv1_q4k_w4_j8") + \
             " (q, k, v, gate, up: 5 weights, one launch" + (", Q8_K in the prologue)" if fused else ")")
+    rus = rsp["mean"]
     achieved = rb / (rus * 1e-6) / 1e9
     result = {
         "value": value,
         "ms_per_step": elapsed / steps * 1e3,
         "steps": steps,
+        "step_us": step_spread,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(args.schedule),
-                     "kernel": kernel, "avg_us": round(rus, 3), "algorithmic_bytes": rb},
+                     "kernel": kernel, "avg_us": round(rus, 3), "us": rsp, "algorithmic_bytes": rb},
         "per_shape": per_shape,
         "weight_copies": copies,
     }
     return result, sets
 
 
-def run_decode(torch, dev, args):
+def run_q8_0(torch, dev, args, cpu):
+    """Config 1: the Q8_0 4096x4096 matvec (QMatMul::forward on a Q8 projection, quant.rs:26-43): weight
+    N(0, 0.02^2) seed 0 (SplitMix64 + Box-Muller, quantized on the GPU, bit-identical to the CPU
+    quantizer), activation 1x4096 N(0, 1) seed 1. One qmm_matmul call = one launch: the f32 row is
+    quantized to Q8_0 in the GEMV's prologue. Copies beyond the first (same distribution, device
+    generator) are rotated over > 2x the MALL. The first copy's output is checked against the oracle."""
+    from inference_amd import GgmlDType, QTensor, qmm
+    from inference_amd.synth import normal
+    L = qmm.lib()
+    n = k = 4096
+    wb = n * (k // 32) * 34
+    copies = max(2, -(-args.rotate_mb * 2 ** 20 // wb))
+    g = torch.Generator(device=dev)
+    g.manual_seed(100)
+    qts = [QTensor.quantize(torch.from_numpy(normal(0, (n, k), 0.02)).to(dev), GgmlDType.Q8_0)]
+    qts += [QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, GgmlDType.Q8_0)
+            for _ in range(copies - 1)]
+    xh = normal(1, (1, k))
+    x = torch.from_numpy(xh).to(dev)
+    y = torch.empty((1, n), dtype=torch.float32, device=dev)
+    wsb = int(L.qmm_matmul_workspace_size(qts[0].handle, 1))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    it = iter(range(10 ** 9))
+
+    def fn():
+        qmm._check(L.qmm_matmul(qts[next(it) % copies].handle, x.data_ptr(), 1, k, y.data_ptr(), n, ws.data_ptr(),
+                                wsb, qmm._stream(dev)))
+    sp = timed_graph(torch, fn, copies)
+    from oracle import oracle as orc
+    w0 = qts[0].to_ggml()
+    qmm._check(L.qmm_matmul(qts[0].handle, x.data_ptr(), 1, k, y.data_ptr(), n, ws.data_ptr(), wsb,
+                            qmm._stream(dev)))
+    want = orc.matmul(orc.Q8_0, xh, w0, k)
+    rel = float(np.abs(y.cpu().numpy() - want).max() / np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    b = wb + 4 * k + 4 * n
+    us = sp["mean"]
+    out = {"shape": [n, k], "us": round(us, 3), "GB/s": round(b / us / 1e3, 1),
+           "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "algorithmic_bytes": b, "copies": copies,
+           "kernel": "qmm_gemv1f_q8_0_w16 (Q8_0 quantization of the row in the prologue, one launch)", "us_spread": sp,
+           "parity_max_rel_vs_oracle": round(rel, 8)}
+    if cpu is not None:
+        cpu["config1_q8_0_matvec"] = cpu_leg(lambda impl: orc.matmul(orc.Q8_0, xh, w0, k, CPU_THREADS, impl),
+                                             b, "GB/s", cpu["budget_s"])
+    del qts
+    return out
+
+
+def run_decode(torch, dev, args, cpu=None):
     """Config 3: greedy decode of a random-init Llama-3-8B-shaped Q4_K_M model at batch 1.
 
     The prompt's first 127 positions run as one batched prefill (matmuls
@@ -294,6 +368,17 @@ def run_decode(torch, dev, args):
     toks = sess.generated(prompt_len + gen)
     assert toks[:prompt_len] == prompt
     tok_s = gen / (t2 - t1)
+    if cpu is not None:
+        # one config-3 token on the CPU: the oracle's decode step over the same weights (32 layers + head),
+        # at position 0 of a fresh cache for every repetition
+        from oracle import llama as ol
+        from oracle import oracle as orc
+        ex = w.export()
+
+        def tok(impl):
+            ol.LlamaOracle(cfg, ex, 1, impl).step(prompt[0], 0)
+        cpu["config3_decode_token"] = cpu_leg(tok, 1, "tok/s", cpu["budget_s"])
+        del ex
     wb = cfg.weight_bytes_per_token()
     return {"tok_s": round(tok_s, 2), "ms_per_token": round((t2 - t1) / gen * 1e3, 4),
             "prompt_tokens": prompt_len, "generated_tokens": gen,
@@ -309,26 +394,21 @@ def run_decode(torch, dev, args):
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 
 
-def timed_graph(torch, fn, reps, per_graph):
-    """Average microseconds per fn() call over graph replays (fn launches on the current stream)."""
+def timed_graph(torch, fn, per_graph, samples=SPREAD_SAMPLES):
+    """Spread of microseconds per fn() call (fn launches on the current stream): a graph of per_graph calls,
+    replayed `samples` times with a HIP event between replays, after untimed replays."""
     fn()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for _ in range(per_graph):
             fn()
-    g.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+    stream = torch.cuda.current_stream()
+    replay_samples(torch, g, 2, stream)
+    return spread(replay_samples(torch, g, samples, stream) * 1e3 / per_graph)
 
 
-def run_prefill(torch, dev):
+def run_prefill(torch, dev, cpu=None):
     """Config 4: M = 512 tokens x 4096 (N(0,1), seed 5) through Q4_K 14336x4096 and 4096x14336
     (N(0, 0.02^2), seed 6, device generator). qmm_matmul: activation quantization to Q8_K planes +
     the int8-MFMA GEMM. MFMA utilisation = 2*M*N*K / time / dense int8 peak."""
@@ -349,10 +429,17 @@ def run_prefill(torch, dev):
         def fn(qt=qt, x=x, y=y, ws=ws, wsb=wsb, n=n, k=k):
             qmm._check(L.qmm_matmul(qt.handle, x.data_ptr(), m, k, y.data_ptr(), n, ws.data_ptr(), wsb,
                                     qmm._stream(dev)))
-        us = timed_graph(torch, fn, 10, 4)
+        sp = timed_graph(torch, fn, 4)
+        us = sp["mean"]
         tops = 2.0 * m * n * k / us / 1e6
         out[name] = {"m_n_k": [m, n, k], "us": round(us, 2), "TOPS": round(tops, 1),
-                     "mfma_util": round(tops / INT8_PEAK_TOPS, 4)}
+                     "mfma_util": round(tops / INT8_PEAK_TOPS, 4), "us_spread": sp}
+        if cpu is not None:
+            from oracle import oracle as orc
+            wq, xs = qt.to_ggml(), x[:CPU_PREFILL_ROWS].cpu().numpy()
+            cpu[f"config4_{name}"] = cpu_leg(lambda impl: orc.matmul(orc.Q4K, xs, wq, k, CPU_THREADS, impl),
+                                             2.0 * CPU_PREFILL_ROWS * n * k / 1e12, "TOPS", cpu["budget_s"])
+            cpu[f"config4_{name}"]["rows"] = CPU_PREFILL_ROWS
         del qt
     return out
 
@@ -381,7 +468,8 @@ def run_moe(torch, dev):
     def fn():
         qmm._check(L.qmm_moe_ffn(x.data_ptr(), T, H, logits.data_ptr(), E, k, gate.handle, up.handle, down.handle,
                                  y.data_ptr(), H, ws.data_ptr(), wsb, qmm._stream(dev)))
-    us = timed_graph(torch, fn, 10, 4)
+    sp = timed_graph(torch, fn, 4)
+    us = sp["mean"]
     # active experts: those in some token's top-k
     active = set()
     for row in logits_np:
@@ -390,7 +478,7 @@ def run_moe(torch, dev):
     wbytes = per_expert * len(active)
     out = {"us": round(us, 2), "active_experts": len(active), "weight_bytes": wbytes,
            "GB/s": round(wbytes / us / 1e3, 1), "hbm_frac": round(wbytes / us / 1e3 / HBM_PEAK_GBS, 4),
-           "tokens": T, "topk": k}
+           "tokens": T, "topk": k, "us_spread": sp}
 
     # MoE prefill on the same experts: 512 tokens N(0,1) seed 9, router logits seed 10, top-2; the
     # routed pairs average 128 rows per expert, so qmm_moe_ffn takes the grouped MFMA GEMMs.
@@ -404,37 +492,87 @@ def run_moe(torch, dev):
     def fnp():
         qmm._check(L.qmm_moe_ffn(xp.data_ptr(), Tp, H, lp.data_ptr(), E, k, gate.handle, up.handle, down.handle,
                                  yp.data_ptr(), H, wsv.data_ptr(), wsp, qmm._stream(dev)))
-    usp = timed_graph(torch, fnp, 4, 2)
+    spp = timed_graph(torch, fnp, 1, 60)
+    usp = spp["mean"]
     ops = 2 * Tp * k * 3 * F * H  # int8 ops of the three projections over every routed pair
     out["prefill"] = {"tokens": Tp, "us": round(usp, 2), "TOPS": round(ops / usp / 1e6, 1),
                       "mfma_util": round(ops / usp / 1e6 / INT8_PEAK_TOPS, 4),
-                      "schedule": "route, gather, grouped MFMA GEMM gate/up, SiLU*mul, grouped GEMM down, combine"}
+                      "schedule": "route, gather, grouped MFMA GEMM gate/up, SiLU*mul, grouped GEMM down, combine",
+                      "us_spread": spp}
     return out
 
 
-def cpu_baseline(sets, budget_s):
-    """Oracle restatement of Candle's CPU quantized matmul over the same GEMV set."""
+CPU_THREADS = min(16, len(os.sched_getaffinity(0)))  # the GPU box's CPU share for one GPU is 16
+CPU_PREFILL_ROWS = 64  # rows of the config-4 activation timed on the CPU (the CPU matmul is linear in rows)
+
+
+def cpu_host():
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus": os.cpu_count(), "cpus_in_affinity": len(os.sched_getaffinity(0)),
+            "threads_used": CPU_THREADS}
+
+
+def cpu_leg(fn, units, unit, budget_s):
+    """Time fn(impl) for both vec_dot builds of the oracle (candle's generic bodies = the reference's
+    default build; its AVX2 + FMA bodies): one warm-up, then >= 5 repetitions within the budget; the median
+    gives units / second."""
+    from oracle import oracle as orc
+    out = {"unit": unit}
+    for name, impl in (("avx2", orc.AVX2), ("generic", orc.GENERIC)):
+        if impl == orc.AVX2 and not orc.simd_supported():
+            continue
+        fn(impl)
+        times, t_end = [], time.perf_counter() + budget_s
+        while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 1000):
+            t0 = time.perf_counter()
+            fn(impl)
+            times.append(time.perf_counter() - t0)
+        med = float(np.median(times))
+        out[name] = {"value": round(units / med / (1e9 if unit == "GB/s" else 1), 4), "median_s": round(med, 6),
+                     "reps": len(times)}
+    return out
+
+
+def cpu_gemv_set(sets, cpu):
+    """Config 2 on the CPU: the oracle's k_quants::matmul over the same Q4_K GEMV set (M = 1), each pass on
+    the next of the GPU's rotated weight copies (> 2x the 256 MB MALL, so beyond the host's caches too)."""
     from oracle import oracle as orc
     from inference_amd.synth import normal
-    threads = min(16, os.cpu_count() or 1)
-    layer = sets[0]
-    w = {name: layer[name].to_ggml() for name, _, _ in GEMV_SET}
-    x4096 = normal(3, (1, 4096))
-    x14336 = normal(3, (1, 14336))
+    ws = [{name: layer[name].to_ggml() for name, _, _ in GEMV_SET} for layer in sets]
+    x4096, x14336 = normal(3, (1, 4096)), normal(3, (1, 14336))
     total_bytes = sum(gemv_bytes(12, n, k) for _, n, k in GEMV_SET)
-    orc.lib()
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
+    turn = iter(range(10 ** 9))
+
+    def one_pass(impl):
+        w = ws[next(turn) % len(ws)]
         for name, n, k in GEMV_SET:
-            orc.matmul(orc.Q4K, x4096 if k == 4096 else x14336, w[name], k, nthreads=threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 100000:
-            break
-    return {"value": round(total_bytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} passes of the Q4_K GEMV set (M=1, 6 projections) with the oracle's generic "
-                      f"vec_dot, {threads} OpenMP threads, {el:.1f} s"}
+            orc.matmul(orc.Q4K, x4096 if k == 4096 else x14336, w[name], k, CPU_THREADS, impl)
+    cpu["config2_q4k_gemv_set"] = cpu_leg(one_pass, total_bytes, "GB/s", cpu["budget_s"])
+
+
+def cpu_summary(cpu):
+    """The bench line's cpu_baseline: config 2 with the faster (AVX2) build as `value`, every timed
+    config under `configs`."""
+    legs = {k: v for k, v in cpu.items() if k not in ("budget_s",)}
+    c2 = legs["config2_q4k_gemv_set"]
+    best = "avx2" if "avx2" in c2 else "generic"
+    return {"value": c2[best]["value"], "unit": "GB/s", "cores": CPU_THREADS, "kind": "port",
+            "build": best, "host": cpu_host(),
+            "sample": (f"config 2 (the Q4_K GEMV set, M = 1, 6 projections, rotated over the GPU's weight copies) "
+                       f"through the oracle's C restatement "
+                       f"of candle's k_quants::matmul, {best} vec_dot, {CPU_THREADS} OpenMP threads; median of "
+                       f">= 5 repetitions. Also timed, both builds: config 1 (Q8_0 4096x4096 matvec), config 4 "
+                       f"({CPU_PREFILL_ROWS} of the 512 rows of each prefill GEMM) and one config-3 decode token "
+                       f"(32 layers + head at position 0)"),
+            "configs": legs}
 
 
 def kernel_only(torch, dev, which, launches):
@@ -490,6 +628,34 @@ def kernel_only(torch, dev, which, launches):
                                      y.data_ptr(), H, ws.data_ptr(), wsb, qmm._stream(dev)))
         torch.cuda.synchronize()
         print(json.dumps({"kernel_only": "moe", "launches": launches}), flush=True)
+        return
+    if which in ("q8_0", "down_q6k"):
+        # config 1: the Q8_0 4096x4096 matvec, one qmm_matmul (fused Q8_0 prologue) per launch; or the
+        # decode step's Q6_K down projection 4096x14336 with a pre-quantized Q8_K row. Rotated copies.
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        L = qmm.lib()
+        dt, n, k = (GgmlDType.Q8_0, 4096, 4096) if which == "q8_0" else (GgmlDType.Q6K, 4096, 14336)
+        nc = 38 if which == "q8_0" else 14
+        ws = [QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, dt) for _ in range(nc)]
+        x = torch.randn(k, device=dev)
+        y = torch.empty(n, dtype=torch.float32, device=dev)
+        if which == "q8_0":
+            wsb = int(L.qmm_matmul_workspace_size(ws[0].handle, 1))
+            buf = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+            for i in range(launches):
+                qmm._check(L.qmm_matmul(ws[i % nc].handle, x.data_ptr(), 1, k, y.data_ptr(), n, buf.data_ptr(), wsb,
+                                        qmm._stream(dev)))
+            alg = n * (k // 32) * 34 + 4 * k + 4 * n
+        else:
+            xq = torch.zeros(k // 256 * 292, dtype=torch.uint8, device=dev)
+            qmm._check(L.qmm_quantize_rows(15, x.data_ptr(), 1, k, k, xq.data_ptr(), qmm._stream(dev)))
+            for i in range(launches):
+                qmm._check(L.qmm_matmul_q(ws[i % nc].handle, xq.data_ptr(), 1, y.data_ptr(), n, None, 0,
+                                          qmm._stream(dev)))
+            alg = n * (k // 256) * 210 + 4 * k + 4 * n
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel_only": which, "algorithmic_bytes": alg, "launches": launches}), flush=True)
         return
     g = torch.Generator(device=dev)
     g.manual_seed(2)
@@ -553,7 +719,8 @@ def main():
                          "same two GEMV launches with Q8_K quantization in their prologues; serial: one launch "
                          "per projection")
     ap.add_argument("--decode-tokens", type=int, default=256, help="config-3 generated tokens (0 = skip)")
-    ap.add_argument("--kernel-only", choices=("gate", "qkvgu", "qkvgu_staged", "copy", "gemm_gate", "gemm_down", "moe"),
+    ap.add_argument("--kernel-only", choices=("gate", "qkvgu", "qkvgu_staged", "copy", "gemm_gate", "gemm_down", "moe",
+                                              "q8_0", "down_q6k"),
                     default=None,
                     help="launch only one GEMV launch kind or a calibration copy --steps times (counter runs)")
     args = ap.parse_args()
@@ -568,14 +735,20 @@ def main():
     if args.kernel_only:
         kernel_only(torch, dev, args.kernel_only, args.steps)
         return
+    cpu = {"budget_s": args.cpu_seconds / 10.0} if args.cpu_seconds > 0 else None
     res, sets = run_gemv_set(torch, dev, args)
-    cpu = cpu_baseline(sets, args.cpu_seconds) if args.cpu_seconds > 0 else None
+    if cpu is not None:
+        log("[bench] CPU baseline: config 2")
+        cpu_gemv_set(sets, cpu)
     del sets
     torch.cuda.empty_cache()
-    dec = run_decode(torch, dev, args) if args.decode_tokens > 0 else None
+    log("[bench] Q8_0 matvec (config 1)")
+    q80 = run_q8_0(torch, dev, args, cpu)
+    torch.cuda.empty_cache()
+    dec = run_decode(torch, dev, args, cpu) if args.decode_tokens > 0 else None
     torch.cuda.empty_cache()
     log("[bench] prefill GEMM (config 4)")
-    pre = run_prefill(torch, dev)
+    pre = run_prefill(torch, dev, cpu)
     torch.cuda.empty_cache()
     log("[bench] MoE expert FFN (config 5)")
     moe = run_moe(torch, dev)
@@ -596,13 +769,15 @@ def main():
                    "batch_m": 1, "weights": "Q4_K, N(0,0.02^2) seed 2", "activations": "Q8_K on device, seed 3",
                    "weight_copies_rotated": res["weight_copies"], "schedule": args.schedule},
         "hbm_frac": round(res["value"] / HBM_PEAK_GBS, 4),
+        "step_us": res["step_us"],
         "roofline": res["roofline"],
         "per_shape": res["per_shape"],
+        "q8_0_matvec": q80,
         "decode_tok_s": dec["tok_s"] if dec else None,
         "decode": dec,
         "prefill_gemm": pre,
         "moe_ffn": moe,
-        "cpu_baseline": cpu,
+        "cpu_baseline": cpu_summary(cpu) if cpu is not None else None,
     }
     print(json.dumps(line), flush=True)
 
