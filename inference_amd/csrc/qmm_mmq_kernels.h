@@ -914,7 +914,367 @@ __device__ __forceinline__ void mmq4_q4k(const uint8_t* __restrict__ wq, const i
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K prefill GEMM, split-scale with the mins term on bf16 matrix cores
+// (mmqs). Per output and super-block the only VALU work left is one integer
+// combine and one f32 multiply-add; everything else runs on MFMA:
+//   * the d term exactly as mmq4: sc = 8 * sh + sl (both in [0, 7]), weight
+//     operands sl * q4 and sh * q4 (int8, one packed 16-bit multiply per
+//     dword), isd = MFMA_acc(x, sl q4) + 8 MFMA_acc(x, sh q4) in int32; then
+//     acc += (dx * d) * isd once per super-block;
+//   * the mins term sum_b dx * dmin * sum_j m_j S_j (S_j the 32-element sums of
+//     the activation codes) is a dense product over (super-block, sub-block)
+//     of A'[m][b, j] = dx * S_j and B'[b, j][n] = -dmin * m_j. Both factors
+//     are formed in f32 while a K step is staged and split into bf16 hi + lo
+//     halves; two v_mfma_f32_32x32x16_bf16 per tile and super-block
+//     ([hi_A | lo_A] . [hi_B | hi_B] and [hi_A | lo_A] . [lo_B | 0]) accumulate
+//     hi*hi + lo*hi + hi*lo in f32 across all super-blocks, no per-step
+//     epilogue. The dropped lo*lo term and the halves' rounding leave a
+//     relative error of about 2^-16 on the mins term;
+//   * workgroup tile 128 x 128, eight waves (two per SIMD, so one wave's
+//     VALU epilogue and LDS waits overlap the other's MFMAs), two along M and
+//     four along N; a wave owns 64 rows (two M tiles) x 32 columns, so a
+//     column's operand products are formed once per K step for two tiles;
+//     the mins MFMAs and the d-term multiply-adds share one f32 accumulator;
+//   * staging: two LDS stages, the next step's global loads in registers
+//     while this step computes (a second register set, loads two steps
+//     ahead, measured no faster); consecutive lanes load
+//     consecutive 16-byte pieces (activation rows, weight quant bytes), so a
+//     wave's load touches few cache lines; threads 0..127 load column t's
+//     block header and form B' and the split-scale multipliers as packed
+//     16-bit pairs; threads 128..255 load row t - 128's scale and sums and
+//     form A' (waves 0, 1 and 2, 3: the staging arithmetic lands on all four
+//     SIMDs, wave w running on SIMD w % 4). A' / B' / multiplier rows sit at odd multiples of 16 bytes
+//     (conflict-free 16-byte access).
+// DUMP instantiations also compute ism exactly (two zero-padded int8 MFMAs)
+// and write the integer block dots, which equal mmq2's.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kSBM = 128, kSBN = 128;          // workgroup tile
+constexpr int kSThreads = 512;                 // eight waves: two along M, four along N
+constexpr int kSTM = 2;                        // M tiles (32 rows) per wave
+constexpr int kSHalf = 48;                     // A' / B' row: bf16 hi[8] | lo[8] | 16 B pad (odd 16-byte stride)
+constexpr int kSOffB = kSBM * kM2AStride;      // LDS: weight blocks
+constexpr int kSOffDx = kSOffB + kSBN * kM2BStride;
+constexpr int kSOffAm = kSOffDx + kSBM * 4;    // A' rows
+constexpr int kSOffBm = kSOffAm + kSBM * kSHalf;  // B' columns
+constexpr int kSOffSc = kSOffBm + kSBN * kSHalf;  // per column: sl_j | sl_j << 16 (j < 8), then sh_j | sh_j << 16
+constexpr int kSScStride = 80;                 // 64 B of multipliers + 16 B pad (odd 16-byte stride)
+constexpr int kSOffSum = kSOffSc + kSBN * kSScStride;  // DUMP: 32-sums as 6-bit low / high bytes
+template <bool DUMP>
+struct SLayout {
+  static constexpr int kStage = kSOffSum + (DUMP ? kSBM * 16 : 0);
+  static constexpr int kBytes = 2 * kStage;
+};
+
+struct SRegs {
+  uint4 a[kSBM * 16 / kSThreads];  // activation rows: 4 x 16 B per thread
+  uint4 q[2];                      // weight quants: pieces 1 + (idx & 7) of column idx >> 3, idx = t + 512 u
+  uint4 e;                         // t < 128: block header of column t; 128 <= t < 256: sums of row t - 128
+  float dx;                        // 128 <= t < 256: scale of row t - 128
+};
+
+// Global loads of one K step. Consecutive lanes read consecutive 16-byte
+// pieces (an activation row's 256 bytes, a weight block's 128 quant bytes),
+// so a wave's load touches as few cache lines as the data allows; the block
+// headers (16 bytes at the blocks' stride) are read once each.
+__device__ __forceinline__ void s_load(SRegs& R, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                       const int16_t* __restrict__ xs, const uint8_t* __restrict__ wq, int M, int N,
+                                       int K, int m0, int n0, int kb) {
+  const int t = threadIdx.x, nbk = K / 256;
+#pragma unroll
+  for (int u = 0; u < kSBM * 16 / kSThreads; ++u) {
+    const int idx = t + kSThreads * u, row = m0 + (idx >> 4);
+    R.a[u] = row < M ? reinterpret_cast<const uint4*>(xq + (size_t)row * K + 256 * kb)[idx & 15] : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int idx = t + kSThreads * u, col = n0 + (idx >> 3);
+    R.q[u] = col < N ? reinterpret_cast<const uint4*>(wq + ((size_t)col * nbk + kb) * kQ4KBytes)[1 + (idx & 7)]
+                     : make_uint4(0, 0, 0, 0);
+  }
+  if (t < 128) {
+    const int col = n0 + t;
+    R.e = col < N ? *reinterpret_cast<const uint4*>(wq + ((size_t)col * nbk + kb) * kQ4KBytes) : make_uint4(0, 0, 0, 0);
+  } else if (t < 256) {
+    const int row = m0 + t - 128;
+    const bool ok = row < M;
+    R.dx = ok ? xd[(size_t)row * nbk + kb] : 0.0f;
+    R.e = ok ? *reinterpret_cast<const uint4*>(xs + ((size_t)row * nbk + kb) * 8) : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// v as bf16 hi (round to nearest even) and the bf16 of the remainder.
+__device__ __forceinline__ void bf16_split(float v, unsigned short& hi, unsigned short& lo) {
+  const __bf16 h = (__bf16)v;
+  hi = __builtin_bit_cast(unsigned short, h);
+  lo = __builtin_bit_cast(unsigned short, (__bf16)(v - (float)h));
+}
+
+__device__ __forceinline__ void s_store_halves(uint8_t* dst, const unsigned short* hi, const unsigned short* lo) {
+  uint4* o = reinterpret_cast<uint4*>(dst);
+  o[0] = make_uint4(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16), hi[4] | ((uint32_t)hi[5] << 16),
+                    hi[6] | ((uint32_t)hi[7] << 16));
+  o[1] = make_uint4(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16), lo[4] | ((uint32_t)lo[5] << 16),
+                    lo[6] | ((uint32_t)lo[7] << 16));
+}
+
+template <bool DUMP>
+__device__ __forceinline__ void s_store(const SRegs& R, uint8_t* buf) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < kSBM * 16 / kSThreads; ++u) {
+    const int idx = t + kSThreads * u;
+    *reinterpret_cast<uint4*>(buf + (idx >> 4) * kM2AStride + 16 * (idx & 15)) = R.a[u];
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int idx = t + kSThreads * u;
+    *reinterpret_cast<uint4*>(buf + kSOffB + (idx >> 3) * kM2BStride + 16 * (1 + (idx & 7))) = R.q[u];
+  }
+  unsigned short hi[8], lo[8];
+  if (t < 128) {
+    // column t's header; B' = -dmin * m_j; the split scales sl_j = sc_j & 7, sh_j = sc_j >> 3 as packed
+    // 16-bit pairs (the multipliers of the weight operands)
+    const uint4 hd = R.e;
+    *reinterpret_cast<uint4*>(buf + kSOffB + t * kM2BStride) = hd;
+    const float dmin = h2f(hd.x >> 16);
+    const uint32_t mn[2] = {hd.z & 0x3f3f3f3fu, ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u)};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) bf16_split(-dmin * (float)((mn[j >> 2] >> (8 * (j & 3))) & 0xffu), hi[j], lo[j]);
+    s_store_halves(buf + kSOffBm + kSHalf * t, hi, lo);
+    const uint32_t sc[2] = {hd.y & 0x3f3f3f3fu, (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u)};
+    uint32_t v[16];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t s8 = (sc[j >> 2] >> (8 * (j & 3))) & 0xffu;
+      v[j] = (s8 & 7u) * 0x10001u;
+      v[8 + j] = (s8 >> 3) * 0x10001u;
+    }
+    uint4* o = reinterpret_cast<uint4*>(buf + kSOffSc + kSScStride * t);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+  } else if (t < 256) {
+    // A' = dx * S_j of row c and the row's scale; (DUMP) the sums as 6-bit low and signed high bytes
+    const int c = t - 128;
+    reinterpret_cast<float*>(buf + kSOffDx)[c] = R.dx;
+    const int16_t* sv = reinterpret_cast<const int16_t*>(&R.e);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) bf16_split(R.dx * (float)sv[j], hi[j], lo[j]);
+    s_store_halves(buf + kSOffAm + kSHalf * c, hi, lo);
+    if (DUMP) {
+      uint32_t sl[2] = {0, 0}, sh[2] = {0, 0};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int v = sv[j];
+        sl[j >> 2] |= (uint32_t)(v & 63) << (8 * (j & 3));
+        sh[j >> 2] |= (uint32_t)((v >> 6) & 0xff) << (8 * (j & 3));
+      }
+      *reinterpret_cast<uint4*>(buf + kSOffSum + 16 * c) = make_uint4(sl[0], sl[1], sh[0], sh[1]);
+    }
+  }
+}
+
+__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Bytes of v times the packed pair s2 = s | s << 16 (each product < 256).
+__device__ __forceinline__ i8x16 bytes_times4p(uint4 v, uint32_t s2) {
+  const u16x2 b = __builtin_bit_cast(u16x2, s2);
+  return as_i8x16(make_uint4(__builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, v.x) * b),
+                             __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, v.y) * b),
+                             __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, v.z) * b),
+                             __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, v.w) * b)));
+}
+
+// The integer part of one K step of mmqs from LDS stage `buf`: accl / acch =
+// the split-scale MFMA sums (isd = accl + 8 acch).
+__device__ __forceinline__ void mmqs_mfma(const uint8_t* __restrict__ buf, i32x16 (&accl)[kSTM],
+                                          i32x16 (&acch)[kSTM], int wm, int r, int h, int bcol) {
+  i32x16 zero;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) zero[j] = 0;
+  const int arow0 = 64 * wm + r;
+  const int8_t* A = reinterpret_cast<const int8_t*>(buf);
+  const uint8_t* Bc = buf + kSOffB + bcol * kM2BStride;
+  const uint4* SC = reinterpret_cast<const uint4*>(buf + kSOffSc + kSScStride * bcol);
+  const uint4 sl4[2] = {SC[0], SC[1]}, sh4[2] = {SC[2], SC[3]};
+  auto pick = [](const uint4* v, int j) {
+    const uint4 q = v[j >> 2];
+    return (j & 3) == 0 ? q.x : (j & 3) == 1 ? q.y : (j & 3) == 2 ? q.z : q.w;
+  };
+#pragma unroll
+  for (int c2 = 0; c2 < 4; ++c2) {
+    const uint4 qv = *reinterpret_cast<const uint4*>(Bc + 16 + 32 * c2 + 16 * h);
+    const uint4 blo = make_uint4(qv.x & 0x0f0f0f0fu, qv.y & 0x0f0f0f0fu, qv.z & 0x0f0f0f0fu, qv.w & 0x0f0f0f0fu);
+    const uint4 bhi = make_uint4((qv.x >> 4) & 0x0f0f0f0fu, (qv.y >> 4) & 0x0f0f0f0fu, (qv.z >> 4) & 0x0f0f0f0fu,
+                                 (qv.w >> 4) & 0x0f0f0f0fu);
+    const i8x16 bl0 = bytes_times4p(blo, pick(sl4, 2 * c2));
+    const i8x16 bh0 = bytes_times4p(blo, pick(sh4, 2 * c2));
+    const i8x16 bl1 = bytes_times4p(bhi, pick(sl4, 2 * c2 + 1));
+    const i8x16 bh1 = bytes_times4p(bhi, pick(sh4, 2 * c2 + 1));
+    i8x16 a0[kSTM], a1[kSTM];
+#pragma unroll
+    for (int i = 0; i < kSTM; ++i) {
+      const int8_t* ar = A + (arow0 + 32 * i) * kM2AStride + 64 * c2 + 16 * h;
+      a0[i] = *reinterpret_cast<const i8x16*>(ar);
+      a1[i] = *reinterpret_cast<const i8x16*>(ar + 32);
+    }
+    // chains on one accumulator four MFMAs apart
+#pragma unroll
+    for (int i = 0; i < kSTM; ++i) accl[i] = mfma_i8(a0[i], bl0, c2 == 0 ? zero : accl[i]);
+#pragma unroll
+    for (int i = 0; i < kSTM; ++i) acch[i] = mfma_i8(a0[i], bh0, c2 == 0 ? zero : acch[i]);
+#pragma unroll
+    for (int i = 0; i < kSTM; ++i) accl[i] = mfma_i8(a1[i], bl1, accl[i]);
+#pragma unroll
+    for (int i = 0; i < kSTM; ++i) acch[i] = mfma_i8(a1[i], bh1, acch[i]);
+  }
+}
+
+// The floating part of one K step from the same LDS stage: the mins term on
+// the bf16 matrix cores and acc += (dx * d) * isd.
+__device__ __forceinline__ void mmqs_epi(const uint8_t* __restrict__ buf, const i32x16 (&accl)[kSTM],
+                                         const i32x16 (&acch)[kSTM], f32x16 (&acc)[kSTM], int wm, int r, int h,
+                                         int bcol) {
+  const int arow0 = 64 * wm + r;
+  const float* DX = reinterpret_cast<const float*>(buf + kSOffDx);
+  const float dw = h2f(*reinterpret_cast<const uint32_t*>(buf + kSOffB + bcol * kM2BStride));
+  const uint8_t* bmp = buf + kSOffBm + kSHalf * bcol;
+  const bf16x8 bm1 = *reinterpret_cast<const bf16x8*>(bmp);
+  const uint4 lo4 = *reinterpret_cast<const uint4*>(bmp + 16);
+  const bf16x8 bm2 = __builtin_bit_cast(bf16x8, h == 0 ? lo4 : make_uint4(0, 0, 0, 0));
+#pragma unroll
+  for (int i = 0; i < kSTM; ++i) {
+    const bf16x8 am = *reinterpret_cast<const bf16x8*>(buf + kSOffAm + kSHalf * (arow0 + 32 * i) + 16 * h);
+    acc[i] = mfma_bf16(am, bm1, acc[i]);
+    acc[i] = mfma_bf16(am, bm2, acc[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < kSTM; ++i) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 dx = *reinterpret_cast<const float4*>(DX + 64 * wm + 32 * i + 8 * g + 4 * h);
+      const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = 4 * g + q;
+        const int isd = accl[i][e] + (acch[i][e] << 3);
+        acc[i][e] = __builtin_fmaf(dxs[q] * dw, (float)isd, acc[i][e]);
+      }
+    }
+  }
+}
+
+// DUMP: one whole K step with exact integer mins, writing every block dot,
+// acc += dx * (d * isd - dmin * ism).
+__device__ __forceinline__ void mmqs_step_dump(const uint8_t* __restrict__ buf, f32x16 (&acc)[kSTM], int wm, int r,
+                                               int h, int bcol, int m0, int col, int M, int N, int nbk, int kb,
+                                               int* __restrict__ dump) {
+  i32x16 zero;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) zero[j] = 0;
+  i32x16 accl[kSTM], acch[kSTM];
+  mmqs_mfma(buf, accl, acch, wm, r, h, bcol);
+  const int arow0 = 64 * wm + r;
+  const float* DX = reinterpret_cast<const float*>(buf + kSOffDx);
+  const uint4 hd = *reinterpret_cast<const uint4*>(buf + kSOffB + bcol * kM2BStride);
+  const float dw = h2f(hd.x), dmw = h2f(hd.x >> 16);
+  const uint32_t mnlo = hd.z & 0x3f3f3f3fu, mnhi = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
+  const uint4 zero4 = make_uint4(0, 0, 0, 0);
+  const i8x16 bmi = as_i8x16(h == 0 ? make_uint4(mnlo, mnhi, 0, 0) : zero4);
+#pragma unroll
+  for (int i = 0; i < kSTM; ++i) {
+    const uint4 sv = *reinterpret_cast<const uint4*>(buf + kSOffSum + 16 * (arow0 + 32 * i));
+    const i8x16 alo = as_i8x16(h == 0 ? make_uint4(sv.x, sv.y, 0, 0) : zero4);
+    const i8x16 ahi = as_i8x16(h == 0 ? make_uint4(sv.z, sv.w, 0, 0) : zero4);
+    const i32x16 Lo = mfma_i8(alo, bmi, zero), Hi = mfma_i8(ahi, bmi, zero);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int rt = 64 * wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+      const int isd = accl[i][e] + (acch[i][e] << 3), ism = Hi[e] * 64 + Lo[e];
+      acc[i][e] += DX[rt] * (dw * (float)isd - dmw * (float)ism);
+      if (m0 + rt < M && col < N) {
+        const size_t o = ((size_t)(m0 + rt) * N + col) * nbk + kb;
+        dump[2 * o] = isd;
+        dump[2 * o + 1] = ism;
+      }
+    }
+  }
+}
+
+template <bool DUMP>
+__device__ __forceinline__ void mmqs_q4k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,
+                                         const float* __restrict__ xd, const int16_t* __restrict__ xs,
+                                         float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,
+                                         int accumulate, int remap, int kb0, int kb1) {
+  using Lay = SLayout<DUMP>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  int mt, nt;
+  gemm_tile(remap, mt, nt);
+  const int m0 = mt * kSBM, n0 = nt * kSBN;
+  const int nbk = K / 256;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int bcol = 32 * wn + r;  // this lane's column in the workgroup tile
+  const int col = n0 + bcol;
+
+  // one f32 accumulator per output: the bf16 MFMAs add the mins term to it, the VALU the d term
+  f32x16 acc[kSTM];
+#pragma unroll
+  for (int i = 0; i < kSTM; ++i)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[i][j] = 0.0f;
+
+  // the next K step's global loads are in registers while this step computes from LDS stage
+  // (kb - kb0) & 1
+  SRegs R;
+  s_load(R, xq, xd, xs, wq, M, N, K, m0, n0, kb0);
+  s_store<DUMP>(R, lds);
+  __syncthreads();
+  i32x16 accl[kSTM], acch[kSTM];
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const uint8_t* cur = lds + ((kb - kb0) & 1) * Lay::kStage;
+    if (kb + 1 < kb1) s_load(R, xq, xd, xs, wq, M, N, K, m0, n0, kb + 1);
+    if constexpr (DUMP) {
+      mmqs_step_dump(cur, acc, wm, r, h, bcol, m0, col, M, N, nbk, kb, dump);
+    } else {
+      mmqs_mfma(cur, accl, acch, wm, r, h, bcol);
+      mmqs_epi(cur, accl, acch, acc, wm, r, h, bcol);
+    }
+    if (kb + 1 < kb1) s_store<DUMP>(R, lds + ((kb + 1 - kb0) & 1) * Lay::kStage);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < kSTM; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int row = m0 + 64 * wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+      if (row < M && col < N) {
+        float* yp = y + (size_t)row * ldy + col;
+        *yp = accumulate ? *yp + acc[i][e] : acc[i][e];
+      }
+    }
+}
+
 }  // namespace qmm
+
+#define QMM_MMQS_KERNEL(SUFFIX, DUMP)                                                                          \
+  extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))                 \
+      qmm_mmqs_q4k##SUFFIX(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                      \
+                           const float* __restrict__ xd, const int16_t* __restrict__ xs, float* __restrict__ y, \
+                           int M, int N, int K, int ldy, int* __restrict__ dump, int accumulate, int remap,     \
+                           int kc, long long ysplit) {                                                          \
+    const qmm::KRange kr = qmm::split_range(K, kc);                                                            \
+    qmm::mmqs_q4k<DUMP>(wq, xq, xd, xs, y + blockIdx.z * ysplit, M, N, K, ldy, dump, accumulate, remap,        \
+                        kr.kb0, kr.kb1);                                                                       \
+  }
+QMM_MMQS_KERNEL(, false)
+QMM_MMQS_KERNEL(_dump, true)
 
 #define QMM_MMQ4_KERNEL(BN)                                                                                    \
   extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))                 \

@@ -369,11 +369,12 @@ def test_gemm_block_dots_bit_exact(dt, n, k, m):
     assert rel_err(y2, orc.matmul(ORC[dt], x, wq, k)) <= TOL
 
 
-@pytest.mark.parametrize("gen", [{"QMM_MMQ": "2"}, {"QMM_MMQ": "4"}, {"QMM_MMQ": "4", "QMM_MMQ4_BN": "128"}])
+@pytest.mark.parametrize("gen", [{}, {"QMM_MMQ": "2"}, {"QMM_MMQ": "4"}, {"QMM_MMQ": "4", "QMM_MMQ4_BN": "128"}])
 @pytest.mark.parametrize("n,k,m", [(300, 1024, 9), (130, 512, 257), (64, 256, 130)])
 def test_gemm_q4k_generations_bit_exact(monkeypatch, gen, n, k, m):
-    """Both Q4_K GEMM generations (mmq2: per-sub-block VALU scaling; mmq4: split-scale MFMA operands, 128x64
-    and 128x128 tiles) give the oracle's integer block dots and f32 outputs within TOL."""
+    """Every Q4_K GEMM generation (the default mmqs: split-scale int8 d term, bf16 mins term; mmq2: per-sub-block
+    VALU scaling; mmq4: split-scale MFMA operands, 128x64 and 128x128 tiles) gives the oracle's integer block
+    dots and f32 outputs within TOL."""
     for key, val in gen.items():
         monkeypatch.setenv(key, val)
     w = np.concatenate([normal(180 + n, (n, k), 0.02), special_weight_rows(k)[:4]])
