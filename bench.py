@@ -629,6 +629,36 @@ def kernel_only(torch, dev, which, launches):
         torch.cuda.synchronize()
         print(json.dumps({"kernel_only": "moe", "launches": launches}), flush=True)
         return
+    if which.startswith("read_"):
+        # plain streaming read of a buffer of the GEMV launches' sizes (q 9.5 MB, gate 33 MB, the five-weight
+        # launch 80 MB, 1 GB), rotating copies over > 512 MB: the ceiling a launch of that size can reach
+        from inference_amd import qmm
+        L = qmm.lib()
+        nbytes = {"read_9mb": 9469952, "read_33mb": 33103872, "read_80mb": 80371712, "read_1gb": 1 << 30}[which]
+        nbytes = (nbytes + 15) // 16 * 16
+        nc = max(1, -(-(640 << 20) // nbytes))
+        bufs = [torch.ones(nbytes // 4, dtype=torch.float32, device=dev) for _ in range(nc)]
+        sink = torch.zeros(1, dtype=torch.int32, device=dev)
+        for i in range(launches):
+            qmm._check(L.qmm_stream_read(bufs[i % nc].data_ptr(), nbytes, sink.data_ptr(), 0, qmm._stream(dev)))
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel_only": which, "bytes": nbytes, "copies": nc, "launches": launches}), flush=True)
+        return
+    if which == "decode":
+        # config 3: the 8B-shape Q4_K_M model, a 128-token prompt through the batched prefill, then
+        # `launches` token steps run eagerly (every kernel of a step is its own dispatch in a trace)
+        from inference_amd.llama_decode import DecodeSession, LlamaConfig, LlamaWeights
+        cfg = LlamaConfig.llama3_8b()
+        w = LlamaWeights.random(cfg, 4, dev)
+        prompt = [int(t) for t in np.random.default_rng(4).integers(0, cfg.vocab, 128)]
+        sess = DecodeSession(w, 128 + launches)
+        sess.reset(prompt)
+        sess.prefill()
+        sess.run(launches, use_graph=False)
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel_only": "decode", "steps": launches, "positions": [127, 127 + launches - 1]}),
+              flush=True)
+        return
     if which in ("q8_0", "down_q6k"):
         # config 1: the Q8_0 4096x4096 matvec, one qmm_matmul (fused Q8_0 prologue) per launch; or the
         # decode step's Q6_K down projection 4096x14336 with a pre-quantized Q8_K row. Rotated copies.
@@ -720,7 +750,8 @@ def main():
                          "per projection")
     ap.add_argument("--decode-tokens", type=int, default=256, help="config-3 generated tokens (0 = skip)")
     ap.add_argument("--kernel-only", choices=("gate", "qkvgu", "qkvgu_staged", "copy", "gemm_gate", "gemm_down", "moe",
-                                              "q8_0", "down_q6k"),
+                                              "q8_0", "down_q6k", "decode", "read_9mb", "read_33mb",
+                                              "read_80mb", "read_1gb"),
                     default=None,
                     help="launch only one GEMV launch kind or a calibration copy --steps times (counter runs)")
     args = ap.parse_args()

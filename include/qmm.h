@@ -417,6 +417,13 @@ int qmm_gguf_meta_string(const qmm_gguf *g, int64_t i, int64_t elem, const char 
  * gguf.rs:333-356: torch row k * hd/2 + j of a head is GGUF row 2j + k). */
 int qmm_gguf_load_qtensor(const qmm_gguf *g, int64_t i, int unpermute_heads, void *stream, qmm_qtensor **out);
 
+/* Measurement aid, no counterpart in the reference: a plain streaming read
+ * of `bytes` (a multiple of 16) at `data` on the device, the ceiling a
+ * weight-streaming launch of the same size is measured against.
+ * wgs_per_cu workgroups of 256 threads per CU (<= 0: 8); `sink` (one word)
+ * is written only if the folded data equals a fixed constant. */
+int qmm_stream_read(const void *data, size_t bytes, uint32_t *sink, int wgs_per_cu, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

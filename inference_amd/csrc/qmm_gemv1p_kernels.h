@@ -235,7 +235,10 @@ __device__ __forceinline__ void gemv1p(const GemvJobs& jobs, const void* __restr
 
 QMM_GEMV1P_KERNELS(qmm::kFmtQ4K, q4k, 1)
 QMM_GEMV1P_KERNELS(qmm::kFmtQ4K, q4k, 2)
+QMM_GEMV1P_KERNELS(qmm::kFmtQ4K, q4k, 4)
 QMM_GEMV1P_KERNELS(qmm::kFmtQ6K, q6k, 1)
 QMM_GEMV1P_KERNELS(qmm::kFmtQ6K, q6k, 2)
+QMM_GEMV1P_KERNELS(qmm::kFmtQ6K, q6k, 3)
 QMM_GEMV1P_MIX_KERNELS(1)
 QMM_GEMV1P_MIX_KERNELS(2)
+QMM_GEMV1P_MIX_KERNELS(3)

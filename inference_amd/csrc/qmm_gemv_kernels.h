@@ -156,7 +156,10 @@ struct WSlice {
 template <int FMT>
 __device__ __forceinline__ void load_slice(WSlice& s, const uint8_t* __restrict__ wrow,
                                            const uint16_t* __restrict__ drow, uint32_t b, int l) {
-  // 32-bit offsets from the uniform row base (global_load with a scalar base)
+  // 32-bit offsets from the uniform row base (global_load with a scalar base).
+  // Plain loads: a lane's two quant loads take alternating 16-byte pieces of
+  // the same cache lines, so a streaming (nontemporal) hint that drops the
+  // lines after the first use measured 25% slower.
   auto ld16 = [wrow](uint32_t o) { return *reinterpret_cast<const uint4*>(wrow + o); };
   if constexpr (FMT == kFmtQ4K) {
     const uint32_t o = b * (uint32_t)kQ4KBytes, ol = o + 32u * (uint32_t)l;

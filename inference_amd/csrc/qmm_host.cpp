@@ -607,9 +607,12 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   if (ring) {
     wv = 16;
     waves_per_cu = 16;
-    // prefetch depth (instantiated: 1, 2)
+    // prefetch depth (instantiated: Q4_K 1, 2, 4; Q6_K and mixed 1, 2, 3)
     int pd = fmt == kFmtQ4K ? 1 : 2;
-    if (tu.gemv1p > 0) pd = std::min(tu.gemv1p, 2);
+    if (tu.gemv1p > 0) {
+      pd = std::min(tu.gemv1p, fmt == kFmtQ4K && !mixed ? 4 : 3);
+      if (fmt == kFmtQ4K && !mixed && pd == 3) pd = 2;
+    }
     snprintf(name, sizeof(name), "qmm_gemv1p%s_%s_w16_p%d%s", fused ? "f" : "", mixed ? "q4k6k" : fmt_name(fmt), pd,
              jcap > 4 ? "_j8" : "");
   } else if (silu) {
@@ -1195,6 +1198,16 @@ int qmm_prefill_attention(const float* q, int64_t ldq, const float* kcache, cons
   QMM_HIP(hipModuleLaunchKernel(fn, (unsigned)kv_heads, (unsigned)count, 1, 256, 1, 1, 0, (hipStream_t)stream, args,
                                 nullptr));
   return QMM_OK;
+}
+
+int qmm_stream_read(const void* data, size_t bytes, uint32_t* sink, int wgs_per_cu, void* stream) {
+  if (!data || !sink || bytes == 0 || bytes % 16) return fail(QMM_ERR_INVALID, "stream_read: bytes must be a positive multiple of 16");
+  Device* d;
+  QMM_TRY(current_device(&d));
+  long long n16 = (long long)(bytes / 16);
+  const int per = wgs_per_cu > 0 ? wgs_per_cu : 8;
+  void* args[] = {&data, &n16, &sink};
+  return launch(d, "qmm_stream_read", (unsigned)(d->num_cu * per), 256, 0, (hipStream_t)stream, args);
 }
 
 int qmm_silu_mul(const float* g, const float* u, float* h, int64_t n, void* stream) {

@@ -9,3 +9,4 @@
 #include "qmm_mmq_kernels.h"
 #include "qmm_moe_kernels.h"
 #include "qmm_decode_kernels.h"
+#include "qmm_calib_kernels.h"

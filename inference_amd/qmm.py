@@ -59,6 +59,7 @@ EXPORTS = (
     "qmm_gguf_meta_u64", "qmm_gguf_meta_i64", "qmm_gguf_meta_f64", "qmm_gguf_meta_string",
     "qmm_gguf_load_qtensor", "qmm_qtensor_dequantize_to", "qmm_embed_rows_n", "qmm_rope_kv_append_n",
     "qmm_prefill_attention", "qmm_silu_mul", "qmm_matmul_q_workspace_size", "qmm_matmul_noalloc",
+    "qmm_stream_read",
 )
 
 
@@ -149,6 +150,7 @@ def lib() -> ctypes.CDLL:
             "qmm_prefill_attention": ([vp, i64, vp, vp, i64, i64, vp, i64, i32, i32, i32, i32, ctypes.c_float, vp],
                                       i32),
             "qmm_silu_mul": ([vp, vp, vp, i64, vp], i32),
+            "qmm_stream_read": ([vp, ctypes.c_size_t, vp, i32, vp], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
