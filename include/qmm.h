@@ -233,10 +233,12 @@ int qmm_rope_kv_append(float *q, float *k, const float *v, const float *cos_t, c
 
 /* Workspace bytes of the two attention calls below (0 for an unsupported
  * geometry): heads % kv_heads == 0, heads / kv_heads <= 8, head_dim in
- * {64, 128, 256}, max_seq <= 4096. The workspace starts with one completion
- * counter per kv head (a 256-byte-aligned region), then per-chunk partial
- * results; it must be zero before its first use, and every call leaves the
- * counters at zero. Calls that share a workspace must not run concurrently. */
+ * {64, 128, 256}, 1 <= max_seq <= 1048576. The workspace starts with one
+ * completion counter per kv head (a 256-byte-aligned region), then per-chunk
+ * partial results; it must be zero before its first use, and every call
+ * leaves the counters at zero. Calls that share a workspace must not run
+ * concurrently; calls with workspaces of their own may run on concurrent
+ * streams. */
 size_t qmm_decode_attention_workspace_size(int heads, int kv_heads, int head_dim, int max_seq);
 
 /* One query per head against cache positions 0..pos[0]: out[h] =

@@ -104,22 +104,25 @@ extern "C" __global__ void qmm_prefill_rope_kv(float* __restrict__ q, float* __r
 //
 // Workgroup (g, c) of a kv_heads x S grid takes the G = heads / kv_heads
 // query heads of kv head g (repeat_kv maps query head h to kv head h / G)
-// and the c-th of S contiguous chunks of the n = p + 1 positions. Its four
+// and the c-th of S contiguous chunks of the n = p + 1 positions. Its NW
 // waves scan the chunk's positions round-robin straight from the cache: lane
 // l holds dims [l * dim/64, (l+1) * dim/64) of q, k_j and v_j, so a score
 // s_j = (q . k_j) * scale is a wave-wide sum (DPP + v_readlane) and the
 // softmax runs online per wave, a batch of positions at a time (m = running
 // max, l = sum exp(s - m), o = sum exp(s - m) v). The next batch's k/v rows
-// are loaded while the current batch is scored. The waves' states are combined through LDS into the
-// chunk's record (m, l, o[dim]) per head. Records are stored with
-// device-scope (agent) atomic stores, which write through the XCD's L2 to
-// the device-coherent level; after s_waitcnt vmcnt(0) and a barrier, one
-// thread bumps the kv head's counter with a device-scope atomic. The
-// workgroup that brings it to S is the last of its kv head: it reads the S
-// records back with device-scope atomic loads (coherent, not served from a
-// stale L2 line), forms out = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c
-// (M = max_c m_c, chunks in order) and resets the counter to zero, so the
-// workspace is ready for the next launch.
+// are loaded while the current batch is scored. The waves' states are
+// combined through LDS.
+//
+// The chunk's record (m, l, o[dim]) per head goes to the workspace with
+// plain stores; after a barrier, one thread bumps the kv
+// head's counter with a device-scope (agent) acquire-release atomic: the
+// release makes the workgroup's records visible at device scope before the
+// count, and in the workgroup that brings the count to S (the last of its kv
+// head) the acquire, followed by a barrier, makes every other workgroup's
+// records visible to its plain loads. That workgroup forms
+// out = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c (M = max_c m_c,
+// chunks in order) and resets the counter to zero, so the workspace is ready
+// for the next launch.
 //
 // With cos/sin (fused RoPE + KV append), q and k are the unrotated
 // projections: q is rotated in registers (the partner of dim d is in lane
@@ -128,7 +131,7 @@ extern "C" __global__ void qmm_prefill_rope_kv(float* __restrict__ q, float* __r
 // q is already rotated and the cache already holds position p.
 // dim = 64 * DPL (64, 128, 256); G <= GT (1, 2, 4, 8).
 namespace qmm {
-constexpr int kAttnSplits = 16;  // S; chunk length <= 256 for max_seq <= 4096
+constexpr int kAttnSplits = 16;  // S
 
 template <int DPL>
 __device__ __forceinline__ void attn_row(float (&dst)[DPL], const float* __restrict__ row, int lane) {
@@ -347,30 +350,33 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
       continue;
     }
     float* r = part + ((size_t)c * heads + g * G + h) * rec;
-    __hip_atomic_store(r + 2 + d, osum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    r[2 + d] = osum;
     if (d == 0) {
-      __hip_atomic_store(r, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(r + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      r[0] = M;
+      r[1] = lsum;
     }
   }
   if constexpr (PREFILL) return;
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this thread's record stores are acknowledged
+  // every thread's record stores have completed before the barrier, so they
+  // precede thread 0's release
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
   __syncthreads();
   if (t == 0)
-    last = __hip_atomic_fetch_add(counters + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+    last = __hip_atomic_fetch_add(counters + g, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
   __syncthreads();
   if (!last) return;
 
-  // last workgroup of kv head g: merge the S chunk records of its G heads
+  // last workgroup of kv head g (its acquire precedes these loads through the
+  // barrier): merge the S chunk records of its G heads
   for (int i = t; i < G * dim; i += NT) {
     const int h = g * G + i / dim, d = i % dim;
     float mc[S], lc[S], oc[S];
 #pragma unroll
     for (int cc = 0; cc < S; ++cc) {
       const float* r = part + ((size_t)cc * heads + h) * rec;
-      mc[cc] = __hip_atomic_load(r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      lc[cc] = __hip_atomic_load(r + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      oc[cc] = __hip_atomic_load(r + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      mc[cc] = r[0];
+      lc[cc] = r[1];
+      oc[cc] = r[2 + d];
     }
     float M = -INFINITY;
 #pragma unroll
@@ -405,6 +411,7 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
 QMM_ATTN_KERNELS(1)
 QMM_ATTN_KERNELS(2)
 QMM_ATTN_KERNELS(4)
+
 
 // Causal attention of a prompt's rows (batched prefill): grid kv_heads x rows.
 #define QMM_PREFILL_ATTN_KERNEL(DPL, GT)                                                                         \

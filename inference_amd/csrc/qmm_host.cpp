@@ -1066,14 +1066,19 @@ int qmm_rope_kv_append(float* q, float* k, const float* v, const float* cos_t, c
 // Workspace of the attention: one counter per kv head (a 256-byte-aligned
 // region), then S chunks x heads x (m, l, o[head_dim]) floats.
 static const int kAttnSplits = 16;  // must equal the kernel's qmm::kAttnSplits
+// Positions per cache: the kernels index positions with 32-bit integers and
+// the cache with 64-bit offsets; 2^20 keeps every position count, and each
+// chunk's scan, far inside that.
+static const int kAttnMaxSeq = 1 << 20;
+
 
 static int check_attention(int heads, int kv_heads, int head_dim, int max_seq) {
   if (heads < 1 || kv_heads < 1 || heads % kv_heads || heads / kv_heads > 8)
     return fail(QMM_ERR_INVALID, "attention needs heads %% kv_heads == 0 and heads / kv_heads <= 8");
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(QMM_ERR_INVALID, "attention head_dim must be 64, 128 or 256 (got %d)", head_dim);
-  if (max_seq < 1 || max_seq > kAttnSplits * 256)
-    return fail(QMM_ERR_INVALID, "attention max_seq must be in [1, %d] (got %d)", kAttnSplits * 256, max_seq);
+  if (max_seq < 1 || max_seq > kAttnMaxSeq)
+    return fail(QMM_ERR_INVALID, "attention max_seq must be in [1, %d] (got %d)", kAttnMaxSeq, max_seq);
   return QMM_OK;
 }
 

@@ -925,12 +925,18 @@ __device__ __forceinline__ void mmq4_q4k(const uint8_t* __restrict__ wq, const i
 //   * the mins term sum_b dx * dmin * sum_j m_j S_j (S_j the 32-element sums of
 //     the activation codes) is a dense product over (super-block, sub-block)
 //     of A'[m][b, j] = dx * S_j and B'[b, j][n] = -dmin * m_j. Both factors
-//     are formed in f32 while a K step is staged and split into bf16 hi + lo
-//     halves; two v_mfma_f32_32x32x16_bf16 per tile and super-block
-//     ([hi_A | lo_A] . [hi_B | hi_B] and [hi_A | lo_A] . [lo_B | 0]) accumulate
-//     hi*hi + lo*hi + hi*lo in f32 across all super-blocks, no per-step
-//     epilogue. The dropped lo*lo term and the halves' rounding leave a
-//     relative error of about 2^-16 on the mins term;
+//     are formed in f32 while a K step is staged (B' exactly: an f16 times a
+//     6-bit integer; A' rounded once) and split into three bf16 pieces each,
+//     v = v1 + v2 + v3 exactly (8 + 8 + 8 significant bits). Three
+//     v_mfma_f32_32x32x16_bf16 per tile and super-block, K-packed as
+//     [a1 | a2] . [b1 | b1], [a1 | a2] . [b2 | b2] and [a1 | a3] . [b3 | b1],
+//     accumulate every product of order <= 2 (a1b1, a2b1, a1b2, a2b2, a1b3,
+//     a3b1) in f32 across all super-blocks, no per-step epilogue; the dropped
+//     products are below 2^-24 of the term, so the mins term carries f32
+//     rounding like the reference's own sum. (Two pieces, 16 of the 24 and 17
+//     bits, left about 2^-16, which the near-cancellation of the d and mins
+//     terms for zero-mean weights raised to ~1e-4 of an output's rms; f32
+//     MFMAs, four per tile, cost 10% of the kernel time);
 //   * workgroup tile 128 x 128, eight waves (two per SIMD, so one wave's
 //     VALU epilogue and LDS waits overlap the other's MFMAs), two along M and
 //     four along N; a wave owns 64 rows (two M tiles) x 32 columns, so a
@@ -949,13 +955,12 @@ __device__ __forceinline__ void mmq4_q4k(const uint8_t* __restrict__ wq, const i
 // DUMP instantiations also compute ism exactly (two zero-padded int8 MFMAs)
 // and write the integer block dots, which equal mmq2's.
 // ---------------------------------------------------------------------------
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kSBM = 128, kSBN = 128;          // workgroup tile
 constexpr int kSThreads = 512;                 // eight waves: two along M, four along N
 constexpr int kSTM = 2;                        // M tiles (32 rows) per wave
-constexpr int kSHalf = 48;                     // A' / B' row: bf16 hi[8] | lo[8] | 16 B pad (odd 16-byte stride)
+constexpr int kSHalf = 48;                     // A' / B' row: bf16 v1[8] | v2[8] | v3[8] (odd 16-byte stride)
 constexpr int kSOffB = kSBM * kM2AStride;      // LDS: weight blocks
 constexpr int kSOffDx = kSOffB + kSBN * kM2BStride;
 constexpr int kSOffAm = kSOffDx + kSBM * 4;    // A' rows
@@ -1006,19 +1011,31 @@ __device__ __forceinline__ void s_load(SRegs& R, const int8_t* __restrict__ xq, 
   }
 }
 
-// v as bf16 hi (round to nearest even) and the bf16 of the remainder.
-__device__ __forceinline__ void bf16_split(float v, unsigned short& hi, unsigned short& lo) {
-  const __bf16 h = (__bf16)v;
-  hi = __builtin_bit_cast(unsigned short, h);
-  lo = __builtin_bit_cast(unsigned short, (__bf16)(v - (float)h));
-}
-
-__device__ __forceinline__ void s_store_halves(uint8_t* dst, const unsigned short* hi, const unsigned short* lo) {
+// One A' / B' row: each of eight f32 values as three bf16 pieces
+// v = p1 + p2 + p3 (each the round-to-nearest-even of what the previous ones
+// leave; the remainders are exact in f32, so the three carry all 24 bits),
+// stored as p1[8] | p2[8] | p3[8] (48 bytes).
+__device__ __forceinline__ void s_store_row(uint8_t* dst, const float* v) {
+  uint32_t w[3][4];
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    unsigned short p[3][2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      float r = v[j + e];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const __bf16 b = (__bf16)r;
+        p[k][e] = __builtin_bit_cast(unsigned short, b);
+        r -= (float)b;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 3; ++k) w[k][j >> 1] = p[k][0] | ((uint32_t)p[k][1] << 16);
+  }
   uint4* o = reinterpret_cast<uint4*>(dst);
-  o[0] = make_uint4(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16), hi[4] | ((uint32_t)hi[5] << 16),
-                    hi[6] | ((uint32_t)hi[7] << 16));
-  o[1] = make_uint4(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16), lo[4] | ((uint32_t)lo[5] << 16),
-                    lo[6] | ((uint32_t)lo[7] << 16));
+#pragma unroll
+  for (int k = 0; k < 3; ++k) o[k] = make_uint4(w[k][0], w[k][1], w[k][2], w[k][3]);
 }
 
 template <bool DUMP>
@@ -1034,7 +1051,7 @@ __device__ __forceinline__ void s_store(const SRegs& R, uint8_t* buf) {
     const int idx = t + kSThreads * u;
     *reinterpret_cast<uint4*>(buf + kSOffB + (idx >> 3) * kM2BStride + 16 * (1 + (idx & 7))) = R.q[u];
   }
-  unsigned short hi[8], lo[8];
+  float row8[8];
   if (t < 128) {
     // column t's header; B' = -dmin * m_j; the split scales sl_j = sc_j & 7, sh_j = sc_j >> 3 as packed
     // 16-bit pairs (the multipliers of the weight operands)
@@ -1043,8 +1060,8 @@ __device__ __forceinline__ void s_store(const SRegs& R, uint8_t* buf) {
     const float dmin = h2f(hd.x >> 16);
     const uint32_t mn[2] = {hd.z & 0x3f3f3f3fu, ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u)};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) bf16_split(-dmin * (float)((mn[j >> 2] >> (8 * (j & 3))) & 0xffu), hi[j], lo[j]);
-    s_store_halves(buf + kSOffBm + kSHalf * t, hi, lo);
+    for (int j = 0; j < 8; ++j) row8[j] = -dmin * (float)((mn[j >> 2] >> (8 * (j & 3))) & 0xffu);
+    s_store_row(buf + kSOffBm + kSHalf * t, row8);
     const uint32_t sc[2] = {hd.y & 0x3f3f3f3fu, (hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u)};
     uint32_t v[16];
 #pragma unroll
@@ -1062,8 +1079,8 @@ __device__ __forceinline__ void s_store(const SRegs& R, uint8_t* buf) {
     reinterpret_cast<float*>(buf + kSOffDx)[c] = R.dx;
     const int16_t* sv = reinterpret_cast<const int16_t*>(&R.e);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) bf16_split(R.dx * (float)sv[j], hi[j], lo[j]);
-    s_store_halves(buf + kSOffAm + kSHalf * c, hi, lo);
+    for (int j = 0; j < 8; ++j) row8[j] = R.dx * (float)sv[j];
+    s_store_row(buf + kSOffAm + kSHalf * c, row8);
     if (DUMP) {
       uint32_t sl[2] = {0, 0}, sh[2] = {0, 0};
 #pragma unroll
@@ -1076,6 +1093,8 @@ __device__ __forceinline__ void s_store(const SRegs& R, uint8_t* buf) {
     }
   }
 }
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -1136,7 +1155,9 @@ __device__ __forceinline__ void mmqs_mfma(const uint8_t* __restrict__ buf, i32x1
 }
 
 // The floating part of one K step from the same LDS stage: the mins term on
-// the bf16 matrix cores and acc += (dx * d) * isd.
+// the bf16 matrix cores (lane half h supplies K half h of each MFMA: pieces
+// [a1 | a2] x [b1 | b1], [a1 | a2] x [b2 | b2], [a1 | a3] x [b3 | b1]) and
+// acc += (dx * d) * isd.
 __device__ __forceinline__ void mmqs_epi(const uint8_t* __restrict__ buf, const i32x16 (&accl)[kSTM],
                                          const i32x16 (&acch)[kSTM], f32x16 (&acc)[kSTM], int wm, int r, int h,
                                          int bcol) {
@@ -1144,14 +1165,17 @@ __device__ __forceinline__ void mmqs_epi(const uint8_t* __restrict__ buf, const 
   const float* DX = reinterpret_cast<const float*>(buf + kSOffDx);
   const float dw = h2f(*reinterpret_cast<const uint32_t*>(buf + kSOffB + bcol * kM2BStride));
   const uint8_t* bmp = buf + kSOffBm + kSHalf * bcol;
-  const bf16x8 bm1 = *reinterpret_cast<const bf16x8*>(bmp);
-  const uint4 lo4 = *reinterpret_cast<const uint4*>(bmp + 16);
-  const bf16x8 bm2 = __builtin_bit_cast(bf16x8, h == 0 ? lo4 : make_uint4(0, 0, 0, 0));
+  const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(bmp);
+  const bf16x8 b2 = *reinterpret_cast<const bf16x8*>(bmp + 16);
+  const bf16x8 b31 = *reinterpret_cast<const bf16x8*>(bmp + (h == 0 ? 32 : 0));
 #pragma unroll
   for (int i = 0; i < kSTM; ++i) {
-    const bf16x8 am = *reinterpret_cast<const bf16x8*>(buf + kSOffAm + kSHalf * (arow0 + 32 * i) + 16 * h);
-    acc[i] = mfma_bf16(am, bm1, acc[i]);
-    acc[i] = mfma_bf16(am, bm2, acc[i]);
+    const uint8_t* amp = buf + kSOffAm + kSHalf * (arow0 + 32 * i);
+    const bf16x8 a12 = *reinterpret_cast<const bf16x8*>(amp + 16 * h);
+    const bf16x8 a13 = *reinterpret_cast<const bf16x8*>(amp + 32 * h);
+    acc[i] = mfma_bf16(a12, b1, acc[i]);
+    acc[i] = mfma_bf16(a12, b2, acc[i]);
+    acc[i] = mfma_bf16(a13, b31, acc[i]);
   }
 #pragma unroll
   for (int i = 0; i < kSTM; ++i) {

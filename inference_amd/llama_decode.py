@@ -221,6 +221,12 @@ class DecodeSession:
         self.cfg, self.w, self.max_seq = cfg, weights, max_seq
         dev = weights.embed.device
         self.dev = dev
+        L = qmm.lib()
+        self.L = L
+        # the attention's geometry and cache length are checked before anything is allocated
+        wsa = int(L.qmm_decode_attention_workspace_size(cfg.heads, cfg.kv_heads, cfg.head_dim, max_seq))
+        if wsa == 0:
+            raise qmm.QmmError(1, "unsupported attention geometry: " + qmm.last_error())
         f32 = dict(dtype=torch.float32, device=dev)
         self.x = torch.zeros(cfg.hidden, **f32)
         self.q = torch.zeros(cfg.heads * cfg.head_dim, **f32)
@@ -243,13 +249,8 @@ class DecodeSession:
         self.prompt_len = 0
         self.steps_done = 0
         self._graph = None
-        L = qmm.lib()
-        self.L = L
         # workspaces of the attention (per-kv-head counters, then chunk partials) and of the
         # argmax; their counters start at zero and every launch leaves them at zero
-        wsa = int(L.qmm_decode_attention_workspace_size(cfg.heads, cfg.kv_heads, cfg.head_dim, max_seq))
-        if wsa == 0:
-            raise qmm.QmmError(1, "unsupported attention geometry: " + qmm.last_error())
         self.ws_attn = torch.zeros(wsa, dtype=torch.uint8, device=dev)
         self.ws_argmax = torch.zeros(int(L.qmm_greedy_workspace_size(cfg.vocab)), dtype=torch.uint8, device=dev)
         # launch arguments prepared once (ctypes arrays of handles / outputs)
@@ -302,9 +303,9 @@ class DecodeSession:
             kc = self.kcache.data_ptr() + 4 * li * kv_stride
             vc = self.vcache.data_ptr() + 4 * li * kv_stride
             qmm._check(L.qmm_decode_rope_attention(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
-                                                   self.cos.data_ptr(), self.sin.data_ptr(), self.pos.data_ptr(),
-                                                   kc, vc, self.attn.data_ptr(), cfg.heads, cfg.kv_heads, hd,
-                                                   self.max_seq, ctypes.c_float(self.scale),
+                                                   self.cos.data_ptr(), self.sin.data_ptr(),
+                                                   self.pos.data_ptr(), kc, vc, self.attn.data_ptr(), cfg.heads,
+                                                   cfg.kv_heads, hd, self.max_seq, ctypes.c_float(self.scale),
                                                    self.ws_attn.data_ptr(), self.ws_attn.numel(), s))
             tr("attention", li)
             qmm._check(L.qmm_matmul_ex(self._o[li], 1, self.attn.data_ptr(), 1, cfg.heads * hd, None, eps, 1,

@@ -171,7 +171,18 @@ def test_decode_position_bounds(small_model):
     with pytest.raises(QmmError):
         sess.reset([cfg.vocab])
     with pytest.raises(QmmError):
-        DecodeSession(w, 5000)  # attention supports up to 4096 positions
+        DecodeSession(w, (1 << 20) + 1)  # attention supports up to 2^20 positions (checked before allocating)
+
+
+@pytest.mark.parametrize("prompt_len,steps", [(250, 270), (4500, 4509)])
+def test_decode_long_context(small_model, prompt_len, steps):
+    """A long prompt through the batched prefill, then greedy steps on one captured graph, every step's
+    logits against the oracle run token by token over all positions: 250 + 20 steps cross the attention's
+    switch from one workgroup per kv head to 16 merged chunks (at 256 positions for this geometry) inside
+    one graph; 4500 + 9 steps run past 4096 positions."""
+    cfg, w = small_model
+    prompt = [int(t) for t in np.random.default_rng(8).integers(0, cfg.vocab, prompt_len)]
+    end_to_end(cfg, w, prompt, steps, steps + 64, prefill=True)
 
 
 def test_decode_gqa_single_kv_head():

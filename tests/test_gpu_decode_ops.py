@@ -231,11 +231,13 @@ def attn_ws(heads, kv_heads, hd, max_seq):
 ATTN_GEOM = [(32, 8, 128), (8, 2, 64), (4, 4, 256), (32, 4, 128), (8, 1, 64)]
 
 
+# Positions on both sides of the switch from one workgroup per kv head (n <= 32 x waves: 128, 256 or
+# 512 positions for these geometries) to 16 chunks merged by the last workgroup, and past 4096.
 @pytest.mark.parametrize("heads,kv_heads,hd", ATTN_GEOM)
-@pytest.mark.parametrize("p", [0, 1, 17, 255, 300, 4095])
+@pytest.mark.parametrize("p", [0, 1, 17, 127, 128, 255, 256, 300, 511, 512, 4095, 6000])
 def test_decode_attention(heads, kv_heads, hd, p):
     rng = np.random.default_rng(60 + p)
-    max_seq = 4096
+    max_seq = 6144
     kc = rng.standard_normal((kv_heads, max_seq, hd)).astype(np.float32)
     vc = rng.standard_normal((kv_heads, max_seq, hd)).astype(np.float32)
     q = rng.standard_normal((heads, hd)).astype(np.float32)
@@ -255,11 +257,12 @@ def test_decode_attention(heads, kv_heads, hd, p):
 
 
 @pytest.mark.parametrize("heads,kv_heads,hd", ATTN_GEOM)
-@pytest.mark.parametrize("p", [0, 5, 130, 511])
+@pytest.mark.parametrize("p", [0, 5, 130, 511, 700, 1023])
 def test_decode_rope_attention(heads, kv_heads, hd, p):
-    """Fused RoPE + KV append + attention == rope_kv_append then attention (oracle on the same cache)."""
+    """Fused RoPE + KV append + attention == rope_kv_append then attention (oracle on the same cache);
+    the appending workgroup is chunk 0's below the split threshold and the one whose chunk holds p above."""
     rng = np.random.default_rng(90 + p)
-    max_seq = 512
+    max_seq = 1024
     cfg = LlamaConfig(heads=heads, kv_heads=kv_heads, head_dim=hd)
     cos, sin = rope_tables(cfg, max_seq)
     kc = rng.standard_normal((kv_heads, max_seq, hd)).astype(np.float32)
@@ -290,8 +293,60 @@ def test_decode_rope_attention(heads, kv_heads, hd, p):
     np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-4, atol=2e-5)
 
 
+def test_two_streams_own_workspaces():
+    """Split-path attention (16 chunks, counter merge) and a split-K prefill GEMM, each issued on two
+    streams at once with a workspace per stream, eight rounds: every output equals the one-stream result
+    (attention: to the oracle's tolerance; GEMM: bit for bit), so concurrent calls with their own
+    workspaces do not see each other's counters or partials."""
+    rng = np.random.default_rng(77)
+    heads, kv_heads, hd, max_seq = 32, 8, 128, 4096
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    g = heads // kv_heads
+    ps = (2999, 4000)
+    kc = [rng.standard_normal((kv_heads, max_seq, hd)).astype(np.float32) for _ in ps]
+    vc = [rng.standard_normal((kv_heads, max_seq, hd)).astype(np.float32) for _ in ps]
+    q = [rng.standard_normal((heads, hd)).astype(np.float32) for _ in ps]
+    want = [np.stack([ol.attend_one(q[i][h], kc[i][h // g, : p + 1], vc[i][h // g, : p + 1], scale)
+                      for h in range(heads)]) for i, p in enumerate(ps)]
+    dev_in = [(t(q[i]), t(kc[i]), t(vc[i]), t(np.array([p], np.int32), torch.int32)) for i, p in enumerate(ps)]
+    outs = [torch.zeros((heads, hd), device=DEV) for _ in ps]
+    wss = [attn_ws(heads, kv_heads, hd, max_seq) for _ in ps]
+    # GEMM: m = 127 rows against a 4096 x 4096 Q4_K weight (split-K partials in the workspace)
+    m, n, k = 127, 4096, 4096
+    w = QTensor.quantize(t((rng.standard_normal((n, k)) * 0.02).astype(np.float32)), GgmlDType.Q4K)
+    xs = [t(rng.standard_normal((m, k)).astype(np.float32)) for _ in ps]
+    wsb = int(L().qmm_matmul_workspace_size(w.handle, m))
+    gws = [torch.zeros(max(wsb, 1), dtype=torch.uint8, device=DEV) for _ in ps]
+    ys = [torch.zeros((m, n), device=DEV) for _ in ps]
+    ref = []
+    for i in range(len(ps)):
+        qmm._check(L().qmm_matmul(w.handle, xs[i].data_ptr(), m, k, ys[i].data_ptr(), n, gws[i].data_ptr(), wsb, S()))
+        ref.append(ys[i].clone())
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for r in range(8):
+        for i, st in enumerate(streams):
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                h = ctypes.c_void_p(st.cuda_stream)
+                qd, kcd, vcd, pos = dev_in[i]
+                outs[i].zero_()
+                ys[i].zero_()
+                qmm._check(L().qmm_decode_attention(qd.data_ptr(), kcd.data_ptr(), vcd.data_ptr(), pos.data_ptr(),
+                                                    outs[i].data_ptr(), heads, kv_heads, hd, max_seq,
+                                                    ctypes.c_float(scale), wss[i].data_ptr(), wss[i].numel(), h))
+                qmm._check(L().qmm_matmul(w.handle, xs[i].data_ptr(), m, k, ys[i].data_ptr(), n, gws[i].data_ptr(),
+                                          wsb, h))
+        for st in streams:
+            torch.cuda.current_stream().wait_stream(st)
+        torch.cuda.synchronize()
+        for i in range(len(ps)):
+            np.testing.assert_allclose(outs[i].cpu().numpy(), want[i], rtol=1e-4, atol=2e-5, err_msg=f"round {r}")
+            assert torch.equal(ys[i], ref[i]), f"round {r} stream {i}"
+
+
 def test_attention_geometry_errors():
-    for bad in [(32, 5, 128, 64), (32, 2, 128, 64), (8, 2, 96, 64), (8, 2, 128, 4097), (8, 2, 128, 0)]:
+    for bad in [(32, 5, 128, 64), (32, 2, 128, 64), (8, 2, 96, 64), (8, 2, 128, (1 << 20) + 1), (8, 2, 128, 0)]:
         assert int(L().qmm_decode_attention_workspace_size(*bad)) == 0
     ws = attn_ws(8, 2, 128, 64)
     x = torch.zeros(16, device=DEV)
