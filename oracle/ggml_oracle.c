@@ -451,6 +451,14 @@ static float make_qx_quants(int n, int nmax, const float *x, int8_t *L, int rmse
     return scale;
 }
 
+void orc_make_qkx1_quants(int nmax, int ntry, const float *x, int n, float *scale, float *neg_min) {
+    make_qkx1_quants(nmax, ntry, x, n, scale, neg_min);
+}
+
+float orc_make_qx_quants(int n, int nmax, const float *x, int8_t *L, int rmse_type) {
+    return make_qx_quants(n, nmax, x, L, rmse_type);
+}
+
 /* BlockQ6K::from_float [upstream k_quants.rs]. */
 static void quantize_q6k(const float *xall, int64_t n, uint8_t *out) {
     int8_t L[QK_K];

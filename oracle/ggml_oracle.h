@@ -66,6 +66,14 @@ int orc_matmul_prequant(int dtype, int64_t m, int64_t k, int64_t n, const void *
  * same integer block dots; they differ only in f32 accumulation order. */
 enum { ORC_IMPL_GENERIC = 0, ORC_IMPL_AVX2 = 1 };
 /* 1 when this CPU runs the AVX2 + FMA bodies. */
+/* Test hooks: the sub-block fits of the weight quantizers (upstream
+ * quantized/utils.rs make_qkx1_quants, make_qx_quants; the static functions
+ * quantize_q4k / quantize_q6k call). make_qkx1_quants returns the scale and
+ * -min of an asymmetric nmax-level fit; make_qx_quants returns the scale and
+ * writes L[i] = l_i + nmax of a symmetric fit. */
+void orc_make_qkx1_quants(int nmax, int ntry, const float *x, int n, float *scale, float *neg_min);
+float orc_make_qx_quants(int n, int nmax, const float *x, int8_t *L, int rmse_type);
+
 int orc_simd_supported(void);
 float orc_vec_dot_avx2(int dtype, int64_t k, const void *w_row, const void *x_row);
 /* orc_matmul_prequant / orc_matmul with a chosen implementation; -1 for an

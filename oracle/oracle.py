@@ -52,6 +52,10 @@ def lib() -> ctypes.CDLL:
         L.orc_matmul_prequant_impl.argtypes = [i32, i64, i64, i64, vp, vp, vp, i32, i32]
         L.orc_vec_dot_avx2.argtypes = [i32, i64, vp, vp]
         L.orc_vec_dot_avx2.restype = ctypes.c_float
+        L.orc_make_qkx1_quants.argtypes = [i32, i32, vp, i32, vp, vp]
+        L.orc_make_qkx1_quants.restype = None
+        L.orc_make_qx_quants.argtypes = [i32, i32, vp, vp, i32]
+        L.orc_make_qx_quants.restype = ctypes.c_float
         for f in ("orc_block_elems", "orc_block_bytes", "orc_vec_dot_type"):
             getattr(L, f).argtypes = [i32]
         _lib = L
@@ -81,6 +85,22 @@ def f32_to_f16_bits(x: float) -> int:
 
 def f16_bits_to_f32(h: int) -> float:
     return lib().orc_f16_to_f32(int(h))
+
+
+def make_qkx1_quants(x: np.ndarray, nmax: int = 15, ntry: int = 5):
+    """The Q4_K sub-block fit (quantized/utils.rs make_qkx1_quants): (scale, -min) of x."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    sc, mn = np.zeros(1, np.float32), np.zeros(1, np.float32)
+    lib().orc_make_qkx1_quants(nmax, ntry, _ptr(x), x.size, _ptr(sc), _ptr(mn))
+    return float(sc[0]), float(mn[0])
+
+
+def make_qx_quants(x: np.ndarray, nmax: int = 32, rmse_type: int = 1):
+    """The Q6_K sub-block fit (quantized/utils.rs make_qx_quants): (scale, l) with l in [-nmax, nmax)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    L = np.zeros(x.size, np.int8)
+    s = lib().orc_make_qx_quants(x.size, nmax, _ptr(x), _ptr(L), rmse_type)
+    return float(s), L.astype(np.int32) - nmax
 
 
 def quantize(dt: int, x: np.ndarray) -> np.ndarray:

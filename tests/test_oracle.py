@@ -332,6 +332,153 @@ def test_q4k_codes_within_range():
     assert sc.max() <= 63 and m.max() <= 63 and q.max() <= 15 and q.min() >= 0
 
 
+# ---------------------------------------------------------------------------
+# weight quantizers: the sub-block fits and the super-block packing pinned by
+# what the mathematics fixes (exact grids, the extremal codes, monotone fits).
+# nearest_int (round half away from zero) is the same function the Q8_0 and
+# Q8_K tie tests above pin.
+# ---------------------------------------------------------------------------
+
+def _q4k_grid_block(rng):
+    """A Q4_K block whose every element lies on its sub-block's grid d_j * l - m_j (l in 0..15, both ends
+    present), d_j = 2^-8 sc_j, m_j = 2^-9 mn_j with 6-bit sc_j, mn_j, one sub-block at sc = 63 and one at
+    mn = 63: every step of the quantizer is exact, so the block must come back bit for bit."""
+    sc = rng.integers(1, 64, 8)
+    mn = rng.integers(0, 64, 8)
+    sc[rng.integers(8)] = 63
+    mn[rng.integers(8)] = 63
+    x = np.zeros(256, np.float32)
+    for j in range(8):
+        l = rng.integers(0, 16, 32)
+        l[rng.choice(32, 2, replace=False)] = [0, 15]
+        x[32 * j:32 * j + 32] = np.float32(sc[j] / 256.0) * l.astype(np.float32) - np.float32(mn[j] / 512.0)
+    return x, sc, mn
+
+
+def test_qkx1_fit_recovers_exact_grid():
+    rng = np.random.default_rng(30)
+    for _ in range(200):
+        d = np.float32(rng.integers(1, 64) / 256.0)
+        m = np.float32(rng.integers(0, 64) / 512.0)
+        l = rng.integers(0, 16, 32)
+        l[rng.choice(32, 2, replace=False)] = [0, 15]
+        x = (d * l.astype(np.float32) - m).astype(np.float32)
+        scale, neg_min = orc.make_qkx1_quants(x)
+        assert scale == d and neg_min == m, (scale, d, neg_min, m)
+
+
+def test_qkx1_min_never_above_zero_and_constant_subblock():
+    """The fitted min is clamped to <= 0 (so -min >= 0 even for sub-blocks entirely above zero, where
+    the least-squares min would be positive); a constant sub-block gives (0, 0)."""
+    rng = np.random.default_rng(36)
+    for t in range(300):
+        x = (rng.standard_normal(32) * 0.1 + (np.float32(1.0) if t % 2 else 0.0)).astype(np.float32)
+        scale, neg_min = orc.make_qkx1_quants(x)
+        assert neg_min >= 0.0 and scale > 0.0, t
+    # every element at or above 1 and the top one far out: the least-squares min of the first fit is > 0
+    x = np.full(32, 1.0, np.float32)
+    x[0] = 3.0
+    assert orc.make_qkx1_quants(x)[1] == 0.0
+    assert orc.make_qkx1_quants(np.full(32, -0.75, np.float32)) == (0.0, 0.0)
+
+
+def _qkx1_err(x, scale, neg_min):
+    """Squared error of the best 4-bit codes for a given (scale, min)."""
+    x = x.astype(np.float64)
+    l = np.clip(np.floor((x + neg_min) / scale + 0.5), 0, 15) if scale > 0 else np.zeros_like(x)
+    return float(((x - (scale * l - neg_min)) ** 2).sum())
+
+
+def test_qkx1_fit_never_worse_than_its_start():
+    """Each pass re-rounds, then solves the least-squares scale and the (non-positive) least-squares min,
+    so the fit's error can only fall from that of its first rounding at iscale = 15 / (max - min(min, 0))."""
+    rng = np.random.default_rng(31)
+    for t in range(400):
+        x = (rng.standard_normal(32) * (0.02 if t % 2 else 1.0) + (0.03 if t % 3 == 0 else 0.0)).astype(np.float32)
+        mn0 = min(float(x.min()), 0.0)
+        iscale0 = 15.0 / (float(x.max()) - mn0)
+        l0 = np.clip(np.floor(iscale0 * (x.astype(np.float64) - mn0) + 0.5), 0, 15)
+        e0 = float(((x - (l0 / iscale0 + mn0)) ** 2).sum())
+        scale, neg_min = orc.make_qkx1_quants(x)
+        assert _qkx1_err(x, scale, neg_min) <= e0 * (1 + 1e-5) + 1e-12, t
+
+
+def test_qx_fit_recovers_exact_grid():
+    rng = np.random.default_rng(32)
+    for _ in range(200):
+        s = np.float32(2.0 ** -rng.integers(4, 12))
+        l = rng.integers(-31, 32, 16)
+        l[rng.integers(16)] = -32  # the largest magnitude: iscale = -32 / max = 1 / s
+        x = (s * l.astype(np.float32)).astype(np.float32)
+        scale, lq = orc.make_qx_quants(x)
+        assert scale == s and np.array_equal(lq, l), (scale, s)
+
+
+def test_qx_refinement_never_increases_weighted_error():
+    """rmse_type 1 (weights x^2): both refinement loops accept a change only when the weighted
+    least-squares objective improves, so the final codes fit no worse than the first rounding."""
+    rng = np.random.default_rng(33)
+    for t in range(400):
+        x = (rng.standard_normal(16) * (0.02 if t % 2 else 3.0)).astype(np.float32)
+        if t % 5 == 0:
+            x[rng.integers(16)] *= 8.0  # an outlier
+        xd = x.astype(np.float64)
+        w = xd * xd
+        i = int(np.argmax(np.abs(x)))
+        iscale = -32.0 / float(x[i])
+        l0 = np.clip(np.where(iscale * xd >= 0, np.floor(iscale * xd + 0.5), np.ceil(iscale * xd - 0.5)), -32, 31)
+
+        def werr(l):
+            sl2 = (w * l * l).sum()
+            return float((w * xd * xd).sum() - ((w * xd * l).sum() ** 2) / sl2) if sl2 > 0 else float((w * xd * xd).sum())
+
+        scale, lq = orc.make_qx_quants(x)
+        assert lq.min() >= -32 and lq.max() <= 31
+        assert werr(lq.astype(np.float64)) <= werr(l0) * (1 + 1e-5) + 1e-18, t
+        # the second loop stops when no single-code move it proposes (l_i -> the least-squares code of
+        # element i given the others) improves sum(w x l)^2 / sum(w l^2): the result is locally optimal
+        lf = lq.astype(np.float64)
+        sx, s2 = (w * xd * lf).sum(), (w * lf * lf).sum()
+        for k in range(16):
+            slx, sl2 = sx - w[k] * xd[k] * lf[k], s2 - w[k] * lf[k] * lf[k]
+            if slx <= 0:
+                continue
+            v = xd[k] * sl2 / slx
+            nl = float(np.clip(np.floor(v + 0.5) if v >= 0 else np.ceil(v - 0.5), -32, 31))
+            if nl != lf[k] and sl2 + w[k] * nl * nl > 0:
+                nx, n2 = slx + w[k] * xd[k] * nl, sl2 + w[k] * nl * nl
+                # (the loop compares f32 sums: an improvement below their rounding may go unseen)
+                assert nx * nx * s2 <= sx * sx * n2 * (1 + 2e-5), (t, k)
+        # the returned scale is the weighted least-squares scale of the returned codes
+        lf = lq.astype(np.float64)
+        assert abs(scale - (w * xd * lf).sum() / (w * lf * lf).sum()) <= 1e-5 * abs(scale)
+
+
+def test_q4k_grid_block_roundtrips_exactly():
+    rng = np.random.default_rng(34)
+    for _ in range(50):
+        x, sc, mn = _q4k_grid_block(rng)
+        raw = orc.quantize(Q4K, x)
+        d, dmin, scq, mq, _ = np_q4k_ints(raw)
+        assert d[0] == 2.0 ** -8 and dmin[0] == 2.0 ** -9
+        assert np.array_equal(scq[0], sc) and np.array_equal(mq[0], mn)
+        np.testing.assert_array_equal(orc.dequantize(Q4K, raw, 256), x)
+
+
+def test_k_quant_extremal_codes():
+    """The super-block scale maps the largest sub-block scale (and min) to the top code: 63 for Q4_K's
+    6-bit scales and mins, -128 for Q6_K's signed 8-bit scales (iscale = -128 / the signed largest)."""
+    rng = np.random.default_rng(35)
+    x = (rng.standard_normal(256 * 200) * np.repeat(rng.uniform(0.01, 3.0, 200), 256)).astype(np.float32)
+    _, _, sc, m, _ = np_q4k_ints(orc.quantize(Q4K, x))
+    assert np.all(sc.max(1) == 63)
+    assert np.all(m.max(1) == 63)
+    q6 = orc.quantize(Q6K, x).reshape(-1, 210)
+    s6 = q6[:, 192:208].view(np.int8).astype(np.int32)
+    big = np.take_along_axis(s6, np.abs(s6).argmax(1)[:, None], 1)[:, 0]
+    assert np.all(big == -128)
+
+
 def _cos(a, b):
     a = a.astype(np.float64).ravel(); b = b.astype(np.float64).ravel()
     return float(a @ b / max(np.linalg.norm(a) * np.linalg.norm(b), 1e-12))
