@@ -352,7 +352,11 @@ int qmm_moe_gemm(const qmm_qtensor *const *w, int count, int experts, const floa
  * [experts*ffn, hidden] and down [experts*hidden, ffn] weights; out f32
  * [tokens, hidden] (row stride ldo) = sum over each token's top-k experts, in
  * increasing expert order, of weight * down(silu(gate(x)) * up(x)).
- * ws: device scratch of qmm_moe_ffn_workspace_size() bytes. */
+ * Any token count: a list longer than the routing limit (min(4096, 8192 /
+ * topk) tokens) runs as consecutive chunks of that many tokens, in stream
+ * order through the same workspace; tokens are routed and combined
+ * independently, so the result is the whole list's.
+ * ws: device scratch of qmm_moe_ffn_workspace_size() bytes (one chunk's). */
 size_t qmm_moe_ffn_workspace_size(const qmm_qtensor *gate, const qmm_qtensor *down, int64_t tokens,
                                   int experts, int topk);
 int qmm_moe_ffn(const float *x, int64_t tokens, int64_t ldx, const float *logits, int experts, int topk,

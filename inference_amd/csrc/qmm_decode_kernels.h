@@ -113,16 +113,30 @@ extern "C" __global__ void qmm_prefill_rope_kv(float* __restrict__ q, float* __r
 // are loaded while the current batch is scored. The waves' states are
 // combined through LDS.
 //
-// The chunk's record (m, l, o[dim]) per head goes to the workspace with
-// plain stores; after a barrier, one thread bumps the kv
-// head's counter with a device-scope (agent) acquire-release atomic: the
-// release makes the workgroup's records visible at device scope before the
-// count, and in the workgroup that brings the count to S (the last of its kv
-// head) the acquire, followed by a barrier, makes every other workgroup's
-// records visible to its plain loads. That workgroup forms
+// The chunk's record (m, l, o[dim]) per head goes to the workspace; one
+// thread then bumps the kv head's counter with a device-scope (agent)
+// atomic, and the workgroup that brings it to S is the last of its kv head:
+// it reads the S records back, forms
 // out = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c (M = max_c m_c,
 // chunks in order) and resets the counter to zero, so the workspace is ready
 // for the next launch.
+//
+// Ordering. Every access to the records is an agent-scope atomic (relaxed),
+// so the protocol is the memory model's release/acquire sequence without the
+// cache maintenance that only non-atomic data needs. On gfx942/gfx950 an
+// agent-scope release is "buffer_wbl2 sc1; s_waitcnt vmcnt(0)" and an
+// acquire "s_waitcnt vmcnt(0); buffer_inv sc1" (LLVM AMDGPUUsage, memory
+// model GFX942): the L2 writeback makes earlier plain stores visible across
+// the XCDs' separate L2s, the invalidate keeps later plain loads from stale
+// L2 lines. Agent-scope atomic stores and loads carry sc1 themselves (the
+// store writes through the L2, the load is served from the device-coherent
+// level), so neither is needed for them; what remains is the wait: each
+// thread's s_waitcnt vmcnt(0) before the barrier completes its record
+// stores before thread 0's counter atomic is issued, and the reader's loads
+// are issued after the atomic's result is back. The full acquire-release
+// form (plain records, acq_rel counter) was measured: its whole-L2 writeback
+// and invalidate in every workgroup cost 1.4% of decode throughput (config 3:
+// 488 vs 495 tok/s).
 //
 // With cos/sin (fused RoPE + KV append), q and k are the unrotated
 // projections: q is rotated in registers (the partner of dim d is in lane
@@ -350,33 +364,33 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
       continue;
     }
     float* r = part + ((size_t)c * heads + g * G + h) * rec;
-    r[2 + d] = osum;
+    __hip_atomic_store(r + 2 + d, osum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (d == 0) {
-      r[0] = M;
-      r[1] = lsum;
+      __hip_atomic_store(r, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(r + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   if constexpr (PREFILL) return;
   // every thread's record stores have completed before the barrier, so they
-  // precede thread 0's release
+  // precede thread 0's counter atomic
   __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
   __syncthreads();
   if (t == 0)
-    last = __hip_atomic_fetch_add(counters + g, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+    last = __hip_atomic_fetch_add(counters + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
   __syncthreads();
   if (!last) return;
 
-  // last workgroup of kv head g (its acquire precedes these loads through the
-  // barrier): merge the S chunk records of its G heads
+  // last workgroup of kv head g (its loads issue after the counter's result):
+  // merge the S chunk records of its G heads
   for (int i = t; i < G * dim; i += NT) {
     const int h = g * G + i / dim, d = i % dim;
     float mc[S], lc[S], oc[S];
 #pragma unroll
     for (int cc = 0; cc < S; ++cc) {
       const float* r = part + ((size_t)cc * heads + h) * rec;
-      mc[cc] = r[0];
-      lc[cc] = r[1];
-      oc[cc] = r[2 + d];
+      mc[cc] = __hip_atomic_load(r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      lc[cc] = __hip_atomic_load(r + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      oc[cc] = __hip_atomic_load(r + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     float M = -INFINITY;
 #pragma unroll

@@ -172,6 +172,32 @@ def test_moe_ffn_default_picks_grouped_at_prefill_sizes(monkeypatch):
     assert torch.equal(y, moe_ffn(xd, ld, gate, up, down, k))
 
 
+@pytest.mark.parametrize("k,T", [(2, 4096 + 300), (8, 1024 * 2 + 77)])
+def test_moe_ffn_beyond_routing_limit(k, T):
+    """More tokens than one routing launch takes (4096 at top-2, 1024 at top-8): qmm_moe_ffn runs chunks
+    of the limit; the result equals the chunk-by-chunk calls bit for bit, the rows around each seam match
+    the oracle, and qmm_moe_route alone refuses the long list with its limit in the message."""
+    from oracle import moe
+    E, H, F = 8, 256, 512
+    chunk = min(4096, 8192 // k)
+    gate, gper = stacked(E, F, H, GgmlDType.Q4K, 540 + k)
+    up, uper = stacked(E, F, H, GgmlDType.Q4K, 541 + k)
+    down, dper = stacked(E, H, F, GgmlDType.Q6K, 542 + k)
+    x = normal(543 + k, (T, H))
+    lg = logits_for(T, E, "random", 544 + k)
+    xd, ld = torch.from_numpy(x).to(DEV), torch.from_numpy(lg).to(DEV)
+    y = moe_ffn(xd, ld, gate, up, down, k)
+    parts = [moe_ffn(xd[t0:t0 + chunk], ld[t0:t0 + chunk], gate, up, down, k) for t0 in range(0, T, chunk)]
+    assert torch.equal(y, torch.cat(parts))
+    yn = y.cpu().numpy()
+    for t0 in range(chunk, T, chunk):
+        sl = slice(t0 - 4, t0 + 4)
+        y_ref = moe.moe_ffn(x[sl], lg[sl], gper, uper, dper, orc.Q4K, orc.Q6K, k)
+        assert rel_err(yn[sl], y_ref) <= 1e-2
+    with pytest.raises(qmm.QmmError, match="routing limits"):
+        moe_route(ld, k)
+
+
 def test_moe_gemm_rejects_bad_arguments():
     E, N, K = 4, 256, 512
     qt, _ = stacked(E, N, K, GgmlDType.Q4K, 530)
