@@ -629,9 +629,11 @@ def kernel_only(torch, dev, which, launches):
         torch.cuda.synchronize()
         print(json.dumps({"kernel_only": "moe", "launches": launches}), flush=True)
         return
-    if which.startswith("read_"):
-        # plain streaming read of a buffer of the GEMV launches' sizes (q 9.5 MB, gate 33 MB, the five-weight
-        # launch 80 MB, 1 GB), rotating copies over > 512 MB: the ceiling a launch of that size can reach
+    if which.startswith("read_") and which != "read_graph":
+        # plain streaming reads of a buffer of the GEMV launches' sizes (q 9.5 MB, gate 33 MB, the five-weight
+        # launch 80 MB, 1 GB), rotating copies over > 512 MB: every read variant (grid-stride 4 / 8 in flight,
+        # chunked nontemporal) at 8 and 16 workgroups per CU, `launches` each; the fastest is the ceiling a
+        # launch of that size can reach
         from inference_amd import qmm
         L = qmm.lib()
         nbytes = {"read_9mb": 9469952, "read_33mb": 33103872, "read_80mb": 80371712, "read_1gb": 1 << 30}[which]
@@ -639,10 +641,36 @@ def kernel_only(torch, dev, which, launches):
         nc = max(1, -(-(640 << 20) // nbytes))
         bufs = [torch.ones(nbytes // 4, dtype=torch.float32, device=dev) for _ in range(nc)]
         sink = torch.zeros(1, dtype=torch.int32, device=dev)
-        for i in range(launches):
-            qmm._check(L.qmm_stream_read(bufs[i % nc].data_ptr(), nbytes, sink.data_ptr(), 0, qmm._stream(dev)))
+        runs = [(v, w) for v in (0, 1, 2) for w in (8, 16)]
+        for v, w in runs:
+            for i in range(launches):
+                qmm._check(L.qmm_stream_read(bufs[i % nc].data_ptr(), nbytes, sink.data_ptr(), v, w,
+                                             qmm._stream(dev)))
         torch.cuda.synchronize()
-        print(json.dumps({"kernel_only": which, "bytes": nbytes, "copies": nc, "launches": launches}), flush=True)
+        print(json.dumps({"kernel_only": which, "bytes": nbytes, "copies": nc, "launches_per_variant": launches,
+                          "variants_wgs_per_cu": runs}), flush=True)
+        return
+    if which == "read_graph":
+        # the read variants of the read_* modes timed in HIP-graph replays (back-to-back launches over the
+        # rotated copies, median of `launches`-sample spreads) at every size: the graph-replay ceiling
+        from inference_amd import qmm
+        L = qmm.lib()
+        sink = torch.zeros(1, dtype=torch.int32, device=dev)
+        for nbytes in (9469952, 33103872, 80371712, 1 << 30):
+            nc = max(1, -(-(640 << 20) // nbytes))
+            bufs = [torch.ones(nbytes // 4, dtype=torch.float32, device=dev) for _ in range(nc)]
+            for v, name in enumerate(("gs4", "gs8", "ch8nt")):
+                for w in (8, 16):
+                    j = [0]
+
+                    def rd():
+                        qmm._check(L.qmm_stream_read(bufs[j[0] % nc].data_ptr(), nbytes, sink.data_ptr(), v, w,
+                                                     qmm._stream(dev)))
+                        j[0] += 1
+                    sp = timed_graph(torch, rd, max(2 * nc, 4), min(launches, 20 if nbytes > (1 << 29) else 40))
+                    print(json.dumps({"kernel_only": "read_graph", "bytes": nbytes, "variant": name,
+                                      "wgs_per_cu": w, "us": sp}), flush=True)
+            del bufs
         return
     if which == "decode":
         # config 3: the 8B-shape Q4_K_M model, a 128-token prompt through the batched prefill, then
@@ -751,7 +779,7 @@ def main():
     ap.add_argument("--decode-tokens", type=int, default=256, help="config-3 generated tokens (0 = skip)")
     ap.add_argument("--kernel-only", choices=("gate", "qkvgu", "qkvgu_staged", "copy", "gemm_gate", "gemm_down", "moe",
                                               "q8_0", "down_q6k", "decode", "read_9mb", "read_33mb",
-                                              "read_80mb", "read_1gb"),
+                                              "read_80mb", "read_1gb", "read_graph"),
                     default=None,
                     help="launch only one GEMV launch kind or a calibration copy --steps times (counter runs)")
     args = ap.parse_args()

@@ -425,10 +425,13 @@ int qmm_gguf_load_qtensor(const qmm_gguf *g, int64_t i, int unpermute_heads, voi
 
 /* Measurement aid, no counterpart in the reference: a plain streaming read
  * of `bytes` (a multiple of 16) at `data` on the device, the ceiling a
- * weight-streaming launch of the same size is measured against.
- * wgs_per_cu workgroups of 256 threads per CU (<= 0: 8); `sink` (one word)
- * is written only if the folded data equals a fixed constant. */
-int qmm_stream_read(const void *data, size_t bytes, uint32_t *sink, int wgs_per_cu, void *stream);
+ * weight-streaming launch of the same size is measured against. variant:
+ * 0 grid-stride with 4 loads in flight per thread, 1 grid-stride with 8,
+ * 2 one contiguous chunk per workgroup with 8 nontemporal loads in flight
+ * (no variant is fastest at every size). wgs_per_cu workgroups of 256
+ * threads per CU (0: 8; at most 64); `sink` (one word) is written only if
+ * the folded data equals a fixed constant. */
+int qmm_stream_read(const void *data, size_t bytes, uint32_t *sink, int variant, int wgs_per_cu, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1205,14 +1205,17 @@ int qmm_prefill_attention(const float* q, int64_t ldq, const float* kcache, cons
   return QMM_OK;
 }
 
-int qmm_stream_read(const void* data, size_t bytes, uint32_t* sink, int wgs_per_cu, void* stream) {
+int qmm_stream_read(const void* data, size_t bytes, uint32_t* sink, int variant, int wgs_per_cu, void* stream) {
   if (!data || !sink || bytes == 0 || bytes % 16) return fail(QMM_ERR_INVALID, "stream_read: bytes must be a positive multiple of 16");
+  static const char* const names[] = {"qmm_stream_read_gs4", "qmm_stream_read_gs8", "qmm_stream_read_ch8nt"};
+  if (variant < 0 || variant > 2) return fail(QMM_ERR_INVALID, "stream_read: variant must be 0 (gs4), 1 (gs8) or 2 (ch8nt)");
+  if (wgs_per_cu < 0 || wgs_per_cu > 64) return fail(QMM_ERR_INVALID, "stream_read: wgs_per_cu must be in [0, 64]");
   Device* d;
   QMM_TRY(current_device(&d));
   long long n16 = (long long)(bytes / 16);
   const int per = wgs_per_cu > 0 ? wgs_per_cu : 8;
   void* args[] = {&data, &n16, &sink};
-  return launch(d, "qmm_stream_read", (unsigned)(d->num_cu * per), 256, 0, (hipStream_t)stream, args);
+  return launch(d, names[variant], (unsigned)(d->num_cu * per), 256, 0, (hipStream_t)stream, args);
 }
 
 int qmm_silu_mul(const float* g, const float* u, float* h, int64_t n, void* stream) {

@@ -150,7 +150,7 @@ def lib() -> ctypes.CDLL:
             "qmm_prefill_attention": ([vp, i64, vp, vp, i64, i64, vp, i64, i32, i32, i32, i32, ctypes.c_float, vp],
                                       i32),
             "qmm_silu_mul": ([vp, vp, vp, i64, vp], i32),
-            "qmm_stream_read": ([vp, ctypes.c_size_t, vp, i32, vp], i32),
+            "qmm_stream_read": ([vp, ctypes.c_size_t, vp, i32, i32, vp], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
