@@ -65,6 +65,7 @@ def log(msg):
 
 
 SPREAD_SAMPLES = 120  # HIP-event samples behind every median / p10 / p90
+LAUNCH_GRAPH_MIN = 48  # launches per graph when one launch kind is timed alone
 
 
 def replay_samples(torch, g, n, stream):
@@ -226,14 +227,18 @@ def run_gemv_set(torch, dev, args):
     replay_samples(torch, g_step, 4, stream)
     step_spread = spread(replay_samples(torch, g_step, SPREAD_SAMPLES, stream) * 1e3 / per_graph)
 
+    # single-launch graphs hold at least LAUNCH_GRAPH_MIN launches, so a replay's own start-up is a small
+    # share of the per-launch figure
+    per_launch_graph = copies * max(1, -(-LAUNCH_GRAPH_MIN // copies))
+
     def time_launch(fn):
-        """us per launch of fn(layer) alone: SPREAD_SAMPLES replays of a graph of per_graph launches over the
-        rotated copies, HIP events between replays on the stream the graph runs on, after untimed replays
+        """us per launch of fn(layer) alone: SPREAD_SAMPLES replays of a graph of per_launch_graph launches over
+        the rotated copies, HIP events between replays on the stream the graph runs on, after untimed replays
         (the first pass over the copies runs a few % slower). Returns the spread of the per-launch time;
         its mean is the average launch."""
-        g = capture(fn, per_graph)
+        g = capture(fn, per_launch_graph)
         replay_samples(torch, g, 4, stream)
-        return spread(replay_samples(torch, g, SPREAD_SAMPLES, stream) * 1e3 / per_graph)
+        return spread(replay_samples(torch, g, SPREAD_SAMPLES, stream) * 1e3 / per_launch_graph)
 
     # per-shape single launches (pre-quantized activation); each shape rotates
     # its own copies over >= rotate_mb MiB, so no launch reads from the MALL
@@ -247,11 +252,12 @@ def run_gemv_set(torch, dev, args):
         gph = torch.cuda.CUDAGraph()
         gemv(own[0], name)
         torch.cuda.synchronize()
+        passes = max(1, -(-LAUNCH_GRAPH_MIN // nc))
         with torch.cuda.graph(gph):
-            for r in range(nc):
-                gemv(own[r], name)
+            for r in range(nc * passes):
+                gemv(own[r % nc], name)
         replay_samples(torch, gph, 4, stream)  # untimed passes over the copies
-        sp = spread(replay_samples(torch, gph, SPREAD_SAMPLES, stream) * 1e3 / nc)
+        sp = spread(replay_samples(torch, gph, SPREAD_SAMPLES, stream) * 1e3 / (nc * passes))
         us = sp["mean"]
         b = gemv_bytes(dt, n, k)
         per_shape[name] = {"shape": [n, k], "us": round(us, 3), "GB/s": round(b / us / 1e3, 1),
