@@ -40,6 +40,31 @@ def test_python_binding_covers_the_header():
     assert sorted(qmm.EXPORTS) == declared_functions()
 
 
+def _c_params():
+    """{function: [parameter names]} of the header's declarations."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for name, args in re.findall(r"\b(qmm_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        args = " ".join(args.split())
+        out[name] = [] if args in ("", "void") else [re.search(r"(\w+)$", a.strip()).group(1)
+                                                    for a in args.split(",")]
+    return out
+
+
+def test_rust_sys_bindings_mirror_the_header():
+    """include/qmm_sys.rs (the Rust -sys layer; no Rust toolchain here) declares every header function
+    with the same parameter names in the same order (a Rust keyword gets a trailing underscore)."""
+    rs = open(os.path.join(ROOT, "include", "qmm_sys.rs")).read()
+    block = rs[rs.index('extern "C" {'):rs.index("\n}\n", rs.index('extern "C" {'))]
+    rust = {}
+    for name, args in re.findall(r"pub fn (qmm_[a-z0-9_]+)\(([^)]*)\)", block, flags=re.S):
+        rust[name] = [a.split(":")[0].strip().rstrip("_") for a in " ".join(args.split()).split(",") if a.strip()]
+    c = _c_params()
+    assert sorted(rust) == sorted(c) == declared_functions()
+    for name, params in c.items():
+        assert rust[name] == params, name
+
+
 def test_geometry(L):
     # crates/llm/mlx-llm/src/gguf/dequant.rs:752-773 (block geometry KAT)
     assert (L.qmm_block_size(8), L.qmm_type_size(8)) == (32, 34)
