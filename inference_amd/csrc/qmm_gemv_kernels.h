@@ -724,7 +724,6 @@ __device__ __forceinline__ void act1_finish(Act1Regs& r, int nb, uint8_t* lds, c
   static_assert(!MIX || FMT == kFmtQ4K, "mixed layouts: Q4_K then Q6_K");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __shared__ float red[16];
-  __shared__ float den1;
   float4* e = r.e;
   const float4* a = r.a;
   if (!SILU && norm_w != nullptr) {
@@ -739,15 +738,18 @@ __device__ __forceinline__ void act1_finish(Act1Regs& r, int nb, uint8_t* lds, c
     ss = wave_total(ss);
     if (lane == 0) red[wave] = ss;
     __syncthreads();
-    if (threadIdx.x == 0) {
-      float t = 0.0f;
-      for (int w = 0; w < nw; ++w) t += red[w];
-      den1 = sqrtf(t / (float)(256 * nb) + eps);
-    }
-    __syncthreads();
-    const float dn = den1;
+    // every wave adds the waves' partial sums itself, in wave order, so all
+    // waves hold the same denominator without a second barrier (a single
+    // thread summing them and broadcasting through LDS cost one more barrier
+    // and a serial chain of LDS reads)
+    float t = 0.0f;
+    for (int w = 0; w < nw; ++w) t += red[w];
+    const float dn = sqrtf(t / (float)(256 * nb) + eps);
+    // only the wave's own blocks (IEEE divisions are long instruction
+    // sequences; at K = 4096 a 16-wave workgroup holds one block per wave)
 #pragma unroll
     for (int i = 0; i < kActPF; ++i) {
+      if (wave + i * nw >= nb) break;  // wave-uniform
       e[i].x = e[i].x / dn * a[i].x;
       e[i].y = e[i].y / dn * a[i].y;
       e[i].z = e[i].z / dn * a[i].z;
@@ -756,6 +758,7 @@ __device__ __forceinline__ void act1_finish(Act1Regs& r, int nb, uint8_t* lds, c
   } else if (SILU) {
 #pragma unroll
     for (int i = 0; i < kActPF; ++i) {
+      if (wave + i * nw >= nb) break;  // wave-uniform
       e[i].x = silu_mul(e[i].x, a[i].x);
       e[i].y = silu_mul(e[i].y, a[i].y);
       e[i].z = silu_mul(e[i].z, a[i].z);
