@@ -201,7 +201,7 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
   __shared__ __attribute__((aligned(16))) float wo[NW][GT * dim];
   __shared__ int last;
   const int g = blockIdx.x, c = PREFILL ? 0 : blockIdx.y, t = threadIdx.x;
-  const int lane = t & 63, wave = t >> 6;
+  const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int G = heads / kv_heads;
   constexpr int S = PREFILL ? 1 : kAttnSplits;
   const bool rope = !PREFILL && cos_t != nullptr;
@@ -266,6 +266,8 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
   // One batch of B positions (i0 .. i0 + B - 1 of this wave; those past npos
   // are clamped duplicates and weigh nothing): all B x GT scores first (their
   // wave sums are independent), then one online-softmax update per head.
+  // Positions past the wave's last (b >= nv, wave-uniform) are skipped: their
+  // weight would be exactly 0, so the sums are the same without them.
   auto scan = [&](const float (&kb)[B][DPL], const float (&vb)[B][DPL], int i0) {
     const int nv = min(B, npos - i0);
     float sc[B][GT];
@@ -275,15 +277,14 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
 #pragma unroll
       for (int h = 0; h < GT; ++h) {
         float d = 0.0f;
+        if (b < nv) {
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) d += qv[h][e] * (at_p ? kn[e] : kb[b][e]);
+          for (int e = 0; e < DPL; ++e) d += qv[h][e] * (at_p ? kn[e] : kb[b][e]);
+          d = wave_total(d) * scale;
+        }
         sc[b][h] = d;
       }
     }
-#pragma unroll
-    for (int b = 0; b < B; ++b)
-#pragma unroll
-      for (int h = 0; h < GT; ++h) sc[b][h] = wave_total(sc[b][h]) * scale;
 #pragma unroll
     for (int h = 0; h < GT; ++h) {
       float mx = m[h];
@@ -296,8 +297,9 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
       for (int e = 0; e < DPL; ++e) acc[e] = o[h][e] * a;
 #pragma unroll
       for (int b = 0; b < B; ++b) {
+        if (b >= nv) break;
         const bool at_p = rope && j0 + wave + NW * (i0 + b) == p;
-        const float w = b < nv ? expf(sc[b][h] - mx) : 0.0f;
+        const float w = expf(sc[b][h] - mx);
         ls += w;
 #pragma unroll
         for (int e = 0; e < DPL; ++e) acc[e] += w * (at_p ? vn[e] : vb[b][e]);
