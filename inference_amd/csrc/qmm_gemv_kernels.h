@@ -91,8 +91,13 @@ __device__ __forceinline__ int q80_slot(int b, int k) { return k ^ ((b >> 2) & 1
 //     Q4_K sums: lane l -> (bsum_4l + bsum_4l+1) | (bsum_4l+2 + bsum_4l+3) << 16
 //     Q6_K sums: lane l -> two u32: bsums of its chunks (0,1) and (2,3)
 //   Q8_0: q8 [blk][32] (swizzled halves), d f32 [blk]
-template <int FMT, int NW = 0>
-__device__ __forceinline__ void stage_act(const uint8_t* __restrict__ xq, int nblk, uint8_t* lds) {
+// MR > 0 (k-quants, nblk = MR * nb): block b of row m goes to LDS block
+// b * MR + m with its chunks swizzled by b, so a lane's reads of one block
+// for successive rows are fixed offsets apart (256 B of quants, 32 B of sums,
+// 4 B of scale).
+template <int FMT, int NW = 0, int MR = 0>
+__device__ __forceinline__ void stage_act(const uint8_t* __restrict__ xq, int nblk, uint8_t* lds, int nb = 0) {
+  static_assert(MR == 0 || FMT != kFmtQ80, "row-interleaved staging is for k-quant activations");
   const int nthr = 64 * block_waves<NW>();
   if constexpr (FMT == kFmtQ80) {
     float* ld = reinterpret_cast<float*>(lds + 32 * nblk);
@@ -112,15 +117,21 @@ __device__ __forceinline__ void stage_act(const uint8_t* __restrict__ xq, int nb
     uint32_t* lsum = reinterpret_cast<uint32_t*>(lds + 256 * nblk);
     float* ld = reinterpret_cast<float*>(lsum + 8 * nblk);
     for (int t = threadIdx.x; t < 16 * nblk; t += nthr) {
-      const int blk = t >> 4, l = (t >> 2) & 3, k = t & 3;
-      const uint8_t* s = xq + (size_t)kQ8KBytes * blk;
+      const int src = t >> 4, l = (t >> 2) & 3, k = t & 3;
+      int blk = src, swb = src;  // LDS block, swizzle block
+      if constexpr (MR > 0) {
+        const int m = src / nb, b = src - m * nb;
+        blk = b * MR + m;
+        swb = b;
+      }
+      const uint8_t* s = xq + (size_t)kQ8KBytes * src;
       const uint32_t* q = reinterpret_cast<const uint32_t*>(s + 4 + act_chunk<FMT>(l, k));
       uint4 v;
       v.x = q[0];
       v.y = q[1];
       v.z = q[2];
       v.w = q[3];
-      *reinterpret_cast<uint4*>(lds + 256 * blk + 16 * kq_slot(blk, l, k)) = v;
+      *reinterpret_cast<uint4*>(lds + 256 * blk + 16 * kq_slot(swb, l, k)) = v;
       const int16_t* bs = reinterpret_cast<const int16_t*>(s + 4 + 256);
       if (k < 2) {
         const int e0 = act_chunk<FMT>(l, 2 * k) / 16;  // chunks 2k and 2k+1
@@ -303,6 +314,13 @@ __device__ __forceinline__ void load_x(XSlice& x, const uint8_t* __restrict__ ld
   }
 }
 
+// A Q4_K block's d * isd - dmin * ism with one fixed rounding sequence (the
+// d product fused), so every kernel that forms it (one-row, multi-row,
+// expert GEMVs) gets the same bits.
+__device__ __forceinline__ float q4k_combine(float dw, float dm, int isd, int ism) {
+  return __builtin_fmaf(dw, (float)isd, -(dm * (float)ism));
+}
+
 // One lane's f32 contribution for one block; its integer partials go to ia / ib.
 template <int FMT>
 __device__ __forceinline__ float dot_wx(const WPrep& w, const XSlice& x, int& ia, int& ib) {
@@ -313,10 +331,9 @@ __device__ __forceinline__ float dot_wx(const WPrep& w, const XSlice& x, int& ia
     // |s0|, |s1| <= 32*15*128 < 2^23 and scales/mins < 64: full-rate 24-bit products
     const int isd = __mul24(w.c0, s0) + __mul24(w.c1, s1);
     const int ism = __mul24(w.c2, bs0) + __mul24(w.c3, bs1);
-    const float t = w.dw * (float)isd - w.dm * (float)ism;
     ia = isd;
     ib = ism;
-    return x.d * t;
+    return x.d * q4k_combine(w.dw, w.dm, isd, ism);
   } else if constexpr (FMT == kFmtQ6K) {
     const int t0 = dot16(w.w0, x.x0, 0) - 32 * (int)(int16_t)(x.s0 & 0xffffu);
     const int t1 = dot16(w.w1, x.x1, 0) - 32 * ((int)x.s0 >> 16);

@@ -1294,8 +1294,11 @@ int qmm_moe_route(const float* logits, int64_t tokens, int experts, int topk, in
   return launch(d, "qmm_moe_route", 1, 256, 0, (hipStream_t)stream, args);
 }
 
-int qmm_moe_gemv(const qmm_qtensor* const* w, int count, int experts, const void* xq, int64_t pairs,
-                 const int32_t* counts, const int32_t* offsets, float* const* y, void* stream) {
+// max_count bounds every counts[e] (the token count under top-k routing, else
+// the pair count): the ring kernel runs one 8-token pass per workgroup, grid y
+// = the passes an expert can need.
+static int moe_gemv(const qmm_qtensor* const* w, int count, int experts, const void* xq, int64_t pairs,
+                    int64_t max_count, const int32_t* counts, const int32_t* offsets, float* const* y, void* stream) {
   if (!w || !y || !xq || !counts || !offsets || count < 1 || count > 2)
     return fail(QMM_ERR_INVALID, "need 1..2 stacked weights, activations, routing arrays and outputs");
   if (experts < 1 || experts > 65535) return fail(QMM_ERR_INVALID, "bad expert count %d", experts);
@@ -1316,9 +1319,14 @@ int qmm_moe_gemv(const qmm_qtensor* const* w, int count, int experts, const void
   // k-quants: the one-row ring kernels (16 waves, two workgroups per CU when
   // every expert is active); QMM_MOE_GEMV=0 selects the generic M = 8 GEMV,
   // QMM_MOE_GEMV=<P> the ring depth.
-  int ring = fmt == kFmtQ4K ? 2 : fmt == kFmtQ6K ? 1 : 0;
+  int ring = fmt == kFmtQ4K || fmt == kFmtQ6K ? 1 : 0;  // depth 2 measured no faster (Q4_K up to 3% slower)
   if (const char* e = getenv("QMM_MOE_GEMV")) ring = fmt != kFmtQ80 ? std::min(std::max(atoi(e), 0), 2) : 0;
   if (experts > 256) ring = 0;  // the ring kernel lists the active experts in a 256-entry LDS table
+  // the ring kernel addresses an expert's rows with 32-bit offsets
+  const unsigned long long body = fmt == kFmtQ4K ? 144 : 208;  // device block bodies (Q6_K's f16 d kept apart)
+  if ((unsigned long long)(w[0]->n / experts) * (unsigned long long)nb * body >= (1ull << 32)) ring = 0;
+  const long long passes = (std::max<long long>(std::min<long long>(max_count, pairs), 1) + 7) / 8;
+  if (passes > 64) ring = 0;  // many idle pass workgroups: the generic kernel loops over its rows instead
   char name[48];
   if (ring)
     snprintf(name, sizeof(name), "qmm_moe_gemv1_%s_p%d", fmt_name(fmt), ring);
@@ -1334,15 +1342,16 @@ int qmm_moe_gemv(const qmm_qtensor* const* w, int count, int experts, const void
   const void* xp = xq;
   void* args[] = {&w0, &w1, &nj, &N, &E, &y0, &y1, &ld, &xp, &xrow, &counts, &offsets, &K};
   // generic: ~20 resident waves per CU spread over the experts (grid y =
-  // expert, idle experts exit at once); ring: two 16-wave workgroups per CU
-  // shared out over the active experts inside the kernel (grid >= E)
+  // expert, idle experts exit at once); ring: per pass (grid y), 2 * CUs
+  // 16-wave workgroups shared out over that pass's experts inside the kernel
+  // (grid x >= E)
   const int wpg = ring ? 16 : 8;
   hipFunction_t f;
   QMM_TRY(kernel(d, name, &f));
-  (void)pairs;
   if (ring) {
     const long long gr = std::max<long long>((long long)d->num_cu * 2, E);
-    QMM_HIP(hipModuleLaunchKernel(f, (unsigned)gr, 1, 1, 64 * wpg, 1, 1, lds, (hipStream_t)stream, args, nullptr));
+    QMM_HIP(hipModuleLaunchKernel(f, (unsigned)gr, (unsigned)passes, 1, 64 * wpg, 1, 1, lds, (hipStream_t)stream,
+                                  args, nullptr));
     return QMM_OK;
   }
   long long gx = ((long long)d->num_cu * 20 / 8 + E - 1) / E;
@@ -1352,6 +1361,11 @@ int qmm_moe_gemv(const qmm_qtensor* const* w, int count, int experts, const void
   QMM_HIP(hipModuleLaunchKernel(f, (unsigned)gx, (unsigned)E, 1, 64 * wpg, 1, 1, lds, (hipStream_t)stream, args,
                                 nullptr));
   return QMM_OK;
+}
+
+int qmm_moe_gemv(const qmm_qtensor* const* w, int count, int experts, const void* xq, int64_t pairs,
+                 const int32_t* counts, const int32_t* offsets, float* const* y, void* stream) {
+  return moe_gemv(w, count, experts, xq, pairs, pairs, counts, offsets, y, stream);
 }
 
 // Grouped prefill GEMM over expert-ordered f32 rows: the rows are quantized
@@ -1484,7 +1498,8 @@ size_t qmm_moe_ffn_workspace_size(const qmm_qtensor* gate, const qmm_qtensor* do
 
 // Decode-sized MoE: gathered Q8_K rows through the expert GEMVs.
 static int moe_gemv_path(Device* d, const MoeWs& L, uint8_t* b, const float* x, int64_t ldx, const int32_t* ptok,
-                         int64_t P, int64_t H, int64_t F, int experts, const int32_t* counts, const int32_t* offsets,
+                         int64_t T, int64_t P, int64_t H, int64_t F, int experts, const int32_t* counts,
+                         const int32_t* offsets,
                          const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* down, hipStream_t s) {
   void* stream = s;
   const int vg = qmm_vec_dot_type(gate->dtype);
@@ -1510,7 +1525,7 @@ static int moe_gemv_path(Device* d, const MoeWs& L, uint8_t* b, const float* x, 
   {
     const qmm_qtensor* gw[2] = {gate, up};
     float* gy[2] = {g, u};
-    QMM_TRY(qmm_moe_gemv(gw, 2, experts, b + L.xq, P, counts, offsets, gy, stream));
+    QMM_TRY(moe_gemv(gw, 2, experts, b + L.xq, P, T, counts, offsets, gy, stream));
   }
   {
     long long n = P * F;
@@ -1522,7 +1537,7 @@ static int moe_gemv_path(Device* d, const MoeWs& L, uint8_t* b, const float* x, 
   float* yp = (float*)(b + L.yp);
   const qmm_qtensor* dw[1] = {down};
   float* dy[1] = {yp};
-  return qmm_moe_gemv(dw, 1, experts, b + L.hq, P, counts, offsets, dy, stream);
+  return moe_gemv(dw, 1, experts, b + L.hq, P, T, counts, offsets, dy, stream);
 }
 
 int qmm_moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* logits, int experts, int topk,
@@ -1582,7 +1597,7 @@ int qmm_moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* logits
     QMM_TRY(qmm_moe_gemm(dw, 1, experts, h, P, F, tokens, counts, offsets, dy, b + L.planes, L.total - L.planes,
                          stream));
   } else {
-    QMM_TRY(moe_gemv_path(d, L, b, x, ldx, ptok, P, H, F, experts, counts, offsets, gate, up, down, s));
+    QMM_TRY(moe_gemv_path(d, L, b, x, ldx, ptok, tokens, P, H, F, experts, counts, offsets, gate, up, down, s));
   }
   {
     int T = (int)tokens, k = topk, N = (int)H, lo = (int)ldo;

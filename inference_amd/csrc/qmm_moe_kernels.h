@@ -195,13 +195,259 @@ __device__ __forceinline__ void moe_gemv(const uint8_t* w0, const uint8_t* w1, i
 }
 
 // Expert-grouped GEMV for k-quant weights, one row per wave at a time with a
-// prefetch ring (the gemv1p structure): blockIdx.y = expert e, whose
-// counts[e] token rows (8 per pass) are staged in LDS once per workgroup; a
-// wave's weight slice is unpacked once (prep_w) and multiplied with each
-// token row, and each row's outputs are stored by lanes 0..rows-1 together.
-// The per-token accumulators are eight scalars, so register use stays at the
-// one-row kernels' level (the generic M = 8 GEMV keeps eight activation
-// slices live and spills at these shapes). Experts without tokens exit at once.
+// prefetch ring (the gemv1p structure). blockIdx.y is the pass: tokens
+// 8y .. 8y + 7 of every expert holding more than 8y of them; the pass's
+// workgroups are shared out over those experts, and a workgroup stages its
+// expert's pass rows in LDS once. A wave's weight slice is unpacked once and
+// multiplied with each token row, and each row's outputs are stored by lanes
+// 0..rows-1 together. The per-token accumulators are scalars, so register
+// use stays near the one-row kernels' (the generic M = 8 GEMV keeps eight
+// activation slices live and spills at these shapes).
+//
+// One pass over MR (compile-time) token rows, with the per-token work cut to
+// the dot products and the block's integer and f32 combine:
+//   * the activations are staged row-interleaved (block b of token m at LDS
+//     block b * MR + m), so a token's reads are immediate offsets from the
+//     first token's addresses, formed once per weight slice;
+//   * the Q4_K high nibbles are unpacked once per slice (the one-row
+//     kernels' 16q - 128 form needs a correction per token);
+//   * a lane past the row's last block gets zero scales, so its products are
+//     zero without a select per token, and the accumulators are cleared when
+//     a row starts;
+//   * no branch per token (the count is a template constant).
+// The integer block dots and the f32 sequence per block are the one-row
+// kernels', so the outputs are unchanged.
+struct MoePass {
+  const uint8_t* wb0;   // expert's first row body of weight 0 / 1
+  const uint8_t* wb1;
+  const uint16_t* db0;  // expert's first separated f16 scale of weight 0 / 1
+  const uint16_t* db1;
+  float* y0;
+  float* y1;
+  int N, ldy, nb, niter, row0, row_step, nslices;
+  uint32_t rowb;   // row body bytes (an expert's rows span < 4 GiB: checked by the host)
+  long long yrow;  // first output row of the pass (offsets[e] + mc)
+};
+
+// Weight-side values of a lane's slice for several tokens: the Q4_K high
+// nibbles as plain 0..15 bytes, the scales that multiply the activation sums
+// packed as int16 pairs for v_dot2 (Q4_K mins m0 | m1; Q6_K scales c0 | c1,
+// c2 | c3), and all scales zero when the lane's block is past the row's end.
+struct WTok {
+  qmm::WPrep w;
+  uint32_t p01, p23;
+};
+
+template <int FMT>
+__device__ __forceinline__ WTok prep_w_tok(const qmm::WSlice& s, int l, bool ok) {
+  using namespace qmm;
+  WTok t;
+  t.w = prep_w<FMT>(s, l);
+  if constexpr (FMT == kFmtQ4K) {
+    t.w.w2 = hi_nib(s.b);
+    t.w.w3 = hi_nib(s.c);
+    t.p01 = (uint32_t)t.w.c2 | ((uint32_t)t.w.c3 << 16);
+    t.p23 = 0;
+  } else {
+    t.p01 = ((uint32_t)t.w.c0 & 0xffffu) | ((uint32_t)t.w.c1 << 16);
+    t.p23 = ((uint32_t)t.w.c2 & 0xffffu) | ((uint32_t)t.w.c3 << 16);
+  }
+  if (!ok) {
+    t.w.c0 = t.w.c1 = t.w.c2 = t.w.c3 = 0;
+    t.p01 = t.p23 = 0;
+    t.w.dw = t.w.dm = 0.0f;
+  }
+  return t;
+}
+
+typedef short moe_short2 __attribute__((ext_vector_type(2)));
+// sum of the two int16 products of packed pairs a, b (v_dot2_i32_i16)
+__device__ __forceinline__ int dot2_i16(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot2(__builtin_bit_cast(moe_short2, a), __builtin_bit_cast(moe_short2, b), c, false);
+}
+
+// One lane's LDS addresses of block bx of the first token in the
+// row-interleaved layout; token m's are fixed offsets from them.
+struct XTok {
+  const uint8_t* q[4];
+  const uint32_t* s;
+  const float* d;
+};
+
+template <int FMT, int MR>
+__device__ __forceinline__ XTok xtok_base(const uint8_t* lds, int nb, int bx, int l) {
+  using namespace qmm;
+  XTok t;
+  const int nblk = MR * nb;
+  const uint8_t* e = lds + 256 * (bx * MR);
+  const int sw = (bx & 3) ^ ((l >> 1) << 1);  // kq_slot's swizzle of block bx
+#pragma unroll
+  for (int i = 0; i < 4; ++i) t.q[i] = e + 16 * (4 * l + (i ^ sw));
+  const uint32_t* lsum = reinterpret_cast<const uint32_t*>(lds + 256 * nblk);
+  t.s = lsum + 8 * (bx * MR) + (FMT == kFmtQ4K ? l : 2 * l);
+  t.d = reinterpret_cast<const float*>(lsum + 8 * nblk) + bx * MR;
+  return t;
+}
+
+template <int FMT>
+__device__ __forceinline__ qmm::XSlice load_xtok(const XTok& t, int m) {
+  qmm::XSlice x;
+  x.x0 = *reinterpret_cast<const uint4*>(t.q[0] + 256 * m);
+  x.x1 = *reinterpret_cast<const uint4*>(t.q[1] + 256 * m);
+  x.x2 = *reinterpret_cast<const uint4*>(t.q[2] + 256 * m);
+  x.x3 = *reinterpret_cast<const uint4*>(t.q[3] + 256 * m);
+  x.s0 = t.s[8 * m];
+  x.s1 = FMT == qmm::kFmtQ4K ? 0u : t.s[8 * m + 1];
+  x.d = t.d[m];
+  return x;
+}
+
+// dot_wx's block value (the same integers, then the same f32 sequence) for
+// prep_w_tok's weights:
+//   Q4_K: isd = c0 s0 + c1 s1; ism = m0 bs0 + m1 bs1 in one v_dot2 over the
+//         packed activation sums;
+//   Q6_K: sum_i c_i (d_i - 32 S_i) = sum_i c_i d_i - 32 sum_i c_i S_i, the
+//         second sum in two v_dot2.
+// |s|, |d| < 2^23 and the sums of 32 int8 fit int16, so every step is exact.
+template <int FMT>
+__device__ __forceinline__ float dot_tok(const WTok& t, const qmm::XSlice& x) {
+  using namespace qmm;
+  const WPrep& w = t.w;
+  if constexpr (FMT == kFmtQ4K) {
+    const int s0 = dot16(w.w1, x.x1, dot16(w.w0, x.x0, 0));
+    const int s1 = dot16(w.w3, x.x3, dot16(w.w2, x.x2, 0));
+    const int isd = __mul24(w.c0, s0) + __mul24(w.c1, s1);
+    const int ism = dot2_i16(t.p01, x.s0, 0);
+    return x.d * q4k_combine(w.dw, w.dm, isd, ism);
+  } else {
+    static_assert(FMT == kFmtQ6K, "k-quant weights");
+    const int d0 = dot16(w.w0, x.x0, 0), d1 = dot16(w.w1, x.x1, 0);
+    const int d2 = dot16(w.w2, x.x2, 0), d3 = dot16(w.w3, x.x3, 0);
+    const int cs = dot2_i16(t.p23, x.s1, dot2_i16(t.p01, x.s0, 0));
+    const int cd = __mul24(w.c0, d0) + __mul24(w.c1, d1) + __mul24(w.c2, d2) + __mul24(w.c3, d3);
+    const int is = cd - 32 * cs;
+    return x.d * (w.dw * (float)is);
+  }
+}
+
+// Per-token wave sums of acc[0..MR) with wave_total's summation tree, the
+// tokens spread across lanes so that a level costs about three instructions
+// per token pair instead of a wave_total per token:
+//   * lanes carry the index v = lane, with bits 0 and 1 flipped in odd quads,
+//     so that the half-row mirror (lane ^ 7) pairs v with v ^ 4;
+//   * levels 1 (lane ^ 1), 2 (lane ^ 2) and 3 (half-row mirror): a lane keeps
+//     the tokens whose index bit equals v's and adds the partner's copy of
+//     them (halving its values while MR allows, else adding its one value);
+//   * level 4 (row rotate by 8) joins the two 8-lane groups of a row;
+//   * lane m < MR fetches token m's four row sums and adds
+//     (R0 + R1) + (R2 + R3).
+// Each add joins the same two partial sums as wave_total, so the totals are
+// bit-identical. Returns token `lane`'s total on lanes < MR.
+template <int MR>
+__device__ __forceinline__ float wave_totals(const float (&acc)[MR], int lane) {
+  using namespace qmm;
+  if constexpr (MR == 1) {
+    return wave_total(acc[0]);
+  } else {
+    constexpr int MRP = MR <= 2 ? 2 : MR <= 4 ? 4 : 8;  // padded with zero tokens
+    const int v = lane ^ (((lane >> 2) & 1) ? 3 : 0);
+    const bool b0 = v & 1, b1 = (v >> 1) & 1, b2 = (v >> 2) & 1;
+    float t[MRP];
+#pragma unroll
+    for (int m = 0; m < MRP; ++m) t[m] = m < MR ? acc[m] : 0.0f;
+    // level 1: u[j] = token 2j + b0
+    float u[MRP / 2];
+#pragma unroll
+    for (int j = 0; j < MRP / 2; ++j) {
+      const float keep = b0 ? t[2 * j + 1] : t[2 * j], send = b0 ? t[2 * j] : t[2 * j + 1];
+      u[j] = keep + dpp_f<0xb1>(send);  // quad_perm [1,0,3,2]
+    }
+    // level 2: w[j] = token 4j + 2 b1 + b0 (MRP >= 4)
+    float w[MRP >= 4 ? MRP / 4 : 1];
+    if constexpr (MRP >= 4) {
+#pragma unroll
+      for (int j = 0; j < MRP / 4; ++j) {
+        const float keep = b1 ? u[2 * j + 1] : u[2 * j], send = b1 ? u[2 * j] : u[2 * j + 1];
+        w[j] = keep + dpp_f<0x4e>(send);  // quad_perm [2,3,0,1]
+      }
+    } else {
+      w[0] = u[0] + dpp_f<0x4e>(u[0]);
+    }
+    // level 3: token v & (MRP - 1)
+    float z;
+    if constexpr (MRP == 8) {
+      const float keep = b2 ? w[1] : w[0], send = b2 ? w[0] : w[1];
+      z = keep + dpp_f<0x141>(send);  // row_half_mirror
+    } else {
+      z = w[0] + dpp_f<0x141>(w[0]);
+    }
+    z += dpp_f<0x128>(z);  // row_ror:8: the row's other 8-lane group
+    // token m's row sums sit in lanes 16 r + j with j = v(m) (v is its own inverse)
+    const int m = lane & 7, j = m ^ (((m >> 2) & 1) ? 3 : 0);
+    auto row = [&](int r) {
+      return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * (16 * r + j), __builtin_bit_cast(int, z)));
+    };
+    return (row(0) + row(1)) + (row(2) + row(3));
+  }
+}
+
+template <int FMT, int P, int NW, int MR>
+__device__ __forceinline__ void moe_gemv1_pass(const MoePass& a, const uint8_t* __restrict__ xs, uint8_t* lds) {
+#pragma clang fp contract(off)
+  using namespace qmm;
+  constexpr int BPI = 16;
+  const int lane = threadIdx.x & 63, l = lane & 3, g = lane >> 2;
+  const int nb = a.nb, niter = a.niter, nslices = a.nslices;
+  int is_s = 0, is_k = 0, is_it = 0;
+  WSlice ring[P];
+  auto issue = [&](WSlice& w) {
+    const int gr = a.row0 + is_k * a.row_step;  // < total while is_s < nslices
+    const int j = gr >= a.N ? 1 : 0;
+    const uint32_t r = (uint32_t)(gr - j * a.N);  // row of the expert's weight j
+    const uint8_t* wrow = (j ? a.wb1 : a.wb0) + r * a.rowb;
+    const uint16_t* drow = (j ? a.db1 : a.db0) + r * (uint32_t)nb;
+    load_slice<FMT>(w, wrow, drow, (uint32_t)min(is_it * BPI + g, nb - 1), l);
+    if (++is_it == niter) {
+      is_it = 0;
+      ++is_k;
+    }
+    ++is_s;
+  };
+#pragma unroll
+  for (int u = 0; u < P; ++u)
+    if (is_s < nslices) issue(ring[u]);
+  stage_act<FMT, NW, MR>(xs, MR * nb, lds, nb);
+  __syncthreads();
+  float acc[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
+  int c_k = 0, c_it = 0;
+  for (int s0 = 0; s0 < nslices; s0 += P) {
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      if (s0 + u < nslices) {
+        const int b = c_it * BPI + g;
+        const bool okb = b < nb;
+        const WTok wp = prep_w_tok<FMT>(ring[u], l, okb);
+        const XTok xt = xtok_base<FMT, MR>(lds, nb, okb ? b : 0, l);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[m] += dot_tok<FMT>(wp, load_xtok<FMT>(xt, m));
+        if (++c_it == niter) {
+          const int gr = a.row0 + c_k * a.row_step;
+          const int j = gr >= a.N ? 1 : 0;
+          const float out = wave_totals<MR>(acc, lane);
+#pragma unroll
+          for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
+          if (lane < MR) (j ? a.y1 : a.y0)[(size_t)(a.yrow + lane) * a.ldy + (gr - j * a.N)] = out;
+          c_it = 0;
+          ++c_k;
+        }
+      }
+      if (is_s < nslices) issue(ring[u]);
+    }
+  }
+}
+
 template <int FMT, int P, int NW>
 __device__ __forceinline__ void moe_gemv1(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, int njobs,
                                           int N, int E, float* __restrict__ y0, float* __restrict__ y1, int ldy,
@@ -217,11 +463,12 @@ __device__ __forceinline__ void moe_gemv1(const uint8_t* __restrict__ w0, const 
   // many experts are idle.
   __shared__ int act[256];
   __shared__ int nact;
-  const int lane = threadIdx.x & 63, l = lane & 3, g = lane >> 2;
+  const int lane = threadIdx.x & 63;
+  const int mc = 8 * (int)blockIdx.y;  // this workgroup's pass: tokens mc .. mc + 7 of its expert
   if (threadIdx.x < 64) {
     int base = 0;
     for (int e0 = 0; e0 < E; e0 += 64) {
-      const bool a = e0 + lane < E && counts[e0 + lane] > 0;
+      const bool a = e0 + lane < E && counts[e0 + lane] > mc;
       const unsigned long long msk = __ballot(a);
       if (a) act[base + __popcll(msk & ((1ull << lane) - 1ull))] = e0 + lane;
       base += __popcll(msk);
@@ -229,88 +476,53 @@ __device__ __forceinline__ void moe_gemv1(const uint8_t* __restrict__ w0, const 
     if (lane == 0) nact = base;
   }
   __syncthreads();
-  const int na = nact;
+  // workgroup-uniform values read from LDS or memory go to scalar registers
+  // (readfirstlane), which keeps the address arithmetic on the scalar unit
+  // and the per-token passes within the vector register budget
+  const int na = __builtin_amdgcn_readfirstlane(nact);
   if (na == 0) return;
   const long long G = gridDim.x;
   const int slot = (int)((long long)blockIdx.x * na / G);
   const int first = (int)(((long long)slot * G + na - 1) / na);
   const int next = (int)(((long long)(slot + 1) * G + na - 1) / na);
-  const int e = act[slot], bx = (int)blockIdx.x - first, gx = next - first;
-  const int me = counts[e];
-  const int off = offsets[e];
+  const int e = __builtin_amdgcn_readfirstlane(act[slot]), bx = (int)blockIdx.x - first, gx = next - first;
+  const int me = __builtin_amdgcn_readfirstlane(counts[e]);
+  const int off = __builtin_amdgcn_readfirstlane(offsets[e]);
   const int nb = K / 256, niter = (nb + BPI - 1) / BPI;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int total = njobs * N;
-  const int row_step = gx * NW;
-  const int row0 = bx * NW + wave;
-  const int nrows = row0 < total ? (total - 1 - row0) / row_step + 1 : 0;
-  const int nslices = nrows * niter;
-  const size_t rowb = (size_t)nb * FmtInfo<FMT>::kBodyBytes;
-  const size_t trows = (size_t)E * N;
-  for (int mc = 0; mc < me; mc += 8) {
-    const int mr = min(8, me - mc);
-    int is_s = 0, is_k = 0, is_it = 0;
-    WSlice ring[P];
-    auto issue = [&](WSlice& w) {
-      const int gr = row0 + is_k * row_step;  // < total while is_s < nslices
-      const int j = gr >= N ? 1 : 0;
-      const uint8_t* wq = j ? w1 : w0;
-      const size_t trow = (size_t)e * N + (gr - j * N);
-      const uint8_t* wrow = wq + trow * rowb;
-      const uint16_t* drow = reinterpret_cast<const uint16_t*>(wq + trows * rowb) + trow * nb;
-      load_slice<FMT>(w, wrow, drow, (uint32_t)min(is_it * BPI + g, nb - 1), l);
-      if (++is_it == niter) {
-        is_it = 0;
-        ++is_k;
-      }
-      ++is_s;
-    };
-#pragma unroll
-    for (int u = 0; u < P; ++u)
-      if (is_s < nslices) issue(ring[u]);
-    if (mc > 0) __syncthreads();  // the previous pass's LDS reads are done
-    stage_act<FMT, NW>(xq + (size_t)(off + mc) * xrow, mr * nb, lds);
-    __syncthreads();
-    float acc[8];
-    int c_k = 0, c_it = 0;
-    for (int s0 = 0; s0 < nslices; s0 += P) {
-#pragma unroll
-      for (int u = 0; u < P; ++u) {
-        if (s0 + u < nslices) {
-          const int b = c_it * BPI + g;
-          const bool okb = b < nb;
-          const int bx = okb ? b : 0;
-          const WPrep wp = prep_w<FMT>(ring[u], l);
-#pragma unroll
-          for (int m = 0; m < 8; ++m) {
-            if (m < mr) {  // wave-uniform
-              XSlice x;
-              load_x<FMT>(x, lds, mr * nb, m * nb + bx, l);
-              int ia, ib;
-              float p = dot_wx<FMT>(wp, x, ia, ib);
-              p = okb ? p : 0.0f;
-              acc[m] = c_it == 0 ? p : acc[m] + p;
-            }
-          }
-          if (++c_it == niter) {
-            const int gr = row0 + c_k * row_step;
-            const int j = gr >= N ? 1 : 0;
-            float out = 0.0f;
-#pragma unroll
-            for (int m = 0; m < 8; ++m) {
-              if (m < mr) {
-                const float v = wave_total(acc[m]);
-                out = lane == m ? v : out;
-              }
-            }
-            if (lane < mr) (j ? y1 : y0)[(size_t)(off + mc + lane) * ldy + (gr - j * N)] = out;
-            c_it = 0;
-            ++c_k;
-          }
-        }
-        if (is_s < nslices) issue(ring[u]);
-      }
-    }
+  MoePass ps;
+  const size_t rowb = (size_t)nb * FmtInfo<FMT>::kBodyBytes, erow = (size_t)e * N, trows = (size_t)E * N;
+  ps.wb0 = w0 + erow * rowb;
+  ps.wb1 = w1 + erow * rowb;
+  ps.db0 = reinterpret_cast<const uint16_t*>(w0 + trows * rowb) + erow * nb;
+  ps.db1 = reinterpret_cast<const uint16_t*>(w1 + trows * rowb) + erow * nb;
+  ps.y0 = y0;
+  ps.y1 = y1;
+  ps.N = N;
+  ps.ldy = ldy;
+  ps.nb = nb;
+  ps.niter = niter;
+  ps.row_step = gx * NW;
+  ps.row0 = bx * NW + wave;
+  const int nrows = ps.row0 < total ? (total - 1 - ps.row0) / ps.row_step + 1 : 0;
+  ps.nslices = nrows * niter;
+  ps.rowb = (uint32_t)rowb;
+  // a single pass per workgroup: with a loop over passes the state carried
+  // across it pushes the eight inlined token counts past the scalar
+  // registers (spilled into vector registers, then to memory)
+  const int mr = min(8, me - mc);
+  const uint8_t* xs = xq + (size_t)(off + mc) * xrow;
+  ps.yrow = off + mc;
+  switch (mr) {  // workgroup-uniform
+    case 1: moe_gemv1_pass<FMT, P, NW, 1>(ps, xs, lds); break;
+    case 2: moe_gemv1_pass<FMT, P, NW, 2>(ps, xs, lds); break;
+    case 3: moe_gemv1_pass<FMT, P, NW, 3>(ps, xs, lds); break;
+    case 4: moe_gemv1_pass<FMT, P, NW, 4>(ps, xs, lds); break;
+    case 5: moe_gemv1_pass<FMT, P, NW, 5>(ps, xs, lds); break;
+    case 6: moe_gemv1_pass<FMT, P, NW, 6>(ps, xs, lds); break;
+    case 7: moe_gemv1_pass<FMT, P, NW, 7>(ps, xs, lds); break;
+    default: moe_gemv1_pass<FMT, P, NW, 8>(ps, xs, lds); break;
   }
 }
 
