@@ -503,7 +503,8 @@ def run_moe(torch, dev):
     ops = 2 * Tp * k * 3 * F * H  # int8 ops of the three projections over every routed pair
     out["prefill"] = {"tokens": Tp, "us": round(usp, 2), "TOPS": round(ops / usp / 1e6, 1),
                       "mfma_util": round(ops / usp / 1e6 / INT8_PEAK_TOPS, 4),
-                      "schedule": "route, gather, grouped MFMA GEMM gate/up, SiLU*mul, grouped GEMM down, combine",
+                      "schedule": "route, gathered rows quantized to GEMM planes, grouped split-scale MFMA GEMM gate/up, "
+                                  "SiLU*mul quantized to planes, grouped GEMM down, combine",
                       "us_spread": spp}
     return out
 

@@ -1376,6 +1376,10 @@ size_t qmm_moe_gemm_workspace_size(const qmm_qtensor* w, int64_t pairs) {
   return mmq_planes(w->dtype, pairs, w->k).total;
 }
 
+static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, int experts, const uint8_t* planes,
+                           int64_t pairs, int64_t max_rows, const int32_t* counts, const int32_t* offsets,
+                           float* const* y, hipStream_t s);
+
 int qmm_moe_gemm(const qmm_qtensor* const* w, int count, int experts, const float* x, int64_t pairs, int64_t ldx,
                  int64_t max_rows, const int32_t* counts, const int32_t* offsets, float* const* y, void* ws,
                  size_t ws_bytes, void* stream) {
@@ -1400,26 +1404,46 @@ int qmm_moe_gemm(const qmm_qtensor* const* w, int count, int experts, const floa
   hipStream_t s = (hipStream_t)stream;
   uint8_t* b = (uint8_t*)ws;
   QMM_TRY(quantize_planes(d, w0->dtype, x, pairs, w0->k, ldx, b, s));
+  return moe_gemm_planes(d, w, count, experts, b, pairs, max_rows, counts, offsets, y, s);
+}
+
+// The grouped GEMM launches over activation planes already at `planes`
+// (mmq_planes(w[0]->dtype, pairs, k) layout).
+static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, int experts, const uint8_t* planes,
+                           int64_t pairs, int64_t max_rows, const int32_t* counts, const int32_t* offsets,
+                           float* const* y, hipStream_t s) {
+  const qmm_qtensor* w0 = w[0];
   const Planes pl = mmq_planes(w0->dtype, pairs, w0->k);
   const int fmt = fmt_of(w0->dtype);
-  const void* q8 = b + pl.q8;
-  const void* dd = b + pl.d;
-  const void* ss = b + pl.s;
+  const void* q8 = planes + pl.q8;
+  const void* dd = planes + pl.d;
+  const void* ss = planes + pl.s;
   int N = (int)(w0->n / experts), K = (int)w0->k, ld = N, E = experts;
-  // Q4_K: 128-row tiles (QMM_MOE_BM=64: 64-row tiles, less padding when an
-  // expert's row count sits just above a multiple of 128)
+  // Q4_K: the split-scale mmqs tile (128 x 128, eight waves) as in the dense
+  // GEMM; QMM_MOE_MMQ=2 selects the older mmq2 tile, 128 rows (QMM_MOE_BM=64:
+  // 64-row tiles, less padding when an expert's row count sits just above a
+  // multiple of 128)
+  const unsigned ldss = 2u * (128 * 272 + 128 * 144 + 128 * 4 + 128 * 48 + 128 * 48 + 128 * 80);
+  const char* gen = getenv("QMM_MOE_MMQ");
+  const bool use_s = fmt == kFmtQ4K && (gen == nullptr || atoi(gen) != 2) && (int)ldss <= d->max_lds;
   int bm = 64;
   if (fmt == kFmtQ4K) {
     bm = 128;
-    if (const char* e = getenv("QMM_MOE_BM")) bm = atoi(e) == 64 ? 64 : 128;
+    if (const char* e = getenv("QMM_MOE_BM"); e && !use_s) bm = atoi(e) == 64 ? 64 : 128;
   }
   const int bn = 128;
-  const unsigned lds = fmt == kFmtQ4K ? (unsigned)(2 * (bm * 272 + 128 * 144 + bm * 4 + bm * 16)) : 0u;
+  unsigned lds = fmt == kFmtQ4K ? (unsigned)(2 * (bm * 272 + 128 * 144 + bm * 4 + bm * 16)) : 0u;
+  unsigned threads = fmt == kFmtQ4K ? (unsigned)(bm * 4) : 256u;
   char name[40];
-  if (fmt == kFmtQ4K)
+  if (use_s) {
+    snprintf(name, sizeof(name), "qmm_moe_mmqs_q4k");
+    lds = ldss;
+    threads = 512;
+  } else if (fmt == kFmtQ4K) {
     snprintf(name, sizeof(name), "qmm_moe_mmq2_q4k%s", bm == 64 ? "_m64" : "");
-  else
+  } else {
     snprintf(name, sizeof(name), "qmm_moe_mmq_%s", fmt_name(fmt));
+  }
   hipFunction_t f;
   QMM_TRY(kernel(d, name, &f));
   for (int j = 0; j < count; ++j) {
@@ -1427,8 +1451,7 @@ int qmm_moe_gemm(const qmm_qtensor* const* w, int count, int experts, const floa
     float* yy = y[j];
     void* args[] = {&wq, &q8, &dd, &ss, &yy, &N, &K, &ld, &E, &counts, &offsets};
     QMM_HIP(hipModuleLaunchKernel(f, (unsigned)((N + bn - 1) / bn), (unsigned)((max_rows + bm - 1) / bm),
-                                  (unsigned)experts, fmt == kFmtQ4K ? (unsigned)(bm * 4) : 256u, 1, 1, lds, s, args,
-                                  nullptr));
+                                  (unsigned)experts, threads, 1, 1, lds, s, args, nullptr));
   }
   return QMM_OK;
 }
@@ -1527,13 +1550,16 @@ static int moe_gemv_path(Device* d, const MoeWs& L, uint8_t* b, const float* x, 
     float* gy[2] = {g, u};
     QMM_TRY(moe_gemv(gw, 2, experts, b + L.xq, P, T, counts, offsets, gy, stream));
   }
-  {
+  const int vd = qmm_vec_dot_type(down->dtype);
+  if (vd == QMM_Q8K) {
+    // silu(g) * u quantized in registers (the same f32 values, one launch)
+    QMM_TRY(qmm_silu_mul_quantize(g, u, P, F, F, b + L.hq, stream));
+  } else {
     long long n = P * F;
     void* args[] = {&g, &u, &h, &n};
     QMM_TRY(launch(d, "qmm_silu_mul", ceil_div(n, 256), 256, 0, s, args));
+    QMM_TRY(qmm_quantize_rows(vd, h, P, F, F, b + L.hq, stream));
   }
-  const int vd = qmm_vec_dot_type(down->dtype);
-  QMM_TRY(qmm_quantize_rows(vd, h, P, F, F, b + L.hq, stream));
   float* yp = (float*)(b + L.yp);
   const qmm_qtensor* dw[1] = {down};
   float* dy[1] = {yp};
@@ -1572,30 +1598,65 @@ int qmm_moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* logits
   float* h = (float*)(b + L.h);
   float* yp = (float*)(b + L.yp);
   if (moe_grouped(P, experts) && H % 256 == 0 && F % 256 == 0) {
-    // prefill: gathered f32 rows -> grouped GEMMs (an expert holds at most
+    // prefill: gathered rows -> grouped GEMMs (an expert holds at most
     // `tokens` pairs: a token's top-k experts are distinct)
-    float* xg = (float*)(b + L.xg);
-    {
-      const void* xp = x;
-      long long lx = ldx;
-      const int32_t* rows = ptok;
-      int kk = (int)H, nr = (int)P;
-      void* args[] = {&xp, &lx, &rows, &xg, &kk, &nr};
-      QMM_TRY(launch(d, "qmm_gather_rows", ceil_div(P * H, 256), 256, 0, s, args));
+    const int vg = qmm_vec_dot_type(gate->dtype), vd = qmm_vec_dot_type(down->dtype);
+    if (vg == QMM_Q8K && vd == QMM_Q8K) {
+      // Q8_K activations: the gather and SiLU*mul write the GEMM planes
+      // directly (the same values as quantizing the f32 rows)
+      uint8_t* pw8 = b + L.planes;
+      {
+        const Planes pl = mmq_planes(gate->dtype, P, H);
+        const void* xp = x;
+        long long lx = ldx;
+        const int32_t* rows = ptok;
+        void* q8 = pw8 + pl.q8;
+        void* dd = pw8 + pl.d;
+        void* ss = pw8 + pl.s;
+        int kk = (int)H, mm = (int)P;
+        void* args[] = {&xp, &lx, &rows, &q8, &dd, &ss, &kk, &mm};
+        QMM_TRY(launch(d, "qmm_quantize_q8k_mmq_rows", ceil_div(P * (H / 256), 4), 256, 0, s, args));
+      }
+      const qmm_qtensor* gw[2] = {gate, up};
+      float* gy[2] = {g, u};
+      QMM_TRY(moe_gemm_planes(d, gw, 2, experts, pw8, P, tokens, counts, offsets, gy, s));
+      {
+        const Planes pl = mmq_planes(down->dtype, P, F);
+        long long ld = F;
+        void* q8 = pw8 + pl.q8;
+        void* dd = pw8 + pl.d;
+        void* ss = pw8 + pl.s;
+        int kk = (int)F, mm = (int)P;
+        void* args[] = {&g, &u, &ld, &q8, &dd, &ss, &kk, &mm};
+        QMM_TRY(launch(d, "qmm_silu_mul_q8k_mmq", ceil_div(P * (F / 256), 4), 256, 0, s, args));
+      }
+      const qmm_qtensor* dw[1] = {down};
+      float* dy[1] = {yp};
+      QMM_TRY(moe_gemm_planes(d, dw, 1, experts, pw8, P, tokens, counts, offsets, dy, s));
+    } else {
+      float* xg = (float*)(b + L.xg);
+      {
+        const void* xp = x;
+        long long lx = ldx;
+        const int32_t* rows = ptok;
+        int kk = (int)H, nr = (int)P;
+        void* args[] = {&xp, &lx, &rows, &xg, &kk, &nr};
+        QMM_TRY(launch(d, "qmm_gather_rows", ceil_div(P * H, 256), 256, 0, s, args));
+      }
+      const qmm_qtensor* gw[2] = {gate, up};
+      float* gy[2] = {g, u};
+      QMM_TRY(qmm_moe_gemm(gw, 2, experts, xg, P, H, tokens, counts, offsets, gy, b + L.planes,
+                           L.total - L.planes, stream));
+      {
+        long long n = P * F;
+        void* args[] = {&g, &u, &h, &n};
+        QMM_TRY(launch(d, "qmm_silu_mul", ceil_div(n, 256), 256, 0, s, args));
+      }
+      const qmm_qtensor* dw[1] = {down};
+      float* dy[1] = {yp};
+      QMM_TRY(qmm_moe_gemm(dw, 1, experts, h, P, F, tokens, counts, offsets, dy, b + L.planes,
+                           L.total - L.planes, stream));
     }
-    const qmm_qtensor* gw[2] = {gate, up};
-    float* gy[2] = {g, u};
-    QMM_TRY(qmm_moe_gemm(gw, 2, experts, xg, P, H, tokens, counts, offsets, gy, b + L.planes,
-                         L.total - L.planes, stream));
-    {
-      long long n = P * F;
-      void* args[] = {&g, &u, &h, &n};
-      QMM_TRY(launch(d, "qmm_silu_mul", ceil_div(n, 256), 256, 0, s, args));
-    }
-    const qmm_qtensor* dw[1] = {down};
-    float* dy[1] = {yp};
-    QMM_TRY(qmm_moe_gemm(dw, 1, experts, h, P, F, tokens, counts, offsets, dy, b + L.planes, L.total - L.planes,
-                         stream));
   } else {
     QMM_TRY(moe_gemv_path(d, L, b, x, ldx, ptok, tokens, P, H, F, experts, counts, offsets, gate, up, down, s));
   }

@@ -430,6 +430,18 @@ __device__ __forceinline__ void mmq(const uint8_t* __restrict__ wq, const uint16
 
 // Activation quantizers writing the GEMM's plane layout.
 //   Q8_K: q8 int8 [m][k], d f32 [m][k/256], 32-element sums int16 [m][k/256][8]
+namespace qmm {
+// One wave's Q8_K block w (row w / nb, block w % nb) in the plane layout.
+__device__ __forceinline__ void put_q8k_plane(const Q8KLane& q, long long w, int nb, int k, int8_t* __restrict__ q8,
+                                              float* __restrict__ d, int16_t* __restrict__ s, int lane) {
+  const int row = (int)(w / nb), b = (int)(w % nb);
+  reinterpret_cast<uint32_t*>(q8 + (size_t)row * k + 256 * b)[lane] = q.packed;
+  const int next = __shfl_down(q.sum16, 4);
+  if ((lane & 7) == 0) s[w * 8 + (lane >> 3)] = (int16_t)(q.sum16 + next);
+  if (lane == 0) d[w] = q.d;
+}
+}  // namespace qmm
+
 extern "C" __global__ void __launch_bounds__(256) qmm_quantize_q8k_mmq(const float* __restrict__ x, long long ldx,
                                                                        int8_t* __restrict__ q8,
                                                                        float* __restrict__ d,
@@ -438,11 +450,41 @@ extern "C" __global__ void __launch_bounds__(256) qmm_quantize_q8k_mmq(const flo
   const long long w = (long long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (w >= (long long)m * nb) return;
   const int row = (int)(w / nb), b = (int)(w % nb), lane = threadIdx.x & 63;
-  const qmm::Q8KLane q = qmm::q8k_lane(x + row * ldx + 256LL * b, lane);
-  reinterpret_cast<uint32_t*>(q8 + (size_t)row * k + 256 * b)[lane] = q.packed;
-  const int next = __shfl_down(q.sum16, 4);
-  if ((lane & 7) == 0) s[w * 8 + (lane >> 3)] = (int16_t)(q.sum16 + next);
-  if (lane == 0) d[w] = q.d;
+  qmm::put_q8k_plane(qmm::q8k_lane(x + row * ldx + 256LL * b, lane), w, nb, k, q8, d, s, lane);
+}
+
+// The same planes for gathered rows: plane row i = x[rows[i]] (the grouped
+// prefill's expert-ordered pairs, without a gathered f32 copy).
+extern "C" __global__ void __launch_bounds__(256) qmm_quantize_q8k_mmq_rows(const float* __restrict__ x,
+                                                                            long long ldx,
+                                                                            const int* __restrict__ rows,
+                                                                            int8_t* __restrict__ q8,
+                                                                            float* __restrict__ d,
+                                                                            int16_t* __restrict__ s, int k, int m) {
+  const int nb = k / 256;
+  const long long w = (long long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (w >= (long long)m * nb) return;
+  const int row = (int)(w / nb), b = (int)(w % nb), lane = threadIdx.x & 63;
+  qmm::put_q8k_plane(qmm::q8k_lane(x + (long long)rows[row] * ldx + 256LL * b, lane), w, nb, k, q8, d, s, lane);
+}
+
+// The same planes for silu(g) * u (rows of k, row stride ld): the f32 values
+// of qmm_silu_mul, quantized in registers.
+extern "C" __global__ void __launch_bounds__(256) qmm_silu_mul_q8k_mmq(const float* __restrict__ g,
+                                                                       const float* __restrict__ u, long long ld,
+                                                                       int8_t* __restrict__ q8,
+                                                                       float* __restrict__ d,
+                                                                       int16_t* __restrict__ s, int k, int m) {
+#pragma clang fp contract(off)
+  const int nb = k / 256;
+  const long long w = (long long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (w >= (long long)m * nb) return;
+  const int row = (int)(w / nb), b = (int)(w % nb), lane = threadIdx.x & 63;
+  const long long o = row * ld + 256LL * b + 4 * lane;
+  float e[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) e[j] = qmm::silu_mul(g[o + j], u[o + j]);
+  qmm::put_q8k_plane(qmm::q8k_lane_vals(e[0], e[1], e[2], e[3], lane), w, nb, k, q8, d, s, lane);
 }
 
 //   Q8_0: q8 int8 [m][k], d f32 [m][k/32] (the f16-rounded block scale)

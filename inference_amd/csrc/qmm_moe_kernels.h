@@ -607,6 +607,20 @@ __device__ __forceinline__ bool group_rows(GroupRows& g, const int8_t* xq, const
 QMM_MOE_MMQ2_KERNEL(128, )
 QMM_MOE_MMQ2_KERNEL(64, _m64)
 
+// Q4_K grouped GEMM on the split-scale tile (mmqs: the d term on int8 MFMA,
+// the mins term on bf16 MFMA): an expert's rows give what the dense mmqs
+// GEMM gives on them alone, unsplit.
+extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+qmm_moe_mmqs_q4k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                 const int16_t* __restrict__ xs, float* __restrict__ y, int N, int K, int ldy, int E,
+                 const int* __restrict__ counts, const int* __restrict__ offsets) {
+  qmm::GroupRows g;
+  if (!qmm::group_rows<qmm::kSBM, false>(g, xq, xd, xs, y, K, ldy, counts, offsets)) return;
+  const uint8_t* we = wq + (size_t)blockIdx.z * N * (K / 256) * qmm::kQ4KBytes;
+  qmm::mmqs_q4k<false>(we, g.xq, g.xd, g.xs, g.y, g.m, N, K, ldy, nullptr, 0, 0, 0, K / 256);
+  (void)E;
+}
+
 #define QMM_MOE_MMQ_KERNEL(FMT, NAME)                                                                          \
   extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))                 \
       qmm_moe_mmq_##NAME(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                        \

@@ -83,22 +83,29 @@ def test_grouped_gemm_equals_per_expert_gemm(monkeypatch, dt, E, N, K, T, mode):
     c, o = counts.cpu().numpy(), offsets.cpu().numpy()
     if mode == "skew":
         assert c[0] == T and c[1] == T and c[2:].sum() == 0
-    monkeypatch.setenv("QMM_MMQ", "2")  # per-expert Q4_K on the same 128x128 kernel as the grouped launch
-    monkeypatch.setenv("QMM_SPLITK", "1")  # and unsplit, as the grouped launch is
-    for e in range(E):
-        if c[e] == 0:
-            continue
-        rows = xg[o[e]:o[e] + c[e]]
-        want = orc.matmul(ORC[dt], rows.cpu().numpy(), per[e], K)
-        assert rel_err(y[o[e]:o[e] + c[e]].cpu().numpy(), want) <= TOL, f"expert {e}"
-        if c[e] > 8:  # qmm_matmul's GEMM path
-            qe = QTensor.from_ggml(per[e], dt, (N, K), device=DEV)
-            ref = QMatMul(qe).forward(rows)
-            assert torch.equal(y[o[e]:o[e] + c[e]], ref), f"expert {e}: differs from the per-expert GEMM"
-    assert not torch.isnan(y).any()
-    if dt == GgmlDType.Q4K:  # 64-row tiles: the same rows through mmq2<64, 128>, the same bits
+    monkeypatch.setenv("QMM_SPLITK", "1")  # per-expert GEMMs unsplit, as the grouped launch is
+
+    def check(y):
+        for e in range(E):
+            if c[e] == 0:
+                continue
+            rows = xg[o[e]:o[e] + c[e]]
+            want = orc.matmul(ORC[dt], rows.cpu().numpy(), per[e], K)
+            assert rel_err(y[o[e]:o[e] + c[e]].cpu().numpy(), want) <= TOL, f"expert {e}"
+            if c[e] > 8:  # qmm_matmul's GEMM path (Q4_K: the same tile generation as the grouped launch)
+                qe = QTensor.from_ggml(per[e], dt, (N, K), device=DEV)
+                ref = QMatMul(qe).forward(rows)
+                assert torch.equal(y[o[e]:o[e] + c[e]], ref), f"expert {e}: differs from the per-expert GEMM"
+        assert not torch.isnan(y).any()
+
+    check(y)  # Q4_K: the split-scale mmqs tile, grouped and dense
+    if dt == GgmlDType.Q4K:  # the older mmq2 tile, grouped and dense: 128-row tiles, then 64-row (same bits)
+        monkeypatch.setenv("QMM_MOE_MMQ", "2")
+        monkeypatch.setenv("QMM_MMQ", "2")
+        y2 = moe_gemm([qt], E, xg, counts, offsets, T)[0]
+        check(y2)
         monkeypatch.setenv("QMM_MOE_BM", "64")
-        assert torch.equal(moe_gemm([qt], E, xg, counts, offsets, T)[0], y)
+        assert torch.equal(moe_gemm([qt], E, xg, counts, offsets, T)[0], y2)
 
 
 @pytest.mark.parametrize("E,H,F,T,mode", [
