@@ -503,9 +503,23 @@ __device__ __forceinline__ void moe_gemv1(const uint8_t* __restrict__ w0, const 
   ps.ldy = ldy;
   ps.nb = nb;
   ps.niter = niter;
-  ps.row_step = gx * NW;
-  ps.row0 = bx * NW + wave;
-  const int nrows = ps.row0 < total ? (total - 1 - ps.row0) / ps.row_step + 1 : 0;
+  // Rows longer than one slice (K > 4096): a contiguous block of the
+  // expert's rows per workgroup, its waves taking every NW-th row of it, so
+  // the workgroups stream separate regions (config-5 down, 11.6 KB rows:
+  // 62.3 -> 58.8 us). One-slice rows stay grid-stride over the workgroups
+  // (gate/up, 2.3 KB rows: contiguous blocks measured 82.3 -> 84.1 us).
+  int nrows;
+  if (niter > 1) {
+    const int per = (total + gx - 1) / gx;
+    const int rb0 = min(bx * per, total), rb1 = min(rb0 + per, total);
+    ps.row_step = NW;
+    ps.row0 = rb0 + wave;
+    nrows = ps.row0 < rb1 ? (rb1 - 1 - ps.row0) / NW + 1 : 0;
+  } else {
+    ps.row_step = gx * NW;
+    ps.row0 = bx * NW + wave;
+    nrows = ps.row0 < total ? (total - 1 - ps.row0) / ps.row_step + 1 : 0;
+  }
   ps.nslices = nrows * niter;
   ps.rowb = (uint32_t)rowb;
   // a single pass per workgroup: with a loop over passes the state carried
