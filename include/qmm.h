@@ -327,8 +327,9 @@ int qmm_moe_route(const float *logits, int64_t tokens, int experts, int topk, in
 /* Expert-grouped GEMV (replaces moe_gemm_gguf, ffi.rs:25-39): w[j] (count 1..2)
  * are stacked expert weights [experts*N, K] of one dtype; xq holds `pairs`
  * rows of vec-dot blocks grouped by expert (counts/offsets as produced by
- * qmm_moe_route); y[j] receives [pairs, N] f32. Each active expert's weights
- * are streamed once; experts without tokens read nothing. */
+ * qmm_moe_route); y[j] receives [pairs, N] f32. An active expert's weights
+ * are streamed once per 8 of its tokens; experts without tokens read nothing.
+ * Every counts[e] must be <= pairs (the launch is sized for that bound). */
 int qmm_moe_gemv(const qmm_qtensor *const *w, int count, int experts, const void *xq, int64_t pairs,
                  const int32_t *counts, const int32_t *offsets, float *const *y, void *stream);
 
