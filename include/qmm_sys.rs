@@ -346,8 +346,9 @@ extern "C" {
     /// Expert-grouped GEMV (replaces moe_gemm_gguf, ffi.rs:25-39): w[j] (count 1..2)
     /// are stacked expert weights [experts*N, K] of one dtype; xq holds `pairs`
     /// rows of vec-dot blocks grouped by expert (counts/offsets as produced by
-    /// qmm_moe_route); y[j] receives [pairs, N] f32. Each active expert's weights
-    /// are streamed once; experts without tokens read nothing.
+    /// qmm_moe_route); y[j] receives [pairs, N] f32. An active expert's weights
+    /// are streamed once per 8 of its tokens; experts without tokens read nothing.
+    /// Every counts[e] must be <= pairs (the launch is sized for that bound).
     pub fn qmm_moe_gemv(
         w: *const *const QmmQTensor, count: c_int, experts: c_int, xq: *const c_void, pairs: i64,
         counts: *const i32, offsets: *const i32, y: *const *mut f32, stream: *mut c_void
