@@ -542,6 +542,29 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   if ((int)lds > d->max_lds)
     return fail(QMM_ERR_UNSUPPORTED, "activation of %d rows x %lld needs %u B of LDS (> %d)", m, (long long)w->k, lds,
                 d->max_lds);
+  // 2..8 staged activation rows of one k-quant weight: the token-interleaved
+  // kernel the expert GEMV uses (one transposed reduction for all rows, no
+  // per-row branches), the same bits as the general multi-row GEMV. From
+  // sweeps (graph replays): m = 8 gate 14336x4096 17.4 vs 27.9 us, down
+  // 4096x14336 21.4 vs 36.0 us, q 4096x4096 6.9 vs 11.6 us; m = 3 11.6 vs
+  // 12.6, 15.0 vs 20.5, 5.1 vs 5.9 us. On 1024-row weights its smaller grid
+  // loses below seven rows (k 1024x4096 at m = 2: 3.94 vs 3.55 us), so
+  // weights under 2048 rows take it from m = 7. QMM_GEMV_ROWS=<m> takes it
+  // from m rows at every size (0: never).
+  int rows_from = w->n >= 2048 ? 2 : 7;
+  if (const char* e = getenv("QMM_GEMV_ROWS")) rows_from = atoi(e);
+  const unsigned long long rbody = fmt == kFmtQ4K ? 144 : 208;  // device block bodies (Q6_K's f16 d kept apart)
+  if (count == 1 && !fused && !silu && dump == nullptr && rows_from > 0 && m >= rows_from && m <= 8 &&
+      fmt != kFmtQ80 && nb <= 64 && (unsigned long long)w->n * nb * rbody < (1ull << 32)) {
+    char rname[32];
+    snprintf(rname, sizeof(rname), "qmm_gemv_rows_%s", fmt_name(fmt));
+    const void* wq = w->data;
+    float* yy = tg[0].y;
+    int ldy = (int)tg[0].ldy, mm = m, K = (int)w->k, N = (int)w->n, acc = accumulate;
+    void* args[] = {&wq, &yy, &ldy, &act, &mm, &K, &N, &acc};
+    const long long grid = std::min<long long>((long long)d->num_cu * 2, (N + 15) / 16);
+    return launch(d, rname, (unsigned)grid, 1024, (unsigned)(m * nb * 292), s, args);
+  }
   GemvJobs jobs = {};
   long long total = 0;
   for (int j = 0; j < count; ++j) {

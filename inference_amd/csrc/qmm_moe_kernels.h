@@ -227,7 +227,31 @@ struct MoePass {
   int N, ldy, nb, niter, row0, row_step, nslices;
   uint32_t rowb;   // row body bytes (an expert's rows span < 4 GiB: checked by the host)
   long long yrow;  // first output row of the pass (offsets[e] + mc)
+  int accumulate;  // y += result (each output has one writer, so y + v exactly)
 };
+
+// A workgroup's rows of the `total` rows shared by gx workgroups (this one is
+// bx). Rows longer than one slice (K > 4096): a contiguous block per
+// workgroup, its waves taking every NW-th row of it, so the workgroups stream
+// separate regions (config-5 down, 11.6 KB rows: 62.3 -> 58.8 us). One-slice
+// rows stay grid-stride over the workgroups (gate/up, 2.3 KB rows: contiguous
+// blocks measured 82.3 -> 84.1 us).
+template <int NW>
+__device__ __forceinline__ void pass_rows(MoePass& ps, int total, int bx, int gx, int wave) {
+  int nrows;
+  if (ps.niter > 1) {
+    const int per = (total + gx - 1) / gx;
+    const int rb0 = min(bx * per, total), rb1 = min(rb0 + per, total);
+    ps.row_step = NW;
+    ps.row0 = rb0 + wave;
+    nrows = ps.row0 < rb1 ? (rb1 - 1 - ps.row0) / NW + 1 : 0;
+  } else {
+    ps.row_step = gx * NW;
+    ps.row0 = bx * NW + wave;
+    nrows = ps.row0 < total ? (total - 1 - ps.row0) / ps.row_step + 1 : 0;
+  }
+  ps.nslices = nrows * ps.niter;
+}
 
 // Weight-side values of a lane's slice for several tokens: the Q4_K high
 // nibbles as plain 0..15 bytes, the scales that multiply the activation sums
@@ -438,13 +462,32 @@ __device__ __forceinline__ void moe_gemv1_pass(const MoePass& a, const uint8_t* 
           const float out = wave_totals<MR>(acc, lane);
 #pragma unroll
           for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
-          if (lane < MR) (j ? a.y1 : a.y0)[(size_t)(a.yrow + lane) * a.ldy + (gr - j * a.N)] = out;
+          if (lane < MR) {
+            float* yp = (j ? a.y1 : a.y0) + (size_t)(a.yrow + lane) * a.ldy + (gr - j * a.N);
+            *yp = a.accumulate ? *yp + out : out;
+          }
           c_it = 0;
           ++c_k;
         }
       }
       if (is_s < nslices) issue(ring[u]);
     }
+  }
+}
+
+// The pass for mr (1..8, workgroup-uniform) token rows.
+template <int FMT, int P, int NW>
+__device__ __forceinline__ void moe_gemv1_rows(const MoePass& ps, int mr, const uint8_t* __restrict__ xs,
+                                               uint8_t* lds) {
+  switch (mr) {
+    case 1: moe_gemv1_pass<FMT, P, NW, 1>(ps, xs, lds); break;
+    case 2: moe_gemv1_pass<FMT, P, NW, 2>(ps, xs, lds); break;
+    case 3: moe_gemv1_pass<FMT, P, NW, 3>(ps, xs, lds); break;
+    case 4: moe_gemv1_pass<FMT, P, NW, 4>(ps, xs, lds); break;
+    case 5: moe_gemv1_pass<FMT, P, NW, 5>(ps, xs, lds); break;
+    case 6: moe_gemv1_pass<FMT, P, NW, 6>(ps, xs, lds); break;
+    case 7: moe_gemv1_pass<FMT, P, NW, 7>(ps, xs, lds); break;
+    default: moe_gemv1_pass<FMT, P, NW, 8>(ps, xs, lds); break;
   }
 }
 
@@ -503,41 +546,14 @@ __device__ __forceinline__ void moe_gemv1(const uint8_t* __restrict__ w0, const 
   ps.ldy = ldy;
   ps.nb = nb;
   ps.niter = niter;
-  // Rows longer than one slice (K > 4096): a contiguous block of the
-  // expert's rows per workgroup, its waves taking every NW-th row of it, so
-  // the workgroups stream separate regions (config-5 down, 11.6 KB rows:
-  // 62.3 -> 58.8 us). One-slice rows stay grid-stride over the workgroups
-  // (gate/up, 2.3 KB rows: contiguous blocks measured 82.3 -> 84.1 us).
-  int nrows;
-  if (niter > 1) {
-    const int per = (total + gx - 1) / gx;
-    const int rb0 = min(bx * per, total), rb1 = min(rb0 + per, total);
-    ps.row_step = NW;
-    ps.row0 = rb0 + wave;
-    nrows = ps.row0 < rb1 ? (rb1 - 1 - ps.row0) / NW + 1 : 0;
-  } else {
-    ps.row_step = gx * NW;
-    ps.row0 = bx * NW + wave;
-    nrows = ps.row0 < total ? (total - 1 - ps.row0) / ps.row_step + 1 : 0;
-  }
-  ps.nslices = nrows * niter;
   ps.rowb = (uint32_t)rowb;
+  ps.accumulate = 0;
+  pass_rows<NW>(ps, total, bx, gx, wave);
   // a single pass per workgroup: with a loop over passes the state carried
   // across it pushes the eight inlined token counts past the scalar
   // registers (spilled into vector registers, then to memory)
-  const int mr = min(8, me - mc);
-  const uint8_t* xs = xq + (size_t)(off + mc) * xrow;
   ps.yrow = off + mc;
-  switch (mr) {  // workgroup-uniform
-    case 1: moe_gemv1_pass<FMT, P, NW, 1>(ps, xs, lds); break;
-    case 2: moe_gemv1_pass<FMT, P, NW, 2>(ps, xs, lds); break;
-    case 3: moe_gemv1_pass<FMT, P, NW, 3>(ps, xs, lds); break;
-    case 4: moe_gemv1_pass<FMT, P, NW, 4>(ps, xs, lds); break;
-    case 5: moe_gemv1_pass<FMT, P, NW, 5>(ps, xs, lds); break;
-    case 6: moe_gemv1_pass<FMT, P, NW, 6>(ps, xs, lds); break;
-    case 7: moe_gemv1_pass<FMT, P, NW, 7>(ps, xs, lds); break;
-    default: moe_gemv1_pass<FMT, P, NW, 8>(ps, xs, lds); break;
-  }
+  moe_gemv1_rows<FMT, P, NW>(ps, min(8, me - mc), xq + (size_t)(off + mc) * xrow, lds);
 }
 
 #define QMM_MOE1_KERNEL(FMT, NAME, P)                                                                           \
@@ -547,6 +563,40 @@ __device__ __forceinline__ void moe_gemv1(const uint8_t* __restrict__ w0, const 
                                   const int* __restrict__ counts, const int* __restrict__ offsets, int K) {    \
     moe_gemv1<FMT, P, 16>(w0, w1, njobs, N, E, y0, y1, ldy, xq, xrow, counts, offsets, K);                     \
   }
+// Dense GEMV of m (1..8) staged activation rows against one k-quant weight
+// [N, K] through the same pass (the expert GEMV with one expert holding every
+// row): for m = 6..8 it beats the general multi-row GEMV, with the same bits.
+template <int FMT, int P, int NW>
+__device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ w, float* __restrict__ y, int ldy,
+                                          const uint8_t* __restrict__ xq, int m, int K, int N, int accumulate) {
+  using namespace qmm;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int nb = K / 256;
+  const size_t rowb = (size_t)nb * FmtInfo<FMT>::kBodyBytes;
+  MoePass ps;
+  ps.wb0 = ps.wb1 = w;
+  ps.db0 = ps.db1 = reinterpret_cast<const uint16_t*>(w + (size_t)N * rowb);
+  ps.y0 = ps.y1 = y;
+  ps.N = N;
+  ps.ldy = ldy;
+  ps.nb = nb;
+  ps.niter = (nb + 15) / 16;
+  ps.rowb = (uint32_t)rowb;
+  ps.yrow = 0;
+  ps.accumulate = accumulate;
+  pass_rows<NW>(ps, N, (int)blockIdx.x, (int)gridDim.x, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+  moe_gemv1_rows<FMT, P, NW>(ps, m, xq, lds);
+}
+
+#define QMM_GEMV_ROWS_KERNEL(FMT, NAME)                                                                         \
+  extern "C" __global__ void __launch_bounds__(1024) qmm_gemv_rows_##NAME(                                     \
+      const uint8_t* __restrict__ w, float* __restrict__ y, int ldy, const uint8_t* __restrict__ xq, int m,     \
+      int K, int N, int accumulate) {                                                                          \
+    gemv_rows<FMT, 1, 16>(w, y, ldy, xq, m, K, N, accumulate);                                                  \
+  }
+QMM_GEMV_ROWS_KERNEL(qmm::kFmtQ4K, q4k)
+QMM_GEMV_ROWS_KERNEL(qmm::kFmtQ6K, q6k)
+
 QMM_MOE1_KERNEL(qmm::kFmtQ4K, q4k, 1)
 QMM_MOE1_KERNEL(qmm::kFmtQ4K, q4k, 2)
 QMM_MOE1_KERNEL(qmm::kFmtQ6K, q6k, 1)

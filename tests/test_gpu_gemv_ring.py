@@ -197,3 +197,39 @@ def test_moe_ring_gemv_equals_generic(monkeypatch, dt, K, skew):
         assert int(counts[3]) == T and int(counts.sum()) == T
     elif skew:
         assert int(counts[0]) > 8
+
+
+def _matmul_q(qt, xq, m, n, y0=None):
+    y = y0.clone() if y0 is not None else torch.full((m, n), float("nan"), device=DEV)
+    qmm._check(L().qmm_matmul_q_ex(qt.handle, xq.data_ptr(), m, y.data_ptr(), n, int(y0 is not None), None, 0,
+                                   S()))
+    torch.cuda.synchronize()
+    return y
+
+
+@pytest.mark.parametrize("dt", [GgmlDType.Q4K, GgmlDType.Q6K])
+@pytest.mark.parametrize("n,k", [(1000, 4096), (4099, 4096), (333, 5120), (700, 14336)])
+@pytest.mark.parametrize("m", [2, 5, 8])
+@pytest.mark.parametrize("acc", [False, True])
+def test_multirow_kernel_equals_general_gemv(monkeypatch, dt, n, k, m, acc):
+    """Two to eight staged rows of one k-quant weight take the token-interleaved multi-row kernel
+    (by default on weights of >= 2048 rows, from seven rows on smaller ones; QMM_GEMV_ROWS=2 forces it):
+    bit-identical to the general multi-row GEMV (QMM_GEMV_ROWS=0), with and without accumulation,
+    including a K with a partial slice (5120) and row counts that are not multiples of 16; within 1e-3
+    of the oracle."""
+    rng = np.random.default_rng(n * 7 + k + m + int(dt) + 100 * int(acc))
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    wq = orc.quantize(ORC[dt], w)
+    qt = QTensor.from_ggml(wq, dt, (n, k), device=DEV)
+    xq = t(orc.quantize(orc.Q8K, x), torch.uint8)
+    y0 = t(rng.standard_normal((m, n)).astype(np.float32)) if acc else None
+    monkeypatch.setenv("QMM_GEMV_ROWS", "2")
+    got = _matmul_q(qt, xq, m, n, y0)
+    monkeypatch.setenv("QMM_GEMV_ROWS", "0")
+    ref = _matmul_q(qt, xq, m, n, y0)
+    assert torch.equal(got, ref), "differs from the general multi-row GEMV"
+    want = orc.matmul(ORC[dt], x, wq, k)
+    if acc:
+        want = want + y0.cpu().numpy()
+    assert rel_err(got.cpu().numpy(), want) <= TOL
