@@ -1027,15 +1027,10 @@ int qmm_matmul_ex(const qmm_qtensor* const* w, int count, const float* x, int64_
     if (!same_act(w[j], w[0])) return fail(QMM_ERR_INVALID, "weights of one call must share k and dtype (or be Q4_K/Q6_K)");
     t[j] = {w[j], y[j], ldy[j]};
   }
-  if (m > 2) {  // quantized activation planes are per format: one pass per dtype
-    GemvTarget a[kMaxJobs], b[kMaxJobs];
-    int na = 0, nb = 0;
-    for (int j = 0; j < count; ++j) (w[j]->dtype == w[0]->dtype ? a[na++] : b[nb++]) = t[j];
-    if (nb > 0) {
-      QMM_TRY(matmul_targets(a, na, x, m, ldx, ws, ws_bytes, stream, norm_weight, eps, accumulate ? 1 : 0));
-      return matmul_targets(b, nb, x, m, ldx, ws, ws_bytes, stream, norm_weight, eps, accumulate ? 1 : 0);
-    }
-  }
+  // Q4_K and Q6_K jobs share one RMSNorm and one Q8_K quantization: both take
+  // Q8_K activations, in the same GGML rows (m <= 8) or GEMM planes (m > 8);
+  // each job's GEMV / GEMM then runs its own format (a q/k/v call with a
+  // Q6_K v normalised and quantized twice before: 2 x 9.7 us per prefill layer)
   return matmul_targets(t, count, x, m, ldx, ws, ws_bytes, stream, norm_weight, eps, accumulate ? 1 : 0);
 }
 

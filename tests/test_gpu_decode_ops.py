@@ -73,12 +73,13 @@ MIXES = [(GgmlDType.Q4K, GgmlDType.Q4K, GgmlDType.Q6K), (GgmlDType.Q6K, GgmlDTyp
 
 
 @pytest.mark.parametrize("dts", MIXES)
-@pytest.mark.parametrize("m", [1, 2, 5])
+@pytest.mark.parametrize("m", [1, 2, 5, 64])
 @pytest.mark.parametrize("norm", [False, True])
 @pytest.mark.parametrize("k", [4096, 20480])
 def test_matmul_ex_mixed_q4k_q6k_equals_separate_calls(dts, m, norm, k):
     """Q4_K and Q6_K weights in one qmm_matmul_ex call (one mixed launch at m = 1; per-format launches
-    otherwise): bit-identical to one call per weight. k = 20480 takes the long-row prologue."""
+    over one shared RMSNorm and Q8_K quantization otherwise: GGML rows at m = 5, GEMM planes at m = 64):
+    bit-identical to one call per weight. k = 20480 takes the long-row prologue."""
     rng = np.random.default_rng(40 + m + len(dts))
     rows = [700, 256, 300, 1000, 33][:len(dts)]
     qts = [QTensor.quantize(t((rng.standard_normal((n, k)) * 0.02).astype(np.float32)), dt)
