@@ -967,14 +967,29 @@ static int matmul_targets(const GemvTarget* tg, int count, const float* x, int64
   // layout: quantized activation (GGML rows or GEMM planes), normalised rows,
   // then (GEMM) split-K partials in the rest
   const size_t base = use_gemm(w, m) ? mmq_planes(w->dtype, m, w->k).total : qmm_matmul_workspace_size(w, m);
-  if (norm_w) {
+  // GEMM over Q8_K planes with RMSNorm: one launch normalises each row and
+  // writes the planes (the same values as qmm_rms_norm, then the quantizer)
+  const bool norm_planes = norm_w && use_gemm(w, m) && qmm_vec_dot_type(w->dtype) == QMM_Q8K &&
+                           w->k * 4 <= d->max_lds;
+  if (norm_w && !norm_planes) {
     float* xn = (float*)((uint8_t*)ws + base);
     QMM_TRY(qmm_rms_norm(x, m, w->k, ldx, norm_w, eps, xn, w->k, stream));
     x = xn;
     ldx = w->k;
   }
   if (use_gemm(w, m)) {
-    QMM_TRY(quantize_planes(d, w->dtype, x, m, w->k, ldx, (uint8_t*)ws, s));
+    if (norm_planes) {
+      const Planes pl = mmq_planes(w->dtype, m, w->k);
+      long long lx = ldx;
+      int kk = (int)w->k;
+      void* q8 = (uint8_t*)ws + pl.q8;
+      void* dd = (uint8_t*)ws + pl.d;
+      void* ss = (uint8_t*)ws + pl.s;
+      void* args[] = {&x, &lx, &norm_w, &eps, &kk, &q8, &dd, &ss};
+      QMM_TRY(launch(d, "qmm_rms_norm_q8k_mmq", (unsigned)m, 256, (unsigned)(w->k * 4), s, args));
+    } else {
+      QMM_TRY(quantize_planes(d, w->dtype, x, m, w->k, ldx, (uint8_t*)ws, s));
+    }
     // a job whose split plan needs more than the rest of the workspace runs
     // unsplit (size ws for the largest weight to split every job)
     float* part = (float*)((uint8_t*)ws + base + nrm);

@@ -468,6 +468,58 @@ extern "C" __global__ void __launch_bounds__(256) qmm_quantize_q8k_mmq_rows(cons
   qmm::put_q8k_plane(qmm::q8k_lane(x + (long long)rows[row] * ldx + 256LL * b, lane), w, nb, k, q8, d, s, lane);
 }
 
+// The same planes for RMSNorm rows, x / sqrt(mean(x^2) + eps) * w: one
+// workgroup of 256 threads per row sums the squares exactly as qmm_rms_norm
+// does (thread t walks t, t + 256, ... eight loads at a time; waves in
+// order) and forms the same f32 values, stages them in LDS (k floats of
+// dynamic LDS) and each wave quantizes whole 256-element blocks: the planes
+// of quantizing qmm_rms_norm's output, without its f32 copy or a launch.
+extern "C" __global__ void __launch_bounds__(256) qmm_rms_norm_q8k_mmq(const float* __restrict__ x, long long ldx,
+                                                                       const float* __restrict__ w, float eps,
+                                                                       int k, int8_t* __restrict__ q8,
+                                                                       float* __restrict__ d,
+                                                                       int16_t* __restrict__ s) {
+#pragma clang fp contract(off)
+  constexpr int NT = 256, U = 8;
+  extern __shared__ __attribute__((aligned(16))) float rowbuf[];
+  __shared__ float red[NT / 64];
+  const float* xr = x + blockIdx.x * ldx;
+  float ss = 0.0f;
+  for (int i0 = threadIdx.x; i0 < k; i0 += U * NT) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = i0 + u * NT < k ? xr[i0 + u * NT] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) ss += v[u] * v[u];
+  }
+  ss = qmm::wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i) t += red[i];
+  const float den = sqrtf(t / (float)k + eps);
+  for (int i0 = threadIdx.x; i0 < k; i0 += U * NT) {
+    float v[U], g[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * NT;
+      v[u] = i < k ? xr[i] : 0.0f;
+      g[u] = i < k ? w[i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i0 + u * NT < k) rowbuf[i0 + u * NT] = v[u] / den * g[u];
+  }
+  __syncthreads();
+  const int nb = k / 256, lane = threadIdx.x & 63;
+  for (int b = threadIdx.x >> 6; b < nb; b += NT / 64) {
+    const float4 e = *reinterpret_cast<const float4*>(rowbuf + 256 * b + 4 * lane);
+    qmm::put_q8k_plane(qmm::q8k_lane_vals(e.x, e.y, e.z, e.w, lane), (long long)blockIdx.x * nb + b, nb, k, q8, d, s,
+                       lane);
+  }
+}
+
 // The same planes for silu(g) * u (rows of k, row stride ld): the f32 values
 // of qmm_silu_mul, quantized in registers.
 extern "C" __global__ void __launch_bounds__(256) qmm_silu_mul_q8k_mmq(const float* __restrict__ g,

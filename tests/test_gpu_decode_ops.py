@@ -454,3 +454,30 @@ def test_greedy_advance():
     with pytest.raises(qmm.QmmError):
         qmm._check(L().qmm_greedy_advance(logits.data_ptr(), 5, toks.data_ptr(), 6, pos.data_ptr(), 1,
                                           ws.data_ptr(), 8, S()))
+
+
+@pytest.mark.parametrize("dt", [GgmlDType.Q4K, GgmlDType.Q6K])
+@pytest.mark.parametrize("m,k", [(37, 4096), (127, 4096), (64, 14336)])
+def test_matmul_ex_gemm_norm_planes_equal_two_launches(dt, m, k):
+    """At m > 8 the RMSNorm and the Q8_K GEMM planes come from one launch (qmm_rms_norm_q8k_mmq): the
+    same bits as qmm_rms_norm's rows quantized and multiplied without the norm."""
+    rng = np.random.default_rng(70 + m + k)
+    n = 768
+    qt = QTensor.quantize(t((rng.standard_normal((n, k)) * 0.02).astype(np.float32)), dt)
+    x = t((rng.standard_normal((m, k)) * 0.3).astype(np.float32))
+    nw = t(rng.uniform(0.5, 1.5, k).astype(np.float32))
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    wsb = int(L().qmm_matmul_ex_workspace_size(qt.handle, m, 1))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+
+    def mm(src, norm):
+        y = torch.full((m, n), float("nan"), device=DEV)
+        qmm._check(L().qmm_matmul_ex((vp * 1)(qt.handle.value), 1, src.data_ptr(), m, k,
+                                     nw.data_ptr() if norm else None, ctypes.c_float(1e-5), 0,
+                                     (vp * 1)(y.data_ptr()), (i64 * 1)(n), ws.data_ptr(), wsb, S()))
+        torch.cuda.synchronize()
+        return y
+    fused = mm(x, True)
+    xn = torch.empty((m, k), device=DEV)
+    qmm._check(L().qmm_rms_norm(x.data_ptr(), m, k, k, nw.data_ptr(), ctypes.c_float(1e-5), xn.data_ptr(), k, S()))
+    assert torch.equal(fused, mm(xn, False))
