@@ -147,35 +147,42 @@ extern "C" __global__ void qmm_prefill_rope_kv(float* __restrict__ q, float* __r
 namespace qmm {
 constexpr int kAttnSplits = 16;  // S
 
-template <int DPL>
-__device__ __forceinline__ void attn_row(float (&dst)[DPL], const float* __restrict__ row, int lane) {
-  if constexpr (DPL == 1) {
-    dst[0] = row[lane];
-  } else if constexpr (DPL == 2) {
-    const float2 v = reinterpret_cast<const float2*>(row)[lane];
-    dst[0] = v.x;
-    dst[1] = v.y;
-  } else {
-    const float4 v = reinterpret_cast<const float4*>(row)[lane];
-    dst[0] = v.x;
-    dst[1] = v.y;
-    dst[2] = v.z;
-    dst[3] = v.w;
+// One lane's share of a dim-wide row in the 16-lane-row layout: lane li
+// (0..15) of every row holds dims [R * li, R * li + R) with R = dim / 16.
+template <int R>
+__device__ __forceinline__ void attn_part(float (&dst)[R], const float* __restrict__ row, int li) {
+  const float4* p = reinterpret_cast<const float4*>(row + R * li);
+#pragma unroll
+  for (int c = 0; c < R / 4; ++c) {
+    const float4 v = p[c];
+    dst[4 * c] = v.x;
+    dst[4 * c + 1] = v.y;
+    dst[4 * c + 2] = v.z;
+    dst[4 * c + 3] = v.w;
   }
 }
 
-// x * cos + rotate_half(x) * sin with rotate_half = cat(-x2, x1): lanes < 32
-// hold the first half of the dims, their partners are lanes ^ 32.
-template <int DPL>
-__device__ __forceinline__ void attn_rope(float (&x)[DPL], const float (&cs)[DPL], const float (&sn)[DPL],
-                                          int lane) {
+// x * cos + rotate_half(x) * sin with rotate_half = cat(-x2, x1): lanes 0..7
+// of a row hold the first half of the dims, their partners are 8 lanes on
+// (a rotate by 8 within the row).
+template <int R>
+__device__ __forceinline__ void attn_rope(float (&x)[R], const float (&cs)[R], const float (&sn)[R], int li) {
 #pragma clang fp contract(off)
 #pragma unroll
-  for (int e = 0; e < DPL; ++e) {
-    const float other = __shfl_xor(x[e], 32);
-    const float rot = lane < 32 ? -other : other;
+  for (int e = 0; e < R; ++e) {
+    const float other = dpp_f<0x128>(x[e]);  // row_ror:8
+    const float rot = li < 8 ? -other : other;
     x[e] = x[e] * cs[e] + rot * sn[e];
   }
+}
+
+// Sum over a row of 16 lanes (every lane of the row receives it).
+__device__ __forceinline__ float row16_total(float v) {
+  v += dpp_f<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  v += dpp_f<0x140>(v);  // row_mirror
+  return v;
 }
 
 // PREFILL: one query per workgroup row, all its positions in one chunk: query
@@ -195,13 +202,16 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
                                                  long long ldo = 0) {
 #pragma clang fp contract(off)
   constexpr int dim = 64 * DPL;
-  constexpr int B = 16 / DPL;  // positions per wave batch
+  constexpr int R = dim / 16;  // dims per lane: a 16-lane row holds one position's row
+  constexpr int NR = 4 * NW;   // rows of 16 lanes in the workgroup, each scanning its own positions
+  constexpr int B = 2;         // positions per row and batch
   constexpr int NT = 64 * NW;
-  __shared__ float wst[NW][2 * GT];
-  __shared__ __attribute__((aligned(16))) float wo[NW][GT * dim];
+  __shared__ float wst[NR][2 * GT];
+  __shared__ __attribute__((aligned(16))) float wo[NR][GT * dim];
   __shared__ int last;
   const int g = blockIdx.x, c = PREFILL ? 0 : blockIdx.y, t = threadIdx.x;
   const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int li = lane & 15, row = 4 * wave + (lane >> 4);  // this lane's place in its row, the row's index
   const int G = heads / kv_heads;
   constexpr int S = PREFILL ? 1 : kAttnSplits;
   const bool rope = !PREFILL && cos_t != nullptr;
@@ -212,13 +222,13 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
 
   // loads, batch 1: pos, q of the group's heads, new k / v rows
   const int p = PREFILL ? min(first + (int)blockIdx.y, max_seq - 1) : min(max(pos[0], 0), max_seq - 1);
-  float qv[GT][DPL];
+  float qv[GT][R];
 #pragma unroll
-  for (int h = 0; h < GT; ++h) attn_row<DPL>(qv[h], q + (size_t)(g * G + min(h, G - 1)) * dim, lane);
-  float kn[DPL], vn[DPL];
+  for (int h = 0; h < GT; ++h) attn_part<R>(qv[h], q + (size_t)(g * G + min(h, G - 1)) * dim, li);
+  float kn[R], vn[R];
   if (rope) {
-    attn_row<DPL>(kn, k_new + (size_t)g * dim, lane);
-    attn_row<DPL>(vn, v_new + (size_t)g * dim, lane);
+    attn_part<R>(kn, k_new + (size_t)g * dim, li);
+    attn_part<R>(vn, v_new + (size_t)g * dim, li);
   }
 
   const int n = p + 1;
@@ -228,104 +238,103 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
   const bool own = j0 <= p && p < j1;
   const float* kc = kcache + (size_t)g * max_seq * dim;
   const float* vc = vcache + (size_t)g * max_seq * dim;
-  const int npos = nc > wave ? (nc - wave + NW - 1) / NW : 0;  // this wave's positions j0 + wave + NW i
+  // row r scans positions j0 + r + NR i; the wave's first row has the most
+  const int npos = nc > row ? (nc - row + NR - 1) / NR : 0;
+  const int nwave = nc > 4 * wave ? (nc - 4 * wave + NR - 1) / NR : 0;  // wave-uniform loop bound
 
-  // loads, batch 2: the wave's first k / v rows (clamped into the chunk), cos / sin at p
-  float kr[B][DPL], vr[B][DPL];
+  // loads, batch 2: the row's first k / v rows (clamped into the chunk), cos / sin at p
+  float kr[B][R], vr[B][R];
   const int jlast = max(j1 - 1, 0);
 #pragma unroll
   for (int b = 0; b < B; ++b) {
-    const int j = min(j0 + wave + NW * b, jlast);
-    attn_row<DPL>(kr[b], kc + (size_t)j * dim, lane);
-    attn_row<DPL>(vr[b], vc + (size_t)j * dim, lane);
+    const int j = min(j0 + row + NR * b, jlast);
+    attn_part<R>(kr[b], kc + (size_t)j * dim, li);
+    attn_part<R>(vr[b], vc + (size_t)j * dim, li);
   }
   if (rope) {
-    float cs[DPL], sn[DPL];
-    attn_row<DPL>(cs, cos_t + (size_t)p * dim, lane);
-    attn_row<DPL>(sn, sin_t + (size_t)p * dim, lane);
+    float cs[R], sn[R];
+    attn_part<R>(cs, cos_t + (size_t)p * dim, li);
+    attn_part<R>(sn, sin_t + (size_t)p * dim, li);
 #pragma unroll
-    for (int h = 0; h < GT; ++h) attn_rope<DPL>(qv[h], cs, sn, lane);
-    attn_rope<DPL>(kn, cs, sn, lane);
-    if (own && wave == 0) {
+    for (int h = 0; h < GT; ++h) attn_rope<R>(qv[h], cs, sn, li);
+    attn_rope<R>(kn, cs, sn, li);
+    if (own && t < 16) {  // the first row appends position p
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) {
-        kcache[((size_t)g * max_seq + p) * dim + lane * DPL + e] = kn[e];
-        vcache[((size_t)g * max_seq + p) * dim + lane * DPL + e] = vn[e];
+      for (int e = 0; e < R; ++e) {
+        kcache[((size_t)g * max_seq + p) * dim + R * li + e] = kn[e];
+        vcache[((size_t)g * max_seq + p) * dim + R * li + e] = vn[e];
       }
     }
   }
 
-  float m[GT], l[GT], o[GT][DPL];
+  float m[GT], l[GT], o[GT][R];
 #pragma unroll
   for (int h = 0; h < GT; ++h) {
     m[h] = -INFINITY;
     l[h] = 0.0f;
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) o[h][e] = 0.0f;
+    for (int e = 0; e < R; ++e) o[h][e] = 0.0f;
   }
-  // One batch of B positions (i0 .. i0 + B - 1 of this wave; those past npos
-  // are clamped duplicates and weigh nothing): all B x GT scores first (their
-  // wave sums are independent), then one online-softmax update per head.
-  // Positions past the wave's last (b >= nv, wave-uniform) are skipped: their
-  // weight would be exactly 0, so the sums are the same without them.
-  auto scan = [&](const float (&kb)[B][DPL], const float (&vb)[B][DPL], int i0) {
-    const int nv = min(B, npos - i0);
+  // One batch of B positions per row (i0 .. i0 + B - 1 of this row; those
+  // past npos are clamped duplicates and are masked to score -inf, weight
+  // 0): all B x GT scores first (16-lane row sums), then one online-softmax
+  // update per head. A row with no position yet keeps m = -inf, and the
+  // guards keep -inf - (-inf) out of exp.
+  auto scan = [&](const float (&kb)[B][R], const float (&vb)[B][R], int i0) {
     float sc[B][GT];
 #pragma unroll
     for (int b = 0; b < B; ++b) {
-      const bool at_p = rope && j0 + wave + NW * (i0 + b) == p;
+      const bool ok = i0 + b < npos;
+      const bool at_p = rope && j0 + row + NR * (i0 + b) == p;
 #pragma unroll
       for (int h = 0; h < GT; ++h) {
         float d = 0.0f;
-        if (b < nv) {
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) d += qv[h][e] * (at_p ? kn[e] : kb[b][e]);
-          d = wave_total(d) * scale;
-        }
-        sc[b][h] = d;
+        for (int e = 0; e < R; ++e) d += qv[h][e] * (at_p ? kn[e] : kb[b][e]);
+        d = row16_total(d) * scale;
+        sc[b][h] = ok ? d : -INFINITY;
       }
     }
 #pragma unroll
     for (int h = 0; h < GT; ++h) {
       float mx = m[h];
 #pragma unroll
-      for (int b = 0; b < B; ++b) mx = b < nv ? fmaxf(mx, sc[b][h]) : mx;
-      const float a = expf(m[h] - mx);  // 0 while m = -inf
+      for (int b = 0; b < B; ++b) mx = fmaxf(mx, sc[b][h]);
+      const float a = mx == -INFINITY ? 0.0f : expf(m[h] - mx);  // 0 while m = -inf
       float ls = l[h] * a;
-      float acc[DPL];
+      float acc[R];
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) acc[e] = o[h][e] * a;
+      for (int e = 0; e < R; ++e) acc[e] = o[h][e] * a;
 #pragma unroll
       for (int b = 0; b < B; ++b) {
-        if (b >= nv) break;
-        const bool at_p = rope && j0 + wave + NW * (i0 + b) == p;
-        const float w = expf(sc[b][h] - mx);
+        const bool at_p = rope && j0 + row + NR * (i0 + b) == p;
+        const float w = sc[b][h] == -INFINITY ? 0.0f : expf(sc[b][h] - mx);
         ls += w;
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[e] += w * (at_p ? vn[e] : vb[b][e]);
+        for (int e = 0; e < R; ++e) acc[e] += w * (at_p ? vn[e] : vb[b][e]);
       }
       m[h] = mx;
       l[h] = ls;
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) o[h][e] = acc[e];
+      for (int e = 0; e < R; ++e) o[h][e] = acc[e];
     }
   };
-  if (npos > 0) {
+  if (nwave > 0) {
     int i0 = 0;
-    for (; i0 + B < npos; i0 += B) {
+    for (; i0 + B < nwave; i0 += B) {
       // next batch in flight (clamped, unconditional) while this one is scored
-      float kx[B][DPL], vx[B][DPL];
+      float kx[B][R], vx[B][R];
 #pragma unroll
       for (int b = 0; b < B; ++b) {
-        const int j = min(j0 + wave + NW * (i0 + B + b), jlast);
-        attn_row<DPL>(kx[b], kc + (size_t)j * dim, lane);
-        attn_row<DPL>(vx[b], vc + (size_t)j * dim, lane);
+        const int j = min(j0 + row + NR * (i0 + B + b), jlast);
+        attn_part<R>(kx[b], kc + (size_t)j * dim, li);
+        attn_part<R>(vx[b], vc + (size_t)j * dim, li);
       }
       scan(kr, vr, i0);
 #pragma unroll
       for (int b = 0; b < B; ++b)
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) {
+        for (int e = 0; e < R; ++e) {
           kr[b][e] = kx[b][e];
           vr[b][e] = vx[b][e];
         }
@@ -333,16 +342,16 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
     scan(kr, vr, i0);
   }
 
-  // the waves' states -> the chunk's record per head
+  // the rows' states -> the chunk's record per head
 #pragma unroll
   for (int h = 0; h < GT; ++h)
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) wo[wave][h * dim + lane * DPL + e] = o[h][e];
-  if (lane == 0) {
+    for (int e = 0; e < R; ++e) wo[row][h * dim + R * li + e] = o[h][e];
+  if (li == 0) {
 #pragma unroll
     for (int h = 0; h < GT; ++h) {
-      wst[wave][2 * h] = m[h];
-      wst[wave][2 * h + 1] = l[h];
+      wst[row][2 * h] = m[h];
+      wst[row][2 * h + 1] = l[h];
     }
   }
   __syncthreads();
@@ -351,10 +360,10 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
     const int h = i / dim, d = i % dim;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, wst[w][2 * h]);
+    for (int w = 0; w < NR; ++w) M = fmaxf(M, wst[w][2 * h]);
     float lsum = 0.0f, osum = 0.0f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
+    for (int w = 0; w < NR; ++w) {
       if (wst[w][2 * h] != -INFINITY) {
         const float a = expf(wst[w][2 * h] - M);
         lsum += wst[w][2 * h + 1] * a;
