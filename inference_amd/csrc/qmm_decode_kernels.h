@@ -104,14 +104,15 @@ extern "C" __global__ void qmm_prefill_rope_kv(float* __restrict__ q, float* __r
 //
 // Workgroup (g, c) of a kv_heads x S grid takes the G = heads / kv_heads
 // query heads of kv head g (repeat_kv maps query head h to kv head h / G)
-// and the c-th of S contiguous chunks of the n = p + 1 positions. Its NW
-// waves scan the chunk's positions round-robin straight from the cache: lane
-// l holds dims [l * dim/64, (l+1) * dim/64) of q, k_j and v_j, so a score
-// s_j = (q . k_j) * scale is a wave-wide sum (DPP + v_readlane) and the
-// softmax runs online per wave, a batch of positions at a time (m = running
-// max, l = sum exp(s - m), o = sum exp(s - m) v). The next batch's k/v rows
-// are loaded while the current batch is scored. The waves' states are
-// combined through LDS.
+// and the c-th of S contiguous chunks of the n = p + 1 positions. Its lanes
+// form 16-lane rows, 4 NW of them; row r scans positions c0 + r,
+// c0 + r + 4 NW, ... of the chunk straight from the cache, lane i of a row
+// holding dims [i * dim/16, (i+1) * dim/16) of q, k_j and v_j, so a score
+// s_j = (q . k_j) * scale is a 16-lane sum (4 DPP steps) and the softmax runs
+// online per row, a batch of positions at a time (m = running max,
+// l = sum exp(s - m), o = sum exp(s - m) v). The next batch's k/v rows are
+// loaded while the current batch is scored. The rows' states are combined
+// through LDS.
 //
 // The chunk's record (m, l, o[dim]) per head goes to the workspace; one
 // thread then bumps the kv head's counter with a device-scope (agent)
@@ -139,8 +140,8 @@ extern "C" __global__ void qmm_prefill_rope_kv(float* __restrict__ q, float* __r
 // 488 vs 495 tok/s).
 //
 // With cos/sin (fused RoPE + KV append), q and k are the unrotated
-// projections: q is rotated in registers (the partner of dim d is in lane
-// l ^ 32); the workgroup whose chunk holds p rotates k, appends k and v at
+// projections: q is rotated in registers (the partner of dim d is 8 lanes
+// away in its row); the workgroup whose chunk holds p rotates k, appends k and v at
 // position p of the cache and uses them for that position. Without cos/sin,
 // q is already rotated and the cache already holds position p.
 // dim = 64 * DPL (64, 128, 256); G <= GT (1, 2, 4, 8).
@@ -431,11 +432,11 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
     qmm::decode_attention<DPL, GT, NW>(q, k_new, v_new, cos_t, sin_t, pos, kcache, vcache, part, counters, out, \
                                        heads, kv_heads, max_seq, scale);                                        \
   }
-#define QMM_ATTN_KERNELS(DPL) \
-  QMM_ATTN_KERNEL(DPL, 1, 4) QMM_ATTN_KERNEL(DPL, 2, 4) QMM_ATTN_KERNEL(DPL, 4, 4) QMM_ATTN_KERNEL(DPL, 8, 4)
-QMM_ATTN_KERNELS(1)
-QMM_ATTN_KERNELS(2)
-QMM_ATTN_KERNELS(4)
+// Eight waves (32 rows) where their LDS staging of the rows' states fits
+// (GT * dim <= 512: 64 KB), four otherwise; the host picks the same.
+QMM_ATTN_KERNEL(1, 1, 8) QMM_ATTN_KERNEL(1, 2, 8) QMM_ATTN_KERNEL(1, 4, 8) QMM_ATTN_KERNEL(1, 8, 8)
+QMM_ATTN_KERNEL(2, 1, 8) QMM_ATTN_KERNEL(2, 2, 8) QMM_ATTN_KERNEL(2, 4, 8) QMM_ATTN_KERNEL(2, 8, 4)
+QMM_ATTN_KERNEL(4, 1, 8) QMM_ATTN_KERNEL(4, 2, 8) QMM_ATTN_KERNEL(4, 4, 4) QMM_ATTN_KERNEL(4, 8, 4)
 
 
 // Causal attention of a prompt's rows (batched prefill): grid kv_heads x rows.

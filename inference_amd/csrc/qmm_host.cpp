@@ -1134,7 +1134,9 @@ static int attention(const float* q, const float* k, const float* v, const float
   float* part = (float*)((uint8_t*)ws + attn_counter_bytes(kv_heads));
   const int G = heads / kv_heads;
   const int gt = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;
-  const int splits = kAttnSplits, nw = 4;
+  // eight waves where the kernel's LDS staging of 32 rows fits (gt * head_dim
+  // <= 512); config 3 (head_dim 128, G = 4): 508 -> 520 tok/s over four waves
+  const int splits = kAttnSplits, nw = gt * head_dim <= 512 ? 8 : 4;
   char name[64];
   snprintf(name, sizeof(name), "qmm_decode_attention_d%d_g%d_w%d", head_dim / 64, gt, nw);
   void* args[] = {&q, &k, &v, &cos_t, &sin_t, &pos, &kcache, &vcache, &part, &counters, &out,

@@ -232,8 +232,8 @@ def attn_ws(heads, kv_heads, hd, max_seq):
 ATTN_GEOM = [(32, 8, 128), (8, 2, 64), (4, 4, 256), (32, 4, 128), (8, 1, 64)]
 
 
-# Positions on both sides of the switch from one workgroup per kv head (n <= 32 x waves: 128, 256 or
-# 512 positions for these geometries) to 16 chunks merged by the last workgroup, and past 4096.
+# Positions from one through fewer positions than the 16 chunks to many per chunk (merged by the
+# last workgroup), and past 4096.
 @pytest.mark.parametrize("heads,kv_heads,hd", ATTN_GEOM)
 @pytest.mark.parametrize("p", [0, 1, 17, 127, 128, 255, 256, 300, 511, 512, 4095, 6000])
 def test_decode_attention(heads, kv_heads, hd, p):
