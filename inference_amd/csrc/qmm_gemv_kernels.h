@@ -951,11 +951,17 @@ __device__ __forceinline__ void gemv(const GemvJobs& jobs, const void* __restric
 // each row's dot, the next row's first slice loaded before this row's
 // reduction, outputs kept one per lane (keep_v / keep_row, `slot` lanes
 // filled) and flushed 64 at a time. ws holds row `row`'s first slice on entry.
+// Q8_0 (one block per lane, so a K = 4096 row is two slices) keeps the next
+// slice in flight while one is used: wn holds the row's second slice on
+// entry (when it has one), and each iteration issues the one after.
+template <int FMT>
+constexpr bool kSlicePipe = FMT == kFmtQ80;
 template <int FMT, int J>
 __device__ __forceinline__ void gemv1_rows(const GemvJobs& jobs, JobCursor& jc, const JobArg* ja, RowRef& rr,
-                                           WSlice& ws, const XSlice& x0, const uint8_t* __restrict__ lds, int nb,
-                                           int& row, int end, int row_step, uint32_t b0, int g, int l, int lane,
-                                           float& keep_v, int& keep_row, int& slot, int accumulate) {
+                                           WSlice& ws, WSlice& wn, const XSlice& x0,
+                                           const uint8_t* __restrict__ lds, int nb, int& row, int end,
+                                           int row_step, uint32_t b0, int g, int l, int lane, float& keep_v,
+                                           int& keep_row, int& slot, int accumulate) {
   constexpr int BPI = 64 / FmtInfo<FMT>::kLanesPerBlock;
   const int niter = (nb + BPI - 1) / BPI;
   const bool ok0 = g < nb;
@@ -968,16 +974,26 @@ __device__ __forceinline__ void gemv1_rows(const GemvJobs& jobs, JobCursor& jc, 
     }
     for (int it = 1; it < niter; ++it) {
       const int b = it * BPI + g;
-      load_slice<FMT>(ws, rr.wrow, rr.drow, (uint32_t)min(b, nb - 1), l);
-      XSlice x;
-      load_x<FMT>(x, lds, nb, b < nb ? b : 0, l);
-      const float p = dot_wx<FMT>(prep_w<FMT>(ws, l), x, ia, ib);
-      acc += b < nb ? p : 0.0f;
+      if constexpr (kSlicePipe<FMT>) {
+        const WSlice cur = wn;
+        if (it + 1 < niter) load_slice<FMT>(wn, rr.wrow, rr.drow, (uint32_t)min(b + BPI, nb - 1), l);
+        XSlice x;
+        load_x<FMT>(x, lds, nb, b < nb ? b : 0, l);
+        const float p = dot_wx<FMT>(prep_w<FMT>(cur, l), x, ia, ib);
+        acc += b < nb ? p : 0.0f;
+      } else {
+        load_slice<FMT>(ws, rr.wrow, rr.drow, (uint32_t)min(b, nb - 1), l);
+        XSlice x;
+        load_x<FMT>(x, lds, nb, b < nb ? b : 0, l);
+        const float p = dot_wx<FMT>(prep_w<FMT>(ws, l), x, ia, ib);
+        acc += b < nb ? p : 0.0f;
+      }
     }
     const int nrow = row + row_step;
-    if (nrow < end) {  // next row's first batch before this row's reduction
+    if (nrow < end) {  // next row's first batch (and second slice) before this row's reduction
       rr = cursor_row<FMT>(jc, ja, jobs.njobs, jobs.total, nrow, nb);
       load_slice<FMT>(ws, rr.wrow, rr.drow, b0, l);
+      if (kSlicePipe<FMT> && niter > 1) load_slice<FMT>(wn, rr.wrow, rr.drow, (uint32_t)min(BPI + g, nb - 1), l);
     }
     const float v = wave_total(acc);
     if (lane == slot) {
@@ -1019,7 +1035,7 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
   const JobArg* ja = job_args();
   JobCursor jc;
   cursor_init(jc, ja);
-  WSlice ws;
+  WSlice ws, wn;
   const uint32_t b0 = (uint32_t)min(g, nb - 1);  // clamped: every lane loads
   RowRef rr;
   const bool first6 = MIX && min(row, jobs.total - 1) >= end4;  // the wave starts in the Q6_K rows
@@ -1032,6 +1048,8 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
     } else {
       rr = cursor_row<FMT>(jc, ja, jobs.njobs, jobs.total, r0, nb);
       load_slice<FMT>(ws, rr.wrow, rr.drow, b0, l);
+      if (kSlicePipe<FMT> && nb > 64 / LPB)
+        load_slice<FMT>(wn, rr.wrow, rr.drow, (uint32_t)min(64 / LPB + g, nb - 1), l);
     }
   }
   if constexpr (FUSED) {
@@ -1052,8 +1070,8 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
     rr = cursor_row<FMT>(jc, ja, jobs.njobs, jobs.total, row, nb);
     XSlice x0;  // loop-invariant activation of the first iteration
     load_x<FMT>(x0, lds, nb, (int)b0, l);
-    gemv1_rows<FMT, J>(jobs, jc, ja, rr, ws, x0, lds, nb, row, end4, row_step, b0, g, l, lane, keep_v, keep_row,
-                       slot, accumulate);
+    gemv1_rows<FMT, J>(jobs, jc, ja, rr, ws, wn, x0, lds, nb, row, end4, row_step, b0, g, l, lane, keep_v,
+                       keep_row, slot, accumulate);
   }
   if constexpr (MIX) {
     if (row < jobs.total) {
@@ -1061,8 +1079,8 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
       if (!first6) load_slice<F6>(ws, rr.wrow, rr.drow, b0, l);  // after Q4_K rows: not prefetched
       XSlice x06;
       load_x<F6>(x06, lds6, nb, (int)b0, l);
-      gemv1_rows<F6, J>(jobs, jc, ja, rr, ws, x06, lds6, nb, row, jobs.total, row_step, b0, g, l, lane, keep_v,
-                        keep_row, slot, accumulate);
+      gemv1_rows<F6, J>(jobs, jc, ja, rr, ws, wn, x06, lds6, nb, row, jobs.total, row_step, b0, g, l, lane,
+                        keep_v, keep_row, slot, accumulate);
     }
   }
   if (slot > 0) flush_outputs<FMT, J>(jobs, nb, keep_v, keep_row, lane < slot, accumulate);
