@@ -76,6 +76,10 @@ def block_bytes(dt: int) -> int:
 
 
 def row_bytes(dt: int, k: int) -> int:
+    """GGML bytes of a row of k elements; k must be a whole number of blocks (the C routines
+    process every element they are given, so a partial block would run past the buffer)."""
+    if k <= 0 or k % _ELEMS[dt]:
+        raise ValueError(f"row length {k} is not a whole number of {_ELEMS[dt]}-element blocks (dtype {dt})")
     return k // _ELEMS[dt] * _BYTES[dt]
 
 

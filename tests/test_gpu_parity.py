@@ -185,6 +185,27 @@ def test_small_grid_walks_many_rows(dt, monkeypatch):
     assert rel_err(y, orc.matmul(ORC[dt], x, wq, k)) <= TOL
 
 
+@pytest.mark.parametrize("dt,k", [(GgmlDType.Q8_0, 4160), (GgmlDType.Q8_0, 5120), (GgmlDType.Q4K, 4352),
+                                  (GgmlDType.Q6K, 4352)])
+def test_one_row_many_rows_ragged_slices(dt, k, monkeypatch):
+    """One activation row (the one-row kernels) with every wave looping over ~12 rows of several
+    slices, the last one ragged: Q8_0 (one block per lane, 64 per slice) rows of 130 / 160 blocks
+    are three slices, the second issued with the first and each next row's first two before the
+    reduction; Q4_K / Q6_K rows of 17 blocks (16 per slice) are two."""
+    monkeypatch.setenv("QMM_GEMV_WAVES_PER_CU", "1")
+    n = 3000
+    w = normal(82, (n, k), 0.02)
+    wq = orc.quantize(ORC[dt], w)
+    qt = QTensor.from_ggml(wq, dt, w.shape, device=DEV)
+    x = normal(83, (1, k))
+    x[0, : k // 3] *= 20.0
+    y = QMatMul.from_qtensor(qt).forward(torch.from_numpy(x).to(DEV)).cpu().numpy()
+    assert rel_err(y, orc.matmul(ORC[dt], x, wq, k)) <= TOL
+    xq = quantize_rows(dt.vec_dot_type(), torch.from_numpy(x).to(DEV))
+    y2 = matmul_q(qt, xq, 1).cpu().numpy()
+    assert rel_err(y2, orc.matmul_prequant(ORC[dt], xq.cpu().numpy(), wq, k)) <= TOL
+
+
 CONFIG_SHAPES = [
     (GgmlDType.Q8_0, 4096, 4096, 0, 1),      # config 1 (seeds 0 / 1)
     (GgmlDType.Q4K, 4096, 4096, 2, 3),       # config 2: q_proj

@@ -111,6 +111,20 @@ def test_block_geometry_matches_reference_kat():
     assert orc.lib().orc_block_bytes(9) == 0  # unknown/unsupported tag
 
 
+def test_partial_blocks_are_refused_before_the_c_routines():
+    """The C routines convert every element they are handed, so a row of a partial block would run
+    past the buffer sized from whole blocks; the wrappers refuse it first."""
+    x = np.zeros((3, 4160), np.float32)  # 130 Q8_0 blocks, 16.25 k-quant blocks
+    assert orc.quantize(Q8_0, x).shape == (3, 130 * 34)
+    for dt in (Q4K, Q6K, Q8K):
+        with pytest.raises(ValueError, match="whole number"):
+            orc.quantize(dt, x)
+        with pytest.raises(ValueError, match="whole number"):
+            orc.row_bytes(dt, 4160)
+    with pytest.raises(ValueError, match="whole number"):
+        orc.row_bytes(Q8_0, 48)
+
+
 def test_q8_0_block_dequant_kat():
     # dequant.rs:834-848: d = 0.5, quants -16..15 -> q * 0.5
     b = np.zeros(34, np.uint8)
