@@ -212,6 +212,23 @@ int qmm_matmul_ex(const qmm_qtensor *const *w, int count, const float *x, int64_
                   void *ws, size_t ws_bytes, void *stream);
 size_t qmm_matmul_ex_workspace_size(const qmm_qtensor *w, int64_t m, int normalize);
 
+/* The gated feed-forward block of m rows (LlamaMlp::forward, SwiGLU,
+ * llama.rs:1385-1392, after the block's RMSNorm, nn.rs:22-31): with n = x
+ * RMS-normalised by norm_weight (or x itself when norm_weight is NULL),
+ * y (+)= down(silu(gate(n)) * up(n)); y may be x (the residual add). gate and
+ * up share shape and k; down's k is their n; every weight Q4_K or Q6_K. At
+ * m > 8 the gate and up GEMMs leave their split-K partials unsummed and one
+ * launch sums them (in split order), forms silu(g) * u and writes the down
+ * GEMM's Q8_K planes: the same values as qmm_matmul_ex, qmm_silu_mul and
+ * qmm_matmul_ex in sequence, in three launches fewer. m <= 8 runs those
+ * GEMV calls. ws: qmm_ffn_workspace_size(gate, up, down, m, norm_weight !=
+ * NULL) bytes. */
+int qmm_ffn(const qmm_qtensor *gate, const qmm_qtensor *up, const qmm_qtensor *down, const float *x, int64_t m,
+            int64_t ldx, const float *norm_weight, float eps, int accumulate, float *y, int64_t ldy, void *ws,
+            size_t ws_bytes, void *stream);
+size_t qmm_ffn_workspace_size(const qmm_qtensor *gate, const qmm_qtensor *up, const qmm_qtensor *down, int64_t m,
+                              int normalize);
+
 /* ---- decode step of a Llama-style decoder (f32 ops around the matmuls) ---- */
 
 /* RMSNorm of m rows: out = x / sqrt(mean(x^2) + eps) * w (nn.rs:22-31). */

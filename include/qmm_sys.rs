@@ -216,6 +216,27 @@ extern "C" {
 
     pub fn qmm_matmul_ex_workspace_size(w: *const QmmQTensor, m: i64, normalize: c_int) -> usize;
 
+    /// The gated feed-forward block of m rows (LlamaMlp::forward, SwiGLU,
+    /// llama.rs:1385-1392, after the block's RMSNorm, nn.rs:22-31): with n = x
+    /// RMS-normalised by norm_weight (or x itself when norm_weight is NULL),
+    /// y (+)= down(silu(gate(n)) * up(n)); y may be x (the residual add). gate and
+    /// up share shape and k; down's k is their n; every weight Q4_K or Q6_K. At
+    /// m > 8 the gate and up GEMMs leave their split-K partials unsummed and one
+    /// launch sums them (in split order), forms silu(g) * u and writes the down
+    /// GEMM's Q8_K planes: the same values as qmm_matmul_ex, qmm_silu_mul and
+    /// qmm_matmul_ex in sequence, in three launches fewer. m <= 8 runs those
+    /// GEMV calls. ws: qmm_ffn_workspace_size(gate, up, down, m, norm_weight !=
+    /// NULL) bytes.
+    pub fn qmm_ffn(
+        gate: *const QmmQTensor, up: *const QmmQTensor, down: *const QmmQTensor, x: *const f32, m: i64, ldx: i64,
+        norm_weight: *const f32, eps: f32, accumulate: c_int, y: *mut f32, ldy: i64, ws: *mut c_void,
+        ws_bytes: usize, stream: *mut c_void
+    ) -> c_int;
+
+    pub fn qmm_ffn_workspace_size(
+        gate: *const QmmQTensor, up: *const QmmQTensor, down: *const QmmQTensor, m: i64, normalize: c_int
+    ) -> usize;
+
     /// RMSNorm of m rows: out = x / sqrt(mean(x^2) + eps) * w (nn.rs:22-31).
     pub fn qmm_rms_norm(
         x: *const f32, m: i64, k: i64, ldx: i64, w: *const f32, eps: f32, out: *mut f32, ldo: i64,

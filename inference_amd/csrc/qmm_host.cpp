@@ -776,18 +776,12 @@ static size_t gemm_split_bytes(const qmm_qtensor* w, int64_t m) {
   return p.splits > 1 ? align256((size_t)p.splits * (size_t)m * (size_t)w->n * 4) : 0;
 }
 
-// Prefill GEMM over activation planes at `ws` (see mmq_planes); `part` holds
-// part_bytes of scratch for split partials (a split plan that does not fit
-// runs as one split).
-static int gemm(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, float* y, int64_t ldy, int* dump,
-                hipStream_t s, int accumulate, float* part, size_t part_bytes) {
+// The GEMM kernel of plan p over activation planes at `ws` (see mmq_planes):
+// unsplit, into y (row stride ldy, accumulate as asked); split, the f32
+// partials [p.splits][m][n] into `part` and nothing summed.
+static int gemm_launch(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, const GemmPlan& p, float* y,
+                       int64_t ldy, int* dump, hipStream_t s, int accumulate, float* part) {
   const Planes pl = mmq_planes(w->dtype, m, w->k);
-  GemmPlan p = gemm_plan(d, w, m, dump != nullptr);
-  const size_t need = (size_t)p.splits * (size_t)m * (size_t)w->n * 4;
-  if (p.splits > 1 && (part == nullptr || need > part_bytes)) {
-    p.splits = 1;
-    p.kc = (int)(w->k / 256);
-  }
   const bool split = p.splits > 1;
   const void* wq = w->data;
   const void* q8 = ws + pl.q8;
@@ -807,7 +801,31 @@ static int gemm(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, f
   hipFunction_t f;
   QMM_TRY(kernel(d, p.name, &f));
   QMM_HIP(hipModuleLaunchKernel(f, p.gx, p.gy, (unsigned)p.splits, p.threads, 1, 1, p.lds, s, args, nullptr));
-  if (split) {
+  return QMM_OK;
+}
+
+// The plan of w at m rows, run unsplit when its partials would not fit in
+// part_bytes.
+static GemmPlan gemm_plan_fit(Device* d, const qmm_qtensor* w, int64_t m, bool dump, const float* part,
+                              size_t part_bytes) {
+  GemmPlan p = gemm_plan(d, w, m, dump);
+  const size_t need = (size_t)p.splits * (size_t)m * (size_t)w->n * 4;
+  if (p.splits > 1 && (part == nullptr || need > part_bytes)) {
+    p.splits = 1;
+    p.kc = (int)(w->k / 256);
+  }
+  return p;
+}
+
+// Prefill GEMM over activation planes at `ws` (see mmq_planes); `part` holds
+// part_bytes of scratch for split partials (a split plan that does not fit
+// runs as one split), which qmm_splitk_sum then adds into y.
+static int gemm(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, float* y, int64_t ldy, int* dump,
+                hipStream_t s, int accumulate, float* part, size_t part_bytes) {
+  const GemmPlan p = gemm_plan_fit(d, w, m, dump != nullptr, part, part_bytes);
+  QMM_TRY(gemm_launch(d, w, ws, m, p, y, ldy, dump, s, accumulate, part));
+  if (p.splits > 1) {
+    int M = (int)m, N = (int)w->n;
     const float* pp = part;
     int sp = p.splits, lo = (int)ldy;
     void* a2[] = {&pp, &sp, &M, &N, &y, &lo, &accumulate};
@@ -1054,6 +1072,139 @@ size_t qmm_matmul_ex_workspace_size(const qmm_qtensor* w, int64_t m, int normali
   size_t b = qmm_matmul_workspace_size(w, m);
   if (normalize && m > 2) b += align256((size_t)(m * w->k) * 4);
   return b;
+}
+
+// ---------------------------------------------------------------------------
+// the feed-forward block of a prompt's rows: y (+)= down(silu(gate(n)) * up(n))
+// ---------------------------------------------------------------------------
+
+// Workspace regions of qmm_ffn. m > 8 (GEMMs): the input's planes (and its
+// normalised rows when the fused norm-planes launch cannot hold a row in LDS),
+// gate's and up's outputs as their split-K partials (one plane when a GEMM
+// runs unsplit), the SiLU product's planes, the down GEMM's split partials.
+// m <= 8 (GEMVs): gate / up outputs, the product's Q8_K rows, then
+// qmm_matmul_ex's workspace for gate / up.
+struct FfnWs {
+  size_t xp, xn, g, u, hp, part, total;
+  int gsplits, usplits;
+};
+
+static int ffn_check(const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* down, int64_t m) {
+  if (!gate || !up || !down) return fail(QMM_ERR_INVALID, "null weight");
+  if (m < 1) return fail(QMM_ERR_INVALID, "ffn needs m >= 1 (got %lld)", (long long)m);
+  if (qmm_vec_dot_type(gate->dtype) != QMM_Q8K || qmm_vec_dot_type(down->dtype) != QMM_Q8K || !same_act(gate, up))
+    return fail(QMM_ERR_UNSUPPORTED, "ffn needs Q4_K / Q6_K gate, up and down weights");
+  if (gate->n != up->n || down->k != gate->n)
+    return fail(QMM_ERR_INVALID, "ffn shapes: gate %lldx%lld, up %lldx%lld, down %lldx%lld", (long long)gate->n,
+                (long long)gate->k, (long long)up->n, (long long)up->k, (long long)down->n, (long long)down->k);
+  return QMM_OK;
+}
+
+static FfnWs ffn_ws(Device* d, const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* down, int64_t m,
+                    bool normalize) {
+  FfnWs w = {};
+  const int64_t H = gate->k, F = gate->n;
+  size_t o = 0;
+  if (m > 8) {
+    w.xp = o;
+    o += mmq_planes(gate->dtype, m, H).total;
+    w.xn = o;
+    if (normalize && (size_t)H * 4 > (size_t)d->max_lds) o += align256((size_t)(m * H) * 4);
+    w.gsplits = gemm_plan(d, gate, m, false).splits;
+    w.usplits = gemm_plan(d, up, m, false).splits;
+    w.g = o;
+    o += align256((size_t)w.gsplits * (size_t)(m * F) * 4);
+    w.u = o;
+    o += align256((size_t)w.usplits * (size_t)(m * F) * 4);
+    w.hp = o;
+    o += mmq_planes(down->dtype, m, F).total;
+    w.part = o;
+    o += gemm_split_bytes(down, m);
+  } else {
+    w.g = o;
+    o += align256((size_t)(m * F) * 4);
+    w.u = o;
+    o += align256((size_t)(m * F) * 4);
+    w.hp = o;
+    o += align256((size_t)m * (size_t)(F / 256) * (size_t)qmm_type_size(QMM_Q8K));
+    w.part = o;
+    o += std::max(qmm_matmul_ex_workspace_size(gate, m, normalize ? 1 : 0),
+                  qmm_matmul_ex_workspace_size(up, m, normalize ? 1 : 0));
+  }
+  w.total = o;
+  return w;
+}
+
+size_t qmm_ffn_workspace_size(const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* down, int64_t m,
+                              int normalize) {
+  if (ffn_check(gate, up, down, m) != QMM_OK) return 0;
+  Device* d;
+  if (current_device(&d) != QMM_OK) return 0;
+  return ffn_ws(d, gate, up, down, m, normalize != 0).total;
+}
+
+int qmm_ffn(const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* down, const float* x, int64_t m,
+            int64_t ldx, const float* norm_weight, float eps, int accumulate, float* y, int64_t ldy, void* ws,
+            size_t ws_bytes, void* stream) {
+  QMM_TRY(ffn_check(gate, up, down, m));
+  QMM_TRY(check_matmul(down, m, y, ldy));
+  if (!x) return fail(QMM_ERR_INVALID, "null activation");
+  const int64_t H = gate->k, F = gate->n;
+  if (ldx < H) return fail(QMM_ERR_INVALID, "row stride %lld < k %lld", (long long)ldx, (long long)H);
+  Device* d;
+  QMM_TRY(current_device(&d));
+  hipStream_t s = (hipStream_t)stream;
+  const FfnWs L = ffn_ws(d, gate, up, down, m, norm_weight != nullptr);
+  if (!ws || ws_bytes < L.total) return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed", ws_bytes, L.total);
+  uint8_t* b = (uint8_t*)ws;
+  float* g = (float*)(b + L.g);
+  float* u = (float*)(b + L.u);
+  if (m <= 8) {
+    const qmm_qtensor* gw[2] = {gate, up};
+    float* gy[2] = {g, u};
+    const int64_t ld2[2] = {F, F};
+    QMM_TRY(qmm_matmul_ex(gw, 2, x, m, ldx, norm_weight, eps, 0, gy, ld2, b + L.part, ws_bytes - L.part, stream));
+    QMM_TRY(qmm_silu_mul_quantize(g, u, m, F, F, b + L.hp, stream));
+    return qmm_matmul_q_ex(down, b + L.hp, m, y, ldy, accumulate, nullptr, 0, stream);
+  }
+  // the input's Q8_K planes, normalised on the way when asked
+  const Planes px = mmq_planes(gate->dtype, m, H);
+  if (norm_weight && (size_t)H * 4 <= (size_t)d->max_lds) {
+    long long lx = ldx;
+    int kk = (int)H;
+    void* q8 = b + L.xp + px.q8;
+    void* dd = b + L.xp + px.d;
+    void* ss = b + L.xp + px.s;
+    void* args[] = {&x, &lx, &norm_weight, &eps, &kk, &q8, &dd, &ss};
+    QMM_TRY(launch(d, "qmm_rms_norm_q8k_mmq", (unsigned)m, 256, (unsigned)(H * 4), s, args));
+  } else {
+    const float* xs = x;
+    int64_t lx = ldx;
+    if (norm_weight) {
+      float* xn = (float*)(b + L.xn);
+      QMM_TRY(qmm_rms_norm(x, m, H, ldx, norm_weight, eps, xn, H, stream));
+      xs = xn;
+      lx = H;
+    }
+    QMM_TRY(quantize_planes(d, gate->dtype, xs, m, H, lx, b + L.xp, s));
+  }
+  // gate and up, their split partials left unsummed
+  const GemmPlan pg = gemm_plan(d, gate, m, false), pu = gemm_plan(d, up, m, false);
+  QMM_TRY(gemm_launch(d, gate, b + L.xp, m, pg, g, F, nullptr, s, 0, g));
+  QMM_TRY(gemm_launch(d, up, b + L.xp, m, pu, u, F, nullptr, s, 0, u));
+  // split sums, silu(g) * u and the down GEMM's Q8_K planes in one launch
+  {
+    const Planes ph = mmq_planes(down->dtype, m, F);
+    const float* gp = g;
+    const float* upp = u;
+    int gsp = pg.splits, usp = pu.splits, kk = (int)F, mm = (int)m;
+    void* q8 = b + L.hp + ph.q8;
+    void* dd = b + L.hp + ph.d;
+    void* ss = b + L.hp + ph.s;
+    void* args[] = {&gp, &gsp, &upp, &usp, &q8, &dd, &ss, &kk, &mm};
+    QMM_TRY(launch(d, "qmm_splitk_silu_mul_q8k_mmq", ceil_div(m * (F / 256), 4), 256, 0, s, args));
+  }
+  return gemm(d, down, b + L.hp, m, y, ldy, nullptr, s, accumulate, (float*)(b + L.part), ws_bytes - L.part);
 }
 
 // ---------------------------------------------------------------------------

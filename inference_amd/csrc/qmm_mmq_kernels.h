@@ -539,6 +539,44 @@ extern "C" __global__ void __launch_bounds__(256) qmm_silu_mul_q8k_mmq(const flo
   qmm::put_q8k_plane(qmm::q8k_lane_vals(e[0], e[1], e[2], e[3], lane), w, nb, k, q8, d, s, lane);
 }
 
+// The same planes from the gate and up GEMMs' unsummed split-K partials
+// (gp [gsplits][m][k], up [usplits][m][k]; one split is the plain output):
+// each value is summed in split order as qmm_splitk_sum sums it, so the
+// planes equal split sums, then qmm_silu_mul, then the quantizer, with three
+// launches fewer.
+extern "C" __global__ void __launch_bounds__(256) qmm_splitk_silu_mul_q8k_mmq(const float* __restrict__ gp, int gsplits,
+                                                                              const float* __restrict__ up, int usplits,
+                                                                              int8_t* __restrict__ q8,
+                                                                              float* __restrict__ d,
+                                                                              int16_t* __restrict__ s, int k, int m) {
+#pragma clang fp contract(off)
+  const int nb = k / 256;
+  const long long w = (long long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (w >= (long long)m * nb) return;
+  const int row = (int)(w / nb), b = (int)(w % nb), lane = threadIdx.x & 63;
+  const long long o = (long long)row * k + 256LL * b + 4 * lane;
+  const size_t plane = (size_t)m * k;
+  float4 g = *reinterpret_cast<const float4*>(gp + o);
+  for (int j = 1; j < gsplits; ++j) {
+    const float4 v = *reinterpret_cast<const float4*>(gp + o + j * plane);
+    g.x += v.x;
+    g.y += v.y;
+    g.z += v.z;
+    g.w += v.w;
+  }
+  float4 u = *reinterpret_cast<const float4*>(up + o);
+  for (int j = 1; j < usplits; ++j) {
+    const float4 v = *reinterpret_cast<const float4*>(up + o + j * plane);
+    u.x += v.x;
+    u.y += v.y;
+    u.z += v.z;
+    u.w += v.w;
+  }
+  qmm::put_q8k_plane(qmm::q8k_lane_vals(qmm::silu_mul(g.x, u.x), qmm::silu_mul(g.y, u.y), qmm::silu_mul(g.z, u.z),
+                                        qmm::silu_mul(g.w, u.w), lane),
+                     w, nb, k, q8, d, s, lane);
+}
+
 //   Q8_0: q8 int8 [m][k], d f32 [m][k/32] (the f16-rounded block scale)
 extern "C" __global__ void __launch_bounds__(256) qmm_quantize_q8_0_mmq(const float* __restrict__ x, long long ldx,
                                                                         int8_t* __restrict__ q8,

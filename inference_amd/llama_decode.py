@@ -341,7 +341,9 @@ class DecodeSession:
 
         `trace(op, layer, bufs)`, when given, is called after each launch is enqueued (ops: embed, qkv,
         rope_kv, attention, o, gate_up, silu_mul, down); `bufs` holds the pass's row buffers (x, q, k, v,
-        att, g, u, h), so a checker can read them between launches."""
+        att, g, u, h), so a checker can read them between launches. Without a trace the feed-forward
+        block is one qmm_ffn call (gate / up split sums, SiLU and the down GEMM's quantization in one
+        launch), which gives the same bits as those three traced launches."""
         if self.prompt_len == 0 or self.steps_done != 0:
             raise qmm.QmmError(1, "prefill() needs the state reset() leaves")
         cfg, L, w = self.cfg, self.L, self.w
@@ -364,6 +366,9 @@ class DecodeSession:
         for lw in w.layers:
             for t in lw.values():
                 wsb = max(wsb, int(L.qmm_matmul_ex_workspace_size(t.handle, rows, 1)))
+            if trace is None:
+                wsb = max(wsb, int(L.qmm_ffn_workspace_size(lw["gate"].handle, lw["up"].handle,
+                                                             lw["down"].handle, rows, 1)))
         ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
         vp, i64 = ctypes.c_void_p, ctypes.c_int64
         eps = ctypes.c_float(cfg.eps)
@@ -394,6 +399,11 @@ class DecodeSession:
             qmm._check(L.qmm_matmul_ex((vp * 1)(lw["o"].handle.value), 1, att.data_ptr(), rows, nq, None, eps, 1,
                                        x_y, x_ld, ws.data_ptr(), ws.numel(), s))
             tr("o", li)
+            if trace is None:
+                qmm._check(L.qmm_ffn(lw["gate"].handle, lw["up"].handle, lw["down"].handle, x.data_ptr(), rows, H,
+                                     w.ffn_norm[li].data_ptr(), eps, 1, x.data_ptr(), H, ws.data_ptr(), ws.numel(),
+                                     s))
+                continue
             qmm._check(L.qmm_matmul_ex(self._gu[li], 2, x.data_ptr(), rows, H, w.ffn_norm[li].data_ptr(), eps, 0,
                                        gu_y, gu_ld, ws.data_ptr(), ws.numel(), s))
             tr("gate_up", li)
