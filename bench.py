@@ -792,7 +792,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
-              f"(the path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
+              f"(the path runs on one GPU; it is measured at one GPU's share of the work)", file=sys.stderr)
         sys.exit(2)
 
     import torch
