@@ -693,15 +693,36 @@ struct GemmPlan {
 // Split-K: a grid of fewer than half as many tiles as CUs (e.g. m = 127
 // against N = 4096: 32-64 tiles) leaves most CUs idle for the whole K loop;
 // splitting the K steps over blockIdx.z fills them, and a small kernel sums
-// the splits' f32 partials in split order. QMM_SPLITK=0 disables it,
-// QMM_SPLITK=<S> forces S splits.
+// the splits' f32 partials in split order. The count minimises (rounds of
+// the grid over the resident workgroup slots) x (K steps per split), with at
+// least two K steps per split (one-step splits spend more on writing and
+// re-reading their partials than they gain) and the smaller count on a tie.
+// Slots are CUs times the workgroups whose LDS fits in one CU. Per call at
+// m = 127 (quantization, GEMM and sum), against one split per CU / tiles:
+// gate 14336x4096 Q4_K 45.7 -> 36.6 us (2 splits, not 3: 336 one-per-CU
+// workgroups ran a second, mostly empty round), Q6_K down 4096x14336
+// 69.3 -> 57.3 us (8, not 4: its 60 KB tile fits twice per CU), k 1024x4096
+// 19.0 -> 17.5 us (8, not 16). QMM_SPLITK=0 disables it, QMM_SPLITK=<S>
+// forces S splits.
+static constexpr unsigned kMmqStaticLds = 61440;  // the first-generation tile's static LDS (MmqLds)
 static void plan_splits(const Device* d, GemmPlan& p, int nbk) {
   const long long tiles = (long long)p.gx * p.gy;
   int sp = 1;
   if (const char* e = getenv("QMM_SPLITK")) {
     sp = atoi(e);
   } else if (tiles * 2 <= d->num_cu) {
-    sp = (int)((d->num_cu + tiles - 1) / tiles);
+    const unsigned lds = p.lds ? p.lds : kMmqStaticLds;
+    const long long slots = (long long)d->num_cu * std::max(1u, (unsigned)d->max_lds / lds);
+    long long best = -1;
+    for (int c = 1; c <= std::min(16, nbk); ++c) {
+      const int kc = (nbk + c - 1) / c;
+      if (c > 1 && kc < 2) break;
+      const long long cost = (tiles * c + slots - 1) / slots * kc;
+      if (best < 0 || cost < best) {
+        best = cost;
+        sp = c;
+      }
+    }
   }
   sp = std::max(1, std::min(std::min(sp, 16), nbk));
   p.kc = (nbk + sp - 1) / sp;
