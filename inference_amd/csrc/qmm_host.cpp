@@ -705,6 +705,7 @@ struct GemmPlan {
 // 19.0 -> 17.5 us (8, not 16). QMM_SPLITK=0 disables it, QMM_SPLITK=<S>
 // forces S splits.
 static constexpr unsigned kMmqStaticLds = 61440;  // the first-generation tile's static LDS (MmqLds)
+static constexpr int kMmqBMRows = 64;             // and its M tile
 static void plan_splits(const Device* d, GemmPlan& p, int nbk) {
   const long long tiles = (long long)p.gx * p.gy;
   int sp = 1;
@@ -1585,7 +1586,7 @@ size_t qmm_moe_gemm_workspace_size(const qmm_qtensor* w, int64_t pairs) {
 
 static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, int experts, const uint8_t* planes,
                            int64_t pairs, int64_t max_rows, const int32_t* counts, const int32_t* offsets,
-                           float* const* y, hipStream_t s);
+                           float* const* y, hipStream_t s, float* part = nullptr, size_t part_bytes = 0);
 
 int qmm_moe_gemm(const qmm_qtensor* const* w, int count, int experts, const float* x, int64_t pairs, int64_t ldx,
                  int64_t max_rows, const int32_t* counts, const int32_t* offsets, float* const* y, void* ws,
@@ -1615,10 +1616,18 @@ int qmm_moe_gemm(const qmm_qtensor* const* w, int count, int experts, const floa
 }
 
 // The grouped GEMM launches over activation planes already at `planes`
-// (mmq_planes(w[0]->dtype, pairs, k) layout).
+// (mmq_planes(w[0]->dtype, pairs, k) layout). With `part` (part_bytes of
+// scratch), the first-generation tile (Q6_K, Q8_0) splits K as the dense
+// GEMM does, its split count from the same rounds x K-steps model over an
+// estimate of the active tiles (each expert's rows padded to the 64-row
+// tile: pairs / 64 + experts row tiles), and qmm_splitk_sum adds the
+// partials in split order. The config-5 prefill's Q6_K down projection
+// (1,024 pairs over 8 experts, ~640 active tiles on 512 resident slots)
+// ran two rounds of 56 K steps, the second a quarter full; 2 splits run
+// 2.5 rounds of 28. QMM_MOE_SPLITK=<S> forces S (0 or 1: unsplit).
 static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, int experts, const uint8_t* planes,
                            int64_t pairs, int64_t max_rows, const int32_t* counts, const int32_t* offsets,
-                           float* const* y, hipStream_t s) {
+                           float* const* y, hipStream_t s, float* part, size_t part_bytes) {
   const qmm_qtensor* w0 = w[0];
   const Planes pl = mmq_planes(w0->dtype, pairs, w0->k);
   const int fmt = fmt_of(w0->dtype);
@@ -1653,6 +1662,48 @@ static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, in
   }
   hipFunction_t f;
   QMM_TRY(kernel(d, name, &f));
+  if (fmt != kFmtQ4K) {
+    const int nbk = K / 256;
+    int sp = 1;
+    if (const char* e = getenv("QMM_MOE_SPLITK")) {
+      sp = std::max(1, atoi(e));
+    } else if (part) {
+      const long long tiles = (pairs / kMmqBMRows + experts) * ((N + bn - 1) / bn);
+      const long long slots = (long long)d->num_cu * std::max(1u, (unsigned)d->max_lds / kMmqStaticLds);
+      long long best = -1;
+      for (int c = 1; c <= std::min(8, nbk); ++c) {
+        const int kcc = (nbk + c - 1) / c;
+        if (c > 1 && kcc < 2) break;
+        const long long cost = (tiles * c + slots - 1) / slots * kcc;
+        if (best < 0 || cost < best) {
+          best = cost;
+          sp = c;
+        }
+      }
+    }
+    int kc = (nbk + sp - 1) / sp;
+    sp = (nbk + kc - 1) / kc;
+    if (sp > 1 && (part == nullptr || (size_t)sp * (size_t)pairs * (size_t)N * 4 > part_bytes)) {
+      sp = 1;
+      kc = nbk;
+    }
+    long long ysplit = sp > 1 ? pairs * N : 0;
+    for (int j = 0; j < count; ++j) {
+      const void* wq = w[j]->data;
+      float* yy = sp > 1 ? part : y[j];
+      void* args[] = {&wq, &q8, &dd, &ss, &yy, &N, &K, &ld, &E, &counts, &offsets, &kc, &ysplit};
+      QMM_HIP(hipModuleLaunchKernel(f, (unsigned)((N + bn - 1) / bn), (unsigned)((max_rows + bm - 1) / bm),
+                                    (unsigned)(experts * sp), threads, 1, 1, lds, s, args, nullptr));
+      if (sp > 1) {
+        const float* pp = part;
+        int spl = sp, M = (int)pairs, acc = 0;
+        float* yo = y[j];
+        void* a2[] = {&pp, &spl, &M, &N, &yo, &ld, &acc};
+        QMM_TRY(launch(d, "qmm_splitk_sum", ceil_div(pairs * N, 256), 256, 0, s, a2));
+      }
+    }
+    return QMM_OK;
+  }
   for (int j = 0; j < count; ++j) {
     const void* wq = w[j]->data;
     float* yy = y[j];
@@ -1837,9 +1888,12 @@ int qmm_moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* logits
         void* args[] = {&g, &u, &ld, &q8, &dd, &ss, &kk, &mm};
         QMM_TRY(launch(d, "qmm_silu_mul_q8k_mmq", ceil_div(P * (F / 256), 4), 256, 0, s, args));
       }
+      // the f32 SiLU rows (L.h) are not used on this path: their P x F floats
+      // hold the down GEMM's split partials (up to F / H splits)
       const qmm_qtensor* dw[1] = {down};
       float* dy[1] = {yp};
-      QMM_TRY(moe_gemm_planes(d, dw, 1, experts, pw8, P, tokens, counts, offsets, dy, s));
+      QMM_TRY(moe_gemm_planes(d, dw, 1, experts, pw8, P, tokens, counts, offsets, dy, s, (float*)(b + L.h),
+                              (size_t)(4 * P * F)));
     } else {
       float* xg = (float*)(b + L.xg);
       {

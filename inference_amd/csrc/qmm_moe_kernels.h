@@ -642,8 +642,7 @@ struct GroupRows {
 template <int BM, bool Q80>
 __device__ __forceinline__ bool group_rows(GroupRows& g, const int8_t* xq, const float* xd, const int16_t* xs,
                                            float* y, int K, int ldy, const int* __restrict__ counts,
-                                           const int* __restrict__ offsets) {
-  const int e = blockIdx.z;
+                                           const int* __restrict__ offsets, int e) {
   g.m = counts[e];
   if ((int)blockIdx.y * BM >= g.m) return false;
   const long long off = offsets[e];
@@ -663,7 +662,7 @@ __device__ __forceinline__ bool group_rows(GroupRows& g, const int8_t* xq, const
                                float* __restrict__ y, int N, int K, int ldy, int E,                             \
                                const int* __restrict__ counts, const int* __restrict__ offsets) {               \
     qmm::GroupRows g;                                                                                           \
-    if (!qmm::group_rows<BM, false>(g, xq, xd, xs, y, K, ldy, counts, offsets)) return;                         \
+    if (!qmm::group_rows<BM, false>(g, xq, xd, xs, y, K, ldy, counts, offsets, blockIdx.z)) return;             \
     const uint8_t* we = wq + (size_t)blockIdx.z * N * (K / 256) * qmm::kQ4KBytes;                               \
     qmm::mmq2_q4k<BM, 128, false>(we, g.xq, g.xd, g.xs, g.y, g.m, N, K, ldy, nullptr, 0, 0, 0, K / 256);        \
     (void)E;                                                                                                    \
@@ -679,25 +678,33 @@ qmm_moe_mmqs_q4k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq, 
                  const int16_t* __restrict__ xs, float* __restrict__ y, int N, int K, int ldy, int E,
                  const int* __restrict__ counts, const int* __restrict__ offsets) {
   qmm::GroupRows g;
-  if (!qmm::group_rows<qmm::kSBM, false>(g, xq, xd, xs, y, K, ldy, counts, offsets)) return;
+  if (!qmm::group_rows<qmm::kSBM, false>(g, xq, xd, xs, y, K, ldy, counts, offsets, blockIdx.z)) return;
   const uint8_t* we = wq + (size_t)blockIdx.z * N * (K / 256) * qmm::kQ4KBytes;
   qmm::mmqs_q4k<false>(we, g.xq, g.xd, g.xs, g.y, g.m, N, K, ldy, nullptr, 0, 0, 0, K / 256);
   (void)E;
 }
 
+// The first-generation tile (Q6_K, Q8_0) also splits K: blockIdx.z = expert
+// + E * split, split s takes K steps [s kc, s kc + kc) and writes its f32
+// partial to y + s * ysplit (the host sums them in split order).
 #define QMM_MOE_MMQ_KERNEL(FMT, NAME)                                                                          \
   extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))                 \
       qmm_moe_mmq_##NAME(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                        \
                          const float* __restrict__ xd, const int16_t* __restrict__ xs, float* __restrict__ y,   \
                          int N, int K, int ldy, int E, const int* __restrict__ counts,                          \
-                         const int* __restrict__ offsets) {                                                    \
+                         const int* __restrict__ offsets, int kc, long long ysplit) {                          \
+    const int e = (int)blockIdx.z % E, sp = (int)blockIdx.z / E;                                               \
     qmm::GroupRows g;                                                                                          \
-    if (!qmm::group_rows<qmm::kMmqBM, FMT == qmm::kFmtQ80>(g, xq, xd, xs, y, K, ldy, counts, offsets)) return; \
+    if (!qmm::group_rows<qmm::kMmqBM, FMT == qmm::kFmtQ80>(g, xq, xd, xs, y + sp * ysplit, K, ldy, counts,      \
+                                                            offsets, e))                                       \
+      return;                                                                                                  \
     const int nbw = FMT == qmm::kFmtQ80 ? K / 32 : K / 256;                                                    \
-    const size_t rows0 = (size_t)blockIdx.z * N;                                                               \
+    const size_t rows0 = (size_t)e * N;                                                                        \
     const uint16_t* wd = qmm::split_scales<FMT>(wq, (long long)E * N, K) + rows0 * nbw;                        \
     const uint8_t* we = wq + rows0 * nbw * qmm::FmtInfo<FMT>::kBodyBytes;                                      \
-    qmm::mmq<FMT, false>(we, wd, g.xq, g.xd, g.xs, g.y, g.m, N, K, ldy, nullptr, 0, 0, 0, K / 256);            \
+    const int kb0 = sp * kc;                                                                                   \
+    qmm::mmq<FMT, false>(we, wd, g.xq, g.xd, g.xs, g.y, g.m, N, K, ldy, nullptr, 0, 0, kb0,                    \
+                         min(kb0 + kc, K / 256));                                                              \
   }
 QMM_MOE_MMQ_KERNEL(qmm::kFmtQ6K, q6k)
 QMM_MOE_MMQ_KERNEL(qmm::kFmtQ80, q8_0)
