@@ -229,6 +229,26 @@ int qmm_ffn(const qmm_qtensor *gate, const qmm_qtensor *up, const qmm_qtensor *d
 size_t qmm_ffn_workspace_size(const qmm_qtensor *gate, const qmm_qtensor *up, const qmm_qtensor *down, int64_t m,
                               int normalize);
 
+/* The attention projections of m prompt rows with RoPE and the KV append
+ * (LlamaAttention::project and the cache update, llama.rs:1066-1114; apply_rope,
+ * rope.rs:289-323; kv_cache.rs:107-111): q / k / v = wq / wk / wv applied to
+ * x RMS-normalised by norm_weight (or x itself when NULL); the rows at
+ * positions first .. first + m - 1 are rotated with the cos/sin tables
+ * [max_seq][head_dim]; rotated q goes to q (row stride ldq), rotated k and v to
+ * the caches [kv_heads][max_seq][head_dim]. Weights Q4_K or Q6_K of one k. At
+ * m > 8 the three GEMMs leave their split-K partials unsummed and one launch
+ * sums them (in split order), rotates and appends: the same values as
+ * qmm_matmul_ex then qmm_rope_kv_append_n, in three launches fewer. m <= 8
+ * runs those two calls. ws: qmm_qkv_rope_kv_append_n_workspace_size(wq, wk,
+ * wv, m, norm_weight != NULL) bytes. */
+int qmm_qkv_rope_kv_append_n(const qmm_qtensor *wq, const qmm_qtensor *wk, const qmm_qtensor *wv, const float *x,
+                             int64_t m, int64_t ldx, const float *norm_weight, float eps, const float *cos_t,
+                             const float *sin_t, int64_t first, float *q, int64_t ldq, float *kcache,
+                             float *vcache, int heads, int kv_heads, int head_dim, int max_seq, void *ws,
+                             size_t ws_bytes, void *stream);
+size_t qmm_qkv_rope_kv_append_n_workspace_size(const qmm_qtensor *wq, const qmm_qtensor *wk, const qmm_qtensor *wv,
+                                               int64_t m, int normalize);
+
 /* ---- decode step of a Llama-style decoder (f32 ops around the matmuls) ---- */
 
 /* RMSNorm of m rows: out = x / sqrt(mean(x^2) + eps) * w (nn.rs:22-31). */

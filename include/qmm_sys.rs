@@ -237,6 +237,29 @@ extern "C" {
         gate: *const QmmQTensor, up: *const QmmQTensor, down: *const QmmQTensor, m: i64, normalize: c_int
     ) -> usize;
 
+    /// The attention projections of m prompt rows with RoPE and the KV append
+    /// (LlamaAttention::project and the cache update, llama.rs:1066-1114; apply_rope,
+    /// rope.rs:289-323; kv_cache.rs:107-111): q / k / v = wq / wk / wv applied to
+    /// x RMS-normalised by norm_weight (or x itself when NULL); the rows at
+    /// positions first .. first + m - 1 are rotated with the cos/sin tables
+    /// [max_seq][head_dim]; rotated q goes to q (row stride ldq), rotated k and v to
+    /// the caches [kv_heads][max_seq][head_dim]. Weights Q4_K or Q6_K of one k. At
+    /// m > 8 the three GEMMs leave their split-K partials unsummed and one launch
+    /// sums them (in split order), rotates and appends: the same values as
+    /// qmm_matmul_ex then qmm_rope_kv_append_n, in three launches fewer. m <= 8
+    /// runs those two calls. ws: qmm_qkv_rope_kv_append_n_workspace_size(wq, wk,
+    /// wv, m, norm_weight != NULL) bytes.
+    pub fn qmm_qkv_rope_kv_append_n(
+        wq: *const QmmQTensor, wk: *const QmmQTensor, wv: *const QmmQTensor, x: *const f32, m: i64, ldx: i64,
+        norm_weight: *const f32, eps: f32, cos_t: *const f32, sin_t: *const f32, first: i64, q: *mut f32, ldq: i64,
+        kcache: *mut f32, vcache: *mut f32, heads: c_int, kv_heads: c_int, head_dim: c_int, max_seq: c_int,
+        ws: *mut c_void, ws_bytes: usize, stream: *mut c_void
+    ) -> c_int;
+
+    pub fn qmm_qkv_rope_kv_append_n_workspace_size(
+        wq: *const QmmQTensor, wk: *const QmmQTensor, wv: *const QmmQTensor, m: i64, normalize: c_int
+    ) -> usize;
+
     /// RMSNorm of m rows: out = x / sqrt(mean(x^2) + eps) * w (nn.rs:22-31).
     pub fn qmm_rms_norm(
         x: *const f32, m: i64, k: i64, ldx: i64, w: *const f32, eps: f32, out: *mut f32, ldo: i64,

@@ -99,6 +99,52 @@ extern "C" __global__ void qmm_prefill_rope_kv(float* __restrict__ q, float* __r
                    max_seq);
 }
 
+// The same from the q / k / v GEMMs' unsummed split-K partials (qp
+// [qs][m][heads * dim], kp / vp [ks] / [vs][m][kv_heads * dim]; one split is
+// the plain output): each element is summed in split order as qmm_splitk_sum
+// sums it, then rotated exactly as qmm_prefill_rope_kv rotates it; the
+// rotated q rows go to q (row stride ldq), k and v to the caches only.
+extern "C" __global__ void qmm_prefill_splitk_rope_kv(const float* __restrict__ qp, int qs,
+                                                      const float* __restrict__ kp, int ks,
+                                                      const float* __restrict__ vp, int vs, int m,
+                                                      float* __restrict__ q, long long ldq,
+                                                      const float* __restrict__ cos_t,
+                                                      const float* __restrict__ sin_t, int first,
+                                                      float* __restrict__ kcache, float* __restrict__ vcache,
+                                                      int heads, int kv_heads, int dim, int max_seq) {
+#pragma clang fp contract(off)
+  __shared__ float row[1024];
+  const int r = blockIdx.y, h = blockIdx.x, i = threadIdx.x;
+  const int p = first + r;
+  if (p < 0 || p >= max_seq) return;
+  const bool isq = h < heads;
+  const int g = h - heads;
+  const int width = isq ? heads * dim : kv_heads * dim;
+  const float* src = isq ? qp : kp;
+  const int splits = isq ? qs : ks;
+  const size_t plane = (size_t)m * width;
+  const size_t o = (size_t)r * width + (size_t)(isq ? h : g) * dim + i;
+  float x = 0.0f;
+  if (i < dim) {
+    x = src[o];
+    for (int j = 1; j < splits; ++j) x += src[o + j * plane];
+    row[i] = x;
+  }
+  __syncthreads();
+  if (i >= dim) return;
+  const int half = dim / 2;
+  const float rot = i < half ? -row[i + half] : row[i - half];
+  const float out = x * cos_t[(size_t)p * dim + i] + rot * sin_t[(size_t)p * dim + i];
+  if (isq) {
+    q[(size_t)r * ldq + (size_t)h * dim + i] = out;
+    return;
+  }
+  kcache[((size_t)g * max_seq + p) * dim + i] = out;
+  float v = vp[o];
+  for (int j = 1; j < vs; ++j) v += vp[o + j * (size_t)m * width];
+  vcache[((size_t)g * max_seq + p) * dim + i] = v;
+}
+
 // One query token against positions 0..p of the cache (p = pos[0]) in one
 // launch ("flash decoding" with the merge done by the last workgroup).
 //

@@ -1100,6 +1100,31 @@ size_t qmm_matmul_ex_workspace_size(const qmm_qtensor* w, int64_t m, int normali
 // the feed-forward block of a prompt's rows: y (+)= down(silu(gate(n)) * up(n))
 // ---------------------------------------------------------------------------
 
+// The GEMM planes of m input rows at `xp` (Q8_K layout of dtype `wdtype`),
+// RMS-normalised first when norm_weight is given: one launch when a row fits
+// in LDS, else qmm_rms_norm into `xn` (m x k floats) and the quantizer.
+static int input_planes(Device* d, int wdtype, const float* x, int64_t m, int64_t k, int64_t ldx,
+                        const float* norm_weight, float eps, uint8_t* xp, float* xn, hipStream_t s) {
+  const Planes px = mmq_planes(wdtype, m, k);
+  if (norm_weight && (size_t)k * 4 <= (size_t)d->max_lds) {
+    long long lx = ldx;
+    int kk = (int)k;
+    void* q8 = xp + px.q8;
+    void* dd = xp + px.d;
+    void* ss = xp + px.s;
+    void* args[] = {&x, &lx, &norm_weight, &eps, &kk, &q8, &dd, &ss};
+    return launch(d, "qmm_rms_norm_q8k_mmq", (unsigned)m, 256, (unsigned)(k * 4), s, args);
+  }
+  const float* xs = x;
+  int64_t lx = ldx;
+  if (norm_weight) {
+    QMM_TRY(qmm_rms_norm(x, m, k, ldx, norm_weight, eps, xn, k, s));
+    xs = xn;
+    lx = k;
+  }
+  return quantize_planes(d, wdtype, xs, m, k, lx, xp, s);
+}
+
 // Workspace regions of qmm_ffn. m > 8 (GEMMs): the input's planes (and its
 // normalised rows when the fused norm-planes launch cannot hold a row in LDS),
 // gate's and up's outputs as their split-K partials (one plane when a GEMM
@@ -1190,26 +1215,7 @@ int qmm_ffn(const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* d
     return qmm_matmul_q_ex(down, b + L.hp, m, y, ldy, accumulate, nullptr, 0, stream);
   }
   // the input's Q8_K planes, normalised on the way when asked
-  const Planes px = mmq_planes(gate->dtype, m, H);
-  if (norm_weight && (size_t)H * 4 <= (size_t)d->max_lds) {
-    long long lx = ldx;
-    int kk = (int)H;
-    void* q8 = b + L.xp + px.q8;
-    void* dd = b + L.xp + px.d;
-    void* ss = b + L.xp + px.s;
-    void* args[] = {&x, &lx, &norm_weight, &eps, &kk, &q8, &dd, &ss};
-    QMM_TRY(launch(d, "qmm_rms_norm_q8k_mmq", (unsigned)m, 256, (unsigned)(H * 4), s, args));
-  } else {
-    const float* xs = x;
-    int64_t lx = ldx;
-    if (norm_weight) {
-      float* xn = (float*)(b + L.xn);
-      QMM_TRY(qmm_rms_norm(x, m, H, ldx, norm_weight, eps, xn, H, stream));
-      xs = xn;
-      lx = H;
-    }
-    QMM_TRY(quantize_planes(d, gate->dtype, xs, m, H, lx, b + L.xp, s));
-  }
+  QMM_TRY(input_planes(d, gate->dtype, x, m, H, ldx, norm_weight, eps, b + L.xp, (float*)(b + L.xn), s));
   // gate and up, their split partials left unsummed
   const GemmPlan pg = gemm_plan(d, gate, m, false), pu = gemm_plan(d, up, m, false);
   QMM_TRY(gemm_launch(d, gate, b + L.xp, m, pg, g, F, nullptr, s, 0, g));
@@ -1227,6 +1233,121 @@ int qmm_ffn(const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* d
     QMM_TRY(launch(d, "qmm_splitk_silu_mul_q8k_mmq", ceil_div(m * (F / 256), 4), 256, 0, s, args));
   }
   return gemm(d, down, b + L.hp, m, y, ldy, nullptr, s, accumulate, (float*)(b + L.part), ws_bytes - L.part);
+}
+
+// ---------------------------------------------------------------------------
+// q / k / v of a prompt's rows with RoPE and the KV append
+// ---------------------------------------------------------------------------
+
+// Workspace regions: m > 8, the input's planes (and normalised rows), then
+// q's, k's and v's split-K partials (one plane each when unsplit); m <= 8,
+// the k and v rows, then qmm_matmul_ex's workspace.
+struct QkvWs {
+  size_t xp, xn, q, k, v, mm, total;
+};
+
+static int qkv_check(const qmm_qtensor* wq, const qmm_qtensor* wk, const qmm_qtensor* wv, int64_t m, int heads,
+                     int kv_heads, int head_dim) {
+  if (!wq || !wk || !wv) return fail(QMM_ERR_INVALID, "null weight");
+  if (m < 1) return fail(QMM_ERR_INVALID, "qkv needs m >= 1 (got %lld)", (long long)m);
+  if (qmm_vec_dot_type(wq->dtype) != QMM_Q8K || !same_act(wq, wk) || !same_act(wq, wv))
+    return fail(QMM_ERR_UNSUPPORTED, "qkv needs Q4_K / Q6_K weights of one k");
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads || head_dim < 2 || head_dim > 1024 || head_dim % 2)
+    return fail(QMM_ERR_INVALID, "bad attention geometry");
+  if (wq->n != (int64_t)heads * head_dim || wk->n != (int64_t)kv_heads * head_dim || wv->n != wk->n)
+    return fail(QMM_ERR_INVALID, "qkv weights of %lld / %lld / %lld rows for %d x %d / %d x %d heads",
+                (long long)wq->n, (long long)wk->n, (long long)wv->n, heads, head_dim, kv_heads, head_dim);
+  return QMM_OK;
+}
+
+static QkvWs qkv_ws(Device* d, const qmm_qtensor* wq, const qmm_qtensor* wk, const qmm_qtensor* wv, int64_t m,
+                    bool normalize) {
+  QkvWs w = {};
+  const int64_t H = wq->k;
+  size_t o = 0;
+  if (m > 8) {
+    w.xp = o;
+    o += mmq_planes(wq->dtype, m, H).total;
+    w.xn = o;
+    if (normalize && (size_t)H * 4 > (size_t)d->max_lds) o += align256((size_t)(m * H) * 4);
+    const qmm_qtensor* ws3[3] = {wq, wk, wv};
+    size_t* at[3] = {&w.q, &w.k, &w.v};
+    for (int j = 0; j < 3; ++j) {
+      *at[j] = o;
+      o += align256((size_t)gemm_plan(d, ws3[j], m, false).splits * (size_t)(m * ws3[j]->n) * 4);
+    }
+  } else {
+    w.k = o;
+    o += align256((size_t)(m * wk->n) * 4);
+    w.v = o;
+    o += align256((size_t)(m * wv->n) * 4);
+    w.mm = o;
+    o += std::max(qmm_matmul_ex_workspace_size(wq, m, normalize ? 1 : 0),
+                  std::max(qmm_matmul_ex_workspace_size(wk, m, normalize ? 1 : 0),
+                           qmm_matmul_ex_workspace_size(wv, m, normalize ? 1 : 0)));
+  }
+  w.total = o;
+  return w;
+}
+
+size_t qmm_qkv_rope_kv_append_n_workspace_size(const qmm_qtensor* wq, const qmm_qtensor* wk, const qmm_qtensor* wv,
+                                               int64_t m, int normalize) {
+  if (!wq || !wk || !wv || m < 1) return 0;
+  Device* d;
+  if (current_device(&d) != QMM_OK) return 0;
+  return qkv_ws(d, wq, wk, wv, m, normalize != 0).total;
+}
+
+int qmm_qkv_rope_kv_append_n(const qmm_qtensor* wq, const qmm_qtensor* wk, const qmm_qtensor* wv, const float* x,
+                             int64_t m, int64_t ldx, const float* norm_weight, float eps, const float* cos_t,
+                             const float* sin_t, int64_t first, float* q, int64_t ldq, float* kcache,
+                             float* vcache, int heads, int kv_heads, int head_dim, int max_seq, void* ws,
+                             size_t ws_bytes, void* stream) {
+  QMM_TRY(qkv_check(wq, wk, wv, m, heads, kv_heads, head_dim));
+  if (!x || !q || !cos_t || !sin_t || !kcache || !vcache) return fail(QMM_ERR_INVALID, "null pointer");
+  const int64_t H = wq->k, nq = wq->n, nkv = wk->n;
+  if (ldx < H || ldq < nq) return fail(QMM_ERR_INVALID, "row strides below the row widths");
+  if (max_seq < 1 || first < 0 || first + m > max_seq || m > 65535)
+    return fail(QMM_ERR_INVALID, "positions [%lld, %lld) outside the cache of %d", (long long)first,
+                (long long)(first + m), max_seq);
+  Device* d;
+  QMM_TRY(current_device(&d));
+  hipStream_t s = (hipStream_t)stream;
+  const QkvWs L = qkv_ws(d, wq, wk, wv, m, norm_weight != nullptr);
+  if (!ws || ws_bytes < L.total) return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed", ws_bytes, L.total);
+  uint8_t* b = (uint8_t*)ws;
+  if (m <= 8) {
+    float* k = (float*)(b + L.k);
+    float* v = (float*)(b + L.v);
+    const qmm_qtensor* w3[3] = {wq, wk, wv};
+    float* y3[3] = {q, k, v};
+    const int64_t ld3[3] = {ldq, nkv, nkv};
+    QMM_TRY(qmm_matmul_ex(w3, 3, x, m, ldx, norm_weight, eps, 0, y3, ld3, b + L.mm, ws_bytes - L.mm, stream));
+    return qmm_rope_kv_append_n(q, k, v, ldq, nkv, nkv, cos_t, sin_t, first, m, kcache, vcache, heads, kv_heads,
+                                head_dim, max_seq, stream);
+  }
+  QMM_TRY(input_planes(d, wq->dtype, x, m, H, ldx, norm_weight, eps, b + L.xp, (float*)(b + L.xn), s));
+  const qmm_qtensor* w3[3] = {wq, wk, wv};
+  float* p3[3] = {(float*)(b + L.q), (float*)(b + L.k), (float*)(b + L.v)};
+  int sp[3];
+  for (int j = 0; j < 3; ++j) {
+    const GemmPlan pj = gemm_plan(d, w3[j], m, false);
+    sp[j] = pj.splits;
+    QMM_TRY(gemm_launch(d, w3[j], b + L.xp, m, pj, p3[j], w3[j]->n, nullptr, s, 0, p3[j]));
+  }
+  const float* qp = p3[0];
+  const float* kp = p3[1];
+  const float* vp = p3[2];
+  int mm = (int)m, f = (int)first;
+  long long lq = ldq;
+  void* args[] = {&qp, &sp[0], &kp, &sp[1], &vp, &sp[2], &mm, &q, &lq, &cos_t, &sin_t, &f, &kcache, &vcache,
+                  &heads, &kv_heads, &head_dim, &max_seq};
+  const unsigned threads = (unsigned)((head_dim + 63) / 64 * 64);
+  hipFunction_t fn;
+  QMM_TRY(kernel(d, "qmm_prefill_splitk_rope_kv", &fn));
+  QMM_HIP(hipModuleLaunchKernel(fn, (unsigned)(heads + kv_heads), (unsigned)m, 1, threads, 1, 1, 0, s, args,
+                                nullptr));
+  return QMM_OK;
 }
 
 // ---------------------------------------------------------------------------

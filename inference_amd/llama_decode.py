@@ -343,7 +343,8 @@ class DecodeSession:
         rope_kv, attention, o, gate_up, silu_mul, down); `bufs` holds the pass's row buffers (x, q, k, v,
         att, g, u, h), so a checker can read them between launches. Without a trace the feed-forward
         block is one qmm_ffn call (gate / up split sums, SiLU and the down GEMM's quantization in one
-        launch), which gives the same bits as those three traced launches."""
+        launch), which gives the same bits as those three traced launches; likewise q / k / v with RoPE
+        and the KV append are one qmm_qkv_rope_kv_append_n call."""
         if self.prompt_len == 0 or self.steps_done != 0:
             raise qmm.QmmError(1, "prefill() needs the state reset() leaves")
         cfg, L, w = self.cfg, self.L, self.w
@@ -368,7 +369,9 @@ class DecodeSession:
                 wsb = max(wsb, int(L.qmm_matmul_ex_workspace_size(t.handle, rows, 1)))
             if trace is None:
                 wsb = max(wsb, int(L.qmm_ffn_workspace_size(lw["gate"].handle, lw["up"].handle,
-                                                             lw["down"].handle, rows, 1)))
+                                                             lw["down"].handle, rows, 1)),
+                          int(L.qmm_qkv_rope_kv_append_n_workspace_size(lw["q"].handle, lw["k"].handle,
+                                                                        lw["v"].handle, rows, 1)))
         ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
         vp, i64 = ctypes.c_void_p, ctypes.c_int64
         eps = ctypes.c_float(cfg.eps)
@@ -384,15 +387,21 @@ class DecodeSession:
         tr("embed", -1)
         for li in range(cfg.layers):
             lw = w.layers[li]
-            qmm._check(L.qmm_matmul_ex(self._qkv[li], 3, x.data_ptr(), rows, H, w.attn_norm[li].data_ptr(), eps, 0,
-                                       qkv_y, qkv_ld, ws.data_ptr(), ws.numel(), s))
-            tr("qkv", li)
             kc = self.kcache.data_ptr() + 4 * li * kv_stride
             vc = self.vcache.data_ptr() + 4 * li * kv_stride
-            qmm._check(L.qmm_rope_kv_append_n(q.data_ptr(), k.data_ptr(), v.data_ptr(), nq, nkv, nkv,
-                                              self.cos.data_ptr(), self.sin.data_ptr(), 0, rows, kc, vc, cfg.heads,
-                                              cfg.kv_heads, hd, self.max_seq, s))
-            tr("rope_kv", li)
+            if trace is None:
+                qmm._check(L.qmm_qkv_rope_kv_append_n(lw["q"].handle, lw["k"].handle, lw["v"].handle, x.data_ptr(),
+                                                      rows, H, w.attn_norm[li].data_ptr(), eps, self.cos.data_ptr(),
+                                                      self.sin.data_ptr(), 0, q.data_ptr(), nq, kc, vc, cfg.heads,
+                                                      cfg.kv_heads, hd, self.max_seq, ws.data_ptr(), ws.numel(), s))
+            else:
+                qmm._check(L.qmm_matmul_ex(self._qkv[li], 3, x.data_ptr(), rows, H, w.attn_norm[li].data_ptr(), eps,
+                                           0, qkv_y, qkv_ld, ws.data_ptr(), ws.numel(), s))
+                tr("qkv", li)
+                qmm._check(L.qmm_rope_kv_append_n(q.data_ptr(), k.data_ptr(), v.data_ptr(), nq, nkv, nkv,
+                                                  self.cos.data_ptr(), self.sin.data_ptr(), 0, rows, kc, vc,
+                                                  cfg.heads, cfg.kv_heads, hd, self.max_seq, s))
+                tr("rope_kv", li)
             qmm._check(L.qmm_prefill_attention(q.data_ptr(), nq, kc, vc, 0, rows, att.data_ptr(), nq, cfg.heads,
                                                cfg.kv_heads, hd, self.max_seq, ctypes.c_float(self.scale), s))
             tr("attention", li)

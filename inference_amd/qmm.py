@@ -49,7 +49,8 @@ EXPORTS = (
     "qmm_quantize_rows", "qmm_matmul_workspace_size", "qmm_matmul", "qmm_matmul_q",
     "qmm_matmul_multi", "qmm_block_dots", "qmm_moe_route", "qmm_moe_gemv", "qmm_moe_gemm_workspace_size", "qmm_moe_gemm",
     "qmm_moe_ffn_workspace_size",
-    "qmm_moe_ffn", "qmm_matmul_ex", "qmm_matmul_ex_workspace_size", "qmm_ffn", "qmm_ffn_workspace_size", "qmm_rms_norm", "qmm_embed_rows",
+    "qmm_moe_ffn", "qmm_matmul_ex", "qmm_matmul_ex_workspace_size", "qmm_ffn", "qmm_ffn_workspace_size",
+    "qmm_qkv_rope_kv_append_n", "qmm_qkv_rope_kv_append_n_workspace_size", "qmm_rms_norm", "qmm_embed_rows",
     "qmm_rope_kv_append", "qmm_decode_attention", "qmm_silu_mul_quantize", "qmm_greedy_advance",
     "qmm_matmul_q_ex", "qmm_decode_attention_workspace_size", "qmm_decode_rope_attention",
     "qmm_greedy_workspace_size", "qmm_matmul_multi_q", "qmm_silu_mul_matmul",
@@ -111,6 +112,9 @@ def lib() -> ctypes.CDLL:
             "qmm_matmul_ex_workspace_size": ([vp, i64, i32], sz),
             "qmm_ffn": ([vp, vp, vp, vp, i64, i64, vp, ctypes.c_float, i32, vp, i64, vp, sz, vp], i32),
             "qmm_ffn_workspace_size": ([vp, vp, vp, i64, i32], sz),
+            "qmm_qkv_rope_kv_append_n": ([vp, vp, vp, vp, i64, i64, vp, ctypes.c_float, vp, vp, i64, vp, i64, vp, vp,
+                                          i32, i32, i32, i32, vp, sz, vp], i32),
+            "qmm_qkv_rope_kv_append_n_workspace_size": ([vp, vp, vp, i64, i32], sz),
             "qmm_rms_norm": ([vp, i64, i64, i64, vp, ctypes.c_float, vp, i64, vp], i32),
             "qmm_embed_rows": ([vp, i64, i64, vp, vp, vp, i64, vp], i32),
             "qmm_rope_kv_append": ([vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp], i32),

@@ -1,4 +1,6 @@
-"""qmm_ffn (the gated feed-forward block of m rows) against the launches it replaces and the CPU oracle.
+"""The prefill's fused entry points against the launches they replace (and qmm_ffn against the CPU oracle):
+qmm_ffn, the gated feed-forward block of m rows, and qmm_qkv_rope_kv_append_n, q / k / v with RoPE and the
+KV append.
 
 At m > 8 the entry point sums the gate / up GEMMs' split-K partials inside its SiLU launch, in the
 order qmm_splitk_sum uses, so its output must equal qmm_matmul_ex (gate, up) -> qmm_silu_mul ->
@@ -12,6 +14,7 @@ import pytest
 import torch
 
 from inference_amd import GgmlDType, QTensor, qmm
+from inference_amd.llama_decode import LlamaConfig, rope_tables
 from oracle import llama as ol
 from oracle import oracle as orc
 
@@ -126,3 +129,66 @@ def test_ffn_rejects_bad_shapes_and_formats():
     with pytest.raises(qmm.QmmError, match="workspace"):
         qmm._check(L().qmm_ffn(gate.handle, up.handle, down.handle, x.data_ptr(), 16, 512, None,
                                ctypes.c_float(1e-5), 0, x.data_ptr(), 512, ws.data_ptr(), need - 1, S()))
+
+
+@pytest.mark.parametrize("m,first", [(127, 0), (64, 5), (9, 0), (8, 0), (3, 7)])
+def test_qkv_rope_equals_the_launches_it_replaces(m, first):
+    """The 8B attention projections (q 4096x4096 and k 1024x4096 Q4_K, v 1024x4096 Q6_K; 32 / 8 heads of
+    128) on the GEMM path (127, 64, 9 rows: q, k and v split over K) and the GEMV path (8, 3): rotated q
+    and both caches equal qmm_matmul_ex followed by qmm_rope_kv_append_n bit for bit."""
+    H, heads, kvh, hd, max_seq = 4096, 32, 8, 128, 256
+    g = torch.Generator(device=DEV).manual_seed(11)
+    wq = QTensor.quantize(torch.randn((heads * hd, H), generator=g, device=DEV) * 0.02, GgmlDType.Q4K)
+    wk = QTensor.quantize(torch.randn((kvh * hd, H), generator=g, device=DEV) * 0.02, GgmlDType.Q4K)
+    wv = QTensor.quantize(torch.randn((kvh * hd, H), generator=g, device=DEV) * 0.02, GgmlDType.Q6K)
+    cos, sin = (t(a) for a in rope_tables(LlamaConfig.llama3_8b(), max_seq))
+    rng = np.random.default_rng(200 + m)
+    x = t(rng.standard_normal((m, H)).astype(np.float32))
+    nw = t(rng.uniform(0.5, 1.5, H).astype(np.float32))
+    eps = ctypes.c_float(1e-5)
+    nq, nkv = heads * hd, kvh * hd
+    caches = [torch.full((kvh, max_seq, hd), 7.0, device=DEV) for _ in range(4)]
+    q1 = torch.zeros((m, nq), device=DEV)
+    wsb = int(L().qmm_qkv_rope_kv_append_n_workspace_size(wq.handle, wk.handle, wv.handle, m, 1))
+    assert wsb > 0
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    qmm._check(L().qmm_qkv_rope_kv_append_n(wq.handle, wk.handle, wv.handle, x.data_ptr(), m, H, nw.data_ptr(), eps,
+                                            cos.data_ptr(), sin.data_ptr(), first, q1.data_ptr(), nq,
+                                            caches[0].data_ptr(), caches[1].data_ptr(), heads, kvh, hd, max_seq,
+                                            ws.data_ptr(), ws.numel(), S()))
+    q2 = torch.zeros((m, nq), device=DEV)
+    k2 = torch.zeros((m, nkv), device=DEV)
+    v2 = torch.zeros((m, nkv), device=DEV)
+    wsb2 = max(int(L().qmm_matmul_ex_workspace_size(w.handle, m, 1)) for w in (wq, wk, wv))
+    ws2 = torch.empty(wsb2, dtype=torch.uint8, device=DEV)
+    qmm._check(L().qmm_matmul_ex((vp * 3)(wq.handle.value, wk.handle.value, wv.handle.value), 3, x.data_ptr(), m, H,
+                                 nw.data_ptr(), eps, 0, (vp * 3)(q2.data_ptr(), k2.data_ptr(), v2.data_ptr()),
+                                 (i64 * 3)(nq, nkv, nkv), ws2.data_ptr(), ws2.numel(), S()))
+    qmm._check(L().qmm_rope_kv_append_n(q2.data_ptr(), k2.data_ptr(), v2.data_ptr(), nq, nkv, nkv, cos.data_ptr(),
+                                        sin.data_ptr(), first, m, caches[2].data_ptr(), caches[3].data_ptr(), heads,
+                                        kvh, hd, max_seq, S()))
+    assert torch.equal(q1, q2)
+    assert torch.equal(caches[0], caches[2]) and torch.equal(caches[1], caches[3])
+    # the positions outside [first, first + m) are untouched
+    assert bool((caches[0][:, :first] == 7.0).all()) and bool((caches[0][:, first + m:] == 7.0).all())
+
+
+def test_qkv_rope_rejects_bad_arguments():
+    g = torch.Generator(device=DEV).manual_seed(12)
+    wq = QTensor.quantize(torch.randn((256, 512), generator=g, device=DEV) * 0.02, GgmlDType.Q4K)
+    wk = QTensor.quantize(torch.randn((128, 512), generator=g, device=DEV) * 0.02, GgmlDType.Q4K)
+    x = torch.zeros((16, 512), device=DEV)
+    cs = torch.zeros((32, 64), device=DEV)
+    kc = torch.zeros((2, 32, 64), device=DEV)
+    ws = torch.empty(1 << 22, dtype=torch.uint8, device=DEV)
+
+    def call(heads, kvh, first, m=16, wv=wk):
+        return L().qmm_qkv_rope_kv_append_n(wq.handle, wk.handle, wv.handle, x.data_ptr(), m, 512, None,
+                                            ctypes.c_float(1e-5), cs.data_ptr(), cs.data_ptr(), first, x.data_ptr(),
+                                            512, kc.data_ptr(), kc.data_ptr(), heads, kvh, 64, 32, ws.data_ptr(),
+                                            ws.numel(), S())
+    assert call(3, 2, 0) != 0     # heads % kv_heads
+    assert call(4, 1, 0) != 0     # wk rows != kv_heads * head_dim
+    assert call(4, 2, 20) != 0    # positions past max_seq
+    wv8 = QTensor.quantize(torch.zeros((128, 512), device=DEV), GgmlDType.Q8_0)
+    assert call(4, 2, 0, wv=wv8) != 0  # Q8_0 weight
