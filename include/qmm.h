@@ -66,6 +66,12 @@ const char *qmm_last_error(void);
  * lazily for the current device). */
 int qmm_init(int device);
 
+/* Re-read the QMM_* tuning overrides from the environment (kernel and launch
+ * shape choices for sweeps and tests). They are read once, at the first call,
+ * and then only here: a launch never consults the environment. No counterpart
+ * in the reference (its launchers take no overrides). */
+void qmm_reload_tuning(void);
+
 /* GGML geometry: elements per block, bytes per block, and the activation type a
  * weight type multiplies against (Q8_0 -> Q8_0, Q4K/Q6K -> Q8K). -1 if unknown.
  * (GgmlDType::block_size / type_size / vec_dot_type.) */
@@ -132,8 +138,7 @@ int qmm_matmul(const qmm_qtensor *w, const float *x, int64_t m, int64_t ldx, flo
 
 /* qmm_matmul without a caller workspace, for callers that cannot allocate
  * (code under stream capture, tight serving loops, harnesses that forbid
- * hipMalloc). No counterpart in the reference: its launchers take caller
- * buffers or allocate their own (moe_gguf.cu:172-174). The workspace is a
+ * hipMalloc). No counterpart in the reference. The workspace is a
  * library-held device array of QMM_NOALLOC_SCRATCH_BYTES per GPU, resolved at
  * set-up (qmm_init(device), else the first call on a device); the call itself
  * allocates nothing. Calls whose qmm_matmul_workspace_size(w, m) exceeds it
@@ -360,6 +365,13 @@ int qmm_greedy_advance(const float *logits, int64_t n, int32_t *tokens, int64_t 
 int qmm_moe_route(const float *logits, int64_t tokens, int experts, int topk, int renormalize,
                   int32_t *counts, int32_t *offsets, int32_t *pair_token, float *pair_weight,
                   int32_t *token_pairs, void *stream);
+/* qmm_moe_route with MoeMlp::forward's other weight branch (llama.rs:1436-1447):
+ * renormalize (norm_topk_prob) gives p / sum over the selection; otherwise each
+ * weight is p * routed_scaling_factor (DeepSeek's routed_scaling_factor; 1.0
+ * for Qwen2-MoE). qmm_moe_route is this with routed_scaling_factor = 1. */
+int qmm_moe_route_ex(const float *logits, int64_t tokens, int experts, int topk, int renormalize,
+                     float routed_scaling_factor, int32_t *counts, int32_t *offsets, int32_t *pair_token,
+                     float *pair_weight, int32_t *token_pairs, void *stream);
 
 /* Expert-grouped GEMV (replaces moe_gemm_gguf, ffi.rs:25-39): w[j] (count 1..2)
  * are stacked expert weights [experts*N, K] of one dtype; xq holds `pairs`
@@ -400,6 +412,28 @@ size_t qmm_moe_ffn_workspace_size(const qmm_qtensor *gate, const qmm_qtensor *do
 int qmm_moe_ffn(const float *x, int64_t tokens, int64_t ldx, const float *logits, int experts, int topk,
                 const qmm_qtensor *gate, const qmm_qtensor *up, const qmm_qtensor *down, float *out,
                 int64_t ldo, void *ws, size_t ws_bytes, void *stream);
+
+/* The whole of MoeMlp::forward (models/llama.rs:1416-1487), of which
+ * qmm_moe_ffn is the Mixtral case (norm_topk_prob, no shared expert):
+ *   * routed weights as qmm_moe_route_ex (norm_topk_prob != 0: renormalised;
+ *     else times routed_scaling_factor);
+ *   * an optional always-on shared expert (shared_gate / shared_up /
+ *     shared_down: a dense-row gated MLP, [Fs, hidden] / [Fs, hidden] /
+ *     [hidden, Fs], as qmm_ffn runs it over every token), added after the
+ *     routed sum; with shared_gate_weight (f32 [hidden] on the device) it is
+ *     first scaled per token by sigmoid(x . shared_gate_weight) (Qwen2-MoE),
+ *     without it added ungated (DeepSeek-V2). All three shared weights NULL: no
+ *     shared expert.
+ * ws: qmm_moe_ffn_ex_workspace_size(...) bytes with the same shared weights. */
+size_t qmm_moe_ffn_ex_workspace_size(const qmm_qtensor *gate, const qmm_qtensor *down, int64_t tokens,
+                                     int experts, int topk, const qmm_qtensor *shared_gate,
+                                     const qmm_qtensor *shared_up, const qmm_qtensor *shared_down);
+int qmm_moe_ffn_ex(const float *x, int64_t tokens, int64_t ldx, const float *logits, int experts, int topk,
+                   int norm_topk_prob, float routed_scaling_factor, const qmm_qtensor *gate,
+                   const qmm_qtensor *up, const qmm_qtensor *down, const qmm_qtensor *shared_gate,
+                   const qmm_qtensor *shared_up, const qmm_qtensor *shared_down,
+                   const float *shared_gate_weight, float *out, int64_t ldo, void *ws, size_t ws_bytes,
+                   void *stream);
 
 /* ---------------------------------------------------------------------------
  * GGUF files (llama.cpp's single-file model container, spec v2/v3).

@@ -54,6 +54,10 @@ extern "C" {
     /// lazily for the current device).
     pub fn qmm_init(device: c_int) -> c_int;
 
+    /// Re-read the QMM_* tuning overrides from the environment (read once, at the first call,
+    /// and then only here).
+    pub fn qmm_reload_tuning();
+
     /// GGML geometry: elements per block, bytes per block, and the activation type a
     /// weight type multiplies against (Q8_0 -> Q8_0, Q4K/Q6K -> Q8K). -1 if unknown.
     /// (GgmlDType::block_size / type_size / vec_dot_type.)
@@ -387,6 +391,13 @@ extern "C" {
         stream: *mut c_void
     ) -> c_int;
 
+    /// `qmm_moe_route` with the routed scaling factor (applied when `renormalize` is 0).
+    pub fn qmm_moe_route_ex(
+        logits: *const f32, tokens: i64, experts: c_int, topk: c_int, renormalize: c_int,
+        routed_scaling_factor: f32, counts: *mut i32, offsets: *mut i32, pair_token: *mut i32,
+        pair_weight: *mut f32, token_pairs: *mut i32, stream: *mut c_void
+    ) -> c_int;
+
     /// Expert-grouped GEMV (replaces moe_gemm_gguf, ffi.rs:25-39): w[j] (count 1..2)
     /// are stacked expert weights [experts*N, K] of one dtype; xq holds `pairs`
     /// rows of vec-dot blocks grouped by expert (counts/offsets as produced by
@@ -433,6 +444,21 @@ extern "C" {
     pub fn qmm_moe_ffn(
         x: *const f32, tokens: i64, ldx: i64, logits: *const f32, experts: c_int, topk: c_int,
         gate: *const QmmQTensor, up: *const QmmQTensor, down: *const QmmQTensor, out: *mut f32, ldo: i64,
+        ws: *mut c_void, ws_bytes: usize, stream: *mut c_void
+    ) -> c_int;
+
+    /// The whole `MoeMlp::forward`: routed weights renormalised or scaled, and an optional shared
+    /// expert (all three weights null: none), gated by sigmoid(x . shared_gate_weight) when that is given.
+    pub fn qmm_moe_ffn_ex_workspace_size(
+        gate: *const QmmQTensor, down: *const QmmQTensor, tokens: i64, experts: c_int, topk: c_int,
+        shared_gate: *const QmmQTensor, shared_up: *const QmmQTensor, shared_down: *const QmmQTensor
+    ) -> usize;
+
+    pub fn qmm_moe_ffn_ex(
+        x: *const f32, tokens: i64, ldx: i64, logits: *const f32, experts: c_int, topk: c_int,
+        norm_topk_prob: c_int, routed_scaling_factor: f32, gate: *const QmmQTensor, up: *const QmmQTensor,
+        down: *const QmmQTensor, shared_gate: *const QmmQTensor, shared_up: *const QmmQTensor,
+        shared_down: *const QmmQTensor, shared_gate_weight: *const f32, out: *mut f32, ldo: i64,
         ws: *mut c_void, ws_bytes: usize, stream: *mut c_void
     ) -> c_int;
 
@@ -556,8 +582,25 @@ pub struct QTensor {
 unsafe impl Send for QTensor {}
 
 impl QTensor {
-    /// `QStorage::from_data` of GGML block bytes held on the host.
+    /// `QStorage::from_data` of GGML block bytes held on the host. `bytes` must hold exactly the
+    /// tensor's n * (k / block) blocks: the C side copies that many bytes from it, so a slice of any
+    /// other length is refused here (QMM_ERR_INVALID) before the call.
     pub fn from_ggml(dtype: c_int, n: i64, k: i64, bytes: &[u8], stream: *mut c_void) -> Result<Self, QmmError> {
+        let invalid = |what: &str| QmmError { status: QMM_ERR_INVALID, message: what.to_string() };
+        let (bs, ts) = unsafe { (qmm_block_size(dtype), qmm_type_size(dtype)) };
+        if bs <= 0 || ts <= 0 {
+            return Err(invalid("unsupported dtype"));
+        }
+        if n <= 0 || k <= 0 || k % bs as i64 != 0 {
+            return Err(invalid("shape is empty or k is not a whole number of blocks"));
+        }
+        let want = (n as u64)
+            .checked_mul((k / bs as i64) as u64)
+            .and_then(|blocks| blocks.checked_mul(ts as u64))
+            .ok_or_else(|| invalid("tensor byte count overflows"))?;
+        if bytes.len() as u64 != want {
+            return Err(invalid("byte slice length differs from the tensor's GGML byte count"));
+        }
         let mut raw = std::ptr::null_mut();
         check(unsafe {
             qmm_qtensor_from_ggml(dtype, n, k, bytes.as_ptr() as *const c_void, 0, stream, &mut raw)

@@ -327,17 +327,27 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
   // 0): all B x GT scores first (16-lane row sums), then one online-softmax
   // update per head. A row with no position yet keeps m = -inf, and the
   // guards keep -inf - (-inf) out of exp.
+  // A masked slot (a clamped duplicate past the row's positions) may hold a
+  // cache row that is not written yet (the chunk owning p reads row p before
+  // this launch appends it): its score is -inf and its value row is replaced
+  // by zeros, so nothing stale (even a NaN) reaches the sums.
   auto scan = [&](const float (&kb)[B][R], const float (&vb)[B][R], int i0) {
     float sc[B][GT];
+    float ks[B][R], vs[B][R];
 #pragma unroll
     for (int b = 0; b < B; ++b) {
       const bool ok = i0 + b < npos;
       const bool at_p = rope && j0 + row + NR * (i0 + b) == p;
 #pragma unroll
+      for (int e = 0; e < R; ++e) {
+        ks[b][e] = at_p ? kn[e] : kb[b][e];
+        vs[b][e] = ok ? (at_p ? vn[e] : vb[b][e]) : 0.0f;
+      }
+#pragma unroll
       for (int h = 0; h < GT; ++h) {
         float d = 0.0f;
 #pragma unroll
-        for (int e = 0; e < R; ++e) d += qv[h][e] * (at_p ? kn[e] : kb[b][e]);
+        for (int e = 0; e < R; ++e) d += qv[h][e] * ks[b][e];
         d = row16_total(d) * scale;
         sc[b][h] = ok ? d : -INFINITY;
       }
@@ -354,11 +364,10 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
       for (int e = 0; e < R; ++e) acc[e] = o[h][e] * a;
 #pragma unroll
       for (int b = 0; b < B; ++b) {
-        const bool at_p = rope && j0 + row + NR * (i0 + b) == p;
         const float w = sc[b][h] == -INFINITY ? 0.0f : expf(sc[b][h] - mx);
         ls += w;
 #pragma unroll
-        for (int e = 0; e < R; ++e) acc[e] += w * (at_p ? vn[e] : vb[b][e]);
+        for (int e = 0; e < R; ++e) acc[e] += w * vs[b][e];
       }
       m[h] = mx;
       l[h] = ls;

@@ -13,9 +13,9 @@
 #include <cstdlib>
 #include <cstring>
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <string>
-#include <unordered_map>
 
 extern "C" const unsigned char qmm_code_object_start[];
 extern "C" const unsigned char qmm_code_object_end[];
@@ -66,40 +66,105 @@ int fmt_of(int dtype) {
 
 const char* fmt_name(int fmt) { return fmt == kFmtQ80 ? "q8_0" : fmt == kFmtQ4K ? "q4k" : "q6k"; }
 
+// Kernel handles of one device: an insert-only open-addressing table read
+// without a lock (a launch hashes its name and probes; only a miss, the first
+// launch of a kernel on the device, takes the mutex and asks the runtime).
+struct KernelEntry {
+  uint64_t hash;
+  std::string name;
+  hipFunction_t fn;
+};
+constexpr int kKernelSlots = 8192;  // > 4x the kernels of the code object
+
 struct Device {
   hipModule_t module = nullptr;
-  std::unordered_map<std::string, hipFunction_t> fns;
+  std::atomic<const KernelEntry*> slots[kKernelSlots];
   int max_lds = 0;
   int num_cu = 0;
+  Device() {
+    for (auto& e : slots) e.store(nullptr, std::memory_order_relaxed);
+  }
 };
 
 std::mutex g_mu;
-Device* g_dev[64] = {};
+std::atomic<Device*> g_dev[64] = {};
 
-// Launch-shape overrides for tuning sweeps, read at every launch:
-// QMM_GEMV_CFG="W,R,U" (waves per workgroup, rows per wave, load iterations per
-// batch), QMM_GEMV_WAVES_PER_CU (resident waves the grid is sized for) and
-// QMM_GEMV1=0 (use the general kernel for one activation row too).
+// Launch-shape and kernel-choice overrides for tuning sweeps and tests: the
+// QMM_* variables below are read into a snapshot at the first launch and again
+// at every qmm_reload_tuning(), never per launch.
+//   QMM_GEMV_CFG="W,R,U" (waves per workgroup, rows per wave, load iterations
+//   per batch), QMM_GEMV_WAVES_PER_CU (resident waves the grid is sized for),
+//   QMM_GEMV1=0 (the general kernel for one activation row too), QMM_GEMV1P=<P>
+//   (the prefetch ring's depth; 0 never), and the GEMM / MoE choices named
+//   where they are used.
+enum EnvKey {
+  kEnvGemv1, kEnvGemv1p, kEnvGemvCfg, kEnvGemvWavesPerCu, kEnvGemvRows, kEnvSplitK, kEnvMmq2, kEnvMmq,
+  kEnvMmq4Bn, kEnvMmq1, kEnvMmqXcd, kEnvMoeGemv, kEnvMoeMmq, kEnvMoeBm, kEnvMoeSplitK, kEnvMoeGrouped, kEnvCount
+};
+const char* const kEnvNames[kEnvCount] = {
+    "QMM_GEMV1", "QMM_GEMV1P", "QMM_GEMV_CFG", "QMM_GEMV_WAVES_PER_CU", "QMM_GEMV_ROWS", "QMM_SPLITK",
+    "QMM_MMQ2", "QMM_MMQ", "QMM_MMQ4_BN", "QMM_MMQ1", "QMM_MMQ_XCD", "QMM_MOE_GEMV", "QMM_MOE_MMQ",
+    "QMM_MOE_BM", "QMM_MOE_SPLITK", "QMM_MOE_GROUPED"};
+
 struct Tuning {
   int w = 0, r = 0, u = 0, waves_per_cu = 0, gemv1 = 1, gemv1p = -1;
 };
-Tuning tuning() {
-  Tuning t;
-  if (const char* s = getenv("QMM_GEMV1")) t.gemv1 = atoi(s);
-  if (const char* s = getenv("QMM_GEMV1P")) t.gemv1p = atoi(s);
-  if (const char* s = getenv("QMM_GEMV_CFG")) {
-    if (sscanf(s, "%d,%d,%d", &t.w, &t.r, &t.u) != 3) t.w = t.r = t.u = 0;
+
+struct EnvSnapshot {
+  bool set[kEnvCount];
+  char val[kEnvCount][48];
+  Tuning tu;
+};
+
+std::mutex g_env_mu;
+std::atomic<const EnvSnapshot*> g_env{nullptr};
+
+const EnvSnapshot* env_read() {
+  EnvSnapshot* e = new EnvSnapshot();
+  for (int k = 0; k < kEnvCount; ++k) {
+    const char* v = getenv(kEnvNames[k]);
+    e->set[k] = v != nullptr;
+    snprintf(e->val[k], sizeof(e->val[k]), "%s", v ? v : "");
   }
-  if (const char* s = getenv("QMM_GEMV_WAVES_PER_CU")) t.waves_per_cu = atoi(s);
-  return t;
+  Tuning& t = e->tu;
+  if (e->set[kEnvGemv1]) t.gemv1 = atoi(e->val[kEnvGemv1]);
+  if (e->set[kEnvGemv1p]) t.gemv1p = atoi(e->val[kEnvGemv1p]);
+  if (e->set[kEnvGemvCfg] && sscanf(e->val[kEnvGemvCfg], "%d,%d,%d", &t.w, &t.r, &t.u) != 3) t.w = t.r = t.u = 0;
+  if (e->set[kEnvGemvWavesPerCu]) t.waves_per_cu = atoi(e->val[kEnvGemvWavesPerCu]);
+  return e;
 }
+
+const EnvSnapshot* env_snapshot() {
+  const EnvSnapshot* e = g_env.load(std::memory_order_acquire);
+  if (e) return e;
+  std::lock_guard<std::mutex> lk(g_env_mu);
+  e = g_env.load(std::memory_order_acquire);
+  if (!e) {
+    e = env_read();
+    g_env.store(e, std::memory_order_release);
+  }
+  return e;
+}
+
+// The override's value, or nullptr when it is not set.
+const char* env(EnvKey k) {
+  const EnvSnapshot* e = env_snapshot();
+  return e->set[k] ? e->val[k] : nullptr;
+}
+
+const Tuning& tuning() { return env_snapshot()->tu; }
 
 int current_device(Device** out) {
   int dev = 0;
   QMM_HIP(hipGetDevice(&dev));
   if (dev < 0 || dev >= 64) return fail(QMM_ERR_INVALID, "device ordinal %d out of range", dev);
+  Device* have = g_dev[dev].load(std::memory_order_acquire);
+  if (have) {
+    *out = have;
+    return QMM_OK;
+  }
   std::lock_guard<std::mutex> lk(g_mu);
-  if (!g_dev[dev]) {
+  if (!g_dev[dev].load(std::memory_order_acquire)) {
     Device* d = new Device();
     hipError_t e = hipModuleLoadData(&d->module, qmm_code_object_start);
     if (e != hipSuccess) {
@@ -114,35 +179,54 @@ int current_device(Device** out) {
       delete d;
       return fail(QMM_ERR_HIP, "hipDeviceGetAttribute: %s", hipGetErrorString(e));
     }
-    g_dev[dev] = d;
+    g_dev[dev].store(d, std::memory_order_release);
   }
-  *out = g_dev[dev];
+  *out = g_dev[dev].load(std::memory_order_acquire);
   return QMM_OK;
 }
 
-int kernel(Device* d, const std::string& name, hipFunction_t* f) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  auto it = d->fns.find(name);
-  if (it != d->fns.end()) {
-    *f = it->second;
-    return QMM_OK;
+uint64_t name_hash(const char* s) {  // FNV-1a
+  uint64_t h = 1469598103934665603ull;
+  for (; *s; ++s) h = (h ^ (unsigned char)*s) * 1099511628211ull;
+  return h;
+}
+
+int kernel(Device* d, const char* name, hipFunction_t* f) {
+  const uint64_t h = name_hash(name);
+  const unsigned start = (unsigned)(h % kKernelSlots);
+  for (unsigned i = 0; i < kKernelSlots; ++i) {
+    const KernelEntry* e = d->slots[(start + i) % kKernelSlots].load(std::memory_order_acquire);
+    if (!e) break;
+    if (e->hash == h && e->name == name) {
+      *f = e->fn;
+      return QMM_OK;
+    }
   }
+  std::lock_guard<std::mutex> lk(g_mu);
+  unsigned i = 0;
+  for (; i < kKernelSlots; ++i) {  // again under the lock: another thread may have added it
+    const KernelEntry* e = d->slots[(start + i) % kKernelSlots].load(std::memory_order_acquire);
+    if (!e) break;
+    if (e->hash == h && e->name == name) {
+      *f = e->fn;
+      return QMM_OK;
+    }
+  }
+  if (i == kKernelSlots) return fail(QMM_ERR_NO_KERNEL, "kernel table full looking up %s", name);
   hipFunction_t fn = nullptr;
-  hipError_t e = hipModuleGetFunction(&fn, d->module, name.c_str());
-  if (e != hipSuccess || !fn) {
+  hipError_t err = hipModuleGetFunction(&fn, d->module, name);
+  if (err != hipSuccess || !fn) {
     // The failed lookup also sets the runtime's last error; clear it so the
     // caller's next unrelated HIP call (e.g. a graph capture) does not report it.
     (void)hipGetLastError();
-    return fail(QMM_ERR_NO_KERNEL, "kernel %s missing from the code object: %s", name.c_str(),
-                hipGetErrorString(e));
+    return fail(QMM_ERR_NO_KERNEL, "kernel %s missing from the code object: %s", name, hipGetErrorString(err));
   }
-  d->fns.emplace(name, fn);
+  d->slots[(start + i) % kKernelSlots].store(new KernelEntry{h, name, fn}, std::memory_order_release);
   *f = fn;
   return QMM_OK;
 }
 
-int launch(Device* d, const std::string& name, unsigned grid, unsigned block, unsigned lds,
-           hipStream_t s, void** args) {
+int launch(Device* d, const char* name, unsigned grid, unsigned block, unsigned lds, hipStream_t s, void** args) {
   hipFunction_t f;
   QMM_TRY(kernel(d, name, &f));
   if (grid == 0) return QMM_OK;
@@ -165,6 +249,13 @@ struct qmm_qtensor {
 extern "C" {
 
 const char* qmm_last_error(void) { return g_err.c_str(); }
+
+void qmm_reload_tuning(void) {
+  const EnvSnapshot* e = env_read();
+  std::lock_guard<std::mutex> lk(g_env_mu);
+  // the previous snapshot stays allocated: a launch on another thread may still read it
+  g_env.store(e, std::memory_order_release);
+}
 
 // qmm_noalloc.hip: resolves the allocation-free entry point's device scratch
 // on the current device (set-up, once per device).
@@ -552,7 +643,7 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   // weights under 2048 rows take it from m = 7. QMM_GEMV_ROWS=<m> takes it
   // from m rows at every size (0: never).
   int rows_from = w->n >= 2048 ? 2 : 7;
-  if (const char* e = getenv("QMM_GEMV_ROWS")) rows_from = atoi(e);
+  if (const char* e = env(kEnvGemvRows)) rows_from = atoi(e);
   const unsigned long long rbody = fmt == kFmtQ4K ? 144 : 208;  // device block bodies (Q6_K's f16 d kept apart)
   if (count == 1 && !fused && !silu && dump == nullptr && rows_from > 0 && m >= rows_from && m <= 8 &&
       fmt != kFmtQ80 && nb <= 64 && (unsigned long long)w->n * nb * rbody < (1ull << 32)) {
@@ -599,7 +690,7 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
     }
   }
   int waves_per_cu = !fused && m > 1 ? 20 : 16;  // m > 1: the earlier sweep's optimum
-  const Tuning tu = tuning();
+  const Tuning& tu = tuning();
   if (tu.w > 0 && tu.r > 0 && tu.u > 0) { wv = tu.w; r = tu.r; u = tu.u; }
   if (tu.waves_per_cu > 0) waves_per_cu = tu.waves_per_cu;
   // more than four weights: the eight-job kernels (M = 1; r = u = 1 shapes)
@@ -709,7 +800,7 @@ static constexpr int kMmqBMRows = 64;             // and its M tile
 static void plan_splits(const Device* d, GemmPlan& p, int nbk) {
   const long long tiles = (long long)p.gx * p.gy;
   int sp = 1;
-  if (const char* e = getenv("QMM_SPLITK")) {
+  if (const char* e = env(kEnvSplitK)) {
     sp = atoi(e);
   } else if (tiles * 2 <= d->num_cu) {
     const unsigned lds = p.lds ? p.lds : kMmqStaticLds;
@@ -738,7 +829,7 @@ static GemmPlan gemm_plan(const Device* d, const qmm_qtensor* w, int64_t m, bool
   // threads per CU, double-buffered LDS of 2 x 58 KB). QMM_MMQ2="BM,BN" picks
   // 64-row tiles instead.
   int bm = 128, bn = 128;
-  if (const char* e = getenv("QMM_MMQ2")) {
+  if (const char* e = env(kEnvMmq2)) {
     int a = 0, b = 0;
     if (sscanf(e, "%d,%d", &a, &b) == 2 && (a == 64 || a == 128) && (b == 64 || b == 128) && !(a == 128 && b == 64)) {
       bm = a;
@@ -752,7 +843,7 @@ static GemmPlan gemm_plan(const Device* d, const qmm_qtensor* w, int64_t m, bool
   // M = 127) the split-scale mmq4 with 128x64 tiles (4 waves, one per SIMD),
   // twice the workgroups (14336x4096 at M = 127: 41 vs 52 us).
   // QMM_MMQ=2 / QMM_MMQ=4 force one; QMM_MMQ4_BN=128 picks 128x128 mmq4 tiles.
-  const char* gen = getenv("QMM_MMQ");
+  const char* gen = env(kEnvMmq);
   const long long tiles2 = (long long)((N + bn - 1) / bn) * ((M + bm - 1) / bm);
   const bool use4 = gen ? atoi(gen) == 4 : tiles2 * 2 < d->num_cu;
   // Q4_K default: mmqs (split-scale d term on int8 MFMA, mins term on bf16
@@ -767,13 +858,13 @@ static GemmPlan gemm_plan(const Device* d, const qmm_qtensor* w, int64_t m, bool
     p.lds = ldss;
   } else if (fmt == kFmtQ4K && use4) {
     int b4 = 64;
-    if (const char* e = getenv("QMM_MMQ4_BN")) b4 = atoi(e) == 128 ? 128 : 64;
+    if (const char* e = env(kEnvMmq4Bn)) b4 = atoi(e) == 128 ? 128 : 64;
     snprintf(p.name, sizeof(p.name), "qmm_mmq4_q4k_n%d%s", b4, dump ? "_dump" : "");
     p.gx = (unsigned)((N + b4 - 1) / b4);
     p.gy = (unsigned)((M + 127) / 128);
     p.threads = 256;
     p.lds = (unsigned)(2 * (128 * 272 + b4 * 144 + 128 * 4 + 128 * 16));
-  } else if (fmt == kFmtQ4K && (int)lds2 <= d->max_lds && getenv("QMM_MMQ1") == nullptr) {
+  } else if (fmt == kFmtQ4K && (int)lds2 <= d->max_lds && env(kEnvMmq1) == nullptr) {
     snprintf(p.name, sizeof(p.name), "qmm_mmq2_q4k_m%d_n%d%s", bm, bn, dump ? "_dump" : "");
     p.gx = (unsigned)((N + bn - 1) / bn);
     p.gy = (unsigned)((M + bm - 1) / bm);
@@ -816,7 +907,7 @@ static int gemm_launch(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64
   // XCD-aware tile order (QMM_MMQ_XCD=0: plain blockIdx order); split
   // launches keep the plain order
   int remap = split ? 0 : 1;
-  if (const char* e = getenv("QMM_MMQ_XCD")) remap = remap && atoi(e) != 0;
+  if (const char* e = env(kEnvMmqXcd)) remap = remap && atoi(e) != 0;
   int kc = p.kc;
   long long ysplit = split ? (long long)M * N : 0;
   void* args[] = {&wq, &q8, &dd, &ss, &yy, &M, &N, &K, &ld, &dp, &acc, &remap, &kc, &ysplit};
@@ -1246,12 +1337,20 @@ struct QkvWs {
   size_t xp, xn, q, k, v, mm, total;
 };
 
-static int qkv_check(const qmm_qtensor* wq, const qmm_qtensor* wk, const qmm_qtensor* wv, int64_t m, int heads,
-                     int kv_heads, int head_dim) {
+// What the weights alone fix (the workspace query has no attention geometry).
+static int qkv_check_weights(const qmm_qtensor* wq, const qmm_qtensor* wk, const qmm_qtensor* wv, int64_t m) {
   if (!wq || !wk || !wv) return fail(QMM_ERR_INVALID, "null weight");
   if (m < 1) return fail(QMM_ERR_INVALID, "qkv needs m >= 1 (got %lld)", (long long)m);
   if (qmm_vec_dot_type(wq->dtype) != QMM_Q8K || !same_act(wq, wk) || !same_act(wq, wv))
     return fail(QMM_ERR_UNSUPPORTED, "qkv needs Q4_K / Q6_K weights of one k");
+  if (wv->n != wk->n)
+    return fail(QMM_ERR_INVALID, "k and v weights of %lld / %lld rows", (long long)wk->n, (long long)wv->n);
+  return QMM_OK;
+}
+
+static int qkv_check(const qmm_qtensor* wq, const qmm_qtensor* wk, const qmm_qtensor* wv, int64_t m, int heads,
+                     int kv_heads, int head_dim) {
+  QMM_TRY(qkv_check_weights(wq, wk, wv, m));
   if (heads < 1 || kv_heads < 1 || heads % kv_heads || head_dim < 2 || head_dim > 1024 || head_dim % 2)
     return fail(QMM_ERR_INVALID, "bad attention geometry");
   if (wq->n != (int64_t)heads * head_dim || wk->n != (int64_t)kv_heads * head_dim || wv->n != wk->n)
@@ -1292,7 +1391,7 @@ static QkvWs qkv_ws(Device* d, const qmm_qtensor* wq, const qmm_qtensor* wk, con
 
 size_t qmm_qkv_rope_kv_append_n_workspace_size(const qmm_qtensor* wq, const qmm_qtensor* wk, const qmm_qtensor* wv,
                                                int64_t m, int normalize) {
-  if (!wq || !wk || !wv || m < 1) return 0;
+  if (qkv_check_weights(wq, wk, wv, m) != QMM_OK) return 0;
   Device* d;
   if (current_device(&d) != QMM_OK) return 0;
   return qkv_ws(d, wq, wk, wv, m, normalize != 0).total;
@@ -1609,18 +1708,27 @@ int qmm_block_dots(const qmm_qtensor* w, const void* xq, int64_t m, float* y, in
 // mixture of experts
 // ---------------------------------------------------------------------------
 
-int qmm_moe_route(const float* logits, int64_t tokens, int experts, int topk, int renormalize, int32_t* counts,
-                  int32_t* offsets, int32_t* pair_token, float* pair_weight, int32_t* token_pairs, void* stream) {
+int qmm_moe_route_ex(const float* logits, int64_t tokens, int experts, int topk, int renormalize,
+                     float routed_scaling_factor, int32_t* counts, int32_t* offsets, int32_t* pair_token,
+                     float* pair_weight, int32_t* token_pairs, void* stream) {
   if (!logits || !counts || !offsets || !pair_token || !pair_weight || !token_pairs)
     return fail(QMM_ERR_INVALID, "null pointer");
   if (tokens < 1 || tokens > 4096 || experts < 1 || experts > 256 || topk < 1 || topk > 8 || topk > experts ||
       tokens * topk > 8192)
     return fail(QMM_ERR_INVALID, "routing limits: 1 <= tokens <= 4096, tokens*topk <= 8192, topk <= min(8, experts)");
+  if (!(routed_scaling_factor == routed_scaling_factor)) return fail(QMM_ERR_INVALID, "routed scaling factor is NaN");
   Device* d;
   QMM_TRY(current_device(&d));
   int T = (int)tokens, E = experts, k = topk, rn = renormalize ? 1 : 0;
-  void* args[] = {&logits, &T, &E, &k, &rn, &counts, &offsets, &pair_token, &pair_weight, &token_pairs};
+  float ps = routed_scaling_factor;
+  void* args[] = {&logits, &T, &E, &k, &rn, &ps, &counts, &offsets, &pair_token, &pair_weight, &token_pairs};
   return launch(d, "qmm_moe_route", 1, 256, 0, (hipStream_t)stream, args);
+}
+
+int qmm_moe_route(const float* logits, int64_t tokens, int experts, int topk, int renormalize, int32_t* counts,
+                  int32_t* offsets, int32_t* pair_token, float* pair_weight, int32_t* token_pairs, void* stream) {
+  return qmm_moe_route_ex(logits, tokens, experts, topk, renormalize, 1.0f, counts, offsets, pair_token, pair_weight,
+                          token_pairs, stream);
 }
 
 // max_count bounds every counts[e] (the token count under top-k routing, else
@@ -1649,7 +1757,7 @@ static int moe_gemv(const qmm_qtensor* const* w, int count, int experts, const v
   // every expert is active); QMM_MOE_GEMV=0 selects the generic M = 8 GEMV,
   // QMM_MOE_GEMV=<P> the ring depth.
   int ring = fmt == kFmtQ4K || fmt == kFmtQ6K ? 1 : 0;  // depth 2 measured no faster (Q4_K up to 3% slower)
-  if (const char* e = getenv("QMM_MOE_GEMV")) ring = fmt != kFmtQ80 ? std::min(std::max(atoi(e), 0), 2) : 0;
+  if (const char* e = env(kEnvMoeGemv)) ring = fmt != kFmtQ80 ? std::min(std::max(atoi(e), 0), 2) : 0;
   if (experts > 256) ring = 0;  // the ring kernel lists the active experts in a 256-entry LDS table
   // the ring kernel addresses an expert's rows with 32-bit offsets
   const unsigned long long body = fmt == kFmtQ4K ? 144 : 208;  // device block bodies (Q6_K's f16 d kept apart)
@@ -1761,12 +1869,12 @@ static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, in
   // 64-row tiles, less padding when an expert's row count sits just above a
   // multiple of 128)
   const unsigned ldss = 2u * (128 * 272 + 128 * 144 + 128 * 4 + 128 * 48 + 128 * 48 + 128 * 80);
-  const char* gen = getenv("QMM_MOE_MMQ");
+  const char* gen = env(kEnvMoeMmq);
   const bool use_s = fmt == kFmtQ4K && (gen == nullptr || atoi(gen) != 2) && (int)ldss <= d->max_lds;
   int bm = 64;
   if (fmt == kFmtQ4K) {
     bm = 128;
-    if (const char* e = getenv("QMM_MOE_BM"); e && !use_s) bm = atoi(e) == 64 ? 64 : 128;
+    if (const char* e = env(kEnvMoeBm); e && !use_s) bm = atoi(e) == 64 ? 64 : 128;
   }
   const int bn = 128;
   unsigned lds = fmt == kFmtQ4K ? (unsigned)(2 * (bm * 272 + 128 * 144 + bm * 4 + bm * 16)) : 0u;
@@ -1786,7 +1894,7 @@ static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, in
   if (fmt != kFmtQ4K) {
     const int nbk = K / 256;
     int sp = 1;
-    if (const char* e = getenv("QMM_MOE_SPLITK")) {
+    if (const char* e = env(kEnvMoeSplitK)) {
       sp = std::max(1, atoi(e));
     } else if (part) {
       const long long tiles = (pairs / kMmqBMRows + experts) * ((N + bn - 1) / bn);
@@ -1840,16 +1948,25 @@ static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, in
 // GEMV streams an expert's weights once per eight rows, the GEMM once per
 // 128-row tile. QMM_MOE_GROUPED=0/1 forces the choice.
 static bool moe_grouped(int64_t pairs, int experts) {
-  if (const char* e = getenv("QMM_MOE_GROUPED")) return atoi(e) != 0;
+  if (const char* e = env(kEnvMoeGrouped)) return atoi(e) != 0;
   return pairs > 16LL * experts;
 }
 
 // Workspace of qmm_moe_ffn, carved in this order.
 struct MoeWs {
-  size_t counts, offsets, pair_token, pair_weight, token_pairs, xg, xq, g, u, h, hq, yp, planes, total;
+  size_t counts, offsets, pair_token, pair_weight, token_pairs, xg, xq, g, u, h, hq, yp, planes;
+  size_t shared, sg, shared_ws, shared_ws_bytes;  // the shared expert (qmm_moe_ffn_ex)
+  size_t total;
 };
-static MoeWs moe_ws(const qmm_qtensor* gate, const qmm_qtensor* down, int64_t T, int E, int k) {
-  MoeWs w;
+// The optional shared expert of qmm_moe_ffn_ex: a dense gated MLP over every
+// token, and its sigmoid gate vector.
+struct MoeShared {
+  const qmm_qtensor *gate = nullptr, *up = nullptr, *down = nullptr;
+  const float* gate_w = nullptr;  // f32 [hidden] or null (ungated)
+};
+static MoeWs moe_ws(const qmm_qtensor* gate, const qmm_qtensor* down, int64_t T, int E, int k,
+                    const MoeShared* sh = nullptr) {
+  MoeWs w = {};
   const int64_t P = T * k, H = gate->k, F = gate->n / E;
   const int vg = qmm_vec_dot_type(gate->dtype), vd = qmm_vec_dot_type(down->dtype);
   size_t o = 0;
@@ -1871,6 +1988,12 @@ static MoeWs moe_ws(const qmm_qtensor* gate, const qmm_qtensor* down, int64_t T,
   w.hq = take(P * (F / qmm_block_size(vd)) * qmm_type_size(vd));
   w.yp = take(4 * P * H);
   w.planes = take(std::max(mmq_planes(gate->dtype, P, H).total, mmq_planes(down->dtype, P, F).total));
+  if (sh != nullptr && sh->gate != nullptr) {
+    w.shared = take(4 * T * H);
+    w.sg = take(4 * T);
+    w.shared_ws_bytes = qmm_ffn_workspace_size(sh->gate, sh->up, sh->down, T, 0);
+    w.shared_ws = take(w.shared_ws_bytes);
+  }
   w.total = o;
   return w;
 }
@@ -1886,6 +2009,19 @@ static int check_moe(const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_q
   return QMM_OK;
 }
 
+static int check_moe_shared(const qmm_qtensor* gate, const MoeShared& sh) {
+  if (sh.gate == nullptr && sh.up == nullptr && sh.down == nullptr) {
+    if (sh.gate_w != nullptr) return fail(QMM_ERR_INVALID, "a shared-expert gate vector without a shared expert");
+    return QMM_OK;
+  }
+  if (!sh.gate || !sh.up || !sh.down) return fail(QMM_ERR_INVALID, "the shared expert needs gate, up and down");
+  if (sh.gate->k != gate->k) return fail(QMM_ERR_INVALID, "shared expert input width differs from the experts'");
+  if (sh.down->n != gate->k) return fail(QMM_ERR_INVALID, "shared expert output width differs from the hidden size");
+  if (qmm_ffn_workspace_size(sh.gate, sh.up, sh.down, 1, 0) == 0)
+    return fail(QMM_ERR_INVALID, "shared expert weights do not form a gated MLP: %s", qmm_last_error());
+  return QMM_OK;
+}
+
 // Tokens per routing launch (qmm_moe_route: tokens <= 4096, tokens * topk <=
 // 8192). qmm_moe_ffn runs longer token lists as consecutive chunks of this
 // many tokens: tokens are routed and combined independently, so the chunks'
@@ -1896,6 +2032,18 @@ size_t qmm_moe_ffn_workspace_size(const qmm_qtensor* gate, const qmm_qtensor* do
                                   int topk) {
   if (!gate || !down || tokens < 1 || experts < 1 || topk < 1) return 0;
   return moe_ws(gate, down, std::min(tokens, moe_chunk(topk)), experts, topk).total;
+}
+
+size_t qmm_moe_ffn_ex_workspace_size(const qmm_qtensor* gate, const qmm_qtensor* down, int64_t tokens, int experts,
+                                     int topk, const qmm_qtensor* shared_gate, const qmm_qtensor* shared_up,
+                                     const qmm_qtensor* shared_down) {
+  if (!gate || !down || tokens < 1 || experts < 1 || topk < 1) return 0;
+  MoeShared sh;
+  sh.gate = shared_gate;
+  sh.up = shared_up;
+  sh.down = shared_down;
+  if (check_moe_shared(gate, sh) != QMM_OK) return 0;
+  return moe_ws(gate, down, std::min(tokens, moe_chunk(topk)), experts, topk, &sh).total;
 }
 
 // Decode-sized MoE: gathered Q8_K rows through the expert GEMVs.
@@ -1945,22 +2093,25 @@ static int moe_gemv_path(Device* d, const MoeWs& L, uint8_t* b, const float* x, 
   return moe_gemv(dw, 1, experts, b + L.hq, P, T, counts, offsets, dy, stream);
 }
 
-int qmm_moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* logits, int experts, int topk,
-                const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* down, float* out, int64_t ldo,
-                void* ws, size_t ws_bytes, void* stream) {
+static int moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* logits, int experts, int topk,
+                   int renormalize, float routed_scaling_factor, const qmm_qtensor* gate, const qmm_qtensor* up,
+                   const qmm_qtensor* down, const MoeShared& sh, float* out, int64_t ldo, void* ws, size_t ws_bytes,
+                   void* stream) {
   QMM_TRY(check_moe(gate, up, down, experts, topk));
+  QMM_TRY(check_moe_shared(gate, sh));
   if (!x || !logits || !out || !ws) return fail(QMM_ERR_INVALID, "null pointer");
   if (tokens < 1) return fail(QMM_ERR_INVALID, "tokens must be >= 1");
   if (ldx < gate->k || ldo < gate->k) return fail(QMM_ERR_INVALID, "row strides must be >= hidden size");
   const int64_t chunk = moe_chunk(topk);
   if (tokens > chunk) {  // consecutive chunks through the same workspace, in stream order
     for (int64_t t0 = 0; t0 < tokens; t0 += chunk)
-      QMM_TRY(qmm_moe_ffn(x + t0 * ldx, std::min(chunk, tokens - t0), ldx, logits + t0 * experts, experts, topk,
-                          gate, up, down, out + t0 * ldo, ldo, ws, ws_bytes, stream));
+      QMM_TRY(moe_ffn(x + t0 * ldx, std::min(chunk, tokens - t0), ldx, logits + t0 * experts, experts, topk,
+                      renormalize, routed_scaling_factor, gate, up, down, sh, out + t0 * ldo, ldo, ws, ws_bytes,
+                      stream));
     return QMM_OK;
   }
   const int64_t H = gate->k, F = gate->n / experts, P = tokens * topk;
-  const MoeWs L = moe_ws(gate, down, tokens, experts, topk);
+  const MoeWs L = moe_ws(gate, down, tokens, experts, topk, &sh);
   if (ws_bytes < L.total) return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed", ws_bytes, L.total);
   Device* d;
   QMM_TRY(current_device(&d));
@@ -1971,7 +2122,8 @@ int qmm_moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* logits
   int32_t* ptok = (int32_t*)(b + L.pair_token);
   float* pw = (float*)(b + L.pair_weight);
   int32_t* tpairs = (int32_t*)(b + L.token_pairs);
-  QMM_TRY(qmm_moe_route(logits, tokens, experts, topk, 1, counts, offsets, ptok, pw, tpairs, stream));
+  QMM_TRY(qmm_moe_route_ex(logits, tokens, experts, topk, renormalize, routed_scaling_factor, counts, offsets, ptok,
+                           pw, tpairs, stream));
   float* g = (float*)(b + L.g);
   float* u = (float*)(b + L.u);
   float* h = (float*)(b + L.h);
@@ -2042,12 +2194,50 @@ int qmm_moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* logits
   } else {
     QMM_TRY(moe_gemv_path(d, L, b, x, ldx, ptok, tokens, P, H, F, experts, counts, offsets, gate, up, down, s));
   }
+  // the always-on shared expert over every token (LlamaMlp::forward) and its
+  // sigmoid gate, added by the combine after the routed sum
+  float* shared = nullptr;
+  float* sg = nullptr;
+  if (sh.gate != nullptr) {
+    shared = (float*)(b + L.shared);
+    QMM_TRY(qmm_ffn(sh.gate, sh.up, sh.down, x, tokens, ldx, nullptr, 0.0f, 0, shared, H, b + L.shared_ws,
+                    L.shared_ws_bytes, stream));
+    if (sh.gate_w != nullptr) {
+      sg = (float*)(b + L.sg);
+      const float* gw = sh.gate_w;
+      long long lx = ldx;
+      int hh = (int)H, tt = (int)tokens;
+      void* args[] = {&x, &lx, &gw, &hh, &tt, &sg};
+      QMM_TRY(launch(d, "qmm_moe_shared_gate", ceil_div(tokens, 4), 256, 0, s, args));
+    }
+  }
   {
     int T = (int)tokens, k = topk, N = (int)H, lo = (int)ldo;
-    void* args[] = {&yp, &pw, &tpairs, &T, &k, &N, &out, &lo};
+    void* args[] = {&yp, &pw, &tpairs, &T, &k, &N, &out, &lo, &shared, &sg};
     QMM_TRY(launch(d, "qmm_moe_combine", ceil_div(tokens * H, 256), 256, 0, s, args));
   }
   return QMM_OK;
+}
+
+int qmm_moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* logits, int experts, int topk,
+                const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* down, float* out, int64_t ldo,
+                void* ws, size_t ws_bytes, void* stream) {
+  return moe_ffn(x, tokens, ldx, logits, experts, topk, 1, 1.0f, gate, up, down, MoeShared(), out, ldo, ws, ws_bytes,
+                 stream);
+}
+
+int qmm_moe_ffn_ex(const float* x, int64_t tokens, int64_t ldx, const float* logits, int experts, int topk,
+                   int norm_topk_prob, float routed_scaling_factor, const qmm_qtensor* gate, const qmm_qtensor* up,
+                   const qmm_qtensor* down, const qmm_qtensor* shared_gate, const qmm_qtensor* shared_up,
+                   const qmm_qtensor* shared_down, const float* shared_gate_weight, float* out, int64_t ldo, void* ws,
+                   size_t ws_bytes, void* stream) {
+  MoeShared sh;
+  sh.gate = shared_gate;
+  sh.up = shared_up;
+  sh.down = shared_down;
+  sh.gate_w = shared_gate_weight;
+  return moe_ffn(x, tokens, ldx, logits, experts, topk, norm_topk_prob, routed_scaling_factor, gate, up, down, sh, out,
+                 ldo, ws, ws_bytes, stream);
 }
 
 }  // extern "C"

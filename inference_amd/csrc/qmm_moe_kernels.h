@@ -27,7 +27,8 @@
 // 64 at a time: a ballot of the lanes whose token selected e ranks them, so
 // pair p = offsets[e] + (pairs of e so far) + (selecting lanes below).
 extern "C" __global__ void __launch_bounds__(256) qmm_moe_route(const float* __restrict__ logits, int T, int E,
-                                                                int k, int renorm, int* __restrict__ counts,
+                                                                int k, int renorm, float post_scale,
+                                                                int* __restrict__ counts,
                                                                 int* __restrict__ offsets,
                                                                 int* __restrict__ pair_token,
                                                                 float* __restrict__ pair_weight,
@@ -70,7 +71,9 @@ extern "C" __global__ void __launch_bounds__(256) qmm_moe_route(const float* __r
     denom = fmaxf(denom, 1.17549435e-38f);
     for (int s = 0; s < k; ++s) {
       sel_e[t * k + s] = (short)ids[s];
-      sel_w[t * k + s] = renorm ? p[s] / denom : p[s];
+      // renormalised over the selection, or (norm_topk_prob false) times the
+      // routed scaling factor: row[e] / denom * post_scale with denom = 1
+      sel_w[t * k + s] = renorm ? p[s] / denom : p[s] * post_scale;
       atomicAdd(&ecount[ids[s]], 1);
     }
   }
@@ -145,10 +148,13 @@ extern "C" __global__ void qmm_silu_mul(const float* __restrict__ g, const float
 }
 
 // out[t][n] = sum over the pairs of token t (in increasing expert order) of
-// weight * y_pair[n], accumulated from zero like index_add.
+// weight * y_pair[n], accumulated from zero like index_add; then, with a
+// shared expert, + shared[t][n] (times sg[t] when the shared expert is gated):
+// MoeMlp::forward's `out + shared` (models/llama.rs:1476-1486).
 extern "C" __global__ void qmm_moe_combine(const float* __restrict__ yp, const float* __restrict__ pair_weight,
                                            const int* __restrict__ token_pairs, int T, int k, int N,
-                                           float* __restrict__ out, int ldo) {
+                                           float* __restrict__ out, int ldo, const float* __restrict__ shared,
+                                           const float* __restrict__ sg) {
 #pragma clang fp contract(off)
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (long long)T * N) return;
@@ -159,7 +165,27 @@ extern "C" __global__ void qmm_moe_combine(const float* __restrict__ yp, const f
     const float v = yp[(size_t)p * N + n] * pair_weight[p];
     acc = acc + v;
   }
+  if (shared != nullptr) {
+    const float sv = shared[(size_t)t * N + n];
+    acc = acc + (sg != nullptr ? sv * sg[t] : sv);
+  }
   out[(size_t)t * ldo + n] = acc;
+}
+
+// The shared expert's sigmoid gate: sg[t] = sigmoid(x[t] . g) (one wave per
+// token; the f32 dot in lane order, then the wave sum), the reference's
+// sigmoid(xf.matmul(shared_gate.t())) (models/llama.rs:1479-1482).
+extern "C" __global__ void __launch_bounds__(256) qmm_moe_shared_gate(const float* __restrict__ x, long long ldx,
+                                                                      const float* __restrict__ g, int H, int T,
+                                                                      float* __restrict__ sg) {
+#pragma clang fp contract(off)
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const float* xr = x + (long long)t * ldx;
+  float acc = 0.0f;
+  for (int h = lane; h < H; h += 64) acc += xr[h] * g[h];
+  acc = qmm::wave_sum(acc);
+  if (lane == 0) sg[t] = 1.0f / (1.0f + expf(-acc));
 }
 
 // Expert-grouped GEMV: blockIdx.y = expert e; its counts[e] token rows (up to

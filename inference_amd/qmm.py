@@ -60,7 +60,7 @@ EXPORTS = (
     "qmm_gguf_meta_u64", "qmm_gguf_meta_i64", "qmm_gguf_meta_f64", "qmm_gguf_meta_string",
     "qmm_gguf_load_qtensor", "qmm_qtensor_dequantize_to", "qmm_embed_rows_n", "qmm_rope_kv_append_n",
     "qmm_prefill_attention", "qmm_silu_mul", "qmm_matmul_q_workspace_size", "qmm_matmul_noalloc",
-    "qmm_stream_read",
+    "qmm_stream_read", "qmm_reload_tuning", "qmm_moe_route_ex", "qmm_moe_ffn_ex_workspace_size", "qmm_moe_ffn_ex",
 )
 
 
@@ -81,6 +81,7 @@ def lib() -> ctypes.CDLL:
         sig = {
             "qmm_last_error": ([], ctypes.c_char_p),
             "qmm_init": ([i32], i32),
+            "qmm_reload_tuning": ([], None),
             "qmm_block_size": ([i32], i32),
             "qmm_type_size": ([i32], i32),
             "qmm_vec_dot_type": ([i32], i32),
@@ -107,6 +108,10 @@ def lib() -> ctypes.CDLL:
                               ctypes.c_size_t, vp], i32),
             "qmm_moe_ffn_workspace_size": ([vp, vp, i64, i32, i32], sz),
             "qmm_moe_ffn": ([vp, i64, i64, vp, i32, i32, vp, vp, vp, vp, i64, vp, sz, vp], i32),
+            "qmm_moe_route_ex": ([vp, i64, i32, i32, i32, ctypes.c_float, vp, vp, vp, vp, vp, vp], i32),
+            "qmm_moe_ffn_ex_workspace_size": ([vp, vp, i64, i32, i32, vp, vp, vp], sz),
+            "qmm_moe_ffn_ex": ([vp, i64, i64, vp, i32, i32, i32, ctypes.c_float, vp, vp, vp, vp, vp, vp, vp, vp, i64,
+                                vp, sz, vp], i32),
             "qmm_matmul_ex": ([ctypes.POINTER(vp), i32, vp, i64, i64, vp, ctypes.c_float, i32, ctypes.POINTER(vp),
                                ctypes.POINTER(i64), vp, sz, vp], i32),
             "qmm_matmul_ex_workspace_size": ([vp, i64, i32], sz),
@@ -487,8 +492,10 @@ def block_dots(qt: QTensor, xq: torch.Tensor, m: int) -> Tuple[torch.Tensor, tor
     return (dots if per == 2 else dots[..., 0]), y
 
 
-def moe_route(logits: torch.Tensor, topk: int, renormalize: bool = True):
-    """Device routing: returns (counts, offsets, pair_token, pair_weight, token_pairs)."""
+def moe_route(logits: torch.Tensor, topk: int, renormalize: bool = True, routed_scaling_factor: float = 1.0):
+    """Device routing: returns (counts, offsets, pair_token, pair_weight, token_pairs). Weights are the
+    selected probabilities renormalised over the selection, or (renormalize False) times
+    routed_scaling_factor (MoeMlp::forward, models/llama.rs:1436-1447)."""
     t, e = logits.shape
     dev = logits.device
     lg = logits.to(torch.float32).contiguous()
@@ -498,14 +505,20 @@ def moe_route(logits: torch.Tensor, topk: int, renormalize: bool = True):
     pw = torch.empty(t * topk, dtype=torch.float32, device=dev)
     tp = torch.empty(t * topk, dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
-        _check(lib().qmm_moe_route(lg.data_ptr(), t, e, topk, int(renormalize), counts.data_ptr(), offsets.data_ptr(),
-                                   ptok.data_ptr(), pw.data_ptr(), tp.data_ptr(), _stream(dev)))
+        _check(lib().qmm_moe_route_ex(lg.data_ptr(), t, e, topk, int(renormalize), routed_scaling_factor,
+                                      counts.data_ptr(), offsets.data_ptr(), ptok.data_ptr(), pw.data_ptr(),
+                                      tp.data_ptr(), _stream(dev)))
     return counts, offsets, ptok, pw, tp
 
 
-def moe_ffn(x: torch.Tensor, logits: torch.Tensor, gate: QTensor, up: QTensor, down: QTensor,
-            topk: int) -> torch.Tensor:
-    """Mixture-of-experts FFN (MoeMlp::forward with renormalised top-k) on stacked expert weights."""
+def moe_ffn(x: torch.Tensor, logits: torch.Tensor, gate: QTensor, up: QTensor, down: QTensor, topk: int,
+            norm_topk_prob: bool = True, routed_scaling_factor: float = 1.0, shared=None,
+            shared_gate: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Mixture-of-experts FFN (MoeMlp::forward, models/llama.rs:1416-1487) on stacked expert weights:
+    top-k routing (renormalised, or scaled by routed_scaling_factor), each expert's gated MLP on its
+    tokens, the weighted outputs summed in expert order; then `shared` = (gate, up, down) QTensors of the
+    always-on shared expert, added after the routed sum, scaled per token by sigmoid(x . shared_gate)
+    when shared_gate (f32 [hidden]) is given."""
     t, hdim = x.shape
     e = logits.shape[1]
     dev = x.device
@@ -513,11 +526,19 @@ def moe_ffn(x: torch.Tensor, logits: torch.Tensor, gate: QTensor, up: QTensor, d
     lg = logits.to(torch.float32).contiguous()
     out = torch.empty((t, hdim), dtype=torch.float32, device=dev)
     L = lib()
-    wsb = int(L.qmm_moe_ffn_workspace_size(gate.handle, down.handle, t, e, topk))
-    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    sg, su, sd = (s.handle for s in shared) if shared is not None else (None, None, None)
+    if shared is None and shared_gate is not None:
+        raise QmmError(QMM_ERR_INVALID, "a shared-expert gate without a shared expert")
+    gw = shared_gate.to(torch.float32).contiguous() if shared_gate is not None else None
     with torch.cuda.device(dev):
-        _check(L.qmm_moe_ffn(xx.data_ptr(), t, hdim, lg.data_ptr(), e, topk, gate.handle, up.handle, down.handle,
-                             out.data_ptr(), hdim, ws.data_ptr(), wsb, _stream(dev)))
+        wsb = int(L.qmm_moe_ffn_ex_workspace_size(gate.handle, down.handle, t, e, topk, sg, su, sd))
+        if wsb == 0:
+            raise QmmError(QMM_ERR_INVALID, "moe_ffn: " + last_error())
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        _check(L.qmm_moe_ffn_ex(xx.data_ptr(), t, hdim, lg.data_ptr(), e, topk, int(norm_topk_prob),
+                                routed_scaling_factor, gate.handle, up.handle, down.handle, sg, su, sd,
+                                gw.data_ptr() if gw is not None else None, out.data_ptr(), hdim, ws.data_ptr(), wsb,
+                                _stream(dev)))
     return out
 
 

@@ -3,11 +3,16 @@
 Follows MoeMlp::forward, crates/llm/candle-llm/src/models/llama.rs:1416-1487:
   * probabilities = softmax over the router logits (f32);
   * per token, the top-k experts by probability (ties: lower expert index);
-  * weights renormalised over the selected experts (norm_topk_prob), :1436-1451;
+  * weights renormalised over the selected experts (norm_topk_prob), or, when
+    not renormalising, times routed_scaling_factor: row[e] / denom * post_scale
+    with (denom, post_scale) = (sum, 1) or (1, routed_scaling_factor), :1436-1451;
   * each expert runs LlamaMlp::forward (llama.rs:1386-1391) on its tokens:
     down(silu(gate(x)) * up(x)) with the quantized matmuls of oracle.matmul;
   * the weighted expert outputs are index_add-ed onto zeros in increasing
-    expert order (:1461-1474).
+    expert order (:1461-1474);
+  * the always-on shared expert (a LlamaMlp over every token), scaled per
+    token by sigmoid(x . shared_gate) when the model has that gate (Qwen2-MoE;
+    DeepSeek-V2 adds it ungated), is added last: out + shared (:1476-1486).
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline use this.
 """
 from __future__ import annotations
@@ -24,7 +29,7 @@ def softmax_f32(logits: np.ndarray) -> np.ndarray:
     return (e / e.sum(axis=-1, keepdims=True, dtype=np.float32)).astype(np.float32)
 
 
-def route(logits: np.ndarray, k: int, renormalize: bool = True):
+def route(logits: np.ndarray, k: int, renormalize: bool = True, routed_scaling_factor: float = 1.0):
     """Per token: (experts[k], weights[k]) with experts in descending probability."""
     p = softmax_f32(logits)
     experts, weights = [], []
@@ -37,9 +42,16 @@ def route(logits: np.ndarray, k: int, renormalize: bool = True):
                 denom = np.float32(denom + v)
             denom = max(denom, np.float32(np.finfo(np.float32).tiny))
             sel = (sel / denom).astype(np.float32)
+        else:
+            sel = ((sel / np.float32(1.0)) * np.float32(routed_scaling_factor)).astype(np.float32)
         experts.append(idx)
         weights.append(sel)
     return experts, weights
+
+
+def sigmoid_f32(v: np.ndarray) -> np.ndarray:
+    v = np.asarray(v, dtype=np.float32)
+    return (np.float32(1.0) / (np.float32(1.0) + np.exp(-v, dtype=np.float32))).astype(np.float32)
 
 
 def silu_f32(v: np.ndarray) -> np.ndarray:
@@ -55,13 +67,16 @@ def mlp(x: np.ndarray, gate: bytes, up: bytes, down: bytes, dt_gu: int, dt_down:
     return orc.matmul(dt_down, h, down, ffn)
 
 
-def moe_ffn(x, logits, gate_experts, up_experts, down_experts, dt_gu, dt_down, k, renormalize=True):
-    """x f32 [T, H]; *_experts: per-expert GGML byte arrays ([F, H] for gate/up, [H, F] for down)."""
+def moe_ffn(x, logits, gate_experts, up_experts, down_experts, dt_gu, dt_down, k, renormalize=True,
+            routed_scaling_factor=1.0, shared=None, shared_gate=None):
+    """x f32 [T, H]; *_experts: per-expert GGML byte arrays ([F, H] for gate/up, [H, F] for down);
+    shared: (gate, up, down, dt_gu, dt_down) GGML bytes of the shared expert ([Fs, H], [Fs, H], [H, Fs]);
+    shared_gate: its f32 [H] sigmoid gate vector (None: ungated)."""
     x = np.asarray(x, dtype=np.float32)
     T, H = x.shape
     E = len(gate_experts)
     F = np.asarray(gate_experts[0]).size // orc.row_bytes(dt_gu, H)
-    experts, weights = route(logits, k, renormalize)
+    experts, weights = route(logits, k, renormalize, routed_scaling_factor)
     out = np.zeros((T, H), dtype=np.float32)
     for e in range(E):
         toks = [(t, weights[t][experts[t].index(e)]) for t in range(T) if e in experts[t]]
@@ -73,4 +88,12 @@ def moe_ffn(x, logits, gate_experts, up_experts, down_experts, dt_gu, dt_down, k
         ye = (ye * w).astype(np.float32)
         for j, t in enumerate(idx):
             out[t] = (out[t] + ye[j]).astype(np.float32)
-    return out
+    if shared is None:
+        return out
+    sgate, sup, sdown, sdt_gu, sdt_down = shared
+    Fs = np.asarray(sgate).size // orc.row_bytes(sdt_gu, H)
+    sh = mlp(x, sgate, sup, sdown, sdt_gu, sdt_down, H, Fs)
+    if shared_gate is not None:
+        sg = sigmoid_f32((x @ np.asarray(shared_gate, np.float32)).astype(np.float32))
+        sh = (sh * sg[:, None]).astype(np.float32)
+    return (out + sh).astype(np.float32)

@@ -65,6 +65,19 @@ def test_rust_sys_bindings_mirror_the_header():
         assert rust[name] == params, name
 
 
+def test_rust_from_ggml_checks_the_slice_length():
+    """The safe Rust wrapper over qmm_qtensor_from_ggml (which copies n * (k / block) * type_size bytes from
+    the host pointer) refuses a slice of any other length before the call: a safe call cannot read past it.
+    No Rust toolchain here, so the order is checked in the source: the length comparison, with checked
+    arithmetic, precedes the only unsafe call of the function."""
+    rs = open(os.path.join(ROOT, "include", "qmm_sys.rs")).read()
+    body = rs[rs.index("pub fn from_ggml("):]
+    body = body[:body.index("\n    }\n")]
+    call = body.index("qmm_qtensor_from_ggml(")
+    assert "bytes.len()" in body[:call] and "checked_mul" in body[:call]
+    assert body.index("return Err(invalid(\"byte slice length") < call
+
+
 def test_geometry(L):
     # crates/llm/mlx-llm/src/gguf/dequant.rs:752-773 (block geometry KAT)
     assert (L.qmm_block_size(8), L.qmm_type_size(8)) == (32, 34)

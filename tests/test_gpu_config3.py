@@ -14,7 +14,9 @@ Checked here:
   the reference's own spread between two of its builds. On this random-init 32-layer stack that
   spread is large (max|d|/rms of the logits ~0.4, cosine ~0.995: every last-bit difference that
   lands on a Q8_K rounding tie moves an activation by a quantum, and the stack amplifies it), so
-  the bar is that the device's distance stays within 1.25x of it in median and maximum;
+  the bar is that the device's distance stays within 1.25x of it in median and maximum, and that
+  the device's greedy token leaves the generic chain's argmax at most 1.25x as often as the AVX2
+  chain's does;
 * where the chains part: the first (position, layer) whose K/V rows leave f32 noise, and at that
   position the activation quantizations just before it, re-run on the device and in the oracle.
   The first op whose Q8_K codes differ must differ by one quantum at elements whose pre-rounding
@@ -127,7 +129,7 @@ def test_config3_full_workload():
     oa = ol.LlamaOracle(cfg, ex, max_seq, orc.AVX2) if orc.simd_supported() else None
     dev_first = avx_first = None
     dev_rec = avx_rec = None
-    err_dev, err_avx, cos_dev, cos_avx, flips = {}, {}, {}, {}, []
+    err_dev, err_avx, cos_dev, cos_avx, flips, avx_flips = {}, {}, {}, {}, [], []
     for p in range(max_seq - 1):
         rg, ra = {}, {}
         lg = og.step(toks[p], p, rg)
@@ -145,9 +147,11 @@ def test_config3_full_workload():
         if p >= PROMPT - 1:
             h = H[p - (PROMPT - 1)]
             err_dev[p], cos_dev[p] = rel_err(h, lg), cosine(h, lg)
+            want = ol.argmax_first(lg)
             if la is not None:
                 err_avx[p], cos_avx[p] = rel_err(la, lg), cosine(la, lg)
-            want = ol.argmax_first(lg)
+                if ol.argmax_first(la) != want:
+                    avx_flips.append(p)
             if toks[p + 1] != want:
                 gap = float(lg[want] - lg[toks[p + 1]])
                 flips.append((p, gap))
@@ -162,7 +166,8 @@ def test_config3_full_workload():
     log(f"[config3] over all 256 steps: device max {ed.max():.2e} median {np.median(ed):.2e} "
         f"cos min {cd.min():.5f} median {np.median(cd):.5f} | AVX2 chain max {ea.max():.2e} "
         f"median {np.median(ea):.2e} cos min {ca.min():.5f} median {np.median(ca):.5f}; "
-        f"device greedy tokens off the generic chain's argmax at near-ties: {len(flips)}")
+        f"greedy tokens off the generic chain's argmax over the 256 teacher-forced steps: device "
+        f"{len(flips)}, AVX2 chain {len(avx_flips)}")
     log(f"[config3] first K/V rows past f32 noise: device {dev_first}, AVX2 chain {avx_first}")
 
     # ---- the CPU chains: where the AVX2 chain leaves the generic one ----
@@ -201,3 +206,6 @@ def test_config3_full_workload():
     assert ed.max() <= 1.25 * ea.max(), (ed.max(), ea.max())
     assert np.median(cd) >= 1.0 - 1.25 * (1.0 - np.median(ca)), (np.median(cd), np.median(ca))
     assert cd.min() >= 1.0 - 1.25 * (1.0 - ca.min()), (cd.min(), ca.min())
+    # greedy tokens: the device's argmax leaves the generic chain's no more often than the AVX2 build's
+    # does (both fed the same tokens), within the same 1.25x
+    assert len(flips) <= 1.25 * len(avx_flips), (len(flips), len(avx_flips))

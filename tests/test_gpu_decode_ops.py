@@ -257,17 +257,16 @@ def test_decode_attention(heads, kv_heads, hd, p):
         np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-4, atol=2e-5)
 
 
-@pytest.mark.parametrize("heads,kv_heads,hd", ATTN_GEOM)
-@pytest.mark.parametrize("p", [0, 5, 130, 511, 700, 1023])
-def test_decode_rope_attention(heads, kv_heads, hd, p):
-    """Fused RoPE + KV append + attention == rope_kv_append then attention (oracle on the same cache);
-    the appending workgroup is chunk 0's below the split threshold and the one whose chunk holds p above."""
+def _rope_attention_case(heads, kv_heads, hd, p, stale_nan):
     rng = np.random.default_rng(90 + p)
     max_seq = 1024
     cfg = LlamaConfig(heads=heads, kv_heads=kv_heads, head_dim=hd)
     cos, sin = rope_tables(cfg, max_seq)
     kc = rng.standard_normal((kv_heads, max_seq, hd)).astype(np.float32)
     vc = rng.standard_normal((kv_heads, max_seq, hd)).astype(np.float32)
+    if stale_nan:  # a cache never written at p and beyond (e.g. torch.empty): nothing there may be read
+        kc[:, p:] = np.nan
+        vc[:, p:] = np.nan
     q = rng.standard_normal((heads, hd)).astype(np.float32)
     k = rng.standard_normal((kv_heads, hd)).astype(np.float32)
     v = rng.standard_normal((kv_heads, hd)).astype(np.float32)
@@ -292,6 +291,22 @@ def test_decode_rope_attention(heads, kv_heads, hd, p):
     g = heads // kv_heads
     want = np.stack([ol.attend_one(qr[h], kref[h // g, : p + 1], vref[h // g, : p + 1], scale) for h in range(heads)])
     np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-4, atol=2e-5)
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd", ATTN_GEOM)
+@pytest.mark.parametrize("p", [0, 5, 130, 511, 700, 1023])
+def test_decode_rope_attention(heads, kv_heads, hd, p):
+    """Fused RoPE + KV append + attention == rope_kv_append then attention (oracle on the same cache);
+    the appending workgroup is chunk 0's below the split threshold and the one whose chunk holds p above."""
+    _rope_attention_case(heads, kv_heads, hd, p, False)
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd", [(32, 8, 128), (8, 1, 64)])
+@pytest.mark.parametrize("p", [0, 5, 17, 130, 700])
+def test_decode_rope_attention_ignores_unwritten_cache(heads, kv_heads, hd, p):
+    """The cache holds NaN at p and beyond before the fused step: the step appends row p itself and its
+    output equals the oracle's, so no masked slot reads the stale rows into the sums."""
+    _rope_attention_case(heads, kv_heads, hd, p, True)
 
 
 def test_two_streams_own_workspaces():

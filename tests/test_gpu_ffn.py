@@ -192,3 +192,9 @@ def test_qkv_rope_rejects_bad_arguments():
     assert call(4, 2, 20) != 0    # positions past max_seq
     wv8 = QTensor.quantize(torch.zeros((128, 512), device=DEV), GgmlDType.Q8_0)
     assert call(4, 2, 0, wv=wv8) != 0  # Q8_0 weight
+    # the workspace query refuses what the weights alone rule out, as qmm_ffn_workspace_size does
+    size = L().qmm_qkv_rope_kv_append_n_workspace_size
+    assert size(wq.handle, wk.handle, wk.handle, 16, 1) > 0
+    assert size(wq.handle, wk.handle, wv8.handle, 16, 1) == 0  # Q8_0 weight
+    assert size(wq.handle, wk.handle, wq.handle, 16, 1) == 0   # k and v of different row counts
+    assert size(wq.handle, wk.handle, wk.handle, 0, 1) == 0    # no rows

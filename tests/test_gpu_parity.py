@@ -18,6 +18,7 @@ from inference_amd import GgmlDType, QMatMul, QTensor, QuantizedLinear, QmmError
 from inference_amd import matmul_q
 from inference_amd.synth import normal
 from oracle import oracle as orc
+import quant_ties
 
 pytestmark = pytest.mark.gpu
 
@@ -100,8 +101,10 @@ def special_weight_rows(k):
 
 @pytest.mark.parametrize("dt", WEIGHT_TYPES)
 def test_weight_quantizer_bit_exact(dt):
+    # the tie rows put every rounding step of the quantizers exactly on k + 0.5 (tests/quant_ties.py;
+    # the oracle's codes there are pinned to round half away from zero by test_oracle_quant_pins.py)
     k = 4096
-    w = np.concatenate([normal(40, (48, k), 0.02), special_weight_rows(k)])
+    w = np.concatenate([normal(40, (48, k), 0.02), special_weight_rows(k), quant_ties.weight_tie_rows(k)])
     qt = QTensor.quantize(torch.from_numpy(w).to(DEV), dt)
     assert qt.shape == w.shape and qt.dtype() == dt
     got = qt.to_ggml()
