@@ -299,6 +299,24 @@ int qmm_decode_rope_attention(const float *q, const float *k, const float *v, co
                               int heads, int kv_heads, int head_dim, int max_seq, float scale, void *ws,
                               size_t ws_bytes, void *stream);
 
+/* qmm_decode_rope_attention that also warms the caches for the one-row GEMV
+ * launches that follow it in the decode step (the o projection, then
+ * gate/up). The attention occupies half the CUs and almost none of the HBM
+ * bandwidth; extra workgroups of the same launch load the first warm_rows[l]
+ * rows per wave of launch l, each into the L2 of the XCD whose workgroup of
+ * that launch will read them (a dispatch deals workgroups to the XCDs
+ * round-robin, the same way for every launch). warm[i] (warm_count 0..3,
+ * Q4_K / Q6_K) are the launches' weights in launch order, warm_launch[i] the
+ * index of the launch weight i belongs to (non-decreasing); those launches
+ * are fused one-row GEMVs (qmm_matmul_ex at m = 1). The loads write nothing,
+ * so the results equal qmm_decode_rope_attention's. No counterpart in the
+ * reference (a scheduling aid of this backend's decode step). */
+int qmm_decode_rope_attention_warm(const float *q, const float *k, const float *v, const float *cos_t,
+                                   const float *sin_t, const int32_t *pos, float *kcache, float *vcache,
+                                   float *out, int heads, int kv_heads, int head_dim, int max_seq, float scale,
+                                   void *ws, size_t ws_bytes, const qmm_qtensor *const *warm,
+                                   const int *warm_launch, int warm_count, const int *warm_rows, void *stream);
+
 /* Batched prefill: the same per-layer operations over `count` prompt rows at
  * positions first .. first + count - 1 (CausalLm::forward over a prompt with
  * seq_len > 1 and the causal mask, llama.rs:410-433, 654-725; causal sdpa,

@@ -318,6 +318,15 @@ extern "C" {
         max_seq: c_int, scale: f32, ws: *mut c_void, ws_bytes: usize, stream: *mut c_void
     ) -> c_int;
 
+    /// `qmm_decode_rope_attention` whose launch also loads the first rows of the following one-row GEMV
+    /// launches into the L2 of the XCDs that will read them (results unchanged).
+    pub fn qmm_decode_rope_attention_warm(
+        q: *const f32, k: *const f32, v: *const f32, cos_t: *const f32, sin_t: *const f32, pos: *const i32,
+        kcache: *mut f32, vcache: *mut f32, out: *mut f32, heads: c_int, kv_heads: c_int, head_dim: c_int,
+        max_seq: c_int, scale: f32, ws: *mut c_void, ws_bytes: usize, warm: *const *const QmmQTensor,
+        warm_launch: *const c_int, warm_count: c_int, warm_rows: *const c_int, stream: *mut c_void
+    ) -> c_int;
+
     /// x[i] = table[tokens[first + i]] for i < count (CausalLm embed, llama.rs:397-408);
     /// token ids outside [0, vocab) give NaN rows as in qmm_embed_rows.
     pub fn qmm_embed_rows_n(

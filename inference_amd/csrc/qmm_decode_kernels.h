@@ -477,13 +477,99 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
 }
 }  // namespace qmm
 
+// L2 warming for the launches that follow the attention. The attention
+// leaves most CUs idle and HBM nearly so for its whole duration, while the
+// next launches (the o projection, then gate/up) each start by waiting on
+// their first weight loads. Workgroups past the attention's own (grid rows
+// y >= kAttnSplits) load those first rows instead: each L2 is private to one
+// XCD and survives kernel boundaries, and a dispatch deals its workgroups to
+// the eight XCDs round-robin by linear index, so warming workgroup j (the
+// j-th past the attention's kv_heads * kAttnSplits, a multiple of 8) shares an
+// XCD, and its L2, with workgroup j of the one-row GEMV launch whose rows it
+// loads: rows j * nw + i + k * grid_waves (wave i, k-th row of the wave) of
+// the launch's concatenated jobs. The loads change no memory; where the
+// dispatch order differs, the rows are still warm in the memory-side cache.
+namespace qmm {
+constexpr int kPfJobs = 3;
+struct PfJobs {
+  const uint8_t* w[kPfJobs];   // device blocks of each job's rows (row-major)
+  unsigned row_bytes[kPfJobs];  // bytes of one row's block bodies
+  int rows[kPfJobs];            // rows of the job
+  int first[kPfJobs];           // the job's first global row in its launch
+  int grid_waves[kPfJobs];      // waves of the consuming launch
+  int kmax[kPfJobs];            // rows per wave to warm
+  int njobs;
+  int nw;                       // waves per workgroup of the consuming launches
+};
+
+template <typename T>
+__device__ __forceinline__ T pick3(const T (&a)[kPfJobs], int i) {  // constant indices only (no scratch)
+  return i == 0 ? a[0] : i == 1 ? a[1] : a[2];
+}
+
+// Warming workgroup j (of nwarm, a multiple of 8) loads for the consuming
+// launches' workgroups j, j + nwarm, ... (all on its XCD). The loads go
+// straight to LDS (global_load_lds_dwordx4), into one 1 KB area per wave that
+// nothing reads: they hold no registers, so a wave keeps all of its loads in
+// flight at once instead of waiting a round trip per batch.
+__device__ __forceinline__ void l2_warm(const PfJobs& pf, int j, int nwarm) {
+  __shared__ __attribute__((aligned(16))) uint8_t dump[16 * 1024];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nwv = blockDim.x >> 6;
+  auto* dst = (__attribute__((address_space(3))) void*)(dump + 1024 * (wave & 15));
+#pragma unroll 1
+  for (int jb = 0; jb < pf.njobs; ++jb) {
+    const uint8_t* w = pick3(pf.w, jb);
+    const unsigned rb = pick3(pf.row_bytes, jb);
+    const int rows = pick3(pf.rows, jb), first = pick3(pf.first, jb), gw = pick3(pf.grid_waves, jb);
+    const int kmax = pick3(pf.kmax, jb), nc = gw / pf.nw;
+#pragma unroll 1
+    for (int k = 0; k < kmax; ++k)
+#pragma unroll 1
+      for (int c = j; c < nc; c += nwarm) {
+        // the consuming workgroup c's rows c * nw + i (i < nw) of the k-th
+        // round are consecutive rows of its launch: one contiguous range
+        const int g0 = c * pf.nw + k * gw - first;
+        const int r0 = max(g0, 0), r1 = min(g0 + pf.nw, rows);
+        if (r0 >= r1) continue;
+        const uint8_t* base = w + (size_t)r0 * rb;
+        const unsigned len = (unsigned)(r1 - r0) * rb;  // a multiple of 16, inside the weight
+#pragma unroll 1
+        for (unsigned ch = (unsigned)wave; 1024u * ch < len; ch += (unsigned)nwv) {
+          const unsigned o = min(1024u * ch + 16u * (unsigned)lane, len - 16u);
+          __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(base + o), dst, 16, 0, 0);
+        }
+      }
+  }
+}
+}  // namespace qmm
+
+#define QMM_PF_PARAMS(i) const uint8_t *pfw##i, unsigned pfb##i, int pfr##i, int pff##i, int pfg##i, int pfk##i
+#define QMM_PF_SET(i)  \
+  pf.w[i] = pfw##i;    \
+  pf.row_bytes[i] = pfb##i; \
+  pf.rows[i] = pfr##i; \
+  pf.first[i] = pff##i; \
+  pf.grid_waves[i] = pfg##i; \
+  pf.kmax[i] = pfk##i;
+
 #define QMM_ATTN_KERNEL(DPL, GT, NW)                                                                             \
   extern "C" __global__ void __launch_bounds__(64 * NW) qmm_decode_attention_d##DPL##_g##GT##_w##NW(             \
       const float* __restrict__ q, const float* __restrict__ k_new, const float* __restrict__ v_new,            \
       const float* __restrict__ cos_t, const float* __restrict__ sin_t, const int* __restrict__ pos,            \
       float* __restrict__ kcache, float* __restrict__ vcache, float* __restrict__ part,                         \
       unsigned* __restrict__ counters, float* __restrict__ out, int heads, int kv_heads, int max_seq,           \
-      float scale) {                                                                                             \
+      float scale, QMM_PF_PARAMS(0), QMM_PF_PARAMS(1), QMM_PF_PARAMS(2), int pf_njobs, int pf_nw) {           \
+    if (blockIdx.y >= (unsigned)qmm::kAttnSplits) {                                                              \
+      qmm::PfJobs pf;                                                                                            \
+      QMM_PF_SET(0) QMM_PF_SET(1) QMM_PF_SET(2)                                                                  \
+      pf.njobs = pf_njobs;                                                                                       \
+      pf.nw = pf_nw;                                                                                             \
+      const int j = (int)(blockIdx.x + (blockIdx.y - qmm::kAttnSplits) * gridDim.x);                            \
+      const int nwarm = (int)((gridDim.y - qmm::kAttnSplits) * gridDim.x);                                      \
+      qmm::l2_warm(pf, j, nwarm);                                                                                \
+      return;                                                                                                    \
+    }                                                                                                            \
     qmm::decode_attention<DPL, GT, NW>(q, k_new, v_new, cos_t, sin_t, pos, kcache, vcache, part, counters, out, \
                                        heads, kv_heads, max_seq, scale);                                        \
   }

@@ -1510,6 +1510,59 @@ static int check_attention(int heads, int kv_heads, int head_dim, int max_seq) {
 
 static size_t attn_counter_bytes(int kv_heads) { return ((size_t)kv_heads * 4 + 255) / 256 * 256; }
 
+// L2 warming by the attention launch (see qmm_decode_kernels.h): the weights of
+// the one-row GEMV launches that follow the attention, each with the launch it
+// belongs to (jobs of one launch consecutive, launches in order) and the rows
+// per wave of that launch to load. The consuming launches' geometry is the one
+// gemv() gives a fused one-row launch: 16-wave workgroups, min(rows / 16, CUs)
+// of them.
+struct WarmPlan {
+  const void* w[3];
+  unsigned row_bytes[3];
+  int rows[3], first[3], grid_waves[3], kmax[3];
+  int njobs = 0;
+};
+static int warm_plan(const Device* d, const qmm_qtensor* const* warm, const int* warm_launch, int count,
+                     const int* warm_rows, WarmPlan* out) {
+  WarmPlan p;
+  if (count == 0) {
+    *out = p;
+    return QMM_OK;
+  }
+  if (!warm || !warm_launch || !warm_rows || count < 0 || count > 3)
+    return fail(QMM_ERR_INVALID, "L2 warming takes 0..3 weights with their launches and rows per wave");
+  int launch = -1, first = 0;
+  long long total = 0;
+  int start = 0;
+  for (int i = 0; i <= count; ++i) {
+    // close the previous launch: every job of it gets the launch's wave count
+    if (i == count || (i > 0 && warm_launch[i] != warm_launch[i - 1])) {
+      const long long wgs = std::min<long long>((total + 15) / 16, d->num_cu);
+      for (int j = start; j < i; ++j) p.grid_waves[j] = (int)(wgs * 16);
+      start = i;
+      total = 0;
+      first = 0;
+      if (i == count) break;
+    }
+    const qmm_qtensor* w = warm[i];
+    if (!w || fmt_of(w->dtype) == kFmtQ80) return fail(QMM_ERR_INVALID, "L2 warming takes Q4_K / Q6_K weights");
+    if (warm_launch[i] < launch || warm_launch[i] < 0) return fail(QMM_ERR_INVALID, "warm_launch must not decrease");
+    launch = warm_launch[i];
+    const int rpw = warm_rows[launch];
+    if (rpw < 0 || rpw > 64) return fail(QMM_ERR_INVALID, "rows per wave to warm: 0..64");
+    p.w[i] = w->data;
+    p.row_bytes[i] = (unsigned)((w->k / 256) * (fmt_of(w->dtype) == kFmtQ4K ? 144 : 208));
+    p.rows[i] = (int)w->n;
+    p.first[i] = first;
+    p.kmax[i] = rpw;
+    first += (int)w->n;
+    total += w->n;
+  }
+  p.njobs = count;
+  *out = p;
+  return QMM_OK;
+}
+
 size_t qmm_decode_attention_workspace_size(int heads, int kv_heads, int head_dim, int max_seq) {
   if (check_attention(heads, kv_heads, head_dim, max_seq) != QMM_OK) return 0;
   return attn_counter_bytes(kv_heads) + (size_t)kAttnSplits * heads * (head_dim + 2) * sizeof(float);
@@ -1517,12 +1570,16 @@ size_t qmm_decode_attention_workspace_size(int heads, int kv_heads, int head_dim
 
 static int attention(const float* q, const float* k, const float* v, const float* cos_t, const float* sin_t,
                      const int32_t* pos, float* kcache, float* vcache, float* out, int heads, int kv_heads,
-                     int head_dim, int max_seq, float scale, void* ws, size_t ws_bytes, void* stream) {
+                     int head_dim, int max_seq, float scale, void* ws, size_t ws_bytes, void* stream,
+                     const qmm_qtensor* const* warm = nullptr, const int* warm_launch = nullptr, int warm_count = 0,
+                     const int* warm_rows = nullptr) {
   QMM_TRY(check_attention(heads, kv_heads, head_dim, max_seq));
   const size_t need = qmm_decode_attention_workspace_size(heads, kv_heads, head_dim, max_seq);
   if (!ws || ws_bytes < need) return fail(QMM_ERR_INVALID, "attention workspace of %zu B < %zu B", ws_bytes, need);
   Device* d;
   QMM_TRY(current_device(&d));
+  WarmPlan wp;
+  QMM_TRY(warm_plan(d, warm, warm_launch, warm_count, warm_rows, &wp));
   unsigned* counters = (unsigned*)ws;
   float* part = (float*)((uint8_t*)ws + attn_counter_bytes(kv_heads));
   const int G = heads / kv_heads;
@@ -1532,11 +1589,27 @@ static int attention(const float* q, const float* k, const float* v, const float
   const int splits = kAttnSplits, nw = gt * head_dim <= 512 ? 8 : 4;
   char name[64];
   snprintf(name, sizeof(name), "qmm_decode_attention_d%d_g%d_w%d", head_dim / 64, gt, nw);
+  int pf_nw = 16, pf_njobs = wp.njobs;
   void* args[] = {&q, &k, &v, &cos_t, &sin_t, &pos, &kcache, &vcache, &part, &counters, &out,
-                  &heads, &kv_heads, &max_seq, &scale};
+                  &heads, &kv_heads, &max_seq, &scale,
+                  &wp.w[0], &wp.row_bytes[0], &wp.rows[0], &wp.first[0], &wp.grid_waves[0], &wp.kmax[0],
+                  &wp.w[1], &wp.row_bytes[1], &wp.rows[1], &wp.first[1], &wp.grid_waves[1], &wp.kmax[1],
+                  &wp.w[2], &wp.row_bytes[2], &wp.rows[2], &wp.first[2], &wp.grid_waves[2], &wp.kmax[2],
+                  &pf_njobs, &pf_nw};
+  // warming workgroups in grid rows past the attention's (kv_heads * splits of
+  // them, a multiple of 8): as many as the CUs the attention leaves free (the
+  // kernel's registers hold one of its workgroups per CU), in whole rows of
+  // kv_heads and a multiple of 8 in all, so that warming workgroup j and the
+  // consuming workgroups j, j + nwarm, ... share an XCD
+  int gy = splits;
+  if (wp.njobs > 0) {
+    int rows_y = std::max(1, (d->num_cu - kv_heads * splits) / kv_heads);
+    while (rows_y > 1 && (rows_y * kv_heads) % 8) --rows_y;
+    if ((rows_y * kv_heads) % 8 == 0) gy += rows_y;
+  }
   hipFunction_t f;
   QMM_TRY(kernel(d, name, &f));
-  QMM_HIP(hipModuleLaunchKernel(f, (unsigned)kv_heads, (unsigned)splits, 1, (unsigned)(64 * nw), 1, 1, 0,
+  QMM_HIP(hipModuleLaunchKernel(f, (unsigned)kv_heads, (unsigned)gy, 1, (unsigned)(64 * nw), 1, 1, 0,
                                 (hipStream_t)stream, args, nullptr));
   return QMM_OK;
 }
@@ -1557,6 +1630,17 @@ int qmm_decode_rope_attention(const float* q, const float* k, const float* v, co
     return fail(QMM_ERR_INVALID, "null pointer");
   return attention(q, k, v, cos_t, sin_t, pos, kcache, vcache, out, heads, kv_heads, head_dim, max_seq, scale, ws,
                    ws_bytes, stream);
+}
+
+int qmm_decode_rope_attention_warm(const float* q, const float* k, const float* v, const float* cos_t,
+                                   const float* sin_t, const int32_t* pos, float* kcache, float* vcache, float* out,
+                                   int heads, int kv_heads, int head_dim, int max_seq, float scale, void* ws,
+                                   size_t ws_bytes, const qmm_qtensor* const* warm, const int* warm_launch,
+                                   int warm_count, const int* warm_rows, void* stream) {
+  if (!q || !k || !v || !cos_t || !sin_t || !pos || !kcache || !vcache || !out)
+    return fail(QMM_ERR_INVALID, "null pointer");
+  return attention(q, k, v, cos_t, sin_t, pos, kcache, vcache, out, heads, kv_heads, head_dim, max_seq, scale, ws,
+                   ws_bytes, stream, warm, warm_launch, warm_count, warm_rows);
 }
 
 // ---------------------------------------------------------------------------

@@ -216,7 +216,10 @@ class LlamaWeights:
 class DecodeSession:
     """Device state and the launch sequence of one token step."""
 
-    def __init__(self, weights: LlamaWeights, max_seq: int):
+    def __init__(self, weights: LlamaWeights, max_seq: int, warm_gate_up_rows: int = 3, warm: bool = True):
+        """`warm`: the attention launch also loads the o projection's rows and the first
+        `warm_gate_up_rows` gate/up rows of every wave of the following launches into the L2 of the XCD
+        that reads them (qmm_decode_rope_attention_warm; the results are the same either way)."""
         cfg = weights.cfg
         self.cfg, self.w, self.max_seq = cfg, weights, max_seq
         dev = weights.embed.device
@@ -276,6 +279,11 @@ class DecodeSession:
         self._head = arr(vp, [weights.head.handle.value])
         self._lg_y = arr(vp, [self.logits.data_ptr()])
         self._lg_ld = arr(i64, [cfg.vocab])
+        ci = ctypes.c_int
+        self._warm = [arr(vp, [lw["o"].handle.value, lw["gate"].handle.value, lw["up"].handle.value])
+                      for lw in weights.layers] if warm else None
+        self._warm_launch = arr(ci, [0, 1, 1])
+        self._warm_rows = arr(ci, [1, int(warm_gate_up_rows)])
 
     # -- one token step --------------------------------------------------
     def step(self, trace: Optional[Callable[[str, int], None]] = None):
@@ -302,11 +310,20 @@ class DecodeSession:
             tr("qkv", li)
             kc = self.kcache.data_ptr() + 4 * li * kv_stride
             vc = self.vcache.data_ptr() + 4 * li * kv_stride
-            qmm._check(L.qmm_decode_rope_attention(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
-                                                   self.cos.data_ptr(), self.sin.data_ptr(),
-                                                   self.pos.data_ptr(), kc, vc, self.attn.data_ptr(), cfg.heads,
-                                                   cfg.kv_heads, hd, self.max_seq, ctypes.c_float(self.scale),
-                                                   self.ws_attn.data_ptr(), self.ws_attn.numel(), s))
+            if self._warm is not None:
+                # the o / gate / up launches' first rows are loaded into L2 during the attention
+                qmm._check(L.qmm_decode_rope_attention_warm(
+                    self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.cos.data_ptr(),
+                    self.sin.data_ptr(), self.pos.data_ptr(), kc, vc, self.attn.data_ptr(), cfg.heads,
+                    cfg.kv_heads, hd, self.max_seq, ctypes.c_float(self.scale), self.ws_attn.data_ptr(),
+                    self.ws_attn.numel(), self._warm[li], self._warm_launch, 3, self._warm_rows, s))
+            else:
+                qmm._check(L.qmm_decode_rope_attention(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                                                       self.cos.data_ptr(), self.sin.data_ptr(),
+                                                       self.pos.data_ptr(), kc, vc, self.attn.data_ptr(),
+                                                       cfg.heads, cfg.kv_heads, hd, self.max_seq,
+                                                       ctypes.c_float(self.scale), self.ws_attn.data_ptr(),
+                                                       self.ws_attn.numel(), s))
             tr("attention", li)
             qmm._check(L.qmm_matmul_ex(self._o[li], 1, self.attn.data_ptr(), 1, cfg.heads * hd, None, eps, 1,
                                        self._x_y, self._x_ld, None, 0, s))

@@ -61,6 +61,7 @@ EXPORTS = (
     "qmm_gguf_load_qtensor", "qmm_qtensor_dequantize_to", "qmm_embed_rows_n", "qmm_rope_kv_append_n",
     "qmm_prefill_attention", "qmm_silu_mul", "qmm_matmul_q_workspace_size", "qmm_matmul_noalloc",
     "qmm_stream_read", "qmm_reload_tuning", "qmm_moe_route_ex", "qmm_moe_ffn_ex_workspace_size", "qmm_moe_ffn_ex",
+    "qmm_decode_rope_attention_warm",
 )
 
 
@@ -126,6 +127,8 @@ def lib() -> ctypes.CDLL:
             "qmm_decode_attention": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp, sz, vp], i32),
             "qmm_decode_rope_attention": ([vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float,
                                            vp, sz, vp], i32),
+            "qmm_decode_rope_attention_warm": ([vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32,
+                                                ctypes.c_float, vp, sz, vp, vp, i32, vp, vp], i32),
             "qmm_decode_attention_workspace_size": ([i32, i32, i32, i32], sz),
             "qmm_greedy_workspace_size": ([i64], sz),
             "qmm_silu_mul_quantize": ([vp, vp, i64, i64, i64, vp, vp], i32),

@@ -496,3 +496,49 @@ def test_matmul_ex_gemm_norm_planes_equal_two_launches(dt, m, k):
     xn = torch.empty((m, k), device=DEV)
     qmm._check(L().qmm_rms_norm(x.data_ptr(), m, k, k, nw.data_ptr(), ctypes.c_float(1e-5), xn.data_ptr(), k, S()))
     assert torch.equal(fused, mm(xn, False))
+
+
+def test_rope_attention_with_l2_warming_equals_plain():
+    """qmm_decode_rope_attention_warm (extra workgroups load the following launches' first weight rows into
+    L2) writes the same bits as qmm_decode_rope_attention: output and both caches; bad warm plans are refused."""
+    heads, kv_heads, hd, max_seq, p = 32, 8, 128, 512, 300
+    rng = np.random.default_rng(77)
+    cfg = LlamaConfig(heads=heads, kv_heads=kv_heads, head_dim=hd)
+    cos, sin = rope_tables(cfg, max_seq)
+    kc = rng.standard_normal((kv_heads, max_seq, hd)).astype(np.float32)
+    vc = rng.standard_normal((kv_heads, max_seq, hd)).astype(np.float32)
+    q = rng.standard_normal((heads, hd)).astype(np.float32)
+    k = rng.standard_normal((kv_heads, hd)).astype(np.float32)
+    v = rng.standard_normal((kv_heads, hd)).astype(np.float32)
+    g = torch.Generator(device=DEV).manual_seed(78)
+    wo = QTensor.quantize(torch.randn((4096, 4096), generator=g, device=DEV) * 0.02, GgmlDType.Q4K)
+    wg = QTensor.quantize(torch.randn((14336, 4096), generator=g, device=DEV) * 0.02, GgmlDType.Q4K)
+    wu = QTensor.quantize(torch.randn((14336, 4096), generator=g, device=DEV) * 0.02, GgmlDType.Q4K)
+    scale = ctypes.c_float(float(np.float32(hd) ** np.float32(-0.5)))
+    outs = []
+    for warm in (False, True):
+        kcd, vcd = t(kc), t(vc)
+        out = torch.full((heads, hd), float("nan"), device=DEV)
+        ws = attn_ws(heads, kv_heads, hd, max_seq)
+        args = (t(q).data_ptr(), t(k).data_ptr(), t(v).data_ptr(), t(cos).data_ptr(), t(sin).data_ptr(),
+                t(np.array([p], np.int32), torch.int32).data_ptr(), kcd.data_ptr(), vcd.data_ptr(), out.data_ptr(),
+                heads, kv_heads, hd, max_seq, scale, ws.data_ptr(), ws.numel())
+        if warm:
+            W = (ctypes.c_void_p * 3)(wo.handle.value, wg.handle.value, wu.handle.value)
+            qmm._check(L().qmm_decode_rope_attention_warm(*args, W, (ctypes.c_int * 3)(0, 1, 1), 3,
+                                                          (ctypes.c_int * 2)(1, 3), S()))
+            # refused: more than three weights, a decreasing launch index, a Q8_0 weight
+            assert L().qmm_decode_rope_attention_warm(*args, W, (ctypes.c_int * 3)(0, 1, 1), 4,
+                                                      (ctypes.c_int * 2)(1, 3), S()) != 0
+            assert L().qmm_decode_rope_attention_warm(*args, W, (ctypes.c_int * 3)(1, 0, 0), 3,
+                                                      (ctypes.c_int * 2)(1, 3), S()) != 0
+            w8 = QTensor.quantize(torch.zeros((256, 4096), device=DEV), GgmlDType.Q8_0)
+            assert L().qmm_decode_rope_attention_warm(*args, (ctypes.c_void_p * 1)(w8.handle.value),
+                                                      (ctypes.c_int * 1)(0), 1, (ctypes.c_int * 1)(1), S()) != 0
+        else:
+            qmm._check(L().qmm_decode_rope_attention(*args, S()))
+        torch.cuda.synchronize()
+        outs.append((out.cpu().numpy(), kcd.cpu().numpy(), vcd.cpu().numpy()))
+    for a, b in zip(outs[0], outs[1]):
+        np.testing.assert_array_equal(a, b)
+    assert np.isfinite(outs[0][0]).all()
