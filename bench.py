@@ -181,7 +181,19 @@ def run_gemv_set(torch, dev, args):
         qkvgu(layer, True)
         down_fused(layer)
 
-    step = {"serial": step_serial, "staged": step_staged, "fused": step_fused}[args.schedule]
+    # grouped: the six GEMVs as one launch (qmm_matmul_grouped): q/k/v/gate/up on the 4096-wide row,
+    # down on the 14336-wide row, each row quantized to Q8_K in the prologue of its workgroups
+    grp_w = [(vp * 6)(*([layer[nm].handle.value for nm in QKVGU] + [layer["down_proj"].handle.value]))
+             for layer in sets]
+    grp_g = (ctypes.c_int * 6)(0, 0, 0, 0, 0, 1)
+    grp_x = (vp * 2)(x4096.data_ptr(), x14336.data_ptr())
+    grp_y = (vp * 6)(*([outs[nm].data_ptr() for nm in QKVGU] + [outs["down_proj"].data_ptr()]))
+
+    def step_grouped(layer):
+        qmm._check(L.qmm_matmul_grouped(grp_w[cidx[id(layer)]], grp_g, 6, grp_x, grp_y, qmm._stream(dev)))
+
+    step = {"serial": step_serial, "staged": step_staged, "fused": step_fused,
+            "grouped": step_grouped}[args.schedule]
 
     # warm up eagerly (module load, kernel lookup), then capture graphs
     for c in range(copies):
@@ -266,7 +278,13 @@ def run_gemv_set(torch, dev, args):
         torch.cuda.empty_cache()
 
     # dominant launch of the step
-    if args.schedule == "serial":
+    if args.schedule == "grouped":
+        # the step is this one launch: algorithmic bytes of the six GEMVs, each activation row read once
+        rsp = time_launch(step_grouped)
+        rb = step_bytes - 4 * 4096 * (len(QKVGU) - 1)
+        kernel = "qmm_gemv1g_q4k_w16 (q, k, v, gate, up on one row and down on another: one launch, Q8_K in the " \
+                 "prologue)"
+    elif args.schedule == "serial":
         kernel, rb = "qmm_gemv1_q4k_w4 (gate_proj 14336x4096, one launch)", gemv_bytes(dt, 14336, 4096)
         rsp = time_launch(lambda layer: gemv(layer, "gate_proj"))
     else:
@@ -729,6 +747,23 @@ def kernel_only(torch, dev, which, launches):
     x = torch.randn(4096, device=dev)
     xq = torch.zeros(16 * 292, dtype=torch.uint8, device=dev)
     qmm._check(L.qmm_quantize_rows(15, x.data_ptr(), 1, 4096, 4096, xq.data_ptr(), qmm._stream(dev)))
+    if which == "grouped":
+        # the config-2 set as one qmm_matmul_grouped launch, over rotated copies
+        nc = 6
+        sets = [[QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
+                 for _, n, k in GEMV_SET] for _ in range(nc)]
+        x14 = torch.randn(14336, device=dev)
+        ys = [torch.empty(n, dtype=torch.float32, device=dev) for _, n, _ in GEMV_SET]
+        hs = [(vp * 6)(*[t.handle.value for t in c]) for c in sets]
+        gp = (ctypes.c_int * 6)(0, 0, 0, 0, 0, 1)
+        xp = (vp * 2)(x.data_ptr(), x14.data_ptr())
+        yp = (vp * 6)(*[y.data_ptr() for y in ys])
+        for i in range(launches):
+            qmm._check(L.qmm_matmul_grouped(hs[i % nc], gp, 6, xp, yp, qmm._stream(dev)))
+        alg = sum(gemv_bytes(12, n, k) for _, n, k in GEMV_SET) - 4 * 4096 * 4
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel_only": which, "algorithmic_bytes": alg, "launches": launches}), flush=True)
+        return
     if which == "gate":
         ws = [QTensor.quantize(torch.randn((14336, 4096), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
               for _ in range(8)]
@@ -758,7 +793,7 @@ def kernel_only(torch, dev, which, launches):
 
 
 PMC_PROFILES = {"serial": "gemv_q4k_gate_pmc.json", "staged": "gemv_q4k_qkvgu_staged_pmc.json",
-                "fused": "gemv_q4k_qkvgu_fused_pmc.json"}
+                "fused": "gemv_q4k_qkvgu_fused_pmc.json", "grouped": "gemv_q4k_grouped_set_pmc.json"}
 
 
 def traffic_from_profile(schedule):
@@ -779,12 +814,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=24)
     ap.add_argument("--rotate-mb", type=int, default=640, help="distinct weight bytes rotated (MiB)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 = skip)")
-    ap.add_argument("--schedule", choices=("fused", "staged", "serial"), default="staged",
-                    help="staged: quantize x (Q8_K), q/k/v/gate/up in one launch, quantize, down; fused: the "
-                         "same two GEMV launches with Q8_K quantization in their prologues; serial: one launch "
-                         "per projection")
+    ap.add_argument("--schedule", choices=("grouped", "fused", "staged", "serial"), default="grouped",
+                    help="grouped: the six GEMVs in one launch (q/k/v/gate/up on one row, down on the other, "
+                         "Q8_K quantization in the prologue); staged: quantize x (Q8_K), q/k/v/gate/up in one "
+                         "launch, quantize, down; fused: the same two GEMV launches with Q8_K quantization in "
+                         "their prologues; serial: one launch per projection")
     ap.add_argument("--decode-tokens", type=int, default=256, help="config-3 generated tokens (0 = skip)")
-    ap.add_argument("--kernel-only", choices=("gate", "qkvgu", "qkvgu_staged", "copy", "gemm_gate", "gemm_down", "moe",
+    ap.add_argument("--kernel-only", choices=("gate", "qkvgu", "qkvgu_staged", "grouped", "copy", "gemm_gate",
+                                              "gemm_down", "moe",
                                               "q8_0", "down_q6k", "decode", "read_9mb", "read_33mb",
                                               "read_80mb", "read_1gb", "read_graph"),
                     default=None,

@@ -203,6 +203,20 @@ int qmm_matmul_q_ex(const qmm_qtensor *w, const void *xq, int64_t m, float *y, i
 int qmm_block_dots(const qmm_qtensor *w, const void *xq, int64_t m, float *y, int64_t ldy,
                    int32_t *dots, void *ws, size_t ws_bytes, void *stream);
 
+/* Several QMatMul::forward calls at m = 1 on two independent input rows, in
+ * one launch: weight w[i] (count 1..16, all Q4_K or all Q6_K, at most eight
+ * per group, k <= 16384) multiplies the f32 row x[group[i]] (group 0 or 1;
+ * the row's length is the k of that group's weights) into y[i] (w[i]->n
+ * floats). Each group's row is quantized to Q8_K in the launch's prologue
+ * as QMatMul::forward quantizes it, and every output equals qmm_matmul's on
+ * that weight and row bit for bit. The launch's CUs are split between the
+ * groups by their weight bytes, so independent GEMVs (e.g. one decoder
+ * layer's projections of two different rows) stream with one ramp-up and one
+ * drain instead of one per launch. No counterpart in the reference (its
+ * launcher takes one weight). */
+int qmm_matmul_grouped(const qmm_qtensor *const *w, const int *group, int count, const float *const *x,
+                       float *const *y, void *stream);
+
 /* QMatMul::forward for 1..8 weights (same k; one dtype, or Q4_K and Q6_K
  * together as for qmm_matmul_multi_q, e.g. a Q4_K_M layer's q, k and v) on
  * one input, with the decoder's neighbouring ops folded in: when norm_weight

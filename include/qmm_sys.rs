@@ -212,6 +212,13 @@ extern "C" {
     /// is added to y (the residual add of llama.rs:958-975). ws: device scratch of
     /// qmm_matmul_ex_workspace_size(w[j], m, norm_weight != NULL) bytes, the
     /// largest over the weights (m > 2 runs one pass per dtype).
+    /// Several `QMatMul::forward` calls at m = 1 on two independent rows in one launch (results equal
+    /// `qmm_matmul` on each weight bit for bit).
+    pub fn qmm_matmul_grouped(
+        w: *const *const QmmQTensor, group: *const c_int, count: c_int, x: *const *const f32,
+        y: *const *mut f32, stream: *mut c_void
+    ) -> c_int;
+
     pub fn qmm_matmul_ex(
         w: *const *const QmmQTensor, count: c_int, x: *const f32, m: i64, ldx: i64, norm_weight: *const f32,
         eps: f32, accumulate: c_int, y: *const *mut f32, ldy: *const i64, ws: *mut c_void, ws_bytes: usize,

@@ -15,6 +15,7 @@ from .qmm import (  # noqa: F401
     QuantizedLinear,
     QuantSpec,
     block_dots,
+    matmul_grouped,
     matmul_multi,
     moe_ffn,
     moe_route,

@@ -70,10 +70,12 @@ __device__ __forceinline__ void stage1_store(const Stage1& r, int nb, uint8_t* l
 // P = prefetch depth (slices in flight per wave). A Q4_K slice is 12 VGPRs,
 // a Q6_K slice 21; with 16 waves per CU a wave has 128.
 // NW = waves per workgroup (the launch's block size, as a constant).
+// ja_in / wg / ngrid: a group of a grouped launch, as for gemv1.
 template <int FMT, int P, bool FUSED, int J, bool SILU = false, bool MIX = false, int NW = 16>
 __device__ __forceinline__ void gemv1p(const GemvJobs& jobs, const void* __restrict__ act, int K,
                                        const float* __restrict__ norm_w, float eps, int accumulate,
-                                       int mix_row = 0x7fffffff) {
+                                       int mix_row = 0x7fffffff, const JobArg* ja_in = nullptr, int wg = -1,
+                                       int ngrid = 0) {
   static_assert(FMT != kFmtQ80, "k-quant weights");
   static_assert(!MIX || FMT == kFmtQ4K, "mixed launches: Q4_K rows, then Q6_K rows");
   constexpr int F6 = kFmtQ6K;
@@ -85,9 +87,9 @@ __device__ __forceinline__ void gemv1p(const GemvJobs& jobs, const void* __restr
   constexpr int nw = NW;
   const int l = lane & 3;
   const int g = lane >> 2;
-  const int row_step = gridDim.x * nw;
+  const int row_step = (ngrid > 0 ? ngrid : (int)gridDim.x) * nw;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int row0 = blockIdx.x * nw + wave;
+  const int row0 = (wg >= 0 ? wg : (int)blockIdx.x) * nw + wave;
   const int nrows = row0 < jobs.total ? (jobs.total - 1 - row0) / row_step + 1 : 0;
   const int nslices = nrows * niter;
   uint8_t* lds6 = lds + (MIX ? kQ8KBytes * nb : 0);  // Q6_K layout (MIX)
@@ -104,7 +106,7 @@ __device__ __forceinline__ void gemv1p(const GemvJobs& jobs, const void* __restr
   }
 
   // 2. the first P slices (issue side: slice is_s = row is_k, iteration is_it)
-  const JobArg* ja = job_args();
+  const JobArg* ja = ja_in != nullptr ? ja_in : job_args();
   JobCursor jc;
   cursor_init(jc, ja);
   int is_s = 0, is_k = 0, is_it = 0;
@@ -232,6 +234,51 @@ __device__ __forceinline__ void gemv1p(const GemvJobs& jobs, const void* __restr
     QMM_GEMV_JOBS8                                                                                            \
     qmm::gemv1p<qmm::kFmtQ4K, P, true, 8, false, true>(jobs, act, K, norm_w, eps, accumulate, mix_row);       \
   }
+
+// Grouped launches (see QMM_GEMV1G_KERNEL): a group whose rows are several
+// slices long (e.g. the down projection's K = 14336) runs the prefetch ring
+// of depth PB, the other gemv1's one-row loop. PA / PB = 0: gemv1.
+namespace qmm {
+template <int FMT, int PP>
+__device__ __forceinline__ void gemv1_group(const GemvJobs& jobs, const float* __restrict__ act, int K,
+                                            int accumulate, const JobArg* ja, int wg, int ngrid) {
+  if constexpr (PP == 0)
+    gemv1<FMT, true, 8, false, false, 16>(jobs, act, 0, K, nullptr, 0.0f, accumulate, 0x7fffffff, ja, wg, ngrid);
+  else
+    gemv1p<FMT, PP, true, 8, false, false, 16>(jobs, act, K, nullptr, 0.0f, accumulate, 0x7fffffff, ja, wg, ngrid);
+}
+}  // namespace qmm
+#define QMM_GEMV1G_RING_KERNEL(FMT, NAME, PA, PB)                                                                \
+  extern "C" __global__ void __launch_bounds__(1024) qmm_gemv1g_##NAME##_w16_p##PA##_p##PB(                      \
+      QMM_JOB_PARAMS(0), QMM_JOB_PARAMS(1), QMM_JOB_PARAMS(2), QMM_JOB_PARAMS(3), QMM_JOB_PARAMS(4),            \
+      QMM_JOB_PARAMS(5), QMM_JOB_PARAMS(6), QMM_JOB_PARAMS(7), QMM_JOB_PARAMS(8), QMM_JOB_PARAMS(9),            \
+      QMM_JOB_PARAMS(10), QMM_JOB_PARAMS(11), QMM_JOB_PARAMS(12), QMM_JOB_PARAMS(13), QMM_JOB_PARAMS(14),       \
+      QMM_JOB_PARAMS(15), int njobs_a, int total_a, int njobs_b, int total_b, const float* __restrict__ act_a,   \
+      const float* __restrict__ act_b, int k_a, int k_b, int ga, int accumulate) {                               \
+    qmm::GemvJobs jobs;                                                                                          \
+    if ((int)blockIdx.x < ga) {                                                                                  \
+      QMM_JOB_SET_AS(jobs, 0, 0) QMM_JOB_SET_AS(jobs, 1, 1) QMM_JOB_SET_AS(jobs, 2, 2) QMM_JOB_SET_AS(jobs, 3, 3) \
+      QMM_JOB_SET_AS(jobs, 4, 4) QMM_JOB_SET_AS(jobs, 5, 5) QMM_JOB_SET_AS(jobs, 6, 6) QMM_JOB_SET_AS(jobs, 7, 7) \
+      jobs.njobs = njobs_a;                                                                                      \
+      jobs.total = total_a;                                                                                      \
+      qmm::gemv1_group<FMT, PA>(jobs, act_a, k_a, accumulate, qmm::job_args(), (int)blockIdx.x, ga);            \
+    } else {                                                                                                     \
+      QMM_JOB_SET_AS(jobs, 0, 8) QMM_JOB_SET_AS(jobs, 1, 9) QMM_JOB_SET_AS(jobs, 2, 10)                          \
+      QMM_JOB_SET_AS(jobs, 3, 11) QMM_JOB_SET_AS(jobs, 4, 12) QMM_JOB_SET_AS(jobs, 5, 13)                        \
+      QMM_JOB_SET_AS(jobs, 6, 14) QMM_JOB_SET_AS(jobs, 7, 15)                                                    \
+      jobs.njobs = njobs_b;                                                                                      \
+      jobs.total = total_b;                                                                                      \
+      qmm::gemv1_group<FMT, PB>(jobs, act_b, k_b, accumulate, qmm::job_args() + 8, (int)blockIdx.x - ga,        \
+                                (int)gridDim.x - ga);                                                            \
+    }                                                                                                            \
+  }
+QMM_GEMV1G_RING_KERNEL(qmm::kFmtQ4K, q4k, 0, 2)
+QMM_GEMV1G_RING_KERNEL(qmm::kFmtQ4K, q4k, 0, 4)
+QMM_GEMV1G_RING_KERNEL(qmm::kFmtQ4K, q4k, 1, 4)
+QMM_GEMV1G_RING_KERNEL(qmm::kFmtQ4K, q4k, 2, 4)
+QMM_GEMV1G_RING_KERNEL(qmm::kFmtQ4K, q4k, 4, 4)
+QMM_GEMV1G_RING_KERNEL(qmm::kFmtQ6K, q6k, 0, 2)
+QMM_GEMV1G_RING_KERNEL(qmm::kFmtQ6K, q6k, 0, 3)
 
 QMM_GEMV1P_KERNELS(qmm::kFmtQ4K, q4k, 1)
 QMM_GEMV1P_KERNELS(qmm::kFmtQ4K, q4k, 2)

@@ -1013,10 +1013,14 @@ __device__ __forceinline__ void gemv1_rows(const GemvJobs& jobs, JobCursor& jc, 
 // MIX (FMT = Q4_K): global rows >= mix_row belong to Q6_K jobs (the host
 // orders the jobs Q4_K first); the activation is staged in both layouts and
 // a wave runs its Q4_K rows, then its Q6_K rows.
+// A grouped launch (qmm_gemv1g_*) runs several of these in one grid: ja_in
+// is then the group's job records, wg its workgroup's index within the group
+// and ngrid the group's workgroup count (defaults: the whole launch).
 template <int FMT, bool FUSED, int J, bool SILU = false, bool MIX = false, int NW = 0>
 __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restrict__ act, long long ldx, int K,
                                       const float* __restrict__ norm_w, float eps, int accumulate,
-                                      int mix_row = 0x7fffffff) {
+                                      int mix_row = 0x7fffffff, const JobArg* ja_in = nullptr, int wg = -1,
+                                      int ngrid = 0) {
   static_assert(!MIX || FMT == kFmtQ4K, "mixed launches: Q4_K rows, then Q6_K rows");
   constexpr int F6 = kFmtQ6K;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -1026,13 +1030,13 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
   const int nw = block_waves<NW>();
   const int l = lane % LPB;
   const int g = lane / LPB;
-  const int row_step = gridDim.x * nw;
+  const int row_step = (ngrid > 0 ? ngrid : (int)gridDim.x) * nw;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  int row = blockIdx.x * nw + wave;
+  int row = (wg >= 0 ? wg : (int)blockIdx.x) * nw + wave;
   uint8_t* lds6 = lds + (MIX ? kQ8KBytes * nb : 0);  // Q6_K layout (MIX)
   const int end4 = MIX ? min(mix_row, jobs.total) : jobs.total;
 
-  const JobArg* ja = job_args();
+  const JobArg* ja = ja_in != nullptr ? ja_in : job_args();
   JobCursor jc;
   cursor_init(jc, ja);
   WSlice ws, wn;
@@ -1253,7 +1257,51 @@ __device__ __forceinline__ void gemv1(const GemvJobs& jobs, const void* __restri
   QMM_GEMVF_SHAPES(FMT, NAME, 2)  \
   QMM_GEMV1_SHAPES(FMT, NAME)
 
+// Grouped one-row launch: two groups of up to eight jobs, each group with its
+// own f32 activation row (length K of its jobs), quantized to Q8_K in the
+// prologue of the group's workgroups. Workgroups [0, ga) serve group A, the
+// rest group B; inside a group the rows are dealt as in gemv1. The job
+// records of group A are the first eight of the argument segment, group B's
+// the next eight. Independent GEMVs of one decoder layer's shapes (the q / k /
+// v / gate / up projections of one row and the down projection of another)
+// then stream as one launch, with one ramp-up and one drain.
+#define QMM_JOB_SET_AS(dst, i, src) \
+  dst.wq[i] = wq##src;              \
+  dst.y[i] = y##src;                \
+  dst.rows[i] = rows##src;          \
+  dst.ldy[i] = ldy##src;            \
+  dst.row0[i] = row0##src;          \
+  dst.trows[i] = trows##src;
+#define QMM_GEMV1G_KERNEL(FMT, NAME, W)                                                                          \
+  extern "C" __global__ void __launch_bounds__(64 * W) qmm_gemv1g_##NAME##_w##W(                                \
+      QMM_JOB_PARAMS(0), QMM_JOB_PARAMS(1), QMM_JOB_PARAMS(2), QMM_JOB_PARAMS(3), QMM_JOB_PARAMS(4),            \
+      QMM_JOB_PARAMS(5), QMM_JOB_PARAMS(6), QMM_JOB_PARAMS(7), QMM_JOB_PARAMS(8), QMM_JOB_PARAMS(9),            \
+      QMM_JOB_PARAMS(10), QMM_JOB_PARAMS(11), QMM_JOB_PARAMS(12), QMM_JOB_PARAMS(13), QMM_JOB_PARAMS(14),       \
+      QMM_JOB_PARAMS(15), int njobs_a, int total_a, int njobs_b, int total_b, const float* __restrict__ act_a,   \
+      const float* __restrict__ act_b, int k_a, int k_b, int ga, int accumulate) {                               \
+    qmm::GemvJobs jobs;                                                                                          \
+    const bool in_a = (int)blockIdx.x < ga;                                                                      \
+    if (in_a) {                                                                                                  \
+      QMM_JOB_SET_AS(jobs, 0, 0) QMM_JOB_SET_AS(jobs, 1, 1) QMM_JOB_SET_AS(jobs, 2, 2) QMM_JOB_SET_AS(jobs, 3, 3) \
+      QMM_JOB_SET_AS(jobs, 4, 4) QMM_JOB_SET_AS(jobs, 5, 5) QMM_JOB_SET_AS(jobs, 6, 6) QMM_JOB_SET_AS(jobs, 7, 7) \
+      jobs.njobs = njobs_a;                                                                                      \
+      jobs.total = total_a;                                                                                      \
+      qmm::gemv1<FMT, true, 8, false, false, W>(jobs, act_a, 0, k_a, nullptr, 0.0f, accumulate, 0x7fffffff,     \
+                                                qmm::job_args(), (int)blockIdx.x, ga);                           \
+    } else {                                                                                                     \
+      QMM_JOB_SET_AS(jobs, 0, 8) QMM_JOB_SET_AS(jobs, 1, 9) QMM_JOB_SET_AS(jobs, 2, 10)                          \
+      QMM_JOB_SET_AS(jobs, 3, 11) QMM_JOB_SET_AS(jobs, 4, 12) QMM_JOB_SET_AS(jobs, 5, 13)                        \
+      QMM_JOB_SET_AS(jobs, 6, 14) QMM_JOB_SET_AS(jobs, 7, 15)                                                    \
+      jobs.njobs = njobs_b;                                                                                      \
+      jobs.total = total_b;                                                                                      \
+      qmm::gemv1<FMT, true, 8, false, false, W>(jobs, act_b, 0, k_b, nullptr, 0.0f, accumulate, 0x7fffffff,     \
+                                                qmm::job_args() + 8, (int)blockIdx.x - ga, (int)gridDim.x - ga); \
+    }                                                                                                            \
+  }
+
 QMM_GEMV_ALL_M(qmm::kFmtQ4K, q4k)
+QMM_GEMV1G_KERNEL(qmm::kFmtQ4K, q4k, 16)
+QMM_GEMV1G_KERNEL(qmm::kFmtQ6K, q6k, 16)
 QMM_GEMV_ALL_M(qmm::kFmtQ6K, q6k)
 QMM_GEMV_ALL_M(qmm::kFmtQ80, q8_0)
 QMM_GEMV1_MIX_KERNELS(4)

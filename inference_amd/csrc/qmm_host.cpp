@@ -99,12 +99,13 @@ std::atomic<Device*> g_dev[64] = {};
 //   where they are used.
 enum EnvKey {
   kEnvGemv1, kEnvGemv1p, kEnvGemvCfg, kEnvGemvWavesPerCu, kEnvGemvRows, kEnvSplitK, kEnvMmq2, kEnvMmq,
-  kEnvMmq4Bn, kEnvMmq1, kEnvMmqXcd, kEnvMoeGemv, kEnvMoeMmq, kEnvMoeBm, kEnvMoeSplitK, kEnvMoeGrouped, kEnvCount
+  kEnvMmq4Bn, kEnvMmq1, kEnvMmqXcd, kEnvMoeGemv, kEnvMoeMmq, kEnvMoeBm, kEnvMoeSplitK, kEnvMoeGrouped, kEnvGroupedP,
+  kEnvGroupedWgs, kEnvCount
 };
 const char* const kEnvNames[kEnvCount] = {
     "QMM_GEMV1", "QMM_GEMV1P", "QMM_GEMV_CFG", "QMM_GEMV_WAVES_PER_CU", "QMM_GEMV_ROWS", "QMM_SPLITK",
     "QMM_MMQ2", "QMM_MMQ", "QMM_MMQ4_BN", "QMM_MMQ1", "QMM_MMQ_XCD", "QMM_MOE_GEMV", "QMM_MOE_MMQ",
-    "QMM_MOE_BM", "QMM_MOE_SPLITK", "QMM_MOE_GROUPED"};
+    "QMM_MOE_BM", "QMM_MOE_SPLITK", "QMM_MOE_GROUPED", "QMM_GROUPED_P", "QMM_GROUPED_WGS"};
 
 struct Tuning {
   int w = 0, r = 0, u = 0, waves_per_cu = 0, gemv1 = 1, gemv1p = -1;
@@ -1160,6 +1161,109 @@ int qmm_matmul_multi(const qmm_qtensor* const* w, int count, const float* x, int
     t[j] = {w[j], y[j], ldy[j]};
   }
   return matmul_targets(t, count, x, m, ldx, ws, ws_bytes, stream);
+}
+
+// Two groups of one-row GEMVs in one launch (qmm_gemv1g_*): one 16-wave
+// workgroup per CU, split between the groups so that the largest per-wave
+// share of weight bytes is smallest (rows are dealt to a group's waves as in
+// gemv1: a wave of a group of G workgroups takes ceil(rows / (16 G)) rows at
+// most). At the config-2 set (q/k/v/gate/up 34816 rows of 2304 B, down 4096
+// rows of 8064 B) that is 170 / 86 workgroups: at most 29,952 B per wave
+// against 27,700 B for a perfect split.
+int qmm_matmul_grouped(const qmm_qtensor* const* w, const int* group, int count, const float* const* x,
+                       float* const* y, void* stream) {
+  if (!w || !group || !x || !y || count < 1 || count > 16) return fail(QMM_ERR_INVALID, "1..16 weights with groups");
+  int njobs[2] = {0, 0};
+  long long total[2] = {0, 0};
+  int64_t kg[2] = {0, 0};
+  const int dtype = w[0] ? w[0]->dtype : -1;
+  const int fmt = fmt_of(dtype);
+  if (fmt != kFmtQ4K && fmt != kFmtQ6K) return fail(QMM_ERR_UNSUPPORTED, "grouped GEMV: Q4_K or Q6_K weights");
+  GemvJobs jobs[2] = {};
+  for (int i = 0; i < count; ++i) {
+    const int gi = group[i];
+    if (!w[i] || !y[i] || (gi != 0 && gi != 1)) return fail(QMM_ERR_INVALID, "weight %d: null, or group not 0/1", i);
+    if (w[i]->dtype != dtype) return fail(QMM_ERR_INVALID, "grouped GEMV weights share one dtype");
+    if (kg[gi] == 0) kg[gi] = w[i]->k;
+    if (w[i]->k != kg[gi]) return fail(QMM_ERR_INVALID, "weights of one group share k");
+    if (njobs[gi] == kMaxJobs) return fail(QMM_ERR_INVALID, "at most %d weights per group", kMaxJobs);
+    const int j = njobs[gi]++;
+    jobs[gi].wq[j] = w[i]->data;
+    jobs[gi].y[j] = y[i];
+    jobs[gi].rows[j] = (int)w[i]->n;
+    jobs[gi].ldy[j] = (int)w[i]->n;
+    jobs[gi].row0[j] = 0;
+    jobs[gi].trows[j] = (int)w[i]->n;
+    total[gi] += w[i]->n;
+  }
+  for (int gi = 0; gi < 2; ++gi) {
+    if (njobs[gi] == 0) continue;
+    if (!x[gi]) return fail(QMM_ERR_INVALID, "null activation of group %d", gi);
+    if (total[gi] > (1LL << 31) - 1) return fail(QMM_ERR_INVALID, "too many rows in group %d", gi);
+    if (kg[gi] / 256 > 64) return fail(QMM_ERR_UNSUPPORTED, "grouped GEMV: k <= 16384");
+    jobs[gi].njobs = njobs[gi];
+    jobs[gi].total = (int)total[gi];
+  }
+  Device* d;
+  QMM_TRY(current_device(&d));
+  const unsigned lds = (unsigned)(std::max(kg[0], kg[1]) / 256 * 292);
+  if ((int)lds > d->max_lds) return fail(QMM_ERR_UNSUPPORTED, "activation needs %u B of LDS", lds);
+  int G = d->num_cu;
+  if (const char* e = env(kEnvGroupedWgs)) G = std::max(2, std::min(8, atoi(e))) * d->num_cu;
+  int ga = njobs[1] == 0 ? G : 0;
+  if (njobs[0] > 0 && njobs[1] > 0) {
+    const long long body = fmt == kFmtQ4K ? 144 : 208;
+    long long best = -1;
+    for (int a = 1; a < G; ++a) {
+      const long long ca = (total[0] + 16LL * a - 1) / (16LL * a) * (kg[0] / 256) * body;
+      const long long cb = (total[1] + 16LL * (G - a) - 1) / (16LL * (G - a)) * (kg[1] / 256) * body;
+      const long long c = std::max(ca, cb);
+      if (best < 0 || c < best) {
+        best = c;
+        ga = a;
+      }
+    }
+  }
+  const float* xa = x[0];
+  const float* xb = x[1];
+  int ka = (int)kg[0], kb = (int)kg[1], acc = 0;
+  void* args[16 * 6 + 10];
+  int na = 0;
+  for (int gi = 0; gi < 2; ++gi)
+    for (int j = 0; j < kMaxJobs; ++j) {
+      args[na++] = &jobs[gi].wq[j];
+      args[na++] = &jobs[gi].y[j];
+      args[na++] = &jobs[gi].rows[j];
+      args[na++] = &jobs[gi].ldy[j];
+      args[na++] = &jobs[gi].row0[j];
+      args[na++] = &jobs[gi].trows[j];
+    }
+  args[na++] = &jobs[0].njobs;
+  args[na++] = &jobs[0].total;
+  args[na++] = &jobs[1].njobs;
+  args[na++] = &jobs[1].total;
+  args[na++] = &xa;
+  args[na++] = &xb;
+  args[na++] = &ka;
+  args[na++] = &kb;
+  args[na++] = &ga;
+  args[na++] = &acc;
+  // a group of rows longer than one wave-wide slice (16 blocks) takes the
+  // prefetch ring for its rows (gemv1 would pay a round trip per slice);
+  // QMM_GROUPED_P="PA,PB" picks the depths (0: gemv1; instantiated: q4k 0/2,
+  // 0/4, 1/4, q6k 0/2, 0/3, and 0/0)
+  int pa = 0, pb = 0;
+  if (kg[1] / 256 > 16) pb = fmt == kFmtQ4K ? 4 : 2;
+  if (kg[0] / 256 > 16 && pb > 0) pa = fmt == kFmtQ4K ? 1 : 0;
+  if (const char* e = env(kEnvGroupedP)) {
+    if (sscanf(e, "%d,%d", &pa, &pb) != 2) pa = pb = 0;
+  }
+  char name[48];
+  if (pa == 0 && pb == 0)
+    snprintf(name, sizeof(name), "qmm_gemv1g_%s_w16", fmt_name(fmt));
+  else
+    snprintf(name, sizeof(name), "qmm_gemv1g_%s_w16_p%d_p%d", fmt_name(fmt), pa, pb);
+  return launch(d, name, (unsigned)G, 1024, lds, (hipStream_t)stream, args);
 }
 
 int qmm_matmul_ex(const qmm_qtensor* const* w, int count, const float* x, int64_t m, int64_t ldx,

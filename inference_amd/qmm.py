@@ -61,7 +61,7 @@ EXPORTS = (
     "qmm_gguf_load_qtensor", "qmm_qtensor_dequantize_to", "qmm_embed_rows_n", "qmm_rope_kv_append_n",
     "qmm_prefill_attention", "qmm_silu_mul", "qmm_matmul_q_workspace_size", "qmm_matmul_noalloc",
     "qmm_stream_read", "qmm_reload_tuning", "qmm_moe_route_ex", "qmm_moe_ffn_ex_workspace_size", "qmm_moe_ffn_ex",
-    "qmm_decode_rope_attention_warm",
+    "qmm_decode_rope_attention_warm", "qmm_matmul_grouped",
 )
 
 
@@ -127,6 +127,7 @@ def lib() -> ctypes.CDLL:
             "qmm_decode_attention": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float, vp, sz, vp], i32),
             "qmm_decode_rope_attention": ([vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, ctypes.c_float,
                                            vp, sz, vp], i32),
+            "qmm_matmul_grouped": ([vp, vp, i32, vp, vp, vp], i32),
             "qmm_decode_rope_attention_warm": ([vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32,
                                                 ctypes.c_float, vp, sz, vp, vp, i32, vp, vp], i32),
             "qmm_decode_attention_workspace_size": ([i32, i32, i32, i32], sz),
@@ -455,6 +456,31 @@ def matmul_multi(qts: Sequence[QTensor], x: torch.Tensor) -> Tuple[torch.Tensor,
         _check(L.qmm_matmul_multi(hs, len(qts), x2.data_ptr(), m, x2.stride(0), yp, ld, ws.data_ptr(),
                                   ws_bytes, _stream(x.device)))
     return tuple(y.reshape(*x.shape[:-1], y.shape[1]) for y in ys)
+
+
+def matmul_grouped(pairs: Sequence[Tuple[QTensor, int]], xs: Sequence[torch.Tensor],
+                   outs: Optional[Sequence[torch.Tensor]] = None) -> Tuple[torch.Tensor, ...]:
+    """QMatMul::forward of each (weight, group) pair on the single f32 row xs[group], all in one launch
+    (qmm_matmul_grouped: up to 8 weights per group, two groups, one k-quant dtype); same bits as one
+    QMatMul::forward per weight."""
+    if not 1 <= len(pairs) <= 16 or not 1 <= len(xs) <= 2:
+        raise QmmError(1, "matmul_grouped takes 1..16 weights over one or two rows")
+    rows = []
+    for x in xs:
+        if x.dtype != torch.float32 or x.numel() != x.shape[-1]:
+            raise QmmError(1, "matmul_grouped expects one float32 row per group")
+        rows.append(x.reshape(-1).contiguous())
+    dev = rows[0].device
+    ys = list(outs) if outs is not None else [torch.empty(q.shape[0], dtype=torch.float32, device=dev)
+                                              for q, _ in pairs]
+    L = lib()
+    hs = (ctypes.c_void_p * len(pairs))(*[q.handle.value for q, _ in pairs])
+    gp = (ctypes.c_int * len(pairs))(*[int(g) for _, g in pairs])
+    xp = (ctypes.c_void_p * 2)(*[r.data_ptr() for r in rows] + [None] * (2 - len(rows)))
+    yp = (ctypes.c_void_p * len(pairs))(*[y.data_ptr() for y in ys])
+    with torch.cuda.device(dev):
+        _check(L.qmm_matmul_grouped(hs, gp, len(pairs), xp, yp, _stream(dev)))
+    return tuple(ys)
 
 
 def q_workspace(qts: Sequence[QTensor], m: int) -> Tuple[Optional[torch.Tensor], int]:
