@@ -277,6 +277,45 @@ def run_gemv_set(torch, dev, args):
         del own, gph
         torch.cuda.empty_cache()
 
+    # the FFN pair as the decoder runs it (LlamaMlp's gate and up on one row): one launch over both
+    # weights with the RMSNorm + Q8_K of the f32 row in the prologue, rotated over the set copies
+    ffn_norm = torch.from_numpy(normal(4, (4096,))).to(dev)
+    hs_gu = [(vp * 2)(layer["gate_proj"].handle.value, layer["up_proj"].handle.value) for layer in sets]
+    y_gu = (vp * 2)(outs["gate_proj"].data_ptr(), outs["up_proj"].data_ptr())
+    ld_gu = (i64 * 2)(14336, 14336)
+
+    def gate_up_pair(layer):
+        qmm._check(L.qmm_matmul_ex(hs_gu[cidx[id(layer)]], 2, x4096.data_ptr(), 1, 4096, ffn_norm.data_ptr(),
+                                   ctypes.c_float(1e-5), 0, y_gu, ld_gu, None, 0, qmm._stream(dev)))
+    gate_up_pair(sets[0])
+    torch.cuda.synchronize()
+    sp = time_launch(gate_up_pair)
+    b = 2 * gemv_bytes(dt, 14336, 4096) - 4 * 4096 + 4 * 4096  # the row once, plus the norm weight
+    per_shape["gate_up_pair_rmsnorm"] = {"shape": [[14336, 4096], [14336, 4096]], "us": round(sp["mean"], 3),
+                                         "GB/s": round(b / sp["mean"] / 1e3, 1),
+                                         "frac": round(b / sp["mean"] / 1e3 / HBM_PEAK_GBS, 4),
+                                         "copies": copies, "us_spread": sp}
+
+    # small batches (the GEMV path serves m <= 8): gate_proj at m = 2, 4, 8 through qmm_matmul (Q8_K of the
+    # rows, then the multi-row GEMV), weights rotated over the set copies
+    small_m = {}
+    for m in (2, 4, 8):
+        xm = torch.from_numpy(normal(30 + m, (m, 4096))).to(dev)
+        ym = torch.empty((m, 14336), dtype=torch.float32, device=dev)
+        wsm = int(L.qmm_matmul_workspace_size(sets[0]["gate_proj"].handle, m))
+        wsbuf = torch.empty(max(wsm, 1), dtype=torch.uint8, device=dev)
+
+        def gate_m(layer, m=m, xm=xm, ym=ym, wsbuf=wsbuf, wsm=wsm):
+            qmm._check(L.qmm_matmul(layer["gate_proj"].handle, xm.data_ptr(), m, 4096, ym.data_ptr(), 14336,
+                                    wsbuf.data_ptr(), wsm, qmm._stream(dev)))
+        gate_m(sets[0])
+        torch.cuda.synchronize()
+        sp = time_launch(gate_m)
+        b = 14336 * 16 * 144 + m * 4 * (4096 + 14336)
+        small_m[f"m{m}"] = {"shape": [m, 14336, 4096], "us": round(sp["mean"], 3),
+                            "GB/s": round(b / sp["mean"] / 1e3, 1),
+                            "frac": round(b / sp["mean"] / 1e3 / HBM_PEAK_GBS, 4), "us_spread": sp}
+
     # dominant launch of the step
     if args.schedule == "grouped":
         # the step is this one launch: algorithmic bytes of the six GEMVs, each activation row read once
@@ -304,6 +343,7 @@ def run_gemv_set(torch, dev, args):
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(args.schedule),
                      "kernel": kernel, "avg_us": round(rus, 3), "us": rsp, "algorithmic_bytes": rb},
         "per_shape": per_shape,
+        "small_batch_gemv": small_m,
         "weight_copies": copies,
     }
     return result, sets
@@ -443,8 +483,13 @@ def run_prefill(torch, dev, cpu=None):
     g = torch.Generator(device=dev)
     g.manual_seed(6)
     out = {}
-    for name, n, k in (("gate_up_shape", 14336, 4096), ("down_shape", 4096, 14336)):
-        qt = QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
+    # config 4 proper (Q4_K), then the same shapes in Q6_K (the Q4_K_M down / v projections) and Q8_0 (the
+    # engine's Q8 projections)
+    legs = [(GgmlDType.Q4K, "gate_up_shape", 14336, 4096), (GgmlDType.Q4K, "down_shape", 4096, 14336),
+            (GgmlDType.Q6K, "q6k_gate_up_shape", 14336, 4096), (GgmlDType.Q6K, "q6k_down_shape", 4096, 14336),
+            (GgmlDType.Q8_0, "q8_0_gate_up_shape", 14336, 4096), (GgmlDType.Q8_0, "q8_0_down_shape", 4096, 14336)]
+    for dt, name, n, k in legs:
+        qt = QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, dt)
         x = torch.from_numpy(normal(5, (m, k))).to(dev)
         y = torch.empty((m, n), dtype=torch.float32, device=dev)
         wsb = int(L.qmm_matmul_workspace_size(qt.handle, m))
@@ -456,9 +501,9 @@ def run_prefill(torch, dev, cpu=None):
         sp = timed_graph(torch, fn, 4)
         us = sp["mean"]
         tops = 2.0 * m * n * k / us / 1e6
-        out[name] = {"m_n_k": [m, n, k], "us": round(us, 2), "TOPS": round(tops, 1),
+        out[name] = {"dtype": dt.name, "m_n_k": [m, n, k], "us": round(us, 2), "TOPS": round(tops, 1),
                      "mfma_util": round(tops / INT8_PEAK_TOPS, 4), "us_spread": sp}
-        if cpu is not None:
+        if cpu is not None and dt == GgmlDType.Q4K:
             from oracle import oracle as orc
             wq, xs = qt.to_ggml(), x[:CPU_PREFILL_ROWS].cpu().numpy()
             cpu[f"config4_{name}"] = cpu_leg(lambda impl: orc.matmul(orc.Q4K, xs, wq, k, CPU_THREADS, impl),
@@ -875,6 +920,7 @@ def main():
         "step_us": res["step_us"],
         "roofline": res["roofline"],
         "per_shape": res["per_shape"],
+        "small_batch_gemv": res["small_batch_gemv"],
         "q8_0_matvec": q80,
         "decode_tok_s": dec["tok_s"] if dec else None,
         "decode": dec,

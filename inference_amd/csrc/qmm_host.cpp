@@ -100,12 +100,13 @@ std::atomic<Device*> g_dev[64] = {};
 enum EnvKey {
   kEnvGemv1, kEnvGemv1p, kEnvGemvCfg, kEnvGemvWavesPerCu, kEnvGemvRows, kEnvSplitK, kEnvMmq2, kEnvMmq,
   kEnvMmq4Bn, kEnvMmq1, kEnvMmqXcd, kEnvMoeGemv, kEnvMoeMmq, kEnvMoeBm, kEnvMoeSplitK, kEnvMoeGrouped, kEnvGroupedP,
-  kEnvGroupedWgs, kEnvCount
+  kEnvGroupedWgs, kEnvStreamK, kEnvCount
 };
 const char* const kEnvNames[kEnvCount] = {
     "QMM_GEMV1", "QMM_GEMV1P", "QMM_GEMV_CFG", "QMM_GEMV_WAVES_PER_CU", "QMM_GEMV_ROWS", "QMM_SPLITK",
     "QMM_MMQ2", "QMM_MMQ", "QMM_MMQ4_BN", "QMM_MMQ1", "QMM_MMQ_XCD", "QMM_MOE_GEMV", "QMM_MOE_MMQ",
-    "QMM_MOE_BM", "QMM_MOE_SPLITK", "QMM_MOE_GROUPED", "QMM_GROUPED_P", "QMM_GROUPED_WGS"};
+    "QMM_MOE_BM", "QMM_MOE_SPLITK", "QMM_MOE_GROUPED", "QMM_GROUPED_P", "QMM_GROUPED_WGS",
+    "QMM_STREAMK"};
 
 struct Tuning {
   int w = 0, r = 0, u = 0, waves_per_cu = 0, gemv1 = 1, gemv1p = -1;
@@ -780,6 +781,8 @@ struct GemmPlan {
   char name[40];
   unsigned gx, gy, threads, lds;
   int splits, kc;  // K steps per split
+  int sk_tiles;    // > 0: the stream-K schedule (qmm_mmqs_q4k_sk) over a grid of gx workgroups
+  int tiles, mtiles;
 };
 
 // Split-K: a grid of fewer than half as many tiles as CUs (e.g. m = 127
@@ -822,8 +825,48 @@ static void plan_splits(const Device* d, GemmPlan& p, int nbk) {
   p.splits = (nbk + p.kc - 1) / p.kc;
 }
 
+// Stream-K (mmqs, one 512-thread workgroup per CU; opt-in, QMM_STREAMK=1):
+// a grid of T tiles that is not a whole number of rounds over the CUs
+// (config 4's gate 14336x4096 at M = 512: 448 tiles, 1.75 rounds, a quarter
+// of the CUs idle in the second) runs as floor rounds of data-parallel tiles
+// plus the rest as stream-K tiles whose (tile, K step) iterations are cut
+// into equal ranges, one per CU (qmm_mmqs_q4k_sk). The stream-K part is the
+// remainder r = T % G, or r + G when r tiles would give a CU fewer than
+// max(2, nbk / 2) K steps; a grid of fewer than G tiles is all stream-K
+// (in place of split-K). Below two K steps per CU the plain plan stays.
+// Measured at M = 512 it is no faster than the plain grid: the schedule
+// without its partial fixup takes 97.5 us at the gate shape against 105.9 us
+// for the plain 1.75 rounds, and the fixup's dependent store / counter /
+// load round trips at the end of the split tiles give the difference back
+// (106.0 us; the down shape 106.9 us against 106.4 us with split-K), so it is
+// not the default. A forced QMM_SPLITK also turns it off.
+static void plan_streamk(const Device* d, GemmPlan& p, int nbk) {
+  p.sk_tiles = 0;
+  p.tiles = (int)(p.gx * p.gy);
+  p.mtiles = (int)p.gy;
+  const char* e = env(kEnvStreamK);
+  if (e == nullptr || atoi(e) == 0 || env(kEnvSplitK) != nullptr) return;
+  const int G = d->num_cu, T = p.tiles;
+  if (G < 8 || G % 8 != 0 || T % G == 0) return;
+  int sk = T < G ? T : T % G;
+  if (T > G && (long long)sk * nbk < (long long)G * std::max(2, nbk / 2)) sk += G;
+  if ((long long)sk * nbk < 2LL * G) return;
+  p.sk_tiles = sk;
+  p.gx = (unsigned)G;
+  p.gy = 1;
+  p.splits = 1;
+  p.kc = nbk;
+}
+
+// Scratch of the stream-K schedule: the partial slots (two 128 x 128 f32
+// tiles per workgroup), then the stream-K tiles' counters.
+static size_t streamk_bytes(const GemmPlan& p) {
+  return p.sk_tiles > 0 ? align256((size_t)2 * p.gx * 128 * 128 * 4) + align256((size_t)p.sk_tiles * 4) : 0;
+}
+
 static GemmPlan gemm_plan(const Device* d, const qmm_qtensor* w, int64_t m, bool dump) {
   GemmPlan p;
+  p.sk_tiles = 0;
   const int fmt = fmt_of(w->dtype);
   const int M = (int)m, N = (int)w->n;
   // Q4_K: the second-generation kernel, 128x128 tiles (one workgroup of 512
@@ -878,29 +921,54 @@ static GemmPlan gemm_plan(const Device* d, const qmm_qtensor* w, int64_t m, bool
     p.threads = 256;
     p.lds = 0;
   }
-  plan_splits(d, p, (int)(w->k / 256));
+  p.tiles = (int)(p.gx * p.gy);
+  p.mtiles = (int)p.gy;
+  if (fmt == kFmtQ4K && gen == nullptr && !dump && p.threads == 512) plan_streamk(d, p, (int)(w->k / 256));
+  if (p.sk_tiles == 0) plan_splits(d, p, (int)(w->k / 256));
   return p;
 }
 
-// Bytes of f32 split partials a GEMM of w at m rows uses (0 without split-K).
+// Scratch bytes gemm() of w at m rows uses: f32 split partials, or the
+// stream-K schedule's partial slots and counters (0 for neither).
 static size_t gemm_split_bytes(const qmm_qtensor* w, int64_t m) {
   Device* d;
   if (current_device(&d) != QMM_OK) return 0;
   const GemmPlan p = gemm_plan(d, w, m, false);
+  if (p.sk_tiles > 0) return streamk_bytes(p);
   return p.splits > 1 ? align256((size_t)p.splits * (size_t)m * (size_t)w->n * 4) : 0;
+}
+
+// The stream-K scratch of w's plan at m rows (0 when it is not stream-K):
+// the callers that keep split partials of their own size it separately.
+static size_t gemm_sk_bytes(const Device* d, const qmm_qtensor* w, int64_t m) {
+  return streamk_bytes(gemm_plan(d, w, m, false));
 }
 
 // The GEMM kernel of plan p over activation planes at `ws` (see mmq_planes):
 // unsplit, into y (row stride ldy, accumulate as asked); split, the f32
 // partials [p.splits][m][n] into `part` and nothing summed.
 static int gemm_launch(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, const GemmPlan& p, float* y,
-                       int64_t ldy, int* dump, hipStream_t s, int accumulate, float* part) {
+                       int64_t ldy, int* dump, hipStream_t s, int accumulate, float* part, void* sk_scratch) {
   const Planes pl = mmq_planes(w->dtype, m, w->k);
   const bool split = p.splits > 1;
   const void* wq = w->data;
   const void* q8 = ws + pl.q8;
   const void* dd = ws + pl.d;
   const void* ss = ws + pl.s;
+  if (p.sk_tiles > 0) {
+    // stream-K: the counters cleared by a kernel (never a memset: callers capture this into graphs), then the
+    // GEMM into y
+    if (sk_scratch == nullptr) return fail(QMM_ERR_INVALID, "stream-K GEMM without scratch");
+    float* slots = (float*)sk_scratch;
+    unsigned* counters = (unsigned*)((uint8_t*)sk_scratch + align256((size_t)2 * p.gx * 128 * 128 * 4));
+    int nc = p.sk_tiles;
+    void* za[] = {&counters, &nc};
+    QMM_TRY(launch(d, "qmm_zero_u32", (unsigned)std::min(64, (nc + 255) / 256), 256, 0, s, za));
+    int M = (int)m, N = (int)w->n, K = (int)w->k, ld = (int)ldy, acc = accumulate;
+    int gy = p.mtiles, T = p.tiles, sk = p.sk_tiles;
+    void* args[] = {&wq, &q8, &dd, &ss, &y, &M, &N, &K, &ld, &acc, &gy, &T, &sk, &slots, &counters};
+    return launch(d, "qmm_mmqs_q4k_sk", p.gx, p.threads, p.lds, s, args);
+  }
   float* yy = split ? part : y;
   int M = (int)m, N = (int)w->n, K = (int)w->k, ld = split ? N : (int)ldy;
   int* dp = dump;
@@ -923,6 +991,13 @@ static int gemm_launch(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64
 static GemmPlan gemm_plan_fit(Device* d, const qmm_qtensor* w, int64_t m, bool dump, const float* part,
                               size_t part_bytes) {
   GemmPlan p = gemm_plan(d, w, m, dump);
+  if (p.sk_tiles > 0 && (part == nullptr || streamk_bytes(p) > part_bytes)) {
+    // no room for the stream-K scratch: the tile grid, split over K when that fits
+    p.sk_tiles = 0;
+    p.gx = (unsigned)((w->n + 127) / 128);
+    p.gy = (unsigned)((m + 127) / 128);
+    plan_splits(d, p, (int)(w->k / 256));
+  }
   const size_t need = (size_t)p.splits * (size_t)m * (size_t)w->n * 4;
   if (p.splits > 1 && (part == nullptr || need > part_bytes)) {
     p.splits = 1;
@@ -937,7 +1012,7 @@ static GemmPlan gemm_plan_fit(Device* d, const qmm_qtensor* w, int64_t m, bool d
 static int gemm(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, float* y, int64_t ldy, int* dump,
                 hipStream_t s, int accumulate, float* part, size_t part_bytes) {
   const GemmPlan p = gemm_plan_fit(d, w, m, dump != nullptr, part, part_bytes);
-  QMM_TRY(gemm_launch(d, w, ws, m, p, y, ldy, dump, s, accumulate, part));
+  QMM_TRY(gemm_launch(d, w, ws, m, p, y, ldy, dump, s, accumulate, part, part));
   if (p.splits > 1) {
     int M = (int)m, N = (int)w->n;
     const float* pp = part;
@@ -1360,8 +1435,8 @@ static FfnWs ffn_ws(Device* d, const qmm_qtensor* gate, const qmm_qtensor* up, c
     o += align256((size_t)w.usplits * (size_t)(m * F) * 4);
     w.hp = o;
     o += mmq_planes(down->dtype, m, F).total;
-    w.part = o;
-    o += gemm_split_bytes(down, m);
+    w.part = o;  // down's split partials or stream-K scratch, and gate's / up's stream-K scratch
+    o += std::max(gemm_split_bytes(down, m), std::max(gemm_sk_bytes(d, gate, m), gemm_sk_bytes(d, up, m)));
   } else {
     w.g = o;
     o += align256((size_t)(m * F) * 4);
@@ -1413,8 +1488,8 @@ int qmm_ffn(const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* d
   QMM_TRY(input_planes(d, gate->dtype, x, m, H, ldx, norm_weight, eps, b + L.xp, (float*)(b + L.xn), s));
   // gate and up, their split partials left unsummed
   const GemmPlan pg = gemm_plan(d, gate, m, false), pu = gemm_plan(d, up, m, false);
-  QMM_TRY(gemm_launch(d, gate, b + L.xp, m, pg, g, F, nullptr, s, 0, g));
-  QMM_TRY(gemm_launch(d, up, b + L.xp, m, pu, u, F, nullptr, s, 0, u));
+  QMM_TRY(gemm_launch(d, gate, b + L.xp, m, pg, g, F, nullptr, s, 0, g, b + L.part));
+  QMM_TRY(gemm_launch(d, up, b + L.xp, m, pu, u, F, nullptr, s, 0, u, b + L.part));
   // split sums, silu(g) * u and the down GEMM's Q8_K planes in one launch
   {
     const Planes ph = mmq_planes(down->dtype, m, F);
@@ -1479,6 +1554,8 @@ static QkvWs qkv_ws(Device* d, const qmm_qtensor* wq, const qmm_qtensor* wk, con
       *at[j] = o;
       o += align256((size_t)gemm_plan(d, ws3[j], m, false).splits * (size_t)(m * ws3[j]->n) * 4);
     }
+    w.mm = o;  // the stream-K scratch of q's, k's and v's GEMMs (one at a time)
+    o += std::max(gemm_sk_bytes(d, wq, m), std::max(gemm_sk_bytes(d, wk, m), gemm_sk_bytes(d, wv, m)));
   } else {
     w.k = o;
     o += align256((size_t)(m * wk->n) * 4);
@@ -1536,7 +1613,7 @@ int qmm_qkv_rope_kv_append_n(const qmm_qtensor* wq, const qmm_qtensor* wk, const
   for (int j = 0; j < 3; ++j) {
     const GemmPlan pj = gemm_plan(d, w3[j], m, false);
     sp[j] = pj.splits;
-    QMM_TRY(gemm_launch(d, w3[j], b + L.xp, m, pj, p3[j], w3[j]->n, nullptr, s, 0, p3[j]));
+    QMM_TRY(gemm_launch(d, w3[j], b + L.xp, m, pj, p3[j], w3[j]->n, nullptr, s, 0, p3[j], b + L.mm));
   }
   const float* qp = p3[0];
   const float* kp = p3[1];
