@@ -891,9 +891,10 @@ static GemmPlan gemm_plan(const Device* d, const qmm_qtensor* w, int64_t m, bool
   const long long tiles2 = (long long)((N + bn - 1) / bn) * ((M + bm - 1) / bm);
   const bool use4 = gen ? atoi(gen) == 4 : tiles2 * 2 < d->num_cu;
   // Q4_K default: mmqs (split-scale d term on int8 MFMA, mins term on bf16
-  // MFMA, 128 x 128 tiles of eight waves, two per SIMD, LDS 2 x 78.5 KB);
+  // MFMA, 128 x 128 tiles of eight waves, two per SIMD, LDS 2 x 72.5 KB);
   // QMM_MMQ=2 / 4 select the older generations
-  const unsigned ldss = 2u * (128 * 272 + 128 * 144 + 128 * 4 + 128 * 48 + 128 * 48 + 128 * 80 + (dump ? 128 * 16 : 0));
+  const unsigned ldss =
+      2u * (128 * 256 + 128 * 128 + 128 * 16 + 128 * 4 + 128 * 48 + 128 * 48 + 128 * 80 + (dump ? 128 * 16 : 0));
   if (fmt == kFmtQ4K && gen == nullptr && (int)ldss <= d->max_lds) {
     snprintf(p.name, sizeof(p.name), "qmm_mmqs_q4k%s", dump ? "_dump" : "");
     p.gx = (unsigned)((N + 127) / 128);

@@ -1074,16 +1074,19 @@ __device__ __forceinline__ void mmq4_q4k(const uint8_t* __restrict__ wq, const i
 //     four along N; a wave owns 64 rows (two M tiles) x 32 columns, so a
 //     column's operand products are formed once per K step for two tiles;
 //     the mins MFMAs and the d-term multiply-adds share one f32 accumulator;
-//   * staging: two LDS stages, the next step's global loads in registers
-//     while this step computes (a second register set, loads two steps
-//     ahead, measured no faster); consecutive lanes load
-//     consecutive 16-byte pieces (activation rows, weight quant bytes), so a
-//     wave's load touches few cache lines; threads 0..127 load column t's
-//     block header and form B' and the split-scale multipliers as packed
-//     16-bit pairs; threads 128..255 load row t - 128's scale and sums and
-//     form A' (waves 0, 1 and 2, 3: the staging arithmetic lands on all four
-//     SIMDs, wave w running on SIMD w % 4). A' / B' / multiplier rows sit at odd multiples of 16 bytes
-//     (conflict-free 16-byte access).
+//   * staging: two LDS stages; the next step's activation rows and weight
+//     quants go from global memory straight into the other stage
+//     (global_load_lds, 16 bytes a lane, 1 KB a wave instruction: no
+//     registers, no LDS store instructions) while this step computes. The
+//     rows (256 bytes) and the quant runs (128 bytes) are unpadded; 16-byte
+//     chunk c of row r sits at slot c ^ (r & 15), chunk k of column n at
+//     slot k ^ (n & 7), so the MFMA operand reads of 32 rows or columns at
+//     one chunk spread over all banks. Threads 0..127 load column t's block
+//     header and form B' and the split-scale multipliers as packed 16-bit
+//     pairs; threads 128..255 load row t - 128's scale and sums and form A'
+//     (waves 0, 1 and 2, 3: the staging arithmetic lands on all four SIMDs,
+//     wave w running on SIMD w % 4). A' / B' / multiplier rows sit at odd
+//     multiples of 16 bytes (conflict-free 16-byte access).
 // DUMP instantiations also compute ism exactly (two zero-padded int8 MFMAs)
 // and write the integer block dots, which equal mmq2's.
 // ---------------------------------------------------------------------------
@@ -1093,8 +1096,9 @@ constexpr int kSBM = 128, kSBN = 128;          // workgroup tile
 constexpr int kSThreads = 512;                 // eight waves: two along M, four along N
 constexpr int kSTM = 2;                        // M tiles (32 rows) per wave
 constexpr int kSHalf = 48;                     // A' / B' row: bf16 v1[8] | v2[8] | v3[8] (odd 16-byte stride)
-constexpr int kSOffB = kSBM * kM2AStride;      // LDS: weight blocks
-constexpr int kSOffDx = kSOffB + kSBN * kM2BStride;
+constexpr int kSOffBq = kSBM * 256;            // LDS: activation rows (swizzled chunks), then weight quants
+constexpr int kSOffHd = kSOffBq + kSBN * 128;  // block headers, 16 bytes per column
+constexpr int kSOffDx = kSOffHd + kSBN * 16;
 constexpr int kSOffAm = kSOffDx + kSBM * 4;    // A' rows
 constexpr int kSOffBm = kSOffAm + kSBM * kSHalf;  // B' columns
 constexpr int kSOffSc = kSOffBm + kSBN * kSHalf;  // per column: sl_j | sl_j << 16 (j < 8), then sh_j | sh_j << 16
@@ -1107,30 +1111,39 @@ struct SLayout {
 };
 
 struct SRegs {
-  uint4 a[kSBM * 16 / kSThreads];  // activation rows: 4 x 16 B per thread
-  uint4 q[2];                      // weight quants: pieces 1 + (idx & 7) of column idx >> 3, idx = t + 512 u
-  uint4 e;                         // t < 128: block header of column t; 128 <= t < 256: sums of row t - 128
-  float dx;                        // 128 <= t < 256: scale of row t - 128
+  uint4 e;   // t < 128: block header of column t; 128 <= t < 256: sums of row t - 128
+  float dx;  // 128 <= t < 256: scale of row t - 128
 };
 
-// Global loads of one K step. Consecutive lanes read consecutive 16-byte
-// pieces (an activation row's 256 bytes, a weight block's 128 quant bytes),
-// so a wave's load touches as few cache lines as the data allows; the block
-// headers (16 bytes at the blocks' stride) are read once each.
-__device__ __forceinline__ void s_load(SRegs& R, const int8_t* __restrict__ xq, const float* __restrict__ xd,
-                                       const int16_t* __restrict__ xs, const uint8_t* __restrict__ wq, int M, int N,
-                                       int K, int m0, int n0, int kb) {
-  const int t = threadIdx.x, nbk = K / 256;
+// 16 bytes per lane from `src` into LDS at dst + 16 * lane (dst wave-uniform).
+__device__ __forceinline__ void lds_dma16(const void* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                   (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+}
+
+// Global loads of one K step. Wave w moves activation rows 16 w .. 16 w + 15
+// (four instructions of four rows) and the quants of weight columns
+// 16 w .. 16 w + 15 (two instructions of eight columns) straight into LDS
+// stage `stg`, a lane's 16 bytes at its swizzled slot; rows and columns past
+// M / N repeat the last one (their outputs are never stored). Threads 0..255
+// load the block headers / the rows' scales and sums into registers (zero
+// past the edges).
+__device__ __forceinline__ void s_load(SRegs& R, uint8_t* stg, const int8_t* __restrict__ xq,
+                                       const float* __restrict__ xd, const int16_t* __restrict__ xs,
+                                       const uint8_t* __restrict__ wq, int M, int N, int K, int m0, int n0, int kb) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nbk = K / 256;
 #pragma unroll
-  for (int u = 0; u < kSBM * 16 / kSThreads; ++u) {
-    const int idx = t + kSThreads * u, row = m0 + (idx >> 4);
-    R.a[u] = row < M ? reinterpret_cast<const uint4*>(xq + (size_t)row * K + 256 * kb)[idx & 15] : make_uint4(0, 0, 0, 0);
+  for (int u = 0; u < 4; ++u) {
+    const int row = 16 * wave + 4 * u + (lane >> 4);
+    const int gr = min(m0 + row, M - 1);
+    lds_dma16(xq + (size_t)gr * K + 256 * kb + 16 * ((lane & 15) ^ (row & 15)), stg + 256 * (16 * wave + 4 * u));
   }
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    const int idx = t + kSThreads * u, col = n0 + (idx >> 3);
-    R.q[u] = col < N ? reinterpret_cast<const uint4*>(wq + ((size_t)col * nbk + kb) * kQ4KBytes)[1 + (idx & 7)]
-                     : make_uint4(0, 0, 0, 0);
+    const int col = 16 * wave + 8 * u + (lane >> 3);
+    const int gc = min(n0 + col, N - 1);
+    lds_dma16(wq + ((size_t)gc * nbk + kb) * kQ4KBytes + 16 + 16 * ((lane & 7) ^ (col & 7)),
+              stg + kSOffBq + 128 * (16 * wave + 8 * u));
   }
   if (t < 128) {
     const int col = n0 + t;
@@ -1170,25 +1183,16 @@ __device__ __forceinline__ void s_store_row(uint8_t* dst, const float* v) {
   for (int k = 0; k < 3; ++k) o[k] = make_uint4(w[k][0], w[k][1], w[k][2], w[k][3]);
 }
 
+// The register-staged parts of one K step into LDS stage `buf`.
 template <bool DUMP>
 __device__ __forceinline__ void s_store(const SRegs& R, uint8_t* buf) {
   const int t = threadIdx.x;
-#pragma unroll
-  for (int u = 0; u < kSBM * 16 / kSThreads; ++u) {
-    const int idx = t + kSThreads * u;
-    *reinterpret_cast<uint4*>(buf + (idx >> 4) * kM2AStride + 16 * (idx & 15)) = R.a[u];
-  }
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int idx = t + kSThreads * u;
-    *reinterpret_cast<uint4*>(buf + kSOffB + (idx >> 3) * kM2BStride + 16 * (1 + (idx & 7))) = R.q[u];
-  }
   float row8[8];
   if (t < 128) {
     // column t's header; B' = -dmin * m_j; the split scales sl_j = sc_j & 7, sh_j = sc_j >> 3 as packed
     // 16-bit pairs (the multipliers of the weight operands)
     const uint4 hd = R.e;
-    *reinterpret_cast<uint4*>(buf + kSOffB + t * kM2BStride) = hd;
+    *reinterpret_cast<uint4*>(buf + kSOffHd + 16 * t) = hd;
     const float dmin = h2f(hd.x >> 16);
     const uint32_t mn[2] = {hd.z & 0x3f3f3f3fu, ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u)};
 #pragma unroll
@@ -1249,8 +1253,9 @@ __device__ __forceinline__ void mmqs_mfma(const uint8_t* __restrict__ buf, i32x1
 #pragma unroll
   for (int j = 0; j < 16; ++j) zero[j] = 0;
   const int arow0 = 64 * wm + r;
+  const int sa = r & 15, sb = r & 7;  // the swizzles of rows arow0 + 32 i and of column bcol
   const int8_t* A = reinterpret_cast<const int8_t*>(buf);
-  const uint8_t* Bc = buf + kSOffB + bcol * kM2BStride;
+  const uint8_t* Bq = buf + kSOffBq + 128 * bcol;
   const uint4* SC = reinterpret_cast<const uint4*>(buf + kSOffSc + kSScStride * bcol);
   const uint4 sl4[2] = {SC[0], SC[1]}, sh4[2] = {SC[2], SC[3]};
   auto pick = [](const uint4* v, int j) {
@@ -1259,7 +1264,7 @@ __device__ __forceinline__ void mmqs_mfma(const uint8_t* __restrict__ buf, i32x1
   };
 #pragma unroll
   for (int c2 = 0; c2 < 4; ++c2) {
-    const uint4 qv = *reinterpret_cast<const uint4*>(Bc + 16 + 32 * c2 + 16 * h);
+    const uint4 qv = *reinterpret_cast<const uint4*>(Bq + 16 * ((2 * c2 + h) ^ sb));
     const uint4 blo = make_uint4(qv.x & 0x0f0f0f0fu, qv.y & 0x0f0f0f0fu, qv.z & 0x0f0f0f0fu, qv.w & 0x0f0f0f0fu);
     const uint4 bhi = make_uint4((qv.x >> 4) & 0x0f0f0f0fu, (qv.y >> 4) & 0x0f0f0f0fu, (qv.z >> 4) & 0x0f0f0f0fu,
                                  (qv.w >> 4) & 0x0f0f0f0fu);
@@ -1270,9 +1275,9 @@ __device__ __forceinline__ void mmqs_mfma(const uint8_t* __restrict__ buf, i32x1
     i8x16 a0[kSTM], a1[kSTM];
 #pragma unroll
     for (int i = 0; i < kSTM; ++i) {
-      const int8_t* ar = A + (arow0 + 32 * i) * kM2AStride + 64 * c2 + 16 * h;
-      a0[i] = *reinterpret_cast<const i8x16*>(ar);
-      a1[i] = *reinterpret_cast<const i8x16*>(ar + 32);
+      const int8_t* ar = A + 256 * (arow0 + 32 * i);
+      a0[i] = *reinterpret_cast<const i8x16*>(ar + 16 * ((4 * c2 + h) ^ sa));
+      a1[i] = *reinterpret_cast<const i8x16*>(ar + 16 * ((4 * c2 + 2 + h) ^ sa));
     }
     // chains on one accumulator four MFMAs apart
 #pragma unroll
@@ -1295,7 +1300,7 @@ __device__ __forceinline__ void mmqs_epi(const uint8_t* __restrict__ buf, const 
                                          int bcol) {
   const int arow0 = 64 * wm + r;
   const float* DX = reinterpret_cast<const float*>(buf + kSOffDx);
-  const float dw = h2f(*reinterpret_cast<const uint32_t*>(buf + kSOffB + bcol * kM2BStride));
+  const float dw = h2f(*reinterpret_cast<const uint32_t*>(buf + kSOffHd + 16 * bcol));
   const uint8_t* bmp = buf + kSOffBm + kSHalf * bcol;
   const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(bmp);
   const bf16x8 b2 = *reinterpret_cast<const bf16x8*>(bmp + 16);
@@ -1337,7 +1342,7 @@ __device__ __forceinline__ void mmqs_step_dump(const uint8_t* __restrict__ buf, 
   mmqs_mfma(buf, accl, acch, wm, r, h, bcol);
   const int arow0 = 64 * wm + r;
   const float* DX = reinterpret_cast<const float*>(buf + kSOffDx);
-  const uint4 hd = *reinterpret_cast<const uint4*>(buf + kSOffB + bcol * kM2BStride);
+  const uint4 hd = *reinterpret_cast<const uint4*>(buf + kSOffHd + 16 * bcol);
   const float dw = h2f(hd.x), dmw = h2f(hd.x >> 16);
   const uint32_t mnlo = hd.z & 0x3f3f3f3fu, mnhi = ((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u);
   const uint4 zero4 = make_uint4(0, 0, 0, 0);
@@ -1385,23 +1390,26 @@ __device__ __forceinline__ void mmqs_run(const uint8_t* __restrict__ wq, const i
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[i][j] = 0.0f;
 
-  // the next K step's global loads are in registers while this step computes from LDS stage
-  // (kb - kb0) & 1
+  // the next K step streams into the other LDS stage (and its headers / scales into registers) while this
+  // step computes from stage (kb - kb0) & 1; each wave waits for its own LDS loads before the barrier
   SRegs R;
-  s_load(R, xq, xd, xs, wq, M, N, K, m0, n0, kb0);
+  s_load(R, lds, xq, xd, xs, wq, M, N, K, m0, n0, kb0);
   s_store<DUMP>(R, lds);
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
   __syncthreads();
   i32x16 accl[kSTM], acch[kSTM];
   for (int kb = kb0; kb < kb1; ++kb) {
     const uint8_t* cur = lds + ((kb - kb0) & 1) * Lay::kStage;
-    if (kb + 1 < kb1) s_load(R, xq, xd, xs, wq, M, N, K, m0, n0, kb + 1);
+    uint8_t* nxt = lds + ((kb + 1 - kb0) & 1) * Lay::kStage;
+    if (kb + 1 < kb1) s_load(R, nxt, xq, xd, xs, wq, M, N, K, m0, n0, kb + 1);
     if constexpr (DUMP) {
       mmqs_step_dump(cur, acc, wm, r, h, bcol, m0, col, M, N, nbk, kb, dump);
     } else {
       mmqs_mfma(cur, accl, acch, wm, r, h, bcol);
       mmqs_epi(cur, accl, acch, acc, wm, r, h, bcol);
     }
-    if (kb + 1 < kb1) s_store<DUMP>(R, lds + ((kb + 1 - kb0) & 1) * Lay::kStage);
+    if (kb + 1 < kb1) s_store<DUMP>(R, nxt);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     __syncthreads();
   }
 }
