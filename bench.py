@@ -89,21 +89,15 @@ def spread(us):
 
 
 def build_set(torch, dev, dt, copies):
-    """`copies` independent weight sets of GEMV_SET, quantized on the GPU."""
+    """`copies` independent weight sets of GEMV_SET, quantized on the GPU: weight i of copy c is
+    N(0, 0.02^2) from SplitMix64 seed 2 + 1000 c + 17 i (synth.normal_torch, on the device)."""
     from inference_amd import QTensor
-    from inference_amd.synth import normal
+    from inference_amd.synth import normal_torch
     sets = []
     for c in range(copies):
         layer = {}
         for i, (name, n, k) in enumerate(GEMV_SET):
-            w = normal(2 + 1000 * c + 17 * i, (n, k), 0.02) if c == 0 else None
-            if w is None:
-                # further copies: same distribution, distinct bytes, generated on device
-                g = torch.Generator(device=dev)
-                g.manual_seed(1000 * c + i)
-                wt = torch.randn((n, k), generator=g, device=dev) * 0.02
-            else:
-                wt = torch.from_numpy(w).to(dev)
+            wt = normal_torch(2 + 1000 * c + 17 * i, (n, k), 0.02, dev)
             layer[name] = QTensor.quantize(wt, dt)
             del wt
         sets.append(layer)
@@ -115,7 +109,7 @@ QKVGU = ("q_proj", "k_proj", "v_proj", "gate_proj", "up_proj")  # the K = 4096 p
 
 def run_gemv_set(torch, dev, args):
     from inference_amd import GgmlDType, QTensor, qmm
-    from inference_amd.synth import normal
+    from inference_amd.synth import normal, normal_torch
 
     dt = GgmlDType.Q4K
     vt = dt.vec_dot_type()
@@ -258,9 +252,8 @@ def run_gemv_set(torch, dev, args):
     for name, n, k in GEMV_SET:
         wb = n * (k // 256) * 144
         nc = max(2, -(-args.rotate_mb * 2 ** 20 // wb))
-        g = torch.Generator(device=dev)
-        g.manual_seed(7000 + n + k)
-        own = [{name: QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, dt)} for _ in range(nc)]
+        own = [{name: QTensor.quantize(normal_torch(7000 + n + k + 101 * c, (n, k), 0.02, dev), dt)}
+               for c in range(nc)]
         gph = torch.cuda.CUDAGraph()
         gemv(own[0], name)
         torch.cuda.synchronize()
@@ -354,18 +347,16 @@ def run_q8_0(torch, dev, args, cpu):
     N(0, 0.02^2) seed 0 (SplitMix64 + Box-Muller, quantized on the GPU, bit-identical to the CPU
     quantizer), activation 1x4096 N(0, 1) seed 1. One qmm_matmul call = one launch: the f32 row is
     quantized to Q8_0 in the GEMV's prologue. Copies beyond the first (same distribution, device
-    generator) are rotated over > 2x the MALL. The first copy's output is checked against the oracle."""
+    generator: SplitMix64 seeds 101, 102, ...) are rotated over > 2x the MALL. The first copy's output is
+    checked against the oracle."""
     from inference_amd import GgmlDType, QTensor, qmm
-    from inference_amd.synth import normal
+    from inference_amd.synth import normal, normal_torch
     L = qmm.lib()
     n = k = 4096
     wb = n * (k // 32) * 34
     copies = max(2, -(-args.rotate_mb * 2 ** 20 // wb))
-    g = torch.Generator(device=dev)
-    g.manual_seed(100)
     qts = [QTensor.quantize(torch.from_numpy(normal(0, (n, k), 0.02)).to(dev), GgmlDType.Q8_0)]
-    qts += [QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, GgmlDType.Q8_0)
-            for _ in range(copies - 1)]
+    qts += [QTensor.quantize(normal_torch(100 + c, (n, k), 0.02, dev), GgmlDType.Q8_0) for c in range(1, copies)]
     xh = normal(1, (1, k))
     x = torch.from_numpy(xh).to(dev)
     y = torch.empty((1, n), dtype=torch.float32, device=dev)
@@ -474,22 +465,21 @@ def timed_graph(torch, fn, per_graph, samples=SPREAD_SAMPLES):
 
 def run_prefill(torch, dev, cpu=None):
     """Config 4: M = 512 tokens x 4096 (N(0,1), seed 5) through Q4_K 14336x4096 and 4096x14336
-    (N(0, 0.02^2), seed 6, device generator). qmm_matmul: activation quantization to Q8_K planes +
-    the int8-MFMA GEMM. MFMA utilisation = 2*M*N*K / time / dense int8 peak."""
+    (N(0, 0.02^2), SplitMix64 seeds 6 and 16 on the device; the Q6_K and Q8_0 legs 26 .. 56).
+    qmm_matmul: activation quantization to Q8_K planes + the int8-MFMA GEMM. MFMA utilisation =
+    2*M*N*K / time / dense int8 peak."""
     from inference_amd import GgmlDType, QTensor, qmm
-    from inference_amd.synth import normal
+    from inference_amd.synth import normal, normal_torch
     L = qmm.lib()
     m = 512
-    g = torch.Generator(device=dev)
-    g.manual_seed(6)
     out = {}
     # config 4 proper (Q4_K), then the same shapes in Q6_K (the Q4_K_M down / v projections) and Q8_0 (the
     # engine's Q8 projections)
     legs = [(GgmlDType.Q4K, "gate_up_shape", 14336, 4096), (GgmlDType.Q4K, "down_shape", 4096, 14336),
             (GgmlDType.Q6K, "q6k_gate_up_shape", 14336, 4096), (GgmlDType.Q6K, "q6k_down_shape", 4096, 14336),
             (GgmlDType.Q8_0, "q8_0_gate_up_shape", 14336, 4096), (GgmlDType.Q8_0, "q8_0_down_shape", 4096, 14336)]
-    for dt, name, n, k in legs:
-        qt = QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, dt)
+    for li, (dt, name, n, k) in enumerate(legs):
+        qt = QTensor.quantize(normal_torch(6 + 10 * li, (n, k), 0.02, dev), dt)
         x = torch.from_numpy(normal(5, (m, k))).to(dev)
         y = torch.empty((m, n), dtype=torch.float32, device=dev)
         wsb = int(L.qmm_matmul_workspace_size(qt.handle, m))
@@ -514,19 +504,17 @@ def run_prefill(torch, dev, cpu=None):
 
 
 def run_moe(torch, dev):
-    """Config 5: 8 experts (Q4_K gate/up 14336x4096, Q6_K down 4096x14336, N(0, 0.02^2) seed 7 on the
-    device generator), 8 tokens N(0,1), router logits N(0,1) seed 8, top-2. One qmm_moe_ffn call:
+    """Config 5: 8 experts (Q4_K gate/up 14336x4096, Q6_K down 4096x14336, N(0, 0.02^2) from SplitMix64
+    seeds 71 / 72 / 73 on the device), 8 tokens N(0,1) seed 7, router logits N(0,1) seed 8, top-2. One qmm_moe_ffn call:
     routing, gathered Q8_K activations, expert GEMVs streaming each active expert once, SiLU*mul, combine.
     Then MoE prefill on the same experts (512 tokens through the grouped MFMA GEMMs)."""
     from inference_amd import GgmlDType, QTensor, qmm
-    from inference_amd.synth import normal
+    from inference_amd.synth import normal, normal_torch
     L = qmm.lib()
     E, H, F, T, k = 8, 4096, 14336, 8, 2
-    g = torch.Generator(device=dev)
-    g.manual_seed(7)
-    gate = QTensor.quantize(torch.randn((E * F, H), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
-    up = QTensor.quantize(torch.randn((E * F, H), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
-    down = QTensor.quantize(torch.randn((E * H, F), generator=g, device=dev) * 0.02, GgmlDType.Q6K)
+    gate = QTensor.quantize(normal_torch(71, (E * F, H), 0.02, dev), GgmlDType.Q4K)
+    up = QTensor.quantize(normal_torch(72, (E * F, H), 0.02, dev), GgmlDType.Q4K)
+    down = QTensor.quantize(normal_torch(73, (E * H, F), 0.02, dev), GgmlDType.Q6K)
     x = torch.from_numpy(normal(7, (T, H))).to(dev)
     logits_np = normal(8, (T, E))
     logits = torch.from_numpy(logits_np).to(dev)
@@ -652,7 +640,7 @@ def kernel_only(torch, dev, which, launches):
     `copy` = a 256 MiB device copy (the calibration for FETCH_SIZE / WRITE_SIZE); `gemm_gate` / `gemm_down` =
     the config-4 GEMMs (M = 512); `moe` = the config-5 expert FFN."""
     from inference_amd import GgmlDType, QTensor, qmm
-    from inference_amd.synth import normal
+    from inference_amd.synth import normal, normal_torch
     if which == "copy":
         a = torch.ones(64 * 2 ** 20, dtype=torch.float32, device=dev)
         b = torch.empty_like(a)
@@ -665,9 +653,7 @@ def kernel_only(torch, dev, which, launches):
     if which in ("gemm_gate", "gemm_down"):
         # config-4 GEMM: 512 rows N(0,1) seed 5 against a Q4_K weight N(0, 0.02^2) seed 6
         n, k = (14336, 4096) if which == "gemm_gate" else (4096, 14336)
-        g = torch.Generator(device=dev)
-        g.manual_seed(6)
-        w = QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
+        w = QTensor.quantize(normal_torch(6 if which == "gemm_gate" else 16, (n, k), 0.02, dev), GgmlDType.Q4K)
         x = torch.from_numpy(normal(5, (512, k))).to(dev)
         y = torch.empty((512, n), dtype=torch.float32, device=dev)
         L = qmm.lib()
@@ -682,11 +668,9 @@ def kernel_only(torch, dev, which, launches):
     if which == "moe":
         # config 5: one qmm_moe_ffn call per launch (route, gather, expert GEMVs, SiLU*mul, combine)
         E, H, F, T, k = 8, 4096, 14336, 8, 2
-        g = torch.Generator(device=dev)
-        g.manual_seed(7)
-        gate = QTensor.quantize(torch.randn((E * F, H), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
-        up = QTensor.quantize(torch.randn((E * F, H), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
-        down = QTensor.quantize(torch.randn((E * H, F), generator=g, device=dev) * 0.02, GgmlDType.Q6K)
+        gate = QTensor.quantize(normal_torch(71, (E * F, H), 0.02, dev), GgmlDType.Q4K)
+        up = QTensor.quantize(normal_torch(72, (E * F, H), 0.02, dev), GgmlDType.Q4K)
+        down = QTensor.quantize(normal_torch(73, (E * H, F), 0.02, dev), GgmlDType.Q6K)
         x = torch.from_numpy(normal(7, (T, H))).to(dev)
         lg = torch.from_numpy(normal(8, (T, E))).to(dev)
         y = torch.empty((T, H), dtype=torch.float32, device=dev)
@@ -760,12 +744,10 @@ def kernel_only(torch, dev, which, launches):
     if which in ("q8_0", "down_q6k"):
         # config 1: the Q8_0 4096x4096 matvec, one qmm_matmul (fused Q8_0 prologue) per launch; or the
         # decode step's Q6_K down projection 4096x14336 with a pre-quantized Q8_K row. Rotated copies.
-        g = torch.Generator(device=dev)
-        g.manual_seed(0)
         L = qmm.lib()
         dt, n, k = (GgmlDType.Q8_0, 4096, 4096) if which == "q8_0" else (GgmlDType.Q6K, 4096, 14336)
         nc = 38 if which == "q8_0" else 14
-        ws = [QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, dt) for _ in range(nc)]
+        ws = [QTensor.quantize(normal_torch(200 + c, (n, k), 0.02, dev), dt) for c in range(nc)]
         x = torch.randn(k, device=dev)
         y = torch.empty(n, dtype=torch.float32, device=dev)
         if which == "q8_0":
@@ -785,8 +767,6 @@ def kernel_only(torch, dev, which, launches):
         torch.cuda.synchronize()
         print(json.dumps({"kernel_only": which, "algorithmic_bytes": alg, "launches": launches}), flush=True)
         return
-    g = torch.Generator(device=dev)
-    g.manual_seed(2)
     L = qmm.lib()
     vp, i64 = ctypes.c_void_p, ctypes.c_int64
     x = torch.randn(4096, device=dev)
@@ -795,8 +775,8 @@ def kernel_only(torch, dev, which, launches):
     if which == "grouped":
         # the config-2 set as one qmm_matmul_grouped launch, over rotated copies
         nc = 6
-        sets = [[QTensor.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
-                 for _, n, k in GEMV_SET] for _ in range(nc)]
+        sets = [[QTensor.quantize(normal_torch(2 + 1000 * c + 17 * i, (n, k), 0.02, dev), GgmlDType.Q4K)
+                 for i, (_, n, k) in enumerate(GEMV_SET)] for c in range(nc)]
         x14 = torch.randn(14336, device=dev)
         ys = [torch.empty(n, dtype=torch.float32, device=dev) for _, n, _ in GEMV_SET]
         hs = [(vp * 6)(*[t.handle.value for t in c]) for c in sets]
@@ -810,8 +790,8 @@ def kernel_only(torch, dev, which, launches):
         print(json.dumps({"kernel_only": which, "algorithmic_bytes": alg, "launches": launches}), flush=True)
         return
     if which == "gate":
-        ws = [QTensor.quantize(torch.randn((14336, 4096), generator=g, device=dev) * 0.02, GgmlDType.Q4K)
-              for _ in range(8)]
+        ws = [QTensor.quantize(normal_torch(2 + 1000 * c + 17 * 3, (14336, 4096), 0.02, dev), GgmlDType.Q4K)
+              for c in range(8)]
         y = torch.empty(14336, dtype=torch.float32, device=dev)
         for i in range(launches):
             qmm._check(L.qmm_matmul_q(ws[i % 8].handle, xq.data_ptr(), 1, y.data_ptr(), 14336, None, 0,
@@ -820,8 +800,8 @@ def kernel_only(torch, dev, which, launches):
     else:
         names = [nm for nm, _, _ in GEMV_SET if nm != "down_proj"]
         shp = {nm: (n, k) for nm, n, k in GEMV_SET}
-        copies = [[QTensor.quantize(torch.randn(shp[nm], generator=g, device=dev) * 0.02, GgmlDType.Q4K)
-                   for nm in names] for _ in range(6)]
+        copies = [[QTensor.quantize(normal_torch(2 + 1000 * c + 17 * i, shp[nm], 0.02, dev), GgmlDType.Q4K)
+                   for i, nm in enumerate(names)] for c in range(6)]
         hs = [(vp * 5)(*[t.handle.value for t in c]) for c in copies]
         ys = [torch.empty(shp[nm][0], dtype=torch.float32, device=dev) for nm in names]
         yp = (vp * 5)(*[y.data_ptr() for y in ys])
@@ -914,7 +894,7 @@ def main():
         "dtype": "int8",
         "data": "synthetic",
         "config": {"workload": "q4k_decode_gemv_set_llama3_8b_m1", "shapes_out_in": [[n, k] for _, n, k in GEMV_SET],
-                   "batch_m": 1, "weights": "Q4_K, N(0,0.02^2) seed 2", "activations": "Q8_K on device, seed 3",
+                   "batch_m": 1, "weights": "Q4_K, N(0,0.02^2) SplitMix64 + Box-Muller, seed 2 + 1000 copy + 17 index", "activations": "Q8_K on device, seed 3",
                    "weight_copies_rotated": res["weight_copies"], "schedule": args.schedule},
         "hbm_frac": round(res["value"] / HBM_PEAK_GBS, 4),
         "step_us": res["step_us"],

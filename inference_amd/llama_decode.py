@@ -117,21 +117,24 @@ class LlamaWeights:
 
     @classmethod
     def random(cls, cfg: LlamaConfig, seed: int, device: torch.device, std: float = 0.02) -> "LlamaWeights":
-        """N(0, std^2) weights from a seeded device generator, quantized on the GPU; norms = 1."""
-        g = torch.Generator(device=device)
-        g.manual_seed(seed)
+        """N(0, std^2) weights, quantized on the GPU; norms = 1. Each tensor is SplitMix64 + Box-Muller
+        (synth.normal_torch, generated on the device, the same values as synth.normal on the host) with
+        its own seed: seed * 1000003 + 16 * layer + j for projection j of q, k, v, o, gate, up, down, then
+        16 * layers for the head and 16 * layers + 1 for the embedding."""
+        from .synth import normal_torch
         sh = cfg.shapes()
+        base = seed * 1000003
 
-        def q(name):
-            n, k = sh[name]
-            w = torch.randn((n, k), generator=g, device=device) * std
+        def q(name, s):
+            w = normal_torch(base + s, sh[name], std, device)
             t = QTensor.quantize(w, cfg.dtypes[name])
             del w
             return t
 
-        layers = [{name: q(name) for name in ("q", "k", "v", "o", "gate", "up", "down")} for _ in range(cfg.layers)]
-        head = q("head")
-        embed = torch.randn((cfg.vocab, cfg.hidden), generator=g, device=device) * std
+        names = ("q", "k", "v", "o", "gate", "up", "down")
+        layers = [{name: q(name, 16 * li + j) for j, name in enumerate(names)} for li in range(cfg.layers)]
+        head = q("head", 16 * cfg.layers)
+        embed = normal_torch(base + 16 * cfg.layers + 1, (cfg.vocab, cfg.hidden), std, device)
         ones = lambda: torch.ones(cfg.hidden, dtype=torch.float32, device=device)  # noqa: E731
         return cls(cfg, layers, head, embed, [ones() for _ in range(cfg.layers)],
                    [ones() for _ in range(cfg.layers)], ones())

@@ -42,3 +42,42 @@ def normal(seed: int, shape, std: float = 1.0, chunk: int = 1 << 24) -> np.ndarr
         hi = min(n, 2 * p1)
         out[lo:hi] = z[: hi - lo]
     return out.reshape(shape)
+
+
+def _i64(v: int) -> int:
+    """The int64 with the bits of the uint64 v."""
+    return v - (1 << 64) if v >= 1 << 63 else v
+
+
+def _srl(t, k: int):
+    """Logical right shift of an int64 tensor read as uint64."""
+    return (t >> k) & ((1 << (64 - k)) - 1)
+
+
+def normal_torch(seed: int, shape, std: float = 1.0, device=None, chunk: int = 1 << 25):
+    """normal() computed with torch on `device` (the large synthetic weights of configs 3-5, generated
+    where they are used): the same SplitMix64 stream in int64 arithmetic (multiplication wraps mod 2^64,
+    shifts are made logical), the same f64 Box-Muller, one rounding to f32. The values equal normal()'s
+    wherever the device's f64 log / sqrt / cos / sin round like the host's before that f32 rounding."""
+    import torch
+    n = int(np.prod(shape))
+    out = torch.empty(n, dtype=torch.float32, device=device)
+    gold, m1, m2 = _i64(int(_GOLDEN)), _i64(int(_M1)), _i64(int(_M2))
+    s = _i64(int(seed) & ((1 << 64) - 1))
+    pairs = (n + 1) // 2
+    for p0 in range(0, pairs, chunk):
+        p1 = min(pairs, p0 + chunk)
+        z = torch.arange(2 * p0 + 1, 2 * p1 + 1, dtype=torch.int64, device=device) * gold + s
+        z = (z ^ _srl(z, 30)) * m1
+        z = (z ^ _srl(z, 27)) * m2
+        z = z ^ _srl(z, 31)
+        z = _srl(z, 11).to(torch.float64)
+        u1 = (z[0::2] + 1.0) * (1.0 / 9007199254740992.0)
+        u2 = z[1::2] * (1.0 / 9007199254740992.0)
+        del z
+        rad = torch.sqrt(-2.0 * torch.log(u1)) * std
+        th = (2.0 * np.pi) * u2
+        v = torch.stack((rad * torch.cos(th), rad * torch.sin(th)), dim=1).reshape(-1)
+        lo, hi = 2 * p0, min(n, 2 * p1)
+        out[lo:hi] = v[: hi - lo].to(torch.float32)
+    return out.reshape(shape)
