@@ -364,7 +364,9 @@ class DecodeSession:
         att, g, u, h), so a checker can read them between launches. Without a trace the feed-forward
         block is one qmm_ffn call (gate / up split sums, SiLU and the down GEMM's quantization in one
         launch), which gives the same bits as those three traced launches; likewise q / k / v with RoPE
-        and the KV append are one qmm_qkv_rope_kv_append_n call."""
+        and the KV append are one qmm_qkv_rope_kv_append_n call. Without a trace the last layer also
+        stops after its K/V append: the rows' hidden states after it feed nothing (the step recomputes
+        the last prompt token's), so its attention, o and feed-forward block over the rows are skipped."""
         if self.prompt_len == 0 or self.steps_done != 0:
             raise qmm.QmmError(1, "prefill() needs the state reset() leaves")
         cfg, L, w = self.cfg, self.L, self.w
@@ -414,6 +416,8 @@ class DecodeSession:
                                                       rows, H, w.attn_norm[li].data_ptr(), eps, self.cos.data_ptr(),
                                                       self.sin.data_ptr(), 0, q.data_ptr(), nq, kc, vc, cfg.heads,
                                                       cfg.kv_heads, hd, self.max_seq, ws.data_ptr(), ws.numel(), s))
+                if li == cfg.layers - 1:
+                    break  # the last layer's K/V is all that the following steps read
             else:
                 qmm._check(L.qmm_matmul_ex(self._qkv[li], 3, x.data_ptr(), rows, H, w.attn_norm[li].data_ptr(), eps,
                                            0, qkv_y, qkv_ld, ws.data_ptr(), ws.numel(), s))
