@@ -1194,7 +1194,7 @@ static int matmul_targets(const GemvTarget* tg, int count, const float* x, int64
       void* dd = (uint8_t*)ws + pl.d;
       void* ss = (uint8_t*)ws + pl.s;
       void* args[] = {&x, &lx, &norm_w, &eps, &kk, &q8, &dd, &ss};
-      QMM_TRY(launch(d, "qmm_rms_norm_q8k_mmq", (unsigned)m, 256, (unsigned)(w->k * 4), s, args));
+      QMM_TRY(launch(d, "qmm_rms_norm_q8k_mmq", (unsigned)m, 1024, (unsigned)(w->k * 4), s, args));
     } else {
       QMM_TRY(quantize_planes(d, w->dtype, x, m, w->k, ldx, (uint8_t*)ws, s));
     }
@@ -1384,7 +1384,7 @@ static int input_planes(Device* d, int wdtype, const float* x, int64_t m, int64_
     void* dd = xp + px.d;
     void* ss = xp + px.s;
     void* args[] = {&x, &lx, &norm_weight, &eps, &kk, &q8, &dd, &ss};
-    return launch(d, "qmm_rms_norm_q8k_mmq", (unsigned)m, 256, (unsigned)(k * 4), s, args);
+    return launch(d, "qmm_rms_norm_q8k_mmq", (unsigned)m, 1024, (unsigned)(k * 4), s, args);
   }
   const float* xs = x;
   int64_t lx = ldx;

@@ -468,52 +468,51 @@ extern "C" __global__ void __launch_bounds__(256) qmm_quantize_q8k_mmq_rows(cons
   qmm::put_q8k_plane(qmm::q8k_lane(x + (long long)rows[row] * ldx + 256LL * b, lane), w, nb, k, q8, d, s, lane);
 }
 
-// The same planes for RMSNorm rows, x / sqrt(mean(x^2) + eps) * w: one
-// workgroup of 256 threads per row sums the squares exactly as qmm_rms_norm
-// does (thread t walks t, t + 256, ... eight loads at a time; waves in
-// order) and forms the same f32 values, stages them in LDS (k floats of
-// dynamic LDS) and each wave quantizes whole 256-element blocks: the planes
-// of quantizing qmm_rms_norm's output, without its f32 copy or a launch.
-extern "C" __global__ void __launch_bounds__(256) qmm_rms_norm_q8k_mmq(const float* __restrict__ x, long long ldx,
-                                                                       const float* __restrict__ w, float eps,
-                                                                       int k, int8_t* __restrict__ q8,
-                                                                       float* __restrict__ d,
-                                                                       int16_t* __restrict__ s) {
+// The same planes for RMSNorm rows, x / sqrt(mean(x^2) + eps) * w, with
+// qmm_rms_norm's values bit for bit: 1024 threads stage the row in LDS (k
+// floats of dynamic LDS; at k = 4096 one load per thread, all in flight at
+// once), then threads 0..255 form qmm_rms_norm's sum of squares in its order
+// (thread t over t, t + 256, ... in turn, wave_sum, the four wave sums in
+// order), every thread normalises its own elements, and each of the 16
+// waves quantizes whole 256-element blocks (one at k = 4096): the planes of
+// quantizing qmm_rms_norm's output, without its f32 copy or a launch.
+extern "C" __global__ void __launch_bounds__(1024) qmm_rms_norm_q8k_mmq(const float* __restrict__ x, long long ldx,
+                                                                        const float* __restrict__ w, float eps,
+                                                                        int k, int8_t* __restrict__ q8,
+                                                                        float* __restrict__ d,
+                                                                        int16_t* __restrict__ s) {
 #pragma clang fp contract(off)
-  constexpr int NT = 256, U = 8;
+  constexpr int NT = 1024, NS = 256;  // threads; the threads of qmm_rms_norm's sum
   extern __shared__ __attribute__((aligned(16))) float rowbuf[];
-  __shared__ float red[NT / 64];
+  __shared__ float red[NS / 64];
   const float* xr = x + blockIdx.x * ldx;
-  float ss = 0.0f;
-  for (int i0 = threadIdx.x; i0 < k; i0 += U * NT) {
-    float v[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = i0 + u * NT < k ? xr[i0 + u * NT] : 0.0f;
-#pragma unroll
-    for (int u = 0; u < U; ++u) ss += v[u] * v[u];
-  }
-  ss = qmm::wave_sum(ss);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  const int t = threadIdx.x;
+  for (int i0 = 4 * t; i0 < k; i0 += 4 * NT)  // k is a multiple of 256; rows need only 4-byte alignment
+    *reinterpret_cast<float4*>(rowbuf + i0) = make_float4(xr[i0], xr[i0 + 1], xr[i0 + 2], xr[i0 + 3]);
   __syncthreads();
-  float t = 0.0f;
-#pragma unroll
-  for (int i = 0; i < NT / 64; ++i) t += red[i];
-  const float den = sqrtf(t / (float)k + eps);
-  for (int i0 = threadIdx.x; i0 < k; i0 += U * NT) {
-    float v[U], g[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = i0 + u * NT;
-      v[u] = i < k ? xr[i] : 0.0f;
-      g[u] = i < k ? w[i] : 0.0f;
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (i0 + u * NT < k) rowbuf[i0 + u * NT] = v[u] / den * g[u];
+  if (t < NS) {
+    float ss = 0.0f;
+    for (int i = t; i < k; i += NS) ss += rowbuf[i] * rowbuf[i];
+    ss = qmm::wave_sum(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
   }
   __syncthreads();
-  const int nb = k / 256, lane = threadIdx.x & 63;
-  for (int b = threadIdx.x >> 6; b < nb; b += NT / 64) {
+  float tot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NS / 64; ++i) tot += red[i];
+  const float den = sqrtf(tot / (float)k + eps);
+  for (int i0 = 4 * t; i0 < k; i0 += 4 * NT) {
+    float4 v = *reinterpret_cast<const float4*>(rowbuf + i0);
+    const float4 g = make_float4(w[i0], w[i0 + 1], w[i0 + 2], w[i0 + 3]);
+    v.x = v.x / den * g.x;
+    v.y = v.y / den * g.y;
+    v.z = v.z / den * g.z;
+    v.w = v.w / den * g.w;
+    *reinterpret_cast<float4*>(rowbuf + i0) = v;
+  }
+  __syncthreads();
+  const int nb = k / 256, lane = t & 63;
+  for (int b = t >> 6; b < nb; b += NT / 64) {
     const float4 e = *reinterpret_cast<const float4*>(rowbuf + 256 * b + 4 * lane);
     qmm::put_q8k_plane(qmm::q8k_lane_vals(e.x, e.y, e.z, e.w, lane), (long long)blockIdx.x * nb + b, nb, k, q8, d, s,
                        lane);
