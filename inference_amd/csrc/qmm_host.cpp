@@ -1974,15 +1974,20 @@ int qmm_block_dots(const qmm_qtensor* w, const void* xq, int64_t m, float* y, in
 // mixture of experts
 // ---------------------------------------------------------------------------
 
+static int route_check(int64_t tokens, int experts, int topk, float routed_scaling_factor) {
+  if (tokens < 1 || tokens > 4096 || experts < 1 || experts > 256 || topk < 1 || topk > 8 || topk > experts ||
+      tokens * topk > 8192)
+    return fail(QMM_ERR_INVALID, "routing limits: 1 <= tokens <= 4096, tokens*topk <= 8192, topk <= min(8, experts)");
+  if (!(routed_scaling_factor == routed_scaling_factor)) return fail(QMM_ERR_INVALID, "routed scaling factor is NaN");
+  return QMM_OK;
+}
+
 int qmm_moe_route_ex(const float* logits, int64_t tokens, int experts, int topk, int renormalize,
                      float routed_scaling_factor, int32_t* counts, int32_t* offsets, int32_t* pair_token,
                      float* pair_weight, int32_t* token_pairs, void* stream) {
   if (!logits || !counts || !offsets || !pair_token || !pair_weight || !token_pairs)
     return fail(QMM_ERR_INVALID, "null pointer");
-  if (tokens < 1 || tokens > 4096 || experts < 1 || experts > 256 || topk < 1 || topk > 8 || topk > experts ||
-      tokens * topk > 8192)
-    return fail(QMM_ERR_INVALID, "routing limits: 1 <= tokens <= 4096, tokens*topk <= 8192, topk <= min(8, experts)");
-  if (!(routed_scaling_factor == routed_scaling_factor)) return fail(QMM_ERR_INVALID, "routed scaling factor is NaN");
+  QMM_TRY(route_check(tokens, experts, topk, routed_scaling_factor));
   Device* d;
   QMM_TRY(current_device(&d));
   int T = (int)tokens, E = experts, k = topk, rn = renormalize ? 1 : 0;
@@ -2316,10 +2321,11 @@ size_t qmm_moe_ffn_ex_workspace_size(const qmm_qtensor* gate, const qmm_qtensor*
 static int moe_gemv_path(Device* d, const MoeWs& L, uint8_t* b, const float* x, int64_t ldx, const int32_t* ptok,
                          int64_t T, int64_t P, int64_t H, int64_t F, int experts, const int32_t* counts,
                          const int32_t* offsets,
-                         const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* down, hipStream_t s) {
+                         const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* down, hipStream_t s,
+                         bool gathered) {
   void* stream = s;
   const int vg = qmm_vec_dot_type(gate->dtype);
-  {
+  if (!gathered) {
     const void* xp = x;
     long long lx = ldx;
     const int32_t* rows = ptok;
@@ -2388,13 +2394,27 @@ static int moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* log
   int32_t* ptok = (int32_t*)(b + L.pair_token);
   float* pw = (float*)(b + L.pair_weight);
   int32_t* tpairs = (int32_t*)(b + L.token_pairs);
-  QMM_TRY(qmm_moe_route_ex(logits, tokens, experts, topk, renormalize, routed_scaling_factor, counts, offsets, ptok,
-                           pw, tpairs, stream));
+  const bool grouped = moe_grouped(P, experts) && H % 256 == 0 && F % 256 == 0;
+  // decode-sized calls with Q8_K activations: routing and the Q8_K gather of the routed rows in one launch
+  // (every workgroup routes the tokens itself; the same lists as qmm_moe_route's)
+  const bool fused_route = !grouped && qmm_vec_dot_type(gate->dtype) == QMM_Q8K && P <= 256;
+  if (fused_route) {
+    QMM_TRY(route_check(tokens, experts, topk, routed_scaling_factor));
+    int T = (int)tokens, E = experts, k = topk, rn = renormalize ? 1 : 0, hh = (int)H;
+    float ps = routed_scaling_factor;
+    long long lx = ldx;
+    void* xq = b + L.xq;
+    void* args[] = {&logits, &T, &E, &k, &rn, &ps, &counts, &offsets, &ptok, &pw, &tpairs, &x, &lx, &xq, &hh};
+    QMM_TRY(launch(d, "qmm_moe_route_gather_q8k", ceil_div(P * (H / 256), 4), 256, 0, s, args));
+  } else {
+    QMM_TRY(qmm_moe_route_ex(logits, tokens, experts, topk, renormalize, routed_scaling_factor, counts, offsets, ptok,
+                             pw, tpairs, stream));
+  }
   float* g = (float*)(b + L.g);
   float* u = (float*)(b + L.u);
   float* h = (float*)(b + L.h);
   float* yp = (float*)(b + L.yp);
-  if (moe_grouped(P, experts) && H % 256 == 0 && F % 256 == 0) {
+  if (grouped) {
     // prefill: gathered rows -> grouped GEMMs (an expert holds at most
     // `tokens` pairs: a token's top-k experts are distinct)
     const int vg = qmm_vec_dot_type(gate->dtype), vd = qmm_vec_dot_type(down->dtype);
@@ -2458,7 +2478,8 @@ static int moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* log
                            L.total - L.planes, stream));
     }
   } else {
-    QMM_TRY(moe_gemv_path(d, L, b, x, ldx, ptok, tokens, P, H, F, experts, counts, offsets, gate, up, down, s));
+    QMM_TRY(moe_gemv_path(d, L, b, x, ldx, ptok, tokens, P, H, F, experts, counts, offsets, gate, up, down, s,
+                          fused_route));
   }
   // the always-on shared expert over every token (LlamaMlp::forward) and its
   // sigmoid gate, added by the combine after the routed sum

@@ -26,22 +26,24 @@
 // Pass 2: each wave takes experts e = wave, wave + 4, ... and walks the tokens
 // 64 at a time: a ballot of the lanes whose token selected e ranks them, so
 // pair p = offsets[e] + (pairs of e so far) + (selecting lanes below).
-extern "C" __global__ void __launch_bounds__(256) qmm_moe_route(const float* __restrict__ logits, int T, int E,
-                                                                int k, int renorm, float post_scale,
-                                                                int* __restrict__ counts,
-                                                                int* __restrict__ offsets,
-                                                                int* __restrict__ pair_token,
-                                                                float* __restrict__ pair_weight,
-                                                                int* __restrict__ token_pairs) {
+namespace qmm {
+// Routing of T tokens by one workgroup of NT threads (MoeMlp::forward's
+// softmax, top-k with the lowest expert index on ties, renormalised or
+// scaled weights), into per-expert pair lists in expert order: counts[e],
+// offsets[e] (offsets[E] = T * k), pair_token / pair_weight per pair, and
+// token_pairs (each token's pairs in increasing expert order). sel_e /
+// sel_w (T * k), ecount (E) and eoff (E + 1) are LDS scratch; the outputs
+// may be global or LDS. Ends after a barrier.
+template <int NT>
+__device__ __forceinline__ void moe_route_block(const float* __restrict__ logits, int T, int E, int k, int renorm,
+                                                float post_scale, short* sel_e, float* sel_w, int* ecount,
+                                                int* eoff, int* counts, int* offsets, int* pair_token,
+                                                float* pair_weight, int* token_pairs) {
 #pragma clang fp contract(off)
-  constexpr int kThreads = 256, kWaves = kThreads / 64;
-  __shared__ short sel_e[8192];
-  __shared__ float sel_w[8192];
-  __shared__ int ecount[256];
-  __shared__ int eoff[257];
-  for (int e = threadIdx.x; e < E; e += kThreads) ecount[e] = 0;
+  constexpr int kWaves = NT / 64;
+  for (int e = threadIdx.x; e < E; e += NT) ecount[e] = 0;
   __syncthreads();
-  for (int t = threadIdx.x; t < T; t += kThreads) {
+  for (int t = threadIdx.x; t < T; t += NT) {
     const float* l = logits + (size_t)t * E;
     float mx = l[0];
     for (int e = 1; e < E; ++e) mx = fmaxf(mx, l[e]);
@@ -87,7 +89,7 @@ extern "C" __global__ void __launch_bounds__(256) qmm_moe_route(const float* __r
     eoff[E] = pos;
   }
   __syncthreads();
-  for (int e = threadIdx.x; e <= E; e += kThreads) {
+  for (int e = threadIdx.x; e <= E; e += NT) {
     offsets[e] = eoff[e];
     if (e < E) counts[e] = ecount[e];
   }
@@ -113,6 +115,63 @@ extern "C" __global__ void __launch_bounds__(256) qmm_moe_route(const float* __r
       base += __popcll(m);
     }
   }
+  __syncthreads();
+}
+}  // namespace qmm
+
+extern "C" __global__ void __launch_bounds__(256) qmm_moe_route(const float* __restrict__ logits, int T, int E,
+                                                                int k, int renorm, float post_scale,
+                                                                int* __restrict__ counts,
+                                                                int* __restrict__ offsets,
+                                                                int* __restrict__ pair_token,
+                                                                float* __restrict__ pair_weight,
+                                                                int* __restrict__ token_pairs) {
+  __shared__ short sel_e[8192];
+  __shared__ float sel_w[8192];
+  __shared__ int ecount[256];
+  __shared__ int eoff[257];
+  qmm::moe_route_block<256>(logits, T, E, k, renorm, post_scale, sel_e, sel_w, ecount, eoff, counts, offsets,
+                            pair_token, pair_weight, token_pairs);
+}
+
+// Routing and the Q8_K gather of the routed rows in one launch, for decode-
+// sized calls (T * k <= 256 pairs): every workgroup routes all T tokens in
+// its own LDS (the same computation, so the same lists everywhere),
+// workgroup 0 writes the routing arrays out, and wave w of the grid then
+// quantizes block w % nb of pair w / nb's token row into xq (one Q8_K row
+// per pair, as qmm_quantize_q8k_gather writes it).
+extern "C" __global__ void __launch_bounds__(256) qmm_moe_route_gather_q8k(
+    const float* __restrict__ logits, int T, int E, int k, int renorm, float post_scale, int* __restrict__ counts,
+    int* __restrict__ offsets, int* __restrict__ pair_token, float* __restrict__ pair_weight,
+    int* __restrict__ token_pairs, const float* __restrict__ x, long long ldx, uint8_t* __restrict__ xq, int hidden) {
+  __shared__ short sel_e[256];
+  __shared__ float sel_w[256];
+  __shared__ int ecount[256];
+  __shared__ int eoff[257];
+  __shared__ int s_counts[256];
+  __shared__ int s_offsets[257];
+  __shared__ int s_ptok[256];
+  __shared__ float s_pw[256];
+  __shared__ int s_tp[256];
+  qmm::moe_route_block<256>(logits, T, E, k, renorm, post_scale, sel_e, sel_w, ecount, eoff, s_counts, s_offsets,
+                            s_ptok, s_pw, s_tp);
+  const int P = T * k;
+  if (blockIdx.x == 0) {
+    for (int e = threadIdx.x; e <= E; e += 256) {
+      offsets[e] = s_offsets[e];
+      if (e < E) counts[e] = s_counts[e];
+    }
+    for (int i = threadIdx.x; i < P; i += 256) {
+      pair_token[i] = s_ptok[i];
+      pair_weight[i] = s_pw[i];
+      token_pairs[i] = s_tp[i];
+    }
+  }
+  const int nb = hidden / 256;
+  const long long w = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= (long long)P * nb) return;
+  const int i = (int)(w / nb), b = (int)(w % nb);
+  qmm::q8k_block(x + (long long)s_ptok[i] * ldx + 256LL * b, xq + w * qmm::kQ8KBytes, threadIdx.x & 63);
 }
 
 // f32 row gather: out row i = x[rows[i]] (k columns).
