@@ -204,11 +204,13 @@ def run_gemv_set(torch, dev, args):
 
     # the timed region runs exactly args.steps steps: whole graphs of per_graph steps, then a graph of
     # the remaining steps (each graph walks the copies from the first, so a copy's weights are never
-    # re-read from the MALL by the step after it)
-    per_graph = copies * max(1, 24 // copies)
+    # re-read from the MALL by the step after it). A graph holds all the steps (up to 1200): each
+    # replay's start-up then falls once into the timed region, not once per few steps
+    per_graph = min(max(1, args.steps), 1200)
     g_step = capture(step, per_graph)
     reps, rem = divmod(args.steps, per_graph)
     g_rem = capture(step, rem) if rem else None
+    g_spread = capture(step, copies * max(1, 24 // copies))  # the spread's samples: 24-step replays
     for _ in range(max(1, -(-args.warmup // per_graph))):
         g_step.replay()
     if g_rem is not None:
@@ -230,8 +232,8 @@ def run_gemv_set(torch, dev, args):
 
     # spread of the step time: SPREAD_SAMPLES replays of the step graph, a HIP event between consecutive
     # replays
-    replay_samples(torch, g_step, 4, stream)
-    step_spread = spread(replay_samples(torch, g_step, SPREAD_SAMPLES, stream) * 1e3 / per_graph)
+    replay_samples(torch, g_spread, 4, stream)
+    step_spread = spread(replay_samples(torch, g_spread, SPREAD_SAMPLES, stream) * 1e3 / (copies * max(1, 24 // copies)))
 
     # single-launch graphs hold at least LAUNCH_GRAPH_MIN launches, so a replay's own start-up is a small
     # share of the per-launch figure
