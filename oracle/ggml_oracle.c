@@ -348,8 +348,11 @@ static void dequant_q4k(const uint8_t *blk, float *y) {
 /* ------------------------------------------------------------------ */
 
 /* make_qx_quants(n, nmax, x, L, rmse_type) [upstream quantized/utils.rs]:
- * symmetric fit with least-squares refinement; L[i] holds l + nmax. */
-static float make_qx_quants(int n, int nmax, const float *x, int8_t *L, int rmse_type) {
+ * symmetric fit with least-squares refinement; L[i] holds l + nmax. Only the two forms this path
+ * reaches are restated: rmse_type 0 (the bare rounding) and 1 (the x^2-weighted refinement that
+ * BlockQ6K::from_float uses); any other rmse_type returns NaN. */
+static float make_qx_quants_stages(int n, int nmax, const float *x, int8_t *L, int rmse_type,
+                                   int *first_passes) {
     float max = 0.0f, amax = 0.0f;
     for (int i = 0; i < n; i++) {
         float ax = fabsf(x[i]);
@@ -367,7 +370,8 @@ static float make_qx_quants(int n, int nmax, const float *x, int8_t *L, int rmse
         }
         return 1.0f / iscale;
     }
-#define QX_W(v) (rmse_type == 1 ? (v) * (v) : rmse_type == 2 ? 1.0f : rmse_type == 3 ? fabsf(v) : sqrtf(fabsf(v)))
+    if (rmse_type != 1) return NAN;
+#define QX_W(v) ((v) * (v))
     float sumlx = 0.0f, suml2 = 0.0f;
     for (int i = 0; i < n; i++) {
         int32_t l = clampi(nearest_int(iscale * x[i]), -nmax, nmax - 1);
@@ -400,7 +404,10 @@ static float make_qx_quants(int n, int nmax, const float *x, int8_t *L, int rmse
         suml2 = sl2;
         scale = sumlx / suml2;
         best = scale * sumlx;
+        if (first_passes) ++*first_passes;
     }
+    /* test hook: stop after the first loop (the count of its accepted passes in *first_passes) */
+    if (first_passes) return scale;
     for (int itry = 0; itry < 5; itry++) {
         int n_changed = 0;
         for (int i = 0; i < n; i++) {
@@ -426,29 +433,12 @@ static float make_qx_quants(int n, int nmax, const float *x, int8_t *L, int rmse
         }
         if (!n_changed) break;
     }
-    if (rmse_type < 3) return scale;
-    for (int is = -4; is <= 4; is++) {
-        if (is == 0) continue;
-        iscale = -((float)nmax + 0.1f * (float)is) / max;
-        float slx = 0.0f, sl2 = 0.0f;
-        for (int i = 0; i < n; i++) {
-            int32_t l = clampi(nearest_int(iscale * x[i]), -nmax, nmax - 1);
-            float w = QX_W(x[i]);
-            float lf = (float)l;
-            slx += w * x[i] * lf;
-            sl2 += w * lf * lf;
-        }
-        if (sl2 > 0.0f && slx * slx > best * sl2) {
-            for (int i = 0; i < n; i++) {
-                int32_t l = nearest_int(iscale * x[i]);
-                L[i] = (int8_t)(nmax + clampi(l, -nmax, nmax - 1));
-            }
-            scale = slx / sl2;
-            best = scale * slx;
-        }
-    }
 #undef QX_W
     return scale;
+}
+
+static float make_qx_quants(int n, int nmax, const float *x, int8_t *L, int rmse_type) {
+    return make_qx_quants_stages(n, nmax, x, L, rmse_type, NULL);
 }
 
 void orc_make_qkx1_quants(int nmax, int ntry, const float *x, int n, float *scale, float *neg_min) {
@@ -457,6 +447,11 @@ void orc_make_qkx1_quants(int nmax, int ntry, const float *x, int n, float *scal
 
 float orc_make_qx_quants(int n, int nmax, const float *x, int8_t *L, int rmse_type) {
     return make_qx_quants(n, nmax, x, L, rmse_type);
+}
+
+float orc_make_qx_quants_first(int n, int nmax, const float *x, int8_t *L, int *passes) {
+    *passes = 0;
+    return make_qx_quants_stages(n, nmax, x, L, 1, passes);
 }
 
 /* BlockQ6K::from_float [upstream k_quants.rs]. */

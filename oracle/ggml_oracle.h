@@ -73,6 +73,9 @@ enum { ORC_IMPL_GENERIC = 0, ORC_IMPL_AVX2 = 1 };
  * writes L[i] = l_i + nmax of a symmetric fit. */
 void orc_make_qkx1_quants(int nmax, int ntry, const float *x, int n, float *scale, float *neg_min);
 float orc_make_qx_quants(int n, int nmax, const float *x, int8_t *L, int rmse_type);
+/* make_qx_quants (rmse_type 1) stopped after its first refinement loop; *passes = the loop's accepted
+ * passes (0..3). Test hook for that loop's exit condition. */
+float orc_make_qx_quants_first(int n, int nmax, const float *x, int8_t *L, int *passes);
 
 int orc_simd_supported(void);
 float orc_vec_dot_avx2(int dtype, int64_t k, const void *w_row, const void *x_row);

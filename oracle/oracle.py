@@ -56,6 +56,8 @@ def lib() -> ctypes.CDLL:
         L.orc_make_qkx1_quants.restype = None
         L.orc_make_qx_quants.argtypes = [i32, i32, vp, vp, i32]
         L.orc_make_qx_quants.restype = ctypes.c_float
+        L.orc_make_qx_quants_first.argtypes = [i32, i32, vp, vp, vp]
+        L.orc_make_qx_quants_first.restype = ctypes.c_float
         for f in ("orc_block_elems", "orc_block_bytes", "orc_vec_dot_type"):
             getattr(L, f).argtypes = [i32]
         _lib = L
@@ -100,11 +102,23 @@ def make_qkx1_quants(x: np.ndarray, nmax: int = 15, ntry: int = 5):
 
 
 def make_qx_quants(x: np.ndarray, nmax: int = 32, rmse_type: int = 1):
-    """The Q6_K sub-block fit (quantized/utils.rs make_qx_quants): (scale, l) with l in [-nmax, nmax)."""
+    """The Q6_K sub-block fit (quantized/utils.rs make_qx_quants): (scale, l) with l in [-nmax, nmax).
+    rmse_type 0 (bare rounding) and 1 (x^2-weighted refinement, the one BlockQ6K uses) are restated."""
+    if rmse_type not in (0, 1):
+        raise ValueError(f"make_qx_quants: rmse_type {rmse_type} is not restated (0 and 1 are)")
     x = np.ascontiguousarray(x, dtype=np.float32)
     L = np.zeros(x.size, np.int8)
     s = lib().orc_make_qx_quants(x.size, nmax, _ptr(x), _ptr(L), rmse_type)
     return float(s), L.astype(np.int32) - nmax
+
+
+def make_qx_quants_first(x: np.ndarray, nmax: int = 32):
+    """make_qx_quants (rmse_type 1) stopped after its first refinement loop: (scale, l, accepted passes)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    L = np.zeros(x.size, np.int8)
+    passes = np.zeros(1, np.int32)
+    s = lib().orc_make_qx_quants_first(x.size, nmax, _ptr(x), _ptr(L), _ptr(passes))
+    return float(s), L.astype(np.int32) - nmax, int(passes[0])
 
 
 def quantize(dt: int, x: np.ndarray) -> np.ndarray:
