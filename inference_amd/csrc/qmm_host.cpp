@@ -100,13 +100,13 @@ std::atomic<Device*> g_dev[64] = {};
 enum EnvKey {
   kEnvGemv1, kEnvGemv1p, kEnvGemvCfg, kEnvGemvWavesPerCu, kEnvGemvRows, kEnvSplitK, kEnvMmq2, kEnvMmq,
   kEnvMmq4Bn, kEnvMmq1, kEnvMmqXcd, kEnvMoeGemv, kEnvMoeMmq, kEnvMoeBm, kEnvMoeSplitK, kEnvMoeGrouped, kEnvGroupedP,
-  kEnvGroupedWgs, kEnvStreamK, kEnvCount
+  kEnvGroupedWgs, kEnvStreamK, kEnvGemvm, kEnvCount
 };
 const char* const kEnvNames[kEnvCount] = {
     "QMM_GEMV1", "QMM_GEMV1P", "QMM_GEMV_CFG", "QMM_GEMV_WAVES_PER_CU", "QMM_GEMV_ROWS", "QMM_SPLITK",
     "QMM_MMQ2", "QMM_MMQ", "QMM_MMQ4_BN", "QMM_MMQ1", "QMM_MMQ_XCD", "QMM_MOE_GEMV", "QMM_MOE_MMQ",
     "QMM_MOE_BM", "QMM_MOE_SPLITK", "QMM_MOE_GROUPED", "QMM_GROUPED_P", "QMM_GROUPED_WGS",
-    "QMM_STREAMK"};
+    "QMM_STREAMK", "QMM_GEMVM"};
 
 struct Tuning {
   int w = 0, r = 0, u = 0, waves_per_cu = 0, gemv1 = 1, gemv1p = -1;
@@ -647,6 +647,26 @@ static int gemv(Device* d, const GemvTarget* tg, int count, const void* act, boo
   int rows_from = w->n >= 2048 ? 2 : 7;
   if (const char* e = env(kEnvGemvRows)) rows_from = atoi(e);
   const unsigned long long rbody = fmt == kFmtQ4K ? 144 : 208;  // device block bodies (Q6_K's f16 d kept apart)
+  // 6..8 staged rows of a Q4_K weight of >= 8192 rows: the multi-token GEMV
+  // on the int8 matrix cores (qmm_gemv_rowsm_q4k: 16 rows x 16 tokens per
+  // MFMA, the activation read once per workgroup instead of once per token
+  // and weight slice). From the sweep at 14336 x 4096 (kernel time): m = 8
+  // 13.9 vs 18.9 us for the token-interleaved kernel, m = 4 about even; its
+  // fixed cost per weight slice loses below six rows. QMM_GEMVM=0 never, 1
+  // wherever it applies (2..8 rows of Q4_K).
+  int gvm = -1;
+  if (const char* e = env(kEnvGemvm)) gvm = atoi(e);
+  if (count == 1 && !fused && !silu && dump == nullptr && fmt == kFmtQ4K && m >= 2 && m <= 8 && nb <= 64 &&
+      (unsigned long long)w->n * nb * rbody < (1ull << 32) &&
+      (gvm > 0 || (gvm < 0 && m >= 6 && w->n >= 8192))) {
+    const void* wq = w->data;
+    float* yy = tg[0].y;
+    int ldy = (int)tg[0].ldy, mm = m, K = (int)w->k, N = (int)w->n, acc = accumulate;
+    void* args[] = {&wq, &yy, &ldy, &act, &mm, &K, &N, &acc};
+    const long long groups = (N + 15) / 16;  // 16 weight rows per wave, four waves per workgroup
+    return launch(d, "qmm_gemv_rowsm_q4k_w4_p4", ceil_div(groups, 4), 256, (unsigned)(m * (K + 16) + 320 * nb), s,
+                  args);
+  }
   if (count == 1 && !fused && !silu && dump == nullptr && rows_from > 0 && m >= rows_from && m <= 8 &&
       fmt != kFmtQ80 && nb <= 64 && (unsigned long long)w->n * nb * rbody < (1ull << 32)) {
     char rname[32];
@@ -2035,6 +2055,35 @@ static int moe_gemv(const qmm_qtensor* const* w, int count, int experts, const v
   if ((unsigned long long)(w[0]->n / experts) * (unsigned long long)nb * body >= (1ull << 32)) ring = 0;
   const long long passes = (std::max<long long>(std::min<long long>(max_count, pairs), 1) + 7) / 8;
   if (passes > 64) ring = 0;  // many idle pass workgroups: the generic kernel loops over its rows instead
+  // Q4_K experts averaging six or more routed pairs: the matrix-core
+  // multi-token GEMV (qmm_moe_gemvm_q4k, passes of up to 16 tokens; 305 vs
+  // 377 us for a 32-token top-2 FFN over 8 Mixtral-shape experts, slower
+  // than the ring kernel at two to four tokens per expert). QMM_GEMVM=0
+  // never, 1 for every Q4_K call the ring kernel would take.
+  int gvm = -1;
+  if (const char* e = env(kEnvGemvm)) gvm = atoi(e);
+  if (ring && fmt == kFmtQ4K && (gvm > 0 || (gvm < 0 && pairs >= 6LL * experts))) {
+    int K = (int)w[0]->k;
+    const int mt = (int)std::min<long long>(16, (d->max_lds - 320LL * nb - 2048) / (K + 16));
+    if (mt >= 1) {
+      const long long gpasses = (std::max<long long>(std::min<long long>(max_count, pairs), 1) + mt - 1) / mt;
+      const int vt = qmm_vec_dot_type(w[0]->dtype);
+      long long xrow = (w[0]->k / qmm_block_size(vt)) * qmm_type_size(vt);
+      int N = (int)(w[0]->n / experts), E = experts, nj = count, ld = N, mtt = mt;
+      const void* w0 = w[0]->data;
+      const void* w1 = count > 1 ? w[1]->data : w[0]->data;
+      float* y0 = y[0];
+      float* y1 = count > 1 ? y[1] : y[0];
+      const void* xp = xq;
+      void* args[] = {&w0, &w1, &nj, &N, &E, &y0, &y1, &ld, &xp, &xrow, &counts, &offsets, &K, &mtt};
+      hipFunction_t f;
+      QMM_TRY(kernel(d, "qmm_moe_gemvm_q4k_w4_p4", &f));
+      const long long gr = std::max<long long>((long long)d->num_cu * 4, E);
+      QMM_HIP(hipModuleLaunchKernel(f, (unsigned)gr, (unsigned)gpasses, 1, 256, 1, 1,
+                                    (unsigned)(mt * (K + 16) + 320 * nb), (hipStream_t)stream, args, nullptr));
+      return QMM_OK;
+    }
+  }
   char name[48];
   if (ring)
     snprintf(name, sizeof(name), "qmm_moe_gemv1_%s_p%d", fmt_name(fmt), ring);

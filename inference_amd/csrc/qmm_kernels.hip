@@ -8,5 +8,6 @@
 #include "qmm_gemv1p_kernels.h"
 #include "qmm_mmq_kernels.h"
 #include "qmm_moe_kernels.h"
+#include "qmm_gemvm_kernels.h"
 #include "qmm_decode_kernels.h"
 #include "qmm_calib_kernels.h"
