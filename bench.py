@@ -640,7 +640,8 @@ def kernel_only(torch, dev, which, launches):
     `gate` = the Q4_K gate GEMV (14336x4096, M = 1, rotated weight copies); `qkvgu` / `qkvgu_staged`
     = the q/k/v/gate/up set in one launch (Q8_K in the prologue / pre-quantized activation);
     `copy` = a 256 MiB device copy (the calibration for FETCH_SIZE / WRITE_SIZE); `gemm_gate` / `gemm_down` =
-    the config-4 GEMMs (M = 512); `moe` = the config-5 expert FFN."""
+    the config-4 GEMMs (M = 512); `moe` = the config-5 expert FFN (`moe32`: at 32 tokens); `gate_m8` = the gate
+    GEMV on eight pre-quantized rows."""
     from inference_amd import GgmlDType, QTensor, qmm
     from inference_amd.synth import normal, normal_torch
     if which == "copy":
@@ -667,9 +668,10 @@ def kernel_only(torch, dev, which, launches):
         torch.cuda.synchronize()
         print(json.dumps({"kernel_only": which, "int8_ops": 2 * 512 * n * k, "launches": launches}), flush=True)
         return
-    if which == "moe":
-        # config 5: one qmm_moe_ffn call per launch (route, gather, expert GEMVs, SiLU*mul, combine)
-        E, H, F, T, k = 8, 4096, 14336, 8, 2
+    if which in ("moe", "moe32"):
+        # config 5: one qmm_moe_ffn call per launch (route, gather, expert GEMVs, SiLU*mul, combine);
+        # moe32: the same experts at 32 tokens (the matrix-core expert GEMV for gate / up)
+        E, H, F, T, k = 8, 4096, 14336, 32 if which == "moe32" else 8, 2
         gate = QTensor.quantize(normal_torch(71, (E * F, H), 0.02, dev), GgmlDType.Q4K)
         up = QTensor.quantize(normal_torch(72, (E * F, H), 0.02, dev), GgmlDType.Q4K)
         down = QTensor.quantize(normal_torch(73, (E * H, F), 0.02, dev), GgmlDType.Q6K)
@@ -683,7 +685,7 @@ def kernel_only(torch, dev, which, launches):
             qmm._check(L.qmm_moe_ffn(x.data_ptr(), T, H, lg.data_ptr(), E, k, gate.handle, up.handle, down.handle,
                                      y.data_ptr(), H, ws.data_ptr(), wsb, qmm._stream(dev)))
         torch.cuda.synchronize()
-        print(json.dumps({"kernel_only": "moe", "launches": launches}), flush=True)
+        print(json.dumps({"kernel_only": which, "tokens": T, "launches": launches}), flush=True)
         return
     if which.startswith("read_") and which != "read_graph":
         # plain streaming reads of a buffer of the GEMV launches' sizes (q 9.5 MB, gate 33 MB, the five-weight
@@ -791,14 +793,20 @@ def kernel_only(torch, dev, which, launches):
         torch.cuda.synchronize()
         print(json.dumps({"kernel_only": which, "algorithmic_bytes": alg, "launches": launches}), flush=True)
         return
-    if which == "gate":
+    if which in ("gate", "gate_m8"):
+        # gate_m8: eight pre-quantized Q8_K rows (the matrix-core multi-token GEMV)
+        m = 8 if which == "gate_m8" else 1
         ws = [QTensor.quantize(normal_torch(2 + 1000 * c + 17 * 3, (14336, 4096), 0.02, dev), GgmlDType.Q4K)
               for c in range(8)]
-        y = torch.empty(14336, dtype=torch.float32, device=dev)
+        if m > 1:
+            xm = torch.from_numpy(normal(11, (m, 4096))).to(dev)
+            xq = torch.zeros(m * 16 * 292, dtype=torch.uint8, device=dev)
+            qmm._check(L.qmm_quantize_rows(15, xm.data_ptr(), m, 4096, 4096, xq.data_ptr(), qmm._stream(dev)))
+        y = torch.empty(m * 14336, dtype=torch.float32, device=dev)
         for i in range(launches):
-            qmm._check(L.qmm_matmul_q(ws[i % 8].handle, xq.data_ptr(), 1, y.data_ptr(), 14336, None, 0,
+            qmm._check(L.qmm_matmul_q(ws[i % 8].handle, xq.data_ptr(), m, y.data_ptr(), 14336, None, 0,
                                       qmm._stream(dev)))
-        alg = gemv_bytes(12, 14336, 4096)
+        alg = gemv_bytes(12, 14336, 4096) + (m - 1) * 4 * (4096 + 14336)
     else:
         names = [nm for nm, _, _ in GEMV_SET if nm != "down_proj"]
         shp = {nm: (n, k) for nm, n, k in GEMV_SET}
@@ -847,8 +855,8 @@ def main():
                          "launch, quantize, down; fused: the same two GEMV launches with Q8_K quantization in "
                          "their prologues; serial: one launch per projection")
     ap.add_argument("--decode-tokens", type=int, default=256, help="config-3 generated tokens (0 = skip)")
-    ap.add_argument("--kernel-only", choices=("gate", "qkvgu", "qkvgu_staged", "grouped", "copy", "gemm_gate",
-                                              "gemm_down", "moe",
+    ap.add_argument("--kernel-only", choices=("gate", "gate_m8", "qkvgu", "qkvgu_staged", "grouped", "copy",
+                                              "gemm_gate", "gemm_down", "moe", "moe32",
                                               "q8_0", "down_q6k", "decode", "read_9mb", "read_33mb",
                                               "read_80mb", "read_1gb", "read_graph"),
                     default=None,
