@@ -100,13 +100,13 @@ std::atomic<Device*> g_dev[64] = {};
 enum EnvKey {
   kEnvGemv1, kEnvGemv1p, kEnvGemvCfg, kEnvGemvWavesPerCu, kEnvGemvRows, kEnvSplitK, kEnvMmq2, kEnvMmq,
   kEnvMmq4Bn, kEnvMmq1, kEnvMmqXcd, kEnvMoeGemv, kEnvMoeMmq, kEnvMoeBm, kEnvMoeSplitK, kEnvMoeGrouped, kEnvGroupedP,
-  kEnvGroupedWgs, kEnvStreamK, kEnvGemvm, kEnvCount
+  kEnvGroupedWgs, kEnvStreamK, kEnvGemvm, kEnvMmq6, kEnvCount
 };
 const char* const kEnvNames[kEnvCount] = {
     "QMM_GEMV1", "QMM_GEMV1P", "QMM_GEMV_CFG", "QMM_GEMV_WAVES_PER_CU", "QMM_GEMV_ROWS", "QMM_SPLITK",
     "QMM_MMQ2", "QMM_MMQ", "QMM_MMQ4_BN", "QMM_MMQ1", "QMM_MMQ_XCD", "QMM_MOE_GEMV", "QMM_MOE_MMQ",
     "QMM_MOE_BM", "QMM_MOE_SPLITK", "QMM_MOE_GROUPED", "QMM_GROUPED_P", "QMM_GROUPED_WGS",
-    "QMM_STREAMK", "QMM_GEMVM"};
+    "QMM_STREAMK", "QMM_GEMVM", "QMM_MMQ6"};
 
 struct Tuning {
   int w = 0, r = 0, u = 0, waves_per_cu = 0, gemv1 = 1, gemv1p = -1;
@@ -820,6 +820,10 @@ struct GemmPlan {
 // 19.0 -> 17.5 us (8, not 16). QMM_SPLITK=0 disables it, QMM_SPLITK=<S>
 // forces S splits.
 static constexpr unsigned kMmqStaticLds = 61440;  // the first-generation tile's static LDS (MmqLds)
+// one LDS stage of the split-digit Q6_K tile (mmqs6): activation rows, int8
+// codes, digit bytes, column d, row scales (128 x 256, 128 x 256, 128 x 48,
+// 128 x 4, 128 x 4 bytes)
+static constexpr unsigned kS6StageBytes = 128 * 256 + 128 * 256 + 128 * 48 + 128 * 4 + 128 * 4;
 static constexpr int kMmqBMRows = 64;             // and its M tile
 static void plan_splits(const Device* d, GemmPlan& p, int nbk) {
   const long long tiles = (long long)p.gx * p.gy;
@@ -929,6 +933,14 @@ static GemmPlan gemm_plan(const Device* d, const qmm_qtensor* w, int64_t m, bool
     p.gy = (unsigned)((M + 127) / 128);
     p.threads = 256;
     p.lds = (unsigned)(2 * (128 * 272 + b4 * 144 + 128 * 4 + 128 * 16));
+  } else if (fmt == kFmtQ6K && env(kEnvMmq6) == nullptr && (int)(2 * kS6StageBytes) <= d->max_lds) {
+    // Q6_K default: mmqs6 (the sub-block scales as three signed digits in the int8 MFMA operands, 128 x 128
+    // tiles of eight waves, LDS 2 x 71 KB); QMM_MMQ6=1 selects the first-generation tile
+    snprintf(p.name, sizeof(p.name), "qmm_mmqs6_q6k%s", dump ? "_dump" : "");
+    p.gx = (unsigned)((N + 127) / 128);
+    p.gy = (unsigned)((M + 127) / 128);
+    p.threads = 512;
+    p.lds = 2 * kS6StageBytes;
   } else if (fmt == kFmtQ4K && (int)lds2 <= d->max_lds && env(kEnvMmq1) == nullptr) {
     snprintf(p.name, sizeof(p.name), "qmm_mmq2_q4k_m%d_n%d%s", bm, bn, dump ? "_dump" : "");
     p.gx = (unsigned)((N + bn - 1) / bn);

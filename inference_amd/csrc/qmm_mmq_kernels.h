@@ -1570,6 +1570,258 @@ __device__ __forceinline__ void mmqs_q4k_sk(const uint8_t* __restrict__ wq, cons
 QMM_MMQS_KERNEL(, false)
 QMM_MMQS_KERNEL(_dump, true)
 
+// ---------------------------------------------------------------------------
+// mmqs6: the Q6_K prefill GEMM with the sub-block scales in the MFMA
+// operands. A Q6_K code q - 32 lies in [-32, 31] and its 16-element sub-block
+// scale sc is a signed byte; sc * q does not fit an int8 operand, but every
+// sc in [-128, 127] is d0 + 8 d1 + 64 d2 with digits d in [-3, 4]
+// (d0 = ((sc + 3) mod 8) - 3, then the same on (sc - d0) / 8; d2 stays in
+// [-2, 2]), and d * q then lies in [-128, 124]. So per 32-element chunk the
+// weight operand of digit i is d_i(sub-block) * q (a lane's 16 K elements
+// belong to one sub-block) and
+//   isum = MFMA-sum(x, d0 q) + 8 MFMA-sum(x, d1 q) + 64 MFMA-sum(x, d2 q)
+// exactly in int32; y += dx * (d * isum) per super-block, the first-generation
+// kernel's f32 sequence. Three int8 MFMA sets per chunk replace the two 24-bit
+// multiply-adds per output and sub-block of the masked first-generation
+// kernel (mmq<Q6_K>).
+// Workgroup and waves as mmqs: a 128 x 128 tile, eight waves (two along M with
+// 64 rows each, four along N with 32 columns), two LDS stages.
+//   * Activation rows go straight to LDS (swizzled chunks), as in mmqs.
+//   * Weights come through registers: thread t takes column t / 4's 64
+//     elements of quarter t % 4 (ql of its half and qh), unpacks them to int8
+//     q - 32 in LDS (16-byte chunk k of column n at slot k ^ (n & 15)) and
+//     writes the digits of four of the column's sixteen scales.
+//   * Per chunk a lane forms each digit's operand from its 16 codes: even and
+//     odd bytes widened to 16-bit lanes, one packed 16-bit multiply each (the
+//     low byte is the product modulo 256, i.e. the int8 product), one byte
+//     permute back.
+// DUMP instantiations write every block's isum, as mmq<Q6_K>'s dump does.
+// ---------------------------------------------------------------------------
+namespace qmm {
+
+constexpr int kS6OffBq = kSBM * 256;             // int8 codes [col][256], swizzled 16-byte slots
+constexpr int kS6OffDg = kS6OffBq + kSBN * 256;  // digit bytes [col][3][16]
+constexpr int kS6OffDw = kS6OffDg + kSBN * 48;   // f32 d per column
+constexpr int kS6OffDx = kS6OffDw + kSBN * 4;    // f32 scale per row
+constexpr int kS6Stage = kS6OffDx + kSBM * 4;
+
+struct SRegs6 {
+  uint4 l0, l1, l2, l3;  // ql[64 n, +64) of the thread's column (n = its half)
+  uint4 h0, h1;          // qh[32 n, +32)
+  uint32_t sc4;          // the column's int8 scales 4 p .. 4 p + 3 (p = the thread's quarter)
+  uint32_t dh;           // f16 d (quarter 0)
+  float dx;              // t < 128: scale of row t
+};
+
+// Global loads of one K step: activation rows straight into stage `stg` (as
+// s_load), the weight bytes and scales into registers (columns past N repeat
+// the last one; their outputs are never stored).
+__device__ __forceinline__ void s6_load(SRegs6& R, uint8_t* stg, const int8_t* __restrict__ xq,
+                                        const float* __restrict__ xd, const uint8_t* __restrict__ wq,
+                                        const uint16_t* __restrict__ wd, int M, int N, int K, int m0, int n0,
+                                        int kb) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nbk = K / 256;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int row = 16 * wave + 4 * u + (lane >> 4);
+    const int gr = min(m0 + row, M - 1);
+    lds_dma16(xq + (size_t)gr * K + 256 * kb + 16 * ((lane & 15) ^ (row & 15)), stg + 256 * (16 * wave + 4 * u));
+  }
+  const int col = t >> 2, p = t & 3, n = p >> 1;
+  const int gc = min(n0 + col, N - 1);
+  const uint4* b = reinterpret_cast<const uint4*>(wq + ((size_t)gc * nbk + kb) * kQ6KBody);
+  R.l0 = b[4 * n];
+  R.l1 = b[4 * n + 1];
+  R.l2 = b[4 * n + 2];
+  R.l3 = b[4 * n + 3];
+  R.h0 = b[8 + 2 * n];
+  R.h1 = b[9 + 2 * n];
+  R.sc4 = reinterpret_cast<const uint32_t*>(b + 12)[p];
+  R.dh = p == 0 ? (uint32_t)wd[(size_t)gc * nbk + kb] : 0u;
+  if (t < 128) {
+    const int row = m0 + t;
+    R.dx = row < M ? xd[(size_t)row * nbk + kb] : 0.0f;
+  }
+}
+
+// The register-staged parts of one K step into stage `buf`: the int8 codes of
+// elements 128 n + 32 j + l (j = 2 (p & 1) + {0, 1}, l < 32) of the thread's
+// column, the digits of scales 4 p .. 4 p + 3, d and the row scales.
+__device__ __forceinline__ void s6_store(const SRegs6& R, uint8_t* buf) {
+  const int t = threadIdx.x, col = t >> 2, p = t & 3, n = p >> 1, hi = p & 1;
+  uint8_t* bq = buf + kS6OffBq + 256 * col;
+  const int sw = col & 15;
+  // ql bytes [32 jj + 16 half, +16) of the half hold elements 32 j + 16 half + [0, 16) for j = 2 hi + jj
+  // (low nibbles for hi = 0, high ones for hi = 1); qh bits 2 j of the same l
+  const int ns = hi ? 4 : 0;
+  auto put = [&](uint4 lq, uint4 hq, int j, int half) {
+    const int qs = 2 * j;
+    auto one = [&](uint32_t l, uint32_t h) {
+      return q6_sub32(((l >> ns) & 0x0f0f0f0fu) | (((h >> qs) & 0x03030303u) << 4));
+    };
+    const int slot = 8 * n + 2 * j + half;
+    *reinterpret_cast<uint4*>(bq + 16 * (slot ^ sw)) =
+        make_uint4(one(lq.x, hq.x), one(lq.y, hq.y), one(lq.z, hq.z), one(lq.w, hq.w));
+  };
+  put(R.l0, R.h0, 2 * hi, 0);
+  put(R.l1, R.h1, 2 * hi, 1);
+  put(R.l2, R.h0, 2 * hi + 1, 0);
+  put(R.l3, R.h1, 2 * hi + 1, 1);
+  // digits of scales 4 p .. 4 p + 3
+  const uint32_t sw4 = R.sc4;
+  uint32_t dg[3] = {0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int s = (int)(int8_t)((sw4 >> (8 * i)) & 0xffu);
+    const int d0 = ((s + 3) & 7) - 3;
+    const int r = (s - d0) >> 3;
+    const int d1 = ((r + 3) & 7) - 3;
+    const int d2 = (r - d1) >> 3;
+    dg[0] |= (uint32_t)(d0 & 0xff) << (8 * i);
+    dg[1] |= (uint32_t)(d1 & 0xff) << (8 * i);
+    dg[2] |= (uint32_t)(d2 & 0xff) << (8 * i);
+  }
+  uint32_t* dgp = reinterpret_cast<uint32_t*>(buf + kS6OffDg + 48 * col);
+#pragma unroll
+  for (int d = 0; d < 3; ++d) dgp[4 * d + p] = dg[d];
+  if (p == 0) reinterpret_cast<float*>(buf + kS6OffDw)[col] = h2f(R.dh);
+  if (t < 128) reinterpret_cast<float*>(buf + kS6OffDx)[t] = R.dx;
+}
+
+// One K step's digit sums from stage `buf`: acc[d][i] = MFMA-sum over the
+// step of x (row tile i) and d_d * q (the lane's column).
+__device__ __forceinline__ void mmqs6_mfma(const uint8_t* __restrict__ buf, i32x16 (&acc)[3][kSTM], int wm, int r,
+                                           int h, int bcol) {
+  i32x16 zero;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) zero[j] = 0;
+  const int arow0 = 64 * wm + r;
+  const int sa = r & 15, sb = bcol & 15;
+  const int8_t* A = reinterpret_cast<const int8_t*>(buf);
+  const uint8_t* Bq = buf + kS6OffBq + 256 * bcol;
+  const uint4* DG = reinterpret_cast<const uint4*>(buf + kS6OffDg + 48 * bcol);
+  const uint4 dgv[3] = {DG[0], DG[1], DG[2]};
+  auto dword = [](const uint4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; };
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const uint4 bv = *reinterpret_cast<const uint4*>(Bq + 16 * ((2 * c + h) ^ sb));
+    const uint32_t bw[4] = {bv.x, bv.y, bv.z, bv.w};
+    uint32_t ev[4], od[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      ev[k] = bw[k] & 0x00ff00ffu;
+      od[k] = (bw[k] >> 8) & 0x00ff00ffu;
+    }
+    i8x16 a[kSTM];
+#pragma unroll
+    for (int i = 0; i < kSTM; ++i)
+      a[i] = *reinterpret_cast<const i8x16*>(A + 256 * (arow0 + 32 * i) + 16 * ((2 * c + h) ^ sa));
+    const int sh = 8 * (2 * (c & 1) + h);  // byte (2 c + h) of the digit rows: dword c / 2
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+      const int dv = (int)(int8_t)((dword(dgv[d], c >> 1) >> sh) & 0xffu);
+      const u16x2 m2 = __builtin_bit_cast(u16x2, ((uint32_t)dv & 0xffffu) * 0x10001u);
+      uint32_t w[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t pe = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, ev[k]) * m2);
+        const uint32_t po = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, od[k]) * m2);
+        w[k] = __builtin_amdgcn_perm(po, pe, 0x06020400u);  // bytes pe.0, po.0, pe.2, po.2
+      }
+      const i8x16 bd = as_i8x16(make_uint4(w[0], w[1], w[2], w[3]));
+#pragma unroll
+      for (int i = 0; i < kSTM; ++i) acc[d][i] = mfma_i8(a[i], bd, c == 0 ? zero : acc[d][i]);
+    }
+  }
+}
+
+// acc = fma(dx, d * isum, acc) per output (isum = D0 + 8 D1 + 64 D2); DUMP:
+// every block's isum.
+template <bool DUMP>
+__device__ __forceinline__ void mmqs6_epi(const uint8_t* __restrict__ buf, const i32x16 (&dsum)[3][kSTM],
+                                          f32x16 (&acc)[kSTM], int wm, int r, int h, int bcol, int m0, int col,
+                                          int M, int N, int nbk, int kb, int* __restrict__ dump) {
+#pragma clang fp contract(off)
+  const float* DX = reinterpret_cast<const float*>(buf + kS6OffDx);
+  const float dw = reinterpret_cast<const float*>(buf + kS6OffDw)[bcol];
+#pragma unroll
+  for (int i = 0; i < kSTM; ++i) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 dx = *reinterpret_cast<const float4*>(DX + 64 * wm + 32 * i + 8 * g + 4 * h);
+      const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = 4 * g + q;
+        const int isum = dsum[0][i][e] + (dsum[1][i][e] << 3) + (dsum[2][i][e] << 6);
+        // the first-generation tile's sequence (its += compiles to one fma): the same bits
+        acc[i][e] = __builtin_fmaf(dxs[q], dw * (float)isum, acc[i][e]);
+        if (DUMP) {
+          const int rt = 64 * wm + 32 * i + 8 * g + 4 * h + q;
+          if (m0 + rt < M && col < N) dump[((size_t)(m0 + rt) * N + col) * nbk + kb] = isum;
+        }
+      }
+    }
+  }
+  (void)r;
+}
+
+template <bool DUMP>
+__device__ __forceinline__ void mmqs6_q6k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,
+                                          const float* __restrict__ xd, float* __restrict__ y, int M, int N, int K,
+                                          int ldy, int* __restrict__ dump, int accumulate, int remap, int kb0,
+                                          int kb1) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  int mt, nt;
+  gemm_tile(remap, mt, nt);
+  const int m0 = mt * kSBM, n0 = nt * kSBN;
+  const int nbk = K / 256;
+  const uint16_t* wd = split_scales<kFmtQ6K>(wq, N, K);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int bcol = 32 * wn + r;
+  const int col = n0 + bcol;
+  f32x16 acc[kSTM];
+#pragma unroll
+  for (int i = 0; i < kSTM; ++i)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[i][j] = 0.0f;
+  SRegs6 R;
+  s6_load(R, lds, xq, xd, wq, wd, M, N, K, m0, n0, kb0);
+  s6_store(R, lds);
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+  __syncthreads();
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const uint8_t* cur = lds + ((kb - kb0) & 1) * kS6Stage;
+    uint8_t* nxt = lds + ((kb + 1 - kb0) & 1) * kS6Stage;
+    if (kb + 1 < kb1) s6_load(R, nxt, xq, xd, wq, wd, M, N, K, m0, n0, kb + 1);
+    i32x16 dsum[3][kSTM];
+    mmqs6_mfma(cur, dsum, wm, r, h, bcol);
+    mmqs6_epi<DUMP>(cur, dsum, acc, wm, r, h, bcol, m0, col, M, N, nbk, kb, dump);
+    if (kb + 1 < kb1) s6_store(R, nxt);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    __syncthreads();
+  }
+  mmqs_store(acc, y, M, N, ldy, m0, n0, accumulate);
+}
+
+}  // namespace qmm
+
+#define QMM_MMQS6_KERNEL(SUFFIX, DUMP)                                                                         \
+  extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))                 \
+      qmm_mmqs6_q6k##SUFFIX(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                     \
+                            const float* __restrict__ xd, const int16_t* __restrict__ xs,                      \
+                            float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,        \
+                            int accumulate, int remap, int kc, long long ysplit) {                             \
+    (void)xs;                                                                                                  \
+    const qmm::KRange kr = qmm::split_range(K, kc);                                                            \
+    qmm::mmqs6_q6k<DUMP>(wq, xq, xd, y + blockIdx.z * ysplit, M, N, K, ldy, dump, accumulate, remap, kr.kb0,   \
+                         kr.kb1);                                                                              \
+  }
+QMM_MMQS6_KERNEL(, false)
+QMM_MMQS6_KERNEL(_dump, true)
+
 extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 qmm_mmqs_q4k_sk(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq, const float* __restrict__ xd,
                 const int16_t* __restrict__ xs, float* __restrict__ y, int M, int N, int K, int ldy, int accumulate,

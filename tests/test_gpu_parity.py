@@ -415,6 +415,31 @@ def test_gemm_q4k_generations_bit_exact(monkeypatch, gen, n, k, m):
     assert rel_err(y2, orc.matmul(orc.Q4K, x, wq, k)) <= TOL
 
 
+@pytest.mark.parametrize("gen", [{}, {"QMM_MMQ6": "1"}])
+@pytest.mark.parametrize("n,k,m", [(300, 1024, 9), (130, 512, 257), (64, 256, 130), (257, 2048, 128)])
+def test_gemm_q6k_generations_bit_exact(monkeypatch, gen, n, k, m):
+    """Both Q6_K GEMM generations (the default mmqs6: each int8 sub-block scale as three digits in [-3, 4]
+    multiplied into the int8 MFMA operands; mmq<Q6_K>: masked MFMAs and a multiply-add per sub-block) give
+    the oracle's integer block dots and f32 outputs within TOL. The weight holds the saturating block (int8
+    scales -128 and 127, the ends of the digit range) and the tie block (odd scales), tiled along k."""
+    for key, val in gen.items():
+        monkeypatch.setenv(key, val)
+    w = np.concatenate([normal(190 + n, (n, k), 0.02), special_weight_rows(k)[:4],
+                        np.tile(quant_ties.q6k_saturating_block()[0], (2, k // 256)),
+                        np.tile(quant_ties.q6k_block()[0], (2, k // 256))]).astype(np.float32)
+    wq = orc.quantize(orc.Q6K, w)
+    qt = QTensor.from_ggml(wq, GgmlDType.Q6K, w.shape, device=DEV)
+    x = normal(191 + m, (m, k))
+    x[1, : k // 2] *= 40.0
+    x[2] = 0.0
+    xq = quantize_rows(GgmlDType.Q8K, torch.from_numpy(x).to(DEV))
+    dots, y = block_dots(qt, xq, m)
+    assert np.array_equal(dots.cpu().numpy(), orc.block_dots(orc.Q6K, wq, xq.cpu().numpy(), k))
+    assert rel_err(y.cpu().numpy(), orc.matmul_prequant(orc.Q6K, xq.cpu().numpy(), wq, k)) <= TOL
+    y2 = QMatMul.from_qtensor(qt).forward(torch.from_numpy(x).to(DEV)).cpu().numpy()
+    assert rel_err(y2, orc.matmul(orc.Q6K, x, wq, k)) <= TOL
+
+
 @pytest.mark.parametrize("dt,n,k,wseed", [(GgmlDType.Q4K, 14336, 4096, 6), (GgmlDType.Q4K, 4096, 14336, 6),
                                           (GgmlDType.Q6K, 4096, 14336, 6)])
 def test_prefill_config_shapes_match_cpu_path(dt, n, k, wseed):
