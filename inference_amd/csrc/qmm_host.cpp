@@ -2211,6 +2211,10 @@ static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, in
   const int bn = 128;
   unsigned lds = fmt == kFmtQ4K ? (unsigned)(2 * (bm * 272 + 128 * 144 + bm * 4 + bm * 16)) : 0u;
   unsigned threads = fmt == kFmtQ4K ? (unsigned)(bm * 4) : 256u;
+  // Q6_K keeps the first-generation 64-row tile here: the split-digit tile's
+  // 128-row tiles pad an expert's 129..143 rows to 256 (192 with 64-row
+  // tiles), and the 512-token config-5 prefill ran 1,086-1,146 us with it
+  // against 1,003-1,044 us
   char name[40];
   if (use_s) {
     snprintf(name, sizeof(name), "qmm_moe_mmqs_q4k");
@@ -2229,7 +2233,7 @@ static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, in
     if (const char* e = env(kEnvMoeSplitK)) {
       sp = std::max(1, atoi(e));
     } else if (part) {
-      const long long tiles = (pairs / kMmqBMRows + experts) * ((N + bn - 1) / bn);
+      const long long tiles = (pairs / bm + experts) * ((N + bn - 1) / bn);
       const long long slots = (long long)d->num_cu * std::max(1u, (unsigned)d->max_lds / kMmqStaticLds);
       long long best = -1;
       for (int c = 1; c <= std::min(8, nbk); ++c) {

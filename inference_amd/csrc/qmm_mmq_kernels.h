@@ -1766,17 +1766,17 @@ __device__ __forceinline__ void mmqs6_epi(const uint8_t* __restrict__ buf, const
   (void)r;
 }
 
+// wd: the weight's separated f16 d per block (row-major, K / 256 per row).
 template <bool DUMP>
-__device__ __forceinline__ void mmqs6_q6k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,
-                                          const float* __restrict__ xd, float* __restrict__ y, int M, int N, int K,
-                                          int ldy, int* __restrict__ dump, int accumulate, int remap, int kb0,
-                                          int kb1) {
+__device__ __forceinline__ void mmqs6_q6k(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                          const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                          float* __restrict__ y, int M, int N, int K, int ldy,
+                                          int* __restrict__ dump, int accumulate, int remap, int kb0, int kb1) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   int mt, nt;
   gemm_tile(remap, mt, nt);
   const int m0 = mt * kSBM, n0 = nt * kSBN;
   const int nbk = K / 256;
-  const uint16_t* wd = split_scales<kFmtQ6K>(wq, N, K);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 31, h = lane >> 5;
   const int wm = wave & 1, wn = wave >> 1;
@@ -1816,8 +1816,8 @@ __device__ __forceinline__ void mmqs6_q6k(const uint8_t* __restrict__ wq, const 
                             int accumulate, int remap, int kc, long long ysplit) {                             \
     (void)xs;                                                                                                  \
     const qmm::KRange kr = qmm::split_range(K, kc);                                                            \
-    qmm::mmqs6_q6k<DUMP>(wq, xq, xd, y + blockIdx.z * ysplit, M, N, K, ldy, dump, accumulate, remap, kr.kb0,   \
-                         kr.kb1);                                                                              \
+    qmm::mmqs6_q6k<DUMP>(wq, qmm::split_scales<qmm::kFmtQ6K>(wq, N, K), xq, xd, y + blockIdx.z * ysplit, M, N, \
+                         K, ldy, dump, accumulate, remap, kr.kb0, kr.kb1);                                     \
   }
 QMM_MMQS6_KERNEL(, false)
 QMM_MMQS6_KERNEL(_dump, true)

@@ -792,4 +792,5 @@ qmm_moe_mmqs_q4k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq, 
                          min(kb0 + kc, K / 256));                                                              \
   }
 QMM_MOE_MMQ_KERNEL(qmm::kFmtQ6K, q6k)
+
 QMM_MOE_MMQ_KERNEL(qmm::kFmtQ80, q8_0)
