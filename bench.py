@@ -640,8 +640,8 @@ def kernel_only(torch, dev, which, launches):
     `gate` = the Q4_K gate GEMV (14336x4096, M = 1, rotated weight copies); `qkvgu` / `qkvgu_staged`
     = the q/k/v/gate/up set in one launch (Q8_K in the prologue / pre-quantized activation);
     `copy` = a 256 MiB device copy (the calibration for FETCH_SIZE / WRITE_SIZE); `gemm_gate` / `gemm_down` =
-    the config-4 GEMMs (M = 512); `moe` = the config-5 expert FFN (`moe32`: at 32 tokens); `gate_m8` = the gate
-    GEMV on eight pre-quantized rows."""
+    the config-4 GEMMs (M = 512; `gemm_q6k_gate` / `gemm_q6k_down`: its Q6_K legs); `moe` = the config-5 expert
+    FFN (`moe32`: at 32 tokens); `gate_m8` = the gate GEMV on eight pre-quantized rows."""
     from inference_amd import GgmlDType, QTensor, qmm
     from inference_amd.synth import normal, normal_torch
     if which == "copy":
@@ -653,10 +653,13 @@ def kernel_only(torch, dev, which, launches):
         print(json.dumps({"kernel_only": "copy", "bytes_read": a.numel() * 4, "bytes_written": b.numel() * 4,
                           "launches": launches}), flush=True)
         return
-    if which in ("gemm_gate", "gemm_down"):
-        # config-4 GEMM: 512 rows N(0,1) seed 5 against a Q4_K weight N(0, 0.02^2) seed 6
-        n, k = (14336, 4096) if which == "gemm_gate" else (4096, 14336)
-        w = QTensor.quantize(normal_torch(6 if which == "gemm_gate" else 16, (n, k), 0.02, dev), GgmlDType.Q4K)
+    if which in ("gemm_gate", "gemm_down", "gemm_q6k_gate", "gemm_q6k_down"):
+        # config-4 GEMM: 512 rows N(0,1) seed 5 against a Q4_K weight N(0, 0.02^2) seed 6 / 16, or the Q6_K
+        # legs' weights (seeds 26 / 36)
+        n, k = (14336, 4096) if which.endswith("gate") else (4096, 14336)
+        q6 = "q6k" in which
+        seed = (26 if which.endswith("gate") else 36) if q6 else (6 if which == "gemm_gate" else 16)
+        w = QTensor.quantize(normal_torch(seed, (n, k), 0.02, dev), GgmlDType.Q6K if q6 else GgmlDType.Q4K)
         x = torch.from_numpy(normal(5, (512, k))).to(dev)
         y = torch.empty((512, n), dtype=torch.float32, device=dev)
         L = qmm.lib()
@@ -856,7 +859,8 @@ def main():
                          "their prologues; serial: one launch per projection")
     ap.add_argument("--decode-tokens", type=int, default=256, help="config-3 generated tokens (0 = skip)")
     ap.add_argument("--kernel-only", choices=("gate", "gate_m8", "qkvgu", "qkvgu_staged", "grouped", "copy",
-                                              "gemm_gate", "gemm_down", "moe", "moe32",
+                                              "gemm_gate", "gemm_down", "gemm_q6k_gate", "gemm_q6k_down", "moe",
+                                              "moe32",
                                               "q8_0", "down_q6k", "decode", "read_9mb", "read_33mb",
                                               "read_80mb", "read_1gb", "read_graph"),
                     default=None,
