@@ -52,6 +52,32 @@ __device__ __forceinline__ void gemvm_stage(const uint8_t* __restrict__ xs, long
   const int stride = gemvm_stride(K), nthr = 64 * NW;
   uint8_t* sums = lds + (size_t)mr * stride;
   float* dx = reinterpret_cast<float*>(sums + 256 * nb);
+  // the first (row, block)'s sums and scale are loaded with the quants (one
+  // memory round trip for both)
+  const int nsb = mr * nb;
+  uint32_t bs0[8];
+  float d0 = 0.0f;
+  if ((int)threadIdx.x < nsb) {
+    const int t = threadIdx.x / nb, b = threadIdx.x - t * nb;
+    const uint8_t* src = xs + t * xrow + (size_t)kQ8KBytes * b;
+    const uint32_t* bs = reinterpret_cast<const uint32_t*>(src + 4 + 256);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) bs0[j] = bs[j];
+    d0 = *reinterpret_cast<const float*>(src);
+  }
+  auto put_sums = [&](int i, const uint32_t* bs, float d) {
+    const int t = i / nb, b = i - t * nb;
+    uint32_t lo[2] = {0u, 0u}, hi[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t pr = bs[j];
+      const int S = (int)(int16_t)(pr & 0xffffu) + ((int)pr >> 16);  // 32-element sum, |S| <= 4096
+      lo[j >> 2] |= (uint32_t)(S & 63) << (8 * (j & 3));
+      hi[j >> 2] |= (uint32_t)((S >> 6) & 0xff) << (8 * (j & 3));
+    }
+    *reinterpret_cast<uint4*>(sums + 16 * (16 * b + t)) = make_uint4(lo[0], lo[1], hi[0], hi[1]);
+    dx[16 * b + t] = d;
+  };
   // quants: 16-byte pieces (4-byte aligned in the Q8_K blocks, so dword
   // loads), eight per thread in flight before their stores
   const int per = 16 * nb, tot = mr * per;
@@ -75,20 +101,15 @@ __device__ __forceinline__ void gemvm_stage(const uint8_t* __restrict__ xs, long
       }
     }
   }
-  for (int i = threadIdx.x; i < mr * nb; i += nthr) {
+  if ((int)threadIdx.x < nsb) put_sums(threadIdx.x, bs0, d0);
+  for (int i = threadIdx.x + nthr; i < nsb; i += nthr) {  // more (row, block) pairs than threads
     const int t = i / nb, b = i - t * nb;
     const uint8_t* src = xs + t * xrow + (size_t)kQ8KBytes * b;
     const uint32_t* bs = reinterpret_cast<const uint32_t*>(src + 4 + 256);  // 16 int16 16-element sums
-    uint32_t lo[2] = {0u, 0u}, hi[2] = {0u, 0u};
+    uint32_t v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t pr = bs[j];
-      const int S = (int)(int16_t)(pr & 0xffffu) + ((int)pr >> 16);  // 32-element sum, |S| <= 4096
-      lo[j >> 2] |= (uint32_t)(S & 63) << (8 * (j & 3));
-      hi[j >> 2] |= (uint32_t)((S >> 6) & 0xff) << (8 * (j & 3));
-    }
-    *reinterpret_cast<uint4*>(sums + 16 * (16 * b + t)) = make_uint4(lo[0], lo[1], hi[0], hi[1]);
-    dx[16 * b + t] = *reinterpret_cast<const float*>(src);
+    for (int j = 0; j < 8; ++j) v[j] = bs[j];
+    put_sums(i, v, *reinterpret_cast<const float*>(src));
   }
 }
 
