@@ -641,7 +641,8 @@ def kernel_only(torch, dev, which, launches):
     = the q/k/v/gate/up set in one launch (Q8_K in the prologue / pre-quantized activation);
     `copy` = a 256 MiB device copy (the calibration for FETCH_SIZE / WRITE_SIZE); `gemm_gate` / `gemm_down` =
     the config-4 GEMMs (M = 512; `gemm_q6k_gate` / `gemm_q6k_down`: its Q6_K legs); `moe` = the config-5 expert
-    FFN (`moe32`: at 32 tokens); `gate_m8` = the gate GEMV on eight pre-quantized rows."""
+    FFN (`moe32`: at 32 tokens); `gate_m8` = the gate GEMV on eight pre-quantized rows; `gate_up` = gate and up
+    in one launch with the RMSNorm + Q8_K prologue (the FFN pair as the decoder runs it)."""
     from inference_amd import GgmlDType, QTensor, qmm
     from inference_amd.synth import normal, normal_torch
     if which == "copy":
@@ -796,6 +797,23 @@ def kernel_only(torch, dev, which, launches):
         torch.cuda.synchronize()
         print(json.dumps({"kernel_only": which, "algorithmic_bytes": alg, "launches": launches}), flush=True)
         return
+    if which == "gate_up":
+        # the FFN pair as the decoder runs it: gate and up in one launch, RMSNorm + Q8_K of the f32 row in
+        # the prologue; 8 rotated copies of the pair (530 MB, more than the MALL)
+        pairs = [[QTensor.quantize(normal_torch(2 + 1000 * c + 17 * j, (14336, 4096), 0.02, dev), GgmlDType.Q4K)
+                  for j in (3, 4)] for c in range(8)]
+        hs = [(vp * 2)(*[q.handle.value for q in pr]) for pr in pairs]
+        nw = torch.from_numpy(normal(4, (4096,))).to(dev)
+        ys = [torch.empty(14336, dtype=torch.float32, device=dev) for _ in range(2)]
+        yp = (vp * 2)(*[y.data_ptr() for y in ys])
+        ld = (i64 * 2)(14336, 14336)
+        for i in range(launches):
+            qmm._check(L.qmm_matmul_ex(hs[i % 8], 2, x.data_ptr(), 1, 4096, nw.data_ptr(), ctypes.c_float(1e-5), 0,
+                                       yp, ld, None, 0, qmm._stream(dev)))
+        alg = 2 * gemv_bytes(12, 14336, 4096)  # the row once plus the norm weight: 2 x 4 x 4096
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel_only": which, "algorithmic_bytes": alg, "launches": launches}), flush=True)
+        return
     if which in ("gate", "gate_m8"):
         # gate_m8: eight pre-quantized Q8_K rows (the matrix-core multi-token GEMV)
         m = 8 if which == "gate_m8" else 1
@@ -858,7 +876,7 @@ def main():
                          "launch, quantize, down; fused: the same two GEMV launches with Q8_K quantization in "
                          "their prologues; serial: one launch per projection")
     ap.add_argument("--decode-tokens", type=int, default=256, help="config-3 generated tokens (0 = skip)")
-    ap.add_argument("--kernel-only", choices=("gate", "gate_m8", "qkvgu", "qkvgu_staged", "grouped", "copy",
+    ap.add_argument("--kernel-only", choices=("gate", "gate_m8", "gate_up", "qkvgu", "qkvgu_staged", "grouped", "copy",
                                               "gemm_gate", "gemm_down", "gemm_q6k_gate", "gemm_q6k_down", "moe",
                                               "moe32",
                                               "q8_0", "down_q6k", "decode", "read_9mb", "read_33mb",
