@@ -100,13 +100,13 @@ std::atomic<Device*> g_dev[64] = {};
 enum EnvKey {
   kEnvGemv1, kEnvGemv1p, kEnvGemvCfg, kEnvGemvWavesPerCu, kEnvGemvRows, kEnvSplitK, kEnvMmq2, kEnvMmq,
   kEnvMmq4Bn, kEnvMmq1, kEnvMmqXcd, kEnvMoeGemv, kEnvMoeMmq, kEnvMoeBm, kEnvMoeSplitK, kEnvMoeGrouped, kEnvGroupedP,
-  kEnvGroupedWgs, kEnvStreamK, kEnvGemvm, kEnvMmq6, kEnvCount
+  kEnvGroupedWgs, kEnvStreamK, kEnvGemvm, kEnvMmq6, kEnvMmq8, kEnvCount
 };
 const char* const kEnvNames[kEnvCount] = {
     "QMM_GEMV1", "QMM_GEMV1P", "QMM_GEMV_CFG", "QMM_GEMV_WAVES_PER_CU", "QMM_GEMV_ROWS", "QMM_SPLITK",
     "QMM_MMQ2", "QMM_MMQ", "QMM_MMQ4_BN", "QMM_MMQ1", "QMM_MMQ_XCD", "QMM_MOE_GEMV", "QMM_MOE_MMQ",
     "QMM_MOE_BM", "QMM_MOE_SPLITK", "QMM_MOE_GROUPED", "QMM_GROUPED_P", "QMM_GROUPED_WGS",
-    "QMM_STREAMK", "QMM_GEMVM", "QMM_MMQ6"};
+    "QMM_STREAMK", "QMM_GEMVM", "QMM_MMQ6", "QMM_MMQ8"};
 
 struct Tuning {
   int w = 0, r = 0, u = 0, waves_per_cu = 0, gemv1 = 1, gemv1p = -1;
@@ -824,6 +824,9 @@ static constexpr unsigned kMmqStaticLds = 61440;  // the first-generation tile's
 // codes, digit bytes, column d, row scales (128 x 256, 128 x 256, 128 x 48,
 // 128 x 4, 128 x 4 bytes)
 static constexpr unsigned kS6StageBytes = 128 * 256 + 128 * 256 + 128 * 48 + 128 * 4 + 128 * 4;
+// One LDS stage of the Q8_0 tile (mmqs8): activation rows, weight codes, f32
+// weight and activation block scales (the kernels' kS8Stage).
+static constexpr unsigned kS8StageBytes = 128 * 256 + 128 * 256 + 128 * 32 + 8 * 128 * 4;
 static constexpr int kMmqBMRows = 64;             // and its M tile
 static void plan_splits(const Device* d, GemmPlan& p, int nbk) {
   const long long tiles = (long long)p.gx * p.gy;
@@ -941,6 +944,14 @@ static GemmPlan gemm_plan(const Device* d, const qmm_qtensor* w, int64_t m, bool
     p.gy = (unsigned)((M + 127) / 128);
     p.threads = 512;
     p.lds = 2 * kS6StageBytes;
+  } else if (fmt == kFmtQ80 && env(kEnvMmq8) == nullptr && (int)(2 * kS8StageBytes) <= d->max_lds) {
+    // Q8_0 default: mmqs8 (both operands straight into LDS, 128 x 128 tiles of eight waves, LDS 2 x 72 KB);
+    // QMM_MMQ8=1 selects the first-generation tile
+    snprintf(p.name, sizeof(p.name), "qmm_mmqs8_q8_0%s", dump ? "_dump" : "");
+    p.gx = (unsigned)((N + 127) / 128);
+    p.gy = (unsigned)((M + 127) / 128);
+    p.threads = 512;
+    p.lds = 2 * kS8StageBytes;
   } else if (fmt == kFmtQ4K && (int)lds2 <= d->max_lds && env(kEnvMmq1) == nullptr) {
     snprintf(p.name, sizeof(p.name), "qmm_mmq2_q4k_m%d_n%d%s", bm, bn, dump ? "_dump" : "");
     p.gx = (unsigned)((N + bn - 1) / bn);
@@ -983,6 +994,7 @@ static size_t gemm_sk_bytes(const Device* d, const qmm_qtensor* w, int64_t m) {
 static int gemm_launch(Device* d, const qmm_qtensor* w, const uint8_t* ws, int64_t m, const GemmPlan& p, float* y,
                        int64_t ldy, int* dump, hipStream_t s, int accumulate, float* part, void* sk_scratch) {
   const Planes pl = mmq_planes(w->dtype, m, w->k);
+  if ((uintptr_t)ws % 16) return fail(QMM_ERR_INVALID, "GEMM workspaces must be 16-byte aligned");
   const bool split = p.splits > 1;
   const void* wq = w->data;
   const void* q8 = ws + pl.q8;

@@ -1806,7 +1806,190 @@ __device__ __forceinline__ void mmqs6_q6k(const uint8_t* __restrict__ wq, const 
   mmqs_store(acc, y, M, N, ldy, m0, n0, accumulate);
 }
 
+// Q8_0 prefill GEMM on the mmqs scaffold (mmqs8_q8_0): 128 x 128 tiles of
+// eight waves (four along M, two along N; each wave 32 rows x 64 columns), two
+// LDS stages. Per 256-wide K step both operands are plain int8 rows of 256
+// bytes (eight 32-blocks), so the activation rows and the weight codes both go
+// from global memory straight into LDS (global_load_lds, 16-byte chunks
+// swizzled by row / column as in mmqs); only the block scales pass through
+// registers (the weight's f16 d as f32 [col][8], the activation's f32 d
+// transposed to [block][row] so that four consecutive rows are one float4).
+// Per 32-block one int8 MFMA per 32 x 32 tile gives the block dot P exactly;
+// acc = fma(dw * dx, float(P), acc), the first-generation tile's sequence, so
+// the outputs equal its bits.
+constexpr int kS8OffBq = kSBM * 256;             // weight codes [col][256], swizzled 16-byte slots
+constexpr int kS8OffDw = kS8OffBq + kSBN * 256;  // f32 d [col][8]
+constexpr int kS8OffDx = kS8OffDw + kSBN * 32;   // f32 d [block][row]
+constexpr int kS8Stage = kS8OffDx + 8 * kSBM * 4;
+
+struct SRegs8 {
+  uint4 dw;   // t < 128: column t's eight f16 block scales
+  float4 dx;  // 128 <= t < 384: block scales 4 q .. 4 q + 3 of row (t - 128) / 2 (q = t & 1)
+};
+
+// Global loads of one K step: activation rows and weight codes straight into
+// stage `stg` (wave w: rows / columns 16 w .. 16 w + 15, four instructions of
+// four each); the scales into registers. Rows and columns past M / N repeat
+// the last one (their outputs are never stored).
+__device__ __forceinline__ void s8_load(SRegs8& R, uint8_t* stg, const int8_t* __restrict__ xq,
+                                        const float* __restrict__ xd, const uint8_t* __restrict__ wq,
+                                        const uint16_t* __restrict__ wd, int M, int N, int K, int m0, int n0,
+                                        int kb) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nbw = K / 32;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int row = 16 * wave + 4 * u + (lane >> 4);
+    const int gr = min(m0 + row, M - 1);
+    lds_dma16(xq + (size_t)gr * K + 256 * kb + 16 * ((lane & 15) ^ (row & 15)), stg + 256 * (16 * wave + 4 * u));
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int col = 16 * wave + 4 * u + (lane >> 4);
+    const int gc = min(n0 + col, N - 1);
+    lds_dma16(wq + ((size_t)gc * nbw + 8 * kb) * kQ80Body + 16 * ((lane & 15) ^ (col & 15)),
+              stg + kS8OffBq + 256 * (16 * wave + 4 * u));
+  }
+  if (t < 128) {
+    const int gc = min(n0 + t, N - 1);
+    R.dw = *reinterpret_cast<const uint4*>(wd + (size_t)gc * nbw + 8 * kb);
+  } else if (t < 384) {
+    const int i = t - 128;
+    const int gr = min(m0 + (i >> 1), M - 1);
+    R.dx = *reinterpret_cast<const float4*>(xd + (size_t)gr * nbw + 8 * kb + 4 * (i & 1));
+  }
+}
+
+__device__ __forceinline__ void s8_store(const SRegs8& R, uint8_t* buf) {
+  const int t = threadIdx.x;
+  if (t < 128) {
+    float* dw = reinterpret_cast<float*>(buf + kS8OffDw) + 8 * t;
+    const uint32_t v[4] = {R.dw.x, R.dw.y, R.dw.z, R.dw.w};
+    *reinterpret_cast<float4*>(dw) = make_float4(h2f(v[0]), h2f(v[0] >> 16), h2f(v[1]), h2f(v[1] >> 16));
+    *reinterpret_cast<float4*>(dw + 4) = make_float4(h2f(v[2]), h2f(v[2] >> 16), h2f(v[3]), h2f(v[3] >> 16));
+  } else if (t < 384) {
+    const int i = t - 128, row = i >> 1, q = i & 1;
+    float* dx = reinterpret_cast<float*>(buf + kS8OffDx);
+    dx[(4 * q) * kSBM + row] = R.dx.x;
+    dx[(4 * q + 1) * kSBM + row] = R.dx.y;
+    dx[(4 * q + 2) * kSBM + row] = R.dx.z;
+    dx[(4 * q + 3) * kSBM + row] = R.dx.w;
+  }
+}
+
+// One K step from stage `buf`. Wave w owns rows 32 (w & 3) .. + 32 and the
+// two 32-column tiles of columns 64 (w >> 2) .. + 64, so a lane's 16 outputs
+// per tile share their rows across both tiles: per 32-block c the lane reads
+// its rows' 16 activation scales once (four float4 from the [block][row]
+// layout) and one weight scale per tile. Per tile j, P = the MFMA block dot,
+// acc += (dw * dx) * P. DUMP: every block dot.
+template <bool DUMP>
+__device__ __forceinline__ void mmqs8_step(const uint8_t* __restrict__ buf, f32x16 (&acc)[2], int wm, int wn, int r,
+                                           int h, int m0, int n0, int M, int N, int nbw, int kb,
+                                           int* __restrict__ dump) {
+#pragma clang fp contract(off)
+  i32x16 zero;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) zero[j] = 0;
+  const int arow = 32 * wm + r, sa = r & 15;
+  const int8_t* A = reinterpret_cast<const int8_t*>(buf) + 256 * arow;
+  const int8_t* B = reinterpret_cast<const int8_t*>(buf + kS8OffBq) + 256 * (64 * wn + r);
+  const float* DW = reinterpret_cast<const float*>(buf + kS8OffDw) + 8 * (64 * wn + r);
+  const float* DX = reinterpret_cast<const float*>(buf + kS8OffDx) + 32 * wm + 4 * h;
+  // two blocks at a time (fully unrolled, the compiler hoists every MFMA of
+  // the step ahead of the epilogues and spills)
+#pragma unroll 2
+  for (int c = 0; c < 8; ++c) {
+    const int slot = 2 * c + h;  // 16-byte chunk of this lane half
+    const i8x16 a = *reinterpret_cast<const i8x16*>(A + 16 * (slot ^ sa));
+    float dxs[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 dx = *reinterpret_cast<const float4*>(DX + c * kSBM + 8 * g);
+      dxs[4 * g] = dx.x;
+      dxs[4 * g + 1] = dx.y;
+      dxs[4 * g + 2] = dx.z;
+      dxs[4 * g + 3] = dx.w;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      // columns 32 j + r: the swizzle of column 64 wn + 32 j + r is r & 15
+      const i8x16 b = *reinterpret_cast<const i8x16*>(B + 256 * 32 * j + 16 * (slot ^ sa));
+      const float dwc = DW[256 * j + c];
+      const i32x16 P = mfma_i8(a, b, zero);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        acc[j][e] = __builtin_fmaf(dwc * dxs[e], (float)P[e], acc[j][e]);
+        if (DUMP) {
+          const int row = m0 + 32 * wm + 8 * (e >> 2) + 4 * h + (e & 3), col = n0 + 64 * wn + 32 * j + r;
+          if (row < M && col < N) dump[((size_t)row * N + col) * nbw + 8 * kb + c] = P[e];
+        }
+      }
+    }
+  }
+}
+
+// wd: the weight's separated f16 d per 32-block (row-major, K / 32 per row).
+template <bool DUMP>
+__device__ __forceinline__ void mmqs8_q8_0(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                           const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                           float* __restrict__ y, int M, int N, int K, int ldy,
+                                           int* __restrict__ dump, int accumulate, int remap, int kb0, int kb1) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  int mt, nt;
+  gemm_tile(remap, mt, nt);
+  const int m0 = mt * kSBM, n0 = nt * kSBN;
+  const int nbw = K / 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int wm = wave & 3, wn = wave >> 2;
+  f32x16 acc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
+  SRegs8 R;
+  s8_load(R, lds, xq, xd, wq, wd, M, N, K, m0, n0, kb0);
+  s8_store(R, lds);
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+  __syncthreads();
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const uint8_t* cur = lds + ((kb - kb0) & 1) * kS8Stage;
+    uint8_t* nxt = lds + ((kb + 1 - kb0) & 1) * kS8Stage;
+    if (kb + 1 < kb1) s8_load(R, nxt, xq, xd, wq, wd, M, N, K, m0, n0, kb + 1);
+    mmqs8_step<DUMP>(cur, acc, wm, wn, r, h, m0, n0, M, N, nbw, kb, dump);
+    if (kb + 1 < kb1) s8_store(R, nxt);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = n0 + 64 * wn + 32 * j + r;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int row = m0 + 32 * wm + 8 * (e >> 2) + 4 * h + (e & 3);
+      if (row < M && col < N) {
+        float* yp = y + (size_t)row * ldy + col;
+        *yp = accumulate ? *yp + acc[j][e] : acc[j][e];
+      }
+    }
+  }
+}
+
 }  // namespace qmm
+
+#define QMM_MMQS8_KERNEL(SUFFIX, DUMP)                                                                         \
+  extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))                 \
+      qmm_mmqs8_q8_0##SUFFIX(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq,                    \
+                             const float* __restrict__ xd, const int16_t* __restrict__ xs,                     \
+                             float* __restrict__ y, int M, int N, int K, int ldy, int* __restrict__ dump,       \
+                             int accumulate, int remap, int kc, long long ysplit) {                            \
+    (void)xs;                                                                                                  \
+    const qmm::KRange kr = qmm::split_range(K, kc);                                                            \
+    qmm::mmqs8_q8_0<DUMP>(wq, qmm::split_scales<qmm::kFmtQ80>(wq, N, K), xq, xd, y + blockIdx.z * ysplit, M, N, \
+                          K, ldy, dump, accumulate, remap, kr.kb0, kr.kb1);                                    \
+  }
+QMM_MMQS8_KERNEL(, false)
+QMM_MMQS8_KERNEL(_dump, true)
 
 #define QMM_MMQS6_KERNEL(SUFFIX, DUMP)                                                                         \
   extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))                 \

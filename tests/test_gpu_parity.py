@@ -440,6 +440,34 @@ def test_gemm_q6k_generations_bit_exact(monkeypatch, gen, n, k, m):
     assert rel_err(y2, orc.matmul(orc.Q6K, x, wq, k)) <= TOL
 
 
+@pytest.mark.parametrize("n,k,m", [(300, 1024, 9), (130, 512, 257), (64, 256, 130), (257, 2048, 128)])
+def test_gemm_q8_0_generations_bit_exact(monkeypatch, n, k, m):
+    """Both Q8_0 GEMM generations (the default mmqs8: activation rows and weight codes straight into LDS,
+    128 x 128 tiles of eight waves; mmq<Q8_0>: 64 x 128 tiles staged through registers) give the oracle's
+    integer block dots, and the same f32 outputs bit for bit (the same multiply-add per block in the same
+    order), within TOL of the oracle; also through the f32 entry point."""
+    w = np.concatenate([normal(200 + n, (n, k), 0.02), special_weight_rows(k)[:4]]).astype(np.float32)
+    wq = orc.quantize(orc.Q8_0, w)
+    qt = QTensor.from_ggml(wq, GgmlDType.Q8_0, w.shape, device=DEV)
+    x = normal(201 + m, (m, k))
+    x[1, : k // 2] *= 40.0
+    x[2] = 0.0
+    xq = quantize_rows(GgmlDType.Q8_0, torch.from_numpy(x).to(DEV))
+    ref_dots = orc.block_dots(orc.Q8_0, wq, xq.cpu().numpy(), k)
+    outs = []
+    for gen in ({}, {"QMM_MMQ8": "1"}):
+        monkeypatch.delenv("QMM_MMQ8", raising=False)
+        for key, val in gen.items():
+            monkeypatch.setenv(key, val)
+        dots, y = block_dots(qt, xq, m)
+        assert np.array_equal(dots.cpu().numpy(), ref_dots), gen
+        y2 = QMatMul.from_qtensor(qt).forward(torch.from_numpy(x).to(DEV))
+        assert rel_err(y2.cpu().numpy(), orc.matmul(orc.Q8_0, x, wq, k)) <= TOL
+        outs.append((y, y2))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    assert rel_err(outs[0][0].cpu().numpy(), orc.matmul_prequant(orc.Q8_0, xq.cpu().numpy(), wq, k)) <= TOL
+
+
 @pytest.mark.parametrize("dt,n,k,wseed", [(GgmlDType.Q4K, 14336, 4096, 6), (GgmlDType.Q4K, 4096, 14336, 6),
                                           (GgmlDType.Q6K, 4096, 14336, 6)])
 def test_prefill_config_shapes_match_cpu_path(dt, n, k, wseed):
