@@ -1079,8 +1079,10 @@ __device__ __forceinline__ void mmq4_q4k(const uint8_t* __restrict__ wq, const i
 //     registers, no LDS store instructions) while this step computes. The
 //     rows (256 bytes) and the quant runs (128 bytes) are unpadded; 16-byte
 //     chunk c of row r sits at slot c ^ (r & 15), chunk k of column n at
-//     slot k ^ (n & 7), so the MFMA operand reads of 32 rows or columns at
-//     one chunk spread over all banks. Threads 0..127 load column t's block
+//     slot k ^ ((n >> 1) & 7), so the MFMA operand reads of 32 rows or
+//     columns at one chunk spread over all 64 banks (a 16-byte LDS read
+//     serves 16 lanes at a time: columns n and n + 8 share a slot under
+//     k ^ (n & 7) and their 128-byte runs the same bank half). Threads 0..127 load column t's block
 //     header and form B' and the split-scale multipliers as packed 16-bit
 //     pairs; threads 128..255 load row t - 128's scale and sums and form A'
 //     (waves 0, 1 and 2, 3: the staging arithmetic lands on all four SIMDs,
@@ -1141,7 +1143,7 @@ __device__ __forceinline__ void s_load(SRegs& R, uint8_t* stg, const int8_t* __r
   for (int u = 0; u < 2; ++u) {
     const int col = 16 * wave + 8 * u + (lane >> 3);
     const int gc = min(n0 + col, N - 1);
-    lds_dma16(wq + ((size_t)gc * nbk + kb) * kQ4KBytes + 16 + 16 * ((lane & 7) ^ (col & 7)),
+    lds_dma16(wq + ((size_t)gc * nbk + kb) * kQ4KBytes + 16 + 16 * ((lane & 7) ^ ((col >> 1) & 7)),
               stg + kSOffBq + 128 * (16 * wave + 8 * u));
   }
   if (t < 128) {
@@ -1252,7 +1254,7 @@ __device__ __forceinline__ void mmqs_mfma(const uint8_t* __restrict__ buf, i32x1
 #pragma unroll
   for (int j = 0; j < 16; ++j) zero[j] = 0;
   const int arow0 = 64 * wm + r;
-  const int sa = r & 15, sb = r & 7;  // the swizzles of rows arow0 + 32 i and of column bcol
+  const int sa = r & 15, sb = (r >> 1) & 7;  // the swizzles of rows arow0 + 32 i and of column bcol
   const int8_t* A = reinterpret_cast<const int8_t*>(buf);
   const uint8_t* Bq = buf + kSOffBq + 128 * bcol;
   const uint4* SC = reinterpret_cast<const uint4*>(buf + kSOffSc + kSScStride * bcol);
