@@ -596,26 +596,51 @@ QMM_PREFILL_ATTN_KERNELS(1)
 QMM_PREFILL_ATTN_KERNELS(2)
 QMM_PREFILL_ATTN_KERNELS(4)
 
-// hq = Q8_K(silu(g) * u) for `rows` rows of k elements (one wave per block).
-extern "C" __global__ void __launch_bounds__(256) qmm_silu_mul_q8k(const float* __restrict__ g,
-                                                                   const float* __restrict__ u, long long ld,
-                                                                   uint8_t* __restrict__ hq, int k, int rows) {
+// One Q8_K block of silu(g) * u (one wave): the 256 elements at g / u
+// into the 292-byte block at blk.
+namespace qmm {
+__device__ __forceinline__ void silu_mul_q8k_block(const float* __restrict__ g, const float* __restrict__ u,
+                                                   uint8_t* __restrict__ blk, int lane) {
 #pragma clang fp contract(off)
-  const int nb = k / 256;
-  const long long w = (long long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (w >= (long long)rows * nb) return;
-  const int row = (int)(w / nb), b = (int)(w % nb), lane = threadIdx.x & 63;
-  const long long o = row * ld + 256LL * b + 4 * lane;
   float e[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) e[j] = qmm::silu_mul(g[o + j], u[o + j]);
-  const qmm::Q8KLane q = qmm::q8k_lane_vals(e[0], e[1], e[2], e[3], lane);
-  uint8_t* blk = hq + w * qmm::kQ8KBytes;
+  for (int j = 0; j < 4; ++j) e[j] = silu_mul(g[4 * lane + j], u[4 * lane + j]);
+  const Q8KLane q = q8k_lane_vals(e[0], e[1], e[2], e[3], lane);
   reinterpret_cast<uint32_t*>(blk + 4)[lane] = q.packed;
   const int next = __shfl_down(q.sum16, 4);
   if ((lane & 7) == 0)
     reinterpret_cast<uint32_t*>(blk + 4 + 256)[lane >> 3] = ((uint32_t)q.sum16 & 0xffffu) | ((uint32_t)next << 16);
   if (lane == 0) *reinterpret_cast<float*>(blk) = q.d;
+}
+}  // namespace qmm
+
+// hq = Q8_K(silu(g) * u) for `rows` rows of k elements (one wave per block).
+extern "C" __global__ void __launch_bounds__(256) qmm_silu_mul_q8k(const float* __restrict__ g,
+                                                                   const float* __restrict__ u, long long ld,
+                                                                   uint8_t* __restrict__ hq, int k, int rows) {
+  const int nb = k / 256;
+  const long long w = (long long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (w >= (long long)rows * nb) return;
+  const int row = (int)(w / nb), b = (int)(w % nb);
+  const long long o = row * ld + 256LL * b;
+  qmm::silu_mul_q8k_block(g + o, u + o, hq + w * qmm::kQ8KBytes, threadIdx.x & 63);
+}
+
+// The same for the rows of per-expert ranges only: rows ot[e] .. ot[e] +
+// ct[e] - 1 (ct[e] <= maxrows) of every expert e (the grouped prefill GEMM's
+// tails, see qmm_moe_split_tails); row r's blocks land at hq + r * nb * 292.
+extern "C" __global__ void __launch_bounds__(256) qmm_silu_mul_q8k_ranges(const float* __restrict__ g,
+                                                                          const float* __restrict__ u, long long ld,
+                                                                          uint8_t* __restrict__ hq, int k, int E,
+                                                                          int maxrows, const int* __restrict__ ct,
+                                                                          const int* __restrict__ ot) {
+  const int nb = k / 256;
+  const long long w = (long long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (w >= (long long)E * maxrows * nb) return;
+  const int b = (int)(w % nb), i = (int)((w / nb) % maxrows), e = (int)(w / ((long long)nb * maxrows));
+  if (i >= ct[e]) return;
+  const long long row = ot[e] + i, o = row * ld + 256LL * b;
+  qmm::silu_mul_q8k_block(g + o, u + o, hq + (row * nb + b) * qmm::kQ8KBytes, threadIdx.x & 63);
 }
 
 // Greedy step end: the argmax of logits (lowest index on ties) becomes

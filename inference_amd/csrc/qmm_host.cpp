@@ -100,13 +100,13 @@ std::atomic<Device*> g_dev[64] = {};
 enum EnvKey {
   kEnvGemv1, kEnvGemv1p, kEnvGemvCfg, kEnvGemvWavesPerCu, kEnvGemvRows, kEnvSplitK, kEnvMmq2, kEnvMmq,
   kEnvMmq4Bn, kEnvMmq1, kEnvMmqXcd, kEnvMoeGemv, kEnvMoeMmq, kEnvMoeBm, kEnvMoeSplitK, kEnvMoeGrouped, kEnvGroupedP,
-  kEnvGroupedWgs, kEnvStreamK, kEnvGemvm, kEnvMmq6, kEnvMmq8, kEnvCount
+  kEnvGroupedWgs, kEnvStreamK, kEnvGemvm, kEnvMmq6, kEnvMmq8, kEnvMoeTails, kEnvCount
 };
 const char* const kEnvNames[kEnvCount] = {
     "QMM_GEMV1", "QMM_GEMV1P", "QMM_GEMV_CFG", "QMM_GEMV_WAVES_PER_CU", "QMM_GEMV_ROWS", "QMM_SPLITK",
     "QMM_MMQ2", "QMM_MMQ", "QMM_MMQ4_BN", "QMM_MMQ1", "QMM_MMQ_XCD", "QMM_MOE_GEMV", "QMM_MOE_MMQ",
     "QMM_MOE_BM", "QMM_MOE_SPLITK", "QMM_MOE_GROUPED", "QMM_GROUPED_P", "QMM_GROUPED_WGS",
-    "QMM_STREAMK", "QMM_GEMVM", "QMM_MMQ6", "QMM_MMQ8"};
+    "QMM_STREAMK", "QMM_GEMVM", "QMM_MMQ6", "QMM_MMQ8", "QMM_MOE_TAILS"};
 
 struct Tuning {
   int w = 0, r = 0, u = 0, waves_per_cu = 0, gemv1 = 1, gemv1p = -1;
@@ -2049,6 +2049,38 @@ int qmm_moe_route(const float* logits, int64_t tokens, int experts, int topk, in
 // max_count bounds every counts[e] (the token count under top-k routing, else
 // the pair count): the ring kernel runs one 8-token pass per workgroup, grid y
 // = the passes an expert can need.
+// Token rows per pass of the matrix-core expert GEMV (qmm_moe_gemvm_q4k) for
+// weights of w's K: up to 16, as many as the staged rows' LDS allows.
+static int moe_gemvm_rows(const Device* d, const qmm_qtensor* w) {
+  const long long K = w->k, nb = K / 256;
+  return (int)std::min<long long>(16, (d->max_lds - 320LL * nb - 2048) / (K + 16));
+}
+
+// The matrix-core expert GEMV (Q4_K experts) over Q8_K rows at xq: passes of
+// moe_gemvm_rows tokens up to a bound of max_count per expert.
+static int moe_gemvm(Device* d, const qmm_qtensor* const* w, int count, int experts, const void* xq, int64_t pairs,
+                     int64_t max_count, const int32_t* counts, const int32_t* offsets, float* const* y,
+                     hipStream_t s) {
+  int K = (int)w[0]->k;
+  const int nb = K / 256, mt = moe_gemvm_rows(d, w[0]);
+  const long long gpasses = (std::max<long long>(std::min<long long>(max_count, pairs), 1) + mt - 1) / mt;
+  const int vt = qmm_vec_dot_type(w[0]->dtype);
+  long long xrow = (w[0]->k / qmm_block_size(vt)) * qmm_type_size(vt);
+  int N = (int)(w[0]->n / experts), E = experts, nj = count, ld = N, mtt = mt;
+  const void* w0 = w[0]->data;
+  const void* w1 = count > 1 ? w[1]->data : w[0]->data;
+  float* y0 = y[0];
+  float* y1 = count > 1 ? y[1] : y[0];
+  const void* xp = xq;
+  void* args[] = {&w0, &w1, &nj, &N, &E, &y0, &y1, &ld, &xp, &xrow, &counts, &offsets, &K, &mtt};
+  hipFunction_t f;
+  QMM_TRY(kernel(d, "qmm_moe_gemvm_q4k_w4_p4", &f));
+  const long long gr = std::max<long long>((long long)d->num_cu * 4, E);
+  QMM_HIP(hipModuleLaunchKernel(f, (unsigned)gr, (unsigned)gpasses, 1, 256, 1, 1,
+                                (unsigned)(mt * (K + 16) + 320 * nb), s, args, nullptr));
+  return QMM_OK;
+}
+
 static int moe_gemv(const qmm_qtensor* const* w, int count, int experts, const void* xq, int64_t pairs,
                     int64_t max_count, const int32_t* counts, const int32_t* offsets, float* const* y, void* stream) {
   if (!w || !y || !xq || !counts || !offsets || count < 1 || count > 2)
@@ -2086,28 +2118,8 @@ static int moe_gemv(const qmm_qtensor* const* w, int count, int experts, const v
   // never, 1 for every Q4_K call the ring kernel would take.
   int gvm = -1;
   if (const char* e = env(kEnvGemvm)) gvm = atoi(e);
-  if (ring && fmt == kFmtQ4K && (gvm > 0 || (gvm < 0 && pairs >= 6LL * experts))) {
-    int K = (int)w[0]->k;
-    const int mt = (int)std::min<long long>(16, (d->max_lds - 320LL * nb - 2048) / (K + 16));
-    if (mt >= 1) {
-      const long long gpasses = (std::max<long long>(std::min<long long>(max_count, pairs), 1) + mt - 1) / mt;
-      const int vt = qmm_vec_dot_type(w[0]->dtype);
-      long long xrow = (w[0]->k / qmm_block_size(vt)) * qmm_type_size(vt);
-      int N = (int)(w[0]->n / experts), E = experts, nj = count, ld = N, mtt = mt;
-      const void* w0 = w[0]->data;
-      const void* w1 = count > 1 ? w[1]->data : w[0]->data;
-      float* y0 = y[0];
-      float* y1 = count > 1 ? y[1] : y[0];
-      const void* xp = xq;
-      void* args[] = {&w0, &w1, &nj, &N, &E, &y0, &y1, &ld, &xp, &xrow, &counts, &offsets, &K, &mtt};
-      hipFunction_t f;
-      QMM_TRY(kernel(d, "qmm_moe_gemvm_q4k_w4_p4", &f));
-      const long long gr = std::max<long long>((long long)d->num_cu * 4, E);
-      QMM_HIP(hipModuleLaunchKernel(f, (unsigned)gr, (unsigned)gpasses, 1, 256, 1, 1,
-                                    (unsigned)(mt * (K + 16) + 320 * nb), (hipStream_t)stream, args, nullptr));
-      return QMM_OK;
-    }
-  }
+  if (ring && fmt == kFmtQ4K && (gvm > 0 || (gvm < 0 && pairs >= 6LL * experts)) && moe_gemvm_rows(d, w[0]) >= 1)
+    return moe_gemvm(d, w, count, experts, xq, pairs, max_count, counts, offsets, y, (hipStream_t)stream);
   char name[48];
   if (ring)
     snprintf(name, sizeof(name), "qmm_moe_gemv1_%s_p%d", fmt_name(fmt), ring);
@@ -2159,7 +2171,8 @@ size_t qmm_moe_gemm_workspace_size(const qmm_qtensor* w, int64_t pairs) {
 
 static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, int experts, const uint8_t* planes,
                            int64_t pairs, int64_t max_rows, const int32_t* counts, const int32_t* offsets,
-                           float* const* y, hipStream_t s, float* part = nullptr, size_t part_bytes = 0);
+                           float* const* y, hipStream_t s, float* part = nullptr, size_t part_bytes = 0,
+                           bool whole_tiles = false);
 
 int qmm_moe_gemm(const qmm_qtensor* const* w, int count, int experts, const float* x, int64_t pairs, int64_t ldx,
                  int64_t max_rows, const int32_t* counts, const int32_t* offsets, float* const* y, void* ws,
@@ -2200,7 +2213,7 @@ int qmm_moe_gemm(const qmm_qtensor* const* w, int count, int experts, const floa
 // 2.5 rounds of 28. QMM_MOE_SPLITK=<S> forces S (0 or 1: unsplit).
 static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, int experts, const uint8_t* planes,
                            int64_t pairs, int64_t max_rows, const int32_t* counts, const int32_t* offsets,
-                           float* const* y, hipStream_t s, float* part, size_t part_bytes) {
+                           float* const* y, hipStream_t s, float* part, size_t part_bytes, bool whole_tiles) {
   const qmm_qtensor* w0 = w[0];
   const Planes pl = mmq_planes(w0->dtype, pairs, w0->k);
   const int fmt = fmt_of(w0->dtype);
@@ -2227,10 +2240,18 @@ static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, in
   // 128-row tiles pad an expert's 129..143 rows to 256 (192 with 64-row
   // tiles), and the 512-token config-5 prefill ran 1,086-1,146 us with it
   // against 1,003-1,044 us
+  // whole_tiles (the tails' split left most experts a multiple of 128 GEMM
+  // rows): Q6_K on the split-digit tile
+  const bool use_s6 = whole_tiles && fmt == kFmtQ6K && (int)(2 * kS6StageBytes) <= d->max_lds;
   char name[40];
   if (use_s) {
     snprintf(name, sizeof(name), "qmm_moe_mmqs_q4k");
     lds = ldss;
+    threads = 512;
+  } else if (use_s6) {
+    snprintf(name, sizeof(name), "qmm_moe_mmqs6_q6k");
+    bm = 128;
+    lds = 2 * kS6StageBytes;
     threads = 512;
   } else if (fmt == kFmtQ4K) {
     snprintf(name, sizeof(name), "qmm_moe_mmq2_q4k%s", bm == 64 ? "_m64" : "");
@@ -2246,7 +2267,7 @@ static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, in
       sp = std::max(1, atoi(e));
     } else if (part) {
       const long long tiles = (pairs / bm + experts) * ((N + bn - 1) / bn);
-      const long long slots = (long long)d->num_cu * std::max(1u, (unsigned)d->max_lds / kMmqStaticLds);
+      const long long slots = (long long)d->num_cu * std::max(1u, (unsigned)d->max_lds / (use_s6 ? lds : kMmqStaticLds));
       long long best = -1;
       for (int c = 1; c <= std::min(8, nbk); ++c) {
         const int kcc = (nbk + c - 1) / c;
@@ -2295,6 +2316,14 @@ static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, in
 // when the routed pairs average more than this many rows per expert: the
 // GEMV streams an expert's weights once per eight rows, the GEMM once per
 // 128-row tile. QMM_MOE_GROUPED=0/1 forces the choice.
+// Grouped prefill tails (see qmm_moe_split_tails): at most this many rows per
+// expert go to the expert GEMV; QMM_MOE_TAILS=0 keeps every row in the GEMM.
+constexpr int kMoeTailRows = 16;
+static bool moe_tails_enabled() {
+  const char* e = env(kEnvMoeTails);
+  return !(e && atoi(e) == 0);
+}
+
 static bool moe_grouped(int64_t pairs, int experts) {
   if (const char* e = env(kEnvMoeGrouped)) return atoi(e) != 0;
   return pairs > 16LL * experts;
@@ -2303,6 +2332,7 @@ static bool moe_grouped(int64_t pairs, int experts) {
 // Workspace of qmm_moe_ffn, carved in this order.
 struct MoeWs {
   size_t counts, offsets, pair_token, pair_weight, token_pairs, xg, xq, g, u, h, hq, yp, planes;
+  size_t tails;  // grouped prefill: per expert the GEMM rows, the tail rows and the tails' first row
   size_t shared, sg, shared_ws, shared_ws_bytes;  // the shared expert (qmm_moe_ffn_ex)
   size_t total;
 };
@@ -2336,6 +2366,7 @@ static MoeWs moe_ws(const qmm_qtensor* gate, const qmm_qtensor* down, int64_t T,
   w.hq = take(P * (F / qmm_block_size(vd)) * qmm_type_size(vd));
   w.yp = take(4 * P * H);
   w.planes = take(std::max(mmq_planes(gate->dtype, P, H).total, mmq_planes(down->dtype, P, F).total));
+  w.tails = take(4 * (3 * (size_t)E + 1));
   if (sh != nullptr && sh->gate != nullptr) {
     w.shared = take(4 * T * H);
     w.sg = take(4 * T);
@@ -2499,6 +2530,27 @@ static int moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* log
       // Q8_K activations: the gather and SiLU*mul write the GEMM planes
       // directly (the same values as quantizing the f32 rows)
       uint8_t* pw8 = b + L.planes;
+      // Q4_K gate / up: an expert's rows past its last full 128-row GEMM tile,
+      // when at most 16, go to the matrix-core expert GEMV instead of a
+      // nearly empty tile (the split is made on the device from the counts)
+      const bool tails = fmt_of(gate->dtype) == kFmtQ4K && moe_gemvm_rows(d, gate) >= kMoeTailRows &&
+                         moe_tails_enabled();
+      int32_t* cg = (int32_t*)(b + L.tails);
+      int32_t* ct = cg + experts;
+      int32_t* ot = ct + experts;
+      if (tails) {
+        int E = experts, tile = 128, mx = kMoeTailRows;
+        void* a1[] = {&counts, &offsets, &E, &tile, &mx, &cg, &ct, &ot};
+        QMM_TRY(launch(d, "qmm_moe_split_tails", ceil_div(experts, 256), 256, 0, s, a1));
+        // Q8_K rows of every routed pair, the tails' activations
+        const void* xp = x;
+        long long lx = ldx;
+        const int32_t* rows = ptok;
+        void* yq = b + L.xq;
+        int kk = (int)H, nr = (int)P;
+        void* a2[] = {&xp, &lx, &rows, &yq, &kk, &nr};
+        QMM_TRY(launch(d, "qmm_quantize_q8k_gather", ceil_div(P * (H / 256), 4), 256, 0, s, a2));
+      }
       {
         const Planes pl = mmq_planes(gate->dtype, P, H);
         const void* xp = x;
@@ -2513,7 +2565,8 @@ static int moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* log
       }
       const qmm_qtensor* gw[2] = {gate, up};
       float* gy[2] = {g, u};
-      QMM_TRY(moe_gemm_planes(d, gw, 2, experts, pw8, P, tokens, counts, offsets, gy, s));
+      QMM_TRY(moe_gemm_planes(d, gw, 2, experts, pw8, P, tokens, tails ? cg : counts, offsets, gy, s));
+      if (tails) QMM_TRY(moe_gemvm(d, gw, 2, experts, b + L.xq, P, kMoeTailRows, ct, ot, gy, s));
       {
         const Planes pl = mmq_planes(down->dtype, P, F);
         long long ld = F;
@@ -2528,8 +2581,18 @@ static int moe_ffn(const float* x, int64_t tokens, int64_t ldx, const float* log
       // hold the down GEMM's split partials (up to F / H splits)
       const qmm_qtensor* dw[1] = {down};
       float* dy[1] = {yp};
-      QMM_TRY(moe_gemm_planes(d, dw, 1, experts, pw8, P, tokens, counts, offsets, dy, s, (float*)(b + L.h),
-                              (size_t)(4 * P * F)));
+      QMM_TRY(moe_gemm_planes(d, dw, 1, experts, pw8, P, tokens, tails ? cg : counts, offsets, dy, s,
+                              (float*)(b + L.h), (size_t)(4 * P * F), tails));
+      if (tails) {
+        // the tails' down projection: their SiLU*mul rows as Q8_K rows, then the expert GEMV
+        long long ld = F;
+        void* hq = b + L.hq;
+        int kk = (int)F, E = experts, mx = kMoeTailRows;
+        void* a3[] = {&g, &u, &ld, &hq, &kk, &E, &mx, &ct, &ot};
+        QMM_TRY(launch(d, "qmm_silu_mul_q8k_ranges", ceil_div((long long)experts * kMoeTailRows * (F / 256), 4), 256,
+                       0, s, a3));
+        QMM_TRY(moe_gemv(dw, 1, experts, b + L.hq, P, kMoeTailRows, ct, ot, dy, stream));
+      }
     } else {
       float* xg = (float*)(b + L.xg);
       {

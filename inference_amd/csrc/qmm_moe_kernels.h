@@ -174,6 +174,25 @@ extern "C" __global__ void __launch_bounds__(256) qmm_moe_route_gather_q8k(
   qmm::q8k_block(x + (long long)s_ptok[i] * ldx + 256LL * b, xq + w * qmm::kQ8KBytes, threadIdx.x & 63);
 }
 
+// Tails of the grouped prefill GEMM: an expert holding c >= tile rows whose
+// last tile would hold r = c mod tile in [1, maxtail] rows leaves those r
+// rows to the multi-token expert GEMV (cg = c - r rows for the GEMM, ct = r
+// tail rows from row ot = offsets + cg); otherwise the GEMM takes all c rows
+// (ct = 0).
+extern "C" __global__ void __launch_bounds__(256) qmm_moe_split_tails(const int* __restrict__ counts,
+                                                                      const int* __restrict__ offsets, int E,
+                                                                      int tile, int maxtail, int* __restrict__ cg,
+                                                                      int* __restrict__ ct, int* __restrict__ ot) {
+  for (int e = blockIdx.x * 256 + threadIdx.x; e < E; e += gridDim.x * 256) {
+    const int c = counts[e], r = c % tile;
+    const bool split = c >= tile && r > 0 && r <= maxtail;
+    const int g = split ? c - r : c;
+    cg[e] = g;
+    ct[e] = split ? r : 0;
+    ot[e] = offsets[e] + g;
+  }
+}
+
 // f32 row gather: out row i = x[rows[i]] (k columns).
 extern "C" __global__ void qmm_gather_rows(const float* __restrict__ x, long long ldx, const int* __restrict__ rows,
                                            float* __restrict__ out, int k, int nrows) {
@@ -792,5 +811,22 @@ qmm_moe_mmqs_q4k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq, 
                          min(kb0 + kc, K / 256));                                                              \
   }
 QMM_MOE_MMQ_KERNEL(qmm::kFmtQ6K, q6k)
+
+// Q6_K grouped GEMM on the split-digit tile (128-row tiles; K split as above):
+// for the grouped prefill with tails, whose experts' GEMM rows are whole tiles.
+extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+qmm_moe_mmqs6_q6k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                  const int16_t* __restrict__ xs, float* __restrict__ y, int N, int K, int ldy, int E,
+                  const int* __restrict__ counts, const int* __restrict__ offsets, int kc, long long ysplit) {
+  const int e = (int)blockIdx.z % E, sp = (int)blockIdx.z / E;
+  qmm::GroupRows g;
+  if (!qmm::group_rows<qmm::kSBM, false>(g, xq, xd, xs, y + sp * ysplit, K, ldy, counts, offsets, e)) return;
+  const int nbk = K / 256;
+  const size_t rows0 = (size_t)e * N;
+  const uint16_t* wd = qmm::split_scales<qmm::kFmtQ6K>(wq, (long long)E * N, K) + rows0 * nbk;
+  const uint8_t* we = wq + rows0 * nbk * qmm::kQ6KBody;
+  const int kb0 = sp * kc;
+  qmm::mmqs6_q6k<false>(we, wd, g.xq, g.xd, g.y, g.m, N, K, ldy, nullptr, 0, 0, kb0, min(kb0 + kc, nbk));
+}
 
 QMM_MOE_MMQ_KERNEL(qmm::kFmtQ80, q8_0)

@@ -130,7 +130,10 @@ def test_moe_ffn_grouped_matches_oracle(monkeypatch, E, H, F, T, mode):
     lg = logits_for(T, E, mode, 514 + T)
     xd, ld = torch.from_numpy(x).to(DEV), torch.from_numpy(lg).to(DEV)
     monkeypatch.setenv("QMM_MOE_GROUPED", "1")
+    y_tails = moe_ffn(xd, ld, gate, up, down, k).cpu().numpy()
+    monkeypatch.setenv("QMM_MOE_TAILS", "0")  # every row through the GEMMs, as the public moe_gemm below
     y = moe_ffn(xd, ld, gate, up, down, k).cpu().numpy()
+    monkeypatch.delenv("QMM_MOE_TAILS")
 
     # the same chain from the public entry points
     counts, offsets, ptok, pw, tp = moe_route(ld, k)
@@ -158,11 +161,41 @@ def test_moe_ffn_grouped_matches_oracle(monkeypatch, E, H, F, T, mode):
     assert rel_err(y, comb) <= 1e-5
 
     y_ref = moe.moe_ffn(x, lg, gper, uper, dper, orc.Q4K, orc.Q6K, k)
-    cos = float((y * y_ref).sum() / np.sqrt((y * y).sum() * (y_ref * y_ref).sum()))
-    assert cos >= 0.99999 and rel_err(y, y_ref) <= 1e-2
+    for got in (y, y_tails):
+        cos = float((got * y_ref).sum() / np.sqrt((got * got).sum() * (y_ref * y_ref).sum()))
+        assert cos >= 0.99999 and rel_err(got, y_ref) <= 1e-2
     monkeypatch.setenv("QMM_MOE_GROUPED", "0")  # the expert-GEMV path on the same inputs
     y_gemv = moe_ffn(xd, ld, gate, up, down, k).cpu().numpy()
     assert rel_err(y_gemv, y_ref) <= 1e-2
+
+
+@pytest.mark.parametrize("T,E", [(268, 4), (300, 8), (128, 4)])
+def test_moe_ffn_grouped_tails(monkeypatch, T, E):
+    """Balanced routing puts T k / E rows on every expert: 134 (a full 128-row GEMM tile and a 6-row tail
+    for the matrix-core expert GEMV), 75 (no full tile: no tail) and 64. The FFN with tails against the
+    oracle's MoeMlp::forward (the chain bar of the test above) and against the run without tails
+    (QMM_MOE_TAILS=0): only the f32 order of the tail rows' gate / up sums differs, so the two stay
+    within the op bar of each other but for a rare Q8_K code of the down activation at a rounding tie."""
+    from oracle import moe
+    H, F, k = 512, 768, 2
+    gate, gper = stacked(E, F, H, GgmlDType.Q4K, 530 + T)
+    up, uper = stacked(E, F, H, GgmlDType.Q4K, 531 + T)
+    down, dper = stacked(E, H, F, GgmlDType.Q6K, 532 + T)
+    x = normal(533 + T, (T, H))
+    lg = logits_for(T, E, "balanced", 534 + T)
+    xd, ld = torch.from_numpy(x).to(DEV), torch.from_numpy(lg).to(DEV)
+    monkeypatch.setenv("QMM_MOE_GROUPED", "1")
+    y = moe_ffn(xd, ld, gate, up, down, k).cpu().numpy()
+    monkeypatch.setenv("QMM_MOE_TAILS", "0")
+    y0 = moe_ffn(xd, ld, gate, up, down, k).cpu().numpy()
+    y_ref = moe.moe_ffn(x, lg, gper, uper, dper, orc.Q4K, orc.Q6K, k)
+    for got in (y, y0):
+        cos = float((got * y_ref).sum() / np.sqrt((got * got).sum() * (y_ref * y_ref).sum()))
+        assert cos >= 0.99999 and rel_err(got, y_ref) <= 1e-2, (cos, rel_err(got, y_ref))
+    cos = float((y * y0).sum() / np.sqrt((y * y).sum() * (y0 * y0).sum()))
+    assert cos >= 0.99999 and rel_err(y, y0) <= 1e-2
+    if T * k // E % 128 == 0 or T * k // E < 128:
+        assert np.array_equal(y, y0)  # no tails: the same launches
 
 
 def test_moe_ffn_default_picks_grouped_at_prefill_sizes(monkeypatch):
