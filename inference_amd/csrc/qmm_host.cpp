@@ -2302,6 +2302,20 @@ static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, in
     }
     return QMM_OK;
   }
+  if (use_s && count == 2 && 2 * experts <= 65535) {
+    // gate and up in one grid (grid z = 2 E): a partial last round of tiles once
+    // instead of twice (config-5 prefill: 896 tiles per weight on 256 CUs)
+    const void* w0 = w[0]->data;
+    const void* w1 = w[1]->data;
+    float* y0 = y[0];
+    float* y1 = y[1];
+    void* args[] = {&w0, &w1, &q8, &dd, &ss, &y0, &y1, &N, &K, &ld, &E, &counts, &offsets};
+    hipFunction_t f2;
+    QMM_TRY(kernel(d, "qmm_moe_mmqs2_q4k", &f2));
+    QMM_HIP(hipModuleLaunchKernel(f2, (unsigned)((N + bn - 1) / bn), (unsigned)((max_rows + bm - 1) / bm),
+                                  (unsigned)(2 * experts), threads, 1, 1, lds, s, args, nullptr));
+    return QMM_OK;
+  }
   for (int j = 0; j < count; ++j) {
     const void* wq = w[j]->data;
     float* yy = y[j];
@@ -2312,10 +2326,6 @@ static int moe_gemm_planes(Device* d, const qmm_qtensor* const* w, int count, in
   return QMM_OK;
 }
 
-// qmm_moe_ffn runs the grouped GEMMs (prefill) instead of the expert GEMVs
-// when the routed pairs average more than this many rows per expert: the
-// GEMV streams an expert's weights once per eight rows, the GEMM once per
-// 128-row tile. QMM_MOE_GROUPED=0/1 forces the choice.
 // Grouped prefill tails (see qmm_moe_split_tails): at most this many rows per
 // expert go to the expert GEMV; QMM_MOE_TAILS=0 keeps every row in the GEMM.
 constexpr int kMoeTailRows = 16;
@@ -2324,6 +2334,10 @@ static bool moe_tails_enabled() {
   return !(e && atoi(e) == 0);
 }
 
+// qmm_moe_ffn runs the grouped GEMMs (prefill) instead of the expert GEMVs
+// when the routed pairs average more than this many rows per expert: the
+// GEMV streams an expert's weights once per eight rows, the GEMM once per
+// 128-row tile. QMM_MOE_GROUPED=0/1 forces the choice.
 static bool moe_grouped(int64_t pairs, int experts) {
   if (const char* e = env(kEnvMoeGrouped)) return atoi(e) != 0;
   return pairs > 16LL * experts;

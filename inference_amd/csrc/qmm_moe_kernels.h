@@ -788,6 +788,21 @@ qmm_moe_mmqs_q4k(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq, 
   (void)E;
 }
 
+// The same over two weights of one shape in one launch (gate and up: grid z =
+// 2 E, weight z / E): the two launches' tiles in one grid, so that a partial
+// last round of workgroups falls once instead of once per weight.
+extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+qmm_moe_mmqs2_q4k(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, const int8_t* __restrict__ xq,
+                  const float* __restrict__ xd, const int16_t* __restrict__ xs, float* __restrict__ y0,
+                  float* __restrict__ y1, int N, int K, int ldy, int E, const int* __restrict__ counts,
+                  const int* __restrict__ offsets) {
+  const int j = (int)blockIdx.z >= E ? 1 : 0, e = (int)blockIdx.z - j * E;
+  qmm::GroupRows g;
+  if (!qmm::group_rows<qmm::kSBM, false>(g, xq, xd, xs, j ? y1 : y0, K, ldy, counts, offsets, e)) return;
+  const uint8_t* we = (j ? w1 : w0) + (size_t)e * N * (K / 256) * qmm::kQ4KBytes;
+  qmm::mmqs_q4k<false>(we, g.xq, g.xd, g.xs, g.y, g.m, N, K, ldy, nullptr, 0, 0, 0, K / 256);
+}
+
 // The first-generation tile (Q6_K, Q8_0) also splits K: blockIdx.z = expert
 // + E * split, split s takes K steps [s kc, s kc + kc) and writes its f32
 // partial to y + s * ysplit (the host sums them in split order).
