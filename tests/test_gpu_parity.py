@@ -469,10 +469,12 @@ def test_gemm_q8_0_generations_bit_exact(monkeypatch, n, k, m):
 
 
 @pytest.mark.parametrize("dt,n,k,wseed", [(GgmlDType.Q4K, 14336, 4096, 6), (GgmlDType.Q4K, 4096, 14336, 6),
-                                          (GgmlDType.Q6K, 4096, 14336, 6)])
+                                          (GgmlDType.Q6K, 4096, 14336, 6), (GgmlDType.Q8_0, 14336, 4096, 6),
+                                          (GgmlDType.Q8_0, 4096, 14336, 6)])
 def test_prefill_config_shapes_match_cpu_path(dt, n, k, wseed):
     """Config 4: x 512 x k (seed 5) through QMatMul.forward; the CPU path is
-    evaluated on 48 of the 512 rows (spread over the batch)."""
+    evaluated on 48 of the 512 rows (spread over the batch). The Q8_0 legs run the
+    bench's Q8_0 GEMM shapes (the engine's Q8 projections)."""
     w = normal(wseed, (n, k), 0.02)
     wq = orc.quantize(ORC[dt], w)
     qt = QTensor.from_ggml(wq, dt, (n, k), device=DEV)
