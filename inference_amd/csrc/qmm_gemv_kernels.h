@@ -172,13 +172,15 @@ __device__ __forceinline__ void load_slice(WSlice& s, const uint8_t* __restrict_
   // the same cache lines, so a streaming (nontemporal) hint that drops the
   // lines after the first use measured 25% slower.
   auto ld16 = [wrow](uint32_t o) { return *reinterpret_cast<const uint4*>(wrow + o); };
+  // block offsets with the full-rate 24-bit multiply (b < 2^16); a 32-bit
+  // product issues the quarter-rate v_mul_lo_u32
   if constexpr (FMT == kFmtQ4K) {
-    const uint32_t o = b * (uint32_t)kQ4KBytes, ol = o + 32u * (uint32_t)l;
+    const uint32_t o = __umul24(b, (uint32_t)kQ4KBytes), ol = o + 32u * (uint32_t)l;
     s.a = ld16(o);
     s.b = ld16(ol + 16u);
     s.c = ld16(ol + 32u);
   } else if constexpr (FMT == kFmtQ6K) {
-    const uint32_t o = b * (uint32_t)kQ6KBody, ol = o + 32u * (uint32_t)l, oh = o + 128u + 32u * (uint32_t)(l >> 1);
+    const uint32_t o = __umul24(b, (uint32_t)kQ6KBody), ol = o + 32u * (uint32_t)l, oh = o + 128u + 32u * (uint32_t)(l >> 1);
     s.a = ld16(ol);
     s.b = ld16(ol + 16u);
     s.c = ld16(oh);
@@ -225,8 +227,15 @@ __device__ __forceinline__ uint4 q6_bytes(uint4 ql, uint4 qh, int sh) {
 struct WPrep {
   uint4 w0, w1, w2, w3;
   int c0, c1, c2, c3;  // Q4_K: sc0, sc1, m0, m1; Q6_K: the four group scales
+  uint32_t scp, mn16;  // Q4_K: sc0 | sc1 << 8 (bytes); m0 | m1 << 16 (16-bit lanes)
   float dw, dm;
 };
+
+// v_dot2_i32_i16: c + the two products of the packed signed 16-bit pairs.
+__device__ __forceinline__ int sdot2_pairs(uint32_t a, uint32_t b, int c) {
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_sdot2(__builtin_bit_cast(s16x2, a), __builtin_bit_cast(s16x2, b), c, false);
+}
 
 template <int FMT>
 __device__ __forceinline__ WPrep prep_w(const WSlice& s, int l) {
@@ -237,13 +246,20 @@ __device__ __forceinline__ WPrep prep_w(const WSlice& s, int l) {
     // 6-bit scale/min of sub-blocks 2l and 2l+1 (get_scale_min_k4).
     const int sh = (l & 1) * 16;
     const uint32_t A = s.a.y >> sh, B = s.a.z >> sh, C = s.a.w >> sh;
-    const bool upper = l >= 2;
-    const uint32_t scp = upper ? ((C & 0x0f0fu) | ((A >> 2) & 0x3030u)) : (A & 0x3f3fu);
-    const uint32_t mnp = upper ? (((C >> 4) & 0x0f0fu) | ((B >> 2) & 0x3030u)) : (B & 0x3f3fu);
+    // lanes 2, 3 take the upper form: a bit-select on a lane mask (both forms
+    // are a few instructions; a branch on the lane would run both and add
+    // exec-mask bookkeeping)
+    const uint32_t um = 0u - (uint32_t)(l >> 1);
+    const uint32_t scu = (C & 0x0f0fu) | ((A >> 2) & 0x3030u), scl = A & 0x3f3fu;
+    const uint32_t mnu = ((C >> 4) & 0x0f0fu) | ((B >> 2) & 0x3030u), mnl = B & 0x3f3fu;
+    const uint32_t scp = (scu & um) | (scl & ~um);
+    const uint32_t mnp = (mnu & um) | (mnl & ~um);
     w.c0 = scp & 0xff;
     w.c1 = (scp >> 8) & 0xff;
     w.c2 = mnp & 0xff;
     w.c3 = (mnp >> 8) & 0xff;
+    w.scp = scp;
+    w.mn16 = __builtin_amdgcn_perm(0u, mnp, 0x0c010c00u);  // m0 | m1 << 16
     // Low nibbles as bytes 0..15; high nibbles kept in place with the top bit
     // flipped, i.e. signed bytes 16*q - 128 (one mask-and-xor per dword instead
     // of shift-and-mask); their dot is corrected with the sub-block's
@@ -325,15 +341,19 @@ __device__ __forceinline__ float q4k_combine(float dw, float dm, int isd, int is
 template <int FMT>
 __device__ __forceinline__ float dot_wx(const WPrep& w, const XSlice& x, int& ia, int& ib) {
   if constexpr (FMT == kFmtQ4K) {
-    const int bs0 = (int)(int16_t)(x.s0 & 0xffffu), bs1 = (int)x.s0 >> 16;
+    const int bs1 = (int)x.s0 >> 16;
     const int s0 = dot16(w.w1, x.x1, dot16(w.w0, x.x0, 0));
     const int s1 = (dot16(w.w3, x.x3, dot16(w.w2, x.x2, 0)) + 128 * bs1) >> 4;
-    // |s0|, |s1| <= 32*15*128 < 2^23 and scales/mins < 64: full-rate 24-bit products
-    const int isd = __mul24(w.c0, s0) + __mul24(w.c1, s1);
-    const int ism = __mul24(w.c2, bs0) + __mul24(w.c3, bs1);
-    ia = isd;
+    // isd = sc0 s0 + sc1 s1 in f32, exactly: |s| <= 32*15*128 and sc < 64, so
+    // each product and the sum are integers below 2^24 (as a 32-bit integer
+    // product the compiler cannot prove s1 fits the 24-bit multiplier and
+    // issues a quarter-rate v_mul_lo_u32)
+    const float isd = __builtin_fmaf((float)(w.scp & 0xffu), (float)s0, (float)((w.scp >> 8) & 0xffu) * (float)s1);
+    // ism = m0 bs0 + m1 bs1 as one dot of the packed 16-bit pairs
+    const int ism = sdot2_pairs(w.mn16, x.s0, 0);
+    ia = (int)isd;
     ib = ism;
-    return x.d * q4k_combine(w.dw, w.dm, isd, ism);
+    return x.d * __builtin_fmaf(w.dw, isd, -(w.dm * (float)ism));
   } else if constexpr (FMT == kFmtQ6K) {
     const int t0 = dot16(w.w0, x.x0, 0) - 32 * (int)(int16_t)(x.s0 & 0xffffu);
     const int t1 = dot16(w.w1, x.x1, 0) - 32 * ((int)x.s0 >> 16);
