@@ -640,8 +640,8 @@ def kernel_only(torch, dev, which, launches):
     `gate` = the Q4_K gate GEMV (14336x4096, M = 1, rotated weight copies); `qkvgu` / `qkvgu_staged`
     = the q/k/v/gate/up set in one launch (Q8_K in the prologue / pre-quantized activation);
     `copy` = a 256 MiB device copy (the calibration for FETCH_SIZE / WRITE_SIZE); `gemm_gate` / `gemm_down` =
-    the config-4 GEMMs (M = 512; `gemm_q6k_gate` / `gemm_q6k_down`: its Q6_K legs); `moe` = the config-5 expert
-    FFN (`moe32`: at 32 tokens); `gate_m8` = the gate GEMV on eight pre-quantized rows; `gate_up` = gate and up
+    the config-4 GEMMs (M = 512; `gemm_q6k_*` / `gemm_q8_0_*`: its Q6_K / Q8_0 legs); `moe` = the config-5 expert
+    FFN (`moe32`: at 32 tokens; `moe_prefill`: at 512 tokens); `gate_m8` = the gate GEMV on eight pre-quantized rows; `gate_up` = gate and up
     in one launch with the RMSNorm + Q8_K prologue (the FFN pair as the decoder runs it)."""
     from inference_amd import GgmlDType, QTensor, qmm
     from inference_amd.synth import normal, normal_torch
@@ -654,13 +654,14 @@ def kernel_only(torch, dev, which, launches):
         print(json.dumps({"kernel_only": "copy", "bytes_read": a.numel() * 4, "bytes_written": b.numel() * 4,
                           "launches": launches}), flush=True)
         return
-    if which in ("gemm_gate", "gemm_down", "gemm_q6k_gate", "gemm_q6k_down"):
-        # config-4 GEMM: 512 rows N(0,1) seed 5 against a Q4_K weight N(0, 0.02^2) seed 6 / 16, or the Q6_K
-        # legs' weights (seeds 26 / 36)
+    if which in ("gemm_gate", "gemm_down", "gemm_q6k_gate", "gemm_q6k_down", "gemm_q8_0_gate", "gemm_q8_0_down"):
+        # config-4 GEMM: 512 rows N(0,1) seed 5 against a Q4_K weight N(0, 0.02^2) seed 6 / 16, or the Q6_K /
+        # Q8_0 legs' weights (seeds 26 / 36, 46 / 56)
         n, k = (14336, 4096) if which.endswith("gate") else (4096, 14336)
-        q6 = "q6k" in which
-        seed = (26 if which.endswith("gate") else 36) if q6 else (6 if which == "gemm_gate" else 16)
-        w = QTensor.quantize(normal_torch(seed, (n, k), 0.02, dev), GgmlDType.Q6K if q6 else GgmlDType.Q4K)
+        dt = GgmlDType.Q6K if "q6k" in which else GgmlDType.Q8_0 if "q8_0" in which else GgmlDType.Q4K
+        base = {GgmlDType.Q4K: 6, GgmlDType.Q6K: 26, GgmlDType.Q8_0: 46}[dt]
+        seed = base if which.endswith("gate") else base + 10
+        w = QTensor.quantize(normal_torch(seed, (n, k), 0.02, dev), dt)
         x = torch.from_numpy(normal(5, (512, k))).to(dev)
         y = torch.empty((512, n), dtype=torch.float32, device=dev)
         L = qmm.lib()
@@ -672,15 +673,18 @@ def kernel_only(torch, dev, which, launches):
         torch.cuda.synchronize()
         print(json.dumps({"kernel_only": which, "int8_ops": 2 * 512 * n * k, "launches": launches}), flush=True)
         return
-    if which in ("moe", "moe32"):
+    if which in ("moe", "moe32", "moe_prefill"):
         # config 5: one qmm_moe_ffn call per launch (route, gather, expert GEMVs, SiLU*mul, combine);
-        # moe32: the same experts at 32 tokens (the matrix-core expert GEMV for gate / up)
-        E, H, F, T, k = 8, 4096, 14336, 32 if which == "moe32" else 8, 2
+        # moe32: the same experts at 32 tokens (the matrix-core expert GEMV for gate / up); moe_prefill: 512
+        # tokens (seeds 9 / 10, the bench's MoE prefill: grouped GEMMs and their tails)
+        E, H, F, k = 8, 4096, 14336, 2
+        T = {"moe": 8, "moe32": 32, "moe_prefill": 512}[which]
         gate = QTensor.quantize(normal_torch(71, (E * F, H), 0.02, dev), GgmlDType.Q4K)
         up = QTensor.quantize(normal_torch(72, (E * F, H), 0.02, dev), GgmlDType.Q4K)
         down = QTensor.quantize(normal_torch(73, (E * H, F), 0.02, dev), GgmlDType.Q6K)
-        x = torch.from_numpy(normal(7, (T, H))).to(dev)
-        lg = torch.from_numpy(normal(8, (T, E))).to(dev)
+        pre = which == "moe_prefill"
+        x = torch.from_numpy(normal(9 if pre else 7, (T, H))).to(dev)
+        lg = torch.from_numpy(normal(10 if pre else 8, (T, E))).to(dev)
         y = torch.empty((T, H), dtype=torch.float32, device=dev)
         L = qmm.lib()
         wsb = int(L.qmm_moe_ffn_workspace_size(gate.handle, down.handle, T, E, k))
@@ -877,8 +881,8 @@ def main():
                          "their prologues; serial: one launch per projection")
     ap.add_argument("--decode-tokens", type=int, default=256, help="config-3 generated tokens (0 = skip)")
     ap.add_argument("--kernel-only", choices=("gate", "gate_m8", "gate_up", "qkvgu", "qkvgu_staged", "grouped", "copy",
-                                              "gemm_gate", "gemm_down", "gemm_q6k_gate", "gemm_q6k_down", "moe",
-                                              "moe32",
+                                              "gemm_gate", "gemm_down", "gemm_q6k_gate", "gemm_q6k_down",
+                                              "gemm_q8_0_gate", "gemm_q8_0_down", "moe", "moe32", "moe_prefill",
                                               "q8_0", "down_q6k", "decode", "read_9mb", "read_33mb",
                                               "read_80mb", "read_1gb", "read_graph"),
                     default=None,
