@@ -100,13 +100,13 @@ std::atomic<Device*> g_dev[64] = {};
 enum EnvKey {
   kEnvGemv1, kEnvGemv1p, kEnvGemvCfg, kEnvGemvWavesPerCu, kEnvGemvRows, kEnvSplitK, kEnvMmq2, kEnvMmq,
   kEnvMmq4Bn, kEnvMmq1, kEnvMmqXcd, kEnvMoeGemv, kEnvMoeMmq, kEnvMoeBm, kEnvMoeSplitK, kEnvMoeGrouped, kEnvGroupedP,
-  kEnvGroupedWgs, kEnvStreamK, kEnvGemvm, kEnvMmq6, kEnvMmq8, kEnvMoeTails, kEnvCount
+  kEnvGroupedWgs, kEnvStreamK, kEnvGemvm, kEnvMmq6, kEnvMmq8, kEnvMoeTails, kEnvFfnPair, kEnvCount
 };
 const char* const kEnvNames[kEnvCount] = {
     "QMM_GEMV1", "QMM_GEMV1P", "QMM_GEMV_CFG", "QMM_GEMV_WAVES_PER_CU", "QMM_GEMV_ROWS", "QMM_SPLITK",
     "QMM_MMQ2", "QMM_MMQ", "QMM_MMQ4_BN", "QMM_MMQ1", "QMM_MMQ_XCD", "QMM_MOE_GEMV", "QMM_MOE_MMQ",
     "QMM_MOE_BM", "QMM_MOE_SPLITK", "QMM_MOE_GROUPED", "QMM_GROUPED_P", "QMM_GROUPED_WGS",
-    "QMM_STREAMK", "QMM_GEMVM", "QMM_MMQ6", "QMM_MMQ8", "QMM_MOE_TAILS"};
+    "QMM_STREAMK", "QMM_GEMVM", "QMM_MMQ6", "QMM_MMQ8", "QMM_MOE_TAILS", "QMM_FFN_SEPARATE"};
 
 struct Tuning {
   int w = 0, r = 0, u = 0, waves_per_cu = 0, gemv1 = 1, gemv1p = -1;
@@ -1198,6 +1198,44 @@ int qmm_matmul_q_ex(const qmm_qtensor* w, const void* xq, int64_t m, float* y, i
   return gemv(d, &t, 1, xq, false, 0, (int)m, nullptr, (hipStream_t)stream, nullptr, 0.0f, 1);
 }
 
+// Two weights of one shape over the same activation planes (the feed-forward
+// block's gate and up) as one unsplit launch of the split-scale tile
+// (qmm_mmqs2_q4k, grid z = weight) when each alone would be split over K (a
+// grid under half the CUs: 8B gate / up at up to 128 rows) and the pair's
+// rounds x K steps are no more than the two split launches': no partials to
+// write and read back, one launch fewer (127 rows: 108.9 us for the block
+// against 114.4). Unsplit grids stay two launches (512 rows: 349 us against
+// 363 paired). QMM_FFN_SEPARATE keeps two launches.
+static bool pair_plan(const Device* d, const qmm_qtensor* a, const qmm_qtensor* b, int64_t m) {
+  if (!use_gemm(a, m) || a->dtype != b->dtype || a->n != b->n || a->k != b->k || env(kEnvFfnPair) != nullptr)
+    return false;
+  const GemmPlan pa = gemm_plan(d, a, m, false);
+  if (pa.sk_tiles != 0 || pa.splits < 2 || strcmp(pa.name, "qmm_mmqs_q4k") != 0) return false;
+  const long long T = pa.tiles, nbk = a->k / 256, slots = d->num_cu, sp = pa.splits;
+  const long long merged = (2 * T + slots - 1) / slots * nbk;
+  const long long split = 2 * ((T * sp + slots - 1) / slots) * ((nbk + sp - 1) / sp);
+  return merged <= split;
+}
+
+static int gemm_pair_launch(Device* d, const qmm_qtensor* a, const qmm_qtensor* b, const uint8_t* planes, int64_t m,
+                            float* ya, int64_t lda, float* yb, int64_t ldb, int accumulate, hipStream_t s) {
+  if ((uintptr_t)planes % 16) return fail(QMM_ERR_INVALID, "GEMM workspaces must be 16-byte aligned");
+  const GemmPlan p = gemm_plan(d, a, m, false);
+  const Planes pl = mmq_planes(a->dtype, m, a->k);
+  const void* w0 = a->data;
+  const void* w1 = b->data;
+  const void* q8 = planes + pl.q8;
+  const void* dd = planes + pl.d;
+  const void* ss = planes + pl.s;
+  int M = (int)m, N = (int)a->n, K = (int)a->k, l0 = (int)lda, l1 = (int)ldb, acc = accumulate;
+  void* args[] = {&w0, &w1, &q8, &dd, &ss, &ya, &yb, &M, &N, &K, &l0, &l1, &acc};
+  hipFunction_t f;
+  QMM_TRY(kernel(d, "qmm_mmqs2_q4k", &f));
+  QMM_HIP(hipModuleLaunchKernel(f, (unsigned)((N + 127) / 128), (unsigned)((M + 127) / 128), 2, p.threads, 1, 1,
+                                p.lds, s, args, nullptr));
+  return QMM_OK;
+}
+
 // Shared by qmm_matmul / qmm_matmul_multi: x f32 [m, k] against `count` weights.
 static int matmul_targets(const GemvTarget* tg, int count, const float* x, int64_t m, int64_t ldx, void* ws,
                           size_t ws_bytes, void* stream, const float* norm_w = nullptr, float eps = 0.0f,
@@ -1246,6 +1284,9 @@ static int matmul_targets(const GemvTarget* tg, int count, const float* x, int64
     // unsplit (size ws for the largest weight to split every job)
     float* part = (float*)((uint8_t*)ws + base + nrm);
     const size_t sb = ws_bytes - base - nrm;
+    if (count == 2 && pair_plan(d, tg[0].w, tg[1].w, m))
+      return gemm_pair_launch(d, tg[0].w, tg[1].w, (const uint8_t*)ws, m, tg[0].y, tg[0].ldy, tg[1].y, tg[1].ldy,
+                              accumulate, s);
     for (int j = 0; j < count; ++j)
       QMM_TRY(gemm(d, tg[j].w, (const uint8_t*)ws, m, tg[j].y, tg[j].ldy, nullptr, s, accumulate, part, sb));
     return QMM_OK;
@@ -1531,16 +1572,22 @@ int qmm_ffn(const qmm_qtensor* gate, const qmm_qtensor* up, const qmm_qtensor* d
   }
   // the input's Q8_K planes, normalised on the way when asked
   QMM_TRY(input_planes(d, gate->dtype, x, m, H, ldx, norm_weight, eps, b + L.xp, (float*)(b + L.xn), s));
-  // gate and up, their split partials left unsummed
+  // gate and up: one launch over both when pair_plan takes them (unsplit),
+  // else their split partials left unsummed
   const GemmPlan pg = gemm_plan(d, gate, m, false), pu = gemm_plan(d, up, m, false);
-  QMM_TRY(gemm_launch(d, gate, b + L.xp, m, pg, g, F, nullptr, s, 0, g, b + L.part));
-  QMM_TRY(gemm_launch(d, up, b + L.xp, m, pu, u, F, nullptr, s, 0, u, b + L.part));
+  const bool pair = pair_plan(d, gate, up, m);
+  if (pair) {
+    QMM_TRY(gemm_pair_launch(d, gate, up, b + L.xp, m, g, F, u, F, 0, s));
+  } else {
+    QMM_TRY(gemm_launch(d, gate, b + L.xp, m, pg, g, F, nullptr, s, 0, g, b + L.part));
+    QMM_TRY(gemm_launch(d, up, b + L.xp, m, pu, u, F, nullptr, s, 0, u, b + L.part));
+  }
   // split sums, silu(g) * u and the down GEMM's Q8_K planes in one launch
   {
     const Planes ph = mmq_planes(down->dtype, m, F);
     const float* gp = g;
     const float* upp = u;
-    int gsp = pg.splits, usp = pu.splits, kk = (int)F, mm = (int)m;
+    int gsp = pair ? 1 : pg.splits, usp = pair ? 1 : pu.splits, kk = (int)F, mm = (int)m;
     void* q8 = b + L.hp + ph.q8;
     void* dd = b + L.hp + ph.d;
     void* ss = b + L.hp + ph.s;

@@ -1572,6 +1572,18 @@ __device__ __forceinline__ void mmqs_q4k_sk(const uint8_t* __restrict__ wq, cons
 QMM_MMQS_KERNEL(, false)
 QMM_MMQS_KERNEL(_dump, true)
 
+// Two Q4_K weights of one shape over the same activation planes in one
+// launch (the feed-forward block's gate and up: grid z = weight), unsplit: the
+// tiles of both in one grid instead of two launches with split-K partials.
+extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+qmm_mmqs2_q4k(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, const int8_t* __restrict__ xq,
+              const float* __restrict__ xd, const int16_t* __restrict__ xs, float* __restrict__ y0,
+              float* __restrict__ y1, int M, int N, int K, int ldy0, int ldy1, int accumulate) {
+  const int j = (int)blockIdx.z;
+  qmm::mmqs_q4k<false>(j ? w1 : w0, xq, xd, xs, j ? y1 : y0, M, N, K, j ? ldy1 : ldy0, nullptr, accumulate, 1, 0,
+                       K / 256);
+}
+
 // ---------------------------------------------------------------------------
 // mmqs6: the Q6_K prefill GEMM with the sub-block scales in the MFMA
 // operands. A Q6_K code q - 32 lies in [-32, 31] and its 16-element sub-block

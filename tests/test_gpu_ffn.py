@@ -3,7 +3,8 @@ qmm_ffn, the gated feed-forward block of m rows, and qmm_qkv_rope_kv_append_n, q
 KV append.
 
 At m > 8 the entry point sums the gate / up GEMMs' split-K partials inside its SiLU launch, in the
-order qmm_splitk_sum uses, so its output must equal qmm_matmul_ex (gate, up) -> qmm_silu_mul ->
+order qmm_splitk_sum uses (or, where gate and up would each be split, runs both as one unsplit launch, as
+qmm_matmul_ex does for the same pair), so its output must equal qmm_matmul_ex (gate, up) -> qmm_silu_mul ->
 qmm_matmul_ex (down, accumulate) bit for bit; at m <= 8 it runs the GEMV calls themselves. The
 oracle check holds the f32 result to max|d| <= 1e-3 * rms.
 """
@@ -74,6 +75,48 @@ def chain(gate, up, down, x, m, nw, y):
     qmm._check(L().qmm_silu_mul(g.data_ptr(), u.data_ptr(), h.data_ptr(), m * F, S()))
     qmm._check(L().qmm_matmul_ex((vp * 1)(down.handle.value), 1, h.data_ptr(), m, F, None, eps, 1,
                                  (vp * 1)(y.data_ptr()), (i64 * 1)(H), ws.data_ptr(), ws.numel(), S()))
+
+
+@pytest.mark.parametrize("m", [127, 64, 24])
+def test_gate_up_pair_equals_unsplit_launches(monkeypatch, m):
+    """Gate and up at 8B shape and m rows (each alone split over K) run as one launch over both weights
+    (grid z = weight), unsplit: bit-identical to one unsplit launch per weight (QMM_SPLITK=1,
+    QMM_FFN_SEPARATE=1), here with the residual add and output strides wider than the rows, and within
+    1e-3 * rms of the oracle. Also the split launches (QMM_FFN_SEPARATE=1) hold the same bar."""
+    H, F = 4096, 14336
+    gate, up, _ = make(H, F, 7)
+    rng = np.random.default_rng(300 + m)
+    x = rng.standard_normal((m, H)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    r0 = rng.standard_normal((m, F)).astype(np.float32)
+    r1 = rng.standard_normal((m, F)).astype(np.float32)
+    ld0, ld1 = F + 64, F + 320
+
+    def run():
+        y0 = torch.full((m, ld0), float("nan"), device=DEV)
+        y1 = torch.full((m, ld1), float("nan"), device=DEV)
+        y0[:, :F], y1[:, :F] = t(r0), t(r1)
+        wsb = max(int(L().qmm_matmul_ex_workspace_size(q.handle, m, 1)) for q in (gate, up))
+        ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+        xd, nwd = t(x), t(nw)
+        qmm._check(L().qmm_matmul_ex((vp * 2)(gate.handle.value, up.handle.value), 2, xd.data_ptr(), m, H,
+                                     nwd.data_ptr(), ctypes.c_float(1e-5), 1, (vp * 2)(y0.data_ptr(), y1.data_ptr()),
+                                     (i64 * 2)(ld0, ld1), ws.data_ptr(), wsb, S()))
+        torch.cuda.synchronize()
+        assert torch.isnan(y0[:, F:]).all() and torch.isnan(y1[:, F:]).all()  # the stride gaps untouched
+        return y0[:, :F].cpu().numpy(), y1[:, :F].cpu().numpy()
+
+    got = run()
+    monkeypatch.setenv("QMM_FFN_SEPARATE", "1")
+    split = run()
+    monkeypatch.setenv("QMM_SPLITK", "1")
+    unsplit = run()
+    for a, b in zip(got, unsplit):
+        assert np.array_equal(a, b)
+    xin = ol.rms_norm(x, nw, 1e-5)
+    for q, r, a, b in zip((gate, up), (r0, r1), got, split):
+        want = r + orc.matmul(orc.Q4K, xin, q.to_ggml(), H)
+        assert rel_err(a, want) <= TOL and rel_err(b, want) <= TOL
 
 
 @pytest.mark.parametrize("m", [127, 64, 9, 8, 3, 1])
