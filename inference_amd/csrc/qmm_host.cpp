@@ -100,13 +100,13 @@ std::atomic<Device*> g_dev[64] = {};
 enum EnvKey {
   kEnvGemv1, kEnvGemv1p, kEnvGemvCfg, kEnvGemvWavesPerCu, kEnvGemvRows, kEnvSplitK, kEnvMmq2, kEnvMmq,
   kEnvMmq4Bn, kEnvMmq1, kEnvMmqXcd, kEnvMoeGemv, kEnvMoeMmq, kEnvMoeBm, kEnvMoeSplitK, kEnvMoeGrouped, kEnvGroupedP,
-  kEnvGroupedWgs, kEnvStreamK, kEnvGemvm, kEnvMmq6, kEnvMmq8, kEnvMoeTails, kEnvFfnPair, kEnvCount
+  kEnvGroupedWgs, kEnvStreamK, kEnvGemvm, kEnvMmq6, kEnvMmq8, kEnvMoeTails, kEnvFfnPair, kEnvQkvSeparate, kEnvCount
 };
 const char* const kEnvNames[kEnvCount] = {
     "QMM_GEMV1", "QMM_GEMV1P", "QMM_GEMV_CFG", "QMM_GEMV_WAVES_PER_CU", "QMM_GEMV_ROWS", "QMM_SPLITK",
     "QMM_MMQ2", "QMM_MMQ", "QMM_MMQ4_BN", "QMM_MMQ1", "QMM_MMQ_XCD", "QMM_MOE_GEMV", "QMM_MOE_MMQ",
     "QMM_MOE_BM", "QMM_MOE_SPLITK", "QMM_MOE_GROUPED", "QMM_GROUPED_P", "QMM_GROUPED_WGS",
-    "QMM_STREAMK", "QMM_GEMVM", "QMM_MMQ6", "QMM_MMQ8", "QMM_MOE_TAILS", "QMM_FFN_SEPARATE"};
+    "QMM_STREAMK", "QMM_GEMVM", "QMM_MMQ6", "QMM_MMQ8", "QMM_MOE_TAILS", "QMM_FFN_SEPARATE", "QMM_QKV_SEPARATE"};
 
 struct Tuning {
   int w = 0, r = 0, u = 0, waves_per_cu = 0, gemv1 = 1, gemv1p = -1;
@@ -1236,6 +1236,112 @@ static int gemm_pair_launch(Device* d, const qmm_qtensor* a, const qmm_qtensor* 
   return QMM_OK;
 }
 
+// Two or three Q4_K / Q6_K weights of one k over the same activation planes
+// (the prefill's q / k / v) as one launch of qmm_mmqs_multi, where each alone
+// would be split over K into partials: the split counts are chosen together
+// so that every workgroup of the launch fits one round over the CUs (one
+// 512-thread workgroup per CU), minimising the longest split (a Q6_K step
+// weighted 5 against a Q4_K step's 4), then the partial bytes. The partials
+// must fit in the largest of the jobs' own split scratch, so a workspace
+// sized for the separate launches holds them. 8B q / k / v at 127 rows:
+// splits 4 / 4 / 8 in one launch of 224 workgroups, against 8 / 8 / 8 in
+// three. QMM_QKV_SEPARATE keeps one launch per weight.
+struct MmqsJobs {  // the kernel's by-value argument (qmm_mmqs_multi)
+  const void* w[3];
+  float* y[3];
+  int n[3], gx[3], kc[3], q6[3];
+  int start[4];
+};
+static_assert(sizeof(MmqsJobs) == 112, "qmm_mmqs_multi argument layout");
+
+struct MultiPlan {
+  int count = 0, splits[3] = {1, 1, 1}, kc[3] = {0, 0, 0}, gx[3] = {0, 0, 0}, wgs = 0;
+  size_t off[3] = {0, 0, 0}, bytes = 0;  // each job's partials in the scratch
+};
+
+static bool multi_plan(const Device* d, const qmm_qtensor* const* w, int count, int64_t m, MultiPlan* out) {
+  if (count < 2 || count > 3 || env(kEnvQkvSeparate) != nullptr) return false;
+  size_t bound = 0;
+  int q6[3] = {0, 0, 0};
+  for (int j = 0; j < count; ++j) {
+    if (!w[j] || !use_gemm(w[j], m) || w[j]->k != w[0]->k) return false;
+    const int f = fmt_of(w[j]->dtype);
+    const GemmPlan pj = gemm_plan(d, w[j], m, false);
+    const bool tile = (f == kFmtQ4K && strcmp(pj.name, "qmm_mmqs_q4k") == 0) ||
+                      (f == kFmtQ6K && strcmp(pj.name, "qmm_mmqs6_q6k") == 0);
+    if (!tile || pj.sk_tiles != 0 || pj.splits < 2) return false;
+    q6[j] = f == kFmtQ6K;
+    bound = std::max(bound, align256((size_t)pj.splits * (size_t)m * (size_t)w[j]->n * 4));
+  }
+  const int nbk = (int)(w[0]->k / 256), gy = (int)((m + 127) / 128);
+  static const int cand[5] = {1, 2, 4, 8, 16};
+  MultiPlan best;
+  long long best_path = -1;
+  int c[3] = {0, 0, 0};
+  const int ncomb = count == 3 ? 125 : 25;
+  for (int t = 0; t < ncomb; ++t) {
+    c[0] = t % 5;
+    c[1] = (t / 5) % 5;
+    c[2] = t / 25;
+    MultiPlan p;
+    p.count = count;
+    long long path = 0;
+    bool ok = true;
+    for (int j = 0; j < count && ok; ++j) {
+      const int sp = cand[c[j]];
+      const int kc = (nbk + sp - 1) / sp;
+      if (sp > nbk || (sp > 1 && kc < 2)) ok = false;
+      p.kc[j] = kc;
+      p.splits[j] = (nbk + kc - 1) / kc;
+      p.gx[j] = (int)((w[j]->n + 127) / 128);
+      p.wgs += p.gx[j] * gy * p.splits[j];
+      path = std::max(path, (long long)kc * (q6[j] ? 5 : 4));
+      p.off[j] = p.bytes;
+      p.bytes += align256((size_t)p.splits[j] * (size_t)m * (size_t)w[j]->n * 4);
+    }
+    if (!ok || p.wgs > d->num_cu || p.bytes > bound) continue;
+    if (best_path < 0 || path < best_path || (path == best_path && p.bytes < best.bytes)) {
+      best = p;
+      best_path = path;
+    }
+  }
+  if (best_path < 0) return false;
+  *out = best;
+  return true;
+}
+
+// The multi launch of plan p over the planes at `planes`: job j's partials at
+// part + p.off[j] (split s at + s * m * n_j floats).
+static int multi_launch(Device* d, const qmm_qtensor* const* w, const MultiPlan& p, const uint8_t* planes, int64_t m,
+                        uint8_t* part, hipStream_t s) {
+  if ((uintptr_t)planes % 16) return fail(QMM_ERR_INVALID, "GEMM workspaces must be 16-byte aligned");
+  MmqsJobs jobs = {};
+  const int gy = (int)((m + 127) / 128);
+  int start = 0;
+  for (int j = 0; j < 3; ++j) {
+    const int jj = j < p.count ? j : p.count - 1;  // unused slots repeat the last job (never selected)
+    jobs.w[j] = w[jj]->data;
+    jobs.y[j] = (float*)(part + p.off[jj]);
+    jobs.n[j] = (int)w[jj]->n;
+    jobs.gx[j] = p.gx[jj];
+    jobs.kc[j] = p.kc[jj];
+    jobs.q6[j] = fmt_of(w[jj]->dtype) == kFmtQ6K;
+    jobs.start[j] = start;
+    if (j < p.count) start += p.gx[j] * gy * p.splits[j];
+  }
+  jobs.start[3] = start;
+  const Planes pl = mmq_planes(w[0]->dtype, m, w[0]->k);
+  const void* q8 = planes + pl.q8;
+  const void* dd = planes + pl.d;
+  const void* ss = planes + pl.s;
+  int M = (int)m, K = (int)w[0]->k;
+  void* args[] = {&jobs, &q8, &dd, &ss, &M, &K};
+  // the larger of the two tiles' LDS (mmqs: 2 x 72.5 KB, mmqs6: 2 x 71 KB)
+  const unsigned lds_q4 = 2u * (128 * 256 + 128 * 128 + 128 * 16 + 128 * 4 + 128 * 48 + 128 * 48 + 128 * 80);
+  const unsigned lds = std::max(2 * kS6StageBytes, lds_q4);
+  return launch(d, "qmm_mmqs_multi", (unsigned)start, 512, lds, s, args);
+}
+
 // Shared by qmm_matmul / qmm_matmul_multi: x f32 [m, k] against `count` weights.
 static int matmul_targets(const GemvTarget* tg, int count, const float* x, int64_t m, int64_t ldx, void* ws,
                           size_t ws_bytes, void* stream, const float* norm_w = nullptr, float eps = 0.0f,
@@ -1287,6 +1393,19 @@ static int matmul_targets(const GemvTarget* tg, int count, const float* x, int64
     if (count == 2 && pair_plan(d, tg[0].w, tg[1].w, m))
       return gemm_pair_launch(d, tg[0].w, tg[1].w, (const uint8_t*)ws, m, tg[0].y, tg[0].ldy, tg[1].y, tg[1].ldy,
                               accumulate, s);
+    const qmm_qtensor* wl[3] = {tg[0].w, count > 1 ? tg[1].w : nullptr, count > 2 ? tg[2].w : nullptr};
+    MultiPlan mp;
+    if (multi_plan(d, wl, count, m, &mp) && mp.bytes <= sb) {
+      QMM_TRY(multi_launch(d, wl, mp, (const uint8_t*)ws, m, (uint8_t*)part, s));
+      for (int j = 0; j < count; ++j) {
+        int M = (int)m, N = (int)tg[j].w->n, sp = mp.splits[j], lo = (int)tg[j].ldy, acc = accumulate;
+        const float* pp = (const float*)((uint8_t*)part + mp.off[j]);
+        float* yy = tg[j].y;
+        void* a2[] = {&pp, &sp, &M, &N, &yy, &lo, &acc};
+        QMM_TRY(launch(d, "qmm_splitk_sum", ceil_div((int64_t)M * N, 256), 256, 0, s, a2));
+      }
+      return QMM_OK;
+    }
     for (int j = 0; j < count; ++j)
       QMM_TRY(gemm(d, tg[j].w, (const uint8_t*)ws, m, tg[j].y, tg[j].ldy, nullptr, s, accumulate, part, sb));
     return QMM_OK;
@@ -1642,9 +1761,12 @@ static QkvWs qkv_ws(Device* d, const qmm_qtensor* wq, const qmm_qtensor* wk, con
     if (normalize && (size_t)H * 4 > (size_t)d->max_lds) o += align256((size_t)(m * H) * 4);
     const qmm_qtensor* ws3[3] = {wq, wk, wv};
     size_t* at[3] = {&w.q, &w.k, &w.v};
+    MultiPlan mp;
+    const bool multi = multi_plan(d, ws3, 3, m, &mp);
     for (int j = 0; j < 3; ++j) {
       *at[j] = o;
-      o += align256((size_t)gemm_plan(d, ws3[j], m, false).splits * (size_t)(m * ws3[j]->n) * 4);
+      const int sp = multi ? mp.splits[j] : gemm_plan(d, ws3[j], m, false).splits;
+      o += align256((size_t)sp * (size_t)(m * ws3[j]->n) * 4);
     }
     w.mm = o;  // the stream-K scratch of q's, k's and v's GEMMs (one at a time)
     o += std::max(gemm_sk_bytes(d, wq, m), std::max(gemm_sk_bytes(d, wk, m), gemm_sk_bytes(d, wv, m)));
@@ -1702,10 +1824,20 @@ int qmm_qkv_rope_kv_append_n(const qmm_qtensor* wq, const qmm_qtensor* wk, const
   const qmm_qtensor* w3[3] = {wq, wk, wv};
   float* p3[3] = {(float*)(b + L.q), (float*)(b + L.k), (float*)(b + L.v)};
   int sp[3];
-  for (int j = 0; j < 3; ++j) {
-    const GemmPlan pj = gemm_plan(d, w3[j], m, false);
-    sp[j] = pj.splits;
-    QMM_TRY(gemm_launch(d, w3[j], b + L.xp, m, pj, p3[j], w3[j]->n, nullptr, s, 0, p3[j], b + L.mm));
+  MultiPlan mp;
+  if (multi_plan(d, w3, 3, m, &mp)) {
+    // one launch over the three weights; its partials in the q / k / v regions (consecutive, in that order)
+    for (int j = 0; j < 3; ++j) {
+      sp[j] = mp.splits[j];
+      mp.off[j] = (size_t)((uint8_t*)p3[j] - (b + L.q));
+    }
+    QMM_TRY(multi_launch(d, w3, mp, b + L.xp, m, b + L.q, s));
+  } else {
+    for (int j = 0; j < 3; ++j) {
+      const GemmPlan pj = gemm_plan(d, w3[j], m, false);
+      sp[j] = pj.splits;
+      QMM_TRY(gemm_launch(d, w3[j], b + L.xp, m, pj, p3[j], w3[j]->n, nullptr, s, 0, p3[j], b + L.mm));
+    }
   }
   const float* qp = p3[0];
   const float* kp = p3[1];

@@ -1780,16 +1780,15 @@ __device__ __forceinline__ void mmqs6_epi(const uint8_t* __restrict__ buf, const
   (void)r;
 }
 
+// The 128 x 128 tile at (m0, n0), K steps [kb0, kb1), into y.
 // wd: the weight's separated f16 d per block (row-major, K / 256 per row).
 template <bool DUMP>
-__device__ __forceinline__ void mmqs6_q6k(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
-                                          const int8_t* __restrict__ xq, const float* __restrict__ xd,
-                                          float* __restrict__ y, int M, int N, int K, int ldy,
-                                          int* __restrict__ dump, int accumulate, int remap, int kb0, int kb1) {
+__device__ __forceinline__ void mmqs6_q6k_at(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                             const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                             float* __restrict__ y, int M, int N, int K, int ldy,
+                                             int* __restrict__ dump, int accumulate, int m0, int n0, int kb0,
+                                             int kb1) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  int mt, nt;
-  gemm_tile(remap, mt, nt);
-  const int m0 = mt * kSBM, n0 = nt * kSBN;
   const int nbk = K / 256;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 31, h = lane >> 5;
@@ -1818,6 +1817,16 @@ __device__ __forceinline__ void mmqs6_q6k(const uint8_t* __restrict__ wq, const 
     __syncthreads();
   }
   mmqs_store(acc, y, M, N, ldy, m0, n0, accumulate);
+}
+
+template <bool DUMP>
+__device__ __forceinline__ void mmqs6_q6k(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                          const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                          float* __restrict__ y, int M, int N, int K, int ldy,
+                                          int* __restrict__ dump, int accumulate, int remap, int kb0, int kb1) {
+  int mt, nt;
+  gemm_tile(remap, mt, nt);
+  mmqs6_q6k_at<DUMP>(wq, wd, xq, xd, y, M, N, K, ldy, dump, accumulate, mt * kSBM, nt * kSBN, kb0, kb1);
 }
 
 // Q8_0 prefill GEMM on the mmqs scaffold (mmqs8_q8_0): 128 x 128 tiles of
@@ -2018,6 +2027,51 @@ QMM_MMQS8_KERNEL(_dump, true)
   }
 QMM_MMQS6_KERNEL(, false)
 QMM_MMQS6_KERNEL(_dump, true)
+
+// Up to three Q4_K / Q6_K weights of one K over the same activation planes in
+// one launch (the prefill's q / k / v), each split over K into f32 partials:
+// workgroup b of the 1-D grid belongs to job j with start[j] <= b <
+// start[j + 1]; within the job, b - start[j] = split * tiles + tile, the tile
+// row-major over gx column tiles, its K steps [split * kc, split * kc + kc),
+// its partial at y + split * M * n (row stride n). The tiles and their
+// arithmetic are the single-weight kernels' (mmqs_q4k, mmqs6_q6k); the
+// dynamic LDS is the larger of their two layouts.
+struct MmqsJobs {
+  const uint8_t* w[3];
+  float* y[3];
+  int n[3], gx[3], kc[3], q6[3];  // q6: 1 for a Q6_K weight, 0 for Q4_K
+  int start[4];
+};
+
+namespace qmm {
+template <typename T>
+__device__ __forceinline__ T job3(const T (&a)[3], int j) {  // constant indices only (no scratch)
+  return j == 0 ? a[0] : j == 1 ? a[1] : a[2];
+}
+}  // namespace qmm
+
+extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+qmm_mmqs_multi(MmqsJobs jobs, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+               const int16_t* __restrict__ xs, int M, int K) {
+  const int b = (int)blockIdx.x;
+  const int j = b < jobs.start[1] ? 0 : b < jobs.start[2] ? 1 : 2;
+  const int local = b - (j == 0 ? jobs.start[0] : j == 1 ? jobs.start[1] : jobs.start[2]);
+  const int n = qmm::job3(jobs.n, j), gx = qmm::job3(jobs.gx, j), kc = qmm::job3(jobs.kc, j);
+  const int tiles = gx * ((M + qmm::kSBM - 1) / qmm::kSBM);
+  const int split = local / tiles, tile = local - split * tiles;
+  const int mt = tile / gx, nt = tile - mt * gx;
+  const int nbk = K / 256, kb0 = split * kc, kb1 = min(kb0 + kc, nbk);
+  const uint8_t* w = qmm::job3(jobs.w, j);
+  float* y = qmm::job3(jobs.y, j) + (size_t)split * M * n;
+  if (qmm::job3(jobs.q6, j))
+    qmm::mmqs6_q6k_at<false>(w, qmm::split_scales<qmm::kFmtQ6K>(w, n, K), xq, xd, y, M, n, K, n, nullptr, 0,
+                             mt * qmm::kSBM, nt * qmm::kSBN, kb0, kb1);
+  else {
+    qmm::f32x16 acc[qmm::kSTM];
+    qmm::mmqs_run<false>(w, xq, xd, xs, M, n, K, mt * qmm::kSBM, nt * qmm::kSBN, kb0, kb1, nullptr, acc);
+    qmm::mmqs_store(acc, y, M, n, n, mt * qmm::kSBM, nt * qmm::kSBN, 0);
+  }
+}
 
 extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 qmm_mmqs_q4k_sk(const uint8_t* __restrict__ wq, const int8_t* __restrict__ xq, const float* __restrict__ xd,

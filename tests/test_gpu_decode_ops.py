@@ -76,10 +76,16 @@ MIXES = [(GgmlDType.Q4K, GgmlDType.Q4K, GgmlDType.Q6K), (GgmlDType.Q6K, GgmlDTyp
 @pytest.mark.parametrize("m", [1, 2, 5, 64])
 @pytest.mark.parametrize("norm", [False, True])
 @pytest.mark.parametrize("k", [4096, 20480])
-def test_matmul_ex_mixed_q4k_q6k_equals_separate_calls(dts, m, norm, k):
+def test_matmul_ex_mixed_q4k_q6k_equals_separate_calls(monkeypatch, dts, m, norm, k):
     """Q4_K and Q6_K weights in one qmm_matmul_ex call (one mixed launch at m = 1; per-format launches
     over one shared RMSNorm and Q8_K quantization otherwise: GGML rows at m = 5, GEMM planes at m = 64):
-    bit-identical to one call per weight. k = 20480 takes the long-row prologue."""
+    bit-identical to one call per weight. k = 20480 takes the long-row prologue. At m = 64 two or three
+    weights that would each be split over K run as one launch with split counts chosen together
+    (qmm_mmqs_multi), so there the call equals one call per weight within 1e-5 * rms (the order of the split
+    sums), and bit for bit with QMM_QKV_SEPARATE=1 (one launch per weight)."""
+    joint = m > 8 and len(dts) <= 3
+    if joint:
+        monkeypatch.setenv("QMM_QKV_SEPARATE", "1")
     rng = np.random.default_rng(40 + m + len(dts))
     rows = [700, 256, 300, 1000, 33][:len(dts)]
     qts = [QTensor.quantize(t((rng.standard_normal((n, k)) * 0.02).astype(np.float32)), dt)
@@ -99,6 +105,14 @@ def test_matmul_ex_mixed_q4k_q6k_equals_separate_calls(dts, m, norm, k):
         qmm._check(L().qmm_matmul_ex((vp * 1)(q.handle.value), 1, x.data_ptr(), m, k, nwp, ctypes.c_float(1e-5), 0,
                                      (vp * 1)(want.data_ptr()), (i64 * 1)(n), ws.data_ptr(), wsb, S()))
         assert torch.equal(y, want)
+    if joint:
+        monkeypatch.delenv("QMM_QKV_SEPARATE")
+        yj = [torch.full((m, n), float("nan"), device=DEV) for n in rows]
+        qmm._check(L().qmm_matmul_ex((vp * len(qts))(*[q.handle.value for q in qts]), len(qts), x.data_ptr(), m, k,
+                                     nwp, ctypes.c_float(1e-5), 0, (vp * len(qts))(*[y.data_ptr() for y in yj]),
+                                     (i64 * len(qts))(*rows), ws.data_ptr(), wsb, S()))
+        for a, b in zip(yj, ys):
+            assert rel_err(a.cpu().numpy(), b.cpu().numpy()) <= 1e-5
 
 
 @pytest.mark.parametrize("m", [1, 3])

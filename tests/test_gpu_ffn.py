@@ -42,6 +42,18 @@ def rel_err(got, want):
     return float(np.abs(got - want).max() / np.sqrt((want ** 2).mean()))
 
 
+def device_rms_norm(x, nw):
+    """The device's RMSNorm rows (qmm_rms_norm, which the GEMMs' fused norm prologue equals bit for bit), so
+    that the oracle quantizes the very f32 values the device did: a last-bit difference of the norm that
+    lands on a Q8_K rounding tie would otherwise move one activation code (up to ~2e-3 of the rms)."""
+    m, k = x.shape
+    xd, nwd, out = t(x), t(nw), torch.empty((m, k), device=DEV)
+    qmm._check(L().qmm_rms_norm(xd.data_ptr(), m, k, k, nwd.data_ptr(), ctypes.c_float(1e-5), out.data_ptr(), k,
+                                S()))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
 def make(H, F, seed, gdt=GgmlDType.Q4K, ddt=GgmlDType.Q6K):
     g = torch.Generator(device=DEV).manual_seed(seed)
     w = {name: torch.randn(shape, generator=g, device=DEV) * 0.02
@@ -113,9 +125,48 @@ def test_gate_up_pair_equals_unsplit_launches(monkeypatch, m):
     unsplit = run()
     for a, b in zip(got, unsplit):
         assert np.array_equal(a, b)
-    xin = ol.rms_norm(x, nw, 1e-5)
+    xin = device_rms_norm(x, nw)
     for q, r, a, b in zip((gate, up), (r0, r1), got, split):
         want = r + orc.matmul(orc.Q4K, xin, q.to_ggml(), H)
+        assert rel_err(a, want) <= TOL and rel_err(b, want) <= TOL
+
+
+@pytest.mark.parametrize("m", [127, 64, 24])
+@pytest.mark.parametrize("kinds", ["q4k_q4k_q6k", "q4k_q4k"])
+def test_multi_weight_launch_matches_separate_launches(monkeypatch, m, kinds):
+    """q / k / v of the 8B shape (4096, 1024, 1024 rows of 4096; v Q6_K) through qmm_matmul_ex at m rows: one
+    launch over all weights with jointly chosen split counts (qmm_mmqs_multi), then a split sum per weight,
+    with the residual add. Against one launch per weight (QMM_QKV_SEPARATE=1: each with its own split count)
+    within 1e-5 * rms (the split sums' f32 order), and against the oracle within 1e-3 * rms."""
+    H = 4096
+    dts = [GgmlDType.Q4K, GgmlDType.Q4K, GgmlDType.Q6K][:len(kinds.split("_"))]
+    rows = [4096, 1024, 1024][:len(dts)]
+    g = torch.Generator(device=DEV).manual_seed(400 + m)
+    qts = [QTensor.quantize(torch.randn((n, H), generator=g, device=DEV) * 0.02, dt) for n, dt in zip(rows, dts)]
+    rng = np.random.default_rng(410 + m)
+    x = rng.standard_normal((m, H)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    r0 = [rng.standard_normal((m, n)).astype(np.float32) for n in rows]
+
+    def run():
+        ys = [t(r) for r in r0]
+        wsb = max(int(L().qmm_matmul_ex_workspace_size(q.handle, m, 1)) for q in qts)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+        xd, nwd = t(x), t(nw)
+        qmm._check(L().qmm_matmul_ex((vp * len(qts))(*[q.handle.value for q in qts]), len(qts), xd.data_ptr(), m, H,
+                                     nwd.data_ptr(), ctypes.c_float(1e-5), 1,
+                                     (vp * len(qts))(*[y.data_ptr() for y in ys]), (i64 * len(qts))(*rows),
+                                     ws.data_ptr(), wsb, S()))
+        torch.cuda.synchronize()
+        return [y.cpu().numpy() for y in ys]
+
+    got = run()
+    monkeypatch.setenv("QMM_QKV_SEPARATE", "1")
+    sep = run()
+    xin = device_rms_norm(x, nw)
+    for q, dt, r, a, b in zip(qts, dts, r0, got, sep):
+        want = r + orc.matmul(orc.Q4K if dt == GgmlDType.Q4K else orc.Q6K, xin, q.to_ggml(), H)
+        assert rel_err(a, b) <= 1e-5
         assert rel_err(a, want) <= TOL and rel_err(b, want) <= TOL
 
 
