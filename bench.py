@@ -642,7 +642,8 @@ def kernel_only(torch, dev, which, launches):
     `copy` = a 256 MiB device copy (the calibration for FETCH_SIZE / WRITE_SIZE); `gemm_gate` / `gemm_down` =
     the config-4 GEMMs (M = 512; `gemm_q6k_*` / `gemm_q8_0_*`: its Q6_K / Q8_0 legs); `moe` = the config-5 expert
     FFN (`moe32`: at 32 tokens; `moe_prefill`: at 512 tokens); `gate_m8` = the gate GEMV on eight pre-quantized rows; `gate_up` = gate and up
-    in one launch with the RMSNorm + Q8_K prologue (the FFN pair as the decoder runs it)."""
+    in one launch with the RMSNorm + Q8_K prologue (the FFN pair as the decoder runs it); `decode` / `prefill` =
+    config-3 token steps / batched 127-row prefills, eagerly."""
     from inference_amd import GgmlDType, QTensor, qmm
     from inference_amd.synth import normal, normal_torch
     if which == "copy":
@@ -752,6 +753,24 @@ def kernel_only(torch, dev, which, launches):
         torch.cuda.synchronize()
         print(json.dumps({"kernel_only": "decode", "steps": launches, "positions": [127, 127 + launches - 1]}),
               flush=True)
+        return
+    if which == "prefill":
+        # config 3: the 8B-shape Q4_K_M model, `launches` eager batched prefills of a 128-token prompt (127
+        # rows through the GEMM path; every kernel its own dispatch in a trace)
+        from inference_amd.llama_decode import DecodeSession, LlamaConfig, LlamaWeights
+        cfg = LlamaConfig.llama3_8b()
+        w = LlamaWeights.random(cfg, 4, dev)
+        prompt = [int(t) for t in np.random.default_rng(4).integers(0, cfg.vocab, 128)]
+        sess = DecodeSession(w, 128 + 8)
+        ms = []
+        for _ in range(launches):
+            sess.reset(prompt)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            rows = sess.prefill()
+            torch.cuda.synchronize()
+            ms.append(round((time.perf_counter() - t0) * 1e3, 3))
+        print(json.dumps({"kernel_only": "prefill", "prefills": launches, "rows": rows, "ms": ms}), flush=True)
         return
     if which in ("q8_0", "down_q6k"):
         # config 1: the Q8_0 4096x4096 matvec, one qmm_matmul (fused Q8_0 prologue) per launch; or the
@@ -883,7 +902,7 @@ def main():
     ap.add_argument("--kernel-only", choices=("gate", "gate_m8", "gate_up", "qkvgu", "qkvgu_staged", "grouped", "copy",
                                               "gemm_gate", "gemm_down", "gemm_q6k_gate", "gemm_q6k_down",
                                               "gemm_q8_0_gate", "gemm_q8_0_down", "moe", "moe32", "moe_prefill",
-                                              "q8_0", "down_q6k", "decode", "read_9mb", "read_33mb",
+                                              "q8_0", "down_q6k", "decode", "prefill", "read_9mb", "read_33mb",
                                               "read_80mb", "read_1gb", "read_graph"),
                     default=None,
                     help="launch only one GEMV launch kind or a calibration copy --steps times (counter runs)")
