@@ -131,13 +131,14 @@ def test_gate_up_pair_equals_unsplit_launches(monkeypatch, m):
         assert rel_err(a, want) <= TOL and rel_err(b, want) <= TOL
 
 
-@pytest.mark.parametrize("m", [127, 64, 24])
+@pytest.mark.parametrize("m", [257, 127, 64, 24, 9])
 @pytest.mark.parametrize("kinds", ["q4k_q4k_q6k", "q4k_q4k"])
 def test_multi_weight_launch_matches_separate_launches(monkeypatch, m, kinds):
     """q / k / v of the 8B shape (4096, 1024, 1024 rows of 4096; v Q6_K) through qmm_matmul_ex at m rows: one
     launch over all weights with jointly chosen split counts (qmm_mmqs_multi), then a split sum per weight,
     with the residual add. Against one launch per weight (QMM_QKV_SEPARATE=1: each with its own split count)
-    within 1e-5 * rms (the split sums' f32 order), and against the oracle within 1e-3 * rms."""
+    within 1e-5 * rms (the split sums' f32 order), and against the oracle within 1e-3 * rms. 257 rows take
+    three row tiles per weight, 9 the smallest GEMM."""
     H = 4096
     dts = [GgmlDType.Q4K, GgmlDType.Q4K, GgmlDType.Q6K][:len(kinds.split("_"))]
     rows = [4096, 1024, 1024][:len(dts)]
