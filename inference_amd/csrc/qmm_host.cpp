@@ -1205,9 +1205,12 @@ int qmm_matmul_q_ex(const qmm_qtensor* w, const void* xq, int64_t m, float* y, i
 // rounds x K steps are no more than the two split launches': no partials to
 // write and read back, one launch fewer (127 rows: 108.9 us for the block
 // against 114.4). Unsplit grids stay two launches (512 rows: 349 us against
-// 363 paired). QMM_FFN_SEPARATE keeps two launches.
+// 363 paired). QMM_FFN_SEPARATE (or a split count forced by QMM_SPLITK) keeps
+// two launches.
 static bool pair_plan(const Device* d, const qmm_qtensor* a, const qmm_qtensor* b, int64_t m) {
-  if (!use_gemm(a, m) || a->dtype != b->dtype || a->n != b->n || a->k != b->k || env(kEnvFfnPair) != nullptr)
+  // QMM_SPLITK (a forced split count) keeps every weight on its own launch
+  if (!use_gemm(a, m) || a->dtype != b->dtype || a->n != b->n || a->k != b->k || env(kEnvFfnPair) != nullptr ||
+      env(kEnvSplitK) != nullptr)
     return false;
   const GemmPlan pa = gemm_plan(d, a, m, false);
   if (pa.sk_tiles != 0 || pa.splits < 2 || strcmp(pa.name, "qmm_mmqs_q4k") != 0) return false;
@@ -1245,7 +1248,8 @@ static int gemm_pair_launch(Device* d, const qmm_qtensor* a, const qmm_qtensor* 
 // must fit in the largest of the jobs' own split scratch, so a workspace
 // sized for the separate launches holds them. 8B q / k / v at 127 rows:
 // splits 4 / 4 / 8 in one launch of 224 workgroups, against 8 / 8 / 8 in
-// three. QMM_QKV_SEPARATE keeps one launch per weight.
+// three. QMM_QKV_SEPARATE (or a split count forced by QMM_SPLITK) keeps one
+// launch per weight.
 struct MmqsJobs {  // the kernel's by-value argument (qmm_mmqs_multi)
   const void* w[3];
   float* y[3];
@@ -1260,7 +1264,7 @@ struct MultiPlan {
 };
 
 static bool multi_plan(const Device* d, const qmm_qtensor* const* w, int count, int64_t m, MultiPlan* out) {
-  if (count < 2 || count > 3 || env(kEnvQkvSeparate) != nullptr) return false;
+  if (count < 2 || count > 3 || env(kEnvQkvSeparate) != nullptr || env(kEnvSplitK) != nullptr) return false;
   size_t bound = 0;
   int q6[3] = {0, 0, 0};
   for (int j = 0; j < count; ++j) {
