@@ -824,6 +824,10 @@ static constexpr unsigned kMmqStaticLds = 61440;  // the first-generation tile's
 // codes, digit bytes, column d, row scales (128 x 256, 128 x 256, 128 x 48,
 // 128 x 4, 128 x 4 bytes)
 static constexpr unsigned kS6StageBytes = 128 * 256 + 128 * 256 + 128 * 48 + 128 * 4 + 128 * 4;
+// one LDS stage of the split-scale Q4_K tile (mmqs): activation rows, weight
+// quants, block headers, row scales, A' and B' rows, split-scale multipliers
+// (the kernels' SLayout<false>::kStage; DUMP adds 128 x 16 bytes of sums)
+static constexpr unsigned kSStageBytes = 128 * 256 + 128 * 128 + 128 * 16 + 128 * 4 + 128 * 48 + 128 * 48 + 128 * 80;
 // One LDS stage of the Q8_0 tile (mmqs8): activation rows, weight codes, f32
 // weight and activation block scales (the kernels' kS8Stage).
 static constexpr unsigned kS8StageBytes = 128 * 256 + 128 * 256 + 128 * 32 + 8 * 128 * 4;
@@ -920,8 +924,7 @@ static GemmPlan gemm_plan(const Device* d, const qmm_qtensor* w, int64_t m, bool
   // Q4_K default: mmqs (split-scale d term on int8 MFMA, mins term on bf16
   // MFMA, 128 x 128 tiles of eight waves, two per SIMD, LDS 2 x 72.5 KB);
   // QMM_MMQ=2 / 4 select the older generations
-  const unsigned ldss =
-      2u * (128 * 256 + 128 * 128 + 128 * 16 + 128 * 4 + 128 * 48 + 128 * 48 + 128 * 80 + (dump ? 128 * 16 : 0));
+  const unsigned ldss = 2u * (kSStageBytes + (dump ? 128 * 16 : 0));
   if (fmt == kFmtQ4K && gen == nullptr && (int)ldss <= d->max_lds) {
     snprintf(p.name, sizeof(p.name), "qmm_mmqs_q4k%s", dump ? "_dump" : "");
     p.gx = (unsigned)((N + 127) / 128);
@@ -1341,8 +1344,7 @@ static int multi_launch(Device* d, const qmm_qtensor* const* w, const MultiPlan&
   int M = (int)m, K = (int)w[0]->k;
   void* args[] = {&jobs, &q8, &dd, &ss, &M, &K};
   // the larger of the two tiles' LDS (mmqs: 2 x 72.5 KB, mmqs6: 2 x 71 KB)
-  const unsigned lds_q4 = 2u * (128 * 256 + 128 * 128 + 128 * 16 + 128 * 4 + 128 * 48 + 128 * 48 + 128 * 80);
-  const unsigned lds = std::max(2 * kS6StageBytes, lds_q4);
+  const unsigned lds = 2 * std::max(kS6StageBytes, kSStageBytes);
   return launch(d, "qmm_mmqs_multi", (unsigned)start, 512, lds, s, args);
 }
 
