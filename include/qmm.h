@@ -354,6 +354,18 @@ int qmm_prefill_attention(const float *q, int64_t ldq, const float *kcache, cons
                           int64_t count, float *out, int64_t ldo, int heads, int kv_heads, int head_dim, int max_seq,
                           float scale, void *stream);
 
+/* qmm_prefill_attention followed by qmm_matmul_ex(&wo, 1, ...) with accumulate:
+ * x[i] += att[i] . wo^T for the count prompt rows (LlamaAttention::forward's
+ * o_proj and the decoder layer's residual add, llama.rs:1115-1120, 654-725),
+ * bit for bit. Where the o GEMM takes Q8_K planes (count > 8, a Q4_K / Q6_K
+ * weight) and heads / kv_heads * head_dim is a multiple of 256, the attention
+ * launch writes those planes itself. ws: device scratch of
+ * qmm_prefill_attention_o_workspace_size(wo, count) bytes. */
+int qmm_prefill_attention_o(const float *q, int64_t ldq, const float *kcache, const float *vcache, int64_t first,
+                            int64_t count, int heads, int kv_heads, int head_dim, int max_seq, float scale,
+                            const qmm_qtensor *wo, float *x, int64_t ldx, void *ws, size_t ws_bytes, void *stream);
+size_t qmm_prefill_attention_o_workspace_size(const qmm_qtensor *wo, int64_t count);
+
 /* h = silu(g) * u over n elements, f32 (LlamaMlp::forward, llama.rs:1386-1391). */
 int qmm_silu_mul(const float *g, const float *u, float *h, int64_t n, void *stream);
 

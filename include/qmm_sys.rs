@@ -357,6 +357,12 @@ extern "C" {
         out: *mut f32, ldo: i64, heads: c_int, kv_heads: c_int, head_dim: c_int, max_seq: c_int, scale: f32,
         stream: *mut c_void
     ) -> c_int;
+    pub fn qmm_prefill_attention_o(
+        q: *const f32, ldq: i64, kcache: *const f32, vcache: *const f32, first: i64, count: i64,
+        heads: c_int, kv_heads: c_int, head_dim: c_int, max_seq: c_int, scale: f32, wo: *const QmmQTensor,
+        x: *mut f32, ldx: i64, ws: *mut c_void, ws_bytes: usize, stream: *mut c_void
+    ) -> c_int;
+    pub fn qmm_prefill_attention_o_workspace_size(wo: *const QmmQTensor, count: i64) -> usize;
 
     /// h = silu(g) * u over n elements, f32 (LlamaMlp::forward, llama.rs:1386-1391).
     pub fn qmm_silu_mul(g: *const f32, u: *const f32, h: *mut f32, n: i64, stream: *mut c_void) -> c_int;

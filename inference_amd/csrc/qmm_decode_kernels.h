@@ -238,7 +238,11 @@ __device__ __forceinline__ float row16_total(float v) {
 // q is already rotated) and writes its normalised output to out + i * ldo.
 // The arithmetic is the S = 1 case of the chunked form (the merge of one
 // record multiplies by e^0 = 1).
-template <int DPL, int GT, int NW, bool PREFILL = false>
+// PLANES (PREFILL only): instead of f32 rows, the query row's G * dim
+// outputs (whole 256-element blocks: G * dim % 256 == 0, starting at column
+// g * G * dim) go to the Q8_K GEMM planes of row blockIdx.y (q8 / d / s over
+// rows of kq values), quantized as qmm_quantize_q8k_mmq quantizes the f32 row.
+template <int DPL, int GT, int NW, bool PREFILL = false, bool PLANES = false>
 __device__ __forceinline__ void decode_attention(const float* __restrict__ q, const float* __restrict__ k_new,
                                                  const float* __restrict__ v_new, const float* __restrict__ cos_t,
                                                  const float* __restrict__ sin_t, const int* __restrict__ pos,
@@ -246,7 +250,9 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
                                                  float* __restrict__ part, unsigned* __restrict__ counters,
                                                  float* __restrict__ out, int heads, int kv_heads, int max_seq,
                                                  float scale, int first = 0, long long ldq = 0,
-                                                 long long ldo = 0) {
+                                                 long long ldo = 0, int8_t* __restrict__ pq8 = nullptr,
+                                                 float* __restrict__ pd = nullptr, int16_t* __restrict__ ps = nullptr,
+                                                 int kq = 0) {
 #pragma clang fp contract(off)
   constexpr int dim = 64 * DPL;
   constexpr int R = dim / 16;  // dims per lane: a 16-lane row holds one position's row
@@ -256,6 +262,7 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
   __shared__ float wst[NR][2 * GT];
   __shared__ __attribute__((aligned(16))) float wo[NR][GT * dim];
   __shared__ int last;
+  __shared__ __attribute__((aligned(16))) float ob[PLANES ? GT * dim : 1];  // PLANES: the row's outputs
   const int g = blockIdx.x, c = PREFILL ? 0 : blockIdx.y, t = threadIdx.x;
   const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int li = lane & 15, row = 4 * wave + (lane >> 4);  // this lane's place in its row, the row's index
@@ -426,7 +433,10 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
         osum += wo[w][i] * a;
       }
     }
-    if constexpr (PREFILL) {
+    if constexpr (PLANES) {
+      ob[i] = osum / lsum;
+      continue;
+    } else if constexpr (PREFILL) {
       out[(size_t)(g * G + h) * dim + d] = osum / lsum;
       continue;
     }
@@ -436,6 +446,14 @@ __device__ __forceinline__ void decode_attention(const float* __restrict__ q, co
       __hip_atomic_store(r, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(r + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+  }
+  if constexpr (PLANES) {
+    // one wave per 256-element block of the row's G * dim outputs
+    __syncthreads();
+    const int nb = kq / 256, nblk = G * dim / 256, b0 = g * G * dim / 256;
+    for (int b = wave; b < nblk; b += NW)
+      put_q8k_plane(q8k_lane(ob + 256 * b, lane), (long long)blockIdx.y * nb + b0 + b, nb, kq, pq8, pd, ps, lane);
+    return;
   }
   if constexpr (PREFILL) return;
   // every thread's record stores have completed before the barrier, so they
@@ -595,6 +613,24 @@ QMM_ATTN_KERNEL(4, 1, 8) QMM_ATTN_KERNEL(4, 2, 8) QMM_ATTN_KERNEL(4, 4, 4) QMM_A
 QMM_PREFILL_ATTN_KERNELS(1)
 QMM_PREFILL_ATTN_KERNELS(2)
 QMM_PREFILL_ATTN_KERNELS(4)
+
+// The same attention writing the o projection's Q8_K GEMM planes (rows of kq
+// = heads * head_dim values) instead of f32 rows; G * head_dim a multiple of
+// 256 (the host checks it).
+#define QMM_PREFILL_ATTN_PLANES_KERNEL(DPL, GT)                                                                  \
+  extern "C" __global__ void __launch_bounds__(256) qmm_prefill_attention_planes_d##DPL##_g##GT(                 \
+      const float* __restrict__ q, long long ldq, const float* __restrict__ kcache,                              \
+      const float* __restrict__ vcache, int first, int8_t* __restrict__ q8, float* __restrict__ d,               \
+      int16_t* __restrict__ s, int kq, int heads, int kv_heads, int max_seq, float scale) {                      \
+    qmm::decode_attention<DPL, GT, 4, true, true>(q, nullptr, nullptr, nullptr, nullptr, nullptr,                \
+                                                  const_cast<float*>(kcache), const_cast<float*>(vcache),        \
+                                                  nullptr, nullptr, nullptr, heads, kv_heads, max_seq, scale,    \
+                                                  first, ldq, 0, q8, d, s, kq);                                  \
+  }
+QMM_PREFILL_ATTN_PLANES_KERNEL(1, 4) QMM_PREFILL_ATTN_PLANES_KERNEL(1, 8)
+QMM_PREFILL_ATTN_PLANES_KERNEL(2, 2) QMM_PREFILL_ATTN_PLANES_KERNEL(2, 4) QMM_PREFILL_ATTN_PLANES_KERNEL(2, 8)
+QMM_PREFILL_ATTN_PLANES_KERNEL(4, 1) QMM_PREFILL_ATTN_PLANES_KERNEL(4, 2) QMM_PREFILL_ATTN_PLANES_KERNEL(4, 4)
+QMM_PREFILL_ATTN_PLANES_KERNEL(4, 8)
 
 // One Q8_K block of silu(g) * u (one wave): the 256 elements at g / u
 // into the 292-byte block at blk.

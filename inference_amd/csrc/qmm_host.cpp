@@ -100,13 +100,14 @@ std::atomic<Device*> g_dev[64] = {};
 enum EnvKey {
   kEnvGemv1, kEnvGemv1p, kEnvGemvCfg, kEnvGemvWavesPerCu, kEnvGemvRows, kEnvSplitK, kEnvMmq2, kEnvMmq,
   kEnvMmq4Bn, kEnvMmq1, kEnvMmqXcd, kEnvMoeGemv, kEnvMoeMmq, kEnvMoeBm, kEnvMoeSplitK, kEnvMoeGrouped, kEnvGroupedP,
-  kEnvGroupedWgs, kEnvStreamK, kEnvGemvm, kEnvMmq6, kEnvMmq8, kEnvMoeTails, kEnvFfnPair, kEnvQkvSeparate, kEnvCount
+  kEnvGroupedWgs, kEnvStreamK, kEnvGemvm, kEnvMmq6, kEnvMmq8, kEnvMoeTails, kEnvFfnPair, kEnvQkvSeparate, kEnvAttnOSeparate, kEnvCount
 };
 const char* const kEnvNames[kEnvCount] = {
     "QMM_GEMV1", "QMM_GEMV1P", "QMM_GEMV_CFG", "QMM_GEMV_WAVES_PER_CU", "QMM_GEMV_ROWS", "QMM_SPLITK",
     "QMM_MMQ2", "QMM_MMQ", "QMM_MMQ4_BN", "QMM_MMQ1", "QMM_MMQ_XCD", "QMM_MOE_GEMV", "QMM_MOE_MMQ",
     "QMM_MOE_BM", "QMM_MOE_SPLITK", "QMM_MOE_GROUPED", "QMM_GROUPED_P", "QMM_GROUPED_WGS",
-    "QMM_STREAMK", "QMM_GEMVM", "QMM_MMQ6", "QMM_MMQ8", "QMM_MOE_TAILS", "QMM_FFN_SEPARATE", "QMM_QKV_SEPARATE"};
+    "QMM_STREAMK", "QMM_GEMVM", "QMM_MMQ6", "QMM_MMQ8", "QMM_MOE_TAILS", "QMM_FFN_SEPARATE", "QMM_QKV_SEPARATE",
+    "QMM_ATTN_O_SEPARATE"};
 
 struct Tuning {
   int w = 0, r = 0, u = 0, waves_per_cu = 0, gemv1 = 1, gemv1p = -1;
@@ -2126,6 +2127,72 @@ int qmm_prefill_attention(const float* q, int64_t ldq, const float* kcache, cons
   QMM_HIP(hipModuleLaunchKernel(fn, (unsigned)kv_heads, (unsigned)count, 1, 256, 1, 1, 0, (hipStream_t)stream, args,
                                 nullptr));
   return QMM_OK;
+}
+
+// Attention of the prompt rows followed by the o projection added into the
+// residual (LlamaAttention::forward's o_proj and the decoder layer's residual
+// add, llama.rs:1115-1120, 654-725): where the o GEMM takes Q8_K planes
+// (m > 8, a k-quant weight) and a kv head's G * head_dim outputs are whole
+// 256-element blocks, the attention launch writes the planes itself
+// (qmm_prefill_attention_planes_*), so the f32 rows and the plane quantizer's
+// launch drop out; the GEMM then runs as qmm_matmul_ex runs it. Otherwise the
+// two calls. Either way the bits of qmm_prefill_attention followed by
+// qmm_matmul_ex(o, accumulate = 1).
+size_t qmm_prefill_attention_o_workspace_size(const qmm_qtensor* wo, int64_t count) {
+  if (!wo || count < 1) return 0;
+  const size_t mm = qmm_matmul_ex_workspace_size(wo, count, 0);
+  if (mm == 0) return 0;
+  return align256((size_t)count * (size_t)wo->k * 4) + mm;
+}
+
+int qmm_prefill_attention_o(const float* q, int64_t ldq, const float* kcache, const float* vcache, int64_t first,
+                            int64_t count, int heads, int kv_heads, int head_dim, int max_seq, float scale,
+                            const qmm_qtensor* wo, float* x, int64_t ldx, void* ws, size_t ws_bytes, void* stream) {
+  if (!q || !kcache || !vcache || !wo || !x) return fail(QMM_ERR_INVALID, "null pointer");
+  QMM_TRY(check_attention(heads, kv_heads, head_dim, max_seq));
+  const int64_t H = (int64_t)heads * head_dim;
+  if (wo->k != H)
+    return fail(QMM_ERR_INVALID, "o weight of k = %lld for %lld attention outputs", (long long)wo->k, (long long)H);
+  if (first < 0 || count < 0 || first + count > max_seq || count > 65535)
+    return fail(QMM_ERR_INVALID, "positions [%lld, %lld) outside the cache of %d", (long long)first,
+                (long long)(first + count), max_seq);
+  if (ldq < H || ldx < wo->n) return fail(QMM_ERR_INVALID, "row strides below the row widths");
+  if (count == 0) return QMM_OK;
+  const size_t need = qmm_prefill_attention_o_workspace_size(wo, count);
+  if (need == 0) return fail(QMM_ERR_UNSUPPORTED, "o weight format not supported");
+  if (!ws || ws_bytes < need) return fail(QMM_ERR_INVALID, "workspace of %zu B < %zu B needed", ws_bytes, need);
+  Device* d;
+  QMM_TRY(current_device(&d));
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t* b = (uint8_t*)ws;
+  const int G = heads / kv_heads;
+  const bool fuse = use_gemm(wo, count) && qmm_vec_dot_type(wo->dtype) == QMM_Q8K && (G * head_dim) % 256 == 0 &&
+                    env(kEnvAttnOSeparate) == nullptr;
+  if (!fuse) {
+    float* att = (float*)b;
+    const size_t a = align256((size_t)count * (size_t)H * 4);
+    QMM_TRY(qmm_prefill_attention(q, ldq, kcache, vcache, first, count, att, H, heads, kv_heads, head_dim, max_seq,
+                                  scale, stream));
+    const qmm_qtensor* w1[1] = {wo};
+    float* y1[1] = {x};
+    const int64_t l1[1] = {ldx};
+    return qmm_matmul_ex(w1, 1, att, count, H, nullptr, 0.0f, 1, y1, l1, b + a, ws_bytes - a, stream);
+  }
+  const Planes pl = mmq_planes(wo->dtype, count, H);
+  const int gt = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;
+  char name[64];
+  snprintf(name, sizeof(name), "qmm_prefill_attention_planes_d%d_g%d", head_dim / 64, gt);
+  long long a = ldq;
+  int f = (int)first, kq = (int)H;
+  void* q8 = b + pl.q8;
+  void* dd = b + pl.d;
+  void* ss = b + pl.s;
+  void* args[] = {&q, &a, &kcache, &vcache, &f, &q8, &dd, &ss, &kq, &heads, &kv_heads, &max_seq, &scale};
+  hipFunction_t fn;
+  QMM_TRY(kernel(d, name, &fn));
+  QMM_HIP(hipModuleLaunchKernel(fn, (unsigned)kv_heads, (unsigned)count, 1, 256, 1, 1, 0, s, args, nullptr));
+  // the GEMM as matmul_targets runs it: planes first, split partials in the rest
+  return gemm(d, wo, b, count, x, ldx, nullptr, s, 1, (float*)(b + pl.total), ws_bytes - pl.total);
 }
 
 int qmm_stream_read(const void* data, size_t bytes, uint32_t* sink, int variant, int wgs_per_cu, void* stream) {

@@ -393,7 +393,8 @@ class DecodeSession:
                 wsb = max(wsb, int(L.qmm_ffn_workspace_size(lw["gate"].handle, lw["up"].handle,
                                                              lw["down"].handle, rows, 1)),
                           int(L.qmm_qkv_rope_kv_append_n_workspace_size(lw["q"].handle, lw["k"].handle,
-                                                                        lw["v"].handle, rows, 1)))
+                                                                        lw["v"].handle, rows, 1)),
+                          int(L.qmm_prefill_attention_o_workspace_size(lw["o"].handle, rows)))
         ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
         vp, i64 = ctypes.c_void_p, ctypes.c_int64
         eps = ctypes.c_float(cfg.eps)
@@ -426,12 +427,18 @@ class DecodeSession:
                                                   self.cos.data_ptr(), self.sin.data_ptr(), 0, rows, kc, vc,
                                                   cfg.heads, cfg.kv_heads, hd, self.max_seq, s))
                 tr("rope_kv", li)
-            qmm._check(L.qmm_prefill_attention(q.data_ptr(), nq, kc, vc, 0, rows, att.data_ptr(), nq, cfg.heads,
-                                               cfg.kv_heads, hd, self.max_seq, ctypes.c_float(self.scale), s))
-            tr("attention", li)
-            qmm._check(L.qmm_matmul_ex((vp * 1)(lw["o"].handle.value), 1, att.data_ptr(), rows, nq, None, eps, 1,
-                                       x_y, x_ld, ws.data_ptr(), ws.numel(), s))
-            tr("o", li)
+            if trace is None:
+                # attention + o + residual in one entry (the attention launch writes the o GEMM's planes)
+                qmm._check(L.qmm_prefill_attention_o(q.data_ptr(), nq, kc, vc, 0, rows, cfg.heads, cfg.kv_heads, hd,
+                                                     self.max_seq, ctypes.c_float(self.scale), lw["o"].handle,
+                                                     x.data_ptr(), H, ws.data_ptr(), ws.numel(), s))
+            else:
+                qmm._check(L.qmm_prefill_attention(q.data_ptr(), nq, kc, vc, 0, rows, att.data_ptr(), nq, cfg.heads,
+                                                   cfg.kv_heads, hd, self.max_seq, ctypes.c_float(self.scale), s))
+                tr("attention", li)
+                qmm._check(L.qmm_matmul_ex((vp * 1)(lw["o"].handle.value), 1, att.data_ptr(), rows, nq, None, eps, 1,
+                                           x_y, x_ld, ws.data_ptr(), ws.numel(), s))
+                tr("o", li)
             if trace is None:
                 qmm._check(L.qmm_ffn(lw["gate"].handle, lw["up"].handle, lw["down"].handle, x.data_ptr(), rows, H,
                                      w.ffn_norm[li].data_ptr(), eps, 1, x.data_ptr(), H, ws.data_ptr(), ws.numel(),

@@ -59,7 +59,8 @@ EXPORTS = (
     "qmm_gguf_tensor_info", "qmm_gguf_type_size", "qmm_gguf_tensor_data", "qmm_gguf_meta_info",
     "qmm_gguf_meta_u64", "qmm_gguf_meta_i64", "qmm_gguf_meta_f64", "qmm_gguf_meta_string",
     "qmm_gguf_load_qtensor", "qmm_qtensor_dequantize_to", "qmm_embed_rows_n", "qmm_rope_kv_append_n",
-    "qmm_prefill_attention", "qmm_silu_mul", "qmm_matmul_q_workspace_size", "qmm_matmul_noalloc",
+    "qmm_prefill_attention", "qmm_prefill_attention_o", "qmm_prefill_attention_o_workspace_size",
+    "qmm_silu_mul", "qmm_matmul_q_workspace_size", "qmm_matmul_noalloc",
     "qmm_stream_read", "qmm_reload_tuning", "qmm_moe_route_ex", "qmm_moe_ffn_ex_workspace_size", "qmm_moe_ffn_ex",
     "qmm_decode_rope_attention_warm", "qmm_matmul_grouped",
 )
@@ -164,6 +165,9 @@ def lib() -> ctypes.CDLL:
                                      i32),
             "qmm_prefill_attention": ([vp, i64, vp, vp, i64, i64, vp, i64, i32, i32, i32, i32, ctypes.c_float, vp],
                                       i32),
+            "qmm_prefill_attention_o": ([vp, i64, vp, vp, i64, i64, i32, i32, i32, i32, ctypes.c_float, vp, vp, i64, vp,
+                                         sz, vp], i32),
+            "qmm_prefill_attention_o_workspace_size": ([vp, i64], sz),
             "qmm_silu_mul": ([vp, vp, vp, i64, vp], i32),
             "qmm_stream_read": ([vp, ctypes.c_size_t, vp, i32, i32, vp], i32),
         }

@@ -293,3 +293,56 @@ def test_qkv_rope_rejects_bad_arguments():
     assert size(wq.handle, wk.handle, wv8.handle, 16, 1) == 0  # Q8_0 weight
     assert size(wq.handle, wk.handle, wq.handle, 16, 1) == 0   # k and v of different row counts
     assert size(wq.handle, wk.handle, wk.handle, 0, 1) == 0    # no rows
+
+@pytest.mark.parametrize("m,heads,kv_heads,hd", [(127, 32, 8, 128), (24, 32, 8, 128), (9, 32, 8, 128),
+                                                 (5, 32, 8, 128), (40, 8, 8, 128), (33, 16, 4, 64)])
+def test_prefill_attention_o_equals_the_two_calls(monkeypatch, m, heads, kv_heads, hd):
+    """qmm_prefill_attention_o (causal attention of m prompt rows, then o and the residual add) against
+    qmm_prefill_attention followed by qmm_matmul_ex(o, accumulate), bit for bit: with the attention launch
+    writing the o GEMM's Q8_K planes (m > 8, G * head_dim a multiple of 256: 32 / 8 heads of 128, 16 / 4 of
+    64), and through the two calls themselves (m = 5: the GEMV; 8 / 8 heads: 128 outputs per kv head;
+    QMM_ATTN_O_SEPARATE=1)."""
+    H, max_seq, first = heads * hd, 160, 3
+    g = torch.Generator(device=DEV).manual_seed(500 + m)
+    wo = QTensor.quantize(torch.randn((4096, H), generator=g, device=DEV) * 0.02, GgmlDType.Q4K)
+    q = torch.randn((m, H), generator=g, device=DEV)
+    kc = torch.randn((kv_heads, max_seq, hd), generator=g, device=DEV)
+    vc = torch.randn((kv_heads, max_seq, hd), generator=g, device=DEV)
+    x0 = torch.randn((m, 4096), generator=g, device=DEV)
+    scale = ctypes.c_float(1.0 / np.sqrt(hd))
+
+    def fused():
+        x = x0.clone()
+        wsb = int(L().qmm_prefill_attention_o_workspace_size(wo.handle, m))
+        ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+        qmm._check(L().qmm_prefill_attention_o(q.data_ptr(), H, kc.data_ptr(), vc.data_ptr(), first, m, heads,
+                                               kv_heads, hd, max_seq, scale, wo.handle, x.data_ptr(), 4096,
+                                               ws.data_ptr(), wsb, S()))
+        return x
+
+    att = torch.empty((m, H), device=DEV)
+    qmm._check(L().qmm_prefill_attention(q.data_ptr(), H, kc.data_ptr(), vc.data_ptr(), first, m, att.data_ptr(), H,
+                                         heads, kv_heads, hd, max_seq, scale, S()))
+    want = x0.clone()
+    wsb = int(L().qmm_matmul_ex_workspace_size(wo.handle, m, 0))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    qmm._check(L().qmm_matmul_ex((vp * 1)(wo.handle.value), 1, att.data_ptr(), m, H, None, ctypes.c_float(0), 1,
+                                 (vp * 1)(want.data_ptr()), (i64 * 1)(4096), ws.data_ptr(), wsb, S()))
+    assert torch.equal(fused(), want)
+    monkeypatch.setenv("QMM_ATTN_O_SEPARATE", "1")
+    assert torch.equal(fused(), want)
+
+
+def test_prefill_attention_o_rejects_bad_arguments():
+    g = torch.Generator(device=DEV).manual_seed(9)
+    wo = QTensor.quantize(torch.randn((512, 1024), generator=g, device=DEV) * 0.02, GgmlDType.Q4K)
+    t1 = torch.zeros(4096, device=DEV)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=DEV)
+    with pytest.raises(qmm.QmmError):  # o weight's k (1024) != heads * head_dim (2048)
+        qmm._check(L().qmm_prefill_attention_o(t1.data_ptr(), 2048, t1.data_ptr(), t1.data_ptr(), 0, 2, 16, 4, 128,
+                                               64, ctypes.c_float(1.0), wo.handle, t1.data_ptr(), 512,
+                                               ws.data_ptr(), ws.numel(), S()))
+    with pytest.raises(qmm.QmmError):  # workspace too small
+        qmm._check(L().qmm_prefill_attention_o(t1.data_ptr(), 1024, t1.data_ptr(), t1.data_ptr(), 0, 2, 8, 4, 128,
+                                               64, ctypes.c_float(1.0), wo.handle, t1.data_ptr(), 512,
+                                               ws.data_ptr(), 16, S()))
