@@ -294,9 +294,11 @@ def test_qkv_rope_rejects_bad_arguments():
     assert size(wq.handle, wk.handle, wq.handle, 16, 1) == 0   # k and v of different row counts
     assert size(wq.handle, wk.handle, wk.handle, 0, 1) == 0    # no rows
 
-@pytest.mark.parametrize("m,heads,kv_heads,hd", [(127, 32, 8, 128), (24, 32, 8, 128), (9, 32, 8, 128),
-                                                 (5, 32, 8, 128), (40, 8, 8, 128), (33, 16, 4, 64)])
-def test_prefill_attention_o_equals_the_two_calls(monkeypatch, m, heads, kv_heads, hd):
+@pytest.mark.parametrize("m,heads,kv_heads,hd,dt", [(127, 32, 8, 128, GgmlDType.Q4K), (127, 32, 8, 128, GgmlDType.Q6K),
+                                                    (24, 32, 8, 128, GgmlDType.Q4K), (9, 32, 8, 128, GgmlDType.Q4K),
+                                                    (5, 32, 8, 128, GgmlDType.Q4K), (40, 8, 8, 128, GgmlDType.Q4K),
+                                                    (33, 16, 4, 64, GgmlDType.Q6K)])
+def test_prefill_attention_o_equals_the_two_calls(monkeypatch, m, heads, kv_heads, hd, dt):
     """qmm_prefill_attention_o (causal attention of m prompt rows, then o and the residual add) against
     qmm_prefill_attention followed by qmm_matmul_ex(o, accumulate), bit for bit: with the attention launch
     writing the o GEMM's Q8_K planes (m > 8, G * head_dim a multiple of 256: 32 / 8 heads of 128, 16 / 4 of
@@ -304,7 +306,7 @@ def test_prefill_attention_o_equals_the_two_calls(monkeypatch, m, heads, kv_head
     QMM_ATTN_O_SEPARATE=1)."""
     H, max_seq, first = heads * hd, 160, 3
     g = torch.Generator(device=DEV).manual_seed(500 + m)
-    wo = QTensor.quantize(torch.randn((4096, H), generator=g, device=DEV) * 0.02, GgmlDType.Q4K)
+    wo = QTensor.quantize(torch.randn((4096, H), generator=g, device=DEV) * 0.02, dt)
     q = torch.randn((m, H), generator=g, device=DEV)
     kc = torch.randn((kv_heads, max_seq, hd), generator=g, device=DEV)
     vc = torch.randn((kv_heads, max_seq, hd), generator=g, device=DEV)
